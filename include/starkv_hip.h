@@ -1,0 +1,151 @@
+/*
+ * starkv_hip.h -- C ABI of the MI355X (gfx950) STAR-KV paged decode library.
+ *
+ * Everything crosses this boundary as plain pointers, element/byte strides and
+ * ints; no framework types. Device pointers are HIP device memory on the current
+ * device, `stream` is a hipStream_t (NULL = the null stream). Every call only
+ * enqueues work: no host synchronisation, no host reads of device data, and the
+ * launch grid depends only on host ints, so the calls can be captured in a HIP
+ * graph. Each function returns 0 on success and a nonzero STARKV_ERR_* code on a
+ * bad argument or a HIP error; starkv_last_error() then holds the message (per
+ * host thread).
+ *
+ * Dtype codes: STARKV_F32, STARKV_F16, STARKV_BF16.
+ */
+#ifndef STARKV_HIP_H
+#define STARKV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STARKV_F32 0
+#define STARKV_F16 1
+#define STARKV_BF16 2
+
+#define STARKV_OK 0
+#define STARKV_ERR_ARG 1
+#define STARKV_ERR_HIP 2
+#define STARKV_ERR_UNSUPPORTED 3
+
+/* Library ABI version (bumped on any signature change). */
+int starkv_abi_version(void);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char *starkv_last_error(void);
+
+/*
+ * bf16/fp16 cache write: cache[slot // block_size, slot % block_size, :] =
+ * cat(k_codes[i], v_codes[i]) cast to the cache dtype; slot < 0 -> slot 0 (the
+ * null block). Replaces the inline index_put of the bf16 write branch in
+ * StarKVAttentionImpl.forward, starkv_serve/attention.py:180-184.
+ *   k_codes  [n, k_width], row stride k_s0 elements, last dim contiguous
+ *   v_codes  [n, v_rank],  row stride v_s0 elements, last dim contiguous
+ *   cache    [num_blocks, block_size, k_width + v_rank] with element strides c_s0, c_s1
+ *   slot_mapping [n] int32 (slot_bits = 32) or int64 (slot_bits = 64); slots at or past
+ *   num_blocks * block_size are skipped (the reference would write past the cache)
+ */
+int starkv_write_codes(void *stream, const void *k_codes, int64_t k_s0, const void *v_codes,
+                       int64_t v_s0, int in_dtype, void *cache, int64_t c_s0, int64_t c_s1,
+                       int cache_dtype, int block_size, int64_t num_blocks, const void *slot_mapping,
+                       int slot_bits, int n, int k_width, int v_rank);
+
+/*
+ * 3.2-bit write path: quantize one row per token (per-KV-head 4-bit outlier /
+ * 3-bit inlier K blocks with bf16 scales, then the head-shared V latent) and
+ * scatter it into its slot, bit for bit kv_quant._q (IEEE fp32 division,
+ * round-half-even). Replaces starkv_serve/kernels/paged_quant.py:205-216
+ * (pack_kv -> _pack_k 146-172, _pack_v 175-202). The row layout is QuantRow
+ * (paged_quant.py:71-111) for (k_width, num_kv_heads, v_rank); row_bytes must
+ * equal QuantRow.nbytes. Bytes [vq_off + v_bytes, row_bytes) are written as 0.
+ *   k_codes [n, k_width], v_codes [n, v_rank] (dtype code_dtype, rows strided)
+ *   cache   uint8 [num_blocks, block_size, row_bytes], byte strides c_s0, c_s1
+ *   k_ranks / k_offsets / k_nouts  [num_kv_heads] int32 device arrays
+ *   slots at or past num_blocks * block_size are skipped
+ */
+int starkv_pack_kv(void *stream, const void *k_codes, int64_t k_s0, const void *v_codes, int64_t v_s0,
+                   int code_dtype, uint8_t *cache, int64_t c_s0, int64_t c_s1, int block_size,
+                   int64_t num_blocks, const void *slot_mapping, int slot_bits, int n, int num_kv_heads,
+                   const int32_t *k_ranks, const int32_t *k_offsets, const int32_t *k_nouts,
+                   int k_width, int v_rank, int row_bytes);
+
+/*
+ * Fold the query into U: AB[b, r, i] = (q_i U[r,i] + q_{i+64} U[r,i+64]) * scale and
+ * AB[b, r, 64 + i] = (q_{i+64} U[r,i] - q_i U[r,i+64]) * scale, i < 64, q of head
+ * head_of_lane[r], stored fp16 [n, k_width, 128] contiguous. Replaces
+ * starkv_serve/kernels/paged_quant.py:241-255 (fold_q). The decode entry points
+ * below fold internally and do not need this; it is kept for the reference API.
+ */
+int starkv_fold_q(void *stream, const void *q, int64_t q_s0, int64_t q_s1, int q_dtype, const void *k_up,
+                  int64_t ku_s0, int ku_dtype, const int32_t *head_of_lane, int n, int k_width,
+                  float scale, void *ab);
+
+/*
+ * Grid (workgroups) the decode calls below use on the current device for n
+ * requests bounded by max_seq_len. A pure function of (device, n, max_seq_len).
+ */
+int starkv_decode_grid(int n, int max_seq_len);
+
+/*
+ * Workspace bytes a decode call needs: the rank-tile table, the token prefix sums,
+ * the q-folded bases (n * k_tiles * 4 KiB) and the split-K partials. k_tiles is the
+ * number of 16-lane rank tiles over all query heads:
+ * (num_heads / num_kv_heads) * k_width / 16.
+ */
+size_t starkv_decode_workspace_bytes(int n, int num_heads, int k_tiles, int v_rank, int grid);
+
+/*
+ * bf16/fp16 low-rank paged decode. Replaces
+ * starkv_serve/kernels/paged_decode.py:150-226 (paged_starkv_decode).
+ * Per request b, query head h and token l < min(seq_lens[b], max_seq_len):
+ *   logit = scale * q[b,h] . RoPE_l(U_kv^T x_l),  x_l = the first k_ranks[kv] codes of
+ *   KV head kv = h / (H_q / H_kv) at lane k_head_offsets[kv] of the token's cache row,
+ *   out[b,h] = (softmax(logit) @ V_codes) @ v_up_by_q[h].
+ *   query       [n, H_q, 128] (element strides q_s0, q_s1; last dim contiguous)
+ *   kv_cache    [num_blocks, block_size, k_width + v_rank], element strides c_s0, c_s1,
+ *               last dim contiguous; code_dtype bf16 or fp16; block_size a multiple of 16
+ *   block_table [n, max_blocks] int32 (strides bt_s0, bt_s1); seq_lens [n] int32
+ *   k_up        [k_width, 128] (row stride ku_s0), k_ranks / k_head_offsets [H_kv] int32
+ *   v_up_by_q   [H_q, v_rank, 128] (strides vu_s0, vu_s1)
+ *   cos_sin     [>= max_seq_len, 128] = cat(cos, sin) (row stride cs_s0)
+ *   out         [n, H_q, 128] (strides o_s0, o_s1), dtype out_dtype
+ *   workspace   >= starkv_decode_workspace_bytes(n, H_q, k_tiles, v_rank, grid) bytes,
+ *               256-byte aligned; grid from starkv_decode_grid(n, max_seq_len) (or any
+ *               grid >= 1)
+ */
+int starkv_lowrank_decode(void *stream, const void *query, int64_t q_s0, int64_t q_s1, int q_dtype,
+                          const void *kv_cache, int64_t c_s0, int64_t c_s1, int code_dtype, int block_size,
+                          const int32_t *block_table, int64_t bt_s0, int64_t bt_s1, const int32_t *seq_lens,
+                          int n, int num_heads, int num_kv_heads, int max_seq_len, const void *k_up,
+                          int64_t ku_s0, int w_dtype, const int32_t *k_ranks, const int32_t *k_head_offsets,
+                          int k_width, const void *v_up_by_q, int64_t vu_s0, int64_t vu_s1, int v_rank,
+                          const void *cos_sin, int64_t cs_s0, int cs_dtype, float scale, void *out,
+                          int64_t o_s0, int64_t o_s1, int out_dtype, void *workspace, size_t workspace_bytes,
+                          int grid);
+
+/*
+ * 3.2-bit paged decode over the QuantRow cache. Replaces
+ * starkv_serve/kernels/paged_quant.py:357-411 (paged_quant_decode: fold_q,
+ * _paged_abx_z, softmax, _paged_pv_fold, lift). MHA, head_dim 128.
+ *   kv_cache    uint8 [num_blocks, block_size, row_bytes], byte strides c_s0, c_s1
+ *   tile_head / tile_nout / tile_last  [k_width / 16] int32 (k_tables' per-16-lane tiles)
+ *   other arguments as starkv_lowrank_decode.
+ */
+int starkv_quant_decode(void *stream, const void *query, int64_t q_s0, int64_t q_s1, int q_dtype,
+                        const uint8_t *kv_cache, int64_t c_s0, int64_t c_s1, int block_size,
+                        const int32_t *block_table, int64_t bt_s0, int64_t bt_s1, const int32_t *seq_lens,
+                        int n, int num_heads, int max_seq_len, int k_width, int v_rank, int row_bytes,
+                        const void *k_up, int64_t ku_s0, int w_dtype, const int32_t *tile_head,
+                        const int32_t *tile_nout, const int32_t *tile_last, const void *v_up_by_q,
+                        int64_t vu_s0, int64_t vu_s1, const void *cos_sin, int64_t cs_s0, int cs_dtype,
+                        float scale, void *out, int64_t o_s0, int64_t o_s1, int out_dtype, void *workspace,
+                        size_t workspace_bytes, int grid);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STARKV_HIP_H */

@@ -1,0 +1,174 @@
+// Shared device/host helpers for the STAR-KV paged decode library (gfx950 / CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "../../include/starkv_hip.h"
+
+namespace starkv {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------------------
+// Error reporting through the C ABI: a thread-local message, nonzero return.
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define SKV_CHECK(cond, ...)                 \
+    do {                                      \
+        if (!(cond)) {                        \
+            ::starkv::set_error(__VA_ARGS__); \
+            return STARKV_ERR_ARG;            \
+        }                                     \
+    } while (0)
+
+#define SKV_HIP(call)                                                            \
+    do {                                                                         \
+        hipError_t e_ = (call);                                                  \
+        if (e_ != hipSuccess) {                                                  \
+            ::starkv::set_error("%s failed: %s", #call, hipGetErrorString(e_)); \
+            return STARKV_ERR_HIP;                                               \
+        }                                                                        \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// Scalar conversions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float load_f(const void* p, int64_t i, int dt) {
+    if (dt == STARKV_BF16) return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+    if (dt == STARKV_F16) return (float)((const _Float16*)p)[i];
+    return ((const float*)p)[i];
+}
+
+__device__ __forceinline__ void store_f(void* p, int64_t i, int dt, float v) {
+    if (dt == STARKV_BF16)
+        ((uint16_t*)p)[i] = f32_to_bf16_rne(v);
+    else if (dt == STARKV_F16)
+        ((_Float16*)p)[i] = (_Float16)v;
+    else
+        ((float*)p)[i] = v;
+}
+
+// Eight consecutive elements starting at element i (16-byte aligned for 2-byte
+// types, 32-byte for fp32) as fp32.
+__device__ __forceinline__ void load8_f(const void* p, int64_t i, int dt, float* o) {
+    if (dt == STARKV_F32) {
+        const float4* v = (const float4*)((const float*)p + i);
+        float4 a = v[0], b = v[1];
+        o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+        o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+        return;
+    }
+    uint4 w = *(const uint4*)((const uint16_t*)p + i);
+    uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    if (dt == STARKV_BF16) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            o[2 * k] = __uint_as_float(ws[k] << 16);
+            o[2 * k + 1] = __uint_as_float(ws[k] & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            _Float16 lo, hi;
+            uint16_t l16 = (uint16_t)(ws[k] & 0xffffu), h16 = (uint16_t)(ws[k] >> 16);
+            memcpy(&lo, &l16, 2);
+            memcpy(&hi, &h16, 2);
+            o[2 * k] = (float)lo;
+            o[2 * k + 1] = (float)hi;
+        }
+    }
+}
+
+__device__ __forceinline__ int dtype_size(int dt) { return dt == STARKV_F32 ? 4 : 2; }
+
+// A value the optimizer cannot see through: address arithmetic derived from it is
+// recomputed where it is used instead of being hoisted out of the main loop and
+// held in registers for the whole kernel.
+__device__ __forceinline__ int opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Reductions over the 16 lanes of a row (lanes 16r .. 16r+15).
+__device__ __forceinline__ float row16_max(float v) {
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// s_waitcnt with a run-time count (the instruction takes an immediate).
+// gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in 15:14, expcnt 6:4,
+// lgkmcnt 11:8.
+// ---------------------------------------------------------------------------
+#define SKV_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (0 << 8))
+
+__device__ __forceinline__ void wait_vmcnt_lgkm0(int n) {
+    switch (n) {
+        case 0: SKV_WAIT_VM_LGKM0(0); break;
+        case 1: SKV_WAIT_VM_LGKM0(1); break;
+        case 2: SKV_WAIT_VM_LGKM0(2); break;
+        case 3: SKV_WAIT_VM_LGKM0(3); break;
+        case 4: SKV_WAIT_VM_LGKM0(4); break;
+        case 5: SKV_WAIT_VM_LGKM0(5); break;
+        case 6: SKV_WAIT_VM_LGKM0(6); break;
+        case 7: SKV_WAIT_VM_LGKM0(7); break;
+        case 8: SKV_WAIT_VM_LGKM0(8); break;
+        case 9: SKV_WAIT_VM_LGKM0(9); break;
+        case 10: SKV_WAIT_VM_LGKM0(10); break;
+        case 11: SKV_WAIT_VM_LGKM0(11); break;
+        case 12: SKV_WAIT_VM_LGKM0(12); break;
+        case 13: SKV_WAIT_VM_LGKM0(13); break;
+        case 14: SKV_WAIT_VM_LGKM0(14); break;
+        case 15: SKV_WAIT_VM_LGKM0(15); break;
+        default: SKV_WAIT_VM_LGKM0(0); break;
+    }
+}
+
+// Workgroup barrier that does not drain outstanding global->LDS copies: the
+// caller has already waited for what it needs (lgkmcnt(0) included).
+__device__ __forceinline__ void lds_barrier() { __builtin_amdgcn_s_barrier(); }
+
+__device__ __forceinline__ void wait_lgkm0_barrier() {
+    __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0) only
+    __builtin_amdgcn_s_barrier();
+}
+
+}  // namespace starkv

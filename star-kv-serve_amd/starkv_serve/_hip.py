@@ -1,0 +1,92 @@
+"""ctypes binding of libstarkv_hip.so, the C ABI declared in include/starkv_hip.h.
+
+Tensors cross the boundary as data pointers, strides and dtype codes; streams as
+the current HIP stream handle. There is no fallback: if the library is missing
+or fails to load, every entry point raises.
+"""
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstarkv_hip.so")
+ABI_VERSION = 1
+
+F32, F16, BF16 = 0, 1, 2
+_DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "starkv_abi_version": (_I, []),
+    "starkv_last_error": (ctypes.c_char_p, []),
+    "starkv_write_codes": (_I, [_P, _P, _I64, _P, _I64, _I, _P, _I64, _I64, _I, _I, _I64, _P, _I, _I, _I, _I]),
+    "starkv_pack_kv": (_I, [_P, _P, _I64, _P, _I64, _I, _P, _I64, _I64, _I, _I64, _P, _I, _I, _I, _P, _P, _P,
+                            _I, _I, _I]),
+    "starkv_fold_q": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I, _P, _I, _I, _F, _P]),
+    "starkv_decode_grid": (_I, [_I, _I]),
+    "starkv_decode_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
+    "starkv_lowrank_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _I, _P, _I64, _I64, _P, _I,
+                                   _I, _I, _I, _P, _I64, _I, _P, _P, _I, _P, _I64, _I64, _I, _P, _I64, _I,
+                                   _F, _P, _I64, _I64, _I, _P, _SZ, _I]),
+    "starkv_quant_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _P, _I64, _I64, _P, _I, _I, _I,
+                                 _I, _I, _I, _P, _I64, _I, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I, _F, _P,
+                                 _I64, _I64, _I, _P, _SZ, _I]),
+}
+
+_LIB = None
+
+
+def lib():
+    """The loaded library; raises RuntimeError if it is missing or stale."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"STAR-KV HIP library not built: {LIB_PATH} is missing "
+                               "(run `python star-kv-serve_amd/build.py`)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        if L.starkv_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH}: ABI {L.starkv_abi_version()} != {ABI_VERSION}; rebuild it")
+        _LIB = L
+    return _LIB
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().starkv_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what}: {msg} (code {rc})")
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}") from None
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """Handle of the current stream on t's device (the launch stream)."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def require_cuda(*ts: torch.Tensor) -> None:
+    dev = ts[0].device
+    for t in ts:
+        if t.device.type != "cuda":
+            raise RuntimeError("STAR-KV kernels run on the GPU only; got a tensor on "
+                               f"{t.device}")
+        if t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} vs {t.device}")

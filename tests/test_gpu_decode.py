@@ -1,0 +1,217 @@
+"""Paged decode on the GPU (through the C ABI) against the float64 oracle.
+
+Tolerance (bf16/fp16 outputs), per output tensor:
+  max |out - truth| <= 2e-2
+  mean |out - round(truth)| / mean |truth| <= 1e-3, round() = the output dtype
+  all outputs finite (unused cache slots hold NaN: masking must keep them out)
+The reference's own rounding error (logits stored in bf16, fp16 z accumulation) is
+printed next to ours where it is emulated.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cquant, ref
+from starkv_serve import _hip
+from starkv_serve import workloads as W
+from starkv_serve.kernels.paged_decode import paged_starkv_decode
+from starkv_serve.kernels.paged_quant import paged_quant_decode
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_REL = 1e-3
+
+
+def metrics(out, truth):
+    o = out.float().cpu().numpy().astype(np.float64)
+    tr = torch.from_numpy(truth).to(out.dtype).double().numpy()
+    return dict(max_abs=float(np.abs(o - truth).max()),
+                mean_rel=float(np.abs(o - tr).mean() / np.abs(truth).mean()),
+                rel_l2=float(np.linalg.norm(o - truth) / np.linalg.norm(truth)),
+                finite=bool(np.isfinite(o).all()))
+
+
+def assert_close(out, truth, label):
+    m = metrics(out, truth)
+    print(f"{label}: {m}", flush=True)
+    assert m["finite"], label
+    assert m["max_abs"] <= MAX_ABS, (label, m)
+    assert m["mean_rel"] <= MEAN_REL, (label, m)
+    return m
+
+
+def lowrank_truth(wl):
+    """float64 oracle; the cache is handed over as float32 (exact for bf16/fp16 codes)."""
+    cache = wl.kv_cache.cpu()
+    if cache.dtype == torch.bfloat16:
+        cache = (cache.view(torch.int16).numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    else:
+        cache = cache.float().numpy()
+    return ref.lowrank_decode(wl.query.float().cpu().numpy(), cache, wl.block_table.cpu().numpy(),
+                              wl.seq_lens.cpu().numpy(), wl.max_seq_len, wl.k_up.float().cpu().numpy(), wl.ranks,
+                              wl.k_head_offsets.tolist(), wl.k_width, wl.v_up_by_q.float().cpu().numpy(),
+                              wl.cos_sin_cache.float().cpu().numpy(), wl.scale)
+
+
+def run_lowrank(wl_gpu, grid=None):
+    if grid is None:
+        return paged_starkv_decode(*wl_gpu.decode_args())
+    # Call the C ABI directly with an explicit split.
+    q, kv, bt, sl = wl_gpu.query, wl_gpu.kv_cache, wl_gpu.block_table, wl_gpu.seq_lens
+    n, H, _ = q.shape
+    Hkv = wl_gpu.k_ranks.numel()
+    tiles = (H // Hkv) * wl_gpu.k_width // 16
+    out = torch.empty(n, H, 128, dtype=wl_gpu.v_up_by_q.dtype, device=q.device)
+    L = _hip.lib()
+    ws = torch.empty(L.starkv_decode_workspace_bytes(n, H, tiles, wl_gpu.v_rank, grid), dtype=torch.uint8,
+                     device=q.device)
+    cs, vq, U = wl_gpu.cos_sin_cache, wl_gpu.v_up_by_q, wl_gpu.k_up
+    rc = L.starkv_lowrank_decode(_hip.stream_of(q), q.data_ptr(), q.stride(0), q.stride(1), _hip.dtype_code(q),
+                                 kv.data_ptr(), kv.stride(0), kv.stride(1), _hip.dtype_code(kv), kv.shape[1],
+                                 bt.data_ptr(), bt.stride(0), bt.stride(1), sl.data_ptr(), n, H, Hkv,
+                                 wl_gpu.max_seq_len, U.data_ptr(), U.stride(0), _hip.dtype_code(U),
+                                 wl_gpu.k_ranks.data_ptr(), wl_gpu.k_head_offsets.data_ptr(), wl_gpu.k_width,
+                                 vq.data_ptr(), vq.stride(0), vq.stride(1), wl_gpu.v_rank, cs.data_ptr(), cs.stride(0),
+                                 _hip.dtype_code(cs), wl_gpu.scale, out.data_ptr(), out.stride(0), out.stride(1),
+                                 _hip.dtype_code(out), ws.data_ptr(), ws.numel(), grid)
+    _hip.check(rc, "lowrank_decode")
+    return out
+
+
+LOWRANK_CASES = {
+    # name: (lengths, kwargs)
+    "c0_b1_4096": ([4096], {}),
+    "ragged_edges": ([1, 15, 16, 17, 100, 1000, 33, 2], {}),
+    "gqa_h32_kv8": ([300, 17, 64], dict(num_kv_heads=8)),
+    "fp16": ([513, 90, 2048], dict(dtype=torch.float16)),
+    "strided_cache": ([200, 31], dict(col_pad=40)),
+    "peaked_q": ([1500, 700], dict(peaked=4.0)),
+    "v_rank_32": ([640, 129], dict(v_rank=32)),
+    "v_rank_256_h16": ([333, 48], dict(v_rank=256, num_heads=16)),
+    "graph_span": ([100, 37, 999], dict(max_seq_len=4096)),
+    "ranks_not_16": ([77, 260], dict(ranks=[20, 1, 33, 64, 7, 48, 16, 50], num_heads=8)),
+}
+
+
+@pytest.mark.parametrize("name", list(LOWRANK_CASES))
+def test_lowrank_decode_vs_oracle(cuda, name):
+    lengths, kw = LOWRANK_CASES[name]
+    kw = dict(kw)
+    print(f"\n[lowrank] case={name} lengths={lengths[:8]} {kw}", flush=True)
+    nh = kw.pop("num_heads", 32)
+    wl = W.make_lowrank(lengths, num_heads=nh, seed=100 + len(name), **kw)
+    out = paged_starkv_decode(*wl.to(cuda).decode_args())
+    torch.cuda.synchronize()
+    truth = lowrank_truth(wl)
+    assert_close(out, truth, name)
+
+
+def test_lowrank_reference_emulation_error_is_reported(cuda):
+    wl = W.make_lowrank([700, 1100], num_heads=32, seed=5)
+    out = paged_starkv_decode(*wl.to(cuda).decode_args())
+    truth = lowrank_truth(wl)
+    emu = ref.emulate_lowrank_reference(wl.query, wl.kv_cache, wl.block_table.numpy(), wl.seq_lens.numpy(),
+                                        wl.max_seq_len, wl.k_up, wl.ranks, wl.k_head_offsets.tolist(), wl.k_width,
+                                        wl.v_up_by_q, wl.cos_sin_cache, wl.scale)
+    mo = assert_close(out, truth, "hip")
+    me = metrics(torch.from_numpy(emu).to(out.dtype), truth)
+    print(f"reference-rounding emulation: {me}", flush=True)
+    assert mo["rel_l2"] <= me["rel_l2"] * 1.5 + 1e-4
+
+
+def test_lowrank_config1_full_size(cuda):
+    lengths = W.config_lengths(1)
+    print(f"\n[lowrank] config 1: 64 requests, {sum(lengths)} tokens", flush=True)
+    wl = W.make_lowrank(lengths, num_heads=32, seed=1001, gen_device=cuda)
+    g = wl.to(cuda)
+    out = paged_starkv_decode(*g.decode_args())
+    torch.cuda.synchronize()
+    truth = lowrank_truth(wl)
+    assert_close(out, truth, "config1")
+    # Size-independent property: permuting the physical pages changes nothing, bit for bit.
+    nb = g.kv_cache.shape[0]
+    perm = torch.cat([torch.zeros(1, dtype=torch.long), 1 + torch.randperm(nb - 1)]).to(cuda)
+    inv = torch.argsort(perm).to(torch.int32)
+    g2 = g.to(cuda)
+    g2.kv_cache = g.kv_cache[perm]
+    g2.block_table = inv[g.block_table.long()]
+    out2 = paged_starkv_decode(*g2.decode_args())
+    assert torch.equal(out, out2)
+    # Different workgroup splits agree with the oracle too.
+    for grid in (1, 7, 300):
+        assert_close(run_lowrank(g, grid=grid), truth, f"config1 grid={grid}")
+
+
+def test_lowrank_zero_length_and_truncation(cuda):
+    wl = W.make_lowrank([50, 40, 30], num_heads=4, ranks=[16, 32, 48, 64], v_rank=32, seed=8)
+    wl.seq_lens = torch.tensor([50, 0, 30], dtype=torch.int32)
+    wl.max_seq_len = 40
+    out = paged_starkv_decode(*wl.to(cuda).decode_args())
+    truth = lowrank_truth(wl)
+    assert torch.isnan(out[1]).all()       # softmax over an empty row, as the reference
+    assert_close(out[[0, 2]], truth[[0, 2]], "truncated")
+
+
+# ---------------------------------------------------------------------------
+# 3.2-bit
+# ---------------------------------------------------------------------------
+
+def quant_truth(wl_gpu):
+    cache = wl_gpu.kv_cache.cpu().numpy()
+    lay = ref.row_layout(wl_gpu.k_width, len(wl_gpu.ranks), wl_gpu.v_rank)
+    return ref.quant_decode(wl_gpu.query.float().cpu().numpy(), cache, wl_gpu.block_table.cpu().numpy(),
+                            wl_gpu.seq_lens.cpu().numpy(), wl_gpu.max_seq_len, lay, wl_gpu.ranks,
+                            wl_gpu.k_up.float().cpu().numpy(), wl_gpu.v_up_by_q.float().cpu().numpy(),
+                            wl_gpu.cos_sin_cache.float().cpu().numpy(), wl_gpu.scale)
+
+
+def check_packed_rows(wl_gpu, count=64):
+    """The GPU-packed cache equals the C oracle's packing of the same codes (sampled rows)."""
+    lay = ref.row_layout(wl_gpu.k_width, len(wl_gpu.ranks), wl_gpu.v_rank)
+    slots = wl_gpu.extra["slots"].cpu().numpy()
+    idx = np.linspace(0, len(slots) - 1, min(count, len(slots))).astype(int)
+    k = wl_gpu.k_codes.float().cpu().numpy()[idx]
+    v = wl_gpu.v_codes.float().cpu().numpy()[idx]
+    want = np.zeros((len(idx), 1, lay["nbytes"]), np.uint8)
+    widths, offsets, _ = ref.head_layout(wl_gpu.ranks)
+    cquant.pack_kv(k, v, want, np.arange(len(idx)), wl_gpu.ranks, offsets,
+                   [ref.n_outlier(r) for r in wl_gpu.ranks], wl_gpu.v_rank, lay["ks_off"], lay["vs_off"],
+                   lay["vq_off"])
+    c = wl_gpu.kv_cache.cpu().numpy()
+    got = c[slots[idx] // 16, slots[idx] % 16]
+    end = lay["vq_off"] + lay["v_bytes"]
+    assert np.array_equal(got[:, :end], want[:, 0, :end])
+
+
+QUANT_CASES = {
+    "c0_b1_4096": ([4096], {}),
+    "ragged_edges": ([1, 15, 16, 17, 100, 1000, 33, 2], {}),
+    "v_rank_32": ([640, 129], dict(v_rank=32)),
+    "peaked_q": ([1500, 700], dict(peaked=4.0)),
+    "strided_cache": ([200, 31], dict(col_pad=48)),
+    "graph_span": ([100, 37, 999], dict(max_seq_len=4096)),
+    "fp16": ([513, 90], dict(dtype=torch.float16)),
+}
+
+
+@pytest.mark.parametrize("name", list(QUANT_CASES))
+def test_quant_decode_vs_oracle(cuda, name):
+    lengths, kw = QUANT_CASES[name]
+    kw = dict(kw)
+    print(f"\n[quant] case={name} lengths={lengths[:8]} {kw}", flush=True)
+    wl = W.make_quant(lengths, num_heads=32, seed=200 + len(name), device=cuda, **kw)
+    check_packed_rows(wl)
+    out = paged_quant_decode(*wl.decode_args())
+    torch.cuda.synchronize()
+    assert_close(out, quant_truth(wl), name)
+
+
+def test_quant_config2_full_size(cuda):
+    lengths = W.config_lengths(2)
+    print(f"\n[quant] config 2: 64 requests, {sum(lengths)} tokens", flush=True)
+    wl = W.make_quant(lengths, num_heads=32, seed=1002, device=cuda, gen_device=cuda)
+    check_packed_rows(wl, count=256)
+    out = paged_quant_decode(*wl.decode_args())
+    torch.cuda.synchronize()
+    assert_close(out, quant_truth(wl), "config2")
