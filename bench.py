@@ -1,0 +1,217 @@
+"""Benchmark: STAR-KV paged decode attention on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+A step is one decode call (one layer) over the whole batch. The headline workload
+is the reference metric's configuration: bf16/low-rank codes, batch 64, every
+request at 8192 tokens of context, 32 heads x head_dim 128, page size 16, K ranks
+per head drawn from {16, 32, 48, 64}, V rank 64, physical pages shuffled. The cache
+(1.4 GB) is larger than the 256 MB Infinity Cache, so every step streams it from
+HBM. `value` = algorithmic bytes per step / wall time per step (whole call: setup,
+fold, decode and merge launches). `roofline.achieved` = the same bytes / the decode
+kernel's own average duration (HIP events around that launch). The 3.2-bit kernel
+at the same shape (three rotating cache copies, 1.3 GB) and the ragged reference
+configurations are reported under "extra". `cpu_baseline` times the float64 CPU
+oracle on a bounded sample of the same workload on this host.
+
+One JSON line is printed on stdout.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "star-kv-serve_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_PEAK_F16_TFLOPS = 2500.0  # dense fp16/bf16
+METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_steps(fn, steps, warmup):
+    """Warmup, then `steps` timed calls bracketed by synchronizes; returns
+    (ms per step, decode-kernel ms per call)."""
+    import torch
+    from starkv_serve import _hip
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    _hip.profile_begin(steps)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i)
+    stop.record()
+    torch.cuda.synchronize()
+    kern_ms, calls = _hip.profile_end()
+    return start.elapsed_time(stop) / steps, kern_ms / max(calls, 1)
+
+
+def bench_lowrank(lengths, steps, warmup, seed, v_rank=64):
+    import torch
+    from starkv_serve import workloads as W
+    from starkv_serve.kernels.paged_decode import paged_starkv_decode
+    dev = torch.device("cuda", 0)
+    wl = W.make_lowrank(lengths, num_heads=32, v_rank=v_rank, seed=seed, gen_device=dev).to(dev)
+    args = wl.decode_args()
+    ms, kern = time_steps(lambda i: paged_starkv_decode(*args), steps, warmup)
+    return wl, ms, kern
+
+
+def bench_quant(lengths, steps, warmup, seed, copies, v_rank=64):
+    import torch
+    from starkv_serve import workloads as W
+    from starkv_serve.kernels.paged_quant import paged_quant_decode
+    dev = torch.device("cuda", 0)
+    wl = W.make_quant(lengths, num_heads=32, v_rank=v_rank, seed=seed, device=dev, gen_device=dev)
+    wl.k_codes = wl.v_codes = None
+    torch.cuda.empty_cache()
+    caches = [wl.kv_cache] + [wl.kv_cache.clone() for _ in range(copies - 1)]
+    base = list(wl.decode_args())
+
+    def step(i):
+        base[1] = caches[i % len(caches)]
+        return paged_quant_decode(*base)
+
+    ms, kern = time_steps(step, steps, warmup)
+    return wl, ms, kern
+
+
+def summarize(wl, ms, kern):
+    b = wl.bytes_per_step()
+    f = wl.flops_per_step()
+    return dict(us_per_step=round(ms * 1e3, 2), decode_kernel_us=round(kern * 1e3, 2),
+                GBps=round(b / (ms * 1e-3) / 1e9, 1), kernel_GBps=round(b / (kern * 1e-3) / 1e9, 1),
+                hbm_frac=round(b / (kern * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                mfma_frac=round(f / (kern * 1e-3) / 1e12 / MFMA_PEAK_F16_TFLOPS, 4),
+                bytes_per_step=int(b), flops_per_step=int(f), tokens=wl.tokens, k_width=wl.k_width,
+                v_rank=wl.v_rank)
+
+
+def cpu_baseline(wl, budget_s=12.0):
+    """The float64 oracle (numpy) on whole requests of the workload until ~budget_s."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_info
+
+    from oracle import ref
+    cores = len(os.sched_getaffinity(0))
+    blas = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
+    q = wl.query.float().cpu().numpy()
+    bt = wl.block_table.cpu().numpy()
+    U = wl.k_up.float().cpu().numpy()
+    vq = wl.v_up_by_q.float().cpu().numpy()
+    cs = wl.cos_sin_cache.float().cpu().numpy()
+    row_bytes = (wl.k_width + wl.v_rank) * wl.kv_cache.element_size()
+    done_tokens, done_bytes, t_total, reqs = 0, 0, 0.0, 0
+    for b in range(wl.n):
+        L = int(wl.lengths[b])
+        pages = (L + 15) // 16
+        blocks = torch.from_numpy(bt[b, :pages]).long().to(wl.kv_cache.device)
+        rows = wl.kv_cache[blocks].float().cpu().numpy()         # [pages, 16, width] of this request
+        local_bt = np.arange(pages, dtype=np.int32)[None, :]
+        t0 = time.perf_counter()
+        ref.lowrank_decode(q[b:b + 1], rows, local_bt, [L], wl.max_seq_len, U, wl.ranks,
+                           wl.k_head_offsets.tolist(), wl.k_width, vq, cs, wl.scale)
+        t_total += time.perf_counter() - t0
+        done_tokens += L
+        done_bytes += L * row_bytes
+        reqs += 1
+        if t_total >= budget_s:
+            break
+    return dict(value=round(done_bytes / t_total / 1e9, 3), unit="GB/s", cores=blas[0] if blas else cores,
+                kind="port",
+                sample=f"float64 numpy oracle (oracle/ref.py lowrank_decode) on {reqs} of the {wl.n} requests "
+                       f"({done_tokens} tokens, {t_total:.1f} s), GB/s of cache rows attended; "
+                       f"host affinity {cores} cores")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extra", action="store_true", help="skip the 3.2-bit and ragged configurations")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (decode shards by request; "
+              "each GPU would run this same kernel on its own requests). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    torch.cuda.set_device(0)
+    log(f"device: {torch.cuda.get_device_name(0)}")
+
+    lengths = [8192] * 64
+    log("headline: bf16 low-rank, 64 x 8192")
+    wl, ms, kern = bench_lowrank(lengths, args.steps, args.warmup, seed=1001)
+    head = summarize(wl, ms, kern)
+    log(json.dumps(head))
+
+    extra = {}
+    if not args.no_extra:
+        from starkv_serve import workloads as W
+        log("3.2-bit, 64 x 8192 (3 rotating caches)")
+        wq, msq, kq = bench_quant(lengths, args.steps, args.warmup, seed=1003, copies=3)
+        extra["quant_bs64x8k"] = summarize(wq, msq, kq)
+        log(json.dumps(extra["quant_bs64x8k"]))
+        del wq
+        torch.cuda.empty_cache()
+        log("config 1: bf16 low-rank, 64 requests, lengths U[1024, 8192]")
+        w1, ms1, k1 = bench_lowrank(W.config_lengths(1), args.steps, args.warmup, seed=1001)
+        extra["lowrank_config1"] = summarize(w1, ms1, k1)
+        log(json.dumps(extra["lowrank_config1"]))
+        del w1
+        torch.cuda.empty_cache()
+        log("config 2: 3.2-bit, 64 requests, lengths U[1024, 8192] (3 rotating caches)")
+        w2, ms2, k2 = bench_quant(W.config_lengths(2), args.steps, args.warmup, seed=1002, copies=3)
+        extra["quant_config2"] = summarize(w2, ms2, k2)
+        log(json.dumps(extra["quant_config2"]))
+        del w2
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline")
+        cpu = cpu_baseline(wl)
+        log(json.dumps(cpu))
+
+    out = {
+        "metric": METRIC,
+        "value": head["GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) codes and queries, random-init bases, shuffled pages)",
+        "config": {"workload": "bf16 low-rank paged decode, one layer, batch 64 x context 8192",
+                   "batch": 64, "context": 8192, "num_heads": 32, "head_dim": 128, "page_size": 16,
+                   "k_width": wl.k_width, "v_rank": wl.v_rank, "k_ranks": "uniform {16,32,48,64} per head",
+                   "decode_us": head["us_per_step"]},
+        "roofline": {"bound": "hbm", "achieved": head["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": head["hbm_frac"], "traffic": None,
+                     "kernel": "decode_kernel", "kernel_us": head["decode_kernel_us"],
+                     "bytes_per_launch": head["bytes_per_step"], "mfma_frac_fp16": head["mfma_frac"]},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -144,6 +144,17 @@ int starkv_quant_decode(void *stream, const void *query, int64_t q_s0, int64_t q
                         float scale, void *out, int64_t o_s0, int64_t o_s1, int out_dtype, void *workspace,
                         size_t workspace_bytes, int grid);
 
+/*
+ * Timing of the decode kernel alone, for benchmarks (no counterpart in the
+ * reference, whose benchmark reads profiler traces instead, bench_serving.py:71-115).
+ * starkv_profile_begin arms up to max_calls event pairs; each following decode call
+ * records one pair around its decode kernel on its stream. starkv_profile_end
+ * synchronizes those events, returns the summed milliseconds and the number of
+ * timed calls, and disarms. Not for use under graph capture.
+ */
+int starkv_profile_begin(int max_calls);
+int starkv_profile_end(double *decode_ms_sum, int *calls);
+
 #ifdef __cplusplus
 }
 #endif

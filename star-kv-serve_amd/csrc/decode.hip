@@ -27,6 +27,8 @@
 //    v_up_by_q.
 #include <stdio.h>
 
+#include <vector>
+
 #include "common.hpp"
 
 namespace starkv {
@@ -702,6 +704,15 @@ static int grid_for(int n, int max_seq_len) {
     return want < 1 ? 1 : (int)want;
 }
 
+// Optional timing of the decode kernel alone (benchmarks): when armed, each call records
+// a HIP event pair around the decode launch on the caller's stream.
+struct DecodeProfile {
+    bool on = false;
+    int used = 0;
+    std::vector<hipEvent_t> ev;
+};
+static DecodeProfile g_prof;
+
 static int mt_for(int TT) {
     int mt = (TT + NWAVE - 1) / NWAVE;
     if (mt <= 4) return 4;
@@ -797,11 +808,17 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
                        a.scale * LOG2E, p.ws + wl.ab);
     SKV_HIP(hipGetLastError());
     const int mt = mt_for(TT);
+    const bool timed = g_prof.on && 2 * g_prof.used + 1 < (int)g_prof.ev.size();
+    if (timed) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
     int rc = fmt == FMT_Q4 ? launch_decode<FMT_Q4, XB_Q4>(p, mt, a.grid, stream)
              : fmt == FMT_BF16 ? launch_decode<FMT_BF16, XB_LOWRANK>(p, mt, a.grid, stream)
                                : launch_decode<FMT_F16, XB_LOWRANK>(p, mt, a.grid, stream);
     if (rc) return rc;
     SKV_HIP(hipGetLastError());
+    if (timed) {
+        SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used + 1], stream));
+        ++g_prof.used;
+    }
     hipLaunchKernelGGL(merge_kernel, dim3(a.n, a.Hq), dim3(128), a.v_rank * 4, stream, (const uint8_t*)p.ws, wl.m,
                        wl.l, wl.acc, a.Hq, a.v_rank, a.vup, a.vu_s0, a.vu_s1, a.w_dt, a.out, a.o_s0, a.o_s1,
                        a.out_dt);
@@ -816,6 +833,33 @@ using namespace starkv;
 extern "C" {
 
 int starkv_decode_grid(int n, int max_seq_len) { return grid_for(n, max_seq_len); }
+
+int starkv_profile_begin(int max_calls) {
+    clear_error();
+    SKV_CHECK(max_calls >= 1 && max_calls <= 100000, "profile_begin: max_calls %d", max_calls);
+    for (hipEvent_t e : g_prof.ev) (void)hipEventDestroy(e);
+    g_prof.ev.assign(2 * (size_t)max_calls, nullptr);
+    for (auto& e : g_prof.ev) SKV_HIP(hipEventCreate(&e));
+    g_prof.used = 0;
+    g_prof.on = true;
+    return STARKV_OK;
+}
+
+int starkv_profile_end(double* decode_ms_sum, int* calls) {
+    clear_error();
+    g_prof.on = false;
+    double sum = 0.0;
+    for (int i = 0; i < g_prof.used; ++i) {
+        SKV_HIP(hipEventSynchronize(g_prof.ev[2 * i + 1]));
+        float ms = 0.f;
+        SKV_HIP(hipEventElapsedTime(&ms, g_prof.ev[2 * i], g_prof.ev[2 * i + 1]));
+        sum += ms;
+    }
+    if (decode_ms_sum) *decode_ms_sum = sum;
+    if (calls) *calls = g_prof.used;
+    g_prof.used = 0;
+    return STARKV_OK;
+}
 
 size_t starkv_decode_workspace_bytes(int n, int num_heads, int k_tiles, int v_rank, int grid) {
     return ws_layout(n, num_heads, k_tiles, v_rank, grid).total;

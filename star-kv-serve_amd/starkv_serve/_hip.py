@@ -30,6 +30,8 @@ SIGNATURES = {
                             _I, _I, _I]),
     "starkv_fold_q": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I, _P, _I, _I, _F, _P]),
     "starkv_decode_grid": (_I, [_I, _I]),
+    "starkv_profile_begin": (_I, [_I]),
+    "starkv_profile_end": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "starkv_decode_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "starkv_lowrank_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _I, _P, _I64, _I64, _P, _I,
                                    _I, _I, _I, _P, _I64, _I, _P, _P, _I, _P, _I64, _I64, _I, _P, _I64, _I,
@@ -80,6 +82,19 @@ def stream_of(t: torch.Tensor) -> int:
 
 def ptr(t: torch.Tensor) -> int:
     return t.data_ptr()
+
+
+def profile_begin(max_calls: int) -> None:
+    """Arm event timing of the decode kernel for the next `max_calls` decode calls."""
+    check(lib().starkv_profile_begin(int(max_calls)), "profile_begin")
+
+
+def profile_end() -> tuple:
+    """(summed decode-kernel milliseconds, timed calls); disarms the timing."""
+    ms = ctypes.c_double(0.0)
+    calls = ctypes.c_int(0)
+    check(lib().starkv_profile_end(ctypes.byref(ms), ctypes.byref(calls)), "profile_end")
+    return ms.value, calls.value
 
 
 def require_cuda(*ts: torch.Tensor) -> None:
