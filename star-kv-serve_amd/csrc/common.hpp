@@ -105,6 +105,13 @@ __device__ __forceinline__ int opaque(int v) {
     return v;
 }
 
+// The same for a wave-uniform value (kept in an SGPR): comparisons and products of it
+// are redone where used rather than hoisted into SGPRs that live across the loop.
+__device__ __forceinline__ int opaque_s(int v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
 // ---------------------------------------------------------------------------
 // Wave64 reductions
 // ---------------------------------------------------------------------------
@@ -120,17 +127,50 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// Reductions over the 16 lanes of a row (lanes 16r .. 16r+15).
+// Reductions over the 16 lanes of a row (lanes 16r .. 16r+15) with DPP: quad_perm
+// [1,0,3,2] (0xB1), quad_perm [2,3,0,1] (0x4E), row_half_mirror (0x141), row_mirror
+// (0x140). Every source lane lies inside the row, so no lane reads a disabled one.
+template <int CTL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTL, 0xF, 0xF, true));
+}
+
 __device__ __forceinline__ float row16_max(float v) {
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
     return v;
 }
 
 __device__ __forceinline__ float row16_sum(float v) {
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
     return v;
+}
+
+// Sums over the 4 rows of a wave (lanes l, l^16, l^32, l^48) with the gfx950 lane
+// swaps. v_permlane32_swap(a, b) leaves a = {a[0:32), b[0:32)}, b = {a[32:64), b[32:64)};
+// v_permlane16_swap(a, b) leaves a = {a.R0, b.R0, a.R2, b.R2}, b = {a.R1, b.R1, a.R3, b.R3}
+// (Rk = lanes 16k .. 16k+15).
+__device__ __forceinline__ float sum_rows(float v) {
+    const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float s = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+    const auto y = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return __uint_as_float(y[0]) + __uint_as_float(y[1]);
+}
+
+// Four row sums at once. The result's row 0 holds the sum of a, row 1 of c, row 2 of b,
+// row 3 of d (each over the 4 rows of its input).
+__device__ __forceinline__ float sum_rows4(float a, float b, float c, float d) {
+    const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    const float X = __uint_as_float(x[0]) + __uint_as_float(x[1]);  // {a02, a13, b02, b13}
+    const auto y = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(d), false, false);
+    const float Y = __uint_as_float(y[0]) + __uint_as_float(y[1]);  // {c02, c13, d02, d13}
+    const auto z = __builtin_amdgcn_permlane16_swap(__float_as_uint(X), __float_as_uint(Y), false, false);
+    return __uint_as_float(z[0]) + __uint_as_float(z[1]);           // {a, c, b, d}
 }
 
 // ---------------------------------------------------------------------------

@@ -15,14 +15,17 @@
 // 3. decode: one persistent workgroup (8 waves) per CU. The requests' tokens are laid
 //    end to end and cut into `grid` equal contiguous ranges, so every workgroup
 //    streams the same number of cache rows whatever the lengths are; a range that
-//    crosses a request boundary emits one split-K partial per request. A tile is one
-//    16-token page; whole rows are copied global->LDS with 16-byte LDS-DMA loads,
-//    three pages in flight. The current request's AB lives in VGPRs (each wave holds
-//    a contiguous slice of rank tiles); z = AB . [cos|sin]^T runs on MFMA with the
-//    page's 16 positions as N, and each lane multiplies its 4 z values by its 4 codes
-//    (bf16/fp16, or unpacked nibbles). Per-tile partials meet in LDS, an online
-//    softmax per (head, token) follows, then P[H, 16] @ V[16, r_v] on
-//    v_mfma_f32_32x32x16 with the accumulator kept in LDS.
+//    crosses a request boundary emits one split-K partial per request. A page is 16
+//    tokens. Its rows and its 16 cos/sin rows are copied global->LDS by buffer loads
+//    with the LDS bit (16 bytes per lane, no VALU address work: every lane's offset
+//    inside a page is fixed for the whole kernel), three pages in flight. Each wave
+//    holds a contiguous run of the request's rank tiles of AB in VGPRs; per tile,
+//    z = AB . [cos|sin]^T runs on MFMA with the page's 16 positions as N, and each
+//    lane folds its 4 z values with its 4 codes. Four tiles' partial logits are summed
+//    over the wave's row groups in one go with the gfx950 lane swaps. An online
+//    softmax per (head, token) follows (lazy running max: the reference point moves
+//    only when a logit exceeds it by 2^8), and P[16 heads, 16] @ V[16, 16 cols] runs
+//    on v_mfma_f32_16x16x16 one page later, so a page costs two workgroup barriers.
 // 4. merge: per (request, head) log-sum-exp of the partials, then the lift through
 //    v_up_by_q.
 #include <stdio.h>
@@ -35,21 +38,36 @@ namespace starkv {
 
 enum { FMT_BF16 = 0, FMT_F16 = 1, FMT_Q4 = 2 };
 
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+
 constexpr int NWAVE = 8;
 constexpr int NTHR = NWAVE * 64;
 constexpr int TILE_TOK = 16;
 constexpr int MAX_REQ_PER_CALL = 1024;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int AB_TILE_BYTES = 4 * 64 * 16;  // 4 K-steps x 64 lanes x 8 fp16
-constexpr int AB_SLACK_TILES = 16;
-constexpr int MAX_TT = 96;                   // rank tiles per call (W <= 1536 for MHA)           // a wave may read up to 10 tiles past its range
+constexpr int AB_SLACK_TILES = 16;          // a wave loads up to MT tiles from its first one
+constexpr int MAX_TT = 96;                  // rank tiles per call (k_width x heads per kv head <= 1536)
+constexpr int MAX_H = 32;                   // query heads (one softmax item per thread)
+constexpr int MT = 10;                      // rank tiles per wave held in VGPRs; more stream from L2
+constexpr int MAX_NLD = 6;                  // 16-byte copies per lane per page (bf16/fp16 rows)
+constexpr int NLD_Q4 = 3;                   // 3.2-bit rows
+constexpr int CS_ROW_LDS = 256;            // LDS bytes per cos/sin row (granules XOR-swizzled by row)
+constexpr int CS_CHUNKS = 4;                // 16 rows x 16 granules -> 4 copies of 64 granules
+constexpr int XB_LOWRANK = 48 * 1024;       // LDS bytes per page buffer
+constexpr int XB_Q4 = 24 * 1024;
+constexpr int MAX_PV_UNITS = 4 * NWAVE;     // 16 x 16 output tiles of P @ V
+constexpr float LAZY_MAX = 8.f;             // log2 headroom before the running max moves
 
 // Workspace layout, in bytes from the base (every region 256-byte aligned):
 //   hdr    int   [2 + n]      S (tokens per workgroup), P[0..n] (prefix of clamped lengths)
 //   tiles  int4  [TT]         {q head, first cache lane, valid | nout << 8 | last << 16, kv head}
 //   htile  int2  [Hq]         {first tile, tiles} per query head
 //   ab     fp16  [n][TT][4][64][8]
-//   m, l   fp32  [slots][Hq]  (log2-domain running max and sum per partial)
+//   m, l   fp32  [slots][Hq]  (log2-domain reference max and sum per partial)
 //   acc    fp32  [slots][Hq][v_rank]
 struct WsLayout {
     size_t hdr, tiles, htile, ab, m, l, acc, total;
@@ -78,13 +96,12 @@ struct DecodeParams {
     const int32_t* bt; int64_t bt_s0, bt_s1;
     int n, Hq, TT, k_width, v_rank;
     int ks_off, vs_off, vq_off, v_nout, v_nbo;     // QuantRow (3.2-bit)
-    int row_g, pitch_g, kv_bytes;                  // LDS staging geometry (granules of 16 bytes)
-    int ngr, nld;                                  // granules per page (rows + cos/sin), copies per wave
-    float inv_pitch;
-    const uint8_t* cs; int64_t cs_s0b; int cs_dt;  // cos/sin table, row stride in bytes, 2-byte dtype
+    int row_g, pitch_g, pitch_b;                   // row granules (16 B), LDS row pitch (granules, bytes)
+    int nkv, nch, nld, cs_lds;                     // copies of 64 granules: K/V rows, all; per wave; cos/sin offset
+    const uint8_t* cs; int cs_s0b;                 // fp16 cos/sin table, row stride in bytes
     uint8_t* ws;
     size_t ws_tiles, ws_htile, ws_ab, ws_m, ws_l, ws_acc;
-    int slots, units, ncol_t, hpad;
+    int ncb, units;                                // P @ V: 16-column blocks, 16 x 16 tiles
 };
 
 __device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -149,24 +166,28 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
 }
 
 // ---------------------------------------------------------------------------
-// 2. fold: AB[b][t][ks][lane] = 8 fp16 of row r = tile lane0 + (lane & 15), columns
-//    32 ks + 8 (lane >> 4) .. +8, scaled by scale*log2(e); rows past the head's
-//    rank are zero (paged_decode.py:79-81 masks them).
+// 2. fold: AB[b][t][ks][lane] = 8 fp16 of tile row m = lane & 15, columns
+//    32 ks + 8 (lane >> 4) .. +8, scaled by scale*log2(e); rows past the head's rank
+//    are zero (paged_decode.py:79-81 masks them). Row m holds rank m of the tile, or,
+//    for the 3.2-bit cache (perm = 1), rank (m >> 2) + 4 (m & 3): then the z values a
+//    lane receives (rows 4g .. 4g+3) are ranks g, g+4, g+8, g+12, whose codes are the
+//    nibbles a lane extracts from the tile's 8 bytes with one shift.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void fold_tiles_kernel(const void* __restrict__ q, int64_t q_s0, int64_t q_s1,
                                                          int q_dt, const void* __restrict__ k_up, int64_t ku_s0,
                                                          int ku_dt, const uint8_t* __restrict__ ws_tiles_p, int TT,
-                                                         float sc, uint8_t* __restrict__ ab) {
+                                                         float sc, int perm, uint8_t* __restrict__ ab) {
     const int b = blockIdx.y;
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;  // (tile, k2, lane)
     const int t = idx >> 7, k2 = (idx >> 6) & 1, lane = idx & 63;
     if (t >= TT) return;
     const int4 tm = ((const int4*)ws_tiles_p)[t];
-    const int lr = lane & 15, lg = lane >> 4;
+    const int m = lane & 15, lg = lane >> 4;
+    const int rr = perm ? (m >> 2) + 4 * (m & 3) : m;
     const int c0 = 32 * k2 + 8 * lg;
-    const int64_t ur = (int64_t)(tm.y + lr) * ku_s0;
+    const int64_t ur = (int64_t)(tm.y + rr) * ku_s0;
     const int64_t qh = (int64_t)b * q_s0 + (int64_t)tm.x * q_s1;
-    const float s = lr < (tm.z & 255) ? sc : 0.f;
+    const float s = rr < (tm.z & 255) ? sc : 0.f;
     float u0[8], u1[8], q0[8], q1[8];
     load8_f(k_up, ur + c0, ku_dt, u0);
     load8_f(k_up, ur + c0 + 64, ku_dt, u1);
@@ -212,7 +233,7 @@ __device__ __forceinline__ void cur_first(Cursor& c, cint_p P, int n, int beg, i
     if (c.valid) cur_set(c, P, beg, end);
 }
 
-// Returns true when the next tile starts a new request (the current one ended).
+// Returns true when the next page starts a new request (the current one ended).
 __device__ __forceinline__ bool cur_next(Cursor& c, cint_p P, int n, int beg, int end) {
     if (TILE_TOK * (c.k + 1) < c.hi) {
         ++c.k;
@@ -230,312 +251,371 @@ __device__ __forceinline__ bool cur_next(Cursor& c, cint_p P, int n, int beg, in
 }
 
 // ---------------------------------------------------------------------------
-// Global -> LDS copy of one page with 16-byte LDS-DMA loads: the 16 token rows at
-// a pitch of pitch_g granules (odd, so rows fall on different banks; granules past
-// row_g are filler), then the page's 16 cos/sin rows at a pitch of 17 granules.
-// Every wave issues exactly nld copies (surplus ones land in `dummy`), so one
+// Global -> LDS copy of one page. LDS layout of a page buffer: the 16 token rows at a
+// pitch of pitch_g granules (odd, so rows fall on different banks; granules past row_g
+// are filler), padded to whole 1 KB copies, then the 16 cos/sin rows of the page's
+// positions, 256 bytes each, granule c of row r stored at granule c ^ r (so the MFMA
+// operand reads of 16 rows hit distinct banks). Copy i of wave w is 1 KB chunk i*8 + w; lane q
+// of it moves granule 64*chunk + q, whose offset inside the page (or inside the page's
+// cos/sin rows) is the same for every page: `doff`. Each page gets two buffer
+// descriptors whose size covers only the request's rows, so rows past the end of a
+// request read as zero without touching memory. Every wave issues exactly NLD copies;
+// surplus ones use an empty descriptor (no memory access) and land in `dummy`, so one
 // vmcnt value covers a page on every wave.
 // ---------------------------------------------------------------------------
+template <int NLD>
 __device__ __forceinline__ void dma_page(const DecodeParams& p, const Cursor& c, cint_p P, uint8_t* buf,
-                                         uint8_t* dummy, int wave, int lane) {
-    const int64_t tok0 = (int64_t)TILE_TOK * c.k;
+                                         uint8_t* dummy, int wave, const uint32_t (&doff)[MAX_NLD]) {
+    wave = opaque_s(wave);  // LDS destinations recomputed per page
+    const int tok0 = TILE_TOK * c.k;
     const int blk = ((cint_p)p.bt)[c.b * p.bt_s0 + (tok0 / p.block_size) * p.bt_s1];
-    const uint8_t* page = p.cache + (int64_t)blk * p.c_s0 + (tok0 % p.block_size) * p.c_s1;
-    const int last = P[c.b + 1] - P[c.b] - 1;  // clamp positions to the request's last token
-    const int kvg = TILE_TOK * p.pitch_g;
-    const int ln = opaque(lane);
-    for (int i = 0; i < p.nld; ++i) {
+    const uint8_t* page = p.cache + (int64_t)blk * p.c_s0 + (int64_t)(tok0 % p.block_size) * p.c_s1;
+    const int rows = min(TILE_TOK, P[c.b + 1] - P[c.b] - tok0);
+    const __amdgpu_buffer_rsrc_t rkv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)page, (short)0, rows * (int)p.c_s1, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rcs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.cs + (int64_t)tok0 * p.cs_s0b), (short)0, rows * p.cs_s0b, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rnull = __builtin_amdgcn_make_buffer_rsrc((void*)p.cs, (short)0, 0, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
         const int ch = i * NWAVE + wave;
-        const int q = ch * 64 + ln;
-        const uint8_t* src;
-        if (q < kvg) {
-            const int row = (int)(((float)q + 0.5f) * p.inv_pitch);
-            const int gr = q - row * p.pitch_g;
-            src = page + row * p.c_s1 + (gr < p.row_g ? gr * 16 : 0);
-        } else {
-            const int qc = min(q - kvg, 16 * 17 - 1);
-            const int row = qc / 17, gr = qc - row * 17;
-            const int64_t pos = min(tok0 + row, (int64_t)last);
-            src = p.cs + pos * p.cs_s0b + (gr < 16 ? gr * 16 : 0);
-        }
-        uint8_t* dst = ch * 64 < p.ngr ? buf + ch * 1024 : dummy;
-        if (q >= p.ngr) src = p.cs;  // surplus lanes: any readable address
-        __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+        uint8_t* dst = ch < p.nch ? buf + ch * 1024 : dummy;
+        const __amdgpu_buffer_rsrc_t r = ch < p.nkv ? rkv : ch < p.nch ? rcs : rnull;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, doff[i], 0, 0,
+                                                 0);
     }
+}
+
+// The kernel's parameter block, read through a pointer the optimizer cannot see
+// through: loads of it are redone where they are used (scalar loads that hit the
+// scalar cache) instead of being hoisted out of the main loop into SGPRs.
+typedef const __attribute__((address_space(4))) DecodeParams kparams_t;
+
+__device__ __forceinline__ const DecodeParams& params() {
+    kparams_t* pp = (kparams_t*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(pp));
+    return *(const DecodeParams*)pp;  // address-space inference keeps these scalar loads
 }
 
 __device__ __forceinline__ int4 load_tile(cint_p tiles, int t) {
     return make_int4(tiles[4 * t], tiles[4 * t + 1], tiles[4 * t + 2], tiles[4 * t + 3]);
 }
 
-// One rank tile: z = AB_tile . cs^T (16 ranks x 16 tokens) and the lane's 4-code product,
-// reduced over the 4 row groups; lanes 0..15 write the tile's per-token partial(s).
-template <int FMT>
-__device__ __forceinline__ void tile_product(const half8_t* a, const half8_t* csb, const uint8_t* xrow, int4 tm,
-                                             int lane, int lg, float* s_spart, int tile) {
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t h2_bits(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+__device__ __forceinline__ half2_t cvt_h2(float a, float b) {
+    return __builtin_convertvector((float2_t){a, b}, half2_t);  // v_cvt_pk_f16_f32, round to nearest even
+}
+__device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+
+__device__ __forceinline__ f32x4_t mfma_tile(const half8_t (&a)[4], const half8_t (&cs)[4]) {
     f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-    z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], csb[0], z, 0, 0, 0);
-    z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1], csb[1], z, 0, 0, 0);
-    z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[2], csb[2], z, 0, 0, 0);
-    z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[3], csb[3], z, 0, 0, 0);
-    if (FMT == FMT_Q4) {
-        // 4 nibbles: lanes x_off + 4 lg .. +4 of token (lane & 15); outlier and inlier sums.
-        const uint32_t w = *(const uint16_t*)(xrow + (tm.y >> 1) + 2 * lg);
-        const int cnt = min(max(((tm.z >> 8) & 255) - 4 * lg, 0), 4);
-        float d = 0.f, dout = 0.f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float v = ((float)((w >> (4 * e)) & 15u) - 8.f) * z[e];
-            d += v;
-            dout += e < cnt ? v : 0.f;
-        }
-        float din = d - dout;
-        din += __shfl_xor(din, 16, 64);
-        dout += __shfl_xor(dout, 16, 64);
-        din += __shfl_xor(din, 32, 64);
-        dout += __shfl_xor(dout, 32, 64);
-        // Lanes 16..63 hold copies of lanes 0..15: they write into the dummy slot.
-        ((float2*)s_spart)[(lane < 16 ? tile : MAX_TT + 1) * 16 + (lane & 15)] = make_float2(din, dout);
+    z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], cs[0], z, 0, 0, 0);
+    z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1], cs[1], z, 0, 0, 0);
+    z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[2], cs[2], z, 0, 0, 0);
+    z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[3], cs[3], z, 0, 0, 0);
+    return z;
+}
+
+// A lane's share of one rank tile's logit for token (lane & 15): its 4 z values (rows
+// 4g .. 4g+3, g = lane >> 4) times their codes. 3.2-bit: the codes are nibbles n with
+// value n - 8, built as fp16 (1024 + n) - 1032 (exact); the scales are applied per
+// (token, head) from the row's bf16 (outlier, inlier) pair, the outlier part from the
+// lane's first k elements (k = outlier ranks among its 4, from the tile's count).
+template <int FMT>
+__device__ __forceinline__ float tile_dot(const f32x4_t& z, const uint8_t* xr, int lane0, int head, int c, int k,
+                                          int lg, int ks_off, const uint2* s_kmask) {
+    if (FMT == FMT_BF16) {
+        const uint2 w = *(const uint2*)(xr + 2 * lane0 + 8 * lg);
+        float v = __uint_as_float(w.x << 16) * z[0];
+        v = fmaf(__uint_as_float(w.x & 0xffff0000u), z[1], v);
+        v = fmaf(__uint_as_float(w.y << 16), z[2], v);
+        return fmaf(__uint_as_float(w.y & 0xffff0000u), z[3], v);
+    } else if (FMT == FMT_F16) {
+        const uint2 w = *(const uint2*)(xr + 2 * lane0 + 8 * lg);
+        return dot2(as_h2(w.x), cvt_h2(z[0], z[1]), dot2(as_h2(w.y), cvt_h2(z[2], z[3]), 0.f));
     } else {
-        const uint2 w = *(const uint2*)(xrow + 2 * (tm.y + 4 * lg));
-        float x0, x1, x2, x3;
-        if (FMT == FMT_BF16) {
-            x0 = __uint_as_float(w.x << 16); x1 = __uint_as_float(w.x & 0xffff0000u);
-            x2 = __uint_as_float(w.y << 16); x3 = __uint_as_float(w.y & 0xffff0000u);
-        } else {
-            _Float16 h[4];
-            uint32_t ww[2] = {w.x, w.y};
-            memcpy(h, ww, 8);
-            x0 = (float)h[0]; x1 = (float)h[1]; x2 = (float)h[2]; x3 = (float)h[3];
-        }
-        float v = x0 * z[0] + x1 * z[1] + x2 * z[2] + x3 * z[3];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        // Lanes 16..63 hold copies of lanes 0..15: they write into the dummy slot.
-        s_spart[(lane < 16 ? tile : MAX_TT + 1) * 16 + (lane & 15)] = v;
+        const uint2 w = *(const uint2*)(xr + (lane0 >> 1));
+        const uint32_t sh = 4 * lg;
+        const half2_t off = {(_Float16)1032.f, (_Float16)1032.f};
+        const half2_t x0 = as_h2(((w.x >> sh) & 0x000F000Fu) | 0x64006400u) - off;  // ranks g, g+4
+        const half2_t x1 = as_h2(((w.y >> sh) & 0x000F000Fu) | 0x64006400u) - off;  // ranks g+8, g+12
+        const half2_t z01 = cvt_h2(z[0], z[1]), z23 = cvt_h2(z[2], z[3]);
+        const float d = dot2(x0, z01, dot2(x1, z23, 0.f));
+        const uint32_t sw = *(const uint32_t*)(xr + ks_off + 4 * head);
+        const float si = __uint_as_float(sw & 0xffff0000u);
+        if (c == 0) return si * d;
+        const uint2 mk = s_kmask[k];
+        const float dout =
+            dot2(as_h2(h2_bits(x0) & mk.x), z01, dot2(as_h2(h2_bits(x1) & mk.y), z23, 0.f));
+        return fmaf(__uint_as_float(sw << 16), dout, si * (d - dout));
     }
 }
 
-constexpr int MAX_HPAD = 64;     // query heads, padded to the PV MFMA's 32
-constexpr int XB_LOWRANK = 48 * 1024;
-constexpr int XB_Q4 = 24 * 1024;
+struct WaveTiles {
+    int ts, ntw;                       // first tile, tiles of this wave
+    int lane0[MT], head[MT], c[MT];    // per slot: first cache lane, query head, outlier lanes
+};
+
+// K side of one page: every tile of this wave, partial logits into s_part[tile][token].
+template <int FMT>
+__device__ __forceinline__ void k_side(const DecodeParams& p, const WaveTiles& wt, const half8_t (&ab)[MT][4],
+                                       const uint8_t* XC, float* s_part, const uint2* s_kmask, uint32_t kpack,
+                                       int lane, int cur_b) {
+    const int ln = opaque(lane);  // LDS addresses are recomputed per page, not held per buffer and tile
+    const int lr = ln & 15, lg = ln >> 4;
+    half8_t csb[4];  // B operand: position lr of the page, K elements 32 ks + 8 lg .. +8 (granule 4 ks + lg)
+    {
+        const uint8_t* csr = XC + p.cs_lds + lr * CS_ROW_LDS;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) csb[ks] = *(const half8_t*)(csr + (((4 * ks + lg) ^ lr) << 4));
+    }
+    const uint8_t* xr = XC + lr * p.pitch_b;
+    const int rslot = ((lg & 1) << 1) | (lg >> 1);  // sum_rows4 puts inputs (a, b, c, d) in rows (0, 2, 1, 3)
+    const int ntw = opaque_s(wt.ntw), ts = opaque_s(wt.ts);
+    float v[4];
+    f32x4_t zc = {0.f, 0.f, 0.f, 0.f}, zn = zc;
+    if (0 < ntw) zc = mfma_tile(ab[0], csb);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        // The next tile's MFMAs are issued before this tile's VALU work.
+        if (i + 1 < MT && i + 1 < ntw) zn = mfma_tile(ab[i + 1], csb);
+        v[i & 3] = 0.f;
+        if (i < ntw)
+            v[i & 3] = tile_dot<FMT>(zc, xr, opaque_s(wt.lane0[i]), opaque_s(wt.head[i]), opaque_s(wt.c[i]),
+                                     (kpack >> (3 * i)) & 7, lg, p.ks_off, s_kmask);
+        zc = zn;
+        if ((i & 3) == 3 || i == MT - 1) {  // four tiles (or the last ones): one reduction over the row groups
+            const int g = i >> 2;
+            if (4 * g < ntw) {
+                const float r = sum_rows4(v[0], (i & 3) >= 1 ? v[1] : 0.f, (i & 3) >= 2 ? v[2] : 0.f,
+                                          (i & 3) >= 3 ? v[3] : 0.f);
+                const int slot = 4 * g + rslot;
+                s_part[(slot < ntw ? ts + slot : MAX_TT) * TILE_TOK + lr] = r;
+            }
+        }
+    }
+    // Tiles past MT: AB from the workspace (L2) on every page.
+    if (wt.ntw > MT) {
+        cint_p tiles = (cint_p)(p.ws + p.ws_tiles);
+        const half8_t* abg = (const half8_t*)(p.ws + p.ws_ab + ((size_t)cur_b * p.TT + wt.ts) * AB_TILE_BYTES);
+        for (int i = MT; i < wt.ntw; ++i) {
+            half8_t a[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) a[ks] = abg[(i * 4 + ks) * 64 + lane];
+            const int4 tm = load_tile(tiles, wt.ts + i);
+            const int c = (tm.z >> 8) & 255;
+            const int k = min(max((c - lg + 3) >> 2, 0), 4);
+            const float r = sum_rows(tile_dot<FMT>(mfma_tile(a, csb), xr, tm.y, tm.x, c, k, lg, p.ks_off, s_kmask));
+            if (lane < 16) s_part[(wt.ts + i) * TILE_TOK + lr] = r;
+        }
+    }
+}
+
+// Online softmax state of this thread's (head, token) item: head tid >> 4, token
+// column tid & 15 (heads <= 32, so one item per thread).
+struct SmState {
+    float m, l;  // log2-domain reference max (same on the head's 16 lanes), this lane's column sum
+    int ht0, htn;
+    bool on;
+};
+
+template <int FMT>
+__device__ __forceinline__ void softmax_page(SmState& sm, const float* s_part, uint16_t* s_p, uint16_t* s_plo,
+                                             float* s_alpha, int tid, int tok0, int lo, int hi) {
+    if (!sm.on) return;
+    tid = opaque(tid);  // LDS addresses recomputed per page
+    const int r = tid & 15;
+    float s = 0.f;
+    for (int t = 0; t < sm.htn; ++t) s += s_part[(sm.ht0 + t) * TILE_TOK + r];
+    s = tok0 + r >= lo && tok0 + r < hi ? s : -INFINITY;
+    float alpha = 1.f;
+    if (__builtin_amdgcn_ballot_w64(s > sm.m + LAZY_MAX) != 0) {
+        const float mn = fmaxf(sm.m, row16_max(s));
+        alpha = __builtin_amdgcn_exp2f(sm.m - mn);
+        sm.m = mn;
+    }
+    const float pe = __builtin_amdgcn_exp2f(s - sm.m);
+    sm.l = fmaf(sm.l, alpha, pe);
+    if (FMT == FMT_BF16) {
+        // P = hi + lo in two bfloat16 parts: the P @ V product keeps ~16 bits of P.
+        const __bf16 ph = (__bf16)pe;
+        const __bf16 pl = (__bf16)(pe - (float)ph);
+        s_p[tid] = __builtin_bit_cast(uint16_t, ph);
+        s_plo[tid] = __builtin_bit_cast(uint16_t, pl);
+    } else {
+        s_p[tid] = __builtin_bit_cast(uint16_t, (_Float16)pe);
+    }
+    if (r == 0) s_alpha[tid >> 4] = alpha;
+}
+
+// m and l of the partial that ends with this page, then reset.
+__device__ __forceinline__ void flush_ml(const DecodeParams& p, SmState& sm, int slot, int tid) {
+    if (!sm.on) return;
+    const float lt = row16_sum(sm.l);
+    if ((tid & 15) == 0) {
+        const int64_t i = (int64_t)slot * p.Hq + (tid >> 4);
+        ((float*)(p.ws + p.ws_m))[i] = sm.m;
+        ((float*)(p.ws + p.ws_l))[i] = lt;
+    }
+    sm.m = -INFINITY;
+    sm.l = 0.f;
+}
+
+struct PvUnits {
+    bool on[4];
+    int hb[4], cb[4];  // head block (16 heads), column block (16 V columns)
+};
+
+// acc[unit] = alpha * acc + P[16 heads, 16 tokens] @ V[16 tokens, 16 columns] for page X.
+// Lane l holds A = P[head 16 hb + (l & 15)][tokens 4 (l >> 4) .. +4] and B = V[same
+// tokens][column 16 cb + (l & 15)]; the result row 4 (l >> 4) + e, column l & 15.
+template <int FMT, int UPW>
+__device__ __forceinline__ void pv_page(const DecodeParams& p, const PvUnits& pu, f32x4_t (&acc)[UPW],
+                                        const uint8_t* X, const uint16_t* s_p, const uint16_t* s_plo,
+                                        const float* s_alpha, int lane) {
+    const int ln = opaque(lane);  // per-lane addresses are recomputed here, not held across the loop
+    const int lr = ln & 15, lg = ln >> 4;
+#pragma unroll
+    for (int k = 0; k < UPW; ++k) {
+        if (!pu.on[k]) continue;
+        const int hb = pu.hb[k];
+        const f32x4_t al = *(const f32x4_t*)(s_alpha + 16 * hb + 4 * lg);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[k][e] *= al[e];
+        const int prow = (16 * hb + lr) * TILE_TOK + 4 * lg;
+        const uint2 pa = *(const uint2*)(s_p + prow);
+        const int c = 16 * pu.cb[k] + lr;  // columns past v_rank compute garbage that is never stored
+        const uint8_t* rows = X + 4 * lg * p.pitch_b;
+        uint32_t b0, b1;
+        if (FMT == FMT_Q4) {
+            const bool o = c < p.v_nout;
+            const int ci = o ? c : c - p.v_nout;
+            const int vb = p.vq_off + (o ? 0 : p.v_nbo) + (ci >> 1);
+            const int vsh = 4 * (ci & 1);
+            const int vso = p.vs_off + (o ? 0 : 2);
+            float val[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint8_t* rp = rows + e * p.pitch_b;
+                const int nib = (int)((rp[vb] >> vsh) & 15u) - 8;
+                val[e] = (float)nib * __uint_as_float((uint32_t)(*(const uint16_t*)(rp + vso)) << 16);
+            }
+            b0 = h2_bits(cvt_h2(val[0], val[1]));
+            b1 = h2_bits(cvt_h2(val[2], val[3]));
+        } else {
+            const uint8_t* vp = rows + 2 * (p.k_width + c);
+            const uint32_t u0 = *(const uint16_t*)vp, u1 = *(const uint16_t*)(vp + p.pitch_b);
+            const uint32_t u2 = *(const uint16_t*)(vp + 2 * p.pitch_b), u3 = *(const uint16_t*)(vp + 3 * p.pitch_b);
+            b0 = u0 | (u1 << 16);
+            b1 = u2 | (u3 << 16);
+        }
+        const uint2 bv = make_uint2(b0, b1);
+        if (FMT == FMT_BF16) {
+            const uint2 pl = *(const uint2*)(s_plo + prow);
+            acc[k] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_t, pa),
+                                                               __builtin_bit_cast(short4_t, bv), acc[k], 0, 0, 0);
+            acc[k] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_t, pl),
+                                                               __builtin_bit_cast(short4_t, bv), acc[k], 0, 0, 0);
+        } else {
+            acc[k] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, pa),
+                                                           __builtin_bit_cast(half4_t, bv), acc[k], 0, 0, 0);
+        }
+    }
+}
+
+template <int UPW>
+__device__ __forceinline__ void flush_acc(const DecodeParams& p, const PvUnits& pu, f32x4_t (&acc)[UPW], int slot,
+                                          int lane) {
+    float* wa = (float*)(p.ws + p.ws_acc) + (int64_t)slot * p.Hq * p.v_rank;
+    const int ln = opaque(lane);
+    const int lr = ln & 15, lg = ln >> 4;
+#pragma unroll
+    for (int k = 0; k < UPW; ++k) {
+        if (!pu.on[k]) continue;
+        const int c = 16 * pu.cb[k] + lr;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int h = 16 * pu.hb[k] + 4 * lg + e;
+            if (h < p.Hq && c < p.v_rank) wa[(int64_t)h * p.v_rank + c] = acc[k][e];
+            acc[k][e] = 0.f;
+        }
+    }
+}
 
 struct LoopState {
     Cursor cc, ld;
-    int issued, j, beg, end, S, g;
-    bool new_seg;
+    int issued, j, beg, end, g;
+    bool new_seg, prev_valid, prev_end;
+    int prev_b;
+};
+
+struct Shared {
+    uint8_t* dummy;
+    float* part;
+    uint16_t* p;
+    uint16_t* plo;
+    float* alpha;
+    const uint2* kmask;
 };
 
 // ---------------------------------------------------------------------------
-// One page of the decode loop. XC holds the page being computed (its copies were
-// issued two pages ago); XN receives the page two ahead. Distinct __shared__
-// arrays per buffer let the compiler see that reads of XC never alias the copies
-// still in flight, so no vmcnt(0) is inserted before them.
+// One page of the decode loop. XC holds page j (copied two pages ago), XP page j - 1
+// (its P @ V runs now, after the barrier that publishes its P) and then receives page
+// j + 2. Distinct __shared__ arrays per buffer let the compiler see that reads of XC
+// never alias the copies in flight into XP, so no vmcnt(0) is inserted before them.
+//   B1  wait for this wave's copies of page j (and its LDS writes); barrier
+//       P @ V of page j - 1 (+ its partial if it ended a request); K side of page j
+//   B2  barrier (partial logits complete; every read of XP done)
+//       copies of page j + 2 into XP; softmax of page j
 // ---------------------------------------------------------------------------
-template <int FMT, int MT>
-__device__ __forceinline__ bool decode_page(const DecodeParams& p, LoopState& st, half8_t (&ab)[MT][4],
-                                            f32x16_t& acc, const uint8_t* XC, uint8_t* XN, uint8_t* dummy,
-                                            float* s_spart, uint16_t* s_p, uint16_t* s_plo, float* s_alpha,
-                                            float* s_m, float* s_l,
-                                            const int2* s_htile, int tid, int lane, int wave, int ts, int ntw) {
-    if (!st.cc.valid) return false;
+template <int FMT, int UPW, int NLD>
+__device__ __forceinline__ bool decode_iter(LoopState& st, const WaveTiles& wt, half8_t (&ab)[MT][4],
+                                            f32x4_t (&acc)[UPW], SmState& sm, const PvUnits& pu,
+                                            const uint32_t (&doff)[MAX_NLD], uint32_t kpack, const uint8_t* XC,
+                                            uint8_t* XP, const Shared& S, int tid, int lane, int wave) {
+    const DecodeParams& p = params();
     cint_p P = (cint_p)(p.ws + 4);
-    cint_p tiles = (cint_p)(p.ws + p.ws_tiles);
-    const int lr = lane & 15, lg = lane >> 4;
+    if (!st.cc.valid) {
+        if (st.prev_valid) {  // drain: P @ V of the last page, then its partial
+            wait_vmcnt_lgkm0(0);
+            lds_barrier();
+            pv_page<FMT, UPW>(p, pu, acc, XP, S.p, S.plo, S.alpha, lane);
+            flush_acc<UPW>(p, pu, acc, st.prev_b + st.g, lane);
+        }
+        return false;
+    }
     const Cursor cc = st.cc;
-    const int tok0 = TILE_TOK * cc.k;
-    const half8_t* ab_base = (const half8_t*)(p.ws + p.ws_ab + ((size_t)cc.b * p.TT + ts) * AB_TILE_BYTES);
     if (st.new_seg) {
-        // Tiles past this wave's range load whatever follows (the AB region has slack
-        // for it); their products go to a dummy slot.
+        // This request's AB into registers. Slots past the wave's range load what
+        // follows (the AB region has slack for it) and are never used.
+        const half8_t* abp = (const half8_t*)(p.ws + p.ws_ab + ((size_t)cc.b * p.TT + wt.ts) * AB_TILE_BYTES);
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) ab[i][ks] = ab_base[(i * 4 + ks) * 64 + lane];
-        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): AB is in registers
+            for (int ks = 0; ks < 4; ++ks) ab[i][ks] = abp[(i * 4 + ks) * 64 + lane];
+        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0)
     }
-
-    // B1: this page is in LDS for every wave (each waited for its own copies).
-    wait_vmcnt_lgkm0(st.issued > st.j + 1 ? p.nld : 0);
-    lds_barrier();
+    wait_vmcnt_lgkm0(st.issued > st.j + 1 ? NLD : 0);
+    lds_barrier();  // B1
+    if (st.prev_valid) {
+        pv_page<FMT, UPW>(p, pu, acc, XP, S.p, S.plo, S.alpha, lane);
+        if (st.prev_end) flush_acc<UPW>(p, pu, acc, st.prev_b + st.g, lane);
+    }
+    k_side<FMT>(p, wt, ab, XC, S.part, S.kmask, kpack, lane, cc.b);
+    wait_lgkm0_barrier();  // B2
     if (st.ld.valid) {
-        dma_page(p, st.ld, P, XN, dummy, wave, lane);
+        dma_page<NLD>(p, st.ld, P, XP, S.dummy, wave, doff);
         ++st.issued;
         cur_next(st.ld, P, p.n, st.beg, st.end);
     }
-
-    // Cos/sin B operand: lane (lr, lg) holds position tok0 + lr, K elements 32 ks + 8 lg .. +8.
-    half8_t csb[4];
-    {
-        const uint8_t* csr = XC + p.kv_bytes + lr * (17 * 16) + 16 * lg;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const uint4 w = *(const uint4*)(csr + 64 * ks);
-            if (p.cs_dt == STARKV_F16) {
-                memcpy(&csb[ks], &w, 16);
-            } else {
-                const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    csb[ks][2 * e] = (_Float16)__uint_as_float(ww[e] << 16);
-                    csb[ks][2 * e + 1] = (_Float16)__uint_as_float(ww[e] & 0xffff0000u);
-                }
-            }
-        }
-    }
-
-    // ---- K side ---------------------------------------------------------------
-    const uint8_t* xrow = XC + lr * p.pitch_g * 16;
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-        const int t = i < ntw ? ts + i : MAX_TT;  // MAX_TT: the dummy slot
-        tile_product<FMT>(ab[i], csb, xrow, load_tile(tiles, min(ts + i, p.TT - 1)), lane, lg, s_spart, t);
-    }
-    for (int i = MT; i < ntw; ++i) {
-        half8_t a[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) a[ks] = ab_base[(i * 4 + ks) * 64 + lane];
-        tile_product<FMT>(a, csb, xrow, load_tile(tiles, ts + i), lane, lg, s_spart, ts + i);
-    }
-    wait_lgkm0_barrier();  // B2: partial logits complete
-
-    // ---- softmax (log2 domain; the scale is folded into AB) -------------------
-    for (int idx = tid; idx < p.Hq * TILE_TOK; idx += NTHR) {
-        const int h = idx >> 4, r = idx & 15;
-        const int tok = tok0 + r;
-        const int2 ht = s_htile[h];
-        float s = -INFINITY;
-        if (tok >= cc.lo && tok < cc.hi) {
-            if (FMT == FMT_Q4) {
-                const uint32_t sw = *(const uint32_t*)(XC + r * p.pitch_g * 16 + p.ks_off + 4 * h);
-                const float so = __uint_as_float(sw << 16), si = __uint_as_float(sw & 0xffff0000u);
-                float din = 0.f, dout = 0.f;
-                for (int t = ht.x; t < ht.x + ht.y; ++t) {
-                    const float2 v = ((const float2*)s_spart)[t * 16 + r];
-                    din += v.x;
-                    dout += v.y;
-                }
-                s = si * din + so * dout;
-            } else {
-                s = 0.f;
-                for (int t = ht.x; t < ht.x + ht.y; ++t) s += s_spart[t * 16 + r];
-            }
-        }
-        const float m_old = s_m[h];
-        const float m_new = fmaxf(m_old, row16_max(s));
-        const float pe = exp2f(s - m_new);
-        const float alpha = exp2f(m_old - m_new);
-        const float psum = row16_sum(pe);
-        if (r == 0) {
-            s_m[h] = m_new;
-            s_l[h] = s_l[h] * alpha + psum;
-            s_alpha[h] = alpha;
-        }
-        if (FMT == FMT_BF16) {
-            // P = hi + lo in two bfloat16 parts: the PV product keeps ~16 bits of P.
-            const uint16_t hi = f32_to_bf16_rne(pe);
-            s_p[idx] = hi;
-            s_plo[idx] = f32_to_bf16_rne(pe - __uint_as_float((uint32_t)hi << 16));
-        } else {
-            _Float16 hv = (_Float16)pe;
-            uint16_t u;
-            memcpy(&u, &hv, 2);
-            s_p[idx] = u;
-        }
-    }
-    wait_lgkm0_barrier();  // B3: P and alpha complete
-
-    // ---- PV: acc[32 heads, 32 cols] = alpha * acc + P[32, 16] @ V[16, 32] -------
-    if (wave < p.units) {
-        const int ln = opaque(lane);
-        const int hb = wave / p.ncol_t, ct = wave % p.ncol_t;
-        const int c = ct * 32 + (ln & 31);
-        const int kh = ln >> 5;  // tokens 8 kh .. 8 kh + 7
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            const f32x4_t al = *(const f32x4_t*)(s_alpha + hb * 32 + 8 * q4 + 4 * kh);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[4 * q4 + e] *= al[e];
-        }
-        const uint4 pa = *(const uint4*)(s_p + (hb * 32 + (ln & 31)) * 16 + 8 * kh);
-        uint32_t bw[4];
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-            uint32_t hw[2];
-#pragma unroll
-            for (int e1 = 0; e1 < 2; ++e1) {
-                const int t = 8 * kh + 2 * e2 + e1;
-                const int tok = tok0 + t;
-                const uint8_t* rowp = XC + t * p.pitch_g * 16;
-                uint32_t bits = 0;
-                if (tok >= cc.lo && tok < cc.hi && c < p.v_rank) {
-                    if (FMT == FMT_Q4) {
-                        const bool o = c < p.v_nout;
-                        const int ci = o ? c : c - p.v_nout;
-                        const int byte = p.vq_off + (o ? 0 : p.v_nbo) + (ci >> 1);
-                        const uint32_t nib = (rowp[byte] >> (4 * (ci & 1))) & 15u;
-                        const uint32_t sw = *(const uint32_t*)(rowp + p.vs_off);
-                        const float sc = o ? __uint_as_float(sw << 16) : __uint_as_float(sw & 0xffff0000u);
-                        _Float16 hv = (_Float16)(((float)nib - 8.f) * sc);
-                        uint16_t u;
-                        memcpy(&u, &hv, 2);
-                        bits = u;
-                    } else {
-                        bits = *(const uint16_t*)(rowp + 2 * (p.k_width + c));
-                    }
-                }
-                hw[e1] = bits;
-            }
-            bw[e2] = hw[0] | (hw[1] << 16);
-        }
-        uint32_t aw[4] = {pa.x, pa.y, pa.z, pa.w};
-        if (FMT == FMT_BF16) {
-            const uint4 pl = *(const uint4*)(s_plo + (hb * 32 + (ln & 31)) * 16 + 8 * kh);
-            uint32_t lw[4] = {pl.x, pl.y, pl.z, pl.w};
-            bf16x8_t a, al, b;
-            memcpy(&a, aw, 16);
-            memcpy(&al, lw, 16);
-            memcpy(&b, bw, 16);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b, acc, 0, 0, 0);
-        } else {
-            half8_t a, b;
-            memcpy(&a, aw, 16);
-            memcpy(&b, bw, 16);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
-        }
-    }
-
-    // ---- end of this request's range: write the partial, reset ----------------
+    softmax_page<FMT>(sm, S.part, S.p, S.plo, S.alpha, tid, TILE_TOK * cc.k, cc.lo, cc.hi);
     Cursor nx = cc;
     const bool seg_end = cur_next(nx, P, p.n, st.beg, st.end);
-    if (seg_end) {
-        const int slot = cc.b + st.g;
-        float* wm = (float*)(p.ws + p.ws_m) + (int64_t)slot * p.Hq;
-        float* wl = (float*)(p.ws + p.ws_l) + (int64_t)slot * p.Hq;
-        float* wa = (float*)(p.ws + p.ws_acc) + (int64_t)slot * p.Hq * p.v_rank;
-        for (int h = tid; h < p.Hq; h += NTHR) {
-            wm[h] = s_m[h];
-            wl[h] = s_l[h];
-        }
-        if (wave < p.units) {
-            const int ln = opaque(lane);
-            const int hb = wave / p.ncol_t, ct = wave % p.ncol_t;
-            const int c = ct * 32 + (ln & 31);
-            const int kh = ln >> 5;
-#pragma unroll
-            for (int jj = 0; jj < 16; ++jj) {
-                const int h = hb * 32 + 8 * (jj >> 2) + 4 * kh + (jj & 3);
-                if (h < p.Hq && c < p.v_rank) wa[(int64_t)h * p.v_rank + c] = acc[jj];
-                acc[jj] = 0.f;
-            }
-        }
-        wait_lgkm0_barrier();  // every read of m and l is done before the reset
-        for (int h = tid; h < p.Hq; h += NTHR) {
-            s_m[h] = -INFINITY;
-            s_l[h] = 0.f;
-        }
-    }
+    if (seg_end) flush_ml(p, sm, cc.b + st.g, tid);
+    st.prev_valid = true;
+    st.prev_end = seg_end;
+    st.prev_b = cc.b;
     st.cc = nx;
     st.new_seg = seg_end;
     ++st.j;
@@ -543,75 +623,133 @@ __device__ __forceinline__ bool decode_page(const DecodeParams& p, LoopState& st
 }
 
 // ---------------------------------------------------------------------------
-// 3. decode. MT = rank tiles per wave held in VGPRs; a wave with more tiles reads
-//    the rest from the workspace (L2) on every page. XB = bytes per page buffer.
+// 3. decode. UPW = P @ V tiles per wave; XB = bytes per page buffer; NLD = copies
+//    per lane per page.
 // ---------------------------------------------------------------------------
-template <int FMT, int MT, int XB>
-__global__ __launch_bounds__(NTHR) void decode_kernel(const DecodeParams p) {
+template <int FMT, int UPW, int XB, int NLD>
+__global__ __launch_bounds__(NTHR) void decode_kernel(const DecodeParams p0) {
     __shared__ __attribute__((aligned(16))) uint8_t s_x0[XB];
     __shared__ __attribute__((aligned(16))) uint8_t s_x1[XB];
     __shared__ __attribute__((aligned(16))) uint8_t s_x2[XB];
     __shared__ __attribute__((aligned(16))) uint8_t s_dummy[1024];
-    __shared__ __attribute__((aligned(16))) float s_spart[(MAX_TT + 2) * TILE_TOK * (FMT == FMT_Q4 ? 2 : 1)];
-    __shared__ __attribute__((aligned(16))) uint16_t s_p[MAX_HPAD * TILE_TOK];
-    __shared__ __attribute__((aligned(16))) uint16_t s_plo[FMT == FMT_BF16 ? MAX_HPAD * TILE_TOK : 8];
-    __shared__ __attribute__((aligned(16))) float s_alpha[MAX_HPAD];
-    __shared__ float s_m[MAX_HPAD];
-    __shared__ float s_l[MAX_HPAD];
-    __shared__ int2 s_htile[MAX_HPAD];
+    __shared__ __attribute__((aligned(16))) float s_part[(MAX_TT + 1) * TILE_TOK];
+    __shared__ __attribute__((aligned(16))) uint16_t s_p[MAX_H * TILE_TOK];
+    __shared__ __attribute__((aligned(16))) uint16_t s_plo[FMT == FMT_BF16 ? MAX_H * TILE_TOK : 8];
+    __shared__ __attribute__((aligned(16))) float s_alpha[MAX_H];
+    __shared__ __attribute__((aligned(16))) uint2 s_kmask[8];
 
+    const DecodeParams& p = params();
     const int tid = threadIdx.x, lane = tid & 63, wave = rfl(tid >> 6);
-    for (int h = tid; h < p.Hq; h += NTHR) {
-        s_htile[h] = ((const int2*)(p.ws + p.ws_htile))[h];
-        s_m[h] = -INFINITY;
-        s_l[h] = 0.f;
-    }
-    for (int h = tid; h < p.hpad; h += NTHR) s_alpha[h] = 1.f;
-    for (int i = tid; i < p.hpad * TILE_TOK; i += NTHR) {
-        s_p[i] = 0;
-        if (FMT == FMT_BF16) s_plo[i] = 0;
-    }
-    __syncthreads();
-
+    const int lg = lane >> 4;
     cint_p P = (cint_p)(p.ws + 4);
     LoopState st;
     st.g = blockIdx.x;
-    st.S = ((cint_p)p.ws)[0];
+    const int S_tok = ((cint_p)p.ws)[0];
     const int T = P[p.n];
-    st.beg = min(st.g * st.S, T);
-    st.end = min(st.beg + st.S, T);
+    st.beg = min(st.g * S_tok, T);
+    st.end = min(st.beg + S_tok, T);
     if (st.beg >= st.end) return;
 
-    const int ts = (wave * p.TT) / NWAVE, ntw = ((wave + 1) * p.TT) / NWAVE - ts;
+    // Page buffers start zeroed: rows past a request's end are never copied, and
+    // must hold finite values (P is 0 there).
+    for (int i = tid; i < XB / 16; i += NTHR) {
+        ((uint4*)s_x0)[i] = make_uint4(0, 0, 0, 0);
+        ((uint4*)s_x1)[i] = make_uint4(0, 0, 0, 0);
+        ((uint4*)s_x2)[i] = make_uint4(0, 0, 0, 0);
+    }
+    for (int i = tid; i < MAX_H * TILE_TOK; i += NTHR) {
+        s_p[i] = 0;
+        if (FMT == FMT_BF16) s_plo[i] = 0;
+    }
+    if (tid < MAX_H) s_alpha[tid] = 1.f;
+    if (tid < 8) {  // fp16-pair masks of a lane's first k elements (pairs (0,1), (2,3))
+        const uint32_t m0 = tid >= 2 ? 0xffffffffu : tid == 1 ? 0x0000ffffu : 0u;
+        const uint32_t m1 = tid >= 4 ? 0xffffffffu : tid == 3 ? 0x0000ffffu : 0u;
+        s_kmask[tid] = make_uint2(m0, m1);
+    }
+
+    // This wave's rank tiles.
+    WaveTiles wt;
+    wt.ts = rfl((wave * p.TT) / NWAVE);
+    wt.ntw = rfl(((wave + 1) * p.TT) / NWAVE - wt.ts);
+    uint32_t kpack = 0;
+    {
+        cint_p tiles = (cint_p)(p.ws + p.ws_tiles);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            const int4 tm = load_tile(tiles, min(wt.ts + i, p.TT - 1));
+            wt.lane0[i] = tm.y;
+            wt.head[i] = tm.x;
+            wt.c[i] = (tm.z >> 8) & 255;
+            if (FMT == FMT_Q4) kpack |= (uint32_t)min(max((wt.c[i] - lg + 3) >> 2, 0), 4) << (3 * i);
+        }
+    }
+    // Softmax item.
+    SmState sm;
+    sm.on = tid < p.Hq * TILE_TOK;
+    {
+        const int2 ht = ((const int2*)(p.ws + p.ws_htile))[sm.on ? tid >> 4 : 0];
+        sm.ht0 = ht.x;
+        sm.htn = ht.y;
+    }
+    sm.m = -INFINITY;
+    sm.l = 0.f;
+    // P @ V tiles of this wave.
+    PvUnits pu;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int u = wave + NWAVE * k;
+        pu.on[k] = k < UPW && u < p.units;
+        pu.hb[k] = u / p.ncb;
+        pu.cb[k] = u - pu.hb[k] * p.ncb;
+    }
+    // Copy offsets of this lane inside a page.
+    uint32_t doff[MAX_NLD];
+#pragma unroll
+    for (int i = 0; i < MAX_NLD; ++i) {
+        const int ch = i * NWAVE + wave;
+        int off = 0;
+        if (i < NLD) {
+            if (ch < p.nkv) {
+                const int g = ch * 64 + lane;
+                const int row = g / p.pitch_g, col = g - row * p.pitch_g;
+                if (row < TILE_TOK && col < p.row_g) off = row * (int)p.c_s1 + col * 16;
+            } else {
+                const int g = (ch - p.nkv) * 64 + lane;  // LDS granule g holds granule (g & 15) ^ row of its row
+                const int row = g >> 4;
+                if (row < TILE_TOK) off = row * p.cs_s0b + (((g & 15) ^ row) << 4);
+            }
+        }
+        doff[i] = (uint32_t)off;
+    }
+    __syncthreads();
+
+    Shared S{s_dummy, s_part, s_p, s_plo, s_alpha, s_kmask};
     cur_first(st.cc, P, p.n, st.beg, st.end);
     st.ld = st.cc;
     st.issued = 0;
     st.j = 0;
     st.new_seg = true;
-    dma_page(p, st.ld, P, s_x0, s_dummy, wave, lane);
+    st.prev_valid = false;
+    st.prev_end = false;
+    st.prev_b = 0;
+    dma_page<NLD>(p, st.ld, P, s_x0, s_dummy, wave, doff);
     ++st.issued;
     cur_next(st.ld, P, p.n, st.beg, st.end);
     if (st.ld.valid) {
-        dma_page(p, st.ld, P, s_x1, s_dummy, wave, lane);
+        dma_page<NLD>(p, st.ld, P, s_x1, s_dummy, wave, doff);
         ++st.issued;
         cur_next(st.ld, P, p.n, st.beg, st.end);
     }
 
     half8_t ab[MT][4];
-    f32x16_t acc = {};
+    f32x4_t acc[UPW];
+#pragma unroll
+    for (int k = 0; k < UPW; ++k) acc[k] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
     while (true) {
-        if (!decode_page<FMT, MT>(p, st, ab, acc, s_x0, s_x2, s_dummy, s_spart, s_p, s_plo, s_alpha, s_m, s_l,
-                                  s_htile, tid,
-                                  lane, wave, ts, ntw))
-            break;
-        if (!decode_page<FMT, MT>(p, st, ab, acc, s_x1, s_x0, s_dummy, s_spart, s_p, s_plo, s_alpha, s_m, s_l,
-                                  s_htile, tid,
-                                  lane, wave, ts, ntw))
-            break;
-        if (!decode_page<FMT, MT>(p, st, ab, acc, s_x2, s_x1, s_dummy, s_spart, s_p, s_plo, s_alpha, s_m, s_l,
-                                  s_htile, tid,
-                                  lane, wave, ts, ntw))
-            break;
+        if (!decode_iter<FMT, UPW, NLD>(st, wt, ab, acc, sm, pu, doff, kpack, s_x0, s_x2, S, tid, lane, wave)) break;
+        if (!decode_iter<FMT, UPW, NLD>(st, wt, ab, acc, sm, pu, doff, kpack, s_x1, s_x0, S, tid, lane, wave)) break;
+        if (!decode_iter<FMT, UPW, NLD>(st, wt, ab, acc, sm, pu, doff, kpack, s_x2, s_x1, S, tid, lane, wave)) break;
     }
 }
 
@@ -713,22 +851,13 @@ struct DecodeProfile {
 };
 static DecodeProfile g_prof;
 
-static int mt_for(int TT) {
-    int mt = (TT + NWAVE - 1) / NWAVE;
-    if (mt <= 4) return 4;
-    if (mt <= 6) return 6;
-    if (mt <= 8) return 8;
-    return 10;  // beyond 10 tiles per wave the rest stream from L2 each page
-}
-
-template <int FMT, int XB>
-static int launch_decode(const DecodeParams& p, int mt, int grid, hipStream_t stream) {
+template <int FMT, int XB, int NLD>
+static int launch_decode(const DecodeParams& p, int upw, int grid, hipStream_t stream) {
     const void* fn = nullptr;
-    switch (mt) {
-        case 4: fn = (const void*)&decode_kernel<FMT, 4, XB>; break;
-        case 6: fn = (const void*)&decode_kernel<FMT, 6, XB>; break;
-        case 8: fn = (const void*)&decode_kernel<FMT, 8, XB>; break;
-        default: fn = (const void*)&decode_kernel<FMT, 10, XB>; break;
+    switch (upw) {
+        case 1: fn = (const void*)&decode_kernel<FMT, 1, XB, NLD>; break;
+        case 2: fn = (const void*)&decode_kernel<FMT, 2, XB, NLD>; break;
+        default: fn = (const void*)&decode_kernel<FMT, 4, XB, NLD>; break;
     }
     void* args[] = {(void*)&p};
     SKV_HIP(hipLaunchKernel(fn, dim3(grid), dim3(NTHR), args, 0, stream));
@@ -753,7 +882,7 @@ struct CommonArgs {
 
 static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_bytes, int TT, hipStream_t stream) {
     SKV_CHECK(a.n >= 1 && a.n <= MAX_REQ_PER_CALL, "decode: n=%d requests (1..%d per call)", a.n, MAX_REQ_PER_CALL);
-    SKV_CHECK(a.Hq >= 1 && a.Hq <= MAX_HPAD, "decode: num_heads=%d (1..%d)", a.Hq, MAX_HPAD);
+    SKV_CHECK(a.Hq >= 1 && a.Hq <= MAX_H, "decode: num_heads=%d (1..%d)", a.Hq, MAX_H);
     SKV_CHECK(a.max_seq_len >= 1, "decode: max_seq_len must be >= 1");
     SKV_CHECK(a.v_rank >= 1, "decode: v_rank must be >= 1");
     SKV_CHECK(a.grid >= 1, "decode: grid must be >= 1");
@@ -768,51 +897,53 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
               (long long)p.c_s1);
     SKV_CHECK(row_bytes % 16 == 0, "decode: cache row (%d bytes) must be a multiple of 16 bytes", row_bytes);
     SKV_CHECK(p.c_s1 >= row_bytes, "decode: slot stride %lld < row bytes %d", (long long)p.c_s1, row_bytes);
-    SKV_CHECK(a.cs_dt == STARKV_F16 || a.cs_dt == STARKV_BF16, "decode: cos_sin must be fp16 or bf16");
-    SKV_CHECK(a.cs_s0 % 8 == 0 && ((uintptr_t)a.cs % 16) == 0, "decode: cos_sin rows must be 16-byte aligned");
+    SKV_CHECK(p.c_s1 * TILE_TOK < ((int64_t)1 << 31), "decode: 16 slots span %lld bytes (>= 2^31)",
+              (long long)(p.c_s1 * TILE_TOK));
+    SKV_CHECK(a.cs_dt == STARKV_F16, "decode: cos_sin must be fp16 (convert the table once; it is exact for bf16)");
+    SKV_CHECK(a.cs_s0 % 8 == 0 && a.cs_s0 >= 128 && a.cs_s0 * 2 * TILE_TOK < ((int64_t)1 << 31) &&
+                  ((uintptr_t)a.cs % 16) == 0,
+              "decode: cos_sin rows must be 16-byte aligned with stride >= 128");
     SKV_CHECK(a.q_s1 % 8 == 0 && a.q_s0 % 8 == 0 && ((uintptr_t)a.q % 16) == 0,
               "decode: query rows must be 16-byte aligned (strides multiples of 8)");
     SKV_CHECK(a.ku_s0 % 8 == 0 && ((uintptr_t)a.k_up % 16) == 0, "decode: k_up rows must be 16-byte aligned");
-    const int ncol_t = (a.v_rank + 31) / 32;
-    const int hblk = (a.Hq + 31) / 32;
-    SKV_CHECK(ncol_t * hblk <= NWAVE, "decode: %d x %d PV tiles exceed %d waves (v_rank %d, heads %d)", hblk, ncol_t,
-              NWAVE, a.v_rank, a.Hq);
+    const int ncb = (a.v_rank + 15) / 16;
+    const int hblk = (a.Hq + 15) / 16;
+    const int units = ncb * hblk;
+    SKV_CHECK(units <= MAX_PV_UNITS, "decode: %d x %d P.V tiles exceed %d (v_rank %d, heads %d)", hblk, ncb,
+              MAX_PV_UNITS, a.v_rank, a.Hq);
+    const int upw = units <= NWAVE ? 1 : units <= 2 * NWAVE ? 2 : 4;
 
     p.bt = a.bt; p.bt_s0 = a.bt_s0; p.bt_s1 = a.bt_s1;
     p.n = a.n; p.Hq = a.Hq; p.TT = TT; p.v_rank = a.v_rank;
-    p.cs = (const uint8_t*)a.cs; p.cs_s0b = a.cs_s0 * 2; p.cs_dt = a.cs_dt;
+    p.cs = (const uint8_t*)a.cs; p.cs_s0b = (int)(a.cs_s0 * 2);
     p.row_g = row_bytes / 16;
     p.pitch_g = p.row_g | 1;
-    p.inv_pitch = 1.0f / (float)p.pitch_g;
-    p.kv_bytes = TILE_TOK * p.pitch_g * 16;
-    p.ngr = TILE_TOK * p.pitch_g + TILE_TOK * 17;
-    const int nch = (p.ngr + 63) / 64;
-    p.nld = (nch + NWAVE - 1) / NWAVE;
-    SKV_CHECK(p.nld <= 15, "decode: %d copies per wave per page (row %d bytes) exceeds 15", p.nld, row_bytes);
+    p.pitch_b = p.pitch_g * 16;
+    p.nkv = (TILE_TOK * p.pitch_g + 63) / 64;
+    p.cs_lds = p.nkv * 1024;
+    p.nch = p.nkv + CS_CHUNKS;
+    p.nld = (p.nch + NWAVE - 1) / NWAVE;
     const int xb = fmt == FMT_Q4 ? XB_Q4 : XB_LOWRANK;
-    SKV_CHECK(nch * 1024 <= xb, "decode: a page needs %d bytes of LDS (> %d): row %d bytes is too wide", nch * 1024,
-              xb, row_bytes);
+    SKV_CHECK(p.nld <= (fmt == FMT_Q4 ? NLD_Q4 : MAX_NLD) && p.nch * 1024 <= xb,
+              "decode: a page needs %d bytes of LDS (> %d): row %d bytes is too wide", p.nch * 1024, xb, row_bytes);
     p.ws = (uint8_t*)a.ws;
     p.ws_tiles = wl.tiles; p.ws_htile = wl.htile; p.ws_ab = wl.ab;
     p.ws_m = wl.m; p.ws_l = wl.l; p.ws_acc = wl.acc;
-    p.slots = a.grid + a.n;
-    p.ncol_t = ncol_t;
-    p.units = ncol_t * hblk;
-    p.hpad = hblk * 32;
+    p.ncb = ncb;
+    p.units = units;
 
     hipLaunchKernelGGL(setup_kernel, dim3(1), dim3(1024), 0, stream, a.seq_lens, a.n, a.max_seq_len, a.grid, a.Hq,
                        a.Hkv, TT, a.k_ranks, a.k_offsets, a.t_head, a.t_nout, a.t_last, p.ws, wl.tiles, wl.htile);
     SKV_HIP(hipGetLastError());
     hipLaunchKernelGGL(fold_tiles_kernel, dim3((TT * 128 + 255) / 256, a.n), dim3(256), 0, stream, a.q, a.q_s0,
                        a.q_s1, a.q_dt, a.k_up, a.ku_s0, a.w_dt, (const uint8_t*)p.ws + wl.tiles, TT,
-                       a.scale * LOG2E, p.ws + wl.ab);
+                       a.scale * LOG2E, fmt == FMT_Q4 ? 1 : 0, p.ws + wl.ab);
     SKV_HIP(hipGetLastError());
-    const int mt = mt_for(TT);
     const bool timed = g_prof.on && 2 * g_prof.used + 1 < (int)g_prof.ev.size();
     if (timed) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
-    int rc = fmt == FMT_Q4 ? launch_decode<FMT_Q4, XB_Q4>(p, mt, a.grid, stream)
-             : fmt == FMT_BF16 ? launch_decode<FMT_BF16, XB_LOWRANK>(p, mt, a.grid, stream)
-                               : launch_decode<FMT_F16, XB_LOWRANK>(p, mt, a.grid, stream);
+    int rc = fmt == FMT_Q4 ? launch_decode<FMT_Q4, XB_Q4, NLD_Q4>(p, upw, a.grid, stream)
+             : fmt == FMT_BF16 ? launch_decode<FMT_BF16, XB_LOWRANK, MAX_NLD>(p, upw, a.grid, stream)
+                               : launch_decode<FMT_F16, XB_LOWRANK, MAX_NLD>(p, upw, a.grid, stream);
     if (rc) return rc;
     SKV_HIP(hipGetLastError());
     if (timed) {

@@ -37,9 +37,10 @@ _cs_cache = {}
 
 
 def cos_sin_for_kernel(cos_sin_cache: torch.Tensor) -> torch.Tensor:
-    """The kernels read fp16 or bf16 tables. An fp32 table is converted once (fp16)
-    and cached by storage, since it is a per-model constant."""
-    if cos_sin_cache.dtype in (torch.float16, torch.bfloat16) and cos_sin_cache.stride(-1) == 1:
+    """The kernels read an fp16 table (the MFMA B operand). A bf16 or fp32 table is
+    converted once and cached by storage, since it is a per-model constant; bf16 ->
+    fp16 is exact for values in [-1, 1]."""
+    if cos_sin_cache.dtype == torch.float16 and cos_sin_cache.stride(-1) == 1:
         return cos_sin_cache
     key = (cos_sin_cache.data_ptr(), tuple(cos_sin_cache.shape), cos_sin_cache.dtype, cos_sin_cache.device)
     t = _cs_cache.get(key)

@@ -14,7 +14,7 @@ import torch
 from oracle import cquant, ref
 from starkv_serve import _hip
 from starkv_serve import workloads as W
-from starkv_serve.kernels.paged_decode import paged_starkv_decode
+from starkv_serve.kernels.paged_decode import cos_sin_for_kernel, paged_starkv_decode
 from starkv_serve.kernels.paged_quant import paged_quant_decode
 
 pytestmark = pytest.mark.gpu
@@ -66,7 +66,7 @@ def run_lowrank(wl_gpu, grid=None):
     L = _hip.lib()
     ws = torch.empty(L.starkv_decode_workspace_bytes(n, H, tiles, wl_gpu.v_rank, grid), dtype=torch.uint8,
                      device=q.device)
-    cs, vq, U = wl_gpu.cos_sin_cache, wl_gpu.v_up_by_q, wl_gpu.k_up
+    cs, vq, U = cos_sin_for_kernel(wl_gpu.cos_sin_cache), wl_gpu.v_up_by_q, wl_gpu.k_up  # the ABI takes fp16
     rc = L.starkv_lowrank_decode(_hip.stream_of(q), q.data_ptr(), q.stride(0), q.stride(1), _hip.dtype_code(q),
                                  kv.data_ptr(), kv.stride(0), kv.stride(1), _hip.dtype_code(kv), kv.shape[1],
                                  bt.data_ptr(), bt.stride(0), bt.stride(1), sl.data_ptr(), n, H, Hkv,
