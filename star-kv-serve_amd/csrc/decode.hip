@@ -7,8 +7,10 @@
 //   out   = (softmax(logit) @ V_codes) @ v_up_by_q[h]  paged_decode.py:105-147, 220-226
 //
 // MI355X design, four launches per call (all grids are functions of host ints):
-// 1. setup: the per-16-lane rank-tile table and the prefix sums of the request
-//    lengths, into the workspace.
+// 1. setup: the per-16-lane rank-tile table, the prefix sums of the request lengths
+//    and the wave plan: whole query heads dealt to the 8 waves of a workgroup,
+//    largest first to the least loaded wave, so every wave owns a balanced set of
+//    rank tiles and every head lives in one wave.
 // 2. fold: AB for every (request, rank tile) in fp16, written in the A-operand lane
 //    order of v_mfma_f32_16x16x32_f16, so the decode kernel loads it straight into
 //    its final registers.
@@ -16,16 +18,17 @@
 //    end to end and cut into `grid` equal contiguous ranges, so every workgroup
 //    streams the same number of cache rows whatever the lengths are; a range that
 //    crosses a request boundary emits one split-K partial per request. A page is 16
-//    tokens. Its rows and its 16 cos/sin rows are copied global->LDS by buffer loads
+//    tokens. Its 16 cos/sin rows and its rows are copied global->LDS by buffer loads
 //    with the LDS bit (16 bytes per lane, no VALU address work: every lane's offset
-//    inside a page is fixed for the whole kernel), three pages in flight. Each wave
-//    holds a contiguous run of the request's rank tiles of AB in VGPRs; per tile,
-//    z = AB . [cos|sin]^T runs on MFMA with the page's 16 positions as N, and each
-//    lane folds its 4 z values with its 4 codes. Four tiles' partial logits are summed
-//    over the wave's row groups in one go with the gfx950 lane swaps. An online
-//    softmax per (head, token) follows (lazy running max: the reference point moves
-//    only when a logit exceeds it by 2^8), and P[16 heads, 16] @ V[16, 16 cols] runs
-//    on v_mfma_f32_16x16x16 one page later, so a page costs two workgroup barriers.
+//    inside a page is fixed for the whole kernel), three pages in flight. The only
+//    workgroup barrier per page hands a page buffer over; everything else is wave
+//    local. Each wave holds its heads' rank tiles of AB in VGPRs; per tile,
+//    z = AB . [cos|sin]^T runs on MFMA with the page's 16 positions as N, and each lane
+//    folds its 4 z values with its 4 codes. Four tiles' partial logits are summed over
+//    the wave's row groups in one go with the gfx950 lane swaps. The online softmax of
+//    the wave's heads runs one head per 16-lane row (lazy running max: the reference
+//    point moves only when a logit exceeds it by 2^8), and P[heads, 16] @ V[16, v_rank]
+//    runs on v_mfma_f32_16x16x16 into per-wave accumulators.
 // 4. merge: per (request, head) log-sum-exp of the partials, then the lift through
 //    v_up_by_q.
 #include <stdio.h>
@@ -49,28 +52,31 @@ constexpr int TILE_TOK = 16;
 constexpr int MAX_REQ_PER_CALL = 1024;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int AB_TILE_BYTES = 4 * 64 * 16;  // 4 K-steps x 64 lanes x 8 fp16
-constexpr int AB_SLACK_TILES = 16;          // a wave loads up to MT tiles from its first one
+constexpr int AB_SLACK_TILES = 16;
 constexpr int MAX_TT = 96;                  // rank tiles per call (k_width x heads per kv head <= 1536)
-constexpr int MAX_H = 32;                   // query heads (one softmax item per thread)
-constexpr int MT = 10;                      // rank tiles per wave held in VGPRs; more stream from L2
+constexpr int MAX_H = 32;                   // query heads
+constexpr int MAX_HW = 8;                   // query heads per wave
+constexpr int MAX_SLOTS = 16;               // rank tiles per wave
+constexpr int PLAN_STRIDE = 64;             // ints per wave in the plan
 constexpr int MAX_NLD = 6;                  // 16-byte copies per lane per page (bf16/fp16 rows)
 constexpr int NLD_Q4 = 3;                   // 3.2-bit rows
-constexpr int CS_ROW_LDS = 256;            // LDS bytes per cos/sin row (granules XOR-swizzled by row)
+constexpr int CS_ROW_LDS = 256;             // LDS bytes per cos/sin row (granules XOR-swizzled by row)
 constexpr int CS_CHUNKS = 4;                // 16 rows x 16 granules -> 4 copies of 64 granules
 constexpr int XB_LOWRANK = 48 * 1024;       // LDS bytes per page buffer
 constexpr int XB_Q4 = 24 * 1024;
-constexpr int MAX_PV_UNITS = 4 * NWAVE;     // 16 x 16 output tiles of P @ V
 constexpr float LAZY_MAX = 8.f;             // log2 headroom before the running max moves
 
 // Workspace layout, in bytes from the base (every region 256-byte aligned):
 //   hdr    int   [2 + n]      S (tokens per workgroup), P[0..n] (prefix of clamped lengths)
 //   tiles  int4  [TT]         {q head, first cache lane, valid | nout << 8 | last << 16, kv head}
-//   htile  int2  [Hq]         {first tile, tiles} per query head
+//   plan   int   [8][64] + 1  per wave: [0] tiles, [1] heads, [8 + s] tile of slot s,
+//                             [32 + k] q head of local head k, [40 + k] its first slot,
+//                             [48 + k] its slots; then 1 if every head found a wave
 //   ab     fp16  [n][TT][4][64][8]
 //   m, l   fp32  [slots][Hq]  (log2-domain reference max and sum per partial)
 //   acc    fp32  [slots][Hq][v_rank]
 struct WsLayout {
-    size_t hdr, tiles, htile, ab, m, l, acc, total;
+    size_t hdr, tiles, plan, ab, m, l, acc, total;
 };
 
 static inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -81,7 +87,7 @@ static WsLayout ws_layout(int n, int Hq, int TT, int v_rank, int grid) {
     size_t o = 0;
     w.hdr = o; o = al256(o + (size_t)(n + 2) * 4);
     w.tiles = o; o = al256(o + (size_t)TT * 16);
-    w.htile = o; o = al256(o + (size_t)Hq * 8);
+    w.plan = o; o = al256(o + (size_t)(NWAVE * PLAN_STRIDE + 1) * 4);
     w.ab = o; o = al256(o + ((size_t)n * TT + AB_SLACK_TILES) * AB_TILE_BYTES);
     w.m = o; o = al256(o + slots * Hq * 4);
     w.l = o; o = al256(o + slots * Hq * 4);
@@ -97,17 +103,16 @@ struct DecodeParams {
     int n, Hq, TT, k_width, v_rank;
     int ks_off, vs_off, vq_off, v_nout, v_nbo;     // QuantRow (3.2-bit)
     int row_g, pitch_g, pitch_b;                   // row granules (16 B), LDS row pitch (granules, bytes)
-    int nkv, nch, nld, cs_lds;                     // copies of 64 granules: K/V rows, all; per wave; cos/sin offset
+    int nkv;                                       // 1 KB copies of K/V rows per page (after 4 of cos/sin)
     const uint8_t* cs; int cs_s0b;                 // fp16 cos/sin table, row stride in bytes
     uint8_t* ws;
-    size_t ws_tiles, ws_htile, ws_ab, ws_m, ws_l, ws_acc;
-    int ncb, units;                                // P @ V: 16-column blocks, 16 x 16 tiles
+    size_t ws_tiles, ws_plan, ws_ab, ws_m, ws_l, ws_acc;
 };
 
 __device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // ---------------------------------------------------------------------------
-// 1. setup: tile table + prefix sums. One workgroup of 1024 threads.
+// 1. setup: tile table, prefix sums and wave plan. One workgroup of 1024 threads.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__ seq_lens, int n, int max_seq_len,
                                                      int grid, int Hq, int Hkv, int TT,
@@ -116,13 +121,14 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
                                                      const int32_t* __restrict__ t_head,
                                                      const int32_t* __restrict__ t_nout,
                                                      const int32_t* __restrict__ t_last, uint8_t* __restrict__ ws,
-                                                     size_t ws_tiles, size_t ws_htile) {
+                                                     size_t ws_tiles, size_t ws_plan) {
     __shared__ int s_wsum[16];
     __shared__ int s_total;
+    __shared__ int s_hf[MAX_H], s_hn[MAX_H];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int* hdr = (int*)ws;
     int4* tiles = (int4*)(ws + ws_tiles);
-    int2* htile = (int2*)(ws + ws_htile);
+    int* plan = (int*)(ws + ws_plan);
 
     // Prefix sums of min(max(seq_len, 0), max_seq_len) over n <= 1024 requests.
     const int a = tid < n ? min(max(seq_lens[tid], 0), max_seq_len) : 0;
@@ -142,7 +148,7 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
     __syncthreads();
     if (tid == 0) hdr[0] = (s_total + grid - 1) / grid;
 
-    // Tile table.
+    // Tile table and (first tile, tiles) per query head.
     if (t_head) {  // 3.2-bit: the k_tables arrays, lanes contiguous, MHA
         for (int t = tid; t < TT; t += blockDim.x)
             tiles[t] = make_int4(t_head[t], 16 * t, 16 | (t_nout[t] << 8) | ((t_last[t] != 0) << 16), t_head[t]);
@@ -150,7 +156,8 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
             int first = -1, cnt = 0;
             for (int t = 0; t < TT; ++t)
                 if (t_head[t] == tid) { if (first < 0) first = t; ++cnt; }
-            htile[tid] = make_int2(first < 0 ? 0 : first, cnt);
+            s_hf[tid] = first < 0 ? 0 : first;
+            s_hn[tid] = cnt;
         }
     } else if (tid < Hq) {  // bf16/fp16: ceil(rank / 16) tiles per query head, kv = h / group
         const int grp = Hq / Hkv;
@@ -161,7 +168,89 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
         int cnt = 0;
         for (int j = 0; j < nt && t0 + j < TT; ++j, ++cnt)
             tiles[t0 + j] = make_int4(tid, o + 16 * j, min(16, R - 16 * j) | ((j == nt - 1) << 16), kv);
-        htile[tid] = make_int2(min(t0, TT), cnt);
+        s_hf[tid] = min(t0, TT);
+        s_hn[tid] = cnt;
+    }
+    __syncthreads();
+
+    // Wave plan. Every wave takes ceil(Hq / 8) heads (one head per 16-lane row of the
+    // softmax). Heads by decreasing tile count (ties: lower head first) go to the wave
+    // with the fewest tiles (then the lowest index) that still has room; then swaps
+    // between the most loaded wave and another lower the maximum while they can. Wave
+    // 0 does it; lane w < 8 keeps wave w's load.
+    __shared__ int s_order[MAX_H], s_wave_of[MAX_H], s_load[NWAVE], s_best;
+    if (tid < Hq) {
+        int rank = 0;
+        for (int h = 0; h < Hq; ++h) rank += s_hn[h] > s_hn[tid] || (s_hn[h] == s_hn[tid] && h < tid);
+        s_order[rank] = tid;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int hw = (Hq + NWAVE - 1) / NWAVE;
+        int load = 0, cnt = 0, ok = 1;
+        for (int i = 0; i < Hq; ++i) {
+            const int h = s_order[i], nt = s_hn[h];
+            const bool room = lane < NWAVE && cnt < hw && load + nt <= MAX_SLOTS;
+            int key = room ? (load << 8) | lane : 0x7fffffff;
+#pragma unroll
+            for (int o = 1; o < 8; o <<= 1) key = min(key, __shfl_xor(key, o, 64));
+            if (key == 0x7fffffff) { ok = 0; break; }
+            const int w = key & 255;
+            if (lane == w) { load += nt; ++cnt; }
+            if (lane == 0) s_wave_of[h] = w;
+        }
+        if (lane < NWAVE) s_load[lane] = load;
+        const int target = (TT + NWAVE - 1) / NWAVE;
+        for (int it = 0; it < 32 && ok; ++it) {
+            int kmax = lane < NWAVE ? (s_load[lane] << 8) | lane : -1;  // most loaded wave A
+#pragma unroll
+            for (int o = 1; o < 8; o <<= 1) kmax = max(kmax, __shfl_xor(kmax, o, 64));
+            const int A = kmax & 255, la = kmax >> 8;
+            if (la <= target) break;
+            // Candidate swaps: head ha of A (its ia-th, ia < 4) with head hb of another wave.
+            const uint64_t inA = __builtin_amdgcn_ballot_w64(lane < Hq && s_wave_of[lane] == A);
+            int best = 0x7fffffff;
+#pragma unroll
+            for (int round = 0; round < 2; ++round) {
+                const int ia = 2 * round + (lane >> 5), hb = lane & 31;
+                uint64_t m = inA;
+                for (int j = 0; j < ia && m; ++j) m &= m - 1;  // drop the first ia heads of A
+                if (m && hb < Hq && s_wave_of[hb] != A) {
+                    const int ha = __builtin_ctzll(m);
+                    const int d = s_hn[ha] - s_hn[hb], lb = s_load[s_wave_of[hb]];
+                    if (d > 0 && lb + d < la) best = min(best, (max(la - d, lb + d) << 16) | (ha << 8) | hb);
+                }
+            }
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) best = min(best, __shfl_xor(best, o, 64));
+            if (best == 0x7fffffff) break;
+            if (lane == 0) {
+                const int ha = (best >> 8) & 255, hb = best & 255, B = s_wave_of[hb];
+                const int d = s_hn[ha] - s_hn[hb];
+                s_wave_of[ha] = B;
+                s_wave_of[hb] = A;
+                s_load[A] -= d;
+                s_load[B] += d;
+            }
+        }
+        if (lane < NWAVE) {  // wave `lane`'s heads in plan order, then its slots
+            int* pw = plan + lane * PLAN_STRIDE;
+            int sl = 0, k = 0;
+            for (int i = 0; i < Hq && ok; ++i) {
+                const int h = s_order[i];
+                if (s_wave_of[h] != lane) continue;
+                pw[32 + k] = h;
+                pw[40 + k] = sl;
+                pw[48 + k] = s_hn[h];
+                for (int j = 0; j < s_hn[h]; ++j) pw[8 + sl++] = s_hf[h] + j;
+                ++k;
+            }
+            for (int kk = k; kk < MAX_HW; ++kk) pw[32 + kk] = pw[40 + kk] = pw[48 + kk] = 0;
+            for (int j = sl; j < MAX_SLOTS + 8; ++j) pw[8 + j] = 0;
+            pw[0] = ok ? sl : 0;
+            pw[1] = ok ? k : 0;
+        }
+        if (lane == 0) plan[NWAVE * PLAN_STRIDE] = ok;
     }
 }
 
@@ -251,38 +340,64 @@ __device__ __forceinline__ bool cur_next(Cursor& c, cint_p P, int n, int beg, in
 }
 
 // ---------------------------------------------------------------------------
-// Global -> LDS copy of one page. LDS layout of a page buffer: the 16 token rows at a
-// pitch of pitch_g granules (odd, so rows fall on different banks; granules past row_g
-// are filler), padded to whole 1 KB copies, then the 16 cos/sin rows of the page's
-// positions, 256 bytes each, granule c of row r stored at granule c ^ r (so the MFMA
-// operand reads of 16 rows hit distinct banks). Copy i of wave w is 1 KB chunk i*8 + w; lane q
-// of it moves granule 64*chunk + q, whose offset inside the page (or inside the page's
-// cos/sin rows) is the same for every page: `doff`. Each page gets two buffer
-// descriptors whose size covers only the request's rows, so rows past the end of a
-// request read as zero without touching memory. Every wave issues exactly NLD copies;
-// surplus ones use an empty descriptor (no memory access) and land in `dummy`, so one
-// vmcnt value covers a page on every wave.
+// Global -> LDS copy of one page. LDS layout of a page buffer: the page's 16 cos/sin
+// rows first (256 bytes each, granule c of row r stored at granule c ^ r, so the MFMA
+// operand reads of 16 rows hit distinct banks: 4 copies of 1 KB), then the 16 token
+// rows at a pitch of pitch_g granules (odd, so rows fall on different banks; granules
+// past row_g are filler). Copy i of wave w is 1 KB chunk ch = 8 i + w; lane q of it
+// moves granule 64 ch + q, whose offset inside the page's cos/sin rows or rows is the
+// same for every page: `doff`. The two buffer descriptors of a page cover only the
+// request's rows, so rows past its end are not read. Every wave issues exactly NLD
+// copies; lanes with nothing to move (filler granules, chunks past the page, which land
+// in the buffer's unused tail) carry an offset past the descriptor's range, so they
+// touch no memory, and one vmcnt value covers a page on every wave.
 // ---------------------------------------------------------------------------
+typedef int int4v_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor: 48-bit base, stride 0, `bytes` in range (offsets at or past it
+// are not read), gfx9 data format word.
+__device__ __forceinline__ int4v_t buffer_rsrc(const void* base, int bytes) {
+    const uint64_t a = (uint64_t)base;
+    return (int4v_t){(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), bytes, 0x00020000};
+}
+
+// One 16-byte-per-lane global->LDS copy: lane q's 16 bytes at `voff` land at LDS
+// byte lds + 16 q. Issued as inline assembly so that the compiler does not track it:
+// it would otherwise wait for copies into other page buffers before reads of the
+// current one. The waits for these copies are explicit (vmcnt at the page barrier).
+// M0 takes the LDS address; one wait state separates the M0 write from its use.
+__device__ __forceinline__ void lds_copy16(const int4v_t& rsrc, uint32_t lds, uint32_t voff) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen lds"
+        :
+        : "s"(lds), "v"(voff), "s"(rsrc)
+        : "memory", "m0");
+}
+
 template <int NLD>
-__device__ __forceinline__ void dma_page(const DecodeParams& p, const Cursor& c, cint_p P, uint8_t* buf,
-                                         uint8_t* dummy, int wave, const uint32_t (&doff)[MAX_NLD]) {
-    wave = opaque_s(wave);  // LDS destinations recomputed per page
-    const int tok0 = TILE_TOK * c.k;
-    const int blk = ((cint_p)p.bt)[c.b * p.bt_s0 + (tok0 / p.block_size) * p.bt_s1];
+__device__ __forceinline__ void dma_page(const DecodeParams& p, const Cursor& c, cint_p P, uint8_t* buf, int wave,
+                                         const uint32_t (&doff)[MAX_NLD]) {
+    // Past the end of the workgroup's range the copies still issue (with empty
+    // descriptors: no memory access), so every page of the loop issues the same NLD
+    // copies and the waits stay static.
+    const bool v = c.valid;
+    const int tok0 = v ? TILE_TOK * c.k : 0;
+    const int blk = v ? ((cint_p)p.bt)[c.b * p.bt_s0 + (tok0 / p.block_size) * p.bt_s1] : 0;
     const uint8_t* page = p.cache + (int64_t)blk * p.c_s0 + (int64_t)(tok0 % p.block_size) * p.c_s1;
-    const int rows = min(TILE_TOK, P[c.b + 1] - P[c.b] - tok0);
-    const __amdgpu_buffer_rsrc_t rkv =
-        __builtin_amdgcn_make_buffer_rsrc((void*)page, (short)0, rows * (int)p.c_s1, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rcs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.cs + (int64_t)tok0 * p.cs_s0b), (short)0, rows * p.cs_s0b, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rnull = __builtin_amdgcn_make_buffer_rsrc((void*)p.cs, (short)0, 0, 0x00020000);
+    const int rows = v ? min(TILE_TOK, P[c.b + 1] - P[c.b] - tok0) : 0;
+    const int4v_t rkv = buffer_rsrc(page, rows * (int)p.c_s1);
+    const int4v_t rcs = buffer_rsrc(p.cs + (int64_t)tok0 * p.cs_s0b, rows * p.cs_s0b);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)buf;
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
         const int ch = i * NWAVE + wave;
-        uint8_t* dst = ch < p.nch ? buf + ch * 1024 : dummy;
-        const __amdgpu_buffer_rsrc_t r = ch < p.nkv ? rkv : ch < p.nch ? rcs : rnull;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, doff[i], 0, 0,
-                                                 0);
+        const uint32_t dst = lds0 + (uint32_t)ch * 1024u;
+        if (i == 0 && ch < CS_CHUNKS)
+            lds_copy16(rcs, dst, doff[i]);
+        else  // rows; filler granules and surplus copies carry an out-of-range offset
+            lds_copy16(rkv, dst, doff[i]);
     }
 }
 
@@ -308,6 +423,11 @@ __device__ __forceinline__ half2_t cvt_h2(float a, float b) {
 }
 __device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
 
+__device__ __forceinline__ uint2 ld64(const uint8_t* p) {
+    const uint64_t v = *(const uint64_t*)p;
+    return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+}
+
 __device__ __forceinline__ f32x4_t mfma_tile(const half8_t (&a)[4], const half8_t (&cs)[4]) {
     f32x4_t z = {0.f, 0.f, 0.f, 0.f};
     z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], cs[0], z, 0, 0, 0);
@@ -318,31 +438,34 @@ __device__ __forceinline__ f32x4_t mfma_tile(const half8_t (&a)[4], const half8_
 }
 
 // A lane's share of one rank tile's logit for token (lane & 15): its 4 z values (rows
-// 4g .. 4g+3, g = lane >> 4) times their codes. 3.2-bit: the codes are nibbles n with
-// value n - 8, built as fp16 (1024 + n) - 1032 (exact); the scales are applied per
-// (token, head) from the row's bf16 (outlier, inlier) pair, the outlier part from the
-// lane's first k elements (k = outlier ranks among its 4, from the tile's count).
+// 4g .. 4g+3, g = lane >> 4) times their codes, read at byte `xoff` of the token's row.
+// 3.2-bit: the codes are nibbles n with value n - 8, built as fp16 (1024 + n) - 1032
+// (exact); the scales come per (token, head) from the row's bf16 (outlier, inlier) pair
+// at byte `soff`, the outlier part from the lane's first k elements (k = outlier ranks
+// among its 4, from the tile's count c).
 template <int FMT>
-__device__ __forceinline__ float tile_dot(const f32x4_t& z, const uint8_t* xr, int lane0, int head, int c, int k,
-                                          int lg, int ks_off, const uint2* s_kmask) {
+__device__ __forceinline__ float tile_dot(const f32x4_t& z, const uint8_t* xr, int xoff, int soff, int c, int k,
+                                          int lg, const uint2* s_kmask) {
+    // One 64-bit LDS load (not two 32-bit ones the backend would pair up: the paired
+    // instruction loses the memory operand that tells it apart from copies in flight).
     if (FMT == FMT_BF16) {
-        const uint2 w = *(const uint2*)(xr + 2 * lane0 + 8 * lg);
+        const uint2 w = ld64(xr + xoff + 8 * lg);
         float v = __uint_as_float(w.x << 16) * z[0];
         v = fmaf(__uint_as_float(w.x & 0xffff0000u), z[1], v);
         v = fmaf(__uint_as_float(w.y << 16), z[2], v);
         return fmaf(__uint_as_float(w.y & 0xffff0000u), z[3], v);
     } else if (FMT == FMT_F16) {
-        const uint2 w = *(const uint2*)(xr + 2 * lane0 + 8 * lg);
+        const uint2 w = ld64(xr + xoff + 8 * lg);
         return dot2(as_h2(w.x), cvt_h2(z[0], z[1]), dot2(as_h2(w.y), cvt_h2(z[2], z[3]), 0.f));
     } else {
-        const uint2 w = *(const uint2*)(xr + (lane0 >> 1));
+        const uint2 w = ld64(xr + xoff);
         const uint32_t sh = 4 * lg;
         const half2_t off = {(_Float16)1032.f, (_Float16)1032.f};
         const half2_t x0 = as_h2(((w.x >> sh) & 0x000F000Fu) | 0x64006400u) - off;  // ranks g, g+4
         const half2_t x1 = as_h2(((w.y >> sh) & 0x000F000Fu) | 0x64006400u) - off;  // ranks g+8, g+12
         const half2_t z01 = cvt_h2(z[0], z[1]), z23 = cvt_h2(z[2], z[3]);
         const float d = dot2(x0, z01, dot2(x1, z23, 0.f));
-        const uint32_t sw = *(const uint32_t*)(xr + ks_off + 4 * head);
+        const uint32_t sw = *(const uint32_t*)(xr + soff);
         const float si = __uint_as_float(sw & 0xffff0000u);
         if (c == 0) return si * d;
         const uint2 mk = s_kmask[k];
@@ -352,270 +475,243 @@ __device__ __forceinline__ float tile_dot(const f32x4_t& z, const uint8_t* xr, i
     }
 }
 
+template <int MTV>
 struct WaveTiles {
-    int ts, ntw;                       // first tile, tiles of this wave
-    int lane0[MT], head[MT], c[MT];    // per slot: first cache lane, query head, outlier lanes
+    int ntw, nh;                   // rank tiles (slots) and query heads of this wave
+    int xoff[MTV], meta[MTV];      // per slot: code byte offset in a row; 3.2-bit: scale offset << 8 | outliers
 };
 
-// K side of one page: every tile of this wave, partial logits into s_part[tile][token].
-template <int FMT>
-__device__ __forceinline__ void k_side(const DecodeParams& p, const WaveTiles& wt, const half8_t (&ab)[MT][4],
-                                       const uint8_t* XC, float* s_part, const uint2* s_kmask, uint32_t kpack,
-                                       int lane, int cur_b) {
-    const int ln = opaque(lane);  // LDS addresses are recomputed per page, not held per buffer and tile
+// K side of one page: MTV slots of this wave, partial logits into sp[slot][token]
+// (this wave's own LDS region). Every slot is computed (slots past the wave's tiles
+// use tile 0 and land in a spare row), so the compiler can hoist the LDS reads and
+// interleave the MFMA chains of neighbouring slots.
+template <int FMT, int MTV>
+__device__ __forceinline__ void k_side(const DecodeParams& p, const WaveTiles<MTV>& wt, const half8_t (&ab)[MTV][4],
+                                       const uint8_t* XC, float* sp, const uint2* s_kmask, uint32_t kpack, int lane,
+                                       int wave, int cur_b) {
+    const int ln = opaque(lane);  // LDS addresses are recomputed per page, not held per buffer and slot
     const int lr = ln & 15, lg = ln >> 4;
     half8_t csb[4];  // B operand: position lr of the page, K elements 32 ks + 8 lg .. +8 (granule 4 ks + lg)
     {
-        const uint8_t* csr = XC + p.cs_lds + lr * CS_ROW_LDS;
+        const uint8_t* csr = XC + lr * CS_ROW_LDS;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) csb[ks] = *(const half8_t*)(csr + (((4 * ks + lg) ^ lr) << 4));
     }
-    const uint8_t* xr = XC + lr * p.pitch_b;
+    const uint8_t* xr = XC + CS_CHUNKS * 1024 + lr * p.pitch_b;
     const int rslot = ((lg & 1) << 1) | (lg >> 1);  // sum_rows4 puts inputs (a, b, c, d) in rows (0, 2, 1, 3)
-    const int ntw = opaque_s(wt.ntw), ts = opaque_s(wt.ts);
+    const int ntw = opaque_s(wt.ntw);
     float v[4];
-    f32x4_t zc = {0.f, 0.f, 0.f, 0.f}, zn = zc;
-    if (0 < ntw) zc = mfma_tile(ab[0], csb);
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-        // The next tile's MFMAs are issued before this tile's VALU work.
-        if (i + 1 < MT && i + 1 < ntw) zn = mfma_tile(ab[i + 1], csb);
-        v[i & 3] = 0.f;
-        if (i < ntw)
-            v[i & 3] = tile_dot<FMT>(zc, xr, opaque_s(wt.lane0[i]), opaque_s(wt.head[i]), opaque_s(wt.c[i]),
-                                     (kpack >> (3 * i)) & 7, lg, p.ks_off, s_kmask);
-        zc = zn;
-        if ((i & 3) == 3 || i == MT - 1) {  // four tiles (or the last ones): one reduction over the row groups
-            const int g = i >> 2;
-            if (4 * g < ntw) {
-                const float r = sum_rows4(v[0], (i & 3) >= 1 ? v[1] : 0.f, (i & 3) >= 2 ? v[2] : 0.f,
-                                          (i & 3) >= 3 ? v[3] : 0.f);
-                const int slot = 4 * g + rslot;
-                s_part[(slot < ntw ? ts + slot : MAX_TT) * TILE_TOK + lr] = r;
-            }
+    for (int i = 0; i < MTV; ++i) {
+        const f32x4_t z = mfma_tile(ab[i], csb);
+        const int meta = FMT == FMT_Q4 ? wt.meta[i] : 0;
+        v[i & 3] = tile_dot<FMT>(z, xr, wt.xoff[i], meta >> 8, meta & 255, (kpack >> (3 * i)) & 7, lg, s_kmask);
+        if ((i & 3) == 3 || i == MTV - 1) {  // four tiles (or the last ones): one reduction over the row groups
+            const float r = sum_rows4(v[0], (i & 3) >= 1 ? v[1] : 0.f, (i & 3) >= 2 ? v[2] : 0.f,
+                                      (i & 3) >= 3 ? v[3] : 0.f);
+            const int slot = 4 * (i >> 2) + rslot;
+            sp[(slot < ntw ? slot : MAX_SLOTS) * TILE_TOK + lr] = r;
         }
     }
-    // Tiles past MT: AB from the workspace (L2) on every page.
-    if (wt.ntw > MT) {
+    // Slots past MTV: AB from the workspace (L2) on every page.
+    if (ntw > MTV) {
+        cint_p plan = (cint_p)(p.ws + p.ws_plan) + wave * PLAN_STRIDE;
         cint_p tiles = (cint_p)(p.ws + p.ws_tiles);
-        const half8_t* abg = (const half8_t*)(p.ws + p.ws_ab + ((size_t)cur_b * p.TT + wt.ts) * AB_TILE_BYTES);
-        for (int i = MT; i < wt.ntw; ++i) {
+        const half8_t* abg = (const half8_t*)(p.ws + p.ws_ab + (size_t)cur_b * p.TT * AB_TILE_BYTES);
+        for (int i = MTV; i < ntw; ++i) {
+            const int t = plan[8 + i];
             half8_t a[4];
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) a[ks] = abg[(i * 4 + ks) * 64 + lane];
-            const int4 tm = load_tile(tiles, wt.ts + i);
+            for (int ks = 0; ks < 4; ++ks) a[ks] = abg[(t * 4 + ks) * 64 + lane];
+            const int4 tm = load_tile(tiles, t);
             const int c = (tm.z >> 8) & 255;
             const int k = min(max((c - lg + 3) >> 2, 0), 4);
-            const float r = sum_rows(tile_dot<FMT>(mfma_tile(a, csb), xr, tm.y, tm.x, c, k, lg, p.ks_off, s_kmask));
-            if (lane < 16) s_part[(wt.ts + i) * TILE_TOK + lr] = r;
+            const int xoff = FMT == FMT_Q4 ? (tm.y >> 1) : 2 * tm.y;
+            const float r = sum_rows(tile_dot<FMT>(mfma_tile(a, csb), xr, xoff, p.ks_off + 4 * tm.x, c, k, lg, s_kmask));
+            if (lane < 16) sp[i * TILE_TOK + lr] = r;
         }
+        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): no tracked load left pending
     }
 }
 
-// Online softmax state of this thread's (head, token) item: head tid >> 4, token
-// column tid & 15 (heads <= 32, so one item per thread).
+// Online softmax of this wave's heads: local head (lane >> 4) on a 16-lane row, token
+// lane & 15.
 struct SmState {
-    float m, l;  // log2-domain reference max (same on the head's 16 lanes), this lane's column sum
-    int ht0, htn;
-    bool on;
+    float m, l;   // log2-domain reference max (same on the head's 16 lanes), this lane's column sum
+    int hf, hn;   // the row's head: first slot, slots (0 for no head)
 };
 
+// Returns true when some head's reference max moved (acc needs rescaling by alpha).
 template <int FMT>
-__device__ __forceinline__ void softmax_page(SmState& sm, const float* s_part, uint16_t* s_p, uint16_t* s_plo,
-                                             float* s_alpha, int tid, int tok0, int lo, int hi) {
-    if (!sm.on) return;
-    tid = opaque(tid);  // LDS addresses recomputed per page
-    const int r = tid & 15;
+__device__ __forceinline__ bool softmax_page(SmState& sm, int nh, const float* sp, uint16_t* spp, uint16_t* spl,
+                                             float* salpha, int lane, int tok0, int lo, int hi) {
+    const int ln = opaque(lane);
+    const int kh = ln >> 4, lr = ln & 15;
     float s = 0.f;
-    for (int t = 0; t < sm.htn; ++t) s += s_part[(sm.ht0 + t) * TILE_TOK + r];
-    s = tok0 + r >= lo && tok0 + r < hi ? s : -INFINITY;
+    for (int t = 0; t < sm.hn; ++t) s += sp[(sm.hf + t) * TILE_TOK + lr];
+    s = tok0 + lr >= lo && tok0 + lr < hi && kh < nh ? s : -INFINITY;
     float alpha = 1.f;
+    bool moved = false;
     if (__builtin_amdgcn_ballot_w64(s > sm.m + LAZY_MAX) != 0) {
         const float mn = fmaxf(sm.m, row16_max(s));
-        alpha = __builtin_amdgcn_exp2f(sm.m - mn);
+        alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(sm.m - mn);
         sm.m = mn;
+        moved = true;
     }
-    const float pe = __builtin_amdgcn_exp2f(s - sm.m);
+    const float pe = s == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - sm.m);
     sm.l = fmaf(sm.l, alpha, pe);
+    const int idx = kh * TILE_TOK + lr;  // rows past the wave's heads hold P = 0
     if (FMT == FMT_BF16) {
         // P = hi + lo in two bfloat16 parts: the P @ V product keeps ~16 bits of P.
         const __bf16 ph = (__bf16)pe;
         const __bf16 pl = (__bf16)(pe - (float)ph);
-        s_p[tid] = __builtin_bit_cast(uint16_t, ph);
-        s_plo[tid] = __builtin_bit_cast(uint16_t, pl);
+        spp[idx] = __builtin_bit_cast(uint16_t, ph);
+        spl[idx] = __builtin_bit_cast(uint16_t, pl);
     } else {
-        s_p[tid] = __builtin_bit_cast(uint16_t, (_Float16)pe);
+        spp[idx] = __builtin_bit_cast(uint16_t, (_Float16)pe);
     }
-    if (r == 0) s_alpha[tid >> 4] = alpha;
+    if (lr == 0) salpha[kh] = alpha;
+    return moved;
 }
 
-// m and l of the partial that ends with this page, then reset.
-__device__ __forceinline__ void flush_ml(const DecodeParams& p, SmState& sm, int slot, int tid) {
-    if (!sm.on) return;
+// acc[nb] = alpha * acc[nb] + P[4 heads, 16 tokens] @ V[16 tokens, 64 columns] for page
+// X, on v_mfma_f32_4x4x4_16b with block 0's A broadcast (cbsz 4): per 4-token step,
+// lanes 0..3 hold P[head l][4 tokens], lane l holds V[4 tokens][column 64 nb + l], and
+// the result lands in lane l as acc[nb][head] for its column.
+template <int FMT, int NB>
+__device__ __forceinline__ void pv_page(const DecodeParams& p, f32x4_t (&acc)[NB], const uint8_t* X,
+                                        const uint16_t* spp, const uint16_t* spl, const float* salpha, bool rescale,
+                                        int lane) {
+    const int ln = opaque(lane);
+    if (rescale) {
+        const f32x4_t al = *(const f32x4_t*)salpha;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[nb][e] *= al[e];
+    }
+    const uint8_t* rows = X + CS_CHUNKS * 1024;
+    const uint16_t* pr = spp + (ln & 3) * TILE_TOK;
+    const uint16_t* plr = spl + (ln & 3) * TILE_TOK;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {  // tokens 4 st .. 4 st + 3
+        const uint2 pa = *(const uint2*)(pr + 4 * st);
+        const uint2 pl = FMT == FMT_BF16 ? *(const uint2*)(plr + 4 * st) : make_uint2(0, 0);
+        const uint8_t* r0 = rows + 4 * st * p.pitch_b;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const int c = 64 * nb + ln;  // columns past v_rank compute garbage that is never stored
+            uint32_t b0, b1;
+            if (FMT == FMT_Q4) {
+                const bool o = c < p.v_nout;
+                const int ci = o ? c : c - p.v_nout;
+                const int vb = p.vq_off + (o ? 0 : p.v_nbo) + (ci >> 1);
+                const int vsh = 4 * (ci & 1);
+                const int vso = p.vs_off + (o ? 0 : 2);
+                float val[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint8_t* rp = r0 + e * p.pitch_b;
+                    const int nib = (int)((rp[vb] >> vsh) & 15u) - 8;
+                    val[e] = (float)nib * __uint_as_float((uint32_t)(*(const uint16_t*)(rp + vso)) << 16);
+                }
+                b0 = h2_bits(cvt_h2(val[0], val[1]));
+                b1 = h2_bits(cvt_h2(val[2], val[3]));
+            } else {
+                const uint8_t* vp = r0 + 2 * (p.k_width + c);
+                const uint32_t u0 = *(const uint16_t*)vp, u1 = *(const uint16_t*)(vp + p.pitch_b);
+                const uint32_t u2 = *(const uint16_t*)(vp + 2 * p.pitch_b), u3 = *(const uint16_t*)(vp + 3 * p.pitch_b);
+                b0 = u0 | (u1 << 16);
+                b1 = u2 | (u3 << 16);
+            }
+            const uint2 bv = make_uint2(b0, b1);
+            if (FMT == FMT_BF16) {
+                acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(short4_t, pa),
+                                                                 __builtin_bit_cast(short4_t, bv), acc[nb], 4, 0, 0);
+                acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(short4_t, pl),
+                                                                 __builtin_bit_cast(short4_t, bv), acc[nb], 4, 0, 0);
+            } else {
+                acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, pa),
+                                                             __builtin_bit_cast(half4_t, bv), acc[nb], 4, 0, 0);
+            }
+        }
+    }
+}
+
+// The partial of the request that ends with this page: m, l and acc of this wave's
+// heads into partial slot `slot`, then reset. The wave's query-head ids come from LDS:
+// a vector load here would leave a tracked load in flight at the loop's join, and the
+// compiler would then drain every copy before the next page's first LDS read.
+template <int NB>
+__device__ __forceinline__ void flush_partial(const DecodeParams& p, SmState& sm, f32x4_t (&acc)[NB], int nh,
+                                              int slot, const int* sqh, int lane) {
+    const int ln = opaque(lane);
+    const int kh = ln >> 4, lr = ln & 15;
+    const int64_t base = (int64_t)slot * p.Hq;
     const float lt = row16_sum(sm.l);
-    if ((tid & 15) == 0) {
-        const int64_t i = (int64_t)slot * p.Hq + (tid >> 4);
-        ((float*)(p.ws + p.ws_m))[i] = sm.m;
-        ((float*)(p.ws + p.ws_l))[i] = lt;
+    if (kh < nh && lr == 0) {
+        const int qh = sqh[kh];
+        ((float*)(p.ws + p.ws_m))[base + qh] = sm.m;
+        ((float*)(p.ws + p.ws_l))[base + qh] = lt;
     }
     sm.m = -INFINITY;
     sm.l = 0.f;
-}
-
-struct PvUnits {
-    bool on[4];
-    int hb[4], cb[4];  // head block (16 heads), column block (16 V columns)
-};
-
-// acc[unit] = alpha * acc + P[16 heads, 16 tokens] @ V[16 tokens, 16 columns] for page X.
-// Lane l holds A = P[head 16 hb + (l & 15)][tokens 4 (l >> 4) .. +4] and B = V[same
-// tokens][column 16 cb + (l & 15)]; the result row 4 (l >> 4) + e, column l & 15.
-template <int FMT, int UPW>
-__device__ __forceinline__ void pv_page(const DecodeParams& p, const PvUnits& pu, f32x4_t (&acc)[UPW],
-                                        const uint8_t* X, const uint16_t* s_p, const uint16_t* s_plo,
-                                        const float* s_alpha, int lane) {
-    const int ln = opaque(lane);  // per-lane addresses are recomputed here, not held across the loop
-    const int lr = ln & 15, lg = ln >> 4;
+    float* wa = (float*)(p.ws + p.ws_acc) + base * p.v_rank;
 #pragma unroll
-    for (int k = 0; k < UPW; ++k) {
-        if (!pu.on[k]) continue;
-        const int hb = pu.hb[k];
-        const f32x4_t al = *(const f32x4_t*)(s_alpha + 16 * hb + 4 * lg);
+    for (int e = 0; e < 4; ++e) {
+        const int qh = sqh[e];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[k][e] *= al[e];
-        const int prow = (16 * hb + lr) * TILE_TOK + 4 * lg;
-        const uint2 pa = *(const uint2*)(s_p + prow);
-        const int c = 16 * pu.cb[k] + lr;  // columns past v_rank compute garbage that is never stored
-        const uint8_t* rows = X + 4 * lg * p.pitch_b;
-        uint32_t b0, b1;
-        if (FMT == FMT_Q4) {
-            const bool o = c < p.v_nout;
-            const int ci = o ? c : c - p.v_nout;
-            const int vb = p.vq_off + (o ? 0 : p.v_nbo) + (ci >> 1);
-            const int vsh = 4 * (ci & 1);
-            const int vso = p.vs_off + (o ? 0 : 2);
-            float val[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint8_t* rp = rows + e * p.pitch_b;
-                const int nib = (int)((rp[vb] >> vsh) & 15u) - 8;
-                val[e] = (float)nib * __uint_as_float((uint32_t)(*(const uint16_t*)(rp + vso)) << 16);
-            }
-            b0 = h2_bits(cvt_h2(val[0], val[1]));
-            b1 = h2_bits(cvt_h2(val[2], val[3]));
-        } else {
-            const uint8_t* vp = rows + 2 * (p.k_width + c);
-            const uint32_t u0 = *(const uint16_t*)vp, u1 = *(const uint16_t*)(vp + p.pitch_b);
-            const uint32_t u2 = *(const uint16_t*)(vp + 2 * p.pitch_b), u3 = *(const uint16_t*)(vp + 3 * p.pitch_b);
-            b0 = u0 | (u1 << 16);
-            b1 = u2 | (u3 << 16);
-        }
-        const uint2 bv = make_uint2(b0, b1);
-        if (FMT == FMT_BF16) {
-            const uint2 pl = *(const uint2*)(s_plo + prow);
-            acc[k] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_t, pa),
-                                                               __builtin_bit_cast(short4_t, bv), acc[k], 0, 0, 0);
-            acc[k] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_t, pl),
-                                                               __builtin_bit_cast(short4_t, bv), acc[k], 0, 0, 0);
-        } else {
-            acc[k] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, pa),
-                                                           __builtin_bit_cast(half4_t, bv), acc[k], 0, 0, 0);
-        }
-    }
-}
-
-template <int UPW>
-__device__ __forceinline__ void flush_acc(const DecodeParams& p, const PvUnits& pu, f32x4_t (&acc)[UPW], int slot,
-                                          int lane) {
-    float* wa = (float*)(p.ws + p.ws_acc) + (int64_t)slot * p.Hq * p.v_rank;
-    const int ln = opaque(lane);
-    const int lr = ln & 15, lg = ln >> 4;
-#pragma unroll
-    for (int k = 0; k < UPW; ++k) {
-        if (!pu.on[k]) continue;
-        const int c = 16 * pu.cb[k] + lr;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int h = 16 * pu.hb[k] + 4 * lg + e;
-            if (h < p.Hq && c < p.v_rank) wa[(int64_t)h * p.v_rank + c] = acc[k][e];
-            acc[k][e] = 0.f;
+        for (int nb = 0; nb < NB; ++nb) {
+            const int c = 64 * nb + ln;
+            if (e < nh && c < p.v_rank) wa[(int64_t)qh * p.v_rank + c] = acc[nb][e];
+            acc[nb][e] = 0.f;
         }
     }
 }
 
 struct LoopState {
     Cursor cc, ld;
-    int issued, j, beg, end, g;
-    bool new_seg, prev_valid, prev_end;
-    int prev_b;
-};
-
-struct Shared {
-    uint8_t* dummy;
-    float* part;
-    uint16_t* p;
-    uint16_t* plo;
-    float* alpha;
-    const uint2* kmask;
+    int j, beg, end, g;
+    bool new_seg;
 };
 
 // ---------------------------------------------------------------------------
-// One page of the decode loop. XC holds page j (copied two pages ago), XP page j - 1
-// (its P @ V runs now, after the barrier that publishes its P) and then receives page
-// j + 2. Distinct __shared__ arrays per buffer let the compiler see that reads of XC
-// never alias the copies in flight into XP, so no vmcnt(0) is inserted before them.
-//   B1  wait for this wave's copies of page j (and its LDS writes); barrier
-//       P @ V of page j - 1 (+ its partial if it ended a request); K side of page j
-//   B2  barrier (partial logits complete; every read of XP done)
-//       copies of page j + 2 into XP; softmax of page j
+// One page of the decode loop: XC holds page j (copied two pages ago) and XN receives
+// page j + 2 (its previous page, j - 1, is finished on every wave once the barrier is
+// passed). Distinct __shared__ arrays per buffer keep every address static.
 // ---------------------------------------------------------------------------
-template <int FMT, int UPW, int NLD>
-__device__ __forceinline__ bool decode_iter(LoopState& st, const WaveTiles& wt, half8_t (&ab)[MT][4],
-                                            f32x4_t (&acc)[UPW], SmState& sm, const PvUnits& pu,
-                                            const uint32_t (&doff)[MAX_NLD], uint32_t kpack, const uint8_t* XC,
-                                            uint8_t* XP, const Shared& S, int tid, int lane, int wave) {
+template <int FMT, int MTV, int NB, int NLD>
+__device__ __forceinline__ bool decode_iter(LoopState& st, const WaveTiles<MTV>& wt, half8_t (&ab)[MTV][4],
+                                            f32x4_t (&acc)[NB], SmState& sm, const uint32_t (&doff)[MAX_NLD],
+                                            uint32_t kpack, const uint8_t* XC, uint8_t* XN, float* sp,
+                                            uint16_t* spp, uint16_t* spl, float* salpha, const uint2* s_kmask,
+                                            const int* sqh, int lane, int wave) {
     const DecodeParams& p = params();
     cint_p P = (cint_p)(p.ws + 4);
-    if (!st.cc.valid) {
-        if (st.prev_valid) {  // drain: P @ V of the last page, then its partial
-            wait_vmcnt_lgkm0(0);
-            lds_barrier();
-            pv_page<FMT, UPW>(p, pu, acc, XP, S.p, S.plo, S.alpha, lane);
-            flush_acc<UPW>(p, pu, acc, st.prev_b + st.g, lane);
-        }
-        return false;
-    }
+    if (!st.cc.valid) return false;
     const Cursor cc = st.cc;
     if (st.new_seg) {
-        // This request's AB into registers. Slots past the wave's range load what
-        // follows (the AB region has slack for it) and are never used.
-        const half8_t* abp = (const half8_t*)(p.ws + p.ws_ab + ((size_t)cc.b * p.TT + wt.ts) * AB_TILE_BYTES);
+        // This request's AB into registers; slots past the wave's tiles load tile 0.
+        cint_p plan = (cint_p)(p.ws + p.ws_plan) + wave * PLAN_STRIDE;
+        const half8_t* abp = (const half8_t*)(p.ws + p.ws_ab + (size_t)cc.b * p.TT * AB_TILE_BYTES);
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
+        for (int i = 0; i < MTV; ++i) {
+            const int t = plan[8 + i];
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) ab[i][ks] = abp[(i * 4 + ks) * 64 + lane];
+            for (int ks = 0; ks < 4; ++ks) ab[i][ks] = abp[(t * 4 + ks) * 64 + lane];
+        }
         __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0)
     }
-    wait_vmcnt_lgkm0(st.issued > st.j + 1 ? NLD : 0);
-    lds_barrier();  // B1
-    if (st.prev_valid) {
-        pv_page<FMT, UPW>(p, pu, acc, XP, S.p, S.plo, S.alpha, lane);
-        if (st.prev_end) flush_acc<UPW>(p, pu, acc, st.prev_b + st.g, lane);
-    }
-    k_side<FMT>(p, wt, ab, XC, S.part, S.kmask, kpack, lane, cc.b);
-    wait_lgkm0_barrier();  // B2
-    if (st.ld.valid) {
-        dma_page<NLD>(p, st.ld, P, XP, S.dummy, wave, doff);
-        ++st.issued;
-        cur_next(st.ld, P, p.n, st.beg, st.end);
-    }
-    softmax_page<FMT>(sm, S.part, S.p, S.plo, S.alpha, tid, TILE_TOK * cc.k, cc.lo, cc.hi);
+    SKV_WAIT_VM_LGKM0(NLD);  // only the copies of page j + 1 may still be in flight
+    lds_barrier();           // page j is in LDS; every wave is done with page j - 1
+    dma_page<NLD>(p, st.ld, P, XN, opaque_s(wave), doff);
+    if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
+    k_side<FMT, MTV>(p, wt, ab, XC, sp, s_kmask, kpack, lane, wave, cc.b);
+    const bool moved = softmax_page<FMT>(sm, wt.nh, sp, spp, spl, salpha, lane, TILE_TOK * cc.k, cc.lo, cc.hi);
+    pv_page<FMT, NB>(p, acc, XC, spp, spl, salpha, moved, lane);
     Cursor nx = cc;
     const bool seg_end = cur_next(nx, P, p.n, st.beg, st.end);
-    if (seg_end) flush_ml(p, sm, cc.b + st.g, tid);
-    st.prev_valid = true;
-    st.prev_end = seg_end;
-    st.prev_b = cc.b;
+    if (seg_end) flush_partial<NB>(p, sm, acc, wt.nh, cc.b + st.g, sqh, lane);
     st.cc = nx;
     st.new_seg = seg_end;
     ++st.j;
@@ -623,25 +719,27 @@ __device__ __forceinline__ bool decode_iter(LoopState& st, const WaveTiles& wt, 
 }
 
 // ---------------------------------------------------------------------------
-// 3. decode. UPW = P @ V tiles per wave; XB = bytes per page buffer; NLD = copies
-//    per lane per page.
+// 3. decode. MTV = rank tiles per wave held in VGPRs (more stream from L2); NB =
+//    64-column blocks of V; XB = bytes per page buffer; NLD = copies per lane per page.
 // ---------------------------------------------------------------------------
-template <int FMT, int UPW, int XB, int NLD>
+template <int FMT, int MTV, int NB, int XB, int NLD>
 __global__ __launch_bounds__(NTHR) void decode_kernel(const DecodeParams p0) {
     __shared__ __attribute__((aligned(16))) uint8_t s_x0[XB];
     __shared__ __attribute__((aligned(16))) uint8_t s_x1[XB];
     __shared__ __attribute__((aligned(16))) uint8_t s_x2[XB];
-    __shared__ __attribute__((aligned(16))) uint8_t s_dummy[1024];
-    __shared__ __attribute__((aligned(16))) float s_part[(MAX_TT + 1) * TILE_TOK];
-    __shared__ __attribute__((aligned(16))) uint16_t s_p[MAX_H * TILE_TOK];
-    __shared__ __attribute__((aligned(16))) uint16_t s_plo[FMT == FMT_BF16 ? MAX_H * TILE_TOK : 8];
-    __shared__ __attribute__((aligned(16))) float s_alpha[MAX_H];
+    __shared__ __attribute__((aligned(16))) float s_part[NWAVE][(MAX_SLOTS + 1) * TILE_TOK];
+    __shared__ __attribute__((aligned(16))) uint16_t s_p[NWAVE][4 * TILE_TOK];
+    __shared__ __attribute__((aligned(16))) uint16_t s_plo[FMT == FMT_BF16 ? NWAVE : 1][4 * TILE_TOK];
+    __shared__ __attribute__((aligned(16))) float s_alpha[NWAVE][4];
     __shared__ __attribute__((aligned(16))) uint2 s_kmask[8];
+    __shared__ int s_qh[NWAVE][4];
 
     const DecodeParams& p = params();
     const int tid = threadIdx.x, lane = tid & 63, wave = rfl(tid >> 6);
     const int lg = lane >> 4;
     cint_p P = (cint_p)(p.ws + 4);
+    cint_p plan = (cint_p)(p.ws + p.ws_plan);
+    if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
     LoopState st;
     st.g = blockIdx.x;
     const int S_tok = ((cint_p)p.ws)[0];
@@ -657,107 +755,92 @@ __global__ __launch_bounds__(NTHR) void decode_kernel(const DecodeParams p0) {
         ((uint4*)s_x1)[i] = make_uint4(0, 0, 0, 0);
         ((uint4*)s_x2)[i] = make_uint4(0, 0, 0, 0);
     }
-    for (int i = tid; i < MAX_H * TILE_TOK; i += NTHR) {
-        s_p[i] = 0;
-        if (FMT == FMT_BF16) s_plo[i] = 0;
-    }
-    if (tid < MAX_H) s_alpha[tid] = 1.f;
+    if (tid < NWAVE * 4) (&s_alpha[0][0])[tid] = 1.f;
     if (tid < 8) {  // fp16-pair masks of a lane's first k elements (pairs (0,1), (2,3))
         const uint32_t m0 = tid >= 2 ? 0xffffffffu : tid == 1 ? 0x0000ffffu : 0u;
         const uint32_t m1 = tid >= 4 ? 0xffffffffu : tid == 3 ? 0x0000ffffu : 0u;
         s_kmask[tid] = make_uint2(m0, m1);
     }
 
-    // This wave's rank tiles.
-    WaveTiles wt;
-    wt.ts = rfl((wave * p.TT) / NWAVE);
-    wt.ntw = rfl(((wave + 1) * p.TT) / NWAVE - wt.ts);
+    // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
+    cint_p pw = plan + wave * PLAN_STRIDE;
+    WaveTiles<MTV> wt;
+    wt.ntw = pw[0];
+    wt.nh = pw[1];
     uint32_t kpack = 0;
     {
         cint_p tiles = (cint_p)(p.ws + p.ws_tiles);
 #pragma unroll
-        for (int i = 0; i < MT; ++i) {
-            const int4 tm = load_tile(tiles, min(wt.ts + i, p.TT - 1));
-            wt.lane0[i] = tm.y;
-            wt.head[i] = tm.x;
-            wt.c[i] = (tm.z >> 8) & 255;
-            if (FMT == FMT_Q4) kpack |= (uint32_t)min(max((wt.c[i] - lg + 3) >> 2, 0), 4) << (3 * i);
+        for (int i = 0; i < MTV; ++i) {
+            const int4 tm = load_tile(tiles, pw[8 + i]);
+            wt.xoff[i] = FMT == FMT_Q4 ? (tm.y >> 1) : 2 * tm.y;
+            const int c = (tm.z >> 8) & 255;
+            wt.meta[i] = ((p.ks_off + 4 * tm.x) << 8) | c;
+            if (FMT == FMT_Q4) kpack |= (uint32_t)min(max((c - lg + 3) >> 2, 0), 4) << (3 * i);
         }
     }
-    // Softmax item.
+    if (lane < 4) s_qh[wave][lane] = lane < wt.nh ? ((const int*)pw)[32 + lane] : 0;
     SmState sm;
-    sm.on = tid < p.Hq * TILE_TOK;
-    {
-        const int2 ht = ((const int2*)(p.ws + p.ws_htile))[sm.on ? tid >> 4 : 0];
-        sm.ht0 = ht.x;
-        sm.htn = ht.y;
-    }
+    sm.hf = lg < wt.nh ? ((const int*)pw)[40 + lg] : 0;
+    sm.hn = lg < wt.nh ? ((const int*)pw)[48 + lg] : 0;
     sm.m = -INFINITY;
     sm.l = 0.f;
-    // P @ V tiles of this wave.
-    PvUnits pu;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int u = wave + NWAVE * k;
-        pu.on[k] = k < UPW && u < p.units;
-        pu.hb[k] = u / p.ncb;
-        pu.cb[k] = u - pu.hb[k] * p.ncb;
-    }
-    // Copy offsets of this lane inside a page.
+    // Copy offsets of this lane inside a page (chunks 0..3: cos/sin rows; then rows).
     uint32_t doff[MAX_NLD];
 #pragma unroll
     for (int i = 0; i < MAX_NLD; ++i) {
         const int ch = i * NWAVE + wave;
-        int off = 0;
+        uint32_t off = 0x80000000u;  // past the descriptor range: no memory access
         if (i < NLD) {
-            if (ch < p.nkv) {
-                const int g = ch * 64 + lane;
+            if (ch < CS_CHUNKS) {
+                const int g = ch * 64 + lane, row = g >> 4;  // LDS granule g holds granule (g & 15) ^ row
+                off = (uint32_t)(row * p.cs_s0b + (((g & 15) ^ row) << 4));
+            } else if (ch < CS_CHUNKS + p.nkv) {
+                const int g = (ch - CS_CHUNKS) * 64 + lane;
                 const int row = g / p.pitch_g, col = g - row * p.pitch_g;
-                if (row < TILE_TOK && col < p.row_g) off = row * (int)p.c_s1 + col * 16;
-            } else {
-                const int g = (ch - p.nkv) * 64 + lane;  // LDS granule g holds granule (g & 15) ^ row of its row
-                const int row = g >> 4;
-                if (row < TILE_TOK) off = row * p.cs_s0b + (((g & 15) ^ row) << 4);
+                if (row < TILE_TOK && col < p.row_g) off = (uint32_t)(row * (int)p.c_s1 + col * 16);
             }
         }
-        doff[i] = (uint32_t)off;
+        doff[i] = off;
     }
     __syncthreads();
 
-    Shared S{s_dummy, s_part, s_p, s_plo, s_alpha, s_kmask};
+    float* sp = &s_part[wave][0];
+    uint16_t* spp = &s_p[wave][0];
+    uint16_t* spl = &s_plo[FMT == FMT_BF16 ? wave : 0][0];
+    float* salpha = &s_alpha[wave][0];
     cur_first(st.cc, P, p.n, st.beg, st.end);
     st.ld = st.cc;
-    st.issued = 0;
     st.j = 0;
     st.new_seg = true;
-    st.prev_valid = false;
-    st.prev_end = false;
-    st.prev_b = 0;
-    dma_page<NLD>(p, st.ld, P, s_x0, s_dummy, wave, doff);
-    ++st.issued;
+    dma_page<NLD>(p, st.ld, P, s_x0, wave, doff);
     cur_next(st.ld, P, p.n, st.beg, st.end);
-    if (st.ld.valid) {
-        dma_page<NLD>(p, st.ld, P, s_x1, s_dummy, wave, doff);
-        ++st.issued;
-        cur_next(st.ld, P, p.n, st.beg, st.end);
-    }
+    dma_page<NLD>(p, st.ld, P, s_x1, wave, doff);
+    if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
 
-    half8_t ab[MT][4];
-    f32x4_t acc[UPW];
+    half8_t ab[MTV][4];
+    f32x4_t acc[NB];
 #pragma unroll
-    for (int k = 0; k < UPW; ++k) acc[k] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < NB; ++k) acc[k] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
     while (true) {
-        if (!decode_iter<FMT, UPW, NLD>(st, wt, ab, acc, sm, pu, doff, kpack, s_x0, s_x2, S, tid, lane, wave)) break;
-        if (!decode_iter<FMT, UPW, NLD>(st, wt, ab, acc, sm, pu, doff, kpack, s_x1, s_x0, S, tid, lane, wave)) break;
-        if (!decode_iter<FMT, UPW, NLD>(st, wt, ab, acc, sm, pu, doff, kpack, s_x2, s_x1, S, tid, lane, wave)) break;
+        if (!decode_iter<FMT, MTV, NB, NLD>(st, wt, ab, acc, sm, doff, kpack, s_x0, s_x2, sp, spp, spl, salpha,
+                                            s_kmask, &s_qh[wave][0], lane, wave))
+            break;
+        if (!decode_iter<FMT, MTV, NB, NLD>(st, wt, ab, acc, sm, doff, kpack, s_x1, s_x0, sp, spp, spl, salpha,
+                                            s_kmask, &s_qh[wave][0], lane, wave))
+            break;
+        if (!decode_iter<FMT, MTV, NB, NLD>(st, wt, ab, acc, sm, doff, kpack, s_x2, s_x1, sp, spp, spl, salpha,
+                                            s_kmask, &s_qh[wave][0], lane, wave))
+            break;
     }
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): no copy may land after the workgroup ends
 }
 
 // ---------------------------------------------------------------------------
 // 4. merge: per (request, head) combine the partials (log2-domain LSE), then lift.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(128) void merge_kernel(const uint8_t* __restrict__ ws, size_t ws_m, size_t ws_l,
-                                                    size_t ws_acc, int Hq, int v_rank, const void* __restrict__ vup,
+__global__ __launch_bounds__(128) void merge_kernel(const uint8_t* __restrict__ ws, size_t ws_plan, size_t ws_m,
+                                                    size_t ws_l, size_t ws_acc, int Hq, int v_rank, const void* __restrict__ vup,
                                                     int64_t vu_s0, int64_t vu_s1, int w_dt, void* __restrict__ out,
                                                     int64_t o_s0, int64_t o_s1, int out_dt) {
     extern __shared__ float s_o[];  // [v_rank]
@@ -765,7 +848,10 @@ __global__ __launch_bounds__(128) void merge_kernel(const uint8_t* __restrict__ 
     const int* hdr = (const int*)ws;
     const int S = hdr[0];
     const int pb = hdr[1 + b], pe = hdr[2 + b];
-    if (pe <= pb || S <= 0) {  // no tokens: softmax over an empty row (NaN, as the reference)
+    const bool planned = ((const int*)(ws + ws_plan))[NWAVE * PLAN_STRIDE] != 0;
+    // No tokens: softmax over an empty row (NaN, as the reference). No wave plan (a
+    // head assignment that does not fit): NaN as well, never a silent wrong result.
+    if (pe <= pb || S <= 0 || !planned) {
         for (int d = tid; d < 128; d += blockDim.x)
             store_f(out, (int64_t)b * o_s0 + (int64_t)h * o_s1 + d, out_dt, __builtin_nanf(""));
         return;
@@ -851,14 +937,23 @@ struct DecodeProfile {
 };
 static DecodeProfile g_prof;
 
+template <int FMT, int MTV, int XB, int NLD>
+static const void* pick_nb(int nb) {
+    if (nb <= 1) return (const void*)&decode_kernel<FMT, MTV, 1, XB, NLD>;
+    if (nb <= 2) return (const void*)&decode_kernel<FMT, MTV, 2, XB, NLD>;
+    return (const void*)&decode_kernel<FMT, MTV, 4, XB, NLD>;
+}
+
+// Rank tiles per wave held in VGPRs: the wave plan balances whole heads to within a
+// tile of TT / 8, so MTV = ceil(TT / 8) covers every wave for the usual rank mixes (a
+// wave with more streams the rest of its tiles from L2).
 template <int FMT, int XB, int NLD>
-static int launch_decode(const DecodeParams& p, int upw, int grid, hipStream_t stream) {
-    const void* fn = nullptr;
-    switch (upw) {
-        case 1: fn = (const void*)&decode_kernel<FMT, 1, XB, NLD>; break;
-        case 2: fn = (const void*)&decode_kernel<FMT, 2, XB, NLD>; break;
-        default: fn = (const void*)&decode_kernel<FMT, 4, XB, NLD>; break;
-    }
+static int launch_decode(const DecodeParams& p, int nb, int grid, hipStream_t stream) {
+    const int need = (p.TT + NWAVE - 1) / NWAVE;
+    const void* fn = need <= 4 ? pick_nb<FMT, 4, XB, NLD>(nb)
+                     : need <= 8 ? pick_nb<FMT, 8, XB, NLD>(nb)
+                     : need <= 9 ? pick_nb<FMT, 9, XB, NLD>(nb)
+                                 : pick_nb<FMT, 10, XB, NLD>(nb);
     void* args[] = {(void*)&p};
     SKV_HIP(hipLaunchKernel(fn, dim3(grid), dim3(NTHR), args, 0, stream));
     return STARKV_OK;
@@ -906,12 +1001,8 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     SKV_CHECK(a.q_s1 % 8 == 0 && a.q_s0 % 8 == 0 && ((uintptr_t)a.q % 16) == 0,
               "decode: query rows must be 16-byte aligned (strides multiples of 8)");
     SKV_CHECK(a.ku_s0 % 8 == 0 && ((uintptr_t)a.k_up % 16) == 0, "decode: k_up rows must be 16-byte aligned");
-    const int ncb = (a.v_rank + 15) / 16;
-    const int hblk = (a.Hq + 15) / 16;
-    const int units = ncb * hblk;
-    SKV_CHECK(units <= MAX_PV_UNITS, "decode: %d x %d P.V tiles exceed %d (v_rank %d, heads %d)", hblk, ncb,
-              MAX_PV_UNITS, a.v_rank, a.Hq);
-    const int upw = units <= NWAVE ? 1 : units <= 2 * NWAVE ? 2 : 4;
+    const int nb = (a.v_rank + 63) / 64;
+    SKV_CHECK(nb <= 4, "decode: v_rank %d > 256", a.v_rank);
 
     p.bt = a.bt; p.bt_s0 = a.bt_s0; p.bt_s1 = a.bt_s1;
     p.n = a.n; p.Hq = a.Hq; p.TT = TT; p.v_rank = a.v_rank;
@@ -920,20 +1011,17 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     p.pitch_g = p.row_g | 1;
     p.pitch_b = p.pitch_g * 16;
     p.nkv = (TILE_TOK * p.pitch_g + 63) / 64;
-    p.cs_lds = p.nkv * 1024;
-    p.nch = p.nkv + CS_CHUNKS;
-    p.nld = (p.nch + NWAVE - 1) / NWAVE;
+    const int nch = CS_CHUNKS + p.nkv;
     const int xb = fmt == FMT_Q4 ? XB_Q4 : XB_LOWRANK;
-    SKV_CHECK(p.nld <= (fmt == FMT_Q4 ? NLD_Q4 : MAX_NLD) && p.nch * 1024 <= xb,
-              "decode: a page needs %d bytes of LDS (> %d): row %d bytes is too wide", p.nch * 1024, xb, row_bytes);
+    const int nld = fmt == FMT_Q4 ? NLD_Q4 : MAX_NLD;
+    SKV_CHECK(nch <= nld * NWAVE && nch * 1024 <= xb,
+              "decode: a page needs %d KB of LDS (> %d): row %d bytes is too wide", nch, nld * NWAVE, row_bytes);
     p.ws = (uint8_t*)a.ws;
-    p.ws_tiles = wl.tiles; p.ws_htile = wl.htile; p.ws_ab = wl.ab;
+    p.ws_tiles = wl.tiles; p.ws_plan = wl.plan; p.ws_ab = wl.ab;
     p.ws_m = wl.m; p.ws_l = wl.l; p.ws_acc = wl.acc;
-    p.ncb = ncb;
-    p.units = units;
 
     hipLaunchKernelGGL(setup_kernel, dim3(1), dim3(1024), 0, stream, a.seq_lens, a.n, a.max_seq_len, a.grid, a.Hq,
-                       a.Hkv, TT, a.k_ranks, a.k_offsets, a.t_head, a.t_nout, a.t_last, p.ws, wl.tiles, wl.htile);
+                       a.Hkv, TT, a.k_ranks, a.k_offsets, a.t_head, a.t_nout, a.t_last, p.ws, wl.tiles, wl.plan);
     SKV_HIP(hipGetLastError());
     hipLaunchKernelGGL(fold_tiles_kernel, dim3((TT * 128 + 255) / 256, a.n), dim3(256), 0, stream, a.q, a.q_s0,
                        a.q_s1, a.q_dt, a.k_up, a.ku_s0, a.w_dt, (const uint8_t*)p.ws + wl.tiles, TT,
@@ -941,17 +1029,17 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     SKV_HIP(hipGetLastError());
     const bool timed = g_prof.on && 2 * g_prof.used + 1 < (int)g_prof.ev.size();
     if (timed) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
-    int rc = fmt == FMT_Q4 ? launch_decode<FMT_Q4, XB_Q4, NLD_Q4>(p, upw, a.grid, stream)
-             : fmt == FMT_BF16 ? launch_decode<FMT_BF16, XB_LOWRANK, MAX_NLD>(p, upw, a.grid, stream)
-                               : launch_decode<FMT_F16, XB_LOWRANK, MAX_NLD>(p, upw, a.grid, stream);
+    int rc = fmt == FMT_Q4 ? launch_decode<FMT_Q4, XB_Q4, NLD_Q4>(p, nb, a.grid, stream)
+             : fmt == FMT_BF16 ? launch_decode<FMT_BF16, XB_LOWRANK, MAX_NLD>(p, nb, a.grid, stream)
+                               : launch_decode<FMT_F16, XB_LOWRANK, MAX_NLD>(p, nb, a.grid, stream);
     if (rc) return rc;
     SKV_HIP(hipGetLastError());
     if (timed) {
         SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used + 1], stream));
         ++g_prof.used;
     }
-    hipLaunchKernelGGL(merge_kernel, dim3(a.n, a.Hq), dim3(128), a.v_rank * 4, stream, (const uint8_t*)p.ws, wl.m,
-                       wl.l, wl.acc, a.Hq, a.v_rank, a.vup, a.vu_s0, a.vu_s1, a.w_dt, a.out, a.o_s0, a.o_s1,
+    hipLaunchKernelGGL(merge_kernel, dim3(a.n, a.Hq), dim3(128), a.v_rank * 4, stream, (const uint8_t*)p.ws, wl.plan,
+                       wl.m, wl.l, wl.acc, a.Hq, a.v_rank, a.vup, a.vu_s0, a.vu_s1, a.w_dt, a.out, a.o_s0, a.o_s1,
                        a.out_dt);
     SKV_HIP(hipGetLastError());
     return STARKV_OK;
