@@ -98,8 +98,8 @@ static WsLayout ws_layout(int n, int Hq, int TT, int v_rank, int grid) {
 
 struct DecodeParams {
     const uint8_t* cache; int64_t c_s0, c_s1;      // bytes
-    int block_size;
-    const int32_t* bt; int64_t bt_s0, bt_s1;
+    int bs_shift;                                  // block_size = 16 << bs_shift
+    const int32_t* bt; int bt_s0, bt_s1;
     int n, Hq, TT, k_width, v_rank;
     int ks_off, vs_off, vq_off, v_nout, v_nbo;     // QuantRow (3.2-bit)
     int row_g, pitch_g, pitch_b;                   // row granules (16 B), LDS row pitch (granules, bytes)
@@ -300,14 +300,15 @@ __global__ __launch_bounds__(256) void fold_tiles_kernel(const void* __restrict_
 typedef const __attribute__((address_space(4))) int32_t* cint_p;
 
 struct Cursor {
-    int b, k, lo, hi;  // request, page, request-local token range [lo, hi) of this workgroup
+    int b, k, lo, hi, len;  // request, page, request-local token range [lo, hi) of this workgroup, length
     bool valid;
 };
 
 __device__ __forceinline__ void cur_set(Cursor& c, cint_p P, int beg, int end) {
-    const int pb = P[c.b];
+    const int pb = P[c.b], pe = P[c.b + 1];
     c.lo = max(beg, pb) - pb;
-    c.hi = min(end, P[c.b + 1]) - pb;
+    c.hi = min(end, pe) - pb;
+    c.len = pe - pb;
     c.k = c.lo / TILE_TOK;
 }
 
@@ -383,10 +384,12 @@ __device__ __forceinline__ void dma_page(const DecodeParams& p, const Cursor& c,
     // descriptors: no memory access), so every page of the loop issues the same NLD
     // copies and the waits stay static.
     const bool v = c.valid;
-    const int tok0 = v ? TILE_TOK * c.k : 0;
-    const int blk = v ? ((cint_p)p.bt)[c.b * p.bt_s0 + (tok0 / p.block_size) * p.bt_s1] : 0;
-    const uint8_t* page = p.cache + (int64_t)blk * p.c_s0 + (int64_t)(tok0 % p.block_size) * p.c_s1;
-    const int rows = v ? min(TILE_TOK, P[c.b + 1] - P[c.b] - tok0) : 0;
+    const int k = v ? c.k : 0;
+    const int blk = v ? ((cint_p)p.bt)[c.b * p.bt_s0 + (k >> p.bs_shift) * p.bt_s1] : 0;
+    const int row0 = (k & ((1 << p.bs_shift) - 1)) * TILE_TOK;  // first slot of the page inside its block
+    const uint8_t* page = p.cache + (int64_t)blk * p.c_s0 + (int64_t)row0 * p.c_s1;
+    const int tok0 = TILE_TOK * k;
+    const int rows = v ? min(TILE_TOK, c.len - tok0) : 0;
     const int4v_t rkv = buffer_rsrc(page, rows * (int)p.c_s1);
     const int4v_t rcs = buffer_rsrc(p.cs + (int64_t)tok0 * p.cs_s0b, rows * p.cs_s0b);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)buf;
@@ -959,6 +962,13 @@ static int launch_decode(const DecodeParams& p, int nb, int grid, hipStream_t st
     return STARKV_OK;
 }
 
+// log2(block_size / 16), or -1 if block_size is not 16 times a power of two.
+static int block_shift(int block_size) {
+    for (int s = 0; s < 16; ++s)
+        if (block_size == (TILE_TOK << s)) return s;
+    return -1;
+}
+
 struct CommonArgs {
     const void* q; int64_t q_s0, q_s1; int q_dt;
     const int32_t* bt; int64_t bt_s0, bt_s1;
@@ -986,7 +996,11 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     const WsLayout wl = ws_layout(a.n, a.Hq, TT, a.v_rank, a.grid);
     SKV_CHECK(a.ws_bytes >= wl.total, "decode: workspace %zu bytes < %zu needed", a.ws_bytes, wl.total);
     SKV_CHECK(((uintptr_t)a.ws % 256) == 0, "decode: workspace must be 256-byte aligned");
-    SKV_CHECK(p.block_size % TILE_TOK == 0, "decode: block_size %d must be a multiple of 16", p.block_size);
+    SKV_CHECK(p.bs_shift >= 0, "decode: block_size must be 16 times a power of two");
+    SKV_CHECK(a.bt_s0 >= 0 && a.bt_s1 >= 0 &&
+                  (int64_t)a.n * a.bt_s0 + (int64_t)(a.max_seq_len + TILE_TOK - 1) / TILE_TOK * a.bt_s1 <
+                      ((int64_t)1 << 31),
+              "decode: block_table strides must keep element indices below 2^31");
     SKV_CHECK(((uintptr_t)p.cache % 16) == 0 && p.c_s0 % 16 == 0 && p.c_s1 % 16 == 0,
               "decode: cache base and byte strides must be 16-byte aligned (c_s0=%lld c_s1=%lld)", (long long)p.c_s0,
               (long long)p.c_s1);
@@ -1004,7 +1018,7 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     const int nb = (a.v_rank + 63) / 64;
     SKV_CHECK(nb <= 4, "decode: v_rank %d > 256", a.v_rank);
 
-    p.bt = a.bt; p.bt_s0 = a.bt_s0; p.bt_s1 = a.bt_s1;
+    p.bt = a.bt; p.bt_s0 = (int)a.bt_s0; p.bt_s1 = (int)a.bt_s1;
     p.n = a.n; p.Hq = a.Hq; p.TT = TT; p.v_rank = a.v_rank;
     p.cs = (const uint8_t*)a.cs; p.cs_s0b = (int)(a.cs_s0 * 2);
     p.row_g = row_bytes / 16;
@@ -1119,7 +1133,7 @@ int starkv_lowrank_decode(void* stream, const void* query, int64_t q_s0, int64_t
     p.cache = (const uint8_t*)kv_cache;
     p.c_s0 = c_s0 * 2;
     p.c_s1 = c_s1 * 2;
-    p.block_size = block_size;
+    p.bs_shift = block_shift(block_size);
     p.k_width = k_width;
     CommonArgs a{query, q_s0, q_s1, q_dtype, block_table, bt_s0, bt_s1, seq_lens, n, num_heads, num_kv_heads,
                  max_seq_len, k_up, ku_s0, w_dtype, k_ranks, k_head_offsets, nullptr, nullptr, nullptr,
@@ -1149,7 +1163,7 @@ int starkv_quant_decode(void* stream, const void* query, int64_t q_s0, int64_t q
     p.cache = kv_cache;
     p.c_s0 = c_s0;
     p.c_s1 = c_s1;
-    p.block_size = block_size;
+    p.bs_shift = block_shift(block_size);
     p.k_width = k_width;
     const int v_nout = (int)(0.2 * (double)v_rank);
     p.v_nout = v_nout;

@@ -6,7 +6,7 @@ decode path itself. Inputs follow the reference benchmark configurations:
 * K ranks per head drawn from {16, 32, 48, 64} (widths = ranks rounded to 16,
   offsets = prefix sums, checkpoint.py:125-128), one head-shared V rank per layer;
 * physical pages: block 0 is the null block, pages 1..N are a random permutation,
-  filled into each request's block-table row in order; block size 16;
+  filled into each request's block-table row in order; block size 16 unless given;
 * codes, queries ~ N(0, 1); K bases N(0, 1) / sqrt(rank), V bases N(0, 1) / sqrt(r_v);
   scale 1/sqrt(128); cos_sin_cache[p] = [cos(p theta) | sin(p theta)],
   theta_i = 10000^(-2i/128), computed in fp32 and stored in the model dtype;
@@ -95,7 +95,8 @@ class Workload:
         """Algorithmic HBM bytes of one decode call: every valid cache row once, the
         block-table entries, q and out, the bases and the cos/sin rows."""
         row = self.row.nbytes if self.quant else (self.k_width + self.v_rank) * self.kv_cache.element_size()
-        pages = sum((L + BLOCK_SIZE - 1) // BLOCK_SIZE for L in self.lengths)
+        bs = self.kv_cache.shape[1]
+        pages = sum((L + bs - 1) // bs for L in self.lengths)
         n, H = self.query.shape[0], self.query.shape[1]
         es = self.query.element_size()
         return (self.tokens * row + pages * 4 + 2 * n * H * HEAD_DIM * es + self.k_up.numel() * self.k_up.element_size()
@@ -109,8 +110,8 @@ class Workload:
         return self.tokens * (2 * HEAD_DIM * W + 2 * H * self.v_rank) + n * 2 * H * self.v_rank * HEAD_DIM
 
 
-def _page_layout(lengths, gen, extra_blocks=0):
-    pages = [(L + BLOCK_SIZE - 1) // BLOCK_SIZE for L in lengths]
+def _page_layout(lengths, gen, extra_blocks=0, block_size=BLOCK_SIZE):
+    pages = [(L + block_size - 1) // block_size for L in lengths]
     total = sum(pages)
     perm = (torch.randperm(total, generator=gen) + 1).to(torch.int32) if total else torch.zeros(0, dtype=torch.int32)
     max_blocks = max(1, max(pages) if pages else 1)
@@ -122,13 +123,13 @@ def _page_layout(lengths, gen, extra_blocks=0):
     return bt, total + 1 + extra_blocks
 
 
-def _token_slots(lengths, bt):
+def _token_slots(lengths, bt, block_size=BLOCK_SIZE):
     """(block, slot) for every token in (b, l) order."""
     blocks, slots = [], []
     for b, L in enumerate(lengths):
         l = torch.arange(L)
-        blocks.append(bt[b, (l // BLOCK_SIZE)].long())
-        slots.append(l % BLOCK_SIZE)
+        blocks.append(bt[b, (l // block_size)].long())
+        slots.append(l % block_size)
     if not blocks:
         return torch.zeros(0, dtype=torch.long), torch.zeros(0, dtype=torch.long)
     return torch.cat(blocks), torch.cat(slots)
@@ -136,7 +137,7 @@ def _token_slots(lengths, bt):
 
 def make_lowrank(lengths, num_heads=32, num_kv_heads=None, ranks=None, v_rank=64, seed=0, dtype=torch.bfloat16,
                  max_seq_len=None, col_pad=0, poison=True, peaked=1.0, gen_device="cpu",
-                 rank_choices=RANK_CHOICES) -> Workload:
+                 rank_choices=RANK_CHOICES, block_size=BLOCK_SIZE) -> Workload:
     """bf16/fp16 low-rank workload. `col_pad` > 0 makes the cache a column slice of a
     wider buffer (strided view); `poison` fills unused slots with NaN."""
     gen = torch.Generator(device="cpu").manual_seed(seed)
@@ -148,7 +149,7 @@ def make_lowrank(lengths, num_heads=32, num_kv_heads=None, ranks=None, v_rank=64
     W = sum(widths)
     n = len(lengths)
     max_seq_len = max_seq_len or max(max(lengths), 1)
-    bt, nblocks = _page_layout(lengths, gen)
+    bt, nblocks = _page_layout(lengths, gen, block_size=block_size)
     width = W + v_rank
 
     q = (torch.randn(n, num_heads, HEAD_DIM, generator=gen) * peaked).to(dtype)
@@ -160,20 +161,20 @@ def make_lowrank(lengths, num_heads=32, num_kv_heads=None, ranks=None, v_rank=64
     cs = cos_sin_table(max(max_seq_len, max(lengths) + 1), dtype)
 
     T = int(sum(lengths))
-    blk, slot = _token_slots(lengths, bt)
+    blk, slot = _token_slots(lengths, bt, block_size)
     if gen_device == "cpu":
         k_codes = torch.randn(T, W, generator=gen).to(dtype)
         v_codes = torch.randn(T, v_rank, generator=gen).to(dtype)
         for h in range(Hkv):  # lanes between a head's rank and its width hold zero codes
             k_codes[:, offsets[h] + ranks[h]:offsets[h] + widths[h]] = 0
-        buf = torch.full((nblocks, BLOCK_SIZE, width + col_pad), float("nan") if poison else 0.0, dtype=dtype)
+        buf = torch.full((nblocks, block_size, width + col_pad), float("nan") if poison else 0.0, dtype=dtype)
         buf[0] = 0  # the null block holds finite codes
         cache = buf[:, :, :width]
         cache[blk, slot, :W] = k_codes
         cache[blk, slot, W:] = v_codes
     else:
         g2 = torch.Generator(device=gen_device).manual_seed(seed + 7919)
-        buf = torch.empty((nblocks, BLOCK_SIZE, width + col_pad), dtype=dtype, device=gen_device)
+        buf = torch.empty((nblocks, block_size, width + col_pad), dtype=dtype, device=gen_device)
         buf.normal_(generator=g2)
         cache = buf[:, :, :width]
         for h in range(Hkv):
@@ -189,7 +190,7 @@ def make_lowrank(lengths, num_heads=32, num_kv_heads=None, ranks=None, v_rank=64
 
 def make_quant(lengths, num_heads=32, ranks=None, v_rank=64, seed=0, dtype=torch.bfloat16, max_seq_len=None,
                col_pad=0, device="cuda", peaked=1.0, rotate=True, rank_choices=RANK_CHOICES,
-               gen_device="cpu") -> Workload:
+               gen_device="cpu", block_size=BLOCK_SIZE) -> Workload:
     """3.2-bit workload: codes drawn (on `gen_device`), rotated, packed on `device` with pack_kv."""
     from starkv_serve.kernels.paged_quant import HADAMARD_SEED, QuantRow, block_hadamard, k_tables, n_outlier, pack_kv
     gen = torch.Generator(device="cpu").manual_seed(seed)
@@ -201,7 +202,7 @@ def make_quant(lengths, num_heads=32, ranks=None, v_rank=64, seed=0, dtype=torch
     W = sum(widths)
     n = len(lengths)
     max_seq_len = max_seq_len or max(max(lengths), 1)
-    bt, nblocks = _page_layout(lengths, gen)
+    bt, nblocks = _page_layout(lengths, gen, block_size=block_size)
     row = QuantRow(W, H, v_rank)
 
     q = (torch.randn(n, H, HEAD_DIM, generator=gen) * peaked).to(dtype)
@@ -236,9 +237,9 @@ def make_quant(lengths, num_heads=32, ranks=None, v_rank=64, seed=0, dtype=torch
     v_up_by_q = v_up.to(dtype)
     cs = cos_sin_table(max(max_seq_len, max(lengths) + 1), dtype)
 
-    blk, slot = _token_slots(lengths, bt)
-    slots = (blk * BLOCK_SIZE + slot).to(torch.int64)
-    buf = torch.randint(0, 256, (nblocks, BLOCK_SIZE, row.nbytes + col_pad), generator=gen, dtype=torch.uint8)
+    blk, slot = _token_slots(lengths, bt, block_size)
+    slots = (blk * block_size + slot).to(torch.int64)
+    buf = torch.randint(0, 256, (nblocks, block_size, row.nbytes + col_pad), generator=gen, dtype=torch.uint8)
     cache = buf[:, :, :row.nbytes]
     nouts, hol, tiles = k_tables(ranks, "cpu")
     wl = Workload(query=q, kv_cache=cache, block_table=bt, seq_lens=torch.tensor(lengths, dtype=torch.int32),

@@ -91,6 +91,8 @@ LOWRANK_CASES = {
     "v_rank_256_h16": ([333, 48], dict(v_rank=256, num_heads=16)),
     "graph_span": ([100, 37, 999], dict(max_seq_len=4096)),
     "ranks_not_16": ([77, 260], dict(ranks=[20, 1, 33, 64, 7, 48, 16, 50], num_heads=8)),
+    "block_32": ([1000, 47, 64], dict(block_size=32)),
+    "block_128": ([700, 129, 1], dict(block_size=128)),
 }
 
 
@@ -153,6 +155,13 @@ def test_lowrank_zero_length_and_truncation(cuda):
     assert_close(out[[0, 2]], truth[[0, 2]], "truncated")
 
 
+def test_lowrank_block_size_not_power_of_two_is_rejected(cuda):
+    # Pages are located with shifts, so block_size must be 16 * 2^s (16, 32, 64, ...).
+    wl = W.make_lowrank([100, 20], num_heads=4, ranks=[16, 32, 48, 64], v_rank=32, seed=9, block_size=48)
+    with pytest.raises(RuntimeError, match="power of two"):
+        paged_starkv_decode(*wl.to(cuda).decode_args())
+
+
 # ---------------------------------------------------------------------------
 # 3.2-bit
 # ---------------------------------------------------------------------------
@@ -179,7 +188,7 @@ def check_packed_rows(wl_gpu, count=64):
                    [ref.n_outlier(r) for r in wl_gpu.ranks], wl_gpu.v_rank, lay["ks_off"], lay["vs_off"],
                    lay["vq_off"])
     c = wl_gpu.kv_cache.cpu().numpy()
-    got = c[slots[idx] // 16, slots[idx] % 16]
+    got = c[slots[idx] // c.shape[1], slots[idx] % c.shape[1]]
     end = lay["vq_off"] + lay["v_bytes"]
     assert np.array_equal(got[:, :end], want[:, 0, :end])
 
@@ -192,6 +201,7 @@ QUANT_CASES = {
     "strided_cache": ([200, 31], dict(col_pad=48)),
     "graph_span": ([100, 37, 999], dict(max_seq_len=4096)),
     "fp16": ([513, 90], dict(dtype=torch.float16)),
+    "block_64": ([900, 65, 3], dict(block_size=64)),
 }
 
 
