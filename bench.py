@@ -30,7 +30,10 @@ for _p in (ROOT, os.path.join(ROOT, "star-kv-serve_amd")):
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_PEAK_F16_TFLOPS = 2500.0  # dense fp16/bf16
-METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
+METRIC = "decode-attn \u00b5s & HBM GB/s (% peak) at bs64\u00d78K; TPOT, tok/s at max sessions"
+# HBM bytes per decode-kernel launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+# scaled by the same counters on a copy of known size); written by hand from the runs.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_kernel_hbm_traffic.md")
 
 
 def log(*a):
@@ -84,6 +87,29 @@ def bench_quant(lengths, steps, warmup, seed, copies, v_rank=64):
 
     ms, kern = time_steps(step, steps, warmup)
     return wl, ms, kern
+
+
+def measured_traffic(key):
+    """HBM bytes per launch for `key` from the committed counter summary, or None."""
+    import re
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(r"^%s_hbm_bytes_per_launch:\s*([0-9]+)\s*$" % re.escape(key), text, re.M)
+    return int(m.group(1)) if m else None
+
+
+def copy_probe(gib, reps):
+    """A plain device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    n = int(gib * (1 << 30))
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "reps": reps}), flush=True)
 
 
 def summarize(wl, ms, kern):
@@ -142,6 +168,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true", help="skip the 3.2-bit and ragged configurations")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=["bf16", "quant"], default=None,
+                    help="profile runs: time one bs64 x 8192 workload only and print its summary")
+    ap.add_argument("--copy-probe", type=float, default=0.0, metavar="GIB",
+                    help="profile runs: only copy GIB GiB device to device 5 times (counter scaling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (decode shards by request; "
@@ -151,12 +181,22 @@ def main():
     import torch
     torch.cuda.set_device(0)
     log(f"device: {torch.cuda.get_device_name(0)}")
+    if args.copy_probe > 0:
+        copy_probe(args.copy_probe, 5)
+        return
 
     lengths = [8192] * 64
+    if args.only == "quant":
+        wq, msq, kq = bench_quant(lengths, args.steps, args.warmup, seed=1003, copies=3)
+        print(json.dumps(summarize(wq, msq, kq)), flush=True)
+        return
     log("headline: bf16 low-rank, 64 x 8192")
     wl, ms, kern = bench_lowrank(lengths, args.steps, args.warmup, seed=1001)
     head = summarize(wl, ms, kern)
     log(json.dumps(head))
+    if args.only == "bf16":
+        print(json.dumps(head), flush=True)
+        return
 
     extra = {}
     if not args.no_extra:
@@ -164,19 +204,20 @@ def main():
         log("3.2-bit, 64 x 8192 (3 rotating caches)")
         wq, msq, kq = bench_quant(lengths, args.steps, args.warmup, seed=1003, copies=3)
         extra["quant_bs64x8k"] = summarize(wq, msq, kq)
+        extra["quant_bs64x8k"]["hbm_traffic_bytes"] = measured_traffic("quant_bs64x8k")
         log(json.dumps(extra["quant_bs64x8k"]))
         del wq
         torch.cuda.empty_cache()
-        log("config 1: bf16 low-rank, 64 requests, lengths U[1024, 8192]")
-        w1, ms1, k1 = bench_lowrank(W.config_lengths(1), args.steps, args.warmup, seed=1001)
-        extra["lowrank_config1"] = summarize(w1, ms1, k1)
-        log(json.dumps(extra["lowrank_config1"]))
+        log("bf16 low-rank, 64 requests, lengths U[1024, 8192]")
+        w1, ms1, k1 = bench_lowrank(W.ragged_lengths(1001), args.steps, args.warmup, seed=1001)
+        extra["lowrank_bs64_ragged_1k_8k"] = summarize(w1, ms1, k1)
+        log(json.dumps(extra["lowrank_bs64_ragged_1k_8k"]))
         del w1
         torch.cuda.empty_cache()
-        log("config 2: 3.2-bit, 64 requests, lengths U[1024, 8192] (3 rotating caches)")
-        w2, ms2, k2 = bench_quant(W.config_lengths(2), args.steps, args.warmup, seed=1002, copies=3)
-        extra["quant_config2"] = summarize(w2, ms2, k2)
-        log(json.dumps(extra["quant_config2"]))
+        log("3.2-bit, 64 requests, lengths U[1024, 8192] (3 rotating caches)")
+        w2, ms2, k2 = bench_quant(W.ragged_lengths(1002), args.steps, args.warmup, seed=1002, copies=3)
+        extra["quant_bs64_ragged_1k_8k"] = summarize(w2, ms2, k2)
+        log(json.dumps(extra["quant_bs64_ragged_1k_8k"]))
         del w2
         torch.cuda.empty_cache()
 
@@ -204,7 +245,7 @@ def main():
                    "k_width": wl.k_width, "v_rank": wl.v_rank, "k_ranks": "uniform {16,32,48,64} per head",
                    "decode_us": head["us_per_step"]},
         "roofline": {"bound": "hbm", "achieved": head["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": head["hbm_frac"], "traffic": None,
+                     "frac": head["hbm_frac"], "traffic": measured_traffic("bf16_bs64x8k"),
                      "kernel": "decode_kernel", "kernel_us": head["decode_kernel_us"],
                      "bytes_per_launch": head["bytes_per_step"], "mfma_frac_fp16": head["mfma_frac"]},
         "cpu_baseline": cpu,

@@ -106,7 +106,7 @@ size_t starkv_decode_workspace_bytes(int n, int num_heads, int k_tiles, int v_ra
  *   out[b,h] = (softmax(logit) @ V_codes) @ v_up_by_q[h].
  *   query       [n, H_q, 128] (element strides q_s0, q_s1; last dim contiguous)
  *   kv_cache    [num_blocks, block_size, k_width + v_rank], element strides c_s0, c_s1,
- *               last dim contiguous; code_dtype bf16 or fp16; block_size a multiple of 16
+ *               last dim contiguous; code_dtype bf16 or fp16; block_size 16 * 2^s
  *   block_table [n, max_blocks] int32 (strides bt_s0, bt_s1); seq_lens [n] int32
  *   k_up        [k_width, 128] (row stride ku_s0), k_ranks / k_head_offsets [H_kv] int32
  *   v_up_by_q   [H_q, v_rank, 128] (strides vu_s0, vu_s1)

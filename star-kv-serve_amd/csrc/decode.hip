@@ -28,7 +28,8 @@
 //    the wave's row groups in one go with the gfx950 lane swaps. The online softmax of
 //    the wave's heads runs one head per 16-lane row (lazy running max: the reference
 //    point moves only when a logit exceeds it by 2^8), and P[heads, 16] @ V[16, v_rank]
-//    runs on v_mfma_f32_16x16x16 into per-wave accumulators.
+//    runs on v_mfma_f32_4x4x4 (P broadcast from lanes 0-3, one V column per lane) into
+//    per-wave accumulators.
 // 4. merge: per (request, head) log-sum-exp of the partials, then the lift through
 //    v_up_by_q.
 #include <stdio.h>

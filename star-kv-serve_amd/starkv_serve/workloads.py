@@ -255,13 +255,7 @@ def make_quant(lengths, num_heads=32, ranks=None, v_rank=64, seed=0, dtype=torch
     return wl
 
 
-# Reference benchmark configurations (lengths only; ranks and values come from the seed).
-def config_lengths(cfg: int, gen_seed: int = None) -> list:
-    g = torch.Generator().manual_seed(1000 + cfg if gen_seed is None else gen_seed)
-    if cfg == 0:
-        return [4096]
-    if cfg in (1, 2):
-        return torch.randint(1024, 8193, (64,), generator=g).tolist()
-    if cfg == 3:
-        return [32768] * 16
-    raise ValueError(cfg)
+def ragged_lengths(seed: int, n: int = 64, lo: int = 1024, hi: int = 8192) -> list:
+    """n request lengths drawn uniformly from [lo, hi] with a CPU generator seeded `seed`."""
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(lo, hi + 1, (n,), generator=g).tolist()

@@ -81,7 +81,7 @@ def run_lowrank(wl_gpu, grid=None):
 
 LOWRANK_CASES = {
     # name: (lengths, kwargs)
-    "c0_b1_4096": ([4096], {}),
+    "b1_4096": ([4096], {}),
     "ragged_edges": ([1, 15, 16, 17, 100, 1000, 33, 2], {}),
     "gqa_h32_kv8": ([300, 17, 64], dict(num_kv_heads=8)),
     "fp16": ([513, 90, 2048], dict(dtype=torch.float16)),
@@ -122,15 +122,15 @@ def test_lowrank_reference_emulation_error_is_reported(cuda):
     assert mo["rel_l2"] <= me["rel_l2"] * 1.5 + 1e-4
 
 
-def test_lowrank_config1_full_size(cuda):
-    lengths = W.config_lengths(1)
-    print(f"\n[lowrank] config 1: 64 requests, {sum(lengths)} tokens", flush=True)
+def test_lowrank_bs64_ragged_full_size(cuda):
+    lengths = W.ragged_lengths(1001)
+    print(f"\n[lowrank] 64 requests, lengths U[1024, 8192]: {sum(lengths)} tokens", flush=True)
     wl = W.make_lowrank(lengths, num_heads=32, seed=1001, gen_device=cuda)
     g = wl.to(cuda)
     out = paged_starkv_decode(*g.decode_args())
     torch.cuda.synchronize()
     truth = lowrank_truth(wl)
-    assert_close(out, truth, "config1")
+    assert_close(out, truth, "bs64_ragged")
     # Size-independent property: permuting the physical pages changes nothing, bit for bit.
     nb = g.kv_cache.shape[0]
     perm = torch.cat([torch.zeros(1, dtype=torch.long), 1 + torch.randperm(nb - 1)]).to(cuda)
@@ -142,7 +142,7 @@ def test_lowrank_config1_full_size(cuda):
     assert torch.equal(out, out2)
     # Different workgroup splits agree with the oracle too.
     for grid in (1, 7, 300):
-        assert_close(run_lowrank(g, grid=grid), truth, f"config1 grid={grid}")
+        assert_close(run_lowrank(g, grid=grid), truth, f"bs64_ragged grid={grid}")
 
 
 def test_lowrank_zero_length_and_truncation(cuda):
@@ -194,7 +194,7 @@ def check_packed_rows(wl_gpu, count=64):
 
 
 QUANT_CASES = {
-    "c0_b1_4096": ([4096], {}),
+    "b1_4096": ([4096], {}),
     "ragged_edges": ([1, 15, 16, 17, 100, 1000, 33, 2], {}),
     "v_rank_32": ([640, 129], dict(v_rank=32)),
     "peaked_q": ([1500, 700], dict(peaked=4.0)),
@@ -217,11 +217,11 @@ def test_quant_decode_vs_oracle(cuda, name):
     assert_close(out, quant_truth(wl), name)
 
 
-def test_quant_config2_full_size(cuda):
-    lengths = W.config_lengths(2)
-    print(f"\n[quant] config 2: 64 requests, {sum(lengths)} tokens", flush=True)
+def test_quant_bs64_ragged_full_size(cuda):
+    lengths = W.ragged_lengths(1002)
+    print(f"\n[quant] 64 requests, lengths U[1024, 8192]: {sum(lengths)} tokens", flush=True)
     wl = W.make_quant(lengths, num_heads=32, seed=1002, device=cuda, gen_device=cuda)
     check_packed_rows(wl, count=256)
     out = paged_quant_decode(*wl.decode_args())
     torch.cuda.synchronize()
-    assert_close(out, quant_truth(wl), "config2")
+    assert_close(out, quant_truth(wl), "quant_bs64_ragged")
