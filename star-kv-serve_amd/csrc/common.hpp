@@ -203,8 +203,13 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0(int n) {
 }
 
 // Workgroup barrier that does not drain outstanding global->LDS copies: the
-// caller has already waited for what it needs (lgkmcnt(0) included).
-__device__ __forceinline__ void lds_barrier() { __builtin_amdgcn_s_barrier(); }
+// caller has already waited for what it needs (lgkmcnt(0) included). The empty asm
+// keeps the compiler from moving LDS accesses across it (the barrier intrinsic itself
+// is not a memory operation to the optimizer).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 __device__ __forceinline__ void wait_lgkm0_barrier() {
     __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0) only

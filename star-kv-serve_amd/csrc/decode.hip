@@ -32,85 +32,11 @@
 //    per-wave accumulators.
 // 4. merge: per (request, head) log-sum-exp of the partials, then the lift through
 //    v_up_by_q.
-#include <stdio.h>
-
 #include <vector>
 
-#include "common.hpp"
+#include "decode_common.hpp"
 
 namespace starkv {
-
-enum { FMT_BF16 = 0, FMT_F16 = 1, FMT_Q4 = 2 };
-
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef float float2_t __attribute__((ext_vector_type(2)));
-typedef short short4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-
-constexpr int NWAVE = 8;
-constexpr int NTHR = NWAVE * 64;
-constexpr int TILE_TOK = 16;
-constexpr int MAX_REQ_PER_CALL = 1024;
-constexpr float LOG2E = 1.4426950408889634f;
-constexpr int AB_TILE_BYTES = 4 * 64 * 16;  // 4 K-steps x 64 lanes x 8 fp16
-constexpr int AB_SLACK_TILES = 16;
-constexpr int MAX_TT = 96;                  // rank tiles per call (k_width x heads per kv head <= 1536)
-constexpr int MAX_H = 32;                   // query heads
-constexpr int MAX_HW = 8;                   // query heads per wave
-constexpr int MAX_SLOTS = 16;               // rank tiles per wave
-constexpr int PLAN_STRIDE = 64;             // ints per wave in the plan
-constexpr int MAX_NLD = 6;                  // 16-byte copies per lane per page (bf16/fp16 rows)
-constexpr int NLD_Q4 = 3;                   // 3.2-bit rows
-constexpr int CS_ROW_LDS = 256;             // LDS bytes per cos/sin row (granules XOR-swizzled by row)
-constexpr int CS_CHUNKS = 4;                // 16 rows x 16 granules -> 4 copies of 64 granules
-constexpr int XB_LOWRANK = 48 * 1024;       // LDS bytes per page buffer
-constexpr int XB_Q4 = 24 * 1024;
-constexpr float LAZY_MAX = 8.f;             // log2 headroom before the running max moves
-
-// Workspace layout, in bytes from the base (every region 256-byte aligned):
-//   hdr    int   [2 + n]      S (tokens per workgroup), P[0..n] (prefix of clamped lengths)
-//   tiles  int4  [TT]         {q head, first cache lane, valid | nout << 8 | last << 16, kv head}
-//   plan   int   [8][64] + 1  per wave: [0] tiles, [1] heads, [8 + s] tile of slot s,
-//                             [32 + k] q head of local head k, [40 + k] its first slot,
-//                             [48 + k] its slots; then 1 if every head found a wave
-//   ab     fp16  [n][TT][4][64][8]
-//   m, l   fp32  [slots][Hq]  (log2-domain reference max and sum per partial)
-//   acc    fp32  [slots][Hq][v_rank]
-struct WsLayout {
-    size_t hdr, tiles, plan, ab, m, l, acc, total;
-};
-
-static inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-static WsLayout ws_layout(int n, int Hq, int TT, int v_rank, int grid) {
-    WsLayout w;
-    const size_t slots = (size_t)grid + n;
-    size_t o = 0;
-    w.hdr = o; o = al256(o + (size_t)(n + 2) * 4);
-    w.tiles = o; o = al256(o + (size_t)TT * 16);
-    w.plan = o; o = al256(o + (size_t)(NWAVE * PLAN_STRIDE + 1) * 4);
-    w.ab = o; o = al256(o + ((size_t)n * TT + AB_SLACK_TILES) * AB_TILE_BYTES);
-    w.m = o; o = al256(o + slots * Hq * 4);
-    w.l = o; o = al256(o + slots * Hq * 4);
-    w.acc = o; o = al256(o + slots * Hq * (size_t)v_rank * 4);
-    w.total = o;
-    return w;
-}
-
-struct DecodeParams {
-    const uint8_t* cache; int64_t c_s0, c_s1;      // bytes
-    int bs_shift;                                  // block_size = 16 << bs_shift
-    const int32_t* bt; int bt_s0, bt_s1;
-    int n, Hq, TT, k_width, v_rank;
-    int ks_off, vs_off, vq_off, v_nout, v_nbo;     // QuantRow (3.2-bit)
-    int row_g, pitch_g, pitch_b;                   // row granules (16 B), LDS row pitch (granules, bytes)
-    int nkv;                                       // 1 KB copies of K/V rows per page (after 4 of cos/sin)
-    const uint8_t* cs; int cs_s0b;                 // fp16 cos/sin table, row stride in bytes
-    uint8_t* ws;
-    size_t ws_tiles, ws_plan, ws_ab, ws_m, ws_l, ws_acc;
-};
-
-__device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // ---------------------------------------------------------------------------
 // 1. setup: tile table, prefix sums and wave plan. One workgroup of 1024 threads.
@@ -295,54 +221,7 @@ __global__ __launch_bounds__(256) void fold_tiles_kernel(const void* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// Token cursor: which (request, page) a workgroup visits next. P (the prefix of
-// the clamped lengths) is read with scalar loads from the workspace header.
-// ---------------------------------------------------------------------------
-typedef const __attribute__((address_space(4))) int32_t* cint_p;
-
-struct Cursor {
-    int b, k, lo, hi, len;  // request, page, request-local token range [lo, hi) of this workgroup, length
-    bool valid;
-};
-
-__device__ __forceinline__ void cur_set(Cursor& c, cint_p P, int beg, int end) {
-    const int pb = P[c.b], pe = P[c.b + 1];
-    c.lo = max(beg, pb) - pb;
-    c.hi = min(end, pe) - pb;
-    c.len = pe - pb;
-    c.k = c.lo / TILE_TOK;
-}
-
-__device__ __forceinline__ void cur_first(Cursor& c, cint_p P, int n, int beg, int end) {
-    int lo = 0, hi = n - 1;  // largest b with P[b] <= beg; then P[b + 1] > beg
-    while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (P[mid] <= beg) lo = mid; else hi = mid - 1;
-    }
-    c.b = lo;
-    c.valid = beg < end;
-    if (c.valid) cur_set(c, P, beg, end);
-}
-
-// Returns true when the next page starts a new request (the current one ended).
-__device__ __forceinline__ bool cur_next(Cursor& c, cint_p P, int n, int beg, int end) {
-    if (TILE_TOK * (c.k + 1) < c.hi) {
-        ++c.k;
-        return false;
-    }
-    int b = c.b + 1;
-    while (b < n && P[b + 1] == P[b]) ++b;
-    if (b >= n || P[b] >= end) {
-        c.valid = false;
-        return true;
-    }
-    c.b = b;
-    cur_set(c, P, beg, end);
-    return true;
-}
-
-// ---------------------------------------------------------------------------
-// Global -> LDS copy of one page. LDS layout of a page buffer: the page's 16 cos/sin
+// 3.2-bit page copies. LDS layout of a page buffer: the page's 16 cos/sin
 // rows first (256 bytes each, granule c of row r stored at granule c ^ r, so the MFMA
 // operand reads of 16 rows hit distinct banks: 4 copies of 1 KB), then the 16 token
 // rows at a pitch of pitch_g granules (odd, so rows fall on different banks; granules
@@ -354,30 +233,6 @@ __device__ __forceinline__ bool cur_next(Cursor& c, cint_p P, int n, int beg, in
 // in the buffer's unused tail) carry an offset past the descriptor's range, so they
 // touch no memory, and one vmcnt value covers a page on every wave.
 // ---------------------------------------------------------------------------
-typedef int int4v_t __attribute__((ext_vector_type(4)));
-
-// Raw buffer descriptor: 48-bit base, stride 0, `bytes` in range (offsets at or past it
-// are not read), gfx9 data format word.
-__device__ __forceinline__ int4v_t buffer_rsrc(const void* base, int bytes) {
-    const uint64_t a = (uint64_t)base;
-    return (int4v_t){(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), bytes, 0x00020000};
-}
-
-// One 16-byte-per-lane global->LDS copy: lane q's 16 bytes at `voff` land at LDS
-// byte lds + 16 q. Issued as inline assembly so that the compiler does not track it:
-// it would otherwise wait for copies into other page buffers before reads of the
-// current one. The waits for these copies are explicit (vmcnt at the page barrier).
-// M0 takes the LDS address; one wait state separates the M0 write from its use.
-__device__ __forceinline__ void lds_copy16(const int4v_t& rsrc, uint32_t lds, uint32_t voff) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %1, %2, 0 offen lds"
-        :
-        : "s"(lds), "v"(voff), "s"(rsrc)
-        : "memory", "m0");
-}
-
 template <int NLD>
 __device__ __forceinline__ void dma_page(const DecodeParams& p, const Cursor& c, cint_p P, uint8_t* buf, int wave,
                                          const uint32_t (&doff)[MAX_NLD]) {
@@ -403,42 +258,6 @@ __device__ __forceinline__ void dma_page(const DecodeParams& p, const Cursor& c,
         else  // rows; filler granules and surplus copies carry an out-of-range offset
             lds_copy16(rkv, dst, doff[i]);
     }
-}
-
-// The kernel's parameter block, read through a pointer the optimizer cannot see
-// through: loads of it are redone where they are used (scalar loads that hit the
-// scalar cache) instead of being hoisted out of the main loop into SGPRs.
-typedef const __attribute__((address_space(4))) DecodeParams kparams_t;
-
-__device__ __forceinline__ const DecodeParams& params() {
-    kparams_t* pp = (kparams_t*)__builtin_amdgcn_kernarg_segment_ptr();
-    asm volatile("" : "+s"(pp));
-    return *(const DecodeParams*)pp;  // address-space inference keeps these scalar loads
-}
-
-__device__ __forceinline__ int4 load_tile(cint_p tiles, int t) {
-    return make_int4(tiles[4 * t], tiles[4 * t + 1], tiles[4 * t + 2], tiles[4 * t + 3]);
-}
-
-__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
-__device__ __forceinline__ uint32_t h2_bits(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
-__device__ __forceinline__ half2_t cvt_h2(float a, float b) {
-    return __builtin_convertvector((float2_t){a, b}, half2_t);  // v_cvt_pk_f16_f32, round to nearest even
-}
-__device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
-
-__device__ __forceinline__ uint2 ld64(const uint8_t* p) {
-    const uint64_t v = *(const uint64_t*)p;
-    return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
-}
-
-__device__ __forceinline__ f32x4_t mfma_tile(const half8_t (&a)[4], const half8_t (&cs)[4]) {
-    f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-    z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], cs[0], z, 0, 0, 0);
-    z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1], cs[1], z, 0, 0, 0);
-    z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[2], cs[2], z, 0, 0, 0);
-    z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[3], cs[3], z, 0, 0, 0);
-    return z;
 }
 
 // A lane's share of one rank tile's logit for token (lane & 15): its 4 z values (rows
@@ -538,13 +357,6 @@ __device__ __forceinline__ void k_side(const DecodeParams& p, const WaveTiles<MT
     }
 }
 
-// Online softmax of this wave's heads: local head (lane >> 4) on a 16-lane row, token
-// lane & 15.
-struct SmState {
-    float m, l;   // log2-domain reference max (same on the head's 16 lanes), this lane's column sum
-    int hf, hn;   // the row's head: first slot, slots (0 for no head)
-};
-
 // Returns true when some head's reference max moved (acc needs rescaling by alpha).
 template <int FMT>
 __device__ __forceinline__ bool softmax_page(SmState& sm, int nh, const float* sp, uint16_t* spp, uint16_t* spl,
@@ -641,43 +453,6 @@ __device__ __forceinline__ void pv_page(const DecodeParams& p, f32x4_t (&acc)[NB
         }
     }
 }
-
-// The partial of the request that ends with this page: m, l and acc of this wave's
-// heads into partial slot `slot`, then reset. The wave's query-head ids come from LDS:
-// a vector load here would leave a tracked load in flight at the loop's join, and the
-// compiler would then drain every copy before the next page's first LDS read.
-template <int NB>
-__device__ __forceinline__ void flush_partial(const DecodeParams& p, SmState& sm, f32x4_t (&acc)[NB], int nh,
-                                              int slot, const int* sqh, int lane) {
-    const int ln = opaque(lane);
-    const int kh = ln >> 4, lr = ln & 15;
-    const int64_t base = (int64_t)slot * p.Hq;
-    const float lt = row16_sum(sm.l);
-    if (kh < nh && lr == 0) {
-        const int qh = sqh[kh];
-        ((float*)(p.ws + p.ws_m))[base + qh] = sm.m;
-        ((float*)(p.ws + p.ws_l))[base + qh] = lt;
-    }
-    sm.m = -INFINITY;
-    sm.l = 0.f;
-    float* wa = (float*)(p.ws + p.ws_acc) + base * p.v_rank;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int qh = sqh[e];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const int c = 64 * nb + ln;
-            if (e < nh && c < p.v_rank) wa[(int64_t)qh * p.v_rank + c] = acc[nb][e];
-            acc[nb][e] = 0.f;
-        }
-    }
-}
-
-struct LoopState {
-    Cursor cc, ld;
-    int j, beg, end, g;
-    bool new_seg;
-};
 
 // ---------------------------------------------------------------------------
 // One page of the decode loop: XC holds page j (copied two pages ago) and XN receives
@@ -1026,11 +801,18 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     p.pitch_g = p.row_g | 1;
     p.pitch_b = p.pitch_g * 16;
     p.nkv = (TILE_TOK * p.pitch_g + 63) / 64;
-    const int nch = CS_CHUNKS + p.nkv;
-    const int xb = fmt == FMT_Q4 ? XB_Q4 : XB_LOWRANK;
-    const int nld = fmt == FMT_Q4 ? NLD_Q4 : MAX_NLD;
-    SKV_CHECK(nch <= nld * NWAVE && nch * 1024 <= xb,
-              "decode: a page needs %d KB of LDS (> %d): row %d bytes is too wide", nch, nld * NWAVE, row_bytes);
+    if (fmt == FMT_Q4) {
+        const int nch = CS_CHUNKS + p.nkv;
+        SKV_CHECK(nch <= NLD_Q4 * NWAVE && nch * 1024 <= XB_Q4,
+                  "decode: a page needs %d KB of LDS (> %d): row %d bytes is too wide", nch, NLD_Q4 * NWAVE,
+                  row_bytes);
+    } else {
+        SKV_CHECK(lowrank_copies(p.k_width, nb) > 0,
+                  "decode: a page of k_width %d and v_rank %d needs more than 48 KB of LDS per buffer", p.k_width,
+                  a.v_rank);
+        p.nch = lowrank_chunks(p.k_width, nb);
+        p.lds_bytes = lowrank_lds_bytes(p.k_width, nb);
+    }
     p.ws = (uint8_t*)a.ws;
     p.ws_tiles = wl.tiles; p.ws_plan = wl.plan; p.ws_ab = wl.ab;
     p.ws_m = wl.m; p.ws_l = wl.l; p.ws_acc = wl.acc;
@@ -1045,8 +827,7 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     const bool timed = g_prof.on && 2 * g_prof.used + 1 < (int)g_prof.ev.size();
     if (timed) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
     int rc = fmt == FMT_Q4 ? launch_decode<FMT_Q4, XB_Q4, NLD_Q4>(p, nb, a.grid, stream)
-             : fmt == FMT_BF16 ? launch_decode<FMT_BF16, XB_LOWRANK, MAX_NLD>(p, nb, a.grid, stream)
-                               : launch_decode<FMT_F16, XB_LOWRANK, MAX_NLD>(p, nb, a.grid, stream);
+                           : launch_lowrank(p, fmt, nb, a.grid, stream);
     if (rc) return rc;
     SKV_HIP(hipGetLastError());
     if (timed) {

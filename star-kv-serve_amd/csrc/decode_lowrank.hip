@@ -1,0 +1,572 @@
+// bf16/fp16 low-rank paged decode: the decode launch of starkv_lowrank_decode
+// (decode.hip holds the setup, fold and merge launches and the host entry points).
+//
+// One persistent workgroup of 8 waves per CU walks its contiguous token range page by
+// page (16 tokens). Each wave owns whole query heads and holds their rank tiles of AB
+// (q folded into U) in VGPRs. Per page: z = AB . [cos|sin]^T on MFMA, the lanes fold z
+// with the codes, the wave's heads run an online softmax, and P @ V accumulates on MFMA.
+//
+// LDS. The three page buffers are interleaved at 1 KB: chunk c of buffer b sits at
+// byte c * 3072 + b * 1024 of the dynamic block. Every read of the current page is a
+// per-lane address computed once per kernel plus the immediate b * 1024, so the page
+// loop does no address arithmetic. The chunks of a page:
+//   0 .. 3            cos/sin rows 4c .. 4c+3, 256 B per row; granule g of row r is
+//                     stored at granule g ^ r, so the 16 rows of an MFMA operand read
+//                     hit distinct banks
+//   4 .. 4+2NB-1      V codes, row t at t * NB * 128 B (columns past v_rank unused)
+//   4+2NB+m           K codes of code tiles 2m (at +0) and 2m+1 (at +512), row r at +32 r
+// Copy i of wave w moves chunk 8 i + w; lane q's offset inside the page depends only on
+// (chunk, q) and is computed once (`doff`). Copies past the page's chunks land in a
+// 1 KB dummy block after the buffers and read nothing.
+
+#include "decode_common.hpp"
+
+namespace starkv {
+
+namespace {
+
+constexpr int LR_STRIDE = 3072;  // bytes between chunks c and c + 1 of one buffer
+// Dynamic LDS limit: 160 KB per CU minus the kernel's static arrays (partial logits,
+// P, alpha, head ids: under 12 KB).
+constexpr int LR_MAX_DYN_LDS = 160 * 1024 - 12 * 1024;
+
+template <int NB>
+struct LrChunks {
+    static constexpr int V0 = CS_CHUNKS;           // first V chunk
+    static constexpr int K0 = CS_CHUNKS + 2 * NB;  // first K chunk
+    static constexpr int VPITCH = NB * 128;        // V row pitch in LDS
+};
+
+typedef short short2_t __attribute__((ext_vector_type(2)));
+
+template <typename T>
+__device__ __forceinline__ T lds_ld(uint32_t a) {
+    return *(const __attribute__((address_space(3))) T*)(a);
+}
+template <typename T>
+__device__ __forceinline__ void lds_st(uint32_t a, T v) {
+    *(__attribute__((address_space(3))) T*)(a) = v;
+}
+__device__ __forceinline__ uint2 lds_ld2(uint32_t a) {
+    const uint64_t v = lds_ld<uint64_t>(a);
+    return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+
+// A 16-byte-per-lane copy to LDS address m0 (a wave-uniform SGPR value).
+__device__ __forceinline__ void copy16(const int4v_t& rsrc, uint32_t m0, uint32_t voff) { lds_copy16(rsrc, m0, voff); }
+
+// Per-lane LDS byte addresses (buffer 0), fixed for the whole kernel.
+template <int MTV>
+struct LaneAddr {
+    uint32_t cs[4];               // B operand: row lr, granule 4 ks + lg
+    uint32_t k[MTV];              // slot i: 8 code bytes of row lr, ranks 4 lg .. 4 lg + 3
+    uint32_t v;                   // V: column lane of row 0
+    uint32_t st[(MTV + 3) / 4];   // partial-logit row of this lane's slot in each group of 4
+    uint32_t sm;                  // softmax: first of the 4 rows of head lane >> 4
+    uint32_t pw, pr;              // P: write (head lane >> 4, token lane & 15), read (head lane & 3)
+    uint32_t base;                // the page buffers (wave-uniform)
+};
+
+// Loop-invariant operands of the page copies, read once from the parameter block and
+// held in SGPRs.
+struct DmaConst {
+    const uint8_t* cache; int64_t c_s0; int c_s1;
+    const int32_t* bt; int bt_s0, bt_s1, bs_shift;
+    const uint8_t* cs; int cs_s0b;
+    int nch;
+    uint32_t m0w, m0dummy;  // LDS address of this wave's first chunk (buffer 0); the dummy block
+};
+
+struct LrLoop {
+    Cursor cc, ld;
+    int beg, end, g;
+    int nblk;  // block of the page `ld` points at, loaded one page ahead of its copies
+    bool new_seg;
+};
+
+// Cache block of the page cursor c points at (0 past the range).
+__device__ __forceinline__ int page_block(const DmaConst& dc, const Cursor& c) {
+    return c.valid ? ((cint_p)dc.bt)[c.b * dc.bt_s0 + (c.k >> dc.bs_shift) * dc.bt_s1] : 0;
+}
+
+// Buffer descriptors of one page: its rows and its cos/sin rows, bounded to the rows
+// the request has (rows past its end are not read). Past the end of the workgroup's
+// range both are empty: the copies still issue, so every page issues NLD copies and
+// the waits stay static.
+struct DmaPage {
+    int4v_t rkv, rcs;
+};
+
+__device__ __forceinline__ DmaPage dma_setup(const DmaConst& dc, const Cursor& c, int blk) {
+    const bool v = c.valid;
+    const int k = v ? c.k : 0;
+    const int row0 = (k & ((1 << dc.bs_shift) - 1)) * TILE_TOK;  // first slot of the page in its block
+    const uint8_t* page = dc.cache + (int64_t)blk * dc.c_s0 + (int64_t)row0 * dc.c_s1;
+    const int tok0 = TILE_TOK * k;
+    const int rows = v ? min(TILE_TOK, c.len - tok0) : 0;
+    DmaPage d;
+    d.rkv = buffer_rsrc(page, rows * dc.c_s1);
+    d.rcs = buffer_rsrc(dc.cs + (int64_t)tok0 * dc.cs_s0b, rows * dc.cs_s0b);
+    return d;
+}
+
+// Copy i of this wave into buffer B: chunk 8 i + wave (cos/sin rows for chunks < 4).
+template <int B>
+__device__ __forceinline__ void dma_one(const DmaConst& dc, const DmaPage& d, int i, int wave, uint32_t off) {
+    const int ch = i * NWAVE + wave;
+    const uint32_t m0 = ch < dc.nch ? dc.m0w + (uint32_t)(i * NWAVE * LR_STRIDE + B * 1024) : dc.m0dummy;
+    if (i == 0 && wave < CS_CHUNKS)
+        copy16(d.rcs, m0, off);
+    else
+        copy16(d.rkv, m0, off);
+}
+
+template <int NLD, int B>
+__device__ __forceinline__ void dma_page(const DmaConst& dc, const Cursor& c, int blk, int wave,
+                                         const uint32_t (&doff)[NLD]) {
+    const DmaPage d = dma_setup(dc, c, blk);
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) dma_one<B>(dc, d, i, wave, doff[i]);
+}
+
+// Copy schedule. A page's copies must reach the copy queue at about the rate the queue
+// drains: a burst fills it, and a wave whose copy finds it full stalls until it has room.
+// The iteration offers copy points: 0 right after the barrier, 1 .. MTV after each K
+// tile, MTV + 1 after the softmax, MTV + 2 .. MTV + 5 after each P @ V step. Their
+// rough positions in the iteration (as fractions of its length) are below. Copy c of the
+// waves on the first wave slot of each SIMD (waves 0-3) goes to the point nearest c / NLD,
+// and of the others (waves 4-7) to the point nearest (c + 1/2) / NLD, so that the two
+// waves of a SIMD never issue at the same point.
+template <int MTV>
+constexpr float copy_point_time(int pos) {
+    return pos == 0 ? 0.f
+           : pos <= MTV ? 0.6f * (float)pos / (float)MTV
+           : pos == MTV + 1 ? 0.75f
+                            : 0.75f + 0.0625f * (float)(pos - MTV - 1);
+}
+
+template <int MTV, int NLD>
+constexpr int copy_point(int c, int half) {
+    const float t = ((float)c + (half ? 0.5f : 0.f)) / (float)NLD;
+    int best = 0;
+    float bd = 2.f;
+    for (int pos = 0; pos <= MTV + 5; ++pos) {
+        const float d = copy_point_time<MTV>(pos) > t ? copy_point_time<MTV>(pos) - t : t - copy_point_time<MTV>(pos);
+        if (d < bd) {
+            bd = d;
+            best = pos;
+        }
+    }
+    return best;
+}
+
+// Issues the copies of this wave that the schedule puts at copy point `pos` (a
+// constant once the callers' loops are unrolled).
+template <int MTV, int NLD, int B>
+__device__ __forceinline__ void copies_at(int pos, const DmaConst& dc, const DmaPage& d, int wave,
+                                          const uint32_t (&doff)[NLD]) {
+#pragma unroll
+    for (int c = 0; c < NLD; ++c) {
+        if (copy_point<MTV, NLD>(c, 0) == pos && wave < NWAVE / 2) dma_one<B>(dc, d, c, wave, doff[c]);
+        if (copy_point<MTV, NLD>(c, 1) == pos && wave >= NWAVE / 2) dma_one<B>(dc, d, c, wave, doff[c]);
+    }
+}
+
+// z . codes for one tile: this lane's 4 z values (rows 4 lg .. 4 lg + 3) times its 4
+// codes (8 bytes).
+template <int FMT>
+__device__ __forceinline__ float tile_dot(const f32x4_t& z, uint2 w) {
+    if (FMT == FMT_BF16) {
+        float v = __uint_as_float(w.x << 16) * z[0];
+        v = fmaf(__uint_as_float(w.x & 0xffff0000u), z[1], v);
+        v = fmaf(__uint_as_float(w.y << 16), z[2], v);
+        return fmaf(__uint_as_float(w.y & 0xffff0000u), z[3], v);
+    } else {
+        return dot2(as_h2(w.x), cvt_h2(z[0], z[1]), dot2(as_h2(w.y), cvt_h2(z[2], z[3]), 0.f));
+    }
+}
+
+// Row of the wave's partial-logit table that slot s writes: with every head at <= 4
+// slots (`fast`), head k's j-th slot goes to row 4 k + j, so a head's rows past its
+// slots stay zero and the softmax sums 4 fixed rows; otherwise row s. Slots past the
+// wave's tiles write the spare row MAX_SLOTS.
+__device__ __forceinline__ int slot_row(cint_p pw, int s, int ntw, int nh, bool fast) {
+    if (s >= ntw) return MAX_SLOTS;
+    if (!fast) return s;
+    int row = MAX_SLOTS;
+    for (int k = 0; k < nh; ++k) {
+        const int f = pw[40 + k], c = pw[48 + k];
+        if (s >= f && s < f + c) row = 4 * k + (s - f);
+    }
+    return row;
+}
+
+// K side of one page (buffer B): MTV slots from VGPR AB, more from L2. Each group of
+// 4 slots is summed over the row groups with the lane swaps and stored as 4 rows.
+template <int FMT, int MTV, int NB, int B, int NLD, int BN>
+__device__ __forceinline__ void k_side(const DecodeParams& p, const LaneAddr<MTV>& la, const half8_t (&ab)[MTV][4],
+                                       int ntw, int nh, bool fast, uint32_t sp, int lane, int wave, int cur_b,
+                                       const DmaConst& dc, const DmaPage& dp, const uint32_t (&doff)[NLD]) {
+    half8_t csb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) csb[ks] = lds_ld<half8_t>(la.cs[ks] + B * 1024);
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < MTV; ++i) {
+        const f32x4_t z = mfma_tile(ab[i], csb);
+        v[i & 3] = tile_dot<FMT>(z, lds_ld2(la.k[i] + B * 1024));
+        if ((i & 3) == 3 || i == MTV - 1) {
+            const float r = sum_rows4(v[0], (i & 3) >= 1 ? v[1] : 0.f, (i & 3) >= 2 ? v[2] : 0.f,
+                                      (i & 3) >= 3 ? v[3] : 0.f);
+            lds_st<float>(la.st[i >> 2], r);
+        }
+        copies_at<MTV, NLD, BN>(1 + i, dc, dp, opaque_s(wave), doff);
+    }
+    if (ntw > MTV) {  // slots past MTV: AB from the workspace (L2) on every page
+        const int lg = lane >> 4, lr = lane & 15;
+        cint_p pw = (cint_p)(p.ws + p.ws_plan) + wave * PLAN_STRIDE;
+        cint_p tiles = (cint_p)(p.ws + p.ws_tiles);
+        const half8_t* abg = (const half8_t*)(p.ws + p.ws_ab + (size_t)cur_b * p.TT * AB_TILE_BYTES);
+        for (int i = MTV; i < ntw; ++i) {
+            const int t = pw[8 + i];
+            half8_t a[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) a[ks] = abg[(t * 4 + ks) * 64 + lane];
+            const int T = ((cint_p)tiles)[4 * t + 1] >> 4;
+            const uint32_t ka = la.base + (uint32_t)((LrChunks<NB>::K0 + (T >> 1)) * LR_STRIDE + (T & 1) * 512 +
+                                                        lr * 32 + 8 * lg + B * 1024);
+            const float r = sum_rows(tile_dot<FMT>(mfma_tile(a, csb), lds_ld2(ka)));
+            const int row = slot_row(pw, i, ntw, nh, fast);
+            if (lane < 16) lds_st<float>(sp + (uint32_t)(row * TILE_TOK + lr) * 4, r);
+        }
+        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): no tracked load left pending
+    }
+}
+
+// Online softmax of the wave's heads (head lane >> 4 on a 16-lane row, token lane & 15).
+// Returns true when some head's reference max moved (acc needs rescaling by alpha).
+template <int FMT>
+__device__ __forceinline__ bool softmax_page(SmState& sm, const uint32_t sm_addr, bool fast, uint32_t sp, int nh,
+                                             uint32_t pw_addr, uint32_t plo_off, uint32_t salpha, int lane, int tok0,
+                                             int lo, int hi) {
+    const int kh = lane >> 4, lr = lane & 15;
+    float s;
+    if (fast) {
+        s = (lds_ld<float>(sm_addr) + lds_ld<float>(sm_addr + 64)) +
+            (lds_ld<float>(sm_addr + 128) + lds_ld<float>(sm_addr + 192));
+    } else {
+        s = 0.f;
+        for (int t = 0; t < sm.hn; ++t) s += lds_ld<float>(sp + (uint32_t)((sm.hf + t) * TILE_TOK + lr) * 4);
+    }
+    const int tok = tok0 + lr;
+    s = tok >= lo && tok < hi && kh < nh ? s : -INFINITY;
+    float alpha = 1.f;
+    bool moved = false;
+    if (__builtin_amdgcn_ballot_w64(s > sm.m + LAZY_MAX) != 0) {
+        const float mn = fmaxf(sm.m, row16_max(s));
+        alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(sm.m - mn);
+        sm.m = mn;
+        moved = true;
+        if (lr == 0) lds_st<float>(salpha + 4 * kh, alpha);
+    }
+    const float pe = s == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - sm.m);
+    sm.l = fmaf(sm.l, alpha, pe);
+    if (FMT == FMT_BF16) {
+        // P = hi + lo in two bfloat16 parts: the P @ V product keeps ~16 bits of P.
+        const __bf16 ph = (__bf16)pe;
+        const __bf16 pl = (__bf16)(pe - (float)ph);
+        lds_st<uint16_t>(pw_addr, __builtin_bit_cast(uint16_t, ph));
+        lds_st<uint16_t>(pw_addr + plo_off, __builtin_bit_cast(uint16_t, pl));
+    } else {
+        lds_st<uint16_t>(pw_addr, __builtin_bit_cast(uint16_t, (_Float16)pe));
+    }
+    return moved;
+}
+
+// Two 16-bit V codes (rows t0, t1 of column lane) packed into one word.
+__device__ __forceinline__ uint32_t v_pair(uint32_t a0, uint32_t a1) {
+    short2_t x;
+    x.x = lds_ld<short>(a0);
+    x.y = lds_ld<short>(a1);
+    return __builtin_bit_cast(uint32_t, x);
+}
+
+// acc[nb] = alpha * acc[nb] + P[4 heads, 16 tokens] @ V[16 tokens, 64 columns] on
+// v_mfma_f32_4x4x4_16b with block 0's A broadcast (cbsz 4): per 4-token step lanes 0..3
+// hold P[head l][4 tokens], lane l holds V[4 tokens][column 64 nb + l], and the result
+// lands in lane l as acc[nb][head] for its column.
+template <int FMT, int NB, int B, int MTV, int NLD, int BN>
+__device__ __forceinline__ void pv_page(f32x4_t (&acc)[NB], uint32_t v_addr, uint32_t pr_addr, uint32_t plo_off,
+                                        uint32_t salpha, bool rescale, const DmaConst& dc, const DmaPage& dp,
+                                        int wave, const uint32_t (&doff)[NLD]) {
+    typedef LrChunks<NB> C;
+    if (rescale) {
+        const f32x4_t al = lds_ld<f32x4_t>(salpha);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[nb][e] *= al[e];
+    }
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        const uint2 pa = lds_ld2(pr_addr + 8 * st);
+        const uint2 pl = FMT == FMT_BF16 ? lds_ld2(pr_addr + plo_off + 8 * st) : make_uint2(0, 0);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            uint32_t off[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int byte = (4 * st + e) * C::VPITCH + 128 * nb;  // inside the V region
+                off[e] = (uint32_t)((byte >> 10) * LR_STRIDE + (byte & 1023) + B * 1024);
+            }
+            const uint2 bv = make_uint2(v_pair(v_addr + off[0], v_addr + off[1]), v_pair(v_addr + off[2], v_addr + off[3]));
+            if (FMT == FMT_BF16) {
+                acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(short4_t, pa),
+                                                                 __builtin_bit_cast(short4_t, bv), acc[nb], 4, 0, 0);
+                acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(short4_t, pl),
+                                                                 __builtin_bit_cast(short4_t, bv), acc[nb], 4, 0, 0);
+            } else {
+                acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, pa),
+                                                             __builtin_bit_cast(half4_t, bv), acc[nb], 4, 0, 0);
+            }
+        }
+        if (st == 0) copies_at<MTV, NLD, BN>(MTV + 2, dc, dp, opaque_s(wave), doff);
+        if (st == 1) copies_at<MTV, NLD, BN>(MTV + 3, dc, dp, opaque_s(wave), doff);
+        if (st == 2) copies_at<MTV, NLD, BN>(MTV + 4, dc, dp, opaque_s(wave), doff);
+        if (st == 3) copies_at<MTV, NLD, BN>(MTV + 5, dc, dp, opaque_s(wave), doff);
+    }
+}
+
+// One page of the loop: buffer BC holds page j (copied two pages ago); buffer BN
+// receives page j + 2 (page j - 1, its previous content, is done on every wave once the
+// barrier is passed).
+template <int FMT, int MTV, int NB, int NLD, int BC, int BN>
+__device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const LaneAddr<MTV>& la,
+                                        half8_t (&ab)[MTV][4], f32x4_t (&acc)[NB], SmState& sm,
+                                        const uint32_t (&doff)[NLD], int ntw, int nh, bool fast, uint32_t sp,
+                                        uint32_t plo_off, uint32_t salpha, const int* sqh, int lane, int wave) {
+    const DecodeParams& p = params();
+    cint_p P = (cint_p)(p.ws + 4);
+    if (!st.cc.valid) return false;
+    const Cursor cc = st.cc;
+    if (st.new_seg) {
+        // This request's AB into registers; slots past the wave's tiles load tile 0.
+        cint_p pw = (cint_p)(p.ws + p.ws_plan) + wave * PLAN_STRIDE;
+        const half8_t* abp = (const half8_t*)(p.ws + p.ws_ab + (size_t)cc.b * p.TT * AB_TILE_BYTES);
+#pragma unroll
+        for (int i = 0; i < MTV; ++i) {
+            const int t = pw[8 + i];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) ab[i][ks] = abp[(t * 4 + ks) * 64 + lane];
+        }
+        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0)
+    }
+    SKV_WAIT_VM_LGKM0(NLD);  // only the copies of page j + 1 may still be in flight
+    lds_barrier();           // page j is in LDS; every wave is done with page j - 1
+    const DmaPage dp = dma_setup(dc, st.ld, st.nblk);
+    copies_at<MTV, NLD, BN>(0, dc, dp, opaque_s(wave), doff);
+    if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
+    k_side<FMT, MTV, NB, BC, NLD, BN>(p, la, ab, ntw, nh, fast, sp, lane, wave, cc.b, dc, dp, doff);
+    const bool moved = softmax_page<FMT>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, TILE_TOK * cc.k,
+                                         cc.lo, cc.hi);
+    copies_at<MTV, NLD, BN>(MTV + 1, dc, dp, opaque_s(wave), doff);
+    pv_page<FMT, NB, BC, MTV, NLD, BN>(acc, la.v, la.pr, plo_off, salpha, moved, dc, dp, wave, doff);
+    Cursor nx = cc;
+    const bool seg_end = cur_next(nx, P, p.n, st.beg, st.end);
+    if (seg_end) flush_partial<NB>(p, sm, acc, nh, cc.b + st.g, sqh, lane);
+    st.cc = nx;
+    st.new_seg = seg_end;
+    // The block of the page the next iteration copies: its load completes under the
+    // wait at the next page's barrier.
+    st.nblk = page_block(dc, st.ld);
+    return true;
+}
+
+template <int FMT, int MTV, int NB, int NLD>
+__global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_pages[];
+    __shared__ __attribute__((aligned(16))) float s_part[NWAVE][(MAX_SLOTS + 1) * TILE_TOK];
+    __shared__ __attribute__((aligned(16))) uint16_t s_p[NWAVE][4 * TILE_TOK];
+    __shared__ __attribute__((aligned(16))) uint16_t s_plo[FMT == FMT_BF16 ? NWAVE : 1][4 * TILE_TOK];
+    __shared__ __attribute__((aligned(16))) float s_alpha[NWAVE][4];
+    __shared__ int s_qh[NWAVE][4];
+    typedef LrChunks<NB> C;
+
+    const DecodeParams& p = params();
+    const int tid = threadIdx.x, lane = tid & 63, wave = rfl(tid >> 6);
+    const int lg = lane >> 4, lr = lane & 15;
+    cint_p P = (cint_p)(p.ws + 4);
+    cint_p plan = (cint_p)(p.ws + p.ws_plan);
+    if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
+    LrLoop st;
+    st.g = blockIdx.x;
+    const int S_tok = ((cint_p)p.ws)[0];
+    const int T = P[p.n];
+    st.beg = min(st.g * S_tok, T);
+    st.end = min(st.beg + S_tok, T);
+    if (st.beg >= st.end) return;
+
+    // Page buffers and partial-logit rows start zeroed: rows past a request's end are
+    // never copied and must hold finite values (P is 0 there); a head's partial rows
+    // past its slots are summed as zeros.
+    for (int i = tid; i < p.lds_bytes / 16; i += NTHR) ((uint4*)s_pages)[i] = make_uint4(0, 0, 0, 0);
+    for (int i = tid; i < NWAVE * (MAX_SLOTS + 1) * TILE_TOK; i += NTHR) (&s_part[0][0])[i] = 0.f;
+    if (tid < NWAVE * 4) (&s_alpha[0][0])[tid] = 1.f;
+
+    // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
+    cint_p pw = plan + wave * PLAN_STRIDE;
+    const int ntw = pw[0], nh = pw[1];
+    bool fast = true;
+    for (int k = 0; k < nh; ++k) fast = fast && pw[48 + k] <= 4;
+    const uint32_t base = lds_addr(s_pages);
+    const uint32_t sp = lds_addr(&s_part[wave][0]);
+    LaneAddr<MTV> la;
+    {
+        cint_p tiles = (cint_p)(p.ws + p.ws_tiles);
+#pragma unroll
+        for (int i = 0; i < MTV; ++i) {
+            const int Tc = tiles[4 * pw[8 + i] + 1] >> 4;  // code tile: first cache lane / 16
+            la.k[i] = base + (uint32_t)((C::K0 + (Tc >> 1)) * LR_STRIDE + (Tc & 1) * 512 + lr * 32 + 8 * lg);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            la.cs[ks] = base + (uint32_t)((lr >> 2) * LR_STRIDE + (lr & 3) * 256 + (((4 * ks + lg) ^ lr) << 4));
+        la.v = base + (uint32_t)(C::V0 * LR_STRIDE + 2 * lane);
+        la.base = base;
+        const int rslot = ((lg & 1) << 1) | (lg >> 1);  // sum_rows4 puts inputs (a, b, c, d) in rows (0, 2, 1, 3)
+#pragma unroll
+        for (int g = 0; g < (MTV + 3) / 4; ++g) {
+            const int s = 4 * g + rslot;
+            const int row = s < MTV ? slot_row(pw, s, ntw, nh, fast) : MAX_SLOTS;
+            la.st[g] = sp + (uint32_t)(row * TILE_TOK + lr) * 4;
+        }
+        la.sm = sp + (uint32_t)(4 * lg * TILE_TOK + lr) * 4;
+        la.pw = lds_addr(&s_p[wave][0]) + (uint32_t)(lg * TILE_TOK + lr) * 2;
+        la.pr = lds_addr(&s_p[wave][0]) + (uint32_t)(lane & 3) * TILE_TOK * 2;
+    }
+    const uint32_t plo_off = lds_addr(&s_plo[FMT == FMT_BF16 ? wave : 0][0]) - lds_addr(&s_p[wave][0]);
+    const uint32_t salpha = lds_addr(&s_alpha[wave][0]);
+    if (lane < 4) s_qh[wave][lane] = lane < nh ? pw[32 + lane] : 0;
+    SmState sm;
+    sm.hf = lg < nh ? pw[40 + lg] : 0;
+    sm.hn = lg < nh ? pw[48 + lg] : 0;
+    sm.m = -INFINITY;
+    sm.l = 0.f;
+
+    // Copy offsets of this lane inside a page, per copy i (chunk 8 i + wave).
+    uint32_t doff[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+        const int ch = i * NWAVE + wave;
+        uint32_t off = 0x80000000u;  // past the descriptor range: no memory access
+        if (ch < CS_CHUNKS) {
+            const int row = 4 * ch + (lane >> 4), g = lane & 15;  // LDS granule g of row holds granule g ^ row
+            off = (uint32_t)(row * p.cs_s0b + ((g ^ row) << 4));
+        } else if (ch < C::K0) {
+            const int vb = (ch - C::V0) * 1024 + 16 * lane;  // byte inside the V rows
+            const int row = vb / C::VPITCH, col = vb % C::VPITCH;
+            if (col < 2 * p.v_rank) off = (uint32_t)(row * (int)p.c_s1 + 2 * p.k_width + col);
+        } else if (ch < p.nch) {
+            const int Tc = 2 * (ch - C::K0) + (lane >> 5), r = (lane >> 1) & 15, h = lane & 1;
+            if (Tc < p.k_width / 16) off = (uint32_t)(r * (int)p.c_s1 + 32 * Tc + 16 * h);
+        }
+        doff[i] = off;
+    }
+    DmaConst dc;
+    dc.cache = p.cache; dc.c_s0 = p.c_s0; dc.c_s1 = (int)p.c_s1;
+    dc.bt = p.bt; dc.bt_s0 = p.bt_s0; dc.bt_s1 = p.bt_s1; dc.bs_shift = p.bs_shift;
+    dc.cs = p.cs; dc.cs_s0b = p.cs_s0b;
+    dc.nch = p.nch;
+    dc.m0w = base + (uint32_t)(wave * LR_STRIDE);
+    dc.m0dummy = base + (uint32_t)(p.nch * LR_STRIDE);
+    __syncthreads();
+
+    cur_first(st.cc, P, p.n, st.beg, st.end);
+    st.ld = st.cc;
+    st.new_seg = true;
+    dma_page<NLD, 0>(dc, st.ld, page_block(dc, st.ld), wave, doff);
+    cur_next(st.ld, P, p.n, st.beg, st.end);
+    dma_page<NLD, 1>(dc, st.ld, page_block(dc, st.ld), wave, doff);
+    if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
+    st.nblk = page_block(dc, st.ld);
+
+    half8_t ab[MTV][4];
+    f32x4_t acc[NB];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) acc[k] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    const int* sqh = &s_qh[wave][0];
+    while (true) {
+        if (!lr_iter<FMT, MTV, NB, NLD, 0, 2>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, sqh,
+                                              lane, wave))
+            break;
+        if (!lr_iter<FMT, MTV, NB, NLD, 1, 0>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, sqh,
+                                              lane, wave))
+            break;
+        if (!lr_iter<FMT, MTV, NB, NLD, 2, 1>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, sqh,
+                                              lane, wave))
+            break;
+    }
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): no copy may land after the workgroup ends
+}
+
+template <int FMT, int MTV, int NLD>
+const void* pick_nb(int nb) {
+    if (nb <= 1) return (const void*)&lowrank_kernel<FMT, MTV, 1, NLD>;
+    if (nb <= 2) return (const void*)&lowrank_kernel<FMT, MTV, 2, NLD>;
+    return (const void*)&lowrank_kernel<FMT, MTV, 4, NLD>;
+}
+
+template <int FMT, int NLD>
+const void* pick_mtv(int need, int nb) {
+    return need <= 4 ? pick_nb<FMT, 4, NLD>(nb)
+           : need <= 8 ? pick_nb<FMT, 8, NLD>(nb)
+           : need <= 9 ? pick_nb<FMT, 9, NLD>(nb)
+                       : pick_nb<FMT, 10, NLD>(nb);
+}
+
+template <int FMT>
+const void* pick(int nld, int need, int nb) {
+    return nld <= 3 ? pick_mtv<FMT, 3>(need, nb) : pick_mtv<FMT, 6>(need, nb);
+}
+
+int nb_blocks(int nb) { return nb <= 1 ? 1 : nb <= 2 ? 2 : 4; }
+
+}  // namespace
+
+int lowrank_chunks(int k_width, int nb) {
+    const int tiles = k_width / 16;
+    return CS_CHUNKS + 2 * nb_blocks(nb) + (tiles + 1) / 2;
+}
+
+// Copies per wave per page: 3 or 6 (the instantiated counts), 0 if a page needs more.
+int lowrank_copies(int k_width, int nb) {
+    const int nld = (lowrank_chunks(k_width, nb) + NWAVE - 1) / NWAVE;
+    return nld <= 3 ? 3 : nld <= 6 ? 6 : 0;
+}
+
+int lowrank_lds_bytes(int k_width, int nb) { return lowrank_chunks(k_width, nb) * LR_STRIDE + 1024; }
+
+// Rank tiles per wave held in VGPRs: the wave plan balances whole heads to within a
+// tile of TT / 8, so MTV = ceil(TT / 8) covers every wave for the usual rank mixes (a
+// wave with more streams the rest of its tiles from L2).
+int launch_lowrank(const DecodeParams& p, int fmt, int nb, int grid, hipStream_t stream) {
+    const int need = (p.TT + NWAVE - 1) / NWAVE;
+    const int nld = lowrank_copies(p.k_width, nb);
+    const void* fn = fmt == FMT_BF16 ? pick<FMT_BF16>(nld, need, nb) : pick<FMT_F16>(nld, need, nb);
+    static const void* raised[256];  // kernels whose dynamic-LDS limit was raised (host-side bookkeeping)
+    static int nraised = 0;
+    bool seen = false;
+    for (int i = 0; i < nraised; ++i) seen = seen || raised[i] == fn;
+    if (!seen) {
+        SKV_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, LR_MAX_DYN_LDS));
+        if (nraised < 256) raised[nraised++] = fn;
+    }
+    void* args[] = {(void*)&p};
+    SKV_HIP(hipLaunchKernel(fn, dim3(grid), dim3(NTHR), args, (size_t)p.lds_bytes, stream));
+    return STARKV_OK;
+}
+
+}  // namespace starkv
