@@ -246,7 +246,7 @@ def main():
                    "decode_us": head["us_per_step"]},
         "roofline": {"bound": "hbm", "achieved": head["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": head["hbm_frac"], "traffic": measured_traffic("bf16_bs64x8k"),
-                     "kernel": "decode_kernel", "kernel_us": head["decode_kernel_us"],
+                     "kernel": "lowrank_kernel (bf16 decode)", "kernel_us": head["decode_kernel_us"],
                      "bytes_per_launch": head["bytes_per_step"], "mfma_frac_fp16": head["mfma_frac"]},
         "cpu_baseline": cpu,
         "extra": extra,
