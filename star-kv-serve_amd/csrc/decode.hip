@@ -41,6 +41,37 @@ namespace starkv {
 // ---------------------------------------------------------------------------
 // 1. setup: tile table, prefix sums and wave plan. One workgroup of 1024 threads.
 // ---------------------------------------------------------------------------
+// Wave-level integer reductions with DPP (the wave plan's steps are chains of them).
+template <int CTL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTL, 0xF, 0xF, true);
+}
+
+// Min / max over lanes 0 .. 7 (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror), as a
+// wave-uniform value. Every lane of the wave must be active.
+__device__ __forceinline__ int lanes8_min(int v) {
+    v = min(v, dpp_i<0xB1>(v));
+    v = min(v, dpp_i<0x4E>(v));
+    v = min(v, dpp_i<0x141>(v));
+    return __builtin_amdgcn_readfirstlane(v);
+}
+__device__ __forceinline__ int lanes8_max(int v) {
+    v = max(v, dpp_i<0xB1>(v));
+    v = max(v, dpp_i<0x4E>(v));
+    v = max(v, dpp_i<0x141>(v));
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
+// Min over all 64 lanes: within each row of 16 with DPP, then over the 4 rows.
+__device__ __forceinline__ int wave_min_i(int v) {
+    v = min(v, dpp_i<0xB1>(v));
+    v = min(v, dpp_i<0x4E>(v));
+    v = min(v, dpp_i<0x141>(v));
+    v = min(v, dpp_i<0x140>(v));
+    const int r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+    const int r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+    return min(min(r0, r1), min(r2, r3));
+}
 __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__ seq_lens, int n, int max_seq_len,
                                                      int grid, int Hq, int Hkv, int TT,
                                                      const int32_t* __restrict__ k_ranks,
@@ -52,13 +83,26 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
     __shared__ int s_wsum[16];
     __shared__ int s_total;
     __shared__ int s_hf[MAX_H], s_hn[MAX_H];
+    __shared__ int s_rank[MAX_H], s_off[MAX_H];        // k_ranks, k_offsets (bf16/fp16)
+    __shared__ int s_thead[MAX_TT], s_tmeta[MAX_TT];   // t_head, nout | last << 8 (3.2-bit)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int* hdr = (int*)ws;
     int4* tiles = (int4*)(ws + ws_tiles);
     int* plan = (int*)(ws + ws_plan);
 
-    // Prefix sums of min(max(seq_len, 0), max_seq_len) over n <= 1024 requests.
+    // Every global input is read at once, up front: the steps below only use LDS.
     const int a = tid < n ? min(max(seq_lens[tid], 0), max_seq_len) : 0;
+    if (t_head) {
+        if (tid < TT) {
+            s_thead[tid] = t_head[tid];
+            s_tmeta[tid] = t_nout[tid] | ((t_last[tid] != 0) << 8);
+        }
+    } else if (tid < Hkv) {
+        s_rank[tid] = k_ranks[tid];
+        s_off[tid] = k_offsets[tid];
+    }
+
+    // Prefix sums of min(max(seq_len, 0), max_seq_len) over n <= 1024 requests.
     int s = a;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -68,30 +112,31 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
     if (lane == 63) s_wsum[wave] = s;
     __syncthreads();
     int off = 0;
-    for (int w = 0; w < wave; ++w) off += s_wsum[w];
+#pragma unroll
+    for (int w = 0; w < 16; ++w) off += w < wave ? s_wsum[w] : 0;
     if (tid < n) hdr[2 + tid] = off + s;
     if (tid == 0) hdr[1] = 0;
     if (tid == 1023) s_total = off + s;
-    __syncthreads();
-    if (tid == 0) hdr[0] = (s_total + grid - 1) / grid;
 
     // Tile table and (first tile, tiles) per query head.
     if (t_head) {  // 3.2-bit: the k_tables arrays, lanes contiguous, MHA
         for (int t = tid; t < TT; t += blockDim.x)
-            tiles[t] = make_int4(t_head[t], 16 * t, 16 | (t_nout[t] << 8) | ((t_last[t] != 0) << 16), t_head[t]);
+            tiles[t] = make_int4(s_thead[t], 16 * t, 16 | ((s_tmeta[t] & 255) << 8) | ((s_tmeta[t] >> 8) << 16),
+                                 s_thead[t]);
         if (tid < Hq) {
             int first = -1, cnt = 0;
             for (int t = 0; t < TT; ++t)
-                if (t_head[t] == tid) { if (first < 0) first = t; ++cnt; }
+                if (s_thead[t] == tid) { if (first < 0) first = t; ++cnt; }
             s_hf[tid] = first < 0 ? 0 : first;
             s_hn[tid] = cnt;
         }
     } else if (tid < Hq) {  // bf16/fp16: ceil(rank / 16) tiles per query head, kv = h / group
-        const int grp = Hq / Hkv;
-        int t0 = 0;
-        for (int h = 0; h < tid; ++h) t0 += (k_ranks[h / grp] + 15) >> 4;
-        const int kv = tid / grp, R = k_ranks[kv], o = k_offsets[kv];
+        const int grp = Hq / Hkv, kv = tid / grp;
+        int t0 = 0;  // tiles of the query heads before this one: whole groups, then this group's
+        for (int k = 0; k < kv; ++k) t0 += grp * ((s_rank[k] + 15) >> 4);
+        const int R = s_rank[kv], o = s_off[kv];
         const int nt = (R + 15) >> 4;
+        t0 += (tid - kv * grp) * nt;
         int cnt = 0;
         for (int j = 0; j < nt && t0 + j < TT; ++j, ++cnt)
             tiles[t0 + j] = make_int4(tid, o + 16 * j, min(16, R - 16 * j) | ((j == nt - 1) << 16), kv);
@@ -99,83 +144,83 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
         s_hn[tid] = cnt;
     }
     __syncthreads();
+    if (tid == 0) hdr[0] = (s_total + grid - 1) / grid;
 
-    // Wave plan. Every wave takes ceil(Hq / 8) heads (one head per 16-lane row of the
-    // softmax). Heads by decreasing tile count (ties: lower head first) go to the wave
-    // with the fewest tiles (then the lowest index) that still has room; then swaps
-    // between the most loaded wave and another lower the maximum while they can. Wave
-    // 0 does it; lane w < 8 keeps wave w's load.
-    __shared__ int s_order[MAX_H], s_wave_of[MAX_H], s_load[NWAVE], s_best;
+    // Wave plan. Heads sorted by decreasing tile count (ties: lower head first) are dealt
+    // to the 8 waves in snake order (0..7, 7..0, 0..7, ...), so every wave takes
+    // ceil(Hq / 8) or fewer heads (one head per 16-lane row of the softmax) and the big
+    // heads pair with small ones; then swaps between the most loaded wave and another
+    // lower the maximum while they can. Wave 0 does it in registers.
+    __shared__ int s_pos[MAX_H];
     if (tid < Hq) {
         int rank = 0;
-        for (int h = 0; h < Hq; ++h) rank += s_hn[h] > s_hn[tid] || (s_hn[h] == s_hn[tid] && h < tid);
-        s_order[rank] = tid;
+        const int mine = s_hn[tid];
+#pragma unroll 8
+        for (int h = 0; h < Hq; ++h) rank += s_hn[h] > mine || (s_hn[h] == mine && h < tid);
+        s_pos[tid] = rank;
     }
     __syncthreads();
     if (wave == 0) {
-        const int hw = (Hq + NWAVE - 1) / NWAVE;
-        int load = 0, cnt = 0, ok = 1;
-        for (int i = 0; i < Hq; ++i) {
-            const int h = s_order[i], nt = s_hn[h];
-            const bool room = lane < NWAVE && cnt < hw && load + nt <= MAX_SLOTS;
-            int key = room ? (load << 8) | lane : 0x7fffffff;
-#pragma unroll
-            for (int o = 1; o < 8; o <<= 1) key = min(key, __shfl_xor(key, o, 64));
-            if (key == 0x7fffffff) { ok = 0; break; }
-            const int w = key & 255;
-            if (lane == w) { load += nt; ++cnt; }
-            if (lane == 0) s_wave_of[h] = w;
-        }
-        if (lane < NWAVE) s_load[lane] = load;
+        // Lane h < Hq: head h's tile count, first tile, order position and wave; lane
+        // w < 8: wave w's tile load.
+        const int hsz = lane < Hq ? s_hn[lane] : 0;
+        const int hfirst = lane < Hq ? s_hf[lane] : 0;
+        const int pos = lane < Hq ? s_pos[lane] : 0;
+        const int round = pos / NWAVE, col = pos % NWAVE;
+        int hwave = lane < Hq ? ((round & 1) ? NWAVE - 1 - col : col) : -1;
+        int load = 0;
+        for (int h = 0; h < Hq; ++h)  // wave loads
+            load += __builtin_amdgcn_readlane(hwave, h) == lane ? __builtin_amdgcn_readlane(hsz, h) : 0;
         const int target = (TT + NWAVE - 1) / NWAVE;
-        for (int it = 0; it < 32 && ok; ++it) {
-            int kmax = lane < NWAVE ? (s_load[lane] << 8) | lane : -1;  // most loaded wave A
-#pragma unroll
-            for (int o = 1; o < 8; o <<= 1) kmax = max(kmax, __shfl_xor(kmax, o, 64));
+        for (int it = 0; it < 64; ++it) {
+            const int kmax = lanes8_max(lane < NWAVE ? (load << 8) | lane : -1);  // most loaded wave A
             const int A = kmax & 255, la = kmax >> 8;
             if (la <= target) break;
-            // Candidate swaps: head ha of A (its ia-th, ia < 4) with head hb of another wave.
-            const uint64_t inA = __builtin_amdgcn_ballot_w64(lane < Hq && s_wave_of[lane] == A);
+            // Candidate swaps: a head ha of A with this lane's head hb of another wave B.
+            const int lb = __builtin_amdgcn_ds_bpermute(max(hwave, 0) * 4, load);  // load of hb's wave
+            uint64_t inA = __builtin_amdgcn_ballot_w64(lane < Hq && hwave == A);
             int best = 0x7fffffff;
-#pragma unroll
-            for (int round = 0; round < 2; ++round) {
-                const int ia = 2 * round + (lane >> 5), hb = lane & 31;
-                uint64_t m = inA;
-                for (int j = 0; j < ia && m; ++j) m &= m - 1;  // drop the first ia heads of A
-                if (m && hb < Hq && s_wave_of[hb] != A) {
-                    const int ha = __builtin_ctzll(m);
-                    const int d = s_hn[ha] - s_hn[hb], lb = s_load[s_wave_of[hb]];
-                    if (d > 0 && lb + d < la) best = min(best, (max(la - d, lb + d) << 16) | (ha << 8) | hb);
-                }
+            while (inA) {
+                const int ha = __builtin_ctzll(inA);
+                inA &= inA - 1;
+                const int d = __builtin_amdgcn_readlane(hsz, ha) - hsz;
+                if (lane < Hq && hwave != A && d > 0 && lb + d < la)
+                    best = min(best, (max(la - d, lb + d) << 16) | (ha << 8) | lane);
             }
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) best = min(best, __shfl_xor(best, o, 64));
+            best = wave_min_i(best);
             if (best == 0x7fffffff) break;
-            if (lane == 0) {
-                const int ha = (best >> 8) & 255, hb = best & 255, B = s_wave_of[hb];
-                const int d = s_hn[ha] - s_hn[hb];
-                s_wave_of[ha] = B;
-                s_wave_of[hb] = A;
-                s_load[A] -= d;
-                s_load[B] += d;
-            }
+            const int ha = (best >> 8) & 255, hb = best & 255;
+            const int B = __builtin_amdgcn_readlane(hwave, hb);
+            const int d = __builtin_amdgcn_readlane(hsz, ha) - __builtin_amdgcn_readlane(hsz, hb);
+            if (lane == ha) hwave = B;
+            if (lane == hb) hwave = A;
+            if (lane == A) load -= d;
+            if (lane == B) load += d;
         }
-        if (lane < NWAVE) {  // wave `lane`'s heads in plan order, then its slots
+        const int ok = lanes8_max(lane < NWAVE ? load : 0) <= MAX_SLOTS;
+        // Each head's place in its wave's plan: k = its wave's heads before it in the size
+        // order, sl = their tiles. Lane w < 8 also counts its wave's heads and tiles.
+        int k = 0, sl = 0, nhw = 0, ntw = 0;
+        for (int h = 0; h < Hq; ++h) {
+            const int wh = __builtin_amdgcn_readlane(hwave, h), ph = __builtin_amdgcn_readlane(pos, h);
+            const int zh = __builtin_amdgcn_readlane(hsz, h);
+            if (wh == hwave && ph < pos) { ++k; sl += zh; }
+            if (wh == lane) { ++nhw; ntw += zh; }
+        }
+        // Clear the 8 plans, then every head writes its own entries (same wave: in order).
+        for (int i = lane; i < NWAVE * PLAN_STRIDE; i += 64) plan[i] = 0;
+        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): the clears land first
+        if (lane < Hq && ok) {
+            int* pw = plan + hwave * PLAN_STRIDE;
+            pw[32 + k] = lane;
+            pw[40 + k] = sl;
+            pw[48 + k] = hsz;
+            for (int j = 0; j < hsz; ++j) pw[8 + sl + j] = hfirst + j;
+        }
+        if (lane < NWAVE) {
             int* pw = plan + lane * PLAN_STRIDE;
-            int sl = 0, k = 0;
-            for (int i = 0; i < Hq && ok; ++i) {
-                const int h = s_order[i];
-                if (s_wave_of[h] != lane) continue;
-                pw[32 + k] = h;
-                pw[40 + k] = sl;
-                pw[48 + k] = s_hn[h];
-                for (int j = 0; j < s_hn[h]; ++j) pw[8 + sl++] = s_hf[h] + j;
-                ++k;
-            }
-            for (int kk = k; kk < MAX_HW; ++kk) pw[32 + kk] = pw[40 + kk] = pw[48 + kk] = 0;
-            for (int j = sl; j < MAX_SLOTS + 8; ++j) pw[8 + j] = 0;
-            pw[0] = ok ? sl : 0;
-            pw[1] = ok ? k : 0;
+            pw[0] = ok ? ntw : 0;
+            pw[1] = ok ? nhw : 0;
         }
         if (lane == 0) plan[NWAVE * PLAN_STRIDE] = ok;
     }
@@ -616,51 +661,102 @@ __global__ __launch_bounds__(NTHR) void decode_kernel(const DecodeParams p0) {
 }
 
 // ---------------------------------------------------------------------------
-// 4. merge: per (request, head) combine the partials (log2-domain LSE), then lift.
+// 4. merge: per (request, head) the partials' log-sum-exp, then the lift through
+//    v_up_by_q. A workgroup takes one head and MERGE_REQ requests, so every row of
+//    v_up_by_q[h] it reads serves MERGE_REQ outputs; the lift loop is unrolled so its
+//    loads are in flight together.
 // ---------------------------------------------------------------------------
+constexpr int MERGE_REQ = 4;
+constexpr int MERGE_MAXK = 64;  // partial slots per request whose weights are kept in LDS
+
+template <typename WT>
+__device__ __forceinline__ float load_w(const WT* p, int64_t i);
+template <>
+__device__ __forceinline__ float load_w<uint16_t>(const uint16_t* p, int64_t i) { return bf16_bits_to_f32(p[i]); }
+template <>
+__device__ __forceinline__ float load_w<_Float16>(const _Float16* p, int64_t i) { return (float)p[i]; }
+template <>
+__device__ __forceinline__ float load_w<float>(const float* p, int64_t i) { return p[i]; }
+
+template <typename WT>
 __global__ __launch_bounds__(128) void merge_kernel(const uint8_t* __restrict__ ws, size_t ws_plan, size_t ws_m,
-                                                    size_t ws_l, size_t ws_acc, int Hq, int v_rank, const void* __restrict__ vup,
-                                                    int64_t vu_s0, int64_t vu_s1, int w_dt, void* __restrict__ out,
-                                                    int64_t o_s0, int64_t o_s1, int out_dt) {
-    extern __shared__ float s_o[];  // [v_rank]
-    const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+                                                    size_t ws_l, size_t ws_acc, int n, int Hq, int v_rank,
+                                                    const WT* __restrict__ vup, int64_t vu_s0, int64_t vu_s1,
+                                                    void* __restrict__ out, int64_t o_s0, int64_t o_s1, int out_dt) {
+    extern __shared__ float s_o[];                // [MERGE_REQ][v_rank]: merged low-rank outputs
+    __shared__ float s_w[MERGE_REQ][MERGE_MAXK];  // per request: weight of each of its partials
+    __shared__ float s_ml[MERGE_REQ][2];          // per request: reference max, 1 / sum
+    __shared__ int s_k[MERGE_REQ][2];             // per request: first partial slot, count (0: no tokens)
+    const int h = blockIdx.y, b0 = blockIdx.x * MERGE_REQ, tid = threadIdx.x;
+    const int lane = tid & 63, wv = tid >> 6;
     const int* hdr = (const int*)ws;
     const int S = hdr[0];
-    const int pb = hdr[1 + b], pe = hdr[2 + b];
     const bool planned = ((const int*)(ws + ws_plan))[NWAVE * PLAN_STRIDE] != 0;
-    // No tokens: softmax over an empty row (NaN, as the reference). No wave plan (a
-    // head assignment that does not fit): NaN as well, never a silent wrong result.
-    if (pe <= pb || S <= 0 || !planned) {
-        for (int d = tid; d < 128; d += blockDim.x)
-            store_f(out, (int64_t)b * o_s0 + (int64_t)h * o_s1 + d, out_dt, __builtin_nanf(""));
-        return;
-    }
-    const int k_lo = pb / S, k_hi = (pe - 1) / S;
     const float* wm = (const float*)(ws + ws_m);
     const float* wl = (const float*)(ws + ws_l);
     const float* wa = (const float*)(ws + ws_acc);
-    float M = -INFINITY;
-    for (int k = k_lo; k <= k_hi; ++k) M = fmaxf(M, wm[(int64_t)(k + b) * Hq + h]);
-    float l = 0.f;
-    for (int k = k_lo; k <= k_hi; ++k) {
-        const int64_t sl = (int64_t)(k + b) * Hq + h;
-        l += wl[sl] * exp2f(wm[sl] - M);
-    }
-    const float inv_l = 1.f / l;
-    for (int c = tid; c < v_rank; c += blockDim.x) {
-        float a = 0.f;
-        for (int k = k_lo; k <= k_hi; ++k) {
-            const int64_t sl = (int64_t)(k + b) * Hq + h;
-            a += wa[sl * v_rank + c] * exp2f(wm[sl] - M);
+
+    // 1. Per request (wave wv takes requests wv, wv + 2): the partials' log-sum-exp, with
+    //    the lanes over the partial slots.
+    for (int r = wv; r < MERGE_REQ; r += 2) {
+        const int b = b0 + r;
+        const int pb = b < n ? hdr[1 + b] : 0, pe = b < n ? hdr[2 + b] : 0;
+        // No tokens: softmax over an empty row (NaN, as the reference). No wave plan (a
+        // head assignment that does not fit): NaN as well, never a silent wrong result.
+        const bool live = b < n && pe > pb && S > 0 && planned;
+        const int k_lo = live ? pb / S : 0, nk = live ? (pe - 1) / S - k_lo + 1 : 0;
+        float M = -INFINITY;
+        for (int k = lane; k < nk; k += 64) M = fmaxf(M, wm[(int64_t)(k_lo + k + b) * Hq + h]);
+        M = wave_max(M);
+        float l = 0.f;
+        for (int k = lane; k < nk; k += 64) {
+            const int64_t sl = (int64_t)(k_lo + k + b) * Hq + h;
+            l += wl[sl] * exp2f(wm[sl] - M);
         }
-        s_o[c] = a * inv_l;
+        l = wave_sum(l);
+        for (int k = lane; k < nk && k < MERGE_MAXK; k += 64)
+            s_w[r][k] = exp2f(wm[(int64_t)(k_lo + k + b) * Hq + h] - M);
+        if (lane == 0) {
+            s_ml[r][0] = M;
+            s_ml[r][1] = 1.f / l;
+            s_k[r][0] = k_lo;
+            s_k[r][1] = nk;
+        }
     }
     __syncthreads();
+
+    // 2. The merged low-rank outputs: threads over (request, column).
+    for (int i = tid; i < MERGE_REQ * v_rank; i += blockDim.x) {
+        const int r = i / v_rank, c = i - r * v_rank, b = b0 + r;
+        const int k_lo = s_k[r][0], nk = s_k[r][1];
+        float a = 0.f;
+#pragma unroll 4
+        for (int k = 0; k < nk; ++k) {
+            const int64_t sl = (int64_t)(k_lo + k + b) * Hq + h;
+            const float w = k < MERGE_MAXK ? s_w[r][k] : exp2f(wm[sl] - s_ml[r][0]);
+            a = fmaf(wa[sl * v_rank + c], w, a);
+        }
+        s_o[i] = a * s_ml[r][1];
+    }
+    __syncthreads();
+
+    // 3. The lift through v_up_by_q[h]: each row serves MERGE_REQ requests.
     for (int d = tid; d < 128; d += blockDim.x) {
-        float o = 0.f;
-        const int64_t vb = (int64_t)h * vu_s0 + d;
-        for (int c = 0; c < v_rank; ++c) o += s_o[c] * load_f(vup, vb + (int64_t)c * vu_s1, w_dt);
-        store_f(out, (int64_t)b * o_s0 + (int64_t)h * o_s1 + d, out_dt, o);
+        float o[MERGE_REQ];
+#pragma unroll
+        for (int r = 0; r < MERGE_REQ; ++r) o[r] = 0.f;
+        const WT* vp = vup + (int64_t)h * vu_s0 + d;
+#pragma unroll 8
+        for (int c = 0; c < v_rank; ++c) {
+            const float v = load_w<WT>(vp, (int64_t)c * vu_s1);
+#pragma unroll
+            for (int r = 0; r < MERGE_REQ; ++r) o[r] = fmaf(s_o[r * v_rank + c], v, o[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < MERGE_REQ; ++r)
+            if (b0 + r < n)
+                store_f(out, (int64_t)(b0 + r) * o_s0 + (int64_t)h * o_s1 + d, out_dt,
+                        s_k[r][1] > 0 ? o[r] : __builtin_nanf(""));
     }
 }
 
@@ -834,9 +930,20 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
         SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used + 1], stream));
         ++g_prof.used;
     }
-    hipLaunchKernelGGL(merge_kernel, dim3(a.n, a.Hq), dim3(128), a.v_rank * 4, stream, (const uint8_t*)p.ws, wl.plan,
-                       wl.m, wl.l, wl.acc, a.Hq, a.v_rank, a.vup, a.vu_s0, a.vu_s1, a.w_dt, a.out, a.o_s0, a.o_s1,
-                       a.out_dt);
+    const dim3 mgrid((a.n + MERGE_REQ - 1) / MERGE_REQ, a.Hq);
+    const size_t mlds = (size_t)MERGE_REQ * a.v_rank * 4;
+    if (a.w_dt == STARKV_BF16)
+        hipLaunchKernelGGL(merge_kernel<uint16_t>, mgrid, dim3(128), mlds, stream, (const uint8_t*)p.ws, wl.plan, wl.m,
+                           wl.l, wl.acc, a.n, a.Hq, a.v_rank, (const uint16_t*)a.vup, a.vu_s0, a.vu_s1, a.out, a.o_s0,
+                           a.o_s1, a.out_dt);
+    else if (a.w_dt == STARKV_F16)
+        hipLaunchKernelGGL(merge_kernel<_Float16>, mgrid, dim3(128), mlds, stream, (const uint8_t*)p.ws, wl.plan, wl.m,
+                           wl.l, wl.acc, a.n, a.Hq, a.v_rank, (const _Float16*)a.vup, a.vu_s0, a.vu_s1, a.out, a.o_s0,
+                           a.o_s1, a.out_dt);
+    else
+        hipLaunchKernelGGL(merge_kernel<float>, mgrid, dim3(128), mlds, stream, (const uint8_t*)p.ws, wl.plan, wl.m,
+                           wl.l, wl.acc, a.n, a.Hq, a.v_rank, (const float*)a.vup, a.vu_s0, a.vu_s1, a.out, a.o_s0,
+                           a.o_s1, a.out_dt);
     SKV_HIP(hipGetLastError());
     return STARKV_OK;
 }
