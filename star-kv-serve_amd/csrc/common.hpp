@@ -112,6 +112,14 @@ __device__ __forceinline__ int opaque_s(int v) {
     return v;
 }
 
+// A per-lane value pinned whole in one VGPR: a lane address computed once stays one
+// register, instead of being split into a wave-uniform SGPR part and a VGPR part that
+// every use adds back together.
+__device__ __forceinline__ uint32_t vgpr_pin(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // ---------------------------------------------------------------------------
 // Wave64 reductions
 // ---------------------------------------------------------------------------

@@ -29,7 +29,9 @@
 //    the wave's heads runs one head per 16-lane row (lazy running max: the reference
 //    point moves only when a logit exceeds it by 2^8), and P[heads, 16] @ V[16, v_rank]
 //    runs on v_mfma_f32_4x4x4 (P broadcast from lanes 0-3, one V column per lane) into
-//    per-wave accumulators.
+//    per-wave accumulators. decode_lowrank.hip holds the bf16/fp16 kernel and
+//    decode_quant.hip the 3.2-bit one, which folds the V scales into P and runs P @ V
+//    one page behind over a V table expanded once per page.
 // 4. merge: per (request, head) log-sum-exp of the partials, then the lift through
 //    v_up_by_q.
 #include <vector>
@@ -230,9 +232,10 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
 // 2. fold: AB[b][t][ks][lane] = 8 fp16 of tile row m = lane & 15, columns
 //    32 ks + 8 (lane >> 4) .. +8, scaled by scale*log2(e); rows past the head's rank
 //    are zero (paged_decode.py:79-81 masks them). Row m holds rank m of the tile, or,
-//    for the 3.2-bit cache (perm = 1), rank (m >> 2) + 4 (m & 3): then the z values a
-//    lane receives (rows 4g .. 4g+3) are ranks g, g+4, g+8, g+12, whose codes are the
-//    nibbles a lane extracts from the tile's 8 bytes with one shift.
+//    for the 3.2-bit cache (perm = 1), rank 2 (m >> 2) + ((m >> 1) & 1) + 8 (m & 1),
+//    scaled by 1/16 when m & 2: then the z values a lane receives (rows 4g .. 4g+3)
+//    are ranks 2g, 2g+8, 2g+1, 2g+9, the low and high nibbles of bytes g and g+4 of
+//    the tile's 8 code bytes (the high nibbles are read as 16 n).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void fold_tiles_kernel(const void* __restrict__ q, int64_t q_s0, int64_t q_s1,
                                                          int q_dt, const void* __restrict__ k_up, int64_t ku_s0,
@@ -244,11 +247,11 @@ __global__ __launch_bounds__(256) void fold_tiles_kernel(const void* __restrict_
     if (t >= TT) return;
     const int4 tm = ((const int4*)ws_tiles_p)[t];
     const int m = lane & 15, lg = lane >> 4;
-    const int rr = perm ? (m >> 2) + 4 * (m & 3) : m;
+    const int rr = perm ? 2 * (m >> 2) + ((m >> 1) & 1) + 8 * (m & 1) : m;
     const int c0 = 32 * k2 + 8 * lg;
     const int64_t ur = (int64_t)(tm.y + rr) * ku_s0;
     const int64_t qh = (int64_t)b * q_s0 + (int64_t)tm.x * q_s1;
-    const float s = rr < (tm.z & 255) ? sc : 0.f;
+    const float s = rr < (tm.z & 255) ? (perm && (m & 2) ? sc * 0.0625f : sc) : 0.f;
     float u0[8], u1[8], q0[8], q1[8];
     load8_f(k_up, ur + c0, ku_dt, u0);
     load8_f(k_up, ur + c0 + 64, ku_dt, u1);
@@ -263,401 +266,6 @@ __global__ __launch_bounds__(256) void fold_tiles_kernel(const void* __restrict_
     half8_t* o = (half8_t*)(ab + ((size_t)b * TT + t) * AB_TILE_BYTES);
     o[k2 * 64 + lane] = a;
     o[(k2 + 2) * 64 + lane] = bb;
-}
-
-// ---------------------------------------------------------------------------
-// 3.2-bit page copies. LDS layout of a page buffer: the page's 16 cos/sin
-// rows first (256 bytes each, granule c of row r stored at granule c ^ r, so the MFMA
-// operand reads of 16 rows hit distinct banks: 4 copies of 1 KB), then the 16 token
-// rows at a pitch of pitch_g granules (odd, so rows fall on different banks; granules
-// past row_g are filler). Copy i of wave w is 1 KB chunk ch = 8 i + w; lane q of it
-// moves granule 64 ch + q, whose offset inside the page's cos/sin rows or rows is the
-// same for every page: `doff`. The two buffer descriptors of a page cover only the
-// request's rows, so rows past its end are not read. Every wave issues exactly NLD
-// copies; lanes with nothing to move (filler granules, chunks past the page, which land
-// in the buffer's unused tail) carry an offset past the descriptor's range, so they
-// touch no memory, and one vmcnt value covers a page on every wave.
-// ---------------------------------------------------------------------------
-template <int NLD>
-__device__ __forceinline__ void dma_page(const DecodeParams& p, const Cursor& c, cint_p P, uint8_t* buf, int wave,
-                                         const uint32_t (&doff)[MAX_NLD]) {
-    // Past the end of the workgroup's range the copies still issue (with empty
-    // descriptors: no memory access), so every page of the loop issues the same NLD
-    // copies and the waits stay static.
-    const bool v = c.valid;
-    const int k = v ? c.k : 0;
-    const int blk = v ? ((cint_p)p.bt)[c.b * p.bt_s0 + (k >> p.bs_shift) * p.bt_s1] : 0;
-    const int row0 = (k & ((1 << p.bs_shift) - 1)) * TILE_TOK;  // first slot of the page inside its block
-    const uint8_t* page = p.cache + (int64_t)blk * p.c_s0 + (int64_t)row0 * p.c_s1;
-    const int tok0 = TILE_TOK * k;
-    const int rows = v ? min(TILE_TOK, c.len - tok0) : 0;
-    const int4v_t rkv = buffer_rsrc(page, rows * (int)p.c_s1);
-    const int4v_t rcs = buffer_rsrc(p.cs + (int64_t)tok0 * p.cs_s0b, rows * p.cs_s0b);
-    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)buf;
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-        const int ch = i * NWAVE + wave;
-        const uint32_t dst = lds0 + (uint32_t)ch * 1024u;
-        if (i == 0 && ch < CS_CHUNKS)
-            lds_copy16(rcs, dst, doff[i]);
-        else  // rows; filler granules and surplus copies carry an out-of-range offset
-            lds_copy16(rkv, dst, doff[i]);
-    }
-}
-
-// A lane's share of one rank tile's logit for token (lane & 15): its 4 z values (rows
-// 4g .. 4g+3, g = lane >> 4) times their codes, read at byte `xoff` of the token's row.
-// 3.2-bit: the codes are nibbles n with value n - 8, built as fp16 (1024 + n) - 1032
-// (exact); the scales come per (token, head) from the row's bf16 (outlier, inlier) pair
-// at byte `soff`, the outlier part from the lane's first k elements (k = outlier ranks
-// among its 4, from the tile's count c).
-template <int FMT>
-__device__ __forceinline__ float tile_dot(const f32x4_t& z, const uint8_t* xr, int xoff, int soff, int c, int k,
-                                          int lg, const uint2* s_kmask) {
-    // One 64-bit LDS load (not two 32-bit ones the backend would pair up: the paired
-    // instruction loses the memory operand that tells it apart from copies in flight).
-    if (FMT == FMT_BF16) {
-        const uint2 w = ld64(xr + xoff + 8 * lg);
-        float v = __uint_as_float(w.x << 16) * z[0];
-        v = fmaf(__uint_as_float(w.x & 0xffff0000u), z[1], v);
-        v = fmaf(__uint_as_float(w.y << 16), z[2], v);
-        return fmaf(__uint_as_float(w.y & 0xffff0000u), z[3], v);
-    } else if (FMT == FMT_F16) {
-        const uint2 w = ld64(xr + xoff + 8 * lg);
-        return dot2(as_h2(w.x), cvt_h2(z[0], z[1]), dot2(as_h2(w.y), cvt_h2(z[2], z[3]), 0.f));
-    } else {
-        const uint2 w = ld64(xr + xoff);
-        const uint32_t sh = 4 * lg;
-        const half2_t off = {(_Float16)1032.f, (_Float16)1032.f};
-        const half2_t x0 = as_h2(((w.x >> sh) & 0x000F000Fu) | 0x64006400u) - off;  // ranks g, g+4
-        const half2_t x1 = as_h2(((w.y >> sh) & 0x000F000Fu) | 0x64006400u) - off;  // ranks g+8, g+12
-        const half2_t z01 = cvt_h2(z[0], z[1]), z23 = cvt_h2(z[2], z[3]);
-        const float d = dot2(x0, z01, dot2(x1, z23, 0.f));
-        const uint32_t sw = *(const uint32_t*)(xr + soff);
-        const float si = __uint_as_float(sw & 0xffff0000u);
-        if (c == 0) return si * d;
-        const uint2 mk = s_kmask[k];
-        const float dout =
-            dot2(as_h2(h2_bits(x0) & mk.x), z01, dot2(as_h2(h2_bits(x1) & mk.y), z23, 0.f));
-        return fmaf(__uint_as_float(sw << 16), dout, si * (d - dout));
-    }
-}
-
-template <int MTV>
-struct WaveTiles {
-    int ntw, nh;                   // rank tiles (slots) and query heads of this wave
-    int xoff[MTV], meta[MTV];      // per slot: code byte offset in a row; 3.2-bit: scale offset << 8 | outliers
-};
-
-// K side of one page: MTV slots of this wave, partial logits into sp[slot][token]
-// (this wave's own LDS region). Every slot is computed (slots past the wave's tiles
-// use tile 0 and land in a spare row), so the compiler can hoist the LDS reads and
-// interleave the MFMA chains of neighbouring slots.
-template <int FMT, int MTV>
-__device__ __forceinline__ void k_side(const DecodeParams& p, const WaveTiles<MTV>& wt, const half8_t (&ab)[MTV][4],
-                                       const uint8_t* XC, float* sp, const uint2* s_kmask, uint32_t kpack, int lane,
-                                       int wave, int cur_b) {
-    const int ln = opaque(lane);  // LDS addresses are recomputed per page, not held per buffer and slot
-    const int lr = ln & 15, lg = ln >> 4;
-    half8_t csb[4];  // B operand: position lr of the page, K elements 32 ks + 8 lg .. +8 (granule 4 ks + lg)
-    {
-        const uint8_t* csr = XC + lr * CS_ROW_LDS;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) csb[ks] = *(const half8_t*)(csr + (((4 * ks + lg) ^ lr) << 4));
-    }
-    const uint8_t* xr = XC + CS_CHUNKS * 1024 + lr * p.pitch_b;
-    const int rslot = ((lg & 1) << 1) | (lg >> 1);  // sum_rows4 puts inputs (a, b, c, d) in rows (0, 2, 1, 3)
-    const int ntw = opaque_s(wt.ntw);
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < MTV; ++i) {
-        const f32x4_t z = mfma_tile(ab[i], csb);
-        const int meta = FMT == FMT_Q4 ? wt.meta[i] : 0;
-        v[i & 3] = tile_dot<FMT>(z, xr, wt.xoff[i], meta >> 8, meta & 255, (kpack >> (3 * i)) & 7, lg, s_kmask);
-        if ((i & 3) == 3 || i == MTV - 1) {  // four tiles (or the last ones): one reduction over the row groups
-            const float r = sum_rows4(v[0], (i & 3) >= 1 ? v[1] : 0.f, (i & 3) >= 2 ? v[2] : 0.f,
-                                      (i & 3) >= 3 ? v[3] : 0.f);
-            const int slot = 4 * (i >> 2) + rslot;
-            sp[(slot < ntw ? slot : MAX_SLOTS) * TILE_TOK + lr] = r;
-        }
-    }
-    // Slots past MTV: AB from the workspace (L2) on every page.
-    if (ntw > MTV) {
-        cint_p plan = (cint_p)(p.ws + p.ws_plan) + wave * PLAN_STRIDE;
-        cint_p tiles = (cint_p)(p.ws + p.ws_tiles);
-        const half8_t* abg = (const half8_t*)(p.ws + p.ws_ab + (size_t)cur_b * p.TT * AB_TILE_BYTES);
-        for (int i = MTV; i < ntw; ++i) {
-            const int t = plan[8 + i];
-            half8_t a[4];
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) a[ks] = abg[(t * 4 + ks) * 64 + lane];
-            const int4 tm = load_tile(tiles, t);
-            const int c = (tm.z >> 8) & 255;
-            const int k = min(max((c - lg + 3) >> 2, 0), 4);
-            const int xoff = FMT == FMT_Q4 ? (tm.y >> 1) : 2 * tm.y;
-            const float r = sum_rows(tile_dot<FMT>(mfma_tile(a, csb), xr, xoff, p.ks_off + 4 * tm.x, c, k, lg, s_kmask));
-            if (lane < 16) sp[i * TILE_TOK + lr] = r;
-        }
-        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): no tracked load left pending
-    }
-}
-
-// Returns true when some head's reference max moved (acc needs rescaling by alpha).
-template <int FMT>
-__device__ __forceinline__ bool softmax_page(SmState& sm, int nh, const float* sp, uint16_t* spp, uint16_t* spl,
-                                             float* salpha, int lane, int tok0, int lo, int hi) {
-    const int ln = opaque(lane);
-    const int kh = ln >> 4, lr = ln & 15;
-    float s = 0.f;
-    for (int t = 0; t < sm.hn; ++t) s += sp[(sm.hf + t) * TILE_TOK + lr];
-    s = tok0 + lr >= lo && tok0 + lr < hi && kh < nh ? s : -INFINITY;
-    float alpha = 1.f;
-    bool moved = false;
-    if (__builtin_amdgcn_ballot_w64(s > sm.m + LAZY_MAX) != 0) {
-        const float mn = fmaxf(sm.m, row16_max(s));
-        alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(sm.m - mn);
-        sm.m = mn;
-        moved = true;
-    }
-    const float pe = s == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - sm.m);
-    sm.l = fmaf(sm.l, alpha, pe);
-    const int idx = kh * TILE_TOK + lr;  // rows past the wave's heads hold P = 0
-    if (FMT == FMT_BF16) {
-        // P = hi + lo in two bfloat16 parts: the P @ V product keeps ~16 bits of P.
-        const __bf16 ph = (__bf16)pe;
-        const __bf16 pl = (__bf16)(pe - (float)ph);
-        spp[idx] = __builtin_bit_cast(uint16_t, ph);
-        spl[idx] = __builtin_bit_cast(uint16_t, pl);
-    } else {
-        spp[idx] = __builtin_bit_cast(uint16_t, (_Float16)pe);
-    }
-    if (lr == 0) salpha[kh] = alpha;
-    return moved;
-}
-
-// acc[nb] = alpha * acc[nb] + P[4 heads, 16 tokens] @ V[16 tokens, 64 columns] for page
-// X, on v_mfma_f32_4x4x4_16b with block 0's A broadcast (cbsz 4): per 4-token step,
-// lanes 0..3 hold P[head l][4 tokens], lane l holds V[4 tokens][column 64 nb + l], and
-// the result lands in lane l as acc[nb][head] for its column.
-template <int FMT, int NB>
-__device__ __forceinline__ void pv_page(const DecodeParams& p, f32x4_t (&acc)[NB], const uint8_t* X,
-                                        const uint16_t* spp, const uint16_t* spl, const float* salpha, bool rescale,
-                                        int lane) {
-    const int ln = opaque(lane);
-    if (rescale) {
-        const f32x4_t al = *(const f32x4_t*)salpha;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[nb][e] *= al[e];
-    }
-    const uint8_t* rows = X + CS_CHUNKS * 1024;
-    const uint16_t* pr = spp + (ln & 3) * TILE_TOK;
-    const uint16_t* plr = spl + (ln & 3) * TILE_TOK;
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {  // tokens 4 st .. 4 st + 3
-        const uint2 pa = *(const uint2*)(pr + 4 * st);
-        const uint2 pl = FMT == FMT_BF16 ? *(const uint2*)(plr + 4 * st) : make_uint2(0, 0);
-        const uint8_t* r0 = rows + 4 * st * p.pitch_b;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const int c = 64 * nb + ln;  // columns past v_rank compute garbage that is never stored
-            uint32_t b0, b1;
-            if (FMT == FMT_Q4) {
-                const bool o = c < p.v_nout;
-                const int ci = o ? c : c - p.v_nout;
-                const int vb = p.vq_off + (o ? 0 : p.v_nbo) + (ci >> 1);
-                const int vsh = 4 * (ci & 1);
-                const int vso = p.vs_off + (o ? 0 : 2);
-                float val[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint8_t* rp = r0 + e * p.pitch_b;
-                    const int nib = (int)((rp[vb] >> vsh) & 15u) - 8;
-                    val[e] = (float)nib * __uint_as_float((uint32_t)(*(const uint16_t*)(rp + vso)) << 16);
-                }
-                b0 = h2_bits(cvt_h2(val[0], val[1]));
-                b1 = h2_bits(cvt_h2(val[2], val[3]));
-            } else {
-                const uint8_t* vp = r0 + 2 * (p.k_width + c);
-                const uint32_t u0 = *(const uint16_t*)vp, u1 = *(const uint16_t*)(vp + p.pitch_b);
-                const uint32_t u2 = *(const uint16_t*)(vp + 2 * p.pitch_b), u3 = *(const uint16_t*)(vp + 3 * p.pitch_b);
-                b0 = u0 | (u1 << 16);
-                b1 = u2 | (u3 << 16);
-            }
-            const uint2 bv = make_uint2(b0, b1);
-            if (FMT == FMT_BF16) {
-                acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(short4_t, pa),
-                                                                 __builtin_bit_cast(short4_t, bv), acc[nb], 4, 0, 0);
-                acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(short4_t, pl),
-                                                                 __builtin_bit_cast(short4_t, bv), acc[nb], 4, 0, 0);
-            } else {
-                acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, pa),
-                                                             __builtin_bit_cast(half4_t, bv), acc[nb], 4, 0, 0);
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// One page of the decode loop: XC holds page j (copied two pages ago) and XN receives
-// page j + 2 (its previous page, j - 1, is finished on every wave once the barrier is
-// passed). Distinct __shared__ arrays per buffer keep every address static.
-// ---------------------------------------------------------------------------
-template <int FMT, int MTV, int NB, int NLD>
-__device__ __forceinline__ bool decode_iter(LoopState& st, const WaveTiles<MTV>& wt, half8_t (&ab)[MTV][4],
-                                            f32x4_t (&acc)[NB], SmState& sm, const uint32_t (&doff)[MAX_NLD],
-                                            uint32_t kpack, const uint8_t* XC, uint8_t* XN, float* sp,
-                                            uint16_t* spp, uint16_t* spl, float* salpha, const uint2* s_kmask,
-                                            const int* sqh, int lane, int wave) {
-    const DecodeParams& p = params();
-    cint_p P = (cint_p)(p.ws + 4);
-    if (!st.cc.valid) return false;
-    const Cursor cc = st.cc;
-    if (st.new_seg) {
-        // This request's AB into registers; slots past the wave's tiles load tile 0.
-        cint_p plan = (cint_p)(p.ws + p.ws_plan) + wave * PLAN_STRIDE;
-        const half8_t* abp = (const half8_t*)(p.ws + p.ws_ab + (size_t)cc.b * p.TT * AB_TILE_BYTES);
-#pragma unroll
-        for (int i = 0; i < MTV; ++i) {
-            const int t = plan[8 + i];
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) ab[i][ks] = abp[(t * 4 + ks) * 64 + lane];
-        }
-        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0)
-    }
-    SKV_WAIT_VM_LGKM0(NLD);  // only the copies of page j + 1 may still be in flight
-    lds_barrier();           // page j is in LDS; every wave is done with page j - 1
-    dma_page<NLD>(p, st.ld, P, XN, opaque_s(wave), doff);
-    if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
-    k_side<FMT, MTV>(p, wt, ab, XC, sp, s_kmask, kpack, lane, wave, cc.b);
-    const bool moved = softmax_page<FMT>(sm, wt.nh, sp, spp, spl, salpha, lane, TILE_TOK * cc.k, cc.lo, cc.hi);
-    pv_page<FMT, NB>(p, acc, XC, spp, spl, salpha, moved, lane);
-    Cursor nx = cc;
-    const bool seg_end = cur_next(nx, P, p.n, st.beg, st.end);
-    if (seg_end) flush_partial<NB>(p, sm, acc, wt.nh, cc.b + st.g, sqh, lane);
-    st.cc = nx;
-    st.new_seg = seg_end;
-    ++st.j;
-    return true;
-}
-
-// ---------------------------------------------------------------------------
-// 3. decode. MTV = rank tiles per wave held in VGPRs (more stream from L2); NB =
-//    64-column blocks of V; XB = bytes per page buffer; NLD = copies per lane per page.
-// ---------------------------------------------------------------------------
-template <int FMT, int MTV, int NB, int XB, int NLD>
-__global__ __launch_bounds__(NTHR) void decode_kernel(const DecodeParams p0) {
-    __shared__ __attribute__((aligned(16))) uint8_t s_x0[XB];
-    __shared__ __attribute__((aligned(16))) uint8_t s_x1[XB];
-    __shared__ __attribute__((aligned(16))) uint8_t s_x2[XB];
-    __shared__ __attribute__((aligned(16))) float s_part[NWAVE][(MAX_SLOTS + 1) * TILE_TOK];
-    __shared__ __attribute__((aligned(16))) uint16_t s_p[NWAVE][4 * TILE_TOK];
-    __shared__ __attribute__((aligned(16))) uint16_t s_plo[FMT == FMT_BF16 ? NWAVE : 1][4 * TILE_TOK];
-    __shared__ __attribute__((aligned(16))) float s_alpha[NWAVE][4];
-    __shared__ __attribute__((aligned(16))) uint2 s_kmask[8];
-    __shared__ int s_qh[NWAVE][4];
-
-    const DecodeParams& p = params();
-    const int tid = threadIdx.x, lane = tid & 63, wave = rfl(tid >> 6);
-    const int lg = lane >> 4;
-    cint_p P = (cint_p)(p.ws + 4);
-    cint_p plan = (cint_p)(p.ws + p.ws_plan);
-    if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
-    LoopState st;
-    st.g = blockIdx.x;
-    const int S_tok = ((cint_p)p.ws)[0];
-    const int T = P[p.n];
-    st.beg = min(st.g * S_tok, T);
-    st.end = min(st.beg + S_tok, T);
-    if (st.beg >= st.end) return;
-
-    // Page buffers start zeroed: rows past a request's end are never copied, and
-    // must hold finite values (P is 0 there).
-    for (int i = tid; i < XB / 16; i += NTHR) {
-        ((uint4*)s_x0)[i] = make_uint4(0, 0, 0, 0);
-        ((uint4*)s_x1)[i] = make_uint4(0, 0, 0, 0);
-        ((uint4*)s_x2)[i] = make_uint4(0, 0, 0, 0);
-    }
-    if (tid < NWAVE * 4) (&s_alpha[0][0])[tid] = 1.f;
-    if (tid < 8) {  // fp16-pair masks of a lane's first k elements (pairs (0,1), (2,3))
-        const uint32_t m0 = tid >= 2 ? 0xffffffffu : tid == 1 ? 0x0000ffffu : 0u;
-        const uint32_t m1 = tid >= 4 ? 0xffffffffu : tid == 3 ? 0x0000ffffu : 0u;
-        s_kmask[tid] = make_uint2(m0, m1);
-    }
-
-    // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
-    cint_p pw = plan + wave * PLAN_STRIDE;
-    WaveTiles<MTV> wt;
-    wt.ntw = pw[0];
-    wt.nh = pw[1];
-    uint32_t kpack = 0;
-    {
-        cint_p tiles = (cint_p)(p.ws + p.ws_tiles);
-#pragma unroll
-        for (int i = 0; i < MTV; ++i) {
-            const int4 tm = load_tile(tiles, pw[8 + i]);
-            wt.xoff[i] = FMT == FMT_Q4 ? (tm.y >> 1) : 2 * tm.y;
-            const int c = (tm.z >> 8) & 255;
-            wt.meta[i] = ((p.ks_off + 4 * tm.x) << 8) | c;
-            if (FMT == FMT_Q4) kpack |= (uint32_t)min(max((c - lg + 3) >> 2, 0), 4) << (3 * i);
-        }
-    }
-    if (lane < 4) s_qh[wave][lane] = lane < wt.nh ? ((const int*)pw)[32 + lane] : 0;
-    SmState sm;
-    sm.hf = lg < wt.nh ? ((const int*)pw)[40 + lg] : 0;
-    sm.hn = lg < wt.nh ? ((const int*)pw)[48 + lg] : 0;
-    sm.m = -INFINITY;
-    sm.l = 0.f;
-    // Copy offsets of this lane inside a page (chunks 0..3: cos/sin rows; then rows).
-    uint32_t doff[MAX_NLD];
-#pragma unroll
-    for (int i = 0; i < MAX_NLD; ++i) {
-        const int ch = i * NWAVE + wave;
-        uint32_t off = 0x80000000u;  // past the descriptor range: no memory access
-        if (i < NLD) {
-            if (ch < CS_CHUNKS) {
-                const int g = ch * 64 + lane, row = g >> 4;  // LDS granule g holds granule (g & 15) ^ row
-                off = (uint32_t)(row * p.cs_s0b + (((g & 15) ^ row) << 4));
-            } else if (ch < CS_CHUNKS + p.nkv) {
-                const int g = (ch - CS_CHUNKS) * 64 + lane;
-                const int row = g / p.pitch_g, col = g - row * p.pitch_g;
-                if (row < TILE_TOK && col < p.row_g) off = (uint32_t)(row * (int)p.c_s1 + col * 16);
-            }
-        }
-        doff[i] = off;
-    }
-    __syncthreads();
-
-    float* sp = &s_part[wave][0];
-    uint16_t* spp = &s_p[wave][0];
-    uint16_t* spl = &s_plo[FMT == FMT_BF16 ? wave : 0][0];
-    float* salpha = &s_alpha[wave][0];
-    cur_first(st.cc, P, p.n, st.beg, st.end);
-    st.ld = st.cc;
-    st.j = 0;
-    st.new_seg = true;
-    dma_page<NLD>(p, st.ld, P, s_x0, wave, doff);
-    cur_next(st.ld, P, p.n, st.beg, st.end);
-    dma_page<NLD>(p, st.ld, P, s_x1, wave, doff);
-    if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
-
-    half8_t ab[MTV][4];
-    f32x4_t acc[NB];
-#pragma unroll
-    for (int k = 0; k < NB; ++k) acc[k] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    while (true) {
-        if (!decode_iter<FMT, MTV, NB, NLD>(st, wt, ab, acc, sm, doff, kpack, s_x0, s_x2, sp, spp, spl, salpha,
-                                            s_kmask, &s_qh[wave][0], lane, wave))
-            break;
-        if (!decode_iter<FMT, MTV, NB, NLD>(st, wt, ab, acc, sm, doff, kpack, s_x1, s_x0, sp, spp, spl, salpha,
-                                            s_kmask, &s_qh[wave][0], lane, wave))
-            break;
-        if (!decode_iter<FMT, MTV, NB, NLD>(st, wt, ab, acc, sm, doff, kpack, s_x2, s_x1, sp, spp, spl, salpha,
-                                            s_kmask, &s_qh[wave][0], lane, wave))
-            break;
-    }
-    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): no copy may land after the workgroup ends
 }
 
 // ---------------------------------------------------------------------------
@@ -812,28 +420,6 @@ struct DecodeProfile {
 };
 static DecodeProfile g_prof;
 
-template <int FMT, int MTV, int XB, int NLD>
-static const void* pick_nb(int nb) {
-    if (nb <= 1) return (const void*)&decode_kernel<FMT, MTV, 1, XB, NLD>;
-    if (nb <= 2) return (const void*)&decode_kernel<FMT, MTV, 2, XB, NLD>;
-    return (const void*)&decode_kernel<FMT, MTV, 4, XB, NLD>;
-}
-
-// Rank tiles per wave held in VGPRs: the wave plan balances whole heads to within a
-// tile of TT / 8, so MTV = ceil(TT / 8) covers every wave for the usual rank mixes (a
-// wave with more streams the rest of its tiles from L2).
-template <int FMT, int XB, int NLD>
-static int launch_decode(const DecodeParams& p, int nb, int grid, hipStream_t stream) {
-    const int need = (p.TT + NWAVE - 1) / NWAVE;
-    const void* fn = need <= 4 ? pick_nb<FMT, 4, XB, NLD>(nb)
-                     : need <= 8 ? pick_nb<FMT, 8, XB, NLD>(nb)
-                     : need <= 9 ? pick_nb<FMT, 9, XB, NLD>(nb)
-                                 : pick_nb<FMT, 10, XB, NLD>(nb);
-    void* args[] = {(void*)&p};
-    SKV_HIP(hipLaunchKernel(fn, dim3(grid), dim3(NTHR), args, 0, stream));
-    return STARKV_OK;
-}
-
 // log2(block_size / 16), or -1 if block_size is not 16 times a power of two.
 static int block_shift(int block_size) {
     for (int s = 0; s < 16; ++s)
@@ -894,17 +480,17 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     p.n = a.n; p.Hq = a.Hq; p.TT = TT; p.v_rank = a.v_rank;
     p.cs = (const uint8_t*)a.cs; p.cs_s0b = (int)(a.cs_s0 * 2);
     p.row_g = row_bytes / 16;
-    p.pitch_g = p.row_g | 1;
-    p.pitch_b = p.pitch_g * 16;
-    p.nkv = (TILE_TOK * p.pitch_g + 63) / 64;
+    int qnb = 0;
     if (fmt == FMT_Q4) {
-        const int nch = CS_CHUNKS + p.nkv;
-        SKV_CHECK(nch <= NLD_Q4 * NWAVE && nch * 1024 <= XB_Q4,
-                  "decode: a page needs %d KB of LDS (> %d): row %d bytes is too wide", nch, NLD_Q4 * NWAVE,
-                  row_bytes);
+        qnb = quant_v_blocks(a.v_rank, p.v_nout);
+        SKV_CHECK(qnb > 0, "decode: v_rank %d needs more than 5 P @ V blocks", a.v_rank);
+        SKV_CHECK(quant_copies(row_bytes) > 0 && quant_lds_bytes(row_bytes, qnb) <= quant_lds_limit(),
+                  "decode: a 3.2-bit page of %d-byte rows (v_rank %d) does not fit in LDS", row_bytes, a.v_rank);
+        p.nch = quant_chunks(row_bytes);
+        p.lds_bytes = quant_lds_bytes(row_bytes, qnb);
     } else {
         SKV_CHECK(lowrank_copies(p.k_width, nb) > 0,
-                  "decode: a page of k_width %d and v_rank %d needs more than 48 KB of LDS per buffer", p.k_width,
+                  "decode: a page of k_width %d and v_rank %d needs more than 64 KB of LDS", p.k_width,
                   a.v_rank);
         p.nch = lowrank_chunks(p.k_width, nb);
         p.lds_bytes = lowrank_lds_bytes(p.k_width, nb);
@@ -922,8 +508,7 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     SKV_HIP(hipGetLastError());
     const bool timed = g_prof.on && 2 * g_prof.used + 1 < (int)g_prof.ev.size();
     if (timed) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
-    int rc = fmt == FMT_Q4 ? launch_decode<FMT_Q4, XB_Q4, NLD_Q4>(p, nb, a.grid, stream)
-                           : launch_lowrank(p, fmt, nb, a.grid, stream);
+    int rc = fmt == FMT_Q4 ? launch_quant(p, qnb, a.grid, stream) : launch_lowrank(p, fmt, nb, a.grid, stream);
     if (rc) return rc;
     SKV_HIP(hipGetLastError());
     if (timed) {

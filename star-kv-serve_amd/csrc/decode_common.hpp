@@ -1,4 +1,5 @@
-// Shared definitions of the paged decode kernels (decode.hip, decode_lowrank.hip):
+// Shared definitions of the paged decode launches (decode.hip, decode_lowrank.hip,
+// decode_quant.hip):
 // constants, the workspace layout, the kernel parameter block, the token cursor, the
 // global->LDS copy primitive and the per-partial flush.
 #pragma once
@@ -27,12 +28,8 @@ constexpr int MAX_H = 32;                   // query heads
 constexpr int MAX_HW = 8;                   // query heads per wave
 constexpr int MAX_SLOTS = 16;               // rank tiles per wave
 constexpr int PLAN_STRIDE = 64;             // ints per wave in the plan
-constexpr int MAX_NLD = 6;                  // 16-byte copies per lane per page (bf16/fp16 rows)
-constexpr int NLD_Q4 = 3;                   // 3.2-bit rows
 constexpr int CS_ROW_LDS = 256;             // LDS bytes per cos/sin row (granules XOR-swizzled by row)
 constexpr int CS_CHUNKS = 4;                // 16 rows x 16 granules -> 4 copies of 64 granules
-constexpr int XB_LOWRANK = 48 * 1024;       // LDS bytes per page buffer
-constexpr int XB_Q4 = 24 * 1024;
 constexpr float LAZY_MAX = 8.f;             // log2 headroom before the running max moves
 
 // Workspace layout, in bytes from the base (every region 256-byte aligned):
@@ -71,9 +68,8 @@ struct DecodeParams {
     const int32_t* bt; int bt_s0, bt_s1;
     int n, Hq, TT, k_width, v_rank;
     int ks_off, vs_off, vq_off, v_nout, v_nbo;     // QuantRow (3.2-bit)
-    int row_g, pitch_g, pitch_b;                   // row granules (16 B), LDS row pitch (granules, bytes)
-    int nkv;                                       // 1 KB copies of K/V rows per page (after 4 of cos/sin)
-    int nch, lds_bytes;                            // bf16/fp16 kernel: 1 KB chunks per page, dynamic LDS
+    int row_g;                                     // row granules (16 B)
+    int nch, lds_bytes;                            // 1 KB chunks copied per page, dynamic LDS bytes
     const uint8_t* cs; int cs_s0b;                 // fp16 cos/sin table, row stride in bytes
     uint8_t* ws;
     size_t ws_tiles, ws_plan, ws_ab, ws_m, ws_l, ws_acc;
@@ -229,20 +225,25 @@ __device__ __forceinline__ void flush_partial(const DecodeParams& p, SmState& sm
     }
 }
 
-struct LoopState {
-    Cursor cc, ld;
-    int j, beg, end, g;
-    bool new_seg;
-};
-
-
 // The bf16/fp16 decode kernel (decode_lowrank.hip): picks the instantiation for
 // (fmt, v column blocks nb, rank tiles per wave) and launches it on `stream`.
 int launch_lowrank(const DecodeParams& p, int fmt, int nb, int grid, hipStream_t stream);
 // The bf16/fp16 kernel's page geometry for (k_width, V column blocks nb): 1 KB chunks
-// per page, dynamic LDS bytes, copies per wave per page (0 if a page does not fit).
+// per page, page buffers (3 or 2), dynamic LDS bytes, copies per wave per page (0 if a
+// page does not fit).
 int lowrank_chunks(int k_width, int nb);
+int lowrank_buffers(int k_width, int nb);
 int lowrank_lds_bytes(int k_width, int nb);
 int lowrank_copies(int k_width, int nb);
+
+// The 3.2-bit decode kernel (decode_quant.hip) and its page geometry: P @ V blocks for
+// (v_rank, v_nout) (0 if too many), 1 KB chunks copied per page and copies per wave (0 if
+// a page does not fit) for a row of row_bytes, dynamic LDS bytes, the LDS limit.
+int launch_quant(const DecodeParams& p, int nb, int grid, hipStream_t stream);
+int quant_v_blocks(int v_rank, int v_nout);
+int quant_chunks(int row_bytes);
+int quant_copies(int row_bytes);
+int quant_lds_bytes(int row_bytes, int nb);
+int quant_lds_limit();
 
 }  // namespace starkv

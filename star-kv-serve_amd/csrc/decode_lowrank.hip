@@ -6,10 +6,11 @@
 // (q folded into U) in VGPRs. Per page: z = AB . [cos|sin]^T on MFMA, the lanes fold z
 // with the codes, the wave's heads run an online softmax, and P @ V accumulates on MFMA.
 //
-// LDS. The three page buffers are interleaved at 1 KB: chunk c of buffer b sits at
-// byte c * 3072 + b * 1024 of the dynamic block. Every read of the current page is a
-// per-lane address computed once per kernel plus the immediate b * 1024, so the page
-// loop does no address arithmetic. The chunks of a page:
+// LDS. The page buffers (three, or two when a page is too large to fit three times) are
+// interleaved at 1 KB: chunk c of buffer b sits at byte c * NBUF KB + b KB of the dynamic
+// block. Every read of the current page is a per-lane address computed once per kernel
+// plus the immediate b * 1024, so the page loop does no address arithmetic. The chunks
+// of a page:
 //   0 .. 3            cos/sin rows 4c .. 4c+3, 256 B per row; granule g of row r is
 //                     stored at granule g ^ r, so the 16 rows of an MFMA operand read
 //                     hit distinct banks
@@ -19,13 +20,12 @@
 // (chunk, q) and is computed once (`doff`). Copies past the page's chunks land in a
 // 1 KB dummy block after the buffers and read nothing.
 
-#include "decode_common.hpp"
+#include "decode_pages.hpp"
 
 namespace starkv {
 
 namespace {
 
-constexpr int LR_STRIDE = 3072;  // bytes between chunks c and c + 1 of one buffer
 // Dynamic LDS limit: 160 KB per CU minus the kernel's static arrays (partial logits,
 // P, alpha, head ids: under 12 KB).
 constexpr int LR_MAX_DYN_LDS = 160 * 1024 - 12 * 1024;
@@ -36,27 +36,6 @@ struct LrChunks {
     static constexpr int K0 = CS_CHUNKS + 2 * NB;  // first K chunk
     static constexpr int VPITCH = NB * 128;        // V row pitch in LDS
 };
-
-typedef short short2_t __attribute__((ext_vector_type(2)));
-
-template <typename T>
-__device__ __forceinline__ T lds_ld(uint32_t a) {
-    return *(const __attribute__((address_space(3))) T*)(a);
-}
-template <typename T>
-__device__ __forceinline__ void lds_st(uint32_t a, T v) {
-    *(__attribute__((address_space(3))) T*)(a) = v;
-}
-__device__ __forceinline__ uint2 lds_ld2(uint32_t a) {
-    const uint64_t v = lds_ld<uint64_t>(a);
-    return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
-}
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
-}
-
-// A 16-byte-per-lane copy to LDS address m0 (a wave-uniform SGPR value).
-__device__ __forceinline__ void copy16(const int4v_t& rsrc, uint32_t m0, uint32_t voff) { lds_copy16(rsrc, m0, voff); }
 
 // Per-lane LDS byte addresses (buffer 0), fixed for the whole kernel.
 template <int MTV>
@@ -70,110 +49,18 @@ struct LaneAddr {
     uint32_t base;                // the page buffers (wave-uniform)
 };
 
-// Loop-invariant operands of the page copies, read once from the parameter block and
-// held in SGPRs.
-struct DmaConst {
-    const uint8_t* cache; int64_t c_s0; int c_s1;
-    const int32_t* bt; int bt_s0, bt_s1, bs_shift;
-    const uint8_t* cs; int cs_s0b;
-    int nch;
-    uint32_t m0w, m0dummy;  // LDS address of this wave's first chunk (buffer 0); the dummy block
-};
-
-struct LrLoop {
-    Cursor cc, ld;
-    int beg, end, g;
-    int nblk;  // block of the page `ld` points at, loaded one page ahead of its copies
-    bool new_seg;
-};
-
-// Cache block of the page cursor c points at (0 past the range).
-__device__ __forceinline__ int page_block(const DmaConst& dc, const Cursor& c) {
-    return c.valid ? ((cint_p)dc.bt)[c.b * dc.bt_s0 + (c.k >> dc.bs_shift) * dc.bt_s1] : 0;
-}
-
-// Buffer descriptors of one page: its rows and its cos/sin rows, bounded to the rows
-// the request has (rows past its end are not read). Past the end of the workgroup's
-// range both are empty: the copies still issue, so every page issues NLD copies and
-// the waits stay static.
-struct DmaPage {
-    int4v_t rkv, rcs;
-};
-
-__device__ __forceinline__ DmaPage dma_setup(const DmaConst& dc, const Cursor& c, int blk) {
-    const bool v = c.valid;
-    const int k = v ? c.k : 0;
-    const int row0 = (k & ((1 << dc.bs_shift) - 1)) * TILE_TOK;  // first slot of the page in its block
-    const uint8_t* page = dc.cache + (int64_t)blk * dc.c_s0 + (int64_t)row0 * dc.c_s1;
-    const int tok0 = TILE_TOK * k;
-    const int rows = v ? min(TILE_TOK, c.len - tok0) : 0;
-    DmaPage d;
-    d.rkv = buffer_rsrc(page, rows * dc.c_s1);
-    d.rcs = buffer_rsrc(dc.cs + (int64_t)tok0 * dc.cs_s0b, rows * dc.cs_s0b);
-    return d;
-}
-
-// Copy i of this wave into buffer B: chunk 8 i + wave (cos/sin rows for chunks < 4).
-template <int B>
-__device__ __forceinline__ void dma_one(const DmaConst& dc, const DmaPage& d, int i, int wave, uint32_t off) {
-    const int ch = i * NWAVE + wave;
-    const uint32_t m0 = ch < dc.nch ? dc.m0w + (uint32_t)(i * NWAVE * LR_STRIDE + B * 1024) : dc.m0dummy;
-    if (i == 0 && wave < CS_CHUNKS)
-        copy16(d.rcs, m0, off);
-    else
-        copy16(d.rkv, m0, off);
-}
-
-template <int NLD, int B>
-__device__ __forceinline__ void dma_page(const DmaConst& dc, const Cursor& c, int blk, int wave,
-                                         const uint32_t (&doff)[NLD]) {
-    const DmaPage d = dma_setup(dc, c, blk);
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) dma_one<B>(dc, d, i, wave, doff[i]);
-}
-
-// Copy schedule. A page's copies must reach the copy queue at about the rate the queue
-// drains: a burst fills it, and a wave whose copy finds it full stalls until it has room.
-// The iteration offers copy points: 0 right after the barrier, 1 .. MTV after each K
-// tile, MTV + 1 after the softmax, MTV + 2 .. MTV + 5 after each P @ V step. Their
-// rough positions in the iteration (as fractions of its length) are below. Copy c of the
-// waves on the first wave slot of each SIMD (waves 0-3) goes to the point nearest c / NLD,
-// and of the others (waves 4-7) to the point nearest (c + 1/2) / NLD, so that the two
-// waves of a SIMD never issue at the same point.
+// Copy points of an iteration: 0 right after the barrier, 1 .. MTV after each K tile,
+// MTV + 1 after the softmax, MTV + 2 .. MTV + 5 after each P @ V step.
 template <int MTV>
-constexpr float copy_point_time(int pos) {
-    return pos == 0 ? 0.f
-           : pos <= MTV ? 0.6f * (float)pos / (float)MTV
-           : pos == MTV + 1 ? 0.75f
-                            : 0.75f + 0.0625f * (float)(pos - MTV - 1);
-}
-
-template <int MTV, int NLD>
-constexpr int copy_point(int c, int half) {
-    const float t = ((float)c + (half ? 0.5f : 0.f)) / (float)NLD;
-    int best = 0;
-    float bd = 2.f;
-    for (int pos = 0; pos <= MTV + 5; ++pos) {
-        const float d = copy_point_time<MTV>(pos) > t ? copy_point_time<MTV>(pos) - t : t - copy_point_time<MTV>(pos);
-        if (d < bd) {
-            bd = d;
-            best = pos;
-        }
+struct LrSched {
+    static constexpr int NPOS = MTV + 6;
+    static constexpr float time(int pos) {
+        return pos == 0 ? 0.f
+               : pos <= MTV ? 0.6f * (float)pos / (float)MTV
+               : pos == MTV + 1 ? 0.75f
+                                : 0.75f + 0.0625f * (float)(pos - MTV - 1);
     }
-    return best;
-}
-
-// Issues the copies of this wave that the schedule puts at copy point `pos` (a
-// constant once the callers' loops are unrolled).
-template <int MTV, int NLD, int B>
-__device__ __forceinline__ void copies_at(int pos, const DmaConst& dc, const DmaPage& d, int wave,
-                                          const uint32_t (&doff)[NLD]) {
-#pragma unroll
-    for (int c = 0; c < NLD; ++c) {
-        if (copy_point<MTV, NLD>(c, 0) == pos && wave < NWAVE / 2) dma_one<B>(dc, d, c, wave, doff[c]);
-        if (copy_point<MTV, NLD>(c, 1) == pos && wave >= NWAVE / 2) dma_one<B>(dc, d, c, wave, doff[c]);
-    }
-}
+};
 
 // z . codes for one tile: this lane's 4 z values (rows 4 lg .. 4 lg + 3) times its 4
 // codes (8 bytes).
@@ -189,24 +76,9 @@ __device__ __forceinline__ float tile_dot(const f32x4_t& z, uint2 w) {
     }
 }
 
-// Row of the wave's partial-logit table that slot s writes: with every head at <= 4
-// slots (`fast`), head k's j-th slot goes to row 4 k + j, so a head's rows past its
-// slots stay zero and the softmax sums 4 fixed rows; otherwise row s. Slots past the
-// wave's tiles write the spare row MAX_SLOTS.
-__device__ __forceinline__ int slot_row(cint_p pw, int s, int ntw, int nh, bool fast) {
-    if (s >= ntw) return MAX_SLOTS;
-    if (!fast) return s;
-    int row = MAX_SLOTS;
-    for (int k = 0; k < nh; ++k) {
-        const int f = pw[40 + k], c = pw[48 + k];
-        if (s >= f && s < f + c) row = 4 * k + (s - f);
-    }
-    return row;
-}
-
 // K side of one page (buffer B): MTV slots from VGPR AB, more from L2. Each group of
 // 4 slots is summed over the row groups with the lane swaps and stored as 4 rows.
-template <int FMT, int MTV, int NB, int B, int NLD, int BN>
+template <int FMT, int MTV, int NB, int B, int NLD, int BN, int NBUF>
 __device__ __forceinline__ void k_side(const DecodeParams& p, const LaneAddr<MTV>& la, const half8_t (&ab)[MTV][4],
                                        int ntw, int nh, bool fast, uint32_t sp, int lane, int wave, int cur_b,
                                        const DmaConst& dc, const DmaPage& dp, const uint32_t (&doff)[NLD]) {
@@ -223,7 +95,7 @@ __device__ __forceinline__ void k_side(const DecodeParams& p, const LaneAddr<MTV
                                       (i & 3) >= 3 ? v[3] : 0.f);
             lds_st<float>(la.st[i >> 2], r);
         }
-        copies_at<MTV, NLD, BN>(1 + i, dc, dp, opaque_s(wave), doff);
+        copies_at<LrSched<MTV>, NLD, BN, NBUF>(1 + i, dc, dp, opaque_s(wave), doff);
     }
     if (ntw > MTV) {  // slots past MTV: AB from the workspace (L2) on every page
         const int lg = lane >> 4, lr = lane & 15;
@@ -236,7 +108,7 @@ __device__ __forceinline__ void k_side(const DecodeParams& p, const LaneAddr<MTV
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) a[ks] = abg[(t * 4 + ks) * 64 + lane];
             const int T = ((cint_p)tiles)[4 * t + 1] >> 4;
-            const uint32_t ka = la.base + (uint32_t)((LrChunks<NB>::K0 + (T >> 1)) * LR_STRIDE + (T & 1) * 512 +
+            const uint32_t ka = la.base + (uint32_t)((LrChunks<NB>::K0 + (T >> 1)) * page_stride<NBUF>() + (T & 1) * 512 +
                                                         lr * 32 + 8 * lg + B * 1024);
             const float r = sum_rows(tile_dot<FMT>(mfma_tile(a, csb), lds_ld2(ka)));
             const int row = slot_row(pw, i, ntw, nh, fast);
@@ -298,7 +170,7 @@ __device__ __forceinline__ uint32_t v_pair(uint32_t a0, uint32_t a1) {
 // v_mfma_f32_4x4x4_16b with block 0's A broadcast (cbsz 4): per 4-token step lanes 0..3
 // hold P[head l][4 tokens], lane l holds V[4 tokens][column 64 nb + l], and the result
 // lands in lane l as acc[nb][head] for its column.
-template <int FMT, int NB, int B, int MTV, int NLD, int BN>
+template <int FMT, int NB, int B, int MTV, int NLD, int BN, int NBUF>
 __device__ __forceinline__ void pv_page(f32x4_t (&acc)[NB], uint32_t v_addr, uint32_t pr_addr, uint32_t plo_off,
                                         uint32_t salpha, bool rescale, const DmaConst& dc, const DmaPage& dp,
                                         int wave, const uint32_t (&doff)[NLD]) {
@@ -320,7 +192,7 @@ __device__ __forceinline__ void pv_page(f32x4_t (&acc)[NB], uint32_t v_addr, uin
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int byte = (4 * st + e) * C::VPITCH + 128 * nb;  // inside the V region
-                off[e] = (uint32_t)((byte >> 10) * LR_STRIDE + (byte & 1023) + B * 1024);
+                off[e] = (uint32_t)((byte >> 10) * page_stride<NBUF>() + (byte & 1023) + B * 1024);
             }
             const uint2 bv = make_uint2(v_pair(v_addr + off[0], v_addr + off[1]), v_pair(v_addr + off[2], v_addr + off[3]));
             if (FMT == FMT_BF16) {
@@ -333,18 +205,18 @@ __device__ __forceinline__ void pv_page(f32x4_t (&acc)[NB], uint32_t v_addr, uin
                                                              __builtin_bit_cast(half4_t, bv), acc[nb], 4, 0, 0);
             }
         }
-        if (st == 0) copies_at<MTV, NLD, BN>(MTV + 2, dc, dp, opaque_s(wave), doff);
-        if (st == 1) copies_at<MTV, NLD, BN>(MTV + 3, dc, dp, opaque_s(wave), doff);
-        if (st == 2) copies_at<MTV, NLD, BN>(MTV + 4, dc, dp, opaque_s(wave), doff);
-        if (st == 3) copies_at<MTV, NLD, BN>(MTV + 5, dc, dp, opaque_s(wave), doff);
+        if (st == 0) copies_at<LrSched<MTV>, NLD, BN, NBUF>(MTV + 2, dc, dp, opaque_s(wave), doff);
+        if (st == 1) copies_at<LrSched<MTV>, NLD, BN, NBUF>(MTV + 3, dc, dp, opaque_s(wave), doff);
+        if (st == 2) copies_at<LrSched<MTV>, NLD, BN, NBUF>(MTV + 4, dc, dp, opaque_s(wave), doff);
+        if (st == 3) copies_at<LrSched<MTV>, NLD, BN, NBUF>(MTV + 5, dc, dp, opaque_s(wave), doff);
     }
 }
 
 // One page of the loop: buffer BC holds page j (copied two pages ago); buffer BN
 // receives page j + 2 (page j - 1, its previous content, is done on every wave once the
 // barrier is passed).
-template <int FMT, int MTV, int NB, int NLD, int BC, int BN>
-__device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const LaneAddr<MTV>& la,
+template <int FMT, int MTV, int NB, int NLD, int BC, int BN, int NBUF>
+__device__ __forceinline__ bool lr_iter(PageLoop& st, const DmaConst& dc, const LaneAddr<MTV>& la,
                                         half8_t (&ab)[MTV][4], f32x4_t (&acc)[NB], SmState& sm,
                                         const uint32_t (&doff)[NLD], int ntw, int nh, bool fast, uint32_t sp,
                                         uint32_t plo_off, uint32_t salpha, const int* sqh, int lane, int wave) {
@@ -364,16 +236,16 @@ __device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const La
         }
         __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0)
     }
-    SKV_WAIT_VM_LGKM0(NLD);  // only the copies of page j + 1 may still be in flight
+    SKV_WAIT_VM_LGKM0(NBUF == 3 ? NLD : 0);  // only the copies of page j + 1 may still be in flight
     lds_barrier();           // page j is in LDS; every wave is done with page j - 1
     const DmaPage dp = dma_setup(dc, st.ld, st.nblk);
-    copies_at<MTV, NLD, BN>(0, dc, dp, opaque_s(wave), doff);
+    copies_at<LrSched<MTV>, NLD, BN, NBUF>(0, dc, dp, opaque_s(wave), doff);
     if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
-    k_side<FMT, MTV, NB, BC, NLD, BN>(p, la, ab, ntw, nh, fast, sp, lane, wave, cc.b, dc, dp, doff);
+    k_side<FMT, MTV, NB, BC, NLD, BN, NBUF>(p, la, ab, ntw, nh, fast, sp, lane, wave, cc.b, dc, dp, doff);
     const bool moved = softmax_page<FMT>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, TILE_TOK * cc.k,
                                          cc.lo, cc.hi);
-    copies_at<MTV, NLD, BN>(MTV + 1, dc, dp, opaque_s(wave), doff);
-    pv_page<FMT, NB, BC, MTV, NLD, BN>(acc, la.v, la.pr, plo_off, salpha, moved, dc, dp, wave, doff);
+    copies_at<LrSched<MTV>, NLD, BN, NBUF>(MTV + 1, dc, dp, opaque_s(wave), doff);
+    pv_page<FMT, NB, BC, MTV, NLD, BN, NBUF>(acc, la.v, la.pr, plo_off, salpha, moved, dc, dp, wave, doff);
     Cursor nx = cc;
     const bool seg_end = cur_next(nx, P, p.n, st.beg, st.end);
     if (seg_end) flush_partial<NB>(p, sm, acc, nh, cc.b + st.g, sqh, lane);
@@ -385,7 +257,7 @@ __device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const La
     return true;
 }
 
-template <int FMT, int MTV, int NB, int NLD>
+template <int FMT, int MTV, int NB, int NLD, int NBUF>
 __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     extern __shared__ __attribute__((aligned(16))) uint8_t s_pages[];
     __shared__ __attribute__((aligned(16))) float s_part[NWAVE][(MAX_SLOTS + 1) * TILE_TOK];
@@ -401,7 +273,7 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     cint_p P = (cint_p)(p.ws + 4);
     cint_p plan = (cint_p)(p.ws + p.ws_plan);
     if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
-    LrLoop st;
+    PageLoop st;
     st.g = blockIdx.x;
     const int S_tok = ((cint_p)p.ws)[0];
     const int T = P[p.n];
@@ -429,12 +301,12 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
 #pragma unroll
         for (int i = 0; i < MTV; ++i) {
             const int Tc = tiles[4 * pw[8 + i] + 1] >> 4;  // code tile: first cache lane / 16
-            la.k[i] = base + (uint32_t)((C::K0 + (Tc >> 1)) * LR_STRIDE + (Tc & 1) * 512 + lr * 32 + 8 * lg);
+            la.k[i] = base + (uint32_t)((C::K0 + (Tc >> 1)) * page_stride<NBUF>() + (Tc & 1) * 512 + lr * 32 + 8 * lg);
         }
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
-            la.cs[ks] = base + (uint32_t)((lr >> 2) * LR_STRIDE + (lr & 3) * 256 + (((4 * ks + lg) ^ lr) << 4));
-        la.v = base + (uint32_t)(C::V0 * LR_STRIDE + 2 * lane);
+            la.cs[ks] = base + cs_read_offset<NBUF>(ks, lg, lr);
+        la.v = base + (uint32_t)(C::V0 * page_stride<NBUF>() + 2 * lane);
         la.base = base;
         const int rslot = ((lg & 1) << 1) | (lg >> 1);  // sum_rows4 puts inputs (a, b, c, d) in rows (0, 2, 1, 3)
 #pragma unroll
@@ -463,8 +335,7 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
         const int ch = i * NWAVE + wave;
         uint32_t off = 0x80000000u;  // past the descriptor range: no memory access
         if (ch < CS_CHUNKS) {
-            const int row = 4 * ch + (lane >> 4), g = lane & 15;  // LDS granule g of row holds granule g ^ row
-            off = (uint32_t)(row * p.cs_s0b + ((g ^ row) << 4));
+            off = cs_copy_offset(ch, lane, p.cs_s0b);
         } else if (ch < C::K0) {
             const int vb = (ch - C::V0) * 1024 + 16 * lane;  // byte inside the V rows
             const int row = vb / C::VPITCH, col = vb % C::VPITCH;
@@ -475,22 +346,18 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
         }
         doff[i] = off;
     }
-    DmaConst dc;
-    dc.cache = p.cache; dc.c_s0 = p.c_s0; dc.c_s1 = (int)p.c_s1;
-    dc.bt = p.bt; dc.bt_s0 = p.bt_s0; dc.bt_s1 = p.bt_s1; dc.bs_shift = p.bs_shift;
-    dc.cs = p.cs; dc.cs_s0b = p.cs_s0b;
-    dc.nch = p.nch;
-    dc.m0w = base + (uint32_t)(wave * LR_STRIDE);
-    dc.m0dummy = base + (uint32_t)(p.nch * LR_STRIDE);
+    const DmaConst dc = dma_const<NBUF>(p, base, wave, base + (uint32_t)(p.nch * page_stride<NBUF>()));
     __syncthreads();
 
     cur_first(st.cc, P, p.n, st.beg, st.end);
     st.ld = st.cc;
     st.new_seg = true;
-    dma_page<NLD, 0>(dc, st.ld, page_block(dc, st.ld), wave, doff);
+    dma_page<NLD, 0, NBUF>(dc, st.ld, page_block(dc, st.ld), wave, doff);
     cur_next(st.ld, P, p.n, st.beg, st.end);
-    dma_page<NLD, 1>(dc, st.ld, page_block(dc, st.ld), wave, doff);
-    if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
+    if (NBUF == 3) {
+        dma_page<NLD, 1, NBUF>(dc, st.ld, page_block(dc, st.ld), wave, doff);
+        if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
+    }
     st.nblk = page_block(dc, st.ld);
 
     half8_t ab[MTV][4];
@@ -498,38 +365,50 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
 #pragma unroll
     for (int k = 0; k < NB; ++k) acc[k] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
     const int* sqh = &s_qh[wave][0];
-    while (true) {
-        if (!lr_iter<FMT, MTV, NB, NLD, 0, 2>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, sqh,
-                                              lane, wave))
-            break;
-        if (!lr_iter<FMT, MTV, NB, NLD, 1, 0>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, sqh,
-                                              lane, wave))
-            break;
-        if (!lr_iter<FMT, MTV, NB, NLD, 2, 1>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, sqh,
-                                              lane, wave))
-            break;
+    if (NBUF == 3) {
+        while (true) {
+            if (!lr_iter<FMT, MTV, NB, NLD, 0, 2, NBUF>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, sqh,
+                                                  lane, wave))
+                break;
+            if (!lr_iter<FMT, MTV, NB, NLD, 1, 0, NBUF>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, sqh,
+                                                  lane, wave))
+                break;
+            if (!lr_iter<FMT, MTV, NB, NLD, 2, 1, NBUF>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, sqh,
+                                                  lane, wave))
+                break;
+        }
+    } else {  // two buffers: page j + 1 goes into the buffer page j - 1 left
+        while (true) {
+            if (!lr_iter<FMT, MTV, NB, NLD, 0, 1, NBUF>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha,
+                                                       sqh, lane, wave))
+                break;
+            if (!lr_iter<FMT, MTV, NB, NLD, 1, 0, NBUF>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha,
+                                                       sqh, lane, wave))
+                break;
+        }
     }
     __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): no copy may land after the workgroup ends
 }
 
-template <int FMT, int MTV, int NLD>
+template <int FMT, int MTV, int NLD, int NBUF>
 const void* pick_nb(int nb) {
-    if (nb <= 1) return (const void*)&lowrank_kernel<FMT, MTV, 1, NLD>;
-    if (nb <= 2) return (const void*)&lowrank_kernel<FMT, MTV, 2, NLD>;
-    return (const void*)&lowrank_kernel<FMT, MTV, 4, NLD>;
+    if (nb <= 1) return (const void*)&lowrank_kernel<FMT, MTV, 1, NLD, NBUF>;
+    if (nb <= 2) return (const void*)&lowrank_kernel<FMT, MTV, 2, NLD, NBUF>;
+    return (const void*)&lowrank_kernel<FMT, MTV, 4, NLD, NBUF>;
 }
 
-template <int FMT, int NLD>
+template <int FMT, int NLD, int NBUF>
 const void* pick_mtv(int need, int nb) {
-    return need <= 4 ? pick_nb<FMT, 4, NLD>(nb)
-           : need <= 8 ? pick_nb<FMT, 8, NLD>(nb)
-           : need <= 9 ? pick_nb<FMT, 9, NLD>(nb)
-                       : pick_nb<FMT, 10, NLD>(nb);
+    return need <= 4 ? pick_nb<FMT, 4, NLD, NBUF>(nb)
+           : need <= 8 ? pick_nb<FMT, 8, NLD, NBUF>(nb)
+           : need <= 9 ? pick_nb<FMT, 9, NLD, NBUF>(nb)
+                       : pick_nb<FMT, 10, NLD, NBUF>(nb);
 }
 
 template <int FMT>
-const void* pick(int nld, int need, int nb) {
-    return nld <= 3 ? pick_mtv<FMT, 3>(need, nb) : pick_mtv<FMT, 6>(need, nb);
+const void* pick(int nbuf, int nld, int need, int nb) {
+    if (nbuf == 2) return pick_mtv<FMT, 8, 2>(need, nb);
+    return nld <= 3 ? pick_mtv<FMT, 3, 3>(need, nb) : pick_mtv<FMT, 6, 3>(need, nb);
 }
 
 int nb_blocks(int nb) { return nb <= 1 ? 1 : nb <= 2 ? 2 : 4; }
@@ -541,21 +420,32 @@ int lowrank_chunks(int k_width, int nb) {
     return CS_CHUNKS + 2 * nb_blocks(nb) + (tiles + 1) / 2;
 }
 
-// Copies per wave per page: 3 or 6 (the instantiated counts), 0 if a page needs more.
-int lowrank_copies(int k_width, int nb) {
-    const int nld = (lowrank_chunks(k_width, nb) + NWAVE - 1) / NWAVE;
-    return nld <= 3 ? 3 : nld <= 6 ? 6 : 0;
+// Page buffers: three while a page's chunks fit three times (up to 48), else two (up to
+// 64); 0 if a page does not fit.
+int lowrank_buffers(int k_width, int nb) {
+    const int ch = lowrank_chunks(k_width, nb);
+    return ch <= 6 * NWAVE ? 3 : ch <= 8 * NWAVE ? 2 : 0;
 }
 
-int lowrank_lds_bytes(int k_width, int nb) { return lowrank_chunks(k_width, nb) * LR_STRIDE + 1024; }
+// Copies per wave per page (the instantiated counts: 3 or 6 with three buffers, 8 with
+// two), 0 if a page does not fit.
+int lowrank_copies(int k_width, int nb) {
+    const int nld = (lowrank_chunks(k_width, nb) + NWAVE - 1) / NWAVE;
+    const int nbuf = lowrank_buffers(k_width, nb);
+    return nbuf == 3 ? (nld <= 3 ? 3 : 6) : nbuf == 2 ? 8 : 0;
+}
+
+int lowrank_lds_bytes(int k_width, int nb) {
+    return lowrank_chunks(k_width, nb) * lowrank_buffers(k_width, nb) * 1024 + 1024;
+}
 
 // Rank tiles per wave held in VGPRs: the wave plan balances whole heads to within a
 // tile of TT / 8, so MTV = ceil(TT / 8) covers every wave for the usual rank mixes (a
 // wave with more streams the rest of its tiles from L2).
 int launch_lowrank(const DecodeParams& p, int fmt, int nb, int grid, hipStream_t stream) {
     const int need = (p.TT + NWAVE - 1) / NWAVE;
-    const int nld = lowrank_copies(p.k_width, nb);
-    const void* fn = fmt == FMT_BF16 ? pick<FMT_BF16>(nld, need, nb) : pick<FMT_F16>(nld, need, nb);
+    const int nld = lowrank_copies(p.k_width, nb), nbuf = lowrank_buffers(p.k_width, nb);
+    const void* fn = fmt == FMT_BF16 ? pick<FMT_BF16>(nbuf, nld, need, nb) : pick<FMT_F16>(nbuf, nld, need, nb);
     static const void* raised[256];  // kernels whose dynamic-LDS limit was raised (host-side bookkeeping)
     static int nraised = 0;
     bool seen = false;

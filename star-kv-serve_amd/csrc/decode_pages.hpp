@@ -1,0 +1,187 @@
+// Page machinery shared by the two decode kernels (decode_lowrank.hip for bf16/fp16
+// codes, decode_quant.hip for 3.2-bit codes): LDS access helpers, the global->LDS page
+// copies and their schedule over an iteration, and the partial-logit row map.
+//
+// Page buffers. A workgroup keeps NBUF page buffers (three: pages j, j + 1, j + 2 in
+// flight; two for pages too large to fit three times) interleaved at 1 KB: chunk c of
+// buffer b sits at byte c * NBUF KB + b KB of the dynamic LDS block, so a read of the
+// current page is a per-lane address fixed for the whole kernel plus the immediate
+// b * 1024. Chunks 0 .. 3 of a page hold its 16
+// cos/sin rows (256 B per row; granule g of row r is stored at granule g ^ r, so the 16
+// rows of an MFMA operand read hit distinct banks); the chunks after them are the
+// kernel's own. Copy i of wave w moves chunk 8 i + w; a lane's source offset inside the
+// page depends only on (chunk, lane) and is computed once. Copies past a page's chunks
+// land in a 1 KB dummy block and read nothing, so every wave issues the same number of
+// copies per page and the waits stay static.
+#pragma once
+
+#include "decode_common.hpp"
+
+namespace starkv {
+
+// Bytes between chunks c and c + 1 of one buffer.
+template <int NBUF>
+constexpr int page_stride() {
+    return NBUF * 1024;
+}
+constexpr int PAGE_STRIDE = page_stride<3>();  // the three-buffer layout
+
+typedef short short2_t __attribute__((ext_vector_type(2)));
+
+template <typename T>
+__device__ __forceinline__ T lds_ld(uint32_t a) {
+    return *(const __attribute__((address_space(3))) T*)(a);
+}
+template <typename T>
+__device__ __forceinline__ void lds_st(uint32_t a, T v) {
+    *(__attribute__((address_space(3))) T*)(a) = v;
+}
+__device__ __forceinline__ uint2 lds_ld2(uint32_t a) {
+    const uint64_t v = lds_ld<uint64_t>(a);
+    return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+
+// A 16-byte-per-lane copy to LDS address m0 (a wave-uniform SGPR value).
+__device__ __forceinline__ void copy16(const int4v_t& rsrc, uint32_t m0, uint32_t voff) { lds_copy16(rsrc, m0, voff); }
+
+// Source offset of lane `lane`'s 16 bytes of cos/sin chunk ch (< CS_CHUNKS): row
+// 4 ch + lane / 16, LDS granule g = lane % 16 holding granule g ^ row.
+__device__ __forceinline__ uint32_t cs_copy_offset(int ch, int lane, int cs_s0b) {
+    const int row = 4 * ch + (lane >> 4), g = lane & 15;
+    return (uint32_t)(row * cs_s0b + ((g ^ row) << 4));
+}
+
+// LDS address (buffer 0, relative to the page block) of granule 4 ks + lg of cos/sin
+// row lr: the B operand of v_mfma_f32_16x16x32_f16 for K-step ks.
+template <int NBUF = 3>
+__device__ __forceinline__ uint32_t cs_read_offset(int ks, int lg, int lr) {
+    return (uint32_t)((lr >> 2) * page_stride<NBUF>() + (lr & 3) * 256 + (((4 * ks + lg) ^ lr) << 4));
+}
+
+// Loop-invariant operands of the page copies, read once from the parameter block and
+// held in SGPRs.
+struct DmaConst {
+    const uint8_t* cache; int64_t c_s0; int c_s1;
+    const int32_t* bt; int bt_s0, bt_s1, bs_shift;
+    const uint8_t* cs; int cs_s0b;
+    int nch;
+    uint32_t m0w, m0dummy;  // LDS address of this wave's first chunk (buffer 0); the dummy block
+};
+
+template <int NBUF = 3>
+__device__ __forceinline__ DmaConst dma_const(const DecodeParams& p, uint32_t base, int wave, uint32_t dummy) {
+    DmaConst dc;
+    dc.cache = p.cache; dc.c_s0 = p.c_s0; dc.c_s1 = (int)p.c_s1;
+    dc.bt = p.bt; dc.bt_s0 = p.bt_s0; dc.bt_s1 = p.bt_s1; dc.bs_shift = p.bs_shift;
+    dc.cs = p.cs; dc.cs_s0b = p.cs_s0b;
+    dc.nch = p.nch;
+    dc.m0w = base + (uint32_t)(wave * page_stride<NBUF>());
+    dc.m0dummy = dummy;
+    return dc;
+}
+
+// Cache block of the page cursor c points at (0 past the range).
+__device__ __forceinline__ int page_block(const DmaConst& dc, const Cursor& c) {
+    return c.valid ? ((cint_p)dc.bt)[c.b * dc.bt_s0 + (c.k >> dc.bs_shift) * dc.bt_s1] : 0;
+}
+
+// Buffer descriptors of one page: its rows and its cos/sin rows, bounded to the rows
+// the request has (rows past its end are not read). Past the end of the workgroup's
+// range both are empty: the copies still issue.
+struct DmaPage {
+    int4v_t rkv, rcs;
+};
+
+__device__ __forceinline__ DmaPage dma_setup(const DmaConst& dc, const Cursor& c, int blk) {
+    const bool v = c.valid;
+    const int k = v ? c.k : 0;
+    const int row0 = (k & ((1 << dc.bs_shift) - 1)) * TILE_TOK;  // first slot of the page in its block
+    const uint8_t* page = dc.cache + (int64_t)blk * dc.c_s0 + (int64_t)row0 * dc.c_s1;
+    const int tok0 = TILE_TOK * k;
+    const int rows = v ? min(TILE_TOK, c.len - tok0) : 0;
+    DmaPage d;
+    d.rkv = buffer_rsrc(page, rows * dc.c_s1);
+    d.rcs = buffer_rsrc(dc.cs + (int64_t)tok0 * dc.cs_s0b, rows * dc.cs_s0b);
+    return d;
+}
+
+// Copy i of this wave into buffer B: chunk 8 i + wave (cos/sin rows for chunks < 4).
+template <int B, int NBUF = 3>
+__device__ __forceinline__ void dma_one(const DmaConst& dc, const DmaPage& d, int i, int wave, uint32_t off) {
+    const int ch = i * NWAVE + wave;
+    const uint32_t m0 = ch < dc.nch ? dc.m0w + (uint32_t)(i * NWAVE * page_stride<NBUF>() + B * 1024) : dc.m0dummy;
+    if (i == 0 && wave < CS_CHUNKS)
+        copy16(d.rcs, m0, off);
+    else
+        copy16(d.rkv, m0, off);
+}
+
+template <int NLD, int B, int NBUF = 3>
+__device__ __forceinline__ void dma_page(const DmaConst& dc, const Cursor& c, int blk, int wave,
+                                         const uint32_t (&doff)[NLD]) {
+    const DmaPage d = dma_setup(dc, c, blk);
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) dma_one<B, NBUF>(dc, d, i, wave, doff[i]);
+}
+
+// Copy schedule. A page's copies must reach the copy queue at about the rate the queue
+// drains: a burst fills it, and a wave whose copy finds it full stalls until it has room.
+// A kernel's iteration offers copy points 0 .. S::NPOS - 1 at rough positions S::time(pos)
+// (fractions of the iteration). Copy c of the waves on the first wave slot of each SIMD
+// (waves 0-3) goes to the point nearest c / NLD, and of the others (waves 4-7) to the
+// point nearest (c + 1/2) / NLD, so that the two waves of a SIMD never issue together.
+template <class S, int NLD>
+constexpr int copy_point(int c, int half) {
+    const float t = ((float)c + (half ? 0.5f : 0.f)) / (float)NLD;
+    int best = 0;
+    float bd = 2.f;
+    for (int pos = 0; pos < S::NPOS; ++pos) {
+        const float d = S::time(pos) > t ? S::time(pos) - t : t - S::time(pos);
+        if (d < bd) {
+            bd = d;
+            best = pos;
+        }
+    }
+    return best;
+}
+
+// Issues the copies of this wave that the schedule puts at copy point `pos` (a
+// constant once the callers' loops are unrolled).
+template <class S, int NLD, int B, int NBUF = 3>
+__device__ __forceinline__ void copies_at(int pos, const DmaConst& dc, const DmaPage& d, int wave,
+                                          const uint32_t (&doff)[NLD]) {
+#pragma unroll
+    for (int c = 0; c < NLD; ++c) {
+        if (copy_point<S, NLD>(c, 0) == pos && wave < NWAVE / 2) dma_one<B, NBUF>(dc, d, c, wave, doff[c]);
+        if (copy_point<S, NLD>(c, 1) == pos && wave >= NWAVE / 2) dma_one<B, NBUF>(dc, d, c, wave, doff[c]);
+    }
+}
+
+// Row of the wave's partial-logit table that slot s writes: with every head at <= 4
+// slots (`fast`), head k's j-th slot goes to row 4 k + j, so a head's rows past its
+// slots stay zero and the softmax sums 4 fixed rows; otherwise row s. Slots past the
+// wave's tiles write the spare row MAX_SLOTS.
+__device__ __forceinline__ int slot_row(cint_p pw, int s, int ntw, int nh, bool fast) {
+    if (s >= ntw) return MAX_SLOTS;
+    if (!fast) return s;
+    int row = MAX_SLOTS;
+    for (int k = 0; k < nh; ++k) {
+        const int f = pw[40 + k], c = pw[48 + k];
+        if (s >= f && s < f + c) row = 4 * k + (s - f);
+    }
+    return row;
+}
+
+// Page-loop state of a workgroup: the page being computed (cc), the page whose copies
+// issue next (ld, two pages ahead) and its cache block, loaded one page ahead.
+struct PageLoop {
+    Cursor cc, ld;
+    int beg, end, g;
+    int nblk;
+    bool new_seg;  // cc starts a new request: its AB goes into registers first
+};
+
+}  // namespace starkv

@@ -93,6 +93,9 @@ LOWRANK_CASES = {
     "ranks_not_16": ([77, 260], dict(ranks=[20, 1, 33, 64, 7, 48, 16, 50], num_heads=8)),
     "block_32": ([1000, 47, 64], dict(block_size=32)),
     "block_128": ([700, 129, 1], dict(block_size=128)),
+    # pages too large for three LDS buffers: the two-buffer layout
+    "wide_k1376": ([300, 17, 1024], dict(ranks=[48] * 22 + [32] * 10)),
+    "wide_k1536_v256": ([150, 33], dict(ranks=[48] * 32, v_rank=256)),
 }
 
 
@@ -202,6 +205,13 @@ QUANT_CASES = {
     "graph_span": ([100, 37, 999], dict(max_seq_len=4096)),
     "fp16": ([513, 90], dict(dtype=torch.float16)),
     "block_64": ([900, 65, 3], dict(block_size=64)),
+    # heads with more than 16 outlier ranks (several outlier tiles), a wave with more
+    # tiles than it holds in registers, ranks that are not multiples of 16
+    "big_heads": ([500, 77], dict(ranks=[256, 16, 100, 20], num_heads=4)),
+    "ranks_not_16": ([77, 260], dict(ranks=[20, 1, 33, 64, 7, 48, 16, 50], num_heads=8)),
+    # V lane maps over 3 and 5 blocks of 64 (outlier columns padded to 4)
+    "v_rank_128": ([300, 45], dict(v_rank=128)),
+    "v_rank_256_h8": ([200, 31], dict(v_rank=256, num_heads=8)),
 }
 
 
@@ -210,7 +220,8 @@ def test_quant_decode_vs_oracle(cuda, name):
     lengths, kw = QUANT_CASES[name]
     kw = dict(kw)
     print(f"\n[quant] case={name} lengths={lengths[:8]} {kw}", flush=True)
-    wl = W.make_quant(lengths, num_heads=32, seed=200 + len(name), device=cuda, **kw)
+    nh = kw.pop("num_heads", 32)
+    wl = W.make_quant(lengths, num_heads=nh, seed=200 + len(name), device=cuda, **kw)
     check_packed_rows(wl)
     out = paged_quant_decode(*wl.decode_args())
     torch.cuda.synchronize()
