@@ -80,13 +80,14 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
                                                      const int32_t* __restrict__ k_offsets,
                                                      const int32_t* __restrict__ t_head,
                                                      const int32_t* __restrict__ t_nout,
-                                                     const int32_t* __restrict__ t_last, uint8_t* __restrict__ ws,
-                                                     size_t ws_tiles, size_t ws_plan) {
+                                                     const int32_t* __restrict__ t_last, int qorder,
+                                                     uint8_t* __restrict__ ws, size_t ws_tiles, size_t ws_plan) {
     __shared__ int s_wsum[16];
     __shared__ int s_total;
     __shared__ int s_hf[MAX_H], s_hn[MAX_H];
     __shared__ int s_rank[MAX_H], s_off[MAX_H];        // k_ranks, k_offsets (bf16/fp16)
     __shared__ int s_thead[MAX_TT], s_tmeta[MAX_TT];   // t_head, nout | last << 8 (3.2-bit)
+    __shared__ int s_tword[MAX_TT];                    // per tile: code tile | outlier ranks << 13
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int* hdr = (int*)ws;
     int4* tiles = (int4*)(ws + ws_tiles);
@@ -122,9 +123,11 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
 
     // Tile table and (first tile, tiles) per query head.
     if (t_head) {  // 3.2-bit: the k_tables arrays, lanes contiguous, MHA
-        for (int t = tid; t < TT; t += blockDim.x)
+        for (int t = tid; t < TT; t += blockDim.x) {
             tiles[t] = make_int4(s_thead[t], 16 * t, 16 | ((s_tmeta[t] & 255) << 8) | ((s_tmeta[t] >> 8) << 16),
                                  s_thead[t]);
+            s_tword[t] = t | (min(s_tmeta[t] & 255, 16) << 13);
+        }
         if (tid < Hq) {
             int first = -1, cnt = 0;
             for (int t = 0; t < TT; ++t)
@@ -140,8 +143,10 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
         const int nt = (R + 15) >> 4;
         t0 += (tid - kv * grp) * nt;
         int cnt = 0;
-        for (int j = 0; j < nt && t0 + j < TT; ++j, ++cnt)
+        for (int j = 0; j < nt && t0 + j < TT; ++j, ++cnt) {
             tiles[t0 + j] = make_int4(tid, o + 16 * j, min(16, R - 16 * j) | ((j == nt - 1) << 16), kv);
+            s_tword[t0 + j] = (o >> 4) + j;
+        }
         s_hf[tid] = min(t0, TT);
         s_hn[tid] = cnt;
     }
@@ -201,13 +206,16 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
         }
         const int ok = lanes8_max(lane < NWAVE ? load : 0) <= MAX_SLOTS;
         // Each head's place in its wave's plan: k = its wave's heads before it in the size
-        // order, sl = their tiles. Lane w < 8 also counts its wave's heads and tiles.
-        int k = 0, sl = 0, nhw = 0, ntw = 0;
+        // order, sl = their tiles, nfb = those of them with tiles, nnb = their tiles past
+        // their first; over its whole wave: nfh heads with tiles, the largest head mxh.
+        // Lane w < 8 also counts its wave's heads, tiles, heads with tiles, largest head.
+        int k = 0, sl = 0, nfb = 0, nnb = 0, nfh = 0, mxh = 0, nhw = 0, ntw = 0, nfw = 0, mxw = 0;
         for (int h = 0; h < Hq; ++h) {
             const int wh = __builtin_amdgcn_readlane(hwave, h), ph = __builtin_amdgcn_readlane(pos, h);
             const int zh = __builtin_amdgcn_readlane(hsz, h);
-            if (wh == hwave && ph < pos) { ++k; sl += zh; }
-            if (wh == lane) { ++nhw; ntw += zh; }
+            if (wh == hwave && ph < pos) { ++k; sl += zh; nfb += zh > 0; nnb += max(zh - 1, 0); }
+            if (wh == hwave) { nfh += zh > 0; mxh = max(mxh, zh); }
+            if (wh == lane) { ++nhw; ntw += zh; nfw += zh > 0; mxw = max(mxw, zh); }
         }
         // Clear the 8 plans, then every head writes its own entries (same wave: in order).
         for (int i = lane; i < NWAVE * PLAN_STRIDE; i += 64) plan[i] = 0;
@@ -217,12 +225,23 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
             pw[32 + k] = lane;
             pw[40 + k] = sl;
             pw[48 + k] = hsz;
-            for (int j = 0; j < hsz; ++j) pw[8 + sl + j] = hfirst + j;
+            for (int j = 0; j < hsz; ++j) {
+                pw[8 + sl + j] = hfirst + j;
+                // The decode kernel's slot order: plan order, or for the 3.2-bit kernel the
+                // heads' first tiles first (the ones with outlier ranks), then the rest.
+                const int ks = qorder ? (j == 0 ? nfb : nfh + nnb + j - 1) : sl + j;
+                const int row = mxh <= 4 ? 4 * k + j : sl + j;  // slot_row()'s partial-logit row
+                pw[PW_SLOTS + ks] = slot_word(s_tword[hfirst + j], row, k, hfirst + j);
+            }
         }
         if (lane < NWAVE) {
             int* pw = plan + lane * PLAN_STRIDE;
             pw[0] = ok ? ntw : 0;
             pw[1] = ok ? nhw : 0;
+            pw[2] = ok ? nfw : 0;
+            pw[3] = mxw <= 4;
+            for (int s = ok ? ntw : 0; s < MAX_SLOTS; ++s)  // slots past the wave's tiles: tile 0, the spare row
+                pw[PW_SLOTS + s] = slot_word(s_tword[0] & SW_CODE_MASK, MAX_SLOTS, 0, 0);
         }
         if (lane == 0) plan[NWAVE * PLAN_STRIDE] = ok;
     }
@@ -500,7 +519,8 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     p.ws_m = wl.m; p.ws_l = wl.l; p.ws_acc = wl.acc;
 
     hipLaunchKernelGGL(setup_kernel, dim3(1), dim3(1024), 0, stream, a.seq_lens, a.n, a.max_seq_len, a.grid, a.Hq,
-                       a.Hkv, TT, a.k_ranks, a.k_offsets, a.t_head, a.t_nout, a.t_last, p.ws, wl.tiles, wl.plan);
+                       a.Hkv, TT, a.k_ranks, a.k_offsets, a.t_head, a.t_nout, a.t_last, fmt == FMT_Q4 ? 1 : 0, p.ws,
+                       wl.tiles, wl.plan);
     SKV_HIP(hipGetLastError());
     hipLaunchKernelGGL(fold_tiles_kernel, dim3((TT * 128 + 255) / 256, a.n), dim3(256), 0, stream, a.q, a.q_s0,
                        a.q_s1, a.q_dt, a.k_up, a.ku_s0, a.w_dt, (const uint8_t*)p.ws + wl.tiles, TT,

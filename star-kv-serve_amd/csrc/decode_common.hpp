@@ -27,7 +27,8 @@ constexpr int MAX_TT = 96;                  // rank tiles per call (k_width x he
 constexpr int MAX_H = 32;                   // query heads
 constexpr int MAX_HW = 8;                   // query heads per wave
 constexpr int MAX_SLOTS = 16;               // rank tiles per wave
-constexpr int PLAN_STRIDE = 64;             // ints per wave in the plan
+constexpr int PLAN_STRIDE = 80;             // ints per wave in the plan
+constexpr int PW_SLOTS = 64;                // first slot word in a wave's plan
 constexpr int CS_ROW_LDS = 256;             // LDS bytes per cos/sin row (granules XOR-swizzled by row)
 constexpr int CS_CHUNKS = 4;                // 16 rows x 16 granules -> 4 copies of 64 granules
 constexpr float LAZY_MAX = 8.f;             // log2 headroom before the running max moves
@@ -35,12 +36,31 @@ constexpr float LAZY_MAX = 8.f;             // log2 headroom before the running 
 // Workspace layout, in bytes from the base (every region 256-byte aligned):
 //   hdr    int   [2 + n]      S (tokens per workgroup), P[0..n] (prefix of clamped lengths)
 //   tiles  int4  [TT]         {q head, first cache lane, valid | nout << 8 | last << 16, kv head}
-//   plan   int   [8][64] + 1  per wave: [0] tiles, [1] heads, [8 + s] tile of slot s,
+//   plan   int   [8][80] + 1  per wave: [0] tiles, [1] heads, [2] heads with tiles,
+//                             [3] 1 if every head has <= 4 tiles, [8 + s] tile of slot s,
 //                             [32 + k] q head of local head k, [40 + k] its first slot,
-//                             [48 + k] its slots; then 1 if every head found a wave
+//                             [48 + k] its slots, [64 + i] slot word of the decode kernel's
+//                             slot i (below); then 1 if every head found a wave
 //   ab     fp16  [n][TT][4][64][8]
 //   m, l   fp32  [slots][Hq]  (log2-domain reference max and sum per partial)
 //   acc    fp32  [slots][Hq][v_rank]
+// Slot word: everything a decode kernel needs of one of its slots, so that its prologue
+// reads a wave's slots with a few wide scalar loads: the code tile (first cache lane /
+// 16), the tile's outlier ranks (3.2-bit), the slot's partial-logit row, its local head
+// and its tile. The row: with every head of the wave at <= 4 slots, head k's j-th slot
+// goes to row 4 k + j, so a head's rows past its slots stay zero and the softmax sums 4
+// fixed rows; otherwise the slot's place in the plan. Slots past the wave's tiles hold
+// tile 0 and the spare row MAX_SLOTS.
+constexpr uint32_t SW_CODE_MASK = 0x1FFF;  // bits 0-12: code tile; 13-17: outlier ranks
+__host__ __device__ constexpr uint32_t slot_word(uint32_t code_nout, int row, int head, int tile) {
+    return code_nout | ((uint32_t)row << 18) | ((uint32_t)head << 23) | ((uint32_t)tile << 25);
+}
+__device__ __forceinline__ int sw_code(uint32_t w) { return (int)(w & SW_CODE_MASK); }
+__device__ __forceinline__ int sw_nout(uint32_t w) { return (int)((w >> 13) & 31); }
+__device__ __forceinline__ int sw_row(uint32_t w) { return (int)((w >> 18) & 31); }
+__device__ __forceinline__ int sw_head(uint32_t w) { return (int)((w >> 23) & 3); }
+__device__ __forceinline__ int sw_tile(uint32_t w) { return (int)(w >> 25); }
+
 struct WsLayout {
     size_t hdr, tiles, plan, ab, m, l, acc, total;
 };

@@ -100,19 +100,18 @@ __device__ __forceinline__ void k_side(const DecodeParams& p, const LaneAddr<MTV
     if (ntw > MTV) {  // slots past MTV: AB from the workspace (L2) on every page
         const int lg = lane >> 4, lr = lane & 15;
         cint_p pw = (cint_p)(p.ws + p.ws_plan) + wave * PLAN_STRIDE;
-        cint_p tiles = (cint_p)(p.ws + p.ws_tiles);
         const half8_t* abg = (const half8_t*)(p.ws + p.ws_ab + (size_t)cur_b * p.TT * AB_TILE_BYTES);
         for (int i = MTV; i < ntw; ++i) {
-            const int t = pw[8 + i];
+            const uint32_t wd = (uint32_t)pw[PW_SLOTS + i];
+            const int t = sw_tile(wd);
             half8_t a[4];
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) a[ks] = abg[(t * 4 + ks) * 64 + lane];
-            const int T = ((cint_p)tiles)[4 * t + 1] >> 4;
+            const int T = sw_code(wd);
             const uint32_t ka = la.base + (uint32_t)((LrChunks<NB>::K0 + (T >> 1)) * page_stride<NBUF>() + (T & 1) * 512 +
                                                         lr * 32 + 8 * lg + B * 1024);
             const float r = sum_rows(tile_dot<FMT>(mfma_tile(a, csb), lds_ld2(ka)));
-            const int row = slot_row(pw, i, ntw, nh, fast);
-            if (lane < 16) lds_st<float>(sp + (uint32_t)(row * TILE_TOK + lr) * 4, r);
+            if (lane < 16) lds_st<float>(sp + (uint32_t)(sw_row(wd) * TILE_TOK + lr) * 4, r);
         }
         __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): no tracked load left pending
     }
@@ -291,16 +290,17 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
     cint_p pw = plan + wave * PLAN_STRIDE;
     const int ntw = pw[0], nh = pw[1];
-    bool fast = true;
-    for (int k = 0; k < nh; ++k) fast = fast && pw[48 + k] <= 4;
+    const bool fast = pw[3] != 0;
     const uint32_t base = lds_addr(s_pages);
     const uint32_t sp = lds_addr(&s_part[wave][0]);
     LaneAddr<MTV> la;
+    uint32_t swd[MTV];  // the wave's slot words (plan order), read with a few wide scalar loads
+#pragma unroll
+    for (int i = 0; i < MTV; ++i) swd[i] = (uint32_t)pw[PW_SLOTS + i];
     {
-        cint_p tiles = (cint_p)(p.ws + p.ws_tiles);
 #pragma unroll
         for (int i = 0; i < MTV; ++i) {
-            const int Tc = tiles[4 * pw[8 + i] + 1] >> 4;  // code tile: first cache lane / 16
+            const int Tc = sw_code(swd[i]);  // code tile: first cache lane / 16
             la.k[i] = base + (uint32_t)((C::K0 + (Tc >> 1)) * page_stride<NBUF>() + (Tc & 1) * 512 + lr * 32 + 8 * lg);
         }
 #pragma unroll
@@ -311,8 +311,10 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
         const int rslot = ((lg & 1) << 1) | (lg >> 1);  // sum_rows4 puts inputs (a, b, c, d) in rows (0, 2, 1, 3)
 #pragma unroll
         for (int g = 0; g < (MTV + 3) / 4; ++g) {
-            const int s = 4 * g + rslot;
-            const int row = s < MTV ? slot_row(pw, s, ntw, nh, fast) : MAX_SLOTS;
+            int row = MAX_SLOTS;  // the row of slot 4 g + rslot (past MTV: the spare row)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (4 * g + j < MTV && rslot == j) row = sw_row(swd[4 * g + j < MTV ? 4 * g + j : 0]);
             la.st[g] = sp + (uint32_t)(row * TILE_TOK + lr) * 4;
         }
         la.sm = sp + (uint32_t)(4 * lg * TILE_TOK + lr) * 4;

@@ -1,6 +1,6 @@
 // Page machinery shared by the two decode kernels (decode_lowrank.hip for bf16/fp16
 // codes, decode_quant.hip for 3.2-bit codes): LDS access helpers, the global->LDS page
-// copies and their schedule over an iteration, and the partial-logit row map.
+// copies and their schedule over an iteration, and the page-loop state.
 //
 // Page buffers. A workgroup keeps NBUF page buffers (three: pages j, j + 1, j + 2 in
 // flight; two for pages too large to fit three times) interleaved at 1 KB: chunk c of
@@ -158,21 +158,6 @@ __device__ __forceinline__ void copies_at(int pos, const DmaConst& dc, const Dma
         if (copy_point<S, NLD>(c, 0) == pos && wave < NWAVE / 2) dma_one<B, NBUF>(dc, d, c, wave, doff[c]);
         if (copy_point<S, NLD>(c, 1) == pos && wave >= NWAVE / 2) dma_one<B, NBUF>(dc, d, c, wave, doff[c]);
     }
-}
-
-// Row of the wave's partial-logit table that slot s writes: with every head at <= 4
-// slots (`fast`), head k's j-th slot goes to row 4 k + j, so a head's rows past its
-// slots stay zero and the softmax sums 4 fixed rows; otherwise row s. Slots past the
-// wave's tiles write the spare row MAX_SLOTS.
-__device__ __forceinline__ int slot_row(cint_p pw, int s, int ntw, int nh, bool fast) {
-    if (s >= ntw) return MAX_SLOTS;
-    if (!fast) return s;
-    int row = MAX_SLOTS;
-    for (int k = 0; k < nh; ++k) {
-        const int f = pw[40 + k], c = pw[48 + k];
-        if (s >= f && s < f + c) row = 4 * k + (s - f);
-    }
-    return row;
 }
 
 // Page-loop state of a workgroup: the page being computed (cc), the page whose copies

@@ -134,27 +134,6 @@ __device__ __forceinline__ float q_outlier(const QDec& t, uint2 m) {
     return dot2(as_h2(h2_bits(t.xa) & m.x), t.za, dot2_0(as_h2(h2_bits(t.xb) & m.y), t.zb));
 }
 
-// Plan slot of kernel slot i. The kernel orders a wave's slots as the first tile of each
-// of its heads (with nout <= 16, the only tiles holding outlier ranks), then the other
-// tiles in plan order; slots past the wave's tiles map to themselves.
-__device__ __forceinline__ int kslot(cint_p pw, int nh, int ntw, int i) {
-    if (i >= ntw) return i;
-    int nf = 0;
-    for (int k = 0; k < nh; ++k) {
-        if (pw[48 + k] > 0) {
-            if (nf == i) return pw[40 + k];
-            ++nf;
-        }
-    }
-    int j = i - nf;
-    for (int k = 0; k < nh; ++k) {
-        const int c = pw[48 + k] > 0 ? pw[48 + k] - 1 : 0;
-        if (j < c) return pw[40 + k] + 1 + j;
-        j -= c;
-    }
-    return i;
-}
-
 // Per-slot wave-uniform values packed into SGPR words (8 bits per slot, 4 per word) and
 // re-read through an opaque SGPR, so they are not unpacked into SGPRs held across the
 // loop: the tile of each kernel slot, the outlier ranks of its tile, its local head.
@@ -234,27 +213,18 @@ __device__ __forceinline__ void q_kside(const DecodeParams& p, const QLane<MTV, 
     if (ntw > MTV) {  // slots past MTV: AB from the workspace (L2) on every page
         const int lr = lane & 15;
         cint_p pw = (cint_p)(p.ws + p.ws_plan) + wave * PLAN_STRIDE;
-        cint_p tiles = (cint_p)(p.ws + p.ws_tiles);
         const half8_t* abg = (const half8_t*)(p.ws + p.ws_ab + (size_t)cur_b * p.TT * AB_TILE_BYTES);
         for (int i = MTV; i < ntw; ++i) {
-            const int s = kslot(pw, nh, ntw, i);
-            const int t = pw[8 + s];
+            const uint32_t wd = (uint32_t)pw[PW_SLOTS + i];
+            const int t = sw_tile(wd), c = sw_nout(wd);
             half8_t a[4];
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) a[ks] = abg[(t * 4 + ks) * 64 + lane];
-            const int Tc = tiles[4 * t + 1] >> 4;
-            const int c = min((tiles[4 * t + 2] >> 8) & 255, 16);
-            const uint32_t ka = base + row_byte(8 * Tc, lr) + B * 1024;
+            const uint32_t ka = base + row_byte(8 * sw_code(wd), lr) + B * 1024;
             const QDec td = q_decode(mfma_tile(a, csb), lds_ld2(ka), la.sel, la.magic);
             const float r = sum_rows(td.d);
-            const int row = slot_row(pw, s, ntw, nh, fast);
-            if (lane < 16) lds_st<float>(sp + (uint32_t)(row * TILE_TOK + lr) * 4, r);
-            if (c != 0) {
-                int k = 0;  // the tile's local head
-                for (int h = 0; h < nh; ++h)
-                    if (s >= pw[40 + h] && s < pw[40 + h] + pw[48 + h]) k = h;
-                q_add_outlier(q_outlier(td, lds_ld2(la.mk + (uint32_t)c * 32u)), sp, k, lane);
-            }
+            if (lane < 16) lds_st<float>(sp + (uint32_t)(sw_row(wd) * TILE_TOK + lr) * 4, r);
+            if (c != 0) q_add_outlier(q_outlier(td, lds_ld2(la.mk + (uint32_t)c * 32u)), sp, sw_head(wd), lane);
         }
         __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): no tracked load left pending
     }
@@ -507,34 +477,28 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
     cint_p pw = plan + wave * PLAN_STRIDE;
     const int ntw = pw[0], nh = pw[1];
-    bool fast = true;
-    for (int k = 0; k < nh; ++k) fast = fast && pw[48 + k] <= 4;
+    const bool fast = pw[3] != 0;
     const uint32_t base = lds_addr(s_pages);
     const uint32_t sp = lds_addr(&s_part[wave][0]);
     const int O4 = (p.v_nout + 3) & ~3;
     const uint32_t vt0 = base + (uint32_t)(p.nch * PAGE_STRIDE);  // V table
     QLane<MTV, NB> la;
     SlotPack<MTV> sp8;
-    bool gen = false;  // some kernel slot other than a head's first tile holds outlier ranks
-    int nf = 0;        // heads with tiles: kernel slots 0 .. nf - 1 are their first tiles
-    for (int k = 0; k < nh; ++k) nf += pw[48 + k] > 0;
+    bool gen = false;         // some kernel slot other than a head's first tile holds outlier ranks
+    const int nf = pw[2];     // heads with tiles: kernel slots 0 .. nf - 1 are their first tiles
+    uint32_t swd[MTV];        // the wave's slot words, in this kernel's order
+#pragma unroll
+    for (int i = 0; i < MTV; ++i) swd[i] = (uint32_t)pw[PW_SLOTS + i];
     {
 #pragma unroll
         for (int w = 0; w < (MTV + 3) / 4; ++w) sp8.tile[w] = sp8.nout[w] = sp8.head[w] = 0;
-        cint_p tiles = (cint_p)(p.ws + p.ws_tiles);
 #pragma unroll
         for (int i = 0; i < MTV; ++i) {
-            const int t = pw[8 + kslot(pw, nh, ntw, i)];  // slots past the wave's tiles: tile 0
-            const int Tc = tiles[4 * t + 1] >> 4;  // code tile: first cache lane / 16
-            la.k[i] = vgpr_pin(base + row_byte(8 * Tc, lr));
-            const int c = i < ntw ? min((tiles[4 * t + 2] >> 8) & 255, 16) : 0;
-            sp8.tile[i / 4] |= (uint32_t)t << (8 * (i % 4));
+            la.k[i] = vgpr_pin(base + row_byte(8 * sw_code(swd[i]), lr));
+            const int c = sw_nout(swd[i]);
+            sp8.tile[i / 4] |= (uint32_t)sw_tile(swd[i]) << (8 * (i % 4));
             sp8.nout[i / 4] |= (uint32_t)c << (8 * (i % 4));
-            int hk = 0;  // local head of the slot's tile
-            const int s = kslot(pw, nh, ntw, i);
-            for (int k = 0; k < nh; ++k)
-                if (s >= pw[40 + k] && s < pw[40 + k] + pw[48 + k]) hk = k;
-            sp8.head[i / 4] |= (uint32_t)hk << (8 * (i % 4));
+            sp8.head[i / 4] |= (uint32_t)sw_head(swd[i]) << (8 * (i % 4));
             gen = gen || (i >= nf && c > 0);
         }
 #pragma unroll
@@ -542,17 +506,19 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
         const int rslot = ((lg & 1) << 1) | (lg >> 1);  // sum_rows4 puts inputs (a, b, c, d) in rows (0, 2, 1, 3)
 #pragma unroll
         for (int g = 0; g < (MTV + 3) / 4; ++g) {
-            const int s = 4 * g + rslot;
-            const int row = s < MTV ? slot_row(pw, kslot(pw, nh, ntw, s), ntw, nh, fast) : MAX_SLOTS;
+            int row = MAX_SLOTS;  // the row of kernel slot 4 g + rslot (past MTV: the spare row)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (4 * g + j < MTV && rslot == j) row = sw_row(swd[4 * g + j < MTV ? 4 * g + j : 0]);
             la.st[g] = sp + (uint32_t)(row * TILE_TOK + lr) * 4;
         }
         la.sm = sp + (uint32_t)(4 * lg * TILE_TOK + lr) * 4;
         la.ksm = base + row_byte(p.ks_off + 4 * (lg < nh ? pw[32 + lg] : 0), lr);
         {  // the outlier-dot row of kernel slot rslot (0 .. 3): its tile's head
             int hk = 0;
-            const int s = kslot(pw, nh, ntw, rslot);
-            for (int k = 0; k < nh; ++k)
-                if (s >= pw[40 + k] && s < pw[40 + k] + pw[48 + k]) hk = k;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (rslot == j) hk = sw_head(swd[j]);
             la.so = sp + (uint32_t)(((rslot < nf ? Q_EROW + 4 * hk : MAX_SLOTS)) * TILE_TOK + lr) * 4;
         }
         la.pw = lds_addr(&s_pq[wave][0][0]) + (uint32_t)(lg * TILE_TOK + lr) * 2;
