@@ -16,6 +16,12 @@
 //                     hit distinct banks
 //   4 .. 4+2NB-1      V codes, row t at t * NB * 128 B (columns past v_rank unused)
 //   4+2NB+m           K codes of code tiles 2m (at +0) and 2m+1 (at +512), row r at +32 r
+//   nch .. nch+2NB-1  (not copied) the page's V transposed into the P @ V B operand:
+//                     entry (step s, column L) is 4 tokens x 16 bit at byte (s 64 NB + L) 8
+// After the barrier of page j every thread moves two V codes of one token into that
+// table, and page j's P @ V runs one page later, one 4-token step per K tile, so its
+// reads and MFMAs ride under the next page's K side (the table survives the copies that
+// refill the page's buffer).
 // Copy i of wave w moves chunk 8 i + w; lane q's offset inside the page depends only on
 // (chunk, q) and is computed once (`doff`). Copies past the page's chunks land in a
 // 1 KB dummy block after the buffers and read nothing.
@@ -38,29 +44,37 @@ struct LrChunks {
 };
 
 // Per-lane LDS byte addresses (buffer 0), fixed for the whole kernel.
-template <int MTV>
+template <int MTV, int NB>
 struct LaneAddr {
     uint32_t cs[4];               // B operand: row lr, granule 4 ks + lg
     uint32_t k[MTV];              // slot i: 8 code bytes of row lr, ranks 4 lg .. 4 lg + 3
-    uint32_t v;                   // V: column lane of row 0
+    uint32_t vt;                  // V table entry (0, lane)
+    uint32_t cv_rd[NB], cv_wr[NB];  // V transpose: the two codes read, the entry written
     uint32_t st[(MTV + 3) / 4];   // partial-logit row of this lane's slot in each group of 4
     uint32_t sm;                  // softmax: first of the 4 rows of head lane >> 4
     uint32_t pw, pr;              // P: write (head lane >> 4, token lane & 15), read (head lane & 3)
     uint32_t base;                // the page buffers (wave-uniform)
 };
 
-// Copy points of an iteration: 0 right after the barrier, 1 .. MTV after each K tile,
-// MTV + 1 after the softmax, MTV + 2 .. MTV + 5 after each P @ V step.
+// Copy points of an iteration: 0 right after the barrier, 1 .. MTV after each K tile
+// (which also carry the previous page's P @ V), MTV + 1 after the softmax.
 template <int MTV>
 struct LrSched {
-    static constexpr int NPOS = MTV + 6;
+    static constexpr int NPOS = MTV + 2;
     static constexpr float time(int pos) {
-        return pos == 0 ? 0.f
-               : pos <= MTV ? 0.6f * (float)pos / (float)MTV
-               : pos == MTV + 1 ? 0.75f
-                                : 0.75f + 0.0625f * (float)(pos - MTV - 1);
+        return pos == 0 ? 0.f : pos <= MTV ? 0.75f * (float)pos / (float)MTV : 0.9f;
     }
 };
+
+// Byte offset of V-table entry (step s, column L) from the table's first chunk.
+template <int NBUF>
+__device__ __forceinline__ uint32_t vt_offset(int logical) {
+    return (uint32_t)((logical >> 10) * page_stride<NBUF>() + (logical & 1023));
+}
+template <int NB, int NBUF>
+constexpr uint32_t vt_step_offset(int s, int nb) {  // entry (s, 64 nb) for lane 0
+    return (uint32_t)(((s * NB + nb) >> 1) * page_stride<NBUF>() + ((s * NB + nb) & 1) * 512);
+}
 
 // z . codes for one tile: this lane's 4 z values (rows 4 lg .. 4 lg + 3) times its 4
 // codes (8 bytes).
@@ -78,10 +92,12 @@ __device__ __forceinline__ float tile_dot(const f32x4_t& z, uint2 w) {
 
 // K side of one page (buffer B): MTV slots from VGPR AB, more from L2. Each group of
 // 4 slots is summed over the row groups with the lane swaps and stored as 4 rows.
-template <int FMT, int MTV, int NB, int B, int NLD, int BN, int NBUF>
-__device__ __forceinline__ void k_side(const DecodeParams& p, const LaneAddr<MTV>& la, const half8_t (&ab)[MTV][4],
+// `hook(i)` runs after tile i's lane work (i a constant once the loop is unrolled).
+template <int FMT, int MTV, int NB, int B, int NLD, int BN, int NBUF, class Hook>
+__device__ __forceinline__ void k_side(const DecodeParams& p, const LaneAddr<MTV, NB>& la, const half8_t (&ab)[MTV][4],
                                        int ntw, int nh, bool fast, uint32_t sp, int lane, int wave, int cur_b,
-                                       const DmaConst& dc, const DmaPage& dp, const uint32_t (&doff)[NLD]) {
+                                       const DmaConst& dc, const DmaPage& dp, const uint32_t (&doff)[NLD],
+                                       Hook&& hook) {
     half8_t csb[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) csb[ks] = lds_ld<half8_t>(la.cs[ks] + B * 1024);
@@ -90,6 +106,7 @@ __device__ __forceinline__ void k_side(const DecodeParams& p, const LaneAddr<MTV
     for (int i = 0; i < MTV; ++i) {
         const f32x4_t z = mfma_tile(ab[i], csb);
         v[i & 3] = tile_dot<FMT>(z, lds_ld2(la.k[i] + B * 1024));
+        hook(i);
         if ((i & 3) == 3 || i == MTV - 1) {
             const float r = sum_rows4(v[0], (i & 3) >= 1 ? v[1] : 0.f, (i & 3) >= 2 ? v[2] : 0.f,
                                       (i & 3) >= 3 ? v[3] : 0.f);
@@ -157,23 +174,53 @@ __device__ __forceinline__ bool softmax_page(SmState& sm, const uint32_t sm_addr
     return moved;
 }
 
-// Two 16-bit V codes (rows t0, t1 of column lane) packed into one word.
-__device__ __forceinline__ uint32_t v_pair(uint32_t a0, uint32_t a1) {
-    short2_t x;
-    x.x = lds_ld<short>(a0);
-    x.y = lds_ld<short>(a1);
-    return __builtin_bit_cast(uint32_t, x);
+// Moves this thread's two V codes of one token (the word xv[k], columns 2 c, 2 c + 1)
+// into the V table of buffer B.
+template <int NB, int B>
+__device__ __forceinline__ void lr_transpose_v(const uint32_t (&xv)[NB], const uint32_t (&wr)[NB]) {
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+        lds_st<uint16_t>(wr[k] + B * 1024, (uint16_t)xv[k]);
+        lds_st<uint16_t>(wr[k] + B * 1024 + 8, (uint16_t)(xv[k] >> 16));
+    }
 }
 
-// acc[nb] = alpha * acc[nb] + P[4 heads, 16 tokens] @ V[16 tokens, 64 columns] on
-// v_mfma_f32_4x4x4_16b with block 0's A broadcast (cbsz 4): per 4-token step lanes 0..3
-// hold P[head l][4 tokens], lane l holds V[4 tokens][column 64 nb + l], and the result
-// lands in lane l as acc[nb][head] for its column.
-template <int FMT, int NB, int B, int MTV, int NLD, int BN, int NBUF>
-__device__ __forceinline__ void pv_page(f32x4_t (&acc)[NB], uint32_t v_addr, uint32_t pr_addr, uint32_t plo_off,
-                                        uint32_t salpha, bool rescale, const DmaConst& dc, const DmaPage& dp,
-                                        int wave, const uint32_t (&doff)[NLD]) {
-    typedef LrChunks<NB> C;
+// One 4-token step of acc[nb] += P[4 heads, 16 tokens] @ V[16 tokens, 64 columns] on
+// v_mfma_f32_4x4x4_16b with block 0's A broadcast (cbsz 4): lanes 0..3 hold P[head l]
+// [4 tokens] (bf16: a high and a low part), lane l holds V[4 tokens][column 64 nb + l],
+// and the result lands in lane l as acc[nb][head] for its column. The operands are read
+// one K tile before the MFMAs that use them.
+template <int NB>
+struct PvStep {
+    uint2 ph, pl, b[NB];
+};
+template <int FMT, int NB, int B, int NBUF>
+__device__ __forceinline__ void pv_load(PvStep<NB>& q, uint32_t pr, uint32_t plo_off, uint32_t vt, int s) {
+    q.ph = lds_ld2(pr + 8 * s);
+    if (FMT == FMT_BF16) q.pl = lds_ld2(pr + plo_off + 8 * s);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) q.b[nb] = lds_ld2(vt + vt_step_offset<NB, NBUF>(s, nb) + B * 1024);
+}
+template <int FMT, int NB>
+__device__ __forceinline__ void pv_mfma(f32x4_t (&acc)[NB], const PvStep<NB>& q) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        if (FMT == FMT_BF16) {
+            acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(short4_t, q.ph),
+                                                             __builtin_bit_cast(short4_t, q.b[nb]), acc[nb], 4, 0, 0);
+            acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(short4_t, q.pl),
+                                                             __builtin_bit_cast(short4_t, q.b[nb]), acc[nb], 4, 0, 0);
+        } else {
+            acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, q.ph),
+                                                         __builtin_bit_cast(half4_t, q.b[nb]), acc[nb], 4, 0, 0);
+        }
+    }
+}
+
+// The whole P @ V of the page whose V table is in buffer B (the last page, after the loop).
+template <int FMT, int NB, int NBUF>
+__device__ __forceinline__ void pv_page(f32x4_t (&acc)[NB], uint32_t pr, uint32_t plo_off, uint32_t vt,
+                                        uint32_t salpha, bool rescale) {
     if (rescale) {
         const f32x4_t al = lds_ld<f32x4_t>(salpha);
 #pragma unroll
@@ -182,46 +229,35 @@ __device__ __forceinline__ void pv_page(f32x4_t (&acc)[NB], uint32_t v_addr, uin
             for (int e = 0; e < 4; ++e) acc[nb][e] *= al[e];
     }
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-        const uint2 pa = lds_ld2(pr_addr + 8 * st);
-        const uint2 pl = FMT == FMT_BF16 ? lds_ld2(pr_addr + plo_off + 8 * st) : make_uint2(0, 0);
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            uint32_t off[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int byte = (4 * st + e) * C::VPITCH + 128 * nb;  // inside the V region
-                off[e] = (uint32_t)((byte >> 10) * page_stride<NBUF>() + (byte & 1023) + B * 1024);
-            }
-            const uint2 bv = make_uint2(v_pair(v_addr + off[0], v_addr + off[1]), v_pair(v_addr + off[2], v_addr + off[3]));
-            if (FMT == FMT_BF16) {
-                acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(short4_t, pa),
-                                                                 __builtin_bit_cast(short4_t, bv), acc[nb], 4, 0, 0);
-                acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(short4_t, pl),
-                                                                 __builtin_bit_cast(short4_t, bv), acc[nb], 4, 0, 0);
-            } else {
-                acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, pa),
-                                                             __builtin_bit_cast(half4_t, bv), acc[nb], 4, 0, 0);
-            }
-        }
-        if (st == 0) copies_at<LrSched<MTV>, NLD, BN, NBUF>(MTV + 2, dc, dp, opaque_s(wave), doff);
-        if (st == 1) copies_at<LrSched<MTV>, NLD, BN, NBUF>(MTV + 3, dc, dp, opaque_s(wave), doff);
-        if (st == 2) copies_at<LrSched<MTV>, NLD, BN, NBUF>(MTV + 4, dc, dp, opaque_s(wave), doff);
-        if (st == 3) copies_at<LrSched<MTV>, NLD, BN, NBUF>(MTV + 5, dc, dp, opaque_s(wave), doff);
+    for (int s = 0; s < 4; ++s) {
+        PvStep<NB> q;
+        pv_load<FMT, NB, 0, NBUF>(q, pr, plo_off, vt, s);
+        pv_mfma<FMT, NB>(acc, q);
     }
 }
 
-// One page of the loop: buffer BC holds page j (copied two pages ago); buffer BN
-// receives page j + 2 (page j - 1, its previous content, is done on every wave once the
-// barrier is passed).
+struct LrLoop : PageLoop {
+    bool pv_moved;  // the previous page's softmax moved a reference max
+    bool pv_end;    // the previous page ended its request: flush after its P @ V
+    int pv_b;       // its request
+    int pv_buf;     // its buffer, when the loop ends
+};
+
+// One page of the loop: buffer BC holds page j (copied NBUF - 1 pages ago); buffer BN
+// receives page j + NBUF - 1 (its previous content, page j - 1, is done on every wave
+// once the barrier is passed, except page j - 1's V table, which this iteration's P @ V
+// reads and the copies do not touch).
 template <int FMT, int MTV, int NB, int NLD, int BC, int BN, int NBUF>
-__device__ __forceinline__ bool lr_iter(PageLoop& st, const DmaConst& dc, const LaneAddr<MTV>& la,
+__device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const LaneAddr<MTV, NB>& la,
                                         half8_t (&ab)[MTV][4], f32x4_t (&acc)[NB], SmState& sm,
                                         const uint32_t (&doff)[NLD], int ntw, int nh, bool fast, uint32_t sp,
                                         uint32_t plo_off, uint32_t salpha, const int* sqh, int lane, int wave) {
     const DecodeParams& p = params();
     cint_p P = (cint_p)(p.ws + 4);
-    if (!st.cc.valid) return false;
+    if (!st.cc.valid) {
+        st.pv_buf = BN;  // the last page's buffer: its P @ V runs after the loop
+        return false;
+    }
     const Cursor cc = st.cc;
     if (st.new_seg) {
         // This request's AB into registers; slots past the wave's tiles load tile 0.
@@ -236,18 +272,40 @@ __device__ __forceinline__ bool lr_iter(PageLoop& st, const DmaConst& dc, const 
         __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0)
     }
     SKV_WAIT_VM_LGKM0(NBUF == 3 ? NLD : 0);  // only the copies of page j + 1 may still be in flight
-    lds_barrier();           // page j is in LDS; every wave is done with page j - 1
+    lds_barrier();  // page j is in LDS, page j - 1's V table is complete; every wave is done with page j - 1
     const DmaPage dp = dma_setup(dc, st.ld, st.nblk);
+    // Page j's V codes for the transpose, read first; page j - 1's P @ V (its P was 0
+    // before the first page) runs inside the K side: its rescale first, then one step
+    // per tile.
+    uint32_t xv[NB];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) xv[k] = lds_ld<uint32_t>(la.cv_rd[k] + BC * 1024);
+    if (st.pv_moved) {
+        const f32x4_t al = lds_ld<f32x4_t>(salpha);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[nb][e] *= al[e];
+    }
     copies_at<LrSched<MTV>, NLD, BN, NBUF>(0, dc, dp, opaque_s(wave), doff);
     if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
-    k_side<FMT, MTV, NB, BC, NLD, BN, NBUF>(p, la, ab, ntw, nh, fast, sp, lane, wave, cc.b, dc, dp, doff);
-    const bool moved = softmax_page<FMT>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, TILE_TOK * cc.k,
-                                         cc.lo, cc.hi);
+    PvStep<NB> pq;
+    auto hook = [&](int i) {
+        if (i == 0) lr_transpose_v<NB, BC>(xv, la.cv_wr);
+        if (i >= 1 && i <= 4) pv_mfma<FMT, NB>(acc, pq);
+        if (i <= 3) pv_load<FMT, NB, BN, NBUF>(pq, la.pr, plo_off, la.vt, i);
+    };
+    k_side<FMT, MTV, NB, BC, NLD, BN, NBUF>(p, la, ab, ntw, nh, fast, sp, lane, wave, cc.b, dc, dp, doff, hook);
+#pragma unroll
+    for (int i = MTV; i <= 4; ++i) hook(i);  // the P @ V steps a short K side left
+    if (st.pv_end) flush_partial<NB>(p, sm, acc, nh, st.pv_b + st.g, sqh, lane);
+    st.pv_moved = softmax_page<FMT>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, TILE_TOK * cc.k, cc.lo,
+                                    cc.hi);
     copies_at<LrSched<MTV>, NLD, BN, NBUF>(MTV + 1, dc, dp, opaque_s(wave), doff);
-    pv_page<FMT, NB, BC, MTV, NLD, BN, NBUF>(acc, la.v, la.pr, plo_off, salpha, moved, dc, dp, wave, doff);
     Cursor nx = cc;
     const bool seg_end = cur_next(nx, P, p.n, st.beg, st.end);
-    if (seg_end) flush_partial<NB>(p, sm, acc, nh, cc.b + st.g, sqh, lane);
+    st.pv_end = seg_end;
+    st.pv_b = cc.b;
     st.cc = nx;
     st.new_seg = seg_end;
     // The block of the page the next iteration copies: its load completes under the
@@ -272,7 +330,7 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     cint_p P = (cint_p)(p.ws + 4);
     cint_p plan = (cint_p)(p.ws + p.ws_plan);
     if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
-    PageLoop st;
+    LrLoop st;
     st.g = blockIdx.x;
     const int S_tok = ((cint_p)p.ws)[0];
     const int T = P[p.n];
@@ -286,6 +344,10 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     for (int i = tid; i < p.lds_bytes / 16; i += NTHR) ((uint4*)s_pages)[i] = make_uint4(0, 0, 0, 0);
     for (int i = tid; i < NWAVE * (MAX_SLOTS + 1) * TILE_TOK; i += NTHR) (&s_part[0][0])[i] = 0.f;
     if (tid < NWAVE * 4) (&s_alpha[0][0])[tid] = 1.f;
+    for (int i = tid; i < NWAVE * 4 * TILE_TOK; i += NTHR) {  // P before the first page
+        (&s_p[0][0])[i] = 0;
+        if (FMT == FMT_BF16) (&s_plo[0][0])[i] = 0;
+    }
 
     // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
     cint_p pw = plan + wave * PLAN_STRIDE;
@@ -293,7 +355,7 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     const bool fast = pw[3] != 0;
     const uint32_t base = lds_addr(s_pages);
     const uint32_t sp = lds_addr(&s_part[wave][0]);
-    LaneAddr<MTV> la;
+    LaneAddr<MTV, NB> la;
     uint32_t swd[MTV];  // the wave's slot words (plan order), read with a few wide scalar loads
 #pragma unroll
     for (int i = 0; i < MTV; ++i) swd[i] = (uint32_t)pw[PW_SLOTS + i];
@@ -306,8 +368,18 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
             la.cs[ks] = base + cs_read_offset<NBUF>(ks, lg, lr);
-        la.v = base + (uint32_t)(C::V0 * page_stride<NBUF>() + 2 * lane);
         la.base = base;
+        const uint32_t vt0 = base + (uint32_t)(p.nch * page_stride<NBUF>());  // V table
+        la.vt = vt0 + 8 * lane;
+        // V transpose: token t = tid % 16, columns L, L + 1 with L = 2 (tid / 16) + 64 k.
+        const int t = tid & 15;
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            const int L = 2 * (tid >> 4) + 64 * k;
+            const int vb = t * C::VPITCH + 2 * L;  // byte inside the V rows
+            la.cv_rd[k] = base + (uint32_t)((C::V0 + (vb >> 10)) * page_stride<NBUF>() + (vb & 1023));
+            la.cv_wr[k] = vt0 + vt_offset<NBUF>((((t >> 2) * 64 * NB + L) << 3) + (t & 3) * 2);
+        }
         const int rslot = ((lg & 1) << 1) | (lg >> 1);  // sum_rows4 puts inputs (a, b, c, d) in rows (0, 2, 1, 3)
 #pragma unroll
         for (int g = 0; g < (MTV + 3) / 4; ++g) {
@@ -348,12 +420,16 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
         }
         doff[i] = off;
     }
-    const DmaConst dc = dma_const<NBUF>(p, base, wave, base + (uint32_t)(p.nch * page_stride<NBUF>()));
+    const DmaConst dc = dma_const<NBUF>(p, base, wave, base + (uint32_t)((p.nch + 2 * NB) * page_stride<NBUF>()));
     __syncthreads();
 
     cur_first(st.cc, P, p.n, st.beg, st.end);
     st.ld = st.cc;
     st.new_seg = true;
+    st.pv_moved = false;
+    st.pv_end = false;
+    st.pv_b = 0;
+    st.pv_buf = 0;
     dma_page<NLD, 0, NBUF>(dc, st.ld, page_block(dc, st.ld), wave, doff);
     cur_next(st.ld, P, p.n, st.beg, st.end);
     if (NBUF == 3) {
@@ -389,7 +465,11 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
                 break;
         }
     }
-    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): no copy may land after the workgroup ends
+    // The last page's P @ V, once its V table is visible to every wave.
+    SKV_WAIT_VM_LGKM0(0);  // also: no copy may land after the workgroup ends
+    lds_barrier();
+    pv_page<FMT, NB, NBUF>(acc, la.pr, plo_off, la.vt + (uint32_t)st.pv_buf * 1024u, salpha, st.pv_moved);
+    flush_partial<NB>(p, sm, acc, nh, st.pv_b + st.g, sqh, lane);
 }
 
 template <int FMT, int MTV, int NLD, int NBUF>
@@ -422,11 +502,11 @@ int lowrank_chunks(int k_width, int nb) {
     return CS_CHUNKS + 2 * nb_blocks(nb) + (tiles + 1) / 2;
 }
 
-// Page buffers: three while a page's chunks fit three times (up to 48), else two (up to
-// 64); 0 if a page does not fit.
+// Page buffers: three while a page's copied chunks and its V table fit three times (48
+// chunks), else two (up to 64 copied chunks); 0 if a page does not fit.
 int lowrank_buffers(int k_width, int nb) {
-    const int ch = lowrank_chunks(k_width, nb);
-    return ch <= 6 * NWAVE ? 3 : ch <= 8 * NWAVE ? 2 : 0;
+    const int ch = lowrank_chunks(k_width, nb), all = ch + 2 * nb_blocks(nb);
+    return all <= 48 && ch <= 6 * NWAVE ? 3 : ch <= 8 * NWAVE && all <= 72 ? 2 : 0;
 }
 
 // Copies per wave per page (the instantiated counts: 3 or 6 with three buffers, 8 with
@@ -438,7 +518,7 @@ int lowrank_copies(int k_width, int nb) {
 }
 
 int lowrank_lds_bytes(int k_width, int nb) {
-    return lowrank_chunks(k_width, nb) * lowrank_buffers(k_width, nb) * 1024 + 1024;
+    return (lowrank_chunks(k_width, nb) + 2 * nb_blocks(nb)) * lowrank_buffers(k_width, nb) * 1024 + 1024;
 }
 
 // Rank tiles per wave held in VGPRs: the wave plan balances whole heads to within a
