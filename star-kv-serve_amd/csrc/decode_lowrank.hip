@@ -363,7 +363,8 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
 #pragma unroll
         for (int i = 0; i < MTV; ++i) {
             const int Tc = sw_code(swd[i]);  // code tile: first cache lane / 16
-            la.k[i] = base + (uint32_t)((C::K0 + (Tc >> 1)) * page_stride<NBUF>() + (Tc & 1) * 512 + lr * 32 + 8 * lg);
+            la.k[i] = vgpr_pin(base + (uint32_t)((C::K0 + (Tc >> 1)) * page_stride<NBUF>() + (Tc & 1) * 512 +
+                                                 lr * 32 + 8 * lg));
         }
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
@@ -392,6 +393,20 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
         la.sm = sp + (uint32_t)(4 * lg * TILE_TOK + lr) * 4;
         la.pw = lds_addr(&s_p[wave][0]) + (uint32_t)(lg * TILE_TOK + lr) * 2;
         la.pr = lds_addr(&s_p[wave][0]) + (uint32_t)(lane & 3) * TILE_TOK * 2;
+        // Whole-VGPR lane addresses (see vgpr_pin).
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) la.cs[ks] = vgpr_pin(la.cs[ks]);
+#pragma unroll
+        for (int g = 0; g < (MTV + 3) / 4; ++g) la.st[g] = vgpr_pin(la.st[g]);
+        la.sm = vgpr_pin(la.sm);
+        la.pw = vgpr_pin(la.pw);
+        la.pr = vgpr_pin(la.pr);
+        la.vt = vgpr_pin(la.vt);
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            la.cv_rd[k] = vgpr_pin(la.cv_rd[k]);
+            la.cv_wr[k] = vgpr_pin(la.cv_wr[k]);
+        }
     }
     const uint32_t plo_off = lds_addr(&s_plo[FMT == FMT_BF16 ? wave : 0][0]) - lds_addr(&s_p[wave][0]);
     const uint32_t salpha = lds_addr(&s_alpha[wave][0]);
