@@ -160,6 +160,13 @@ __device__ __forceinline__ void copies_at(int pos, const DmaConst& dc, const Dma
     }
 }
 
+// The token range of workgroup x. Workgroups are dealt to the 8 XCDs round-robin (x % 8);
+// consecutive ranges, which mostly hold one request's pages, go to one XCD, so that the
+// request's AB tiles are read into one L2 and shared there.
+__device__ __forceinline__ int xcd_range(int x, int grid) {
+    return grid % 8 == 0 ? (x % 8) * (grid / 8) + x / 8 : x;
+}
+
 // Page-loop state of a workgroup: the page being computed (cc), the page whose copies
 // issue next (ld, two pages ahead) and its cache block, loaded one page ahead.
 struct PageLoop {

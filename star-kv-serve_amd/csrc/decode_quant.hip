@@ -453,7 +453,7 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     cint_p plan = (cint_p)(p.ws + p.ws_plan);
     if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
     QLoop st;
-    st.g = blockIdx.x;
+    st.g = xcd_range(blockIdx.x, gridDim.x);
     const int S_tok = ((cint_p)p.ws)[0];
     const int T = P[p.n];
     st.beg = min(st.g * S_tok, T);
