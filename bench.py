@@ -7,9 +7,10 @@ is the reference metric's configuration: bf16/low-rank codes, batch 64, every
 request at 8192 tokens of context, 32 heads x head_dim 128, page size 16, K ranks
 per head drawn from {16, 32, 48, 64}, V rank 64, physical pages shuffled. The cache
 (1.4 GB) is larger than the 256 MB Infinity Cache, so every step streams it from
-HBM. `value` = algorithmic bytes per step / wall time per step (whole call: setup,
-fold, decode and merge launches). `roofline.achieved` = the same bytes / the decode
-kernel's own average duration (HIP events around that launch). The 3.2-bit kernel
+HBM. `value` = algorithmic bytes per step / wall time per step (whole call: prep,
+decode and merge launches). `roofline.achieved` = the same bytes / the decode
+kernel's own average duration (HIP events around that launch, in a second pass of
+the same steps). The 3.2-bit kernel
 at the same shape (three rotating cache copies, 1.3 GB) and the ragged reference
 configurations are reported under "extra". `cpu_baseline` times the float64 CPU
 oracle on a bounded sample of the same workload on this host.
@@ -41,22 +42,28 @@ def log(*a):
 
 
 def time_steps(fn, steps, warmup):
-    """Warmup, then `steps` timed calls bracketed by synchronizes; returns
-    (ms per step, decode-kernel ms per call)."""
+    """Warmup, then `steps` timed calls bracketed by synchronizes (ms per step, the
+    whole call), then `steps` more calls with HIP events around each decode launch
+    (decode-kernel ms per call). The events sit in a pass of their own: each record
+    holds the stream for a few microseconds, which would count in the whole-call time."""
     import torch
     from starkv_serve import _hip
     for _ in range(warmup):
         fn(0)
     torch.cuda.synchronize()
-    _hip.profile_begin(steps)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for i in range(steps):
         fn(i)
     stop.record()
     torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    _hip.profile_begin(steps)
+    for i in range(steps):
+        fn(i)
+    torch.cuda.synchronize()
     kern_ms, calls = _hip.profile_end()
-    return start.elapsed_time(stop) / steps, kern_ms / max(calls, 1)
+    return ms, kern_ms / max(calls, 1)
 
 
 def bench_lowrank(lengths, steps, warmup, seed, v_rank=64):

@@ -6,15 +6,14 @@
 //                                                      kv_quant.py:42-50)
 //   out   = (softmax(logit) @ V_codes) @ v_up_by_q[h]  paged_decode.py:105-147, 220-226
 //
-// MI355X design, four launches per call (all grids are functions of host ints):
-// 1. setup: the per-16-lane rank-tile table, the prefix sums of the request lengths
-//    and the wave plan: whole query heads dealt to the 8 waves of a workgroup,
-//    largest first to the least loaded wave, so every wave owns a balanced set of
-//    rank tiles and every head lives in one wave.
-// 2. fold: AB for every (request, rank tile) in fp16, written in the A-operand lane
-//    order of v_mfma_f32_16x16x32_f16, so the decode kernel loads it straight into
-//    its final registers.
-// 3. decode: one persistent workgroup (8 waves) per CU. The requests' tokens are laid
+// MI355X design, three launches per call (all grids are functions of host ints):
+// 1. prep: workgroup 0 writes the prefix sums of the request lengths and the wave
+//    plan: whole query heads dealt to the 8 waves of a decode workgroup, so every wave
+//    owns a balanced set of rank tiles and every head lives in one wave. The other
+//    workgroups fold AB for every (request, rank tile) in fp16, written in the
+//    A-operand lane order of v_mfma_f32_16x16x32_f16, so the decode kernel loads it
+//    straight into its final registers.
+// 2. decode: one persistent workgroup (8 waves) per CU. The requests' tokens are laid
 //    end to end and cut into `grid` equal contiguous ranges, so every workgroup
 //    streams the same number of cache rows whatever the lengths are; a range that
 //    crosses a request boundary emits one split-K partial per request. A page is 16
@@ -32,31 +31,109 @@
 //    per-wave accumulators. decode_lowrank.hip holds the bf16/fp16 kernel and
 //    decode_quant.hip the 3.2-bit one, which folds the V scales into P and runs P @ V
 //    one page behind over a V table expanded once per page.
-// 4. merge: per (request, head) log-sum-exp of the partials, then the lift through
+// 3. merge: per (request, head) log-sum-exp of the partials, then the lift through
 //    v_up_by_q.
 #include <vector>
 
 #include "decode_common.hpp"
 
 namespace starkv {
+// ---------------------------------------------------------------------------
+// 1. prep: one launch of PREP_THR-thread workgroups. Workgroup 0 writes the prefix
+//    sums of the request lengths and the wave plan; every other workgroup folds AB for
+//    two rank tiles and up to PREP_REQ requests. Both read the rank-tile table, which
+//    each workgroup builds in LDS from the per-head ranks (bf16/fp16) or the per-tile
+//    arrays (3.2-bit).
+// ---------------------------------------------------------------------------
+constexpr int PREP_THR = 256;
+constexpr int PREP_REQ = 8;  // requests per fold workgroup
 
-// ---------------------------------------------------------------------------
-// 1. setup: tile table, prefix sums and wave plan. One workgroup of 1024 threads.
-// ---------------------------------------------------------------------------
+struct PrepArgs {
+    const int32_t* seq_lens;
+    int n, max_seq_len, grid, Hq, Hkv, TT, k_rows;
+    const int32_t* k_ranks; const int32_t* k_offsets;                       // bf16/fp16
+    const int32_t* t_head; const int32_t* t_nout; const int32_t* t_last;  // 3.2-bit (t_head set)
+    const void* q; int64_t q_s0, q_s1; int q_dt;
+    const void* k_up; int64_t ku_s0; int ku_dt;
+    float sc;  // scale * log2(e)
+    uint8_t* ws; size_t ws_plan, ws_ab;
+    int tile_pairs;  // ceil(TT / 2): fold workgroups per group of PREP_REQ requests
+};
+
+// Rank-tile table: per tile its query head, first k_up row, valid ranks (rows past them
+// fold to zero) and code word (slot_word's code tile | outlier ranks << 13); per query
+// head its first tile and tile count.
+struct TileTable {
+    int head[MAX_TT], row[MAX_TT], valid[MAX_TT], word[MAX_TT];
+    int hf[MAX_H], hn[MAX_H];
+    int rank[MAX_H], off[MAX_H];
+};
+
+// Fills `tt` (every thread of the workgroup calls it; it ends with a barrier).
+//   bf16/fp16: query head h (kv head h / (Hq / Hkv)) has ceil(rank / 16) tiles; the
+//     heads' tiles are laid out head after head, k_up rows from the kv head's offset.
+//   3.2-bit: tile t belongs to head t_head[t], k_up rows 16 t .. 16 t + 15 (lanes
+//     contiguous), outlier ranks t_nout[t].
+__device__ void tile_table(const PrepArgs& a, TileTable& tt, int tid) {
+    int h = 0, hp = -1, nout = 0;  // 3.2-bit: tile tid's head, tile tid - 1's head, outlier ranks
+    if (a.t_head) {
+        if (tid < a.TT) {
+            h = min(max(a.t_head[tid], 0), a.Hq - 1);
+            if (tid > 0) hp = min(max(a.t_head[tid - 1], 0), a.Hq - 1);
+            nout = min(max(a.t_nout[tid], 0), 16);
+        }
+    } else if (tid < a.Hkv) {
+        tt.rank[tid] = min(max(a.k_ranks[tid], 0), 16 * MAX_TT);
+        tt.off[tid] = a.k_offsets[tid];
+    }
+    if (tid < MAX_TT) {
+        tt.head[tid] = 0;
+        tt.row[tid] = 0;
+        tt.valid[tid] = 0;
+        tt.word[tid] = 0;
+    }
+    if (tid < MAX_H) {
+        tt.hf[tid] = 0;
+        tt.hn[tid] = 0;
+    }
+    __syncthreads();
+    if (a.t_head) {
+        if (tid < a.TT) {
+            tt.head[tid] = h;
+            tt.row[tid] = 16 * tid;
+            tt.valid[tid] = 16;
+            tt.word[tid] = tid | (nout << 13);
+            atomicAdd(&tt.hn[h], 1);
+            if (hp != h) tt.hf[h] = tid;  // a head's tiles are contiguous
+        }
+    } else if (tid < a.Hq) {
+        const int grp = a.Hq / a.Hkv, kv = tid / grp;
+        int t0 = 0;  // tiles of the query heads before this one: whole groups, then this group's
+        for (int k = 0; k < kv; ++k) t0 += grp * ((tt.rank[k] + 15) >> 4);
+        const int R = tt.rank[kv], o = tt.off[kv];
+        const int nt = (R + 15) >> 4;
+        t0 += (tid - kv * grp) * nt;
+        int cnt = 0;
+        for (int j = 0; j < nt && t0 + j < a.TT; ++j, ++cnt) {
+            tt.head[t0 + j] = tid;
+            tt.row[t0 + j] = min(max(o + 16 * j, 0), a.k_rows - 16);
+            tt.valid[t0 + j] = min(16, R - 16 * j);
+            tt.word[t0 + j] = (o >> 4) + j;
+        }
+        tt.hf[tid] = min(t0, a.TT);
+        tt.hn[tid] = cnt;
+    }
+    __syncthreads();
+}
+
 // Wave-level integer reductions with DPP (the wave plan's steps are chains of them).
 template <int CTL>
 __device__ __forceinline__ int dpp_i(int v) {
     return __builtin_amdgcn_update_dpp(0, v, CTL, 0xF, 0xF, true);
 }
 
-// Min / max over lanes 0 .. 7 (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror), as a
+// Max over lanes 0 .. 7 (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror), as a
 // wave-uniform value. Every lane of the wave must be active.
-__device__ __forceinline__ int lanes8_min(int v) {
-    v = min(v, dpp_i<0xB1>(v));
-    v = min(v, dpp_i<0x4E>(v));
-    v = min(v, dpp_i<0x141>(v));
-    return __builtin_amdgcn_readfirstlane(v);
-}
 __device__ __forceinline__ int lanes8_max(int v) {
     v = max(v, dpp_i<0xB1>(v));
     v = max(v, dpp_i<0x4E>(v));
@@ -74,124 +151,86 @@ __device__ __forceinline__ int wave_min_i(int v) {
     const int r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
     return min(min(r0, r1), min(r2, r3));
 }
-__global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__ seq_lens, int n, int max_seq_len,
-                                                     int grid, int Hq, int Hkv, int TT,
-                                                     const int32_t* __restrict__ k_ranks,
-                                                     const int32_t* __restrict__ k_offsets,
-                                                     const int32_t* __restrict__ t_head,
-                                                     const int32_t* __restrict__ t_nout,
-                                                     const int32_t* __restrict__ t_last, int qorder,
-                                                     uint8_t* __restrict__ ws, size_t ws_tiles, size_t ws_plan) {
-    __shared__ int s_wsum[16];
-    __shared__ int s_total;
-    __shared__ int s_hf[MAX_H], s_hn[MAX_H];
-    __shared__ int s_rank[MAX_H], s_off[MAX_H];        // k_ranks, k_offsets (bf16/fp16)
-    __shared__ int s_thead[MAX_TT], s_tmeta[MAX_TT];   // t_head, nout | last << 8 (3.2-bit)
-    __shared__ int s_tword[MAX_TT];                    // per tile: code tile | outlier ranks << 13
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int* hdr = (int*)ws;
-    int4* tiles = (int4*)(ws + ws_tiles);
-    int* plan = (int*)(ws + ws_plan);
 
-    // Every global input is read at once, up front: the steps below only use LDS.
-    const int a = tid < n ? min(max(seq_lens[tid], 0), max_seq_len) : 0;
-    if (t_head) {
-        if (tid < TT) {
-            s_thead[tid] = t_head[tid];
-            s_tmeta[tid] = t_nout[tid] | ((t_last[tid] != 0) << 8);
-        }
-    } else if (tid < Hkv) {
-        s_rank[tid] = k_ranks[tid];
-        s_off[tid] = k_offsets[tid];
+// Workgroup 0 of prep. Writes hdr[0] = tokens per decode workgroup, hdr[1 + b] = first
+// token of request b in the concatenation, and the plan: per wave (PLAN_STRIDE ints)
+// [0] its tiles, [1] its heads, [2] its heads with tiles, [3] whether every head of it
+// has at most 4 tiles, [8 + s] the tile of slot s, [32 + k], [40 + k], [48 + k] head k's
+// query head, first slot and tile count, [PW_SLOTS + s] the slot words; then one int,
+// 1 if the heads fit the waves (every wave at most MAX_SLOTS tiles).
+__device__ void prep_setup(const PrepArgs& a, const TileTable& tt, int tid, int (&v)[4]) {
+    __shared__ int s_wsum[PREP_THR / 64];
+    __shared__ int s_byp[MAX_H];   // query head at each position of the size order
+    __shared__ int s_load[NWAVE];  // tiles per decode wave
+    __shared__ int s_plan[NWAVE * PLAN_STRIDE + 1];
+    const int lane = tid & 63, wave = tid >> 6;
+    int* hdr = (int*)a.ws;
+
+    // Prefix sums of min(max(seq_len, 0), max_seq_len); thread tid takes requests
+    // 4 tid .. 4 tid + 3.
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[i] = min(max(v[i], 0), a.max_seq_len);
+        s += v[i];
     }
-
-    // Prefix sums of min(max(seq_len, 0), max_seq_len) over n <= 1024 requests.
-    int s = a;
+    int incl = s;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        int y = __shfl_up(s, o, 64);
-        if (lane >= o) s += y;
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
     }
-    if (lane == 63) s_wsum[wave] = s;
-    __syncthreads();
-    int off = 0;
-#pragma unroll
-    for (int w = 0; w < 16; ++w) off += w < wave ? s_wsum[w] : 0;
-    if (tid < n) hdr[2 + tid] = off + s;
-    if (tid == 0) hdr[1] = 0;
-    if (tid == 1023) s_total = off + s;
-
-    // Tile table and (first tile, tiles) per query head.
-    if (t_head) {  // 3.2-bit: the k_tables arrays, lanes contiguous, MHA
-        for (int t = tid; t < TT; t += blockDim.x) {
-            tiles[t] = make_int4(s_thead[t], 16 * t, 16 | ((s_tmeta[t] & 255) << 8) | ((s_tmeta[t] >> 8) << 16),
-                                 s_thead[t]);
-            s_tword[t] = t | (min(s_tmeta[t] & 255, 16) << 13);
-        }
-        if (tid < Hq) {
-            int first = -1, cnt = 0;
-            for (int t = 0; t < TT; ++t)
-                if (s_thead[t] == tid) { if (first < 0) first = t; ++cnt; }
-            s_hf[tid] = first < 0 ? 0 : first;
-            s_hn[tid] = cnt;
-        }
-    } else if (tid < Hq) {  // bf16/fp16: ceil(rank / 16) tiles per query head, kv = h / group
-        const int grp = Hq / Hkv, kv = tid / grp;
-        int t0 = 0;  // tiles of the query heads before this one: whole groups, then this group's
-        for (int k = 0; k < kv; ++k) t0 += grp * ((s_rank[k] + 15) >> 4);
-        const int R = s_rank[kv], o = s_off[kv];
-        const int nt = (R + 15) >> 4;
-        t0 += (tid - kv * grp) * nt;
-        int cnt = 0;
-        for (int j = 0; j < nt && t0 + j < TT; ++j, ++cnt) {
-            tiles[t0 + j] = make_int4(tid, o + 16 * j, min(16, R - 16 * j) | ((j == nt - 1) << 16), kv);
-            s_tword[t0 + j] = (o >> 4) + j;
-        }
-        s_hf[tid] = min(t0, TT);
-        s_hn[tid] = cnt;
-    }
-    __syncthreads();
-    if (tid == 0) hdr[0] = (s_total + grid - 1) / grid;
-
-    // Wave plan. Heads sorted by decreasing tile count (ties: lower head first) are dealt
-    // to the 8 waves in snake order (0..7, 7..0, 0..7, ...), so every wave takes
-    // ceil(Hq / 8) or fewer heads (one head per 16-lane row of the softmax) and the big
-    // heads pair with small ones; then swaps between the most loaded wave and another
-    // lower the maximum while they can. Wave 0 does it in registers.
-    __shared__ int s_pos[MAX_H];
-    if (tid < Hq) {
-        int rank = 0;
-        const int mine = s_hn[tid];
+    if (lane == 63) s_wsum[wave] = incl;
+    // Heads by decreasing tile count (ties: lower head first).
+    if (tid < a.Hq) {
+        const int mine = tt.hn[tid];
+        int pos = 0;
 #pragma unroll 8
-        for (int h = 0; h < Hq; ++h) rank += s_hn[h] > mine || (s_hn[h] == mine && h < tid);
-        s_pos[tid] = rank;
+        for (int h = 0; h < a.Hq; ++h) pos += tt.hn[h] > mine || (tt.hn[h] == mine && h < tid);
+        s_byp[pos] = tid;
     }
+    for (int i = tid; i < NWAVE * PLAN_STRIDE + 1; i += PREP_THR) s_plan[i] = 0;
+    if (tid < NWAVE) s_load[tid] = 0;
     __syncthreads();
+    int run = incl - s;
+#pragma unroll
+    for (int w = 0; w < PREP_THR / 64; ++w) run += w < wave ? s_wsum[w] : 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        run += v[i];
+        if (4 * tid + i < a.n) hdr[2 + 4 * tid + i] = run;
+    }
+    if (tid == PREP_THR - 1) hdr[0] = (run + a.grid - 1) / a.grid;
+    if (tid == 0) hdr[1] = 0;
+
+    // Wave plan, in wave 0 with lane p holding the head at position p of the size order.
+    // Heads are dealt to the 8 waves in snake order (0..7, 7..0, 0..7, ...), so every
+    // wave takes ceil(Hq / 8) or fewer heads (one head per 16-lane row of the softmax)
+    // and the big heads pair with small ones; then swaps between the most loaded wave
+    // and another lower the maximum while they can.
     if (wave == 0) {
-        // Lane h < Hq: head h's tile count, first tile, order position and wave; lane
-        // w < 8: wave w's tile load.
-        const int hsz = lane < Hq ? s_hn[lane] : 0;
-        const int hfirst = lane < Hq ? s_hf[lane] : 0;
-        const int pos = lane < Hq ? s_pos[lane] : 0;
-        const int round = pos / NWAVE, col = pos % NWAVE;
-        int hwave = lane < Hq ? ((round & 1) ? NWAVE - 1 - col : col) : -1;
-        int load = 0;
-        for (int h = 0; h < Hq; ++h)  // wave loads
-            load += __builtin_amdgcn_readlane(hwave, h) == lane ? __builtin_amdgcn_readlane(hsz, h) : 0;
-        const int target = (TT + NWAVE - 1) / NWAVE;
+        const bool act = lane < a.Hq;
+        const int head = act ? s_byp[lane] : 0;
+        const int hsz = act ? tt.hn[head] : 0;
+        const int hfirst = act ? tt.hf[head] : 0;
+        const int col = lane % NWAVE;
+        int hwave = act ? (((lane / NWAVE) & 1) ? NWAVE - 1 - col : col) : -1;
+        if (act) atomicAdd(&s_load[hwave], hsz);
+        int load = lane < NWAVE ? s_load[lane] : 0;  // lane w < 8: wave w's tiles
+        const int target = (a.TT + NWAVE - 1) / NWAVE;
         for (int it = 0; it < 64; ++it) {
             const int kmax = lanes8_max(lane < NWAVE ? (load << 8) | lane : -1);  // most loaded wave A
             const int A = kmax & 255, la = kmax >> 8;
             if (la <= target) break;
             // Candidate swaps: a head ha of A with this lane's head hb of another wave B.
             const int lb = __builtin_amdgcn_ds_bpermute(max(hwave, 0) * 4, load);  // load of hb's wave
-            uint64_t inA = __builtin_amdgcn_ballot_w64(lane < Hq && hwave == A);
+            uint64_t inA = __builtin_amdgcn_ballot_w64(act && hwave == A);
             int best = 0x7fffffff;
             while (inA) {
                 const int ha = __builtin_ctzll(inA);
                 inA &= inA - 1;
                 const int d = __builtin_amdgcn_readlane(hsz, ha) - hsz;
-                if (lane < Hq && hwave != A && d > 0 && lb + d < la)
+                if (act && hwave != A && d > 0 && lb + d < la)
                     best = min(best, (max(la - d, lb + d) << 16) | (ha << 8) | lane);
             }
             best = wave_min_i(best);
@@ -205,186 +244,325 @@ __global__ __launch_bounds__(1024) void setup_kernel(const int32_t* __restrict__
             if (lane == B) load += d;
         }
         const int ok = lanes8_max(lane < NWAVE ? load : 0) <= MAX_SLOTS;
-        // Each head's place in its wave's plan: k = its wave's heads before it in the size
-        // order, sl = their tiles, nfb = those of them with tiles, nnb = their tiles past
-        // their first; over its whole wave: nfh heads with tiles, the largest head mxh.
-        // Lane w < 8 also counts its wave's heads, tiles, heads with tiles, largest head.
-        int k = 0, sl = 0, nfb = 0, nnb = 0, nfh = 0, mxh = 0, nhw = 0, ntw = 0, nfw = 0, mxw = 0;
-        for (int h = 0; h < Hq; ++h) {
-            const int wh = __builtin_amdgcn_readlane(hwave, h), ph = __builtin_amdgcn_readlane(pos, h);
-            const int zh = __builtin_amdgcn_readlane(hsz, h);
-            if (wh == hwave && ph < pos) { ++k; sl += zh; nfb += zh > 0; nnb += max(zh - 1, 0); }
-            if (wh == hwave) { nfh += zh > 0; mxh = max(mxh, zh); }
-            if (wh == lane) { ++nhw; ntw += zh; nfw += zh > 0; mxw = max(mxw, zh); }
+        // Each head's place in its wave's plan, from its wave's heads in lane (= size)
+        // order: k = the heads before it, sl = their tiles, nfb = those of them with
+        // tiles; over its whole wave: nfh heads with tiles, the largest head mxh (the
+        // first). Lane w < 8 also takes wave w's heads, heads with tiles, largest head.
+        int k = 0, sl = 0, nfb = 0, nfh = 0, mxh = 0, nhw = 0, nfw = 0, mxw = 0;
+        for (int w = 0; w < NWAVE; ++w) {
+            uint64_t bw = __builtin_amdgcn_ballot_w64(act && hwave == w);
+            int cnt = 0, acc = 0, fb = 0, big = 0;
+            while (bw) {
+                const int h = __builtin_ctzll(bw);
+                bw &= bw - 1;
+                const int z = __builtin_amdgcn_readlane(hsz, h);
+                if (lane == h) {
+                    k = cnt;
+                    sl = acc;
+                    nfb = fb;
+                }
+                big = max(big, z);
+                ++cnt;
+                acc += z;
+                fb += z > 0;
+            }
+            if (act && hwave == w) {
+                nfh = fb;
+                mxh = big;
+            }
+            if (lane == w) {
+                nhw = cnt;
+                nfw = fb;
+                mxw = big;
+            }
         }
-        // Clear the 8 plans, then every head writes its own entries (same wave: in order).
-        for (int i = lane; i < NWAVE * PLAN_STRIDE; i += 64) plan[i] = 0;
-        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): the clears land first
-        if (lane < Hq && ok) {
-            int* pw = plan + hwave * PLAN_STRIDE;
-            pw[32 + k] = lane;
+        const int nnb = sl - nfb;  // tiles past their first of the heads before this one
+        if (act && ok) {
+            int* pw = s_plan + hwave * PLAN_STRIDE;
+            pw[32 + k] = head;
             pw[40 + k] = sl;
             pw[48 + k] = hsz;
             for (int j = 0; j < hsz; ++j) {
                 pw[8 + sl + j] = hfirst + j;
                 // The decode kernel's slot order: plan order, or for the 3.2-bit kernel the
                 // heads' first tiles first (the ones with outlier ranks), then the rest.
-                const int ks = qorder ? (j == 0 ? nfb : nfh + nnb + j - 1) : sl + j;
-                const int row = mxh <= 4 ? 4 * k + j : sl + j;  // slot_row()'s partial-logit row
-                pw[PW_SLOTS + ks] = slot_word(s_tword[hfirst + j], row, k, hfirst + j);
+                const int ks = a.t_head ? (j == 0 ? nfb : nfh + nnb + j - 1) : sl + j;
+                const int row = mxh <= 4 ? 4 * k + j : sl + j;  // the slot's partial-logit row
+                pw[PW_SLOTS + ks] = slot_word(tt.word[hfirst + j], row, k, hfirst + j);
             }
         }
         if (lane < NWAVE) {
-            int* pw = plan + lane * PLAN_STRIDE;
-            pw[0] = ok ? ntw : 0;
+            int* pw = s_plan + lane * PLAN_STRIDE;
+            pw[0] = ok ? load : 0;
             pw[1] = ok ? nhw : 0;
             pw[2] = ok ? nfw : 0;
             pw[3] = mxw <= 4;
-            for (int s = ok ? ntw : 0; s < MAX_SLOTS; ++s)  // slots past the wave's tiles: tile 0, the spare row
-                pw[PW_SLOTS + s] = slot_word(s_tword[0] & SW_CODE_MASK, MAX_SLOTS, 0, 0);
+            for (int s2 = ok ? load : 0; s2 < MAX_SLOTS; ++s2)  // slots past the wave's tiles: tile 0, the spare row
+                pw[PW_SLOTS + s2] = slot_word(tt.word[0] & SW_CODE_MASK, MAX_SLOTS, 0, 0);
         }
-        if (lane == 0) plan[NWAVE * PLAN_STRIDE] = ok;
+        if (lane == 0) s_plan[NWAVE * PLAN_STRIDE] = ok;
+    }
+    __syncthreads();
+    int* plan = (int*)(a.ws + a.ws_plan);
+    for (int i = tid; i < NWAVE * PLAN_STRIDE + 1; i += PREP_THR) plan[i] = s_plan[i];
+}
+
+// Eight consecutive elements of a DT array from element i, as raw bits (2-byte types:
+// r[0]; fp32: r[0], r[1]), and their fp32 values.
+template <int DT>
+struct Raw8 {
+    uint4 r[DT == STARKV_F32 ? 2 : 1];
+};
+template <int DT>
+__device__ __forceinline__ Raw8<DT> raw8(const void* p, int64_t i) {
+    Raw8<DT> v;
+    if constexpr (DT == STARKV_F32) {
+        const uint4* s = (const uint4*)((const float*)p + i);
+        v.r[0] = s[0];
+        v.r[1] = s[1];
+    } else {
+        v.r[0] = *(const uint4*)((const uint16_t*)p + i);
+    }
+    return v;
+}
+template <int DT>
+__device__ __forceinline__ void raw8_f(const Raw8<DT>& v, float* o) {
+    if constexpr (DT == STARKV_F32) {
+        const uint32_t w[8] = {v.r[0].x, v.r[0].y, v.r[0].z, v.r[0].w, v.r[1].x, v.r[1].y, v.r[1].z, v.r[1].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = __uint_as_float(w[e]);
+    } else {
+        const uint32_t w[4] = {v.r[0].x, v.r[0].y, v.r[0].z, v.r[0].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if constexpr (DT == STARKV_BF16) {
+                o[2 * k] = __uint_as_float(w[k] << 16);
+                o[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+            } else {
+                const half2_t h = __builtin_bit_cast(half2_t, w[k]);
+                o[2 * k] = (float)h[0];
+                o[2 * k + 1] = (float)h[1];
+            }
+        }
     }
 }
 
-// ---------------------------------------------------------------------------
-// 2. fold: AB[b][t][ks][lane] = 8 fp16 of tile row m = lane & 15, columns
-//    32 ks + 8 (lane >> 4) .. +8, scaled by scale*log2(e); rows past the head's rank
-//    are zero (paged_decode.py:79-81 masks them). Row m holds rank m of the tile, or,
-//    for the 3.2-bit cache (perm = 1), rank 2 (m >> 2) + ((m >> 1) & 1) + 8 (m & 1),
-//    scaled by 1/16 when m & 2: then the z values a lane receives (rows 4g .. 4g+3)
-//    are ranks 2g, 2g+8, 2g+1, 2g+9, the low and high nibbles of bytes g and g+4 of
-//    the tile's 8 code bytes (the high nibbles are read as 16 n).
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void fold_tiles_kernel(const void* __restrict__ q, int64_t q_s0, int64_t q_s1,
-                                                         int q_dt, const void* __restrict__ k_up, int64_t ku_s0,
-                                                         int ku_dt, const uint8_t* __restrict__ ws_tiles_p, int TT,
-                                                         float sc, int perm, uint8_t* __restrict__ ab) {
-    const int b = blockIdx.y;
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;  // (tile, k2, lane)
-    const int t = idx >> 7, k2 = (idx >> 6) & 1, lane = idx & 63;
-    if (t >= TT) return;
-    const int4 tm = ((const int4*)ws_tiles_p)[t];
+// Fold workgroups of prep: AB[b][t][ks][lane] = 8 fp16 of tile row m = lane & 15,
+// columns 32 ks + 8 (lane >> 4) .. +8, scaled by scale*log2(e); rows past the head's
+// rank are zero (paged_decode.py:79-81 masks them). Row m holds rank m of the tile, or,
+// for the 3.2-bit cache, rank 2 (m >> 2) + ((m >> 1) & 1) + 8 (m & 1), scaled by 1/16
+// when m & 2: then the z values a lane receives (rows 4g .. 4g+3) are ranks 2g, 2g+8,
+// 2g+1, 2g+9, the low and high nibbles of bytes g and g+4 of the tile's 8 code bytes
+// (the high nibbles are read as 16 n). Thread (tile, k2, lane) reads its two k_up
+// granules once and folds them with the query of each of its requests; every load is
+// issued before the first conversion, so their latencies overlap.
+template <int QT, int UT>
+__device__ void prep_fold(const PrepArgs& a, const TileTable& tt, int tid, int bid) {
+    const int tp = bid % a.tile_pairs, b0 = (bid / a.tile_pairs) * PREP_REQ;
+    const int t = 2 * tp + (tid >> 7), k2 = (tid >> 6) & 1, lane = tid & 63;
+    if (t >= a.TT) return;
+    const bool perm = a.t_head != nullptr;
     const int m = lane & 15, lg = lane >> 4;
     const int rr = perm ? 2 * (m >> 2) + ((m >> 1) & 1) + 8 * (m & 1) : m;
     const int c0 = 32 * k2 + 8 * lg;
-    const int64_t ur = (int64_t)(tm.y + rr) * ku_s0;
-    const int64_t qh = (int64_t)b * q_s0 + (int64_t)tm.x * q_s1;
-    const float s = rr < (tm.z & 255) ? (perm && (m & 2) ? sc * 0.0625f : sc) : 0.f;
-    float u0[8], u1[8], q0[8], q1[8];
-    load8_f(k_up, ur + c0, ku_dt, u0);
-    load8_f(k_up, ur + c0 + 64, ku_dt, u1);
-    load8_f(q, qh + c0, q_dt, q0);
-    load8_f(q, qh + c0 + 64, q_dt, q1);
-    half8_t a, bb;
+    const int h = tt.head[t];
+    const float s = rr < tt.valid[t] ? (perm && (m & 2) ? a.sc * 0.0625f : a.sc) : 0.f;
+    const int64_t ur = (int64_t)(tt.row[t] + rr) * a.ku_s0;
+    const Raw8<UT> ru0 = raw8<UT>(a.k_up, ur + c0), ru1 = raw8<UT>(a.k_up, ur + c0 + 64);
+    Raw8<QT> rq0[PREP_REQ], rq1[PREP_REQ];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        a[e] = (_Float16)((q0[e] * u0[e] + q1[e] * u1[e]) * s);
-        bb[e] = (_Float16)((q1[e] * u0[e] - q0[e] * u1[e]) * s);
+    for (int i = 0; i < PREP_REQ; ++i) {
+        const int b = min(b0 + i, a.n - 1);
+        const int64_t qh = (int64_t)b * a.q_s0 + (int64_t)h * a.q_s1;
+        rq0[i] = raw8<QT>(a.q, qh + c0);
+        rq1[i] = raw8<QT>(a.q, qh + c0 + 64);
     }
-    half8_t* o = (half8_t*)(ab + ((size_t)b * TT + t) * AB_TILE_BYTES);
-    o[k2 * 64 + lane] = a;
-    o[(k2 + 2) * 64 + lane] = bb;
+    float u0[8], u1[8];
+    raw8_f<UT>(ru0, u0);
+    raw8_f<UT>(ru1, u1);
+#pragma unroll
+    for (int i = 0; i < PREP_REQ; ++i) {
+        float q0[8], q1[8];
+        raw8_f<QT>(rq0[i], q0);
+        raw8_f<QT>(rq1[i], q1);
+        half8_t x, y;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            x[e] = (_Float16)((q0[e] * u0[e] + q1[e] * u1[e]) * s);
+            y[e] = (_Float16)((q1[e] * u0[e] - q0[e] * u1[e]) * s);
+        }
+        if (b0 + i < a.n) {
+            half8_t* o = (half8_t*)(a.ws + a.ws_ab + ((size_t)(b0 + i) * a.TT + t) * AB_TILE_BYTES);
+            o[k2 * 64 + lane] = x;
+            o[(k2 + 2) * 64 + lane] = y;
+        }
+    }
+}
+
+template <int QT>
+__device__ void prep_fold_q(const PrepArgs& a, const TileTable& tt, int tid, int bid) {
+    if (a.ku_dt == STARKV_BF16)
+        prep_fold<QT, STARKV_BF16>(a, tt, tid, bid);
+    else if (a.ku_dt == STARKV_F16)
+        prep_fold<QT, STARKV_F16>(a, tt, tid, bid);
+    else
+        prep_fold<QT, STARKV_F32>(a, tt, tid, bid);
+}
+
+__global__ __launch_bounds__(PREP_THR) void prep_kernel(PrepArgs a) {
+    __shared__ TileTable tt;
+    const int tid = threadIdx.x;
+    if (blockIdx.x == 0) {
+        int v[4];  // request lengths, read before the table's barriers
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = 4 * tid + i < a.n ? a.seq_lens[4 * tid + i] : 0;
+        tile_table(a, tt, tid);
+        prep_setup(a, tt, tid, v);
+    } else {
+        tile_table(a, tt, tid);
+        if (a.q_dt == STARKV_BF16)
+            prep_fold_q<STARKV_BF16>(a, tt, tid, blockIdx.x - 1);
+        else if (a.q_dt == STARKV_F16)
+            prep_fold_q<STARKV_F16>(a, tt, tid, blockIdx.x - 1);
+        else
+            prep_fold_q<STARKV_F32>(a, tt, tid, blockIdx.x - 1);
+    }
 }
 
 // ---------------------------------------------------------------------------
-// 4. merge: per (request, head) the partials' log-sum-exp, then the lift through
-//    v_up_by_q. A workgroup takes one head and MERGE_REQ requests, so every row of
-//    v_up_by_q[h] it reads serves MERGE_REQ outputs; the lift loop is unrolled so its
-//    loads are in flight together.
+// 3. merge: per (request, head) the partials' log-sum-exp, then the lift through
+//    v_up_by_q. A workgroup takes one head and MERGE_REQ requests, one wave each, so
+//    every row of v_up_by_q[h] serves MERGE_REQ outputs. The loads come in two rounds:
+//    the request's partial range (with v_up_by_q[h] staged into LDS meanwhile), then
+//    every partial's max and sum and the first MERGE_PRE partials' accumulator rows
+//    together.
 // ---------------------------------------------------------------------------
 constexpr int MERGE_REQ = 4;
-constexpr int MERGE_MAXK = 64;  // partial slots per request whose weights are kept in LDS
+constexpr int MERGE_THR = 64 * MERGE_REQ;
+constexpr int MERGE_PRE = 8;  // partials per request whose accumulator rows are read in the second round
+constexpr int MERGE_CB = 4;   // column blocks of 64: v_rank <= 256
+
+// LDS of one merge workgroup: v_up_by_q[h] (v_rank x 128 WT), then the merged
+// low-rank outputs [MERGE_REQ][v_rank] (fp32).
+static size_t merge_lds_bytes(int v_rank, int w_dt) {
+    return (size_t)v_rank * 128 * (w_dt == STARKV_F32 ? 4 : 2) + (size_t)MERGE_REQ * v_rank * 4;
+}
 
 template <typename WT>
-__device__ __forceinline__ float load_w(const WT* p, int64_t i);
+__device__ __forceinline__ float lds_w(const WT* p, int i);
 template <>
-__device__ __forceinline__ float load_w<uint16_t>(const uint16_t* p, int64_t i) { return bf16_bits_to_f32(p[i]); }
+__device__ __forceinline__ float lds_w<uint16_t>(const uint16_t* p, int i) { return bf16_bits_to_f32(p[i]); }
 template <>
-__device__ __forceinline__ float load_w<_Float16>(const _Float16* p, int64_t i) { return (float)p[i]; }
+__device__ __forceinline__ float lds_w<_Float16>(const _Float16* p, int i) { return (float)p[i]; }
 template <>
-__device__ __forceinline__ float load_w<float>(const float* p, int64_t i) { return p[i]; }
+__device__ __forceinline__ float lds_w<float>(const float* p, int i) { return p[i]; }
 
 template <typename WT>
-__global__ __launch_bounds__(128) void merge_kernel(const uint8_t* __restrict__ ws, size_t ws_plan, size_t ws_m,
-                                                    size_t ws_l, size_t ws_acc, int n, int Hq, int v_rank,
-                                                    const WT* __restrict__ vup, int64_t vu_s0, int64_t vu_s1,
-                                                    void* __restrict__ out, int64_t o_s0, int64_t o_s1, int out_dt) {
-    extern __shared__ float s_o[];                // [MERGE_REQ][v_rank]: merged low-rank outputs
-    __shared__ float s_w[MERGE_REQ][MERGE_MAXK];  // per request: weight of each of its partials
-    __shared__ float s_ml[MERGE_REQ][2];          // per request: reference max, 1 / sum
-    __shared__ int s_k[MERGE_REQ][2];             // per request: first partial slot, count (0: no tokens)
-    const int h = blockIdx.y, b0 = blockIdx.x * MERGE_REQ, tid = threadIdx.x;
-    const int lane = tid & 63, wv = tid >> 6;
+__global__ __launch_bounds__(MERGE_THR) void merge_kernel(const uint8_t* __restrict__ ws, size_t ws_plan,
+                                                          size_t ws_m, size_t ws_l, size_t ws_acc, int n, int Hq,
+                                                          int v_rank, const WT* __restrict__ vup, int64_t vu_s0,
+                                                          int64_t vu_s1, void* __restrict__ out, int64_t o_s0,
+                                                          int64_t o_s1, int out_dt) {
+    extern __shared__ __align__(16) uint8_t s_dyn[];
+    WT* s_v = (WT*)s_dyn;                                     // [v_rank][128]
+    float* s_o = (float*)(s_dyn + (size_t)v_rank * 128 * sizeof(WT));  // [MERGE_REQ][v_rank]
+    __shared__ int s_live[MERGE_REQ];
+    const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, r = tid >> 6;
+    const int b = blockIdx.x * MERGE_REQ + r;
     const int* hdr = (const int*)ws;
-    const int S = hdr[0];
-    const bool planned = ((const int*)(ws + ws_plan))[NWAVE * PLAN_STRIDE] != 0;
     const float* wm = (const float*)(ws + ws_m);
     const float* wl = (const float*)(ws + ws_l);
     const float* wa = (const float*)(ws + ws_acc);
 
-    // 1. Per request (wave wv takes requests wv, wv + 2): the partials' log-sum-exp, with
-    //    the lanes over the partial slots.
-    for (int r = wv; r < MERGE_REQ; r += 2) {
-        const int b = b0 + r;
-        const int pb = b < n ? hdr[1 + b] : 0, pe = b < n ? hdr[2 + b] : 0;
-        // No tokens: softmax over an empty row (NaN, as the reference). No wave plan (a
-        // head assignment that does not fit): NaN as well, never a silent wrong result.
-        const bool live = b < n && pe > pb && S > 0 && planned;
-        const int k_lo = live ? pb / S : 0, nk = live ? (pe - 1) / S - k_lo + 1 : 0;
-        float M = -INFINITY;
-        for (int k = lane; k < nk; k += 64) M = fmaxf(M, wm[(int64_t)(k_lo + k + b) * Hq + h]);
-        M = wave_max(M);
-        float l = 0.f;
-        for (int k = lane; k < nk; k += 64) {
-            const int64_t sl = (int64_t)(k_lo + k + b) * Hq + h;
-            l += wl[sl] * exp2f(wm[sl] - M);
-        }
-        l = wave_sum(l);
-        for (int k = lane; k < nk && k < MERGE_MAXK; k += 64)
-            s_w[r][k] = exp2f(wm[(int64_t)(k_lo + k + b) * Hq + h] - M);
-        if (lane == 0) {
-            s_ml[r][0] = M;
-            s_ml[r][1] = 1.f / l;
-            s_k[r][0] = k_lo;
-            s_k[r][1] = nk;
-        }
-    }
-    __syncthreads();
-
-    // 2. The merged low-rank outputs: threads over (request, column).
-    for (int i = tid; i < MERGE_REQ * v_rank; i += blockDim.x) {
-        const int r = i / v_rank, c = i - r * v_rank, b = b0 + r;
-        const int k_lo = s_k[r][0], nk = s_k[r][1];
-        float a = 0.f;
-#pragma unroll 4
-        for (int k = 0; k < nk; ++k) {
-            const int64_t sl = (int64_t)(k_lo + k + b) * Hq + h;
-            const float w = k < MERGE_MAXK ? s_w[r][k] : exp2f(wm[sl] - s_ml[r][0]);
-            a = fmaf(wa[sl * v_rank + c], w, a);
-        }
-        s_o[i] = a * s_ml[r][1];
-    }
-    __syncthreads();
-
-    // 3. The lift through v_up_by_q[h]: each row serves MERGE_REQ requests.
-    for (int d = tid; d < 128; d += blockDim.x) {
-        float o[MERGE_REQ];
+    // Round 1: request b's tokens [pb, pe) in the concatenation, hence its partial slots
+    // k_lo + k + b, k < nk (S tokens per decode workgroup). No tokens: softmax over an
+    // empty row (NaN, as the reference). No wave plan (a head assignment that does not
+    // fit): NaN as well, never a silent wrong result.
+    const int S = hdr[0];
+    const bool planned = ((const int*)(ws + ws_plan))[NWAVE * PLAN_STRIDE] != 0;
+    const int pb = b < n ? hdr[1 + b] : 0, pe = b < n ? hdr[2 + b] : 0;
+    {
+        // v_up_by_q[h] into LDS, 8 granules (16 bytes) per thread in flight at a time.
+        constexpr int GPR = 128 * (int)sizeof(WT) / 16;  // granules per row
+        constexpr int BATCH = 8;
+        const uint8_t* vh = (const uint8_t*)(vup + (int64_t)h * vu_s0);
+        const int total = v_rank * GPR;
+        for (int base = 0; base < total; base += BATCH * MERGE_THR) {
+            uint4 g[BATCH];
 #pragma unroll
-        for (int r = 0; r < MERGE_REQ; ++r) o[r] = 0.f;
-        const WT* vp = vup + (int64_t)h * vu_s0 + d;
+            for (int u = 0; u < BATCH; ++u) {
+                const int i = min(base + u * MERGE_THR + tid, total - 1), c = i / GPR;  // no branch: loads overlap
+                g[u] = *(const uint4*)(vh + (int64_t)c * vu_s1 * (int64_t)sizeof(WT) + 16 * (i - c * GPR));
+            }
+#pragma unroll
+            for (int u = 0; u < BATCH; ++u)  // past the end: granule total - 1 again, same bytes
+                ((uint4*)s_dyn)[min(base + u * MERGE_THR + tid, total - 1)] = g[u];
+        }
+    }
+    const bool live = b < n && pe > pb && S > 0 && planned;
+    const int k_lo = live ? pb / S : 0, nk = live ? (pe - 1) / S - k_lo + 1 : 0;
+    const int64_t s0 = (int64_t)(k_lo + b) * Hq + h;  // slot index of partial k: s0 + k * Hq
+
+    // Round 2: partial k = lane's max and sum, and lane's columns c = lane + 64 j of the
+    // first MERGE_PRE partials.
+    const float mk = lane < nk ? wm[s0 + (int64_t)lane * Hq] : -INFINITY;
+    const float lk = lane < nk ? wl[s0 + (int64_t)lane * Hq] : 0.f;
+    float pre[MERGE_PRE][MERGE_CB];
+#pragma unroll
+    for (int k = 0; k < MERGE_PRE; ++k)
+#pragma unroll
+        for (int j = 0; j < MERGE_CB; ++j) {
+            const int c = lane + 64 * j;
+            pre[k][j] = k < nk && c < v_rank ? wa[(s0 + (int64_t)k * Hq) * v_rank + c] : 0.f;
+        }
+    float M = mk;
+    for (int k = lane + 64; k < nk; k += 64) M = fmaxf(M, wm[s0 + (int64_t)k * Hq]);
+    M = wave_max(M);
+    const float wk = lane < nk ? exp2f(mk - M) : 0.f;  // weight of partial k = lane
+    float l = lk * wk;
+    for (int k = lane + 64; k < nk; k += 64) {
+        const int64_t sl = s0 + (int64_t)k * Hq;
+        l += wl[sl] * exp2f(wm[sl] - M);
+    }
+    l = wave_sum(l);
+    float acc[MERGE_CB] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < MERGE_PRE; ++k) {
+        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k));
+#pragma unroll
+        for (int j = 0; j < MERGE_CB; ++j) acc[j] = fmaf(pre[k][j], w, acc[j]);
+    }
+    for (int k = MERGE_PRE; k < nk; ++k) {  // requests spread over more than MERGE_PRE workgroups
+        const int64_t sl = s0 + (int64_t)k * Hq;
+        const float w = k < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k))
+                               : exp2f(wm[sl] - M);
+#pragma unroll
+        for (int j = 0; j < MERGE_CB; ++j) {
+            const int c = lane + 64 * j;
+            if (c < v_rank) acc[j] = fmaf(wa[sl * v_rank + c], w, acc[j]);
+        }
+    }
+    const float inv = 1.f / l;
+#pragma unroll
+    for (int j = 0; j < MERGE_CB; ++j)
+        if (lane + 64 * j < v_rank) s_o[r * v_rank + lane + 64 * j] = acc[j] * inv;
+    if (lane == 0) s_live[r] = live;
+    __syncthreads();
+
+    // The lift through v_up_by_q[h]: thread (d, request pair) takes two requests' column d.
+    const int d = tid & 127, r0 = 2 * (tid >> 7);
+    float o0 = 0.f, o1 = 0.f;
 #pragma unroll 8
-        for (int c = 0; c < v_rank; ++c) {
-            const float v = load_w<WT>(vp, (int64_t)c * vu_s1);
-#pragma unroll
-            for (int r = 0; r < MERGE_REQ; ++r) o[r] = fmaf(s_o[r * v_rank + c], v, o[r]);
-        }
-#pragma unroll
-        for (int r = 0; r < MERGE_REQ; ++r)
-            if (b0 + r < n)
-                store_f(out, (int64_t)(b0 + r) * o_s0 + (int64_t)h * o_s1 + d, out_dt,
-                        s_k[r][1] > 0 ? o[r] : __builtin_nanf(""));
+    for (int c = 0; c < v_rank; ++c) {
+        const float v = lds_w<WT>(s_v, c * 128 + d);
+        o0 = fmaf(s_o[r0 * v_rank + c], v, o0);
+        o1 = fmaf(s_o[(r0 + 1) * v_rank + c], v, o1);
     }
+    const int bb = blockIdx.x * MERGE_REQ + r0;
+    if (bb < n) store_f(out, (int64_t)bb * o_s0 + (int64_t)h * o_s1 + d, out_dt, s_live[r0] ? o0 : __builtin_nanf(""));
+    if (bb + 1 < n)
+        store_f(out, (int64_t)(bb + 1) * o_s0 + (int64_t)h * o_s1 + d, out_dt,
+                s_live[r0 + 1] ? o1 : __builtin_nanf(""));
 }
 
 // ---------------------------------------------------------------------------
@@ -462,6 +640,22 @@ struct CommonArgs {
     int grid;
 };
 
+template <typename WT>
+static int launch_merge(dim3 grid, size_t lds, hipStream_t stream, const DecodeParams& p, const WsLayout& wl,
+                        const CommonArgs& a) {
+    static size_t lds_allowed = 65536;  // per function: raised as larger v_rank need it (at most 132 KB)
+    if (lds > lds_allowed) {
+        SKV_HIP(hipFuncSetAttribute((const void*)merge_kernel<WT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)lds));
+        lds_allowed = lds;
+    }
+    hipLaunchKernelGGL(merge_kernel<WT>, grid, dim3(MERGE_THR), lds, stream, (const uint8_t*)p.ws, wl.plan, wl.m, wl.l,
+                       wl.acc, a.n, a.Hq, a.v_rank, (const WT*)a.vup, a.vu_s0, a.vu_s1, a.out, a.o_s0, a.o_s1,
+                       a.out_dt);
+    SKV_HIP(hipGetLastError());
+    return STARKV_OK;
+}
+
 static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_bytes, int TT, hipStream_t stream) {
     SKV_CHECK(a.n >= 1 && a.n <= MAX_REQ_PER_CALL, "decode: n=%d requests (1..%d per call)", a.n, MAX_REQ_PER_CALL);
     SKV_CHECK(a.Hq >= 1 && a.Hq <= MAX_H, "decode: num_heads=%d (1..%d)", a.Hq, MAX_H);
@@ -485,6 +679,9 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     SKV_CHECK(p.c_s1 >= row_bytes, "decode: slot stride %lld < row bytes %d", (long long)p.c_s1, row_bytes);
     SKV_CHECK(p.c_s1 * TILE_TOK < ((int64_t)1 << 31), "decode: 16 slots span %lld bytes (>= 2^31)",
               (long long)(p.c_s1 * TILE_TOK));
+    SKV_CHECK(a.q_dt >= STARKV_F32 && a.q_dt <= STARKV_BF16 && a.w_dt >= STARKV_F32 && a.w_dt <= STARKV_BF16 &&
+                  a.out_dt >= STARKV_F32 && a.out_dt <= STARKV_BF16,
+              "decode: query, k_up / v_up_by_q and output dtypes must be bf16, fp16 or fp32");
     SKV_CHECK(a.cs_dt == STARKV_F16, "decode: cos_sin must be fp16 (convert the table once; it is exact for bf16)");
     SKV_CHECK(a.cs_s0 % 8 == 0 && a.cs_s0 >= 128 && a.cs_s0 * 2 * TILE_TOK < ((int64_t)1 << 31) &&
                   ((uintptr_t)a.cs % 16) == 0,
@@ -494,6 +691,9 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     SKV_CHECK(a.ku_s0 % 8 == 0 && ((uintptr_t)a.k_up % 16) == 0, "decode: k_up rows must be 16-byte aligned");
     const int nb = (a.v_rank + 63) / 64;
     SKV_CHECK(nb <= 4, "decode: v_rank %d > 256", a.v_rank);
+    const int wsz = a.w_dt == STARKV_F32 ? 4 : 2;
+    SKV_CHECK(((uintptr_t)a.vup % 16) == 0 && (a.vu_s0 * wsz) % 16 == 0 && (a.vu_s1 * wsz) % 16 == 0,
+              "decode: v_up_by_q rows must be 16-byte aligned");
 
     p.bt = a.bt; p.bt_s0 = (int)a.bt_s0; p.bt_s1 = (int)a.bt_s1;
     p.n = a.n; p.Hq = a.Hq; p.TT = TT; p.v_rank = a.v_rank;
@@ -515,16 +715,21 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
         p.lds_bytes = lowrank_lds_bytes(p.k_width, nb);
     }
     p.ws = (uint8_t*)a.ws;
-    p.ws_tiles = wl.tiles; p.ws_plan = wl.plan; p.ws_ab = wl.ab;
+    p.ws_plan = wl.plan; p.ws_ab = wl.ab;
     p.ws_m = wl.m; p.ws_l = wl.l; p.ws_acc = wl.acc;
 
-    hipLaunchKernelGGL(setup_kernel, dim3(1), dim3(1024), 0, stream, a.seq_lens, a.n, a.max_seq_len, a.grid, a.Hq,
-                       a.Hkv, TT, a.k_ranks, a.k_offsets, a.t_head, a.t_nout, a.t_last, fmt == FMT_Q4 ? 1 : 0, p.ws,
-                       wl.tiles, wl.plan);
-    SKV_HIP(hipGetLastError());
-    hipLaunchKernelGGL(fold_tiles_kernel, dim3((TT * 128 + 255) / 256, a.n), dim3(256), 0, stream, a.q, a.q_s0,
-                       a.q_s1, a.q_dt, a.k_up, a.ku_s0, a.w_dt, (const uint8_t*)p.ws + wl.tiles, TT,
-                       a.scale * LOG2E, fmt == FMT_Q4 ? 1 : 0, p.ws + wl.ab);
+    PrepArgs pa;
+    pa.seq_lens = a.seq_lens; pa.n = a.n; pa.max_seq_len = a.max_seq_len; pa.grid = a.grid;
+    pa.Hq = a.Hq; pa.Hkv = a.Hkv; pa.TT = TT; pa.k_rows = p.k_width;
+    pa.k_ranks = a.k_ranks; pa.k_offsets = a.k_offsets;
+    pa.t_head = a.t_head; pa.t_nout = a.t_nout; pa.t_last = a.t_last;
+    pa.q = a.q; pa.q_s0 = a.q_s0; pa.q_s1 = a.q_s1; pa.q_dt = a.q_dt;
+    pa.k_up = a.k_up; pa.ku_s0 = a.ku_s0; pa.ku_dt = a.w_dt;
+    pa.sc = a.scale * LOG2E;
+    pa.ws = p.ws; pa.ws_plan = wl.plan; pa.ws_ab = wl.ab;
+    pa.tile_pairs = (TT + 1) / 2;
+    const int prep_grid = 1 + pa.tile_pairs * ((a.n + PREP_REQ - 1) / PREP_REQ);
+    hipLaunchKernelGGL(prep_kernel, dim3(prep_grid), dim3(PREP_THR), 0, stream, pa);
     SKV_HIP(hipGetLastError());
     const bool timed = g_prof.on && 2 * g_prof.used + 1 < (int)g_prof.ev.size();
     if (timed) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
@@ -536,21 +741,10 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
         ++g_prof.used;
     }
     const dim3 mgrid((a.n + MERGE_REQ - 1) / MERGE_REQ, a.Hq);
-    const size_t mlds = (size_t)MERGE_REQ * a.v_rank * 4;
-    if (a.w_dt == STARKV_BF16)
-        hipLaunchKernelGGL(merge_kernel<uint16_t>, mgrid, dim3(128), mlds, stream, (const uint8_t*)p.ws, wl.plan, wl.m,
-                           wl.l, wl.acc, a.n, a.Hq, a.v_rank, (const uint16_t*)a.vup, a.vu_s0, a.vu_s1, a.out, a.o_s0,
-                           a.o_s1, a.out_dt);
-    else if (a.w_dt == STARKV_F16)
-        hipLaunchKernelGGL(merge_kernel<_Float16>, mgrid, dim3(128), mlds, stream, (const uint8_t*)p.ws, wl.plan, wl.m,
-                           wl.l, wl.acc, a.n, a.Hq, a.v_rank, (const _Float16*)a.vup, a.vu_s0, a.vu_s1, a.out, a.o_s0,
-                           a.o_s1, a.out_dt);
-    else
-        hipLaunchKernelGGL(merge_kernel<float>, mgrid, dim3(128), mlds, stream, (const uint8_t*)p.ws, wl.plan, wl.m,
-                           wl.l, wl.acc, a.n, a.Hq, a.v_rank, (const float*)a.vup, a.vu_s0, a.vu_s1, a.out, a.o_s0,
-                           a.o_s1, a.out_dt);
-    SKV_HIP(hipGetLastError());
-    return STARKV_OK;
+    const size_t mlds = merge_lds_bytes(a.v_rank, a.w_dt);
+    if (a.w_dt == STARKV_BF16) return launch_merge<uint16_t>(mgrid, mlds, stream, p, wl, a);
+    if (a.w_dt == STARKV_F16) return launch_merge<_Float16>(mgrid, mlds, stream, p, wl, a);
+    return launch_merge<float>(mgrid, mlds, stream, p, wl, a);
 }
 
 }  // namespace starkv
@@ -566,7 +760,9 @@ int starkv_profile_begin(int max_calls) {
     SKV_CHECK(max_calls >= 1 && max_calls <= 100000, "profile_begin: max_calls %d", max_calls);
     for (hipEvent_t e : g_prof.ev) (void)hipEventDestroy(e);
     g_prof.ev.assign(2 * (size_t)max_calls, nullptr);
-    for (auto& e : g_prof.ev) SKV_HIP(hipEventCreate(&e));
+    // Timing-only events: without the system-scope fence a record does not write back
+    // and invalidate the caches between the launches it separates.
+    for (auto& e : g_prof.ev) SKV_HIP(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
     g_prof.used = 0;
     g_prof.on = true;
     return STARKV_OK;

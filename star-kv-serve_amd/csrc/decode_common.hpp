@@ -35,7 +35,6 @@ constexpr float LAZY_MAX = 8.f;             // log2 headroom before the running 
 
 // Workspace layout, in bytes from the base (every region 256-byte aligned):
 //   hdr    int   [2 + n]      S (tokens per workgroup), P[0..n] (prefix of clamped lengths)
-//   tiles  int4  [TT]         {q head, first cache lane, valid | nout << 8 | last << 16, kv head}
 //   plan   int   [8][80] + 1  per wave: [0] tiles, [1] heads, [2] heads with tiles,
 //                             [3] 1 if every head has <= 4 tiles, [8 + s] tile of slot s,
 //                             [32 + k] q head of local head k, [40 + k] its first slot,
@@ -62,7 +61,7 @@ __device__ __forceinline__ int sw_head(uint32_t w) { return (int)((w >> 23) & 3)
 __device__ __forceinline__ int sw_tile(uint32_t w) { return (int)(w >> 25); }
 
 struct WsLayout {
-    size_t hdr, tiles, plan, ab, m, l, acc, total;
+    size_t hdr, plan, ab, m, l, acc, total;
 };
 
 static inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -72,7 +71,6 @@ static WsLayout ws_layout(int n, int Hq, int TT, int v_rank, int grid) {
     const size_t slots = (size_t)grid + n;
     size_t o = 0;
     w.hdr = o; o = al256(o + (size_t)(n + 2) * 4);
-    w.tiles = o; o = al256(o + (size_t)TT * 16);
     w.plan = o; o = al256(o + (size_t)(NWAVE * PLAN_STRIDE + 1) * 4);
     w.ab = o; o = al256(o + ((size_t)n * TT + AB_SLACK_TILES) * AB_TILE_BYTES);
     w.m = o; o = al256(o + slots * Hq * 4);
@@ -92,7 +90,7 @@ struct DecodeParams {
     int nch, lds_bytes;                            // 1 KB chunks copied per page, dynamic LDS bytes
     const uint8_t* cs; int cs_s0b;                 // fp16 cos/sin table, row stride in bytes
     uint8_t* ws;
-    size_t ws_tiles, ws_plan, ws_ab, ws_m, ws_l, ws_acc;
+    size_t ws_plan, ws_ab, ws_m, ws_l, ws_acc;
 };
 
 __device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -180,10 +178,6 @@ __device__ __forceinline__ const DecodeParams& params() {
     kparams_t* pp = (kparams_t*)__builtin_amdgcn_kernarg_segment_ptr();
     asm volatile("" : "+s"(pp));
     return *(const DecodeParams*)pp;  // address-space inference keeps these scalar loads
-}
-
-__device__ __forceinline__ int4 load_tile(cint_p tiles, int t) {
-    return make_int4(tiles[4 * t], tiles[4 * t + 1], tiles[4 * t + 2], tiles[4 * t + 3]);
 }
 
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
