@@ -1,0 +1,173 @@
+"""The fused-checkpoint loader, its kernel operands and the synthetic writer
+(starkv_serve/checkpoint.py, after the reference's checkpoint.py:66-169 and
+attention.py:134-166).
+
+What pins the loader without the reference's own import:
+- the product U VS of every K head and of V is what the checkpoint holds, exactly
+  for the bf16/fp16 cache (a pure repack) and to fp32 rounding after the Hadamard
+  fold of the 3.2-bit cache (T T^T = I);
+- the rotated factors equal the oracle's block_hadamard (pinned by golden sign
+  vectors) applied with a fresh generator per projection, head by head;
+- widths, offsets, zero padding, skipped layers and the errors follow the format.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref
+from starkv_serve import checkpoint as ck
+from starkv_serve.kernels.paged_quant import QuantRow
+
+H, HD, HIDDEN = 4, 128, 96
+LAYERS = {1: ([16, 24, 40, 64], 48), 3: ([32, 7, 16, 50], 32)}  # ranks not all multiples of 16
+
+
+@pytest.fixture(scope="module")
+def ckpt(tmp_path_factory):
+    path = str(tmp_path_factory.mktemp("ckpt") / "fused_weights.pt")
+    sd = ck.write_fused_checkpoint(path, num_layers=4, num_kv_heads=H, head_dim=HD, hidden=HIDDEN,
+                                   compressed=LAYERS, seed=7, dtype=torch.float32)
+    return path, sd
+
+
+def _raw(sd, li):
+    pre = f"model.layers.{li}.self_attn."
+    return (sd[pre + "k_proj.VS.weight"].double(), sd[pre + "k_proj.U.weight"].double(),
+            sd[pre + "v_proj.VS.weight"].double(), sd[pre + "v_proj.U.weight"].double())
+
+
+@pytest.mark.parametrize("kv_quant", [False, True])
+def test_layout(ckpt, kv_quant):
+    path, _ = ckpt
+    c = ck.load_fused_checkpoint(path, 4, H, HD, dtype=torch.float32, kv_quant=kv_quant)
+    assert sorted(c.layers) == [1, 3] and c.skip_layers == (0, 2)
+    assert c.is_compressed(1) and not c.is_compressed(0)
+    for li, (ranks, rv) in LAYERS.items():
+        w = c.layers[li]
+        widths = [ref.align16(r) for r in ranks]
+        assert w.k_head_ranks.tolist() == ranks and w.k_head_widths.tolist() == widths
+        assert w.k_head_offsets.tolist() == [sum(widths[:h]) for h in range(H)]
+        assert w.k_width == sum(widths) and w.k_max_rank == max(widths)
+        assert w.v_rank_real == rv and w.v_rank == (rv if kv_quant else ref.align16(rv))
+        assert w.k_down.shape == (w.k_width, HIDDEN) and w.k_up.shape == (w.k_width, HD)
+        assert w.v_down.shape == (w.v_rank, HIDDEN) and w.v_up.shape == (H * HD, w.v_rank)
+        for h, r in enumerate(ranks):  # rows between a head's rank and its width are zero
+            o = w.k_head_offsets[h].item()
+            assert not w.k_down[o + r:o + widths[h]].any() and not w.k_up[o + r:o + widths[h]].any()
+        assert not w.v_down[rv:].any() and not w.v_up[:, rv:].any()
+        if kv_quant:
+            assert w.cache_bytes(2) == QuantRow(w.k_width, H, w.v_rank).nbytes
+        else:
+            assert w.cache_width == w.k_width + w.v_rank and w.cache_bytes(2) == 2 * w.cache_width
+
+
+@pytest.mark.parametrize("kv_quant", [False, True])
+def test_products_preserved(ckpt, kv_quant):
+    """k_up[head rows]^T k_down[head rows] = U_h VS_h and v_up v_down = U_v VS_v."""
+    path, sd = ckpt
+    c = ck.load_fused_checkpoint(path, 4, H, HD, dtype=torch.float32, kv_quant=kv_quant)
+    tol = 1e-5 if kv_quant else 0.0
+    for li, (ranks, rv) in LAYERS.items():
+        w = c.layers[li]
+        kvs, ku, vvs, vu = _raw(sd, li)
+        col = 0
+        for h, r in enumerate(ranks):
+            o = w.k_head_offsets[h].item()
+            got = w.k_up[o:o + ref.align16(r)].double().T @ w.k_down[o:o + ref.align16(r)].double()
+            want = ku[h * HD:(h + 1) * HD, col:col + r] @ kvs[col:col + r]
+            assert (got - want).abs().max().item() <= tol * want.abs().max().item()
+            col += r
+        got = w.v_up.double() @ w.v_down.double()
+        want = vu @ vvs
+        assert (got - want).abs().max().item() <= tol * want.abs().max().item()
+
+
+def test_rotation_matches_oracle_hadamard(ckpt):
+    """3.2-bit cache: VS_h <- T_h^T VS_h, U_h <- U_h T_h with the oracle's T (golden-pinned),
+    one generator per projection seeded 1234, consumed head by head."""
+    path, sd = ckpt
+    c = ck.load_fused_checkpoint(path, 4, H, HD, dtype=torch.float32, kv_quant=True)
+    for li, (ranks, rv) in LAYERS.items():
+        w = c.layers[li]
+        kvs, ku, vvs, vu = (t.numpy() for t in _raw(sd, li))
+        g = torch.Generator().manual_seed(1234)
+        col = 0
+        for h, r in enumerate(ranks):
+            T = ref.block_hadamard(r, ref.n_outlier(r), g)
+            o = w.k_head_offsets[h].item()
+            np.testing.assert_allclose(w.k_down[o:o + r].numpy(), (T.T @ kvs[col:col + r]).astype(np.float32),
+                                       rtol=0, atol=2e-6)
+            np.testing.assert_allclose(w.k_up[o:o + r].numpy(),
+                                       (ku[h * HD:(h + 1) * HD, col:col + r] @ T).T.astype(np.float32),
+                                       rtol=0, atol=2e-6)
+            col += r
+        T = ref.block_hadamard(rv, ref.n_outlier(rv), torch.Generator().manual_seed(1234))
+        np.testing.assert_allclose(w.v_down.numpy(), (T.T @ vvs).astype(np.float32), rtol=0, atol=2e-6)
+        np.testing.assert_allclose(w.v_up.numpy(), (vu @ T).astype(np.float32), rtol=0, atol=2e-6)
+
+
+def test_operands(ckpt):
+    path, _ = ckpt
+    for kv_quant in (False, True):
+        c = ck.load_fused_checkpoint(path, 4, H, HD, dtype=torch.float32, kv_quant=kv_quant)
+        w = c.layers[3]
+        for nq in (H, 2 * H):
+            ops = ck.layer_operands(w, nq, "cpu", torch.float32)
+            grp = nq // H
+            assert ops.v_up_by_q.shape == (nq, w.v_rank, HD) and ops.v_up_by_q.is_contiguous()
+            for h in range(nq):
+                kv = h // grp
+                assert torch.equal(ops.v_up_by_q[h], w.v_up[kv * HD:(kv + 1) * HD].T)
+            assert torch.equal(ops.kv_down, torch.cat([w.k_down, w.v_down]))
+            assert ops.k_width == w.k_width and torch.equal(ops.k_up, w.k_up)
+            if kv_quant:
+                assert ops.row == QuantRow(w.k_width, H, w.v_rank)
+                nouts, lanes, tiles = ref.k_tables(w.k_head_ranks.tolist())
+                assert ops.k_nouts.tolist() == list(nouts) and ops.head_of_lane.tolist() == list(lanes)
+                assert [t.tolist() for t in ops.k_tiles] == [list(x) for x in tiles]
+            else:
+                assert ops.row is None
+        with pytest.raises(ValueError):
+            ck.layer_operands(w, H + 1, "cpu", torch.float32)
+
+
+def test_errors(tmp_path):
+    base = ck.write_fused_checkpoint(str(tmp_path / "a.pt"), 2, H, HD, HIDDEN, {1: ([16] * H, 16)})
+    # legacy U/Sigma/V layer
+    legacy = dict(base)
+    legacy["model.layers.0.self_attn.k_proj.Sigma_blocks.0.diag"] = torch.ones(4)
+    torch.save(legacy, tmp_path / "legacy.pt")
+    with pytest.raises(ValueError, match="legacy"):
+        ck.load_fused_checkpoint(str(tmp_path / "legacy.pt"), 2, H, HD)
+    # no compressed layer
+    torch.save({"model.layers.0.self_attn.k_proj.weight": torch.zeros(4, 4)}, tmp_path / "none.pt")
+    with pytest.raises(ValueError, match="no fused"):
+        ck.load_fused_checkpoint(str(tmp_path / "none.pt"), 2, H, HD)
+    # head-rank count and shape mismatches
+    with pytest.raises(ValueError, match="head ranks"):
+        ck.load_fused_checkpoint(str(tmp_path / "a.pt"), 2, H + 1, HD)
+    bad = dict(base)
+    bad["model.layers.1.self_attn.k_proj.U.weight"] = torch.zeros(H * HD, 5)
+    torch.save(bad, tmp_path / "bad.pt")
+    with pytest.raises(ValueError, match="k_proj"):
+        ck.load_fused_checkpoint(str(tmp_path / "bad.pt"), 2, H, HD)
+    bad = dict(base)
+    bad["model.layers.1.self_attn.v_proj.U.weight"] = torch.zeros(H * HD, 3)
+    torch.save(bad, tmp_path / "badv.pt")
+    with pytest.raises(ValueError, match="v_proj"):
+        ck.load_fused_checkpoint(str(tmp_path / "badv.pt"), 2, H, HD)
+    with pytest.raises(ValueError):
+        ck.write_fused_checkpoint(str(tmp_path / "c.pt"), 2, H, HD, HIDDEN, {1: ([16] * (H - 1), 16)})
+
+
+def test_writer_statistics(tmp_path):
+    """Codes of a unit-variance hidden state, and the K they lift to, have about unit variance."""
+    sd = ck.write_fused_checkpoint(str(tmp_path / "s.pt"), 1, H, HD, 1024, {0: ([64] * H, 64)}, seed=3,
+                                   dtype=torch.float32)
+    w = ck.load_fused_checkpoint(str(tmp_path / "s.pt"), 1, H, HD, dtype=torch.float32).layers[0]
+    x = torch.randn(2048, 1024, generator=torch.Generator().manual_seed(5))
+    codes = x @ w.k_down.T
+    assert 0.8 < codes.std().item() < 1.2
+    k0 = codes[:, :64] @ w.k_up[:64]
+    assert 0.8 < k0.std().item() < 1.2
+    assert sd["model.layers.0.self_attn.k_proj.head_ranks"].dtype == torch.int32
