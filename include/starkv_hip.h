@@ -54,6 +54,38 @@ int starkv_write_codes(void *stream, const void *k_codes, int64_t k_s0, const vo
                        int slot_bits, int n, int k_width, int v_rank);
 
 /*
+ * Fused cache write of one layer step: codes = hidden @ kv_down^T (fp32 accumulate,
+ * rounded to the model dtype with round-to-nearest-even, as F.linear returns them),
+ * then either the bf16/fp16 scatter (row_bytes == 0) or the 3.2-bit quantize + scatter
+ * (row_bytes == QuantRow.nbytes), in two launches. Replaces the code GEMM of
+ * StarKVLlamaAttention.forward, starkv_serve/model.py:71 (kv = F.linear(hidden,
+ * kv_down), kv_down = cat(k_down, v_down) from attention.py:161), followed by the cache
+ * write of StarKVAttentionImpl.forward, starkv_serve/attention.py:179-188 (cat +
+ * index_put, or pack_kv = paged_quant.py:205-216; the 3.2-bit rows are bit for bit
+ * pack_kv of the rounded codes).
+ *   hidden    [n, hidden_size], row stride h_s0 elements, bf16 or fp16 (w_dtype)
+ *   kv_down   [k_width + v_rank, hidden_size], row stride w_s0, same dtype; rows 16-byte
+ *             aligned, hidden_size a multiple of 32
+ *   cache     row_bytes == 0: [num_blocks, block_size, >= k_width + v_rank] of the model
+ *             dtype (cache_dtype == w_dtype), element strides c_s0, c_s1;
+ *             row_bytes > 0: uint8 [num_blocks, block_size, row_bytes], byte strides
+ *   slot_mapping [n] int32 / int64 (slot_bits); slot < 0 -> slot 0 (the null block);
+ *             slots at or past num_blocks * block_size are skipped
+ *   k_ranks / k_offsets / k_nouts [num_kv_heads] int32 device arrays (3.2-bit only)
+ *   codes_out [n, k_width + v_rank] of the model dtype, row stride co_s0, or NULL: the
+ *             rounded codes (what F.linear returns)
+ *   workspace >= starkv_write_kv_workspace_bytes(n, k_width + v_rank, hidden_size) bytes,
+ *             16-byte aligned (fp32 split-K partials)
+ */
+size_t starkv_write_kv_workspace_bytes(int n, int width, int hidden_size);
+int starkv_write_kv(void *stream, const void *hidden, int64_t h_s0, const void *kv_down, int64_t w_s0,
+                    int w_dtype, int n, int hidden_size, int k_width, int v_rank, void *cache, int64_t c_s0,
+                    int64_t c_s1, int cache_dtype, int block_size, int64_t num_blocks,
+                    const void *slot_mapping, int slot_bits, int num_kv_heads, const int32_t *k_ranks,
+                    const int32_t *k_offsets, const int32_t *k_nouts, int row_bytes, void *codes_out,
+                    int64_t co_s0, void *workspace, size_t workspace_bytes);
+
+/*
  * 3.2-bit write path: quantize one row per token (per-KV-head 4-bit outlier /
  * 3-bit inlier K blocks with bf16 scales, then the head-shared V latent) and
  * scatter it into its slot, bit for bit kv_quant._q (IEEE fp32 division,

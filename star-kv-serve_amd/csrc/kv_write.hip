@@ -1,0 +1,239 @@
+// Fused cache write of one layer step: the code projection hidden @ kv_down^T on MFMA,
+// then the bf16/fp16 scatter or the 3.2-bit quantize + scatter, in two launches.
+//
+// Reference: the model's code GEMM (starkv_serve/model.py:71: kv = F.linear(hidden,
+// kv_down), kv_down = [k_down; v_down], attention.py:161) and the cache write of
+// StarKVAttentionImpl.forward (attention.py:179-188: cat + index_put into the bf16/fp16
+// cache, or pack_kv into the 3.2-bit cache, paged_quant.py:205-216).
+//
+// 1. kv_gemm_kernel: split-K partial products. Workgroup (code tile t of 64, K split s,
+//    token block of 64) has 4 waves; wave w takes codes [64 t + 16 w, +16) and the
+//    block's tokens in 16-row MFMA tiles over split s with v_mfma_f32_16x16x32 (A = 16
+//    hidden rows x 32 channels, B = 32 channels x 16 kv_down rows), and writes fp32
+//    partials [s][token][code]. kv_down (the layer's only large operand) is read once,
+//    spread over ~256+ workgroups.
+// 2. kv_store_kernel: one workgroup per token sums its partials in a fixed order, rounds
+//    every code to the model dtype (the dtype F.linear returns, round-to-nearest-even),
+//    optionally writes the rounded codes out, and stores the row: the codes themselves
+//    (bf16/fp16 cache) or the packed 3.2-bit row, the packers reading the rounded codes
+//    from LDS exactly as pack_kv reads them from memory.
+#include "pack_rows.hpp"
+
+namespace starkv {
+
+constexpr int KVW_THR = 256;
+constexpr int KVW_COLS = 64;    // codes per GEMM workgroup (4 waves x 16)
+constexpr int KVW_TOKENS = 64;  // tokens per GEMM workgroup (4 MFMA row tiles)
+constexpr int KVW_MAX_SPLIT = 16;
+constexpr int KVW_CHUNK = 8;     // K steps (of 32 channels) whose loads are in flight together
+
+struct KvGemmParams {
+    const uint16_t* hidden; int64_t h_s0;  // [n, hidden] elements
+    const uint16_t* w; int64_t w_s0;       // kv_down [width, hidden]
+    int n, width, ksteps, splits;           // ksteps = hidden / 32
+    float* part;                            // [splits][n][width]
+};
+
+template <int DT>
+__device__ __forceinline__ f32x4_t mfma_16x16x32(uint4 a, uint4 b, f32x4_t c) {
+    if constexpr (DT == STARKV_BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                       c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c,
+                                                      0, 0, 0);
+}
+
+template <int DT>
+__global__ __launch_bounds__(KVW_THR) void kv_gemm_kernel(const KvGemmParams p) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int s = blockIdx.y, m0 = KVW_TOKENS * blockIdx.z;
+    const int col = KVW_COLS * blockIdx.x + 16 * wave + (lane & 15);  // this lane's B column (code)
+    const int kq = 8 * (lane >> 4);                                    // its 8 channels of each 32
+    const int k0 = s * p.ksteps / p.splits, k1 = (s + 1) * p.ksteps / p.splits;
+    const int tiles = min(4, (p.n - m0 + 15) / 16);  // row tiles with tokens (uniform)
+    // Rows past the code or token range read row width - 1 / n - 1 (valid memory);
+    // their products are never stored.
+    const uint16_t* wr = p.w + (int64_t)min(col, p.width - 1) * p.w_s0 + kq;
+    const uint16_t* ar[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) ar[t] = p.hidden + (int64_t)min(m0 + 16 * t + (lane & 15), p.n - 1) * p.h_s0 + kq;
+    f32x4_t acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    // K steps go in chunks of KVW_CHUNK: every load of a chunk is issued before its
+    // first MFMA. Every row tile runs, past-n rows included, and steps past the split's
+    // end reload its last step with B zeroed, so nothing branches between the loads.
+    for (int kc = k0; kc < k1; kc += KVW_CHUNK) {
+        uint4 b[KVW_CHUNK], a[KVW_CHUNK][4];
+#pragma unroll
+        for (int j = 0; j < KVW_CHUNK; ++j) {
+            const int k = min(kc + j, k1 - 1);
+            b[j] = *(const uint4*)(wr + 32 * k);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[j][t] = *(const uint4*)(ar[t] + 32 * k);
+        }
+#pragma unroll
+        for (int j = 0; j < KVW_CHUNK; ++j) {
+            const uint4 bj = kc + j < k1 ? b[j] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[t] = mfma_16x16x32<DT>(a[j][t], bj, acc[t]);
+        }
+    }
+    if (col >= p.width) return;
+    // acc[t][e] = code `col` of token m0 + 16 t + 4 (lane >> 4) + e.
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int m = m0 + 16 * t + 4 * (lane >> 4) + e;
+            if (t < tiles && m < p.n) p.part[((int64_t)s * p.n + m) * p.width + col] = acc[t][e];
+        }
+}
+
+struct KvStoreParams {
+    const float* part; int splits, n, width;
+    int k_width, v_rank;
+    uint16_t* codes; int64_t co_s0;  // optional [n, width] rounded codes
+    void* cache; int64_t c_s0, c_s1;  // element strides (bytes for the 3.2-bit cache)
+    int block_size; int64_t num_blocks;
+    const void* slots; int slot_bits;
+    int quant;                        // 1: 3.2-bit rows
+    int H; const int32_t* ranks; const int32_t* offsets; const int32_t* nouts;
+    RowLayout row;
+};
+
+template <int DT>
+__device__ __forceinline__ uint16_t round_code(float x) {
+    if constexpr (DT == STARKV_BF16) return f32_to_bf16_rne(x);
+    else return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+template <int DT>
+__device__ __forceinline__ float code_value(uint16_t r) {
+    if constexpr (DT == STARKV_BF16) return bf16_bits_to_f32(r);
+    else return (float)__builtin_bit_cast(_Float16, r);
+}
+
+template <int DT>
+__global__ __launch_bounds__(KVW_THR) void kv_store_kernel(const KvStoreParams p) {
+    extern __shared__ float s_code[];  // [width]: the token's rounded codes
+    const int i = blockIdx.x, tid = threadIdx.x;
+    const int64_t slot = load_slot(p.slots, p.slot_bits, i);
+    const bool store = slot < p.num_blocks * p.block_size;  // slots past the cache are skipped
+    const int64_t row = (slot / p.block_size) * p.c_s0 + (slot % p.block_size) * p.c_s1;
+    for (int c = tid; c < p.width; c += KVW_THR) {
+        float a = 0.f;
+        for (int s = 0; s < p.splits; ++s) a += p.part[((int64_t)s * p.n + i) * p.width + c];
+        const uint16_t r = round_code<DT>(a);
+        s_code[c] = code_value<DT>(r);
+        if (p.codes) p.codes[(int64_t)i * p.co_s0 + c] = r;
+        if (!p.quant && store) ((uint16_t*)p.cache)[row + c] = r;
+    }
+    if (!p.quant || !store) return;
+    __syncthreads();
+    const int lane = tid & 63;
+    uint8_t* dst = (uint8_t*)p.cache + row;
+    for (int u = tid >> 6; u <= p.H; u += KVW_THR / 64) {
+        if (u < p.H) {
+            const float* src = s_code + p.offsets[u];
+            pack_k_block([&](int l) { return src[l]; }, p.ranks[u], p.nouts[u], p.offsets[u], u, p.row.ks_off, dst,
+                         lane);
+        } else {
+            const float* src = s_code + p.k_width;
+            pack_v_block([&](int c) { return src[c]; }, p.v_rank, p.row.v_nout, p.row.v_nbo, p.row.v_bytes,
+                         p.row.vq_off, p.row.vs_off, p.row.nbytes, dst, lane);
+        }
+    }
+}
+
+// K splits: doubled while the GEMM grid has fewer than 256 workgroups (one per CU) and
+// every split keeps at least one chunk of K steps.
+static int kv_splits(int n, int width, int hidden) {
+    const int tiles = ((width + KVW_COLS - 1) / KVW_COLS) * ((n + KVW_TOKENS - 1) / KVW_TOKENS);
+    const int ksteps = hidden / 32;
+    int s = 1;
+    while (s < KVW_MAX_SPLIT && 2 * s * KVW_CHUNK <= ksteps && tiles * s < 256) s *= 2;
+    return s;
+}
+
+}  // namespace starkv
+
+using namespace starkv;
+
+extern "C" {
+
+size_t starkv_write_kv_workspace_bytes(int n, int width, int hidden) {
+    if (n <= 0 || width <= 0 || hidden < 32) return 0;
+    return (size_t)kv_splits(n, width, hidden) * n * width * sizeof(float);
+}
+
+int starkv_write_kv(void* stream, const void* hidden, int64_t h_s0, const void* kv_down, int64_t w_s0, int w_dtype,
+                    int n, int hidden_size, int k_width, int v_rank, void* cache, int64_t c_s0, int64_t c_s1,
+                    int cache_dtype, int block_size, int64_t num_blocks, const void* slot_mapping, int slot_bits,
+                    int num_kv_heads, const int32_t* k_ranks, const int32_t* k_offsets, const int32_t* k_nouts,
+                    int row_bytes, void* codes_out, int64_t co_s0, void* workspace, size_t workspace_bytes) {
+    clear_error();
+    SKV_CHECK(n >= 0 && k_width > 0 && v_rank > 0 && hidden_size > 0, "write_kv: bad sizes");
+    SKV_CHECK(w_dtype == STARKV_BF16 || w_dtype == STARKV_F16, "write_kv: hidden and kv_down must be bf16 or fp16");
+    SKV_CHECK(hidden_size % 32 == 0, "write_kv: hidden size %d must be a multiple of 32", hidden_size);
+    SKV_CHECK(k_width % 16 == 0, "write_kv: k_width must be a multiple of 16 (head widths are)");
+    SKV_CHECK(block_size > 0, "write_kv: block_size must be positive");
+    SKV_CHECK(slot_bits == 32 || slot_bits == 64, "write_kv: slot_mapping must be int32 or int64");
+    SKV_CHECK(h_s0 >= hidden_size && w_s0 >= hidden_size && h_s0 % 8 == 0 && w_s0 % 8 == 0 &&
+                  ((uintptr_t)hidden % 16) == 0 && ((uintptr_t)kv_down % 16) == 0,
+              "write_kv: hidden and kv_down rows must be 16-byte aligned and at least hidden_size long");
+    const int width = k_width + v_rank;
+    const bool quant = row_bytes > 0;
+    RowLayout rl{};
+    if (quant) {
+        SKV_CHECK(num_kv_heads > 0, "write_kv: num_kv_heads must be positive");
+        rl = row_layout_host(k_width, num_kv_heads, v_rank);
+        SKV_CHECK(row_bytes == rl.nbytes, "write_kv: row_bytes %d != QuantRow.nbytes %d", row_bytes, rl.nbytes);
+        SKV_CHECK(c_s0 % 4 == 0 && c_s1 % 4 == 0 && ((uintptr_t)cache % 4) == 0,
+                  "write_kv: 3.2-bit cache base and byte strides must be multiples of 4");
+        SKV_CHECK(c_s1 >= row_bytes, "write_kv: cache slot stride %lld < row_bytes %d", (long long)c_s1, row_bytes);
+    } else {
+        SKV_CHECK(cache_dtype == w_dtype, "write_kv: the bf16/fp16 cache must have the model dtype");
+        SKV_CHECK(c_s1 >= width, "write_kv: cache slot stride %lld < %d codes", (long long)c_s1, width);
+    }
+    if (n == 0) return STARKV_OK;
+    SKV_CHECK(hidden && kv_down && cache && slot_mapping && workspace, "write_kv: null pointer");
+    SKV_CHECK(!quant || (k_ranks && k_offsets && k_nouts), "write_kv: null head arrays");
+    SKV_CHECK(!codes_out || co_s0 >= width, "write_kv: codes_out row stride %lld < %d", (long long)co_s0, width);
+    const int splits = kv_splits(n, width, hidden_size);
+    SKV_CHECK(workspace_bytes >= (size_t)splits * n * width * sizeof(float), "write_kv: workspace %zu bytes < %zu",
+              workspace_bytes, (size_t)splits * n * width * sizeof(float));
+    SKV_CHECK(((uintptr_t)workspace % 16) == 0, "write_kv: workspace must be 16-byte aligned");
+
+    KvGemmParams g;
+    g.hidden = (const uint16_t*)hidden; g.h_s0 = h_s0;
+    g.w = (const uint16_t*)kv_down; g.w_s0 = w_s0;
+    g.n = n; g.width = width; g.ksteps = hidden_size / 32; g.splits = splits;
+    g.part = (float*)workspace;
+    const dim3 ggrid((width + KVW_COLS - 1) / KVW_COLS, splits, (n + KVW_TOKENS - 1) / KVW_TOKENS);
+    KvStoreParams s;
+    s.part = g.part; s.splits = splits; s.n = n; s.width = width;
+    s.k_width = k_width; s.v_rank = v_rank;
+    s.codes = (uint16_t*)codes_out; s.co_s0 = co_s0;
+    s.cache = cache; s.c_s0 = c_s0; s.c_s1 = c_s1;
+    s.block_size = block_size; s.num_blocks = num_blocks;
+    s.slots = slot_mapping; s.slot_bits = slot_bits;
+    s.quant = quant; s.H = num_kv_heads; s.ranks = k_ranks; s.offsets = k_offsets; s.nouts = k_nouts;
+    s.row = rl;
+    const size_t lds = (size_t)width * sizeof(float);
+    SKV_CHECK(lds <= 64 * 1024, "write_kv: %d codes per token exceed the 64 KB LDS block", width);
+    hipStream_t st = (hipStream_t)stream;
+    if (w_dtype == STARKV_BF16) {
+        hipLaunchKernelGGL(kv_gemm_kernel<STARKV_BF16>, ggrid, dim3(KVW_THR), 0, st, g);
+        SKV_HIP(hipGetLastError());
+        hipLaunchKernelGGL(kv_store_kernel<STARKV_BF16>, dim3(n), dim3(KVW_THR), lds, st, s);
+    } else {
+        hipLaunchKernelGGL(kv_gemm_kernel<STARKV_F16>, ggrid, dim3(KVW_THR), 0, st, g);
+        SKV_HIP(hipGetLastError());
+        hipLaunchKernelGGL(kv_store_kernel<STARKV_F16>, dim3(n), dim3(KVW_THR), lds, st, s);
+    }
+    SKV_HIP(hipGetLastError());
+    return STARKV_OK;
+}
+
+}  // extern "C"

@@ -1,15 +1,10 @@
-// Cache write path: the bf16/fp16 code scatter and the 3.2-bit quantize + scatter.
-//
-// Quantizer semantics are those of kv_quant._q (kv_quant.py:111-120) as the
-// reference's Triton packers apply them (starkv_serve/kernels/paged_quant.py:146-202):
-// amax floored at fp32(1e-5), scale = amax / 7 (outliers) or / 3 (inliers) with IEEE
-// division, code = clamp(rint(x / scale)) + 8 with round-half-even, scales stored as
-// bfloat16 (round-to-nearest-even), the outlier scale stored as 1.0 when a block has
-// no outliers. One wave quantizes one (token, KV head) block, or the token's V latent.
+// Cache write path: the bf16/fp16 code scatter and the 3.2-bit quantize + scatter
+// (the quantizer and the row packing are in pack_rows.hpp). One wave quantizes one
+// (token, KV head) block, or the token's V latent.
 #include <stdarg.h>
 #include <stdio.h>
 
-#include "common.hpp"
+#include "pack_rows.hpp"
 
 namespace starkv {
 
@@ -23,19 +18,6 @@ void set_error(const char* fmt, ...) {
 }
 
 void clear_error() { g_err[0] = 0; }
-
-__device__ __forceinline__ int64_t load_slot(const void* slots, int bits, int i) {
-    int64_t s = bits == 64 ? ((const int64_t*)slots)[i] : (int64_t)((const int32_t*)slots)[i];
-    return s < 0 ? 0 : s;  // padding tokens carry -1: the null block (paged_quant.py:141-143)
-}
-
-// Slots past the cache (num_blocks * block_size) are skipped rather than written.
-
-__device__ __forceinline__ int quant_code(float x, float s, float lo, float hi) {
-    float q = rintf(__fdiv_rn(x, s));
-    q = fminf(fmaxf(q, lo), hi);
-    return (int)(q + 8.0f);
-}
 
 // ---------------------------------------------------------------------------
 // bf16/fp16 codes: one workgroup per token copies its K and V codes to the slot.
@@ -92,69 +74,15 @@ __global__ __launch_bounds__(256) void pack_kv_kernel(const PackParams p) {
     uint8_t* row = p.cache + (slot / p.block_size) * p.c_s0 + (slot % p.block_size) * p.c_s1;
 
     if (u < p.H) {
-        const int R = p.ranks[u], nout = p.nouts[u], off = p.offsets[u];
-        const int wh = ((R + 15) >> 4) << 4;  // stored width: lanes past R hold zero codes
-        const int64_t base = (int64_t)i * p.k_s0 + off;
-        float a_out = 0.f, a_in = 0.f;
-        for (int l = lane; l < wh; l += 64) {
-            float x = fabsf(load_f(p.k, base + l, p.dt));
-            if (l < nout) a_out = fmaxf(a_out, x); else a_in = fmaxf(a_in, x);
-        }
-        a_out = fmaxf(wave_max(a_out), 1e-5f);
-        a_in = fmaxf(wave_max(a_in), 1e-5f);
-        const float s_out = __fdiv_rn(a_out, 7.0f);
-        const float s_in = __fdiv_rn(a_in, 3.0f);
-        for (int kb = lane; 2 * kb < wh; kb += 64) {
-            int n0, n1;
-            {
-                int l = 2 * kb;
-                float x = load_f(p.k, base + l, p.dt);
-                n0 = l < nout ? quant_code(x, s_out, -8.f, 7.f) : quant_code(x, s_in, -4.f, 3.f);
-                x = load_f(p.k, base + l + 1, p.dt);
-                n1 = l + 1 < nout ? quant_code(x, s_out, -8.f, 7.f) : quant_code(x, s_in, -4.f, 3.f);
-            }
-            row[off / 2 + kb] = (uint8_t)(n0 | (n1 << 4));
-        }
-        if (lane == 0) {
-            uint16_t so = f32_to_bf16_rne(nout > 0 ? s_out : 1.0f), si = f32_to_bf16_rne(s_in);
-            *(uint32_t*)(row + p.ks_off + 4 * u) = (uint32_t)so | ((uint32_t)si << 16);
-        }
+        const int64_t base = (int64_t)i * p.k_s0 + p.offsets[u];
+        pack_k_block([&](int l) { return load_f(p.k, base + l, p.dt); }, p.ranks[u], p.nouts[u], p.offsets[u], u,
+                     p.ks_off, row, lane);
         return;
     }
-
-    // V latent: outlier channels [0, nout) at 4 bits, then inliers at 3 bits, each
-    // block byte-aligned; an odd block ends in a padding nibble 8 (paged_quant.py:184-199).
-    const int R = p.v_rank, nout = p.v_nout, nbo = p.v_nbo, nb = p.v_bytes;
     const int64_t base = (int64_t)i * p.v_s0;
-    float a_out = 0.f, a_in = 0.f;
-    for (int c = lane; c < R; c += 64) {
-        float x = fabsf(load_f(p.v, base + c, p.dt));
-        if (c < nout) a_out = fmaxf(a_out, x); else a_in = fmaxf(a_in, x);
-    }
-    a_out = fmaxf(wave_max(a_out), 1e-5f);
-    a_in = fmaxf(wave_max(a_in), 1e-5f);
-    const float s_out = __fdiv_rn(a_out, 7.0f);
-    const float s_in = __fdiv_rn(a_in, 3.0f);
-    for (int j = lane; j < nb; j += 64) {
-        const bool in_out = j < nbo;
-        const int c_lo = in_out ? 2 * j : nout + 2 * (j - nbo);
-        const int c_end = in_out ? nout : R;
-        const float s = in_out ? s_out : s_in;
-        const float lo = in_out ? -8.f : -4.f, hi = in_out ? 7.f : 3.f;
-        int nl = 8, nh = 8;
-        if (c_lo < c_end) nl = quant_code(load_f(p.v, base + c_lo, p.dt), s, lo, hi);
-        if (c_lo + 1 < c_end) nh = quant_code(load_f(p.v, base + c_lo + 1, p.dt), s, lo, hi);
-        row[p.vq_off + j] = (uint8_t)(nl | (nh << 4));
-    }
-    // The row's trailing pad bytes are defined here as zero.
-    for (int j = p.vq_off + nb + lane; j < p.row_bytes; j += 64) row[j] = 0;
-    if (lane == 0) {
-        uint16_t so = f32_to_bf16_rne(nout > 0 ? s_out : 1.0f), si = f32_to_bf16_rne(s_in);
-        *(uint32_t*)(row + p.vs_off) = (uint32_t)so | ((uint32_t)si << 16);
-    }
+    pack_v_block([&](int c) { return load_f(p.v, base + c, p.dt); }, p.v_rank, p.v_nout, p.v_nbo, p.v_bytes, p.vq_off,
+                 p.vs_off, p.row_bytes, row, lane);
 }
-
-static int n_outlier_host(int rank) { return (int)(0.2 * (double)rank); }
 
 }  // namespace starkv
 
@@ -202,13 +130,14 @@ int starkv_pack_kv(void* stream, const void* k_codes, int64_t k_s0, const void* 
     p.slots = slot_mapping; p.slot_bits = slot_bits; p.H = num_kv_heads;
     p.ranks = k_ranks; p.offsets = k_offsets; p.nouts = k_nouts;
     p.k_width = k_width; p.v_rank = v_rank;
-    p.v_nout = n_outlier_host(v_rank);
-    p.v_nbo = (p.v_nout + 1) / 2;
-    p.v_bytes = p.v_nbo + (v_rank - p.v_nout + 1) / 2;
-    p.ks_off = k_width / 2;
-    p.vs_off = p.ks_off + 4 * num_kv_heads;
-    p.vq_off = p.vs_off + 4;
-    p.row_bytes = (p.vq_off + p.v_bytes + 15) / 16 * 16;
+    const RowLayout rl = row_layout_host(k_width, num_kv_heads, v_rank);
+    p.v_nout = rl.v_nout;
+    p.v_nbo = rl.v_nbo;
+    p.v_bytes = rl.v_bytes;
+    p.ks_off = rl.ks_off;
+    p.vs_off = rl.vs_off;
+    p.vq_off = rl.vq_off;
+    p.row_bytes = rl.nbytes;
     SKV_CHECK(row_bytes == p.row_bytes, "pack_kv: row_bytes %d != QuantRow.nbytes %d", row_bytes, p.row_bytes);
     if (n == 0) return STARKV_OK;
     SKV_CHECK(k_codes && v_codes && cache && slot_mapping && k_ranks && k_offsets && k_nouts, "pack_kv: null pointer");

@@ -1,0 +1,110 @@
+// 3.2-bit row packing of one (token, KV head) K block or one token's V latent, shared by
+// the pack_kv kernel (codes read from memory) and the fused write kernel (codes in LDS).
+//
+// Quantizer semantics are those of kv_quant._q (kv_quant.py:111-120) as the reference's
+// Triton packers apply them (starkv_serve/kernels/paged_quant.py:146-202): amax floored
+// at fp32(1e-5), scale = amax / 7 (outliers) or / 3 (inliers) with IEEE division,
+// code = clamp(rint(x / scale)) + 8 with round-half-even, scales stored as bfloat16
+// (round-to-nearest-even), the outlier scale stored as 1.0 when a block has no outliers.
+// Every function is called by one whole wave (the amax is a wave reduction).
+#pragma once
+
+#include "common.hpp"
+
+namespace starkv {
+
+// Slot of token i; padding tokens carry -1: the null block (paged_quant.py:141-143).
+// Callers skip slots past the cache (num_blocks * block_size) rather than write them.
+__device__ __forceinline__ int64_t load_slot(const void* slots, int bits, int i) {
+    const int64_t s = bits == 64 ? ((const int64_t*)slots)[i] : (int64_t)((const int32_t*)slots)[i];
+    return s < 0 ? 0 : s;
+}
+
+__device__ __forceinline__ int quant_code(float x, float s, float lo, float hi) {
+    float q = rintf(__fdiv_rn(x, s));
+    q = fminf(fmaxf(q, lo), hi);
+    return (int)(q + 8.0f);
+}
+
+// K block of KV head u: rank R, `nout` outlier lanes, first lane `off` of the row;
+// src(l) is the code of the head's lane l, l < align16(R) (lanes past R hold zero codes
+// and count as inliers, paged_quant.py:150-163). Nibbles go to row[off / 2 ..], the two
+// bf16 scales to row[ks_off + 4 u].
+template <class Src>
+__device__ __forceinline__ void pack_k_block(Src&& src, int R, int nout, int off, int u, int ks_off, uint8_t* row,
+                                             int lane) {
+    const int wh = ((R + 15) >> 4) << 4;
+    float a_out = 0.f, a_in = 0.f;
+    for (int l = lane; l < wh; l += 64) {
+        const float x = fabsf(src(l));
+        if (l < nout) a_out = fmaxf(a_out, x); else a_in = fmaxf(a_in, x);
+    }
+    a_out = fmaxf(wave_max(a_out), 1e-5f);
+    a_in = fmaxf(wave_max(a_in), 1e-5f);
+    const float s_out = __fdiv_rn(a_out, 7.0f);
+    const float s_in = __fdiv_rn(a_in, 3.0f);
+    for (int kb = lane; 2 * kb < wh; kb += 64) {
+        const int l = 2 * kb;
+        const int n0 = l < nout ? quant_code(src(l), s_out, -8.f, 7.f) : quant_code(src(l), s_in, -4.f, 3.f);
+        const int n1 = l + 1 < nout ? quant_code(src(l + 1), s_out, -8.f, 7.f) : quant_code(src(l + 1), s_in, -4.f, 3.f);
+        row[off / 2 + kb] = (uint8_t)(n0 | (n1 << 4));
+    }
+    if (lane == 0) {
+        const uint16_t so = f32_to_bf16_rne(nout > 0 ? s_out : 1.0f), si = f32_to_bf16_rne(s_in);
+        *(uint32_t*)(row + ks_off + 4 * u) = (uint32_t)so | ((uint32_t)si << 16);
+    }
+}
+
+// V latent of rank R: outlier channels [0, nout) at 4 bits, then inliers at 3 bits,
+// each block byte-aligned (nbo outlier bytes, nb bytes in all); an odd block ends in a
+// padding nibble 8 (paged_quant.py:184-199). src(c) is channel c. Bytes
+// [vq_off + nb, row_bytes) are written as zero (the reference leaves them unwritten).
+template <class Src>
+__device__ __forceinline__ void pack_v_block(Src&& src, int R, int nout, int nbo, int nb, int vq_off, int vs_off,
+                                             int row_bytes, uint8_t* row, int lane) {
+    float a_out = 0.f, a_in = 0.f;
+    for (int c = lane; c < R; c += 64) {
+        const float x = fabsf(src(c));
+        if (c < nout) a_out = fmaxf(a_out, x); else a_in = fmaxf(a_in, x);
+    }
+    a_out = fmaxf(wave_max(a_out), 1e-5f);
+    a_in = fmaxf(wave_max(a_in), 1e-5f);
+    const float s_out = __fdiv_rn(a_out, 7.0f);
+    const float s_in = __fdiv_rn(a_in, 3.0f);
+    for (int j = lane; j < nb; j += 64) {
+        const bool in_out = j < nbo;
+        const int c_lo = in_out ? 2 * j : nout + 2 * (j - nbo);
+        const int c_end = in_out ? nout : R;
+        const float s = in_out ? s_out : s_in;
+        const float lo = in_out ? -8.f : -4.f, hi = in_out ? 7.f : 3.f;
+        int nl = 8, nh = 8;
+        if (c_lo < c_end) nl = quant_code(src(c_lo), s, lo, hi);
+        if (c_lo + 1 < c_end) nh = quant_code(src(c_lo + 1), s, lo, hi);
+        row[vq_off + j] = (uint8_t)(nl | (nh << 4));
+    }
+    for (int j = vq_off + nb + lane; j < row_bytes; j += 64) row[j] = 0;
+    if (lane == 0) {
+        const uint16_t so = f32_to_bf16_rne(nout > 0 ? s_out : 1.0f), si = f32_to_bf16_rne(s_in);
+        *(uint32_t*)(row + vs_off) = (uint32_t)so | ((uint32_t)si << 16);
+    }
+}
+
+// QuantRow (paged_quant.py:71-111) on the host: V outlier channels, V outlier bytes,
+// V bytes, K-scale / V-scale / V-code offsets and the row size (16-byte aligned).
+struct RowLayout {
+    int v_nout, v_nbo, v_bytes, ks_off, vs_off, vq_off, nbytes;
+};
+static inline int n_outlier_host(int rank) { return (int)(0.2 * (double)rank); }
+static inline RowLayout row_layout_host(int k_width, int num_kv_heads, int v_rank) {
+    RowLayout r;
+    r.v_nout = n_outlier_host(v_rank);
+    r.v_nbo = (r.v_nout + 1) / 2;
+    r.v_bytes = r.v_nbo + (v_rank - r.v_nout + 1) / 2;
+    r.ks_off = k_width / 2;
+    r.vs_off = r.ks_off + 4 * num_kv_heads;
+    r.vq_off = r.vs_off + 4;
+    r.nbytes = (r.vq_off + r.v_bytes + 15) / 16 * 16;
+    return r;
+}
+
+}  // namespace starkv

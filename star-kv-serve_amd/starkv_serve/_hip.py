@@ -29,6 +29,9 @@ SIGNATURES = {
     "starkv_pack_kv": (_I, [_P, _P, _I64, _P, _I64, _I, _P, _I64, _I64, _I, _I64, _P, _I, _I, _I, _P, _P, _P,
                             _I, _I, _I]),
     "starkv_fold_q": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I, _P, _I, _I, _F, _P]),
+    "starkv_write_kv_workspace_bytes": (_SZ, [_I, _I, _I]),
+    "starkv_write_kv": (_I, [_P, _P, _I64, _P, _I64, _I, _I, _I, _I, _I, _P, _I64, _I64, _I, _I, _I64, _P, _I,
+                             _I, _P, _P, _P, _I, _P, _I64, _P, _SZ]),
     "starkv_decode_grid": (_I, [_I, _I]),
     "starkv_profile_begin": (_I, [_I]),
     "starkv_profile_end": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),

@@ -20,7 +20,7 @@ def test_header_declares_the_api():
     names = declared()
     for n in ("starkv_lowrank_decode", "starkv_quant_decode", "starkv_pack_kv", "starkv_write_codes",
               "starkv_fold_q", "starkv_decode_grid", "starkv_decode_workspace_bytes", "starkv_last_error",
-              "starkv_abi_version"):
+              "starkv_abi_version", "starkv_write_kv", "starkv_write_kv_workspace_bytes"):
         assert n in names
 
 
@@ -52,3 +52,32 @@ def test_workspace_size_is_a_host_function():
     a = L.starkv_decode_workspace_bytes(64, 32, 80, 64, 256)
     b = L.starkv_decode_workspace_bytes(64, 32, 80, 64, 128)
     assert a > b > 64 * 80 * 4096
+
+
+def test_write_kv_validation():
+    """Fused write: argument checks return errors before any launch (no GPU here)."""
+    from starkv_serve import _hip
+    L = _hip.lib()
+    F32, F16, BF16 = 0, 1, 2
+
+    def call(**kw):
+        a = dict(stream=None, hidden=None, h_s0=4096, kv_down=None, w_s0=4096, w_dtype=BF16, n=0, hidden_size=4096,
+                 k_width=1280, v_rank=64, cache=None, c_s0=0, c_s1=1344, cache_dtype=BF16, block_size=16,
+                 num_blocks=1, slots=None, slot_bits=32, heads=32, ranks=None, offsets=None, nouts=None,
+                 row_bytes=0, codes=None, co_s0=0, ws=None, ws_bytes=0)
+        a.update(kw)
+        return L.starkv_write_kv(*a.values())
+
+    assert call() == 0  # n = 0: nothing to do
+    assert call(w_dtype=F32) != 0 and b"bf16 or fp16" in L.starkv_last_error()
+    assert call(hidden_size=4016, h_s0=4016, w_s0=4016) != 0 and b"multiple of 32" in L.starkv_last_error()
+    assert call(k_width=1288) != 0 and b"multiple of 16" in L.starkv_last_error()
+    assert call(slot_bits=16) != 0 and b"int32 or int64" in L.starkv_last_error()
+    assert call(cache_dtype=F16) != 0 and b"model dtype" in L.starkv_last_error()
+    assert call(row_bytes=800) != 0 and b"QuantRow.nbytes 816" in L.starkv_last_error()
+    assert call(row_bytes=816, c_s1=800) != 0 and b"slot stride" in L.starkv_last_error()
+    assert call(n=1) != 0 and b"null pointer" in L.starkv_last_error()
+    # workspace: split-K partials, a pure function of (n, width, hidden)
+    assert L.starkv_write_kv_workspace_bytes(64, 1344, 4096) == 16 * 64 * 1344 * 4
+    assert L.starkv_write_kv_workspace_bytes(1024, 1344, 4096) == 1 * 1024 * 1344 * 4
+    assert L.starkv_write_kv_workspace_bytes(0, 1344, 4096) == 0
