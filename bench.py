@@ -96,6 +96,67 @@ def bench_quant(lengths, steps, warmup, seed, copies, v_rank=64):
     return wl, ms, kern
 
 
+def bench_write(n, quant, steps, warmup, seed=1004, layers=24, hidden=4096, num_heads=32, v_rank=64):
+    """One layer step of the cache write for n tokens: the fused write_kv (kv_down GEMM +
+    scatter / 3.2-bit pack) against the unfused sequence (F.linear, then the scatter or
+    pack_kv), rotating over `layers` kv_down matrices (264 MB: more than the Infinity
+    Cache, as a model's layers are). Algorithmic bytes per step: kv_down + hidden read,
+    the rows written, the slots."""
+    import torch
+    import torch.nn.functional as F
+    from starkv_serve import workloads as W
+    from starkv_serve.kernels.kv_write import write_codes, write_kv
+    from starkv_serve.kernels.paged_quant import QuantRow, k_tables, pack_kv
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(seed)
+    ranks = [W.RANK_CHOICES[i] for i in torch.randint(0, len(W.RANK_CHOICES), (num_heads,), generator=g).tolist()]
+    k_width = sum(ranks)  # every rank a multiple of 16
+    width = k_width + v_rank
+    offsets = torch.tensor([sum(ranks[:h]) for h in range(num_heads)], dtype=torch.int32, device=dev)
+    k_ranks = torch.tensor(ranks, dtype=torch.int32, device=dev)
+    kv_down = [(torch.randn(width, hidden, device=dev) * hidden ** -0.5).to(torch.bfloat16) for _ in range(layers)]
+    x = torch.randn(n, hidden, device=dev).to(torch.bfloat16)
+    nb = 4096
+    slots = (torch.randperm(nb * 16, device=dev)[:n]).to(torch.int64)
+    if quant:
+        row = QuantRow(k_width, num_heads, v_rank)
+        nouts, _, _ = k_tables(ranks, dev)
+        cache = torch.zeros(nb, 16, row.nbytes, dtype=torch.uint8, device=dev)
+        row_bytes = row.nbytes
+        fused = lambda i: write_kv(x, kv_down[i % layers], cache, slots, k_width, row=row, k_ranks=k_ranks,
+                                   k_offsets=offsets, k_nouts=nouts)
+
+        def unfused(i):
+            c = F.linear(x, kv_down[i % layers])
+            pack_kv(c[:, :k_width], c[:, k_width:], cache, slots, row, k_ranks, offsets, nouts)
+    else:
+        cache = torch.zeros(nb, 16, width, dtype=torch.bfloat16, device=dev)
+        row_bytes = 2 * width
+        fused = lambda i: write_kv(x, kv_down[i % layers], cache, slots, k_width)
+
+        def unfused(i):
+            c = F.linear(x, kv_down[i % layers])
+            write_codes(c[:, :k_width], c[:, k_width:], cache, slots)
+
+    def timed(fn):
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(steps):
+            fn(i)
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / steps * 1e3
+
+    fu, un = timed(fused), timed(unfused)
+    by = width * hidden * 2 + n * hidden * 2 + n * row_bytes + n * 8
+    return dict(tokens=n, cache="3.2-bit" if quant else "bf16", hidden=hidden, k_width=k_width, v_rank=v_rank,
+                fused_us=round(fu, 2), unfused_us=round(un, 2), bytes_per_step=by,
+                GBps=round(by / (fu * 1e-6) / 1e9, 1), hbm_frac=round(by / (fu * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+
+
 def measured_traffic(key):
     """HBM bytes per launch for `key` from the committed counter summary, or None."""
     import re
@@ -175,7 +236,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true", help="skip the 3.2-bit and ragged configurations")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["bf16", "quant"], default=None,
+    ap.add_argument("--only", choices=["bf16", "quant", "write"], default=None,
                     help="profile runs: time one bs64 x 8192 workload only and print its summary")
     ap.add_argument("--copy-probe", type=float, default=0.0, metavar="GIB",
                     help="profile runs: only copy GIB GiB device to device 5 times (counter scaling)")
@@ -193,6 +254,11 @@ def main():
         return
 
     lengths = [8192] * 64
+    if args.only == "write":
+        for n_tok in (16, 64):
+            for quant in (True, False):
+                print(json.dumps(bench_write(n_tok, quant, args.steps, args.warmup)), flush=True)
+        return
     if args.only == "quant":
         wq, msq, kq = bench_quant(lengths, args.steps, args.warmup, seed=1003, copies=3)
         print(json.dumps(summarize(wq, msq, kq)), flush=True)
@@ -226,6 +292,13 @@ def main():
         extra["quant_bs64_ragged_1k_8k"] = summarize(w2, ms2, k2)
         log(json.dumps(extra["quant_bs64_ragged_1k_8k"]))
         del w2
+        torch.cuda.empty_cache()
+        for n_tok in (16, 64):
+            for quant in (True, False):
+                key = f"write_{'quant' if quant else 'bf16'}_n{n_tok}"
+                log(f"cache write, {n_tok} tokens, {'3.2-bit' if quant else 'bf16'} (fused vs unfused)")
+                extra[key] = bench_write(n_tok, quant, args.steps, args.warmup)
+                log(json.dumps(extra[key]))
         torch.cuda.empty_cache()
 
     cpu = None

@@ -65,7 +65,7 @@ int starkv_write_codes(void *stream, const void *k_codes, int64_t k_s0, const vo
  * pack_kv of the rounded codes).
  *   hidden    [n, hidden_size], row stride h_s0 elements, bf16 or fp16 (w_dtype)
  *   kv_down   [k_width + v_rank, hidden_size], row stride w_s0, same dtype; rows 16-byte
- *             aligned, hidden_size a multiple of 32
+ *             aligned, hidden_size a multiple of 64
  *   cache     row_bytes == 0: [num_blocks, block_size, >= k_width + v_rank] of the model
  *             dtype (cache_dtype == w_dtype), element strides c_s0, c_s1;
  *             row_bytes > 0: uint8 [num_blocks, block_size, row_bytes], byte strides

@@ -9,10 +9,10 @@
 // 1. kv_gemm_kernel: split-K partial products. Workgroup (code tile t of 64, K split s,
 //    token block of 64) has 4 waves; wave w takes codes [64 t + 16 w, +16) and the
 //    block's tokens in 16-row MFMA tiles over split s with v_mfma_f32_16x16x32 (A = 16
-//    hidden rows x 32 channels, B = 32 channels x 16 kv_down rows), and writes fp32
-//    partials [s][token][code]. kv_down (the layer's only large operand) is read once,
+//    hidden rows x 32 channels, B = 32 channels x 16 kv_down rows; channels in an order
+//    that reads whole 128-byte lines), and writes fp32 partials [s][token][code]. kv_down (the layer's only large operand) is read once,
 //    spread over ~256+ workgroups.
-// 2. kv_store_kernel: one workgroup per token sums its partials in a fixed order, rounds
+// 2. kv_store_kernel: one workgroup per token sums its partials in split order, rounds
 //    every code to the model dtype (the dtype F.linear returns, round-to-nearest-even),
 //    optionally writes the rounded codes out, and stores the row: the codes themselves
 //    (bf16/fp16 cache) or the packed 3.2-bit row, the packers reading the rounded codes
@@ -21,7 +21,8 @@
 
 namespace starkv {
 
-constexpr int KVW_THR = 256;
+constexpr int KVW_THR = 256;    // GEMM workgroup
+constexpr int KVS_THR = 1024;   // store workgroup (one token)
 constexpr int KVW_COLS = 64;    // codes per GEMM workgroup (4 waves x 16)
 constexpr int KVW_TOKENS = 64;  // tokens per GEMM workgroup (4 MFMA row tiles)
 constexpr int KVW_MAX_SPLIT = 16;
@@ -44,13 +45,46 @@ __device__ __forceinline__ f32x4_t mfma_16x16x32(uint4 a, uint4 b, f32x4_t c) {
                                                       0, 0, 0);
 }
 
+// K steps [k0, k1) of one wave: TILES row tiles (uniform per workgroup) x 16 codes.
+// The channel sum is order-free, so the channels go to MFMA steps in an order that
+// reads whole lines: over steps 2m and 2m + 1, lane group g (lane / 16) supplies
+// channels 64 m + 16 g .. + 8 and then + 8 .. + 16 of its row, 32 contiguous bytes,
+// and the 4 groups cover the row's 128 bytes; A (hidden) and B (kv_down) use the same
+// order. Every load of a chunk of KVW_CHUNK steps is issued before its first MFMA; pairs
+// past the split's end reload its last pair with B zeroed (no branch between loads).
+template <int DT, int TILES>
+__device__ __forceinline__ void kv_gemm_steps(const uint16_t* wr, const uint16_t* const (&ar)[4], int k0, int k1,
+                                              f32x4_t (&acc)[4]) {
+    for (int kc = k0; kc < k1; kc += KVW_CHUNK) {
+        uint4 b[KVW_CHUNK], a[KVW_CHUNK][TILES];
+#pragma unroll
+        for (int j = 0; j < KVW_CHUNK; j += 2) {
+            const int m = min(kc + j, k1 - 2) >> 1;  // the pair's 64-channel block
+            b[j] = *(const uint4*)(wr + 64 * m);
+            b[j + 1] = *(const uint4*)(wr + 64 * m + 8);
+#pragma unroll
+            for (int t = 0; t < TILES; ++t) {
+                a[j][t] = *(const uint4*)(ar[t] + 64 * m);
+                a[j + 1][t] = *(const uint4*)(ar[t] + 64 * m + 8);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < KVW_CHUNK; ++j) {
+            const uint4 bj = kc + j < k1 ? b[j] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < TILES; ++t) acc[t] = mfma_16x16x32<DT>(a[j][t], bj, acc[t]);
+        }
+    }
+}
+
 template <int DT>
 __global__ __launch_bounds__(KVW_THR) void kv_gemm_kernel(const KvGemmParams p) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int s = blockIdx.y, m0 = KVW_TOKENS * blockIdx.z;
     const int col = KVW_COLS * blockIdx.x + 16 * wave + (lane & 15);  // this lane's B column (code)
-    const int kq = 8 * (lane >> 4);                                    // its 8 channels of each 32
-    const int k0 = s * p.ksteps / p.splits, k1 = (s + 1) * p.ksteps / p.splits;
+    const int kq = 16 * (lane >> 4);                                   // its 16 channels of each 64
+    // Splits cover whole pairs of K steps (ksteps is even: hidden is a multiple of 64).
+    const int k0 = 2 * (s * (p.ksteps / 2) / p.splits), k1 = 2 * ((s + 1) * (p.ksteps / 2) / p.splits);
     const int tiles = min(4, (p.n - m0 + 15) / 16);  // row tiles with tokens (uniform)
     // Rows past the code or token range read row width - 1 / n - 1 (valid memory);
     // their products are never stored.
@@ -61,24 +95,11 @@ __global__ __launch_bounds__(KVW_THR) void kv_gemm_kernel(const KvGemmParams p) 
     f32x4_t acc[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    // K steps go in chunks of KVW_CHUNK: every load of a chunk is issued before its
-    // first MFMA. Every row tile runs, past-n rows included, and steps past the split's
-    // end reload its last step with B zeroed, so nothing branches between the loads.
-    for (int kc = k0; kc < k1; kc += KVW_CHUNK) {
-        uint4 b[KVW_CHUNK], a[KVW_CHUNK][4];
-#pragma unroll
-        for (int j = 0; j < KVW_CHUNK; ++j) {
-            const int k = min(kc + j, k1 - 1);
-            b[j] = *(const uint4*)(wr + 32 * k);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) a[j][t] = *(const uint4*)(ar[t] + 32 * k);
-        }
-#pragma unroll
-        for (int j = 0; j < KVW_CHUNK; ++j) {
-            const uint4 bj = kc + j < k1 ? b[j] : make_uint4(0, 0, 0, 0);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) acc[t] = mfma_16x16x32<DT>(a[j][t], bj, acc[t]);
-        }
+    switch (tiles) {
+        case 1: kv_gemm_steps<DT, 1>(wr, ar, k0, k1, acc); break;
+        case 2: kv_gemm_steps<DT, 2>(wr, ar, k0, k1, acc); break;
+        case 3: kv_gemm_steps<DT, 3>(wr, ar, k0, k1, acc); break;
+        default: kv_gemm_steps<DT, 4>(wr, ar, k0, k1, acc); break;
     }
     if (col >= p.width) return;
     // acc[t][e] = code `col` of token m0 + 16 t + 4 (lane >> 4) + e.
@@ -115,25 +136,43 @@ __device__ __forceinline__ float code_value(uint16_t r) {
 }
 
 template <int DT>
-__global__ __launch_bounds__(KVW_THR) void kv_store_kernel(const KvStoreParams p) {
+__global__ __launch_bounds__(KVS_THR) void kv_store_kernel(const KvStoreParams p) {
     extern __shared__ float s_code[];  // [width]: the token's rounded codes
     const int i = blockIdx.x, tid = threadIdx.x;
     const int64_t slot = load_slot(p.slots, p.slot_bits, i);
     const bool store = slot < p.num_blocks * p.block_size;  // slots past the cache are skipped
     const int64_t row = (slot / p.block_size) * p.c_s0 + (slot % p.block_size) * p.c_s1;
-    for (int c = tid; c < p.width; c += KVW_THR) {
-        float a = 0.f;
-        for (int s = 0; s < p.splits; ++s) a += p.part[((int64_t)s * p.n + i) * p.width + c];
-        const uint16_t r = round_code<DT>(a);
-        s_code[c] = code_value<DT>(r);
-        if (p.codes) p.codes[(int64_t)i * p.co_s0 + c] = r;
-        if (!p.quant && store) ((uint16_t*)p.cache)[row + c] = r;
+    // Columns c0 + tid and c0 + tid + KVS_THR: every split's partial of both is loaded
+    // before the first add (indices clamped, so no branch sits between the loads), then
+    // summed in split order.
+    for (int c0 = 0; c0 < p.width; c0 += 2 * KVS_THR) {
+        float v[2][KVW_MAX_SPLIT];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int c = min(c0 + tid + j * KVS_THR, p.width - 1);
+#pragma unroll
+            for (int sp = 0; sp < KVW_MAX_SPLIT; ++sp)
+                v[j][sp] = p.part[((int64_t)min(sp, p.splits - 1) * p.n + i) * p.width + c];
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int c = c0 + tid + j * KVS_THR;
+            float a = v[j][0];
+#pragma unroll
+            for (int sp = 1; sp < KVW_MAX_SPLIT; ++sp) a = sp < p.splits ? a + v[j][sp] : a;
+            if (c < p.width) {
+                const uint16_t r = round_code<DT>(a);
+                s_code[c] = code_value<DT>(r);
+                if (p.codes) p.codes[(int64_t)i * p.co_s0 + c] = r;
+                if (!p.quant && store) ((uint16_t*)p.cache)[row + c] = r;
+            }
+        }
     }
     if (!p.quant || !store) return;
     __syncthreads();
     const int lane = tid & 63;
     uint8_t* dst = (uint8_t*)p.cache + row;
-    for (int u = tid >> 6; u <= p.H; u += KVW_THR / 64) {
+    for (int u = tid >> 6; u <= p.H; u += KVS_THR / 64) {
         if (u < p.H) {
             const float* src = s_code + p.offsets[u];
             pack_k_block([&](int l) { return src[l]; }, p.ranks[u], p.nouts[u], p.offsets[u], u, p.row.ks_off, dst,
@@ -152,7 +191,7 @@ static int kv_splits(int n, int width, int hidden) {
     const int tiles = ((width + KVW_COLS - 1) / KVW_COLS) * ((n + KVW_TOKENS - 1) / KVW_TOKENS);
     const int ksteps = hidden / 32;
     int s = 1;
-    while (s < KVW_MAX_SPLIT && 2 * s * KVW_CHUNK <= ksteps && tiles * s < 256) s *= 2;
+    while (s < KVW_MAX_SPLIT && 2 * s * KVW_CHUNK <= ksteps && tiles * s < 256) s *= 2;  // ksteps even
     return s;
 }
 
@@ -175,7 +214,7 @@ int starkv_write_kv(void* stream, const void* hidden, int64_t h_s0, const void* 
     clear_error();
     SKV_CHECK(n >= 0 && k_width > 0 && v_rank > 0 && hidden_size > 0, "write_kv: bad sizes");
     SKV_CHECK(w_dtype == STARKV_BF16 || w_dtype == STARKV_F16, "write_kv: hidden and kv_down must be bf16 or fp16");
-    SKV_CHECK(hidden_size % 32 == 0, "write_kv: hidden size %d must be a multiple of 32", hidden_size);
+    SKV_CHECK(hidden_size % 64 == 0, "write_kv: hidden size %d must be a multiple of 64", hidden_size);
     SKV_CHECK(k_width % 16 == 0, "write_kv: k_width must be a multiple of 16 (head widths are)");
     SKV_CHECK(block_size > 0, "write_kv: block_size must be positive");
     SKV_CHECK(slot_bits == 32 || slot_bits == 64, "write_kv: slot_mapping must be int32 or int64");
@@ -226,11 +265,11 @@ int starkv_write_kv(void* stream, const void* hidden, int64_t h_s0, const void* 
     if (w_dtype == STARKV_BF16) {
         hipLaunchKernelGGL(kv_gemm_kernel<STARKV_BF16>, ggrid, dim3(KVW_THR), 0, st, g);
         SKV_HIP(hipGetLastError());
-        hipLaunchKernelGGL(kv_store_kernel<STARKV_BF16>, dim3(n), dim3(KVW_THR), lds, st, s);
+        hipLaunchKernelGGL(kv_store_kernel<STARKV_BF16>, dim3(n), dim3(KVS_THR), lds, st, s);
     } else {
         hipLaunchKernelGGL(kv_gemm_kernel<STARKV_F16>, ggrid, dim3(KVW_THR), 0, st, g);
         SKV_HIP(hipGetLastError());
-        hipLaunchKernelGGL(kv_store_kernel<STARKV_F16>, dim3(n), dim3(KVW_THR), lds, st, s);
+        hipLaunchKernelGGL(kv_store_kernel<STARKV_F16>, dim3(n), dim3(KVS_THR), lds, st, s);
     }
     SKV_HIP(hipGetLastError());
     return STARKV_OK;

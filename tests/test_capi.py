@@ -70,7 +70,7 @@ def test_write_kv_validation():
 
     assert call() == 0  # n = 0: nothing to do
     assert call(w_dtype=F32) != 0 and b"bf16 or fp16" in L.starkv_last_error()
-    assert call(hidden_size=4016, h_s0=4016, w_s0=4016) != 0 and b"multiple of 32" in L.starkv_last_error()
+    assert call(hidden_size=4000, h_s0=4000, w_s0=4000) != 0 and b"multiple of 64" in L.starkv_last_error()
     assert call(k_width=1288) != 0 and b"multiple of 16" in L.starkv_last_error()
     assert call(slot_bits=16) != 0 and b"int32 or int64" in L.starkv_last_error()
     assert call(cache_dtype=F16) != 0 and b"model dtype" in L.starkv_last_error()
