@@ -97,3 +97,24 @@ def test_write_codes_matches_index_put(cuda, dtype):
     _hip.check(rc, "write_codes")
     torch.cuda.synchronize()
     assert torch.equal(cache, want)
+
+
+@pytest.mark.parametrize("qdt,udt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)])
+def test_fold_q_matches_oracle(cuda, qdt, udt):
+    """starkv_fold_q: A|B of paged_quant.py:241-255 in fp16, against the float64 oracle
+    (one fp16 rounding of an fp32 product: relative error <= 2^-11 of |A|B|, plus the
+    fp32 rounding of two products)."""
+    print(f"\n[fold_q] q {qdt}, k_up {udt}", flush=True)
+    g = torch.Generator().manual_seed(12)
+    ranks = [16, 48, 20, 64]
+    nouts, lanes, _ = pq.k_tables(ranks, "cpu")
+    W = lanes.numel()
+    q = torch.randn(5, len(ranks), 128, generator=g).to(qdt)
+    U = (torch.randn(W, 128, generator=g) * 0.3).to(udt)
+    ab = pq.fold_q(q.to(cuda), U.to(cuda), lanes.to(cuda), 0.125)
+    torch.cuda.synchronize()
+    want = ref.fold_q(q.float().numpy(), U.float().numpy(), lanes.numpy(), 0.125)
+    got = ab.float().cpu().numpy()
+    assert got.shape == want.shape and ab.dtype == torch.float16
+    err = np.abs(got - want)
+    assert np.all(err <= np.abs(want) * 2.0 ** -10 + 1e-6), float(err.max())
