@@ -236,3 +236,22 @@ def test_quant_bs64_ragged_full_size(cuda):
     out = paged_quant_decode(*wl.decode_args())
     torch.cuda.synchronize()
     assert_close(out, quant_truth(wl), "quant_bs64_ragged")
+
+
+@pytest.mark.parametrize("quant", [False, True])
+def test_more_requests_than_one_launch(cuda, quant):
+    """1100 requests: the wrappers split the batch into library calls of at most 1024
+    requests (attention.py:194-213 dispatches any batch); every request still matches."""
+    g = torch.Generator().manual_seed(77)
+    lengths = torch.randint(1, 48, (1100,), generator=g).tolist()
+    print(f"\n[chunked] quant={quant} {len(lengths)} requests, {sum(lengths)} tokens", flush=True)
+    if quant:
+        wl = W.make_quant(lengths, num_heads=8, ranks=[16, 32, 48, 64, 16, 32, 48, 64], seed=78, device=cuda)
+        out = paged_quant_decode(*wl.decode_args())
+        torch.cuda.synchronize()
+        assert_close(out, quant_truth(wl), "chunked quant")
+    else:
+        wl = W.make_lowrank(lengths, num_heads=8, seed=78).to(cuda)
+        out = paged_starkv_decode(*wl.decode_args())
+        torch.cuda.synchronize()
+        assert_close(out, lowrank_truth(wl), "chunked bf16")
