@@ -1,0 +1,174 @@
+"""The attention backend's per-layer implementation, over the MI355X library.
+
+This restates ``StarKVAttentionImpl`` of the reference's vLLM backend
+(starkv_serve/attention.py:105-217) with the same constructor arguments, checks and
+errors, the same ``to_device`` attributes and the same ``forward`` contract:
+
+- ``forward`` writes this step's K/V codes into the paged cache, then decodes every
+  single-token request against the cache (attention.py:168-213).
+- The bf16/fp16 write is ``write_codes``; the 3.2-bit write is ``pack_kv``.
+- The decode is ``paged_starkv_decode`` / ``paged_quant_decode``.
+- ``write_from_hidden`` is the fused route for the codes' own GEMM (model.py:71 + the
+  write): one ``write_kv`` call from the layer's hidden states.
+
+vLLM is not needed to import or run this module. The two values the reference reads
+from vLLM are taken from it when it is importable, else from arguments:
+
+- the model's ``max_model_len`` (``get_current_vllm_config``);
+- whether the step runs inside a full CUDA/HIP graph (``get_forward_context``).
+
+Differences from the reference, by design:
+
+- Dense prefill (attention.py:219-251, FlashAttention over lifted K/V) is not part of
+  this library. A batch with prefill tokens raises ``NotImplementedError`` before any
+  work is enqueued.
+- The reference splits large decode batches so that its logits buffer stays under
+  2^26 floats (attention.py:52, 198-199). These kernels keep logits on chip and need
+  no such buffer; the decode wrappers only split batches above 1024 requests.
+"""
+from dataclasses import dataclass
+from typing import List, Optional
+
+import torch
+
+from starkv_serve.checkpoint import StarKVLayerWeights, layer_operands
+from starkv_serve.kernels.kv_write import write_codes, write_kv
+from starkv_serve.kernels.paged_decode import paged_starkv_decode
+from starkv_serve.kernels.paged_quant import HEAD_DIM, pack_kv, paged_quant_decode
+
+DECODER = "decoder"  # AttentionType.DECODER
+
+
+@dataclass
+class StarKVMetadata:
+    """One step's batch, decodes first (attention.py:55-67)."""
+    num_actual_tokens: int
+    num_decodes: int
+    num_decode_tokens: int
+    num_prefills: int
+    max_seq_len: int
+    seq_lens: torch.Tensor       # [>= num_decodes] int32, length including this step's token
+    block_table: torch.Tensor    # [>= num_decodes, max_blocks] int32
+    slot_mapping: torch.Tensor   # [>= num_actual_tokens] int64 (-1: padding token)
+    prefill_seq_lens_cpu: Optional[List[int]] = None
+    prefill_query_start_loc_cpu: Optional[List[int]] = None
+
+
+def _vllm_max_model_len() -> Optional[int]:
+    try:
+        from vllm.config import get_current_vllm_config
+    except ImportError:
+        return None
+    return get_current_vllm_config().model_config.max_model_len
+
+
+def _vllm_in_full_graph() -> bool:
+    try:
+        from vllm.config import CUDAGraphMode
+        from vllm.forward_context import get_forward_context
+    except ImportError:
+        return False
+    return get_forward_context().cudagraph_runtime_mode == CUDAGraphMode.FULL
+
+
+def _attn_type_name(attn_type) -> str:
+    return str(getattr(attn_type, "value", attn_type)).lower()
+
+
+class StarKVAttentionImpl:
+    """Per-layer attention over the compressed cache (attention.py:105-217)."""
+
+    def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: Optional[int] = None,
+                 alibi_slopes=None, sliding_window=None, kv_cache_dtype: str = "auto", logits_soft_cap=None,
+                 attn_type=DECODER, kv_sharing_target_layer_name=None, *, starkv_layer: StarKVLayerWeights,
+                 rotary_emb, max_model_len: Optional[int] = None):
+        if alibi_slopes is not None or sliding_window is not None or logits_soft_cap:
+            raise NotImplementedError("STAR-KV attention: no alibi, sliding window or softcap")
+        if _attn_type_name(attn_type) != DECODER or kv_sharing_target_layer_name is not None:
+            raise NotImplementedError("STAR-KV attention: decoder self-attention only")
+        if kv_cache_dtype not in ("auto", "float16", "bfloat16"):
+            raise NotImplementedError(f"STAR-KV attention: kv_cache_dtype {kv_cache_dtype!r}")
+        if starkv_layer.kv_quant and ((num_kv_heads or num_heads) != num_heads or head_size != HEAD_DIM):
+            raise NotImplementedError("STAR-KV 4-bit cache: MHA with head_dim 128 only")
+        self.num_heads = num_heads
+        self.head_size = head_size
+        self.scale = float(scale)
+        self.num_kv_heads = num_kv_heads or num_heads
+        self.kv_cache_dtype = kv_cache_dtype
+        self.w = starkv_layer
+        self.rotary_emb = rotary_emb
+        vllm_len = _vllm_max_model_len()
+        self.max_model_len = vllm_len if vllm_len is not None else max_model_len
+        if self.max_model_len is None:
+            raise ValueError("max_model_len is needed when vLLM is not present")
+
+    def to_device(self, device: torch.device, dtype: torch.dtype) -> None:
+        """The kernel operands on `device` (attention.py:134-166), before any graph capture."""
+        ops = layer_operands(self.w, self.num_heads, device, dtype)
+        self.k_ranks = ops.k_ranks
+        self.k_head_offsets = ops.k_head_offsets
+        self.k_width = ops.k_width
+        self.k_up = ops.k_up
+        self.v_up_by_q = ops.v_up_by_q
+        self.kv_down = ops.kv_down
+        self.row = ops.row
+        if self.row is not None:
+            self.k_nouts, self.head_of_lane, self.k_tiles = ops.k_nouts, ops.head_of_lane, ops.k_tiles
+
+    def _cache(self, kv_cache: torch.Tensor) -> torch.Tensor:
+        cache = kv_cache.squeeze(1) if kv_cache.dim() == 4 else kv_cache  # [num_blocks, block_size, width]
+        return cache if self.row is None else cache.view(torch.uint8)
+
+    def forward(self, layer, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
+                attn_metadata: Optional[StarKVMetadata], output: torch.Tensor, output_scale=None,
+                output_block_scale=None, in_full_graph: Optional[bool] = None) -> torch.Tensor:
+        """Writes the step's codes (`key` [T, k_width], `value` [T, v_rank]) and decodes
+        `query` [T, H*128] into `output` [T, H*128] (attention.py:168-217). `in_full_graph`
+        defaults to vLLM's forward context (False without vLLM)."""
+        if output_scale is not None or output_block_scale is not None:
+            raise NotImplementedError("STAR-KV attention: fused output quantization")
+        if attn_metadata is None:  # profiling run
+            return output.fill_(0)
+        md = attn_metadata
+        if md.num_prefills:
+            raise NotImplementedError("STAR-KV attention on MI355X: dense prefill is not part of this library")
+        n = md.num_actual_tokens
+        Hq, Hd = self.num_heads, self.head_size
+        cache = self._cache(kv_cache)
+        if self.row is None:
+            # Padding tokens carry slot -1: the write sends them to the reserved null block 0.
+            write_codes(key[:n], value[:n], cache, md.slot_mapping[:n])
+        else:
+            pack_kv(key[:n], value[:n], cache, md.slot_mapping[:n], self.row, self.k_ranks, self.k_head_offsets,
+                    self.k_nouts)
+        nd = md.num_decode_tokens
+        if nd:
+            self._decode(query[:nd].view(nd, Hq, Hd), cache, md, output[:nd].view(nd, Hq, Hd), in_full_graph)
+        return output
+
+    def write_from_hidden(self, hidden: torch.Tensor, kv_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                          return_codes: bool = False) -> Optional[torch.Tensor]:
+        """The step's write straight from the layer input: codes = hidden @ kv_down^T,
+        rounded to the model dtype (model.py:71), written or packed into their slots."""
+        cache = self._cache(kv_cache)
+        if self.row is None:
+            return write_kv(hidden, self.kv_down, cache, slot_mapping, self.k_width, return_codes=return_codes)
+        return write_kv(hidden, self.kv_down, cache, slot_mapping, self.k_width, row=self.row, k_ranks=self.k_ranks,
+                        k_offsets=self.k_head_offsets, k_nouts=self.k_nouts, return_codes=return_codes)
+
+    def _decode(self, q: torch.Tensor, cache: torch.Tensor, md: StarKVMetadata, out: torch.Tensor,
+                in_full_graph: Optional[bool]) -> None:
+        nd = q.shape[0]
+        full = _vllm_in_full_graph() if in_full_graph is None else in_full_graph
+        # Inside a full graph nothing may depend on the step's lengths: the span is fixed.
+        span = self.max_model_len if full else max(md.max_seq_len, 1)
+        # Padding rows have length 0; give them one (null-block) position to attend to.
+        seq_lens = md.seq_lens[:nd].clamp(min=1)
+        cs = self.rotary_emb.cos_sin_cache
+        if self.row is None:
+            o = paged_starkv_decode(q, cache, md.block_table[:nd], seq_lens, span, self.k_up, self.k_ranks,
+                                    self.k_head_offsets, self.k_width, self.v_up_by_q, cs, self.scale)
+        else:
+            o = paged_quant_decode(q, cache, md.block_table[:nd], seq_lens, span, self.row, self.k_up,
+                                   self.head_of_lane, self.k_tiles, self.v_up_by_q, cs, self.scale)
+        out.copy_(o)
