@@ -96,6 +96,40 @@ def bench_quant(lengths, steps, warmup, seed, copies, v_rank=64):
     return wl, ms, kern
 
 
+def bench_stock(n, context, steps, warmup, num_heads=32):
+    """Uncompressed bf16 decode attention at the same shape, as the comparator for
+    "stock" attention: torch's fused SDPA (flash or memory-efficient kernels only,
+    never the unfused math path) over contiguous K/V [n, H, context, 128]. Stock
+    paged attention reads the same K/V bytes through a block table, so this
+    contiguous read is the more favourable case for the comparator."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    g = torch.Generator(device="cuda").manual_seed(7)
+    q = torch.randn(n, num_heads, 1, 128, generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn(n, num_heads, context, 128, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(n, num_heads, context, 128, generator=g, device="cuda").to(torch.bfloat16)
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            fn = lambda: F.scaled_dot_product_attention(q, k, v)
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(steps):
+                fn()
+            stop.record()
+            torch.cuda.synchronize()
+    except RuntimeError as e:  # no fused kernel for this shape/device
+        return dict(error=str(e)[:200])
+    ms = start.elapsed_time(stop) / steps
+    b = 2 * k.numel() * 2 + 2 * q.numel() * 2
+    return dict(us_per_step=round(ms * 1e3, 2), GBps=round(b / (ms * 1e-3) / 1e9, 1),
+                hbm_frac=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), bytes_per_step=int(b),
+                kernel="torch SDPA (flash / memory-efficient), contiguous bf16 K/V, no paging")
+
+
 def bench_write(n, quant, steps, warmup, seed=1004, layers=24, hidden=4096, num_heads=32, v_rank=64):
     """One layer step of the cache write for n tokens: the fused write_kv (kv_down GEMM +
     scatter / 3.2-bit pack) against the unfused sequence (F.linear, then the scatter or
@@ -299,6 +333,14 @@ def main():
                 log(f"cache write, {n_tok} tokens, {'3.2-bit' if quant else 'bf16'} (fused vs unfused)")
                 extra[key] = bench_write(n_tok, quant, args.steps, args.warmup)
                 log(json.dumps(extra[key]))
+        torch.cuda.empty_cache()
+        log("uncompressed bf16 attention (torch fused SDPA), 64 x 8192")
+        stock = bench_stock(64, 8192, args.steps, args.warmup)
+        if "us_per_step" in stock:
+            stock["starkv_bf16_speedup"] = round(stock["us_per_step"] / head["us_per_step"], 2)
+            stock["starkv_quant_speedup"] = round(stock["us_per_step"] / extra["quant_bs64x8k"]["us_per_step"], 2)
+        extra["stock_bf16_sdpa_bs64x8k"] = stock
+        log(json.dumps(stock))
         torch.cuda.empty_cache()
 
     cpu = None
