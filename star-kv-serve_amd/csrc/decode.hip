@@ -603,6 +603,10 @@ static int device_cus() {
 static int grid_for(int n, int max_seq_len) {
     const int64_t tokens = (int64_t)n * (int64_t)(max_seq_len > 0 ? max_seq_len : 1);
     int64_t want = (tokens + 255) / 256;  // at least ~16 pages per workgroup
+    // Each request a workgroup moves on to costs a reload of that request's folded query
+    // tiles (about as long as 2-3 pages), so short requests get a workgroup each where the
+    // device has one to spare.
+    if (want < n) want = n;
     const int cus = device_cus();
     if (want > cus) want = cus;
     return want < 1 ? 1 : (int)want;
