@@ -432,7 +432,7 @@ __global__ __launch_bounds__(PREP_THR) void prep_kernel(PrepArgs a) {
 // ---------------------------------------------------------------------------
 // 3. merge: per (request, head) the partials' log-sum-exp, then the lift through
 //    v_up_by_q. A workgroup takes one head and MERGE_REQ requests, one wave each, so
-//    every row of v_up_by_q[h] serves MERGE_REQ outputs. The loads come in two rounds:
+//    every row of v_up_by_q[h] serves MERGE_REQ outputs. The loads come in two phases:
 //    the request's partial range (with v_up_by_q[h] staged into LDS meanwhile), then
 //    every partial's max and sum and the first MERGE_PRE partials' accumulator rows
 //    together.
@@ -474,7 +474,7 @@ __global__ __launch_bounds__(MERGE_THR) void merge_kernel(const uint8_t* __restr
     const float* wl = (const float*)(ws + ws_l);
     const float* wa = (const float*)(ws + ws_acc);
 
-    // Round 1: request b's tokens [pb, pe) in the concatenation, hence its partial slots
+    // Load phase 1: request b's tokens [pb, pe) in the concatenation, hence its partial slots
     // k_lo + k + b, k < nk (S tokens per decode workgroup). No tokens: softmax over an
     // empty row (NaN, as the reference). No wave plan (a head assignment that does not
     // fit): NaN as well, never a silent wrong result.
@@ -503,7 +503,7 @@ __global__ __launch_bounds__(MERGE_THR) void merge_kernel(const uint8_t* __restr
     const int k_lo = live ? pb / S : 0, nk = live ? (pe - 1) / S - k_lo + 1 : 0;
     const int64_t s0 = (int64_t)(k_lo + b) * Hq + h;  // slot index of partial k: s0 + k * Hq
 
-    // Round 2: partial k = lane's max and sum, and lane's columns c = lane + 64 j of the
+    // Load phase 2: partial k = lane's max and sum, and lane's columns c = lane + 64 j of the
     // first MERGE_PRE partials.
     const float mk = lane < nk ? wm[s0 + (int64_t)lane * Hq] : -INFINITY;
     const float lk = lane < nk ? wl[s0 + (int64_t)lane * Hq] : 0.f;
