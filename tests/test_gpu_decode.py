@@ -158,6 +158,25 @@ def test_lowrank_zero_length_and_truncation(cuda):
     assert_close(out[[0, 2]], truth[[0, 2]], "truncated")
 
 
+def test_decode_grid_rule(cuda):
+    """Grid = min(CUs, max(n, ceil(n * max_seq_len / 256))): at least ~16 pages per
+    workgroup, but a workgroup per request for short requests; never above the CUs."""
+    L = _hip.lib()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    print(f"\n[grid] CUs={cus}", flush=True)
+    for n, S in [(1, 4096), (1, 1), (64, 16), (64, 8192), (16, 32768), (300, 1), (1024, 48), (7, 700)]:
+        want = min(cus, max(n, -(-n * S // 256)))
+        assert L.starkv_decode_grid(n, S) == want, (n, S)
+
+
+def test_short_requests_one_workgroup_each(cuda):
+    """64 requests of 16 tokens (one workgroup per request) against the oracle."""
+    wl = W.make_lowrank([16] * 64, num_heads=32, seed=9)
+    out = paged_starkv_decode(*wl.to(cuda).decode_args())
+    torch.cuda.synchronize()
+    assert_close(out, lowrank_truth(wl), "short requests")
+
+
 def test_lowrank_block_size_not_power_of_two_is_rejected(cuda):
     # Pages are located with shifts, so block_size must be 16 * 2^s (16, 32, 64, ...).
     wl = W.make_lowrank([100, 20], num_heads=4, ranks=[16, 32, 48, 64], v_rank=32, seed=9, block_size=48)
