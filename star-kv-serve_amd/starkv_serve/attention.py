@@ -54,21 +54,20 @@ class StarKVMetadata:
     prefill_query_start_loc_cpu: Optional[List[int]] = None
 
 
+try:  # looked up once: forward runs every layer of every step
+    from vllm.config import CUDAGraphMode, get_current_vllm_config
+    from vllm.forward_context import get_forward_context
+    _HAVE_VLLM = True
+except ImportError:
+    _HAVE_VLLM = False
+
+
 def _vllm_max_model_len() -> Optional[int]:
-    try:
-        from vllm.config import get_current_vllm_config
-    except ImportError:
-        return None
-    return get_current_vllm_config().model_config.max_model_len
+    return get_current_vllm_config().model_config.max_model_len if _HAVE_VLLM else None
 
 
 def _vllm_in_full_graph() -> bool:
-    try:
-        from vllm.config import CUDAGraphMode
-        from vllm.forward_context import get_forward_context
-    except ImportError:
-        return False
-    return get_forward_context().cudagraph_runtime_mode == CUDAGraphMode.FULL
+    return _HAVE_VLLM and get_forward_context().cudagraph_runtime_mode == CUDAGraphMode.FULL
 
 
 def _attn_type_name(attn_type) -> str:
