@@ -295,8 +295,9 @@ def main():
                     help="each workload's warmup continues until this many ms of back-to-back calls")
     ap.add_argument("--no-extra", action="store_true", help="skip the 3.2-bit and ragged configurations")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["bf16", "quant", "write"], default=None,
-                    help="profile runs: time one bs64 x 8192 workload only and print its summary")
+    ap.add_argument("--only", choices=["bf16", "quant", "write", "short"], default=None,
+                    help="profile runs: time one workload only (bs64 x 8192; short: 64 requests x 16 "
+                         "tokens, bf16) and print its summary")
     ap.add_argument("--copy-probe", type=float, default=0.0, metavar="GIB",
                     help="profile runs: only copy GIB GiB device to device 5 times (counter scaling)")
     args = ap.parse_args()
@@ -318,6 +319,10 @@ def main():
         for n_tok in (16, 64):
             for quant in (True, False):
                 print(json.dumps(bench_write(n_tok, quant, args.steps, args.warmup)), flush=True)
+        return
+    if args.only == "short":
+        ws_, mss, ks = bench_lowrank([16] * 64, args.steps, args.warmup, seed=1005)
+        print(json.dumps(summarize(ws_, mss, ks)), flush=True)
         return
     if args.only == "quant":
         wq, msq, kq = bench_quant(lengths, args.steps, args.warmup, seed=1003, copies=3)
