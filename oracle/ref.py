@@ -17,6 +17,10 @@ something other than itself) -- see tests/test_oracle_*.py:
                                       permutation invariance, one-token closed form
   emulate_lowrank_reference           reports the reference's own rounding error;
                                       not used as a pass/fail truth
+  dense_prefill                       a prompt's last token equals lowrank_decode over
+                                      the same codes; a first token returns its own V
+                                      lifted; causality (a later token changes no
+                                      earlier output)
 """
 import math
 
@@ -239,6 +243,43 @@ def lowrank_decode_bruteforce(q, cache, block_table, seq_lens, max_seq_len, k_up
             w = w / w.sum()
             o = sum(w[l] * vrows[l] for l in range(L))
             out[b, h] = o @ np.asarray(v_up_by_q[h], np.float64)
+    return out
+
+
+def dense_prefill(q, k_codes, v_codes, query_start_loc, k_up, k_ranks, k_offsets, v_up, cos_sin, scale):
+    """float64 truth for the backend's dense prefill (attention.py:219-251): per prompt
+    (tokens query_start_loc[i] .. query_start_loc[i + 1], positions from 0, no cached
+    context), K of KV head h = RoPE(codes[:, off_h : off_h + rank_h] @ k_up[off_h : ...]),
+    V = v_codes @ v_up^T ([T, H_kv * D]), causal softmax(q . k * scale) @ V per query head
+    (query head h reads KV head h // (H_q / H_kv)). q [T, H_q, D]. Returns [T, H_q, D]."""
+    q = np.asarray(q, np.float64)
+    T, Hq, D = q.shape
+    Hkv = len(k_ranks)
+    G = Hq // Hkv
+    kc = np.asarray(k_codes, np.float64)
+    U = np.asarray(k_up, np.float64)
+    Vall = np.asarray(v_codes, np.float64) @ np.asarray(v_up, np.float64).T  # [T, Hkv * D]
+    cs_all = np.asarray(cos_sin, np.float64)
+    out = np.zeros((T, Hq, D))
+    qsl = [int(x) for x in query_start_loc]
+    for i in range(len(qsl) - 1):
+        a, b = qsl[i], qsl[i + 1]
+        L = b - a
+        if L <= 0:
+            continue
+        cs = cs_all[:L]
+        causal = np.tril(np.ones((L, L), bool))
+        for kv in range(Hkv):
+            R, off = int(k_ranks[kv]), int(k_offsets[kv])
+            keys = _rope(kc[a:b, off:off + R] @ U[off:off + R], cs)        # [L, D]
+            V = Vall[a:b, kv * D:(kv + 1) * D]
+            for g in range(G):
+                h = kv * G + g
+                logits = (q[a:b, h] @ keys.T) * scale
+                logits = np.where(causal, logits, -np.inf)
+                p = np.exp(logits - logits.max(axis=1, keepdims=True))
+                p /= p.sum(axis=1, keepdims=True)
+                out[a:b, h] = p @ V
     return out
 
 

@@ -10,6 +10,11 @@ errors, the same ``to_device`` attributes and the same ``forward`` contract:
 - The decode is ``paged_starkv_decode`` / ``paged_quant_decode``.
 - ``write_from_hidden`` is the fused route for the codes' own GEMM (model.py:71 + the
   write): one ``write_kv`` call from the layer's hidden states.
+- Prefill is dense, as in the reference (attention.py:219-251): this step's codes are
+  lifted back to K (RoPE applied) and V, and every prompt attends causally to itself
+  through torch's fused attention (flash or memory-efficient kernels only, never the
+  unfused math path). It is the one part of the layer that is not a kernel of this
+  library.
 
 vLLM is not needed to import or run this module. The two values the reference reads
 from vLLM are taken from it when it is importable, else from arguments:
@@ -19,9 +24,10 @@ from vLLM are taken from it when it is importable, else from arguments:
 
 Differences from the reference, by design:
 
-- Dense prefill (attention.py:219-251, FlashAttention over lifted K/V) is not part of
-  this library. A batch with prefill tokens raises ``NotImplementedError`` before any
-  work is enqueued.
+- The prefill lift and RoPE run in float32 and round K and V once to the model dtype;
+  the reference lifts and rotates in the model dtype. Prefill metadata that the dense
+  prefill cannot serve (chunked prompts, cached context) raises before any work is
+  enqueued, where the reference raises after the cache write.
 - The reference splits large decode batches so that its logits buffer stays under
   2^26 floats (attention.py:52, 198-199). These kernels keep logits on chip and need
   no such buffer; the decode wrappers only split batches above 1024 requests.
@@ -30,6 +36,7 @@ from dataclasses import dataclass
 from typing import List, Optional
 
 import torch
+import torch.nn.functional as F
 
 from starkv_serve.checkpoint import StarKVLayerWeights, layer_operands
 from starkv_serve.kernels.kv_write import write_codes, write_kv
@@ -113,6 +120,20 @@ class StarKVAttentionImpl:
         self.row = ops.row
         if self.row is not None:
             self.k_nouts, self.head_of_lane, self.k_tiles = ops.k_nouts, ops.head_of_lane, ops.k_tiles
+        # Prefill lifts every KV head in one batched product, which needs one width: the
+        # codes are gathered into a padded [T, H, R] view. Lanes past a head's width point
+        # at its first code; the rows of U they meet are zero (attention.py:144-160).
+        w, H, Hd = self.w, self.num_kv_heads, self.head_size
+        R = w.k_max_rank
+        idx = torch.empty(H * R, dtype=torch.long)
+        k_up_pad = torch.zeros(H, R, Hd, dtype=w.k_up.dtype)
+        for h, (off, width) in enumerate(zip(w.k_head_offsets.tolist(), w.k_head_widths.tolist())):
+            idx[h * R:h * R + width] = torch.arange(off, off + width)
+            idx[h * R + width:(h + 1) * R] = off
+            k_up_pad[h, :width] = w.k_up[off:off + width]
+        self.k_prefill_gather = idx.to(device)
+        self.k_up_T = k_up_pad.to(device=device, dtype=torch.float32).contiguous()
+        self.v_up = w.v_up.to(device=device, dtype=torch.float32).contiguous()  # [H * Hd, v_rank]
 
     def _cache(self, kv_cache: torch.Tensor) -> torch.Tensor:
         cache = kv_cache.squeeze(1) if kv_cache.dim() == 4 else kv_cache  # [num_blocks, block_size, width]
@@ -129,8 +150,7 @@ class StarKVAttentionImpl:
         if attn_metadata is None:  # profiling run
             return output.fill_(0)
         md = attn_metadata
-        if md.num_prefills:
-            raise NotImplementedError("STAR-KV attention on MI355X: dense prefill is not part of this library")
+        query_lens = self._prefill_lens(md) if md.num_prefills else None
         n = md.num_actual_tokens
         Hq, Hd = self.num_heads, self.head_size
         cache = self._cache(kv_cache)
@@ -143,7 +163,53 @@ class StarKVAttentionImpl:
         nd = md.num_decode_tokens
         if nd:
             self._decode(query[:nd].view(nd, Hq, Hd), cache, md, output[:nd].view(nd, Hq, Hd), in_full_graph)
+        if md.num_prefills:
+            self._dense_prefill(query_lens, query[nd:n].view(n - nd, Hq, Hd), key[nd:n], value[nd:n],
+                                output[nd:n].view(n - nd, Hq, Hd))
         return output
+
+    @staticmethod
+    def _prefill_lens(md: StarKVMetadata) -> List[int]:
+        """The prompts' lengths; each prompt must arrive whole, with no cached context
+        (attention.py:221-230)."""
+        p0, p1 = md.num_decodes, md.num_decodes + md.num_prefills
+        qsl = md.prefill_query_start_loc_cpu
+        if qsl is None:
+            raise NotImplementedError("STAR-KV prefill needs prefill_query_start_loc_cpu")
+        seq_lens = md.prefill_seq_lens_cpu or md.seq_lens[p0:p1].tolist()
+        query_lens = [qsl[i + 1] - qsl[i] for i in range(len(seq_lens))]
+        if list(seq_lens) != query_lens:
+            raise NotImplementedError(
+                "STAR-KV prefill needs every prompt in one step with no cached context "
+                "(no prefix caching, no chunked prefill)")
+        return query_lens
+
+    def _dense_prefill(self, query_lens: List[int], q: torch.Tensor, k_codes: torch.Tensor, v_codes: torch.Tensor,
+                       out: torch.Tensor) -> None:
+        """STAR-KV's prefill (attention.py:219-251): K = RoPE(codes @ U) and V = codes @
+        v_up for this step's tokens (positions from 0 in every prompt), then causal
+        attention of every prompt to itself. q and out [T, H_q, 128]."""
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        T = q.shape[0]
+        H, R, Hd = self.num_kv_heads, self.w.k_max_rank, self.head_size
+        G = self.num_heads // H
+        pos = torch.cat([torch.arange(L) for L in query_lens]).to(q.device)
+        kp = k_codes[:, self.k_prefill_gather].float().view(T, H, R).transpose(0, 1).contiguous()
+        k = torch.bmm(kp, self.k_up_T).transpose(0, 1)                                     # [T, H, Hd] fp32
+        cos, sin = self.rotary_emb.cos_sin_cache[pos].float().chunk(2, dim=-1)
+        cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
+        k1, k2 = k.chunk(2, dim=-1)
+        k = torch.cat([k1 * cos - k2 * sin, k2 * cos + k1 * sin], dim=-1).to(q.dtype)
+        v = F.linear(v_codes.float(), self.v_up).view(T, H, Hd).to(q.dtype)
+        a = 0
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            for L in query_lens:
+                qi = q[a:a + L].transpose(0, 1).unsqueeze(0).contiguous()                  # [1, H_q, L, Hd]
+                ki = k[a:a + L].repeat_interleave(G, dim=1).transpose(0, 1).unsqueeze(0).contiguous()
+                vi = v[a:a + L].repeat_interleave(G, dim=1).transpose(0, 1).unsqueeze(0).contiguous()
+                o = F.scaled_dot_product_attention(qi, ki, vi, is_causal=True, scale=self.scale)
+                out[a:a + L] = o[0].transpose(0, 1)
+                a += L
 
     def write_from_hidden(self, hidden: torch.Tensor, kv_cache: torch.Tensor, slot_mapping: torch.Tensor,
                           return_codes: bool = False) -> Optional[torch.Tensor]:

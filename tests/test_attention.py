@@ -69,11 +69,17 @@ def test_to_device_operands(layers, quant):
         assert impl.row.nbytes % 16 == 0 and impl.k_nouts.numel() == 4
 
 
-def _md(n_dec, n_pre):
-    return StarKVMetadata(num_actual_tokens=n_dec + n_pre, num_decodes=n_dec, num_decode_tokens=n_dec,
-                          num_prefills=n_pre, max_seq_len=10, seq_lens=torch.ones(n_dec + n_pre, dtype=torch.int32),
+def _md(n_dec, n_pre, prompt=1, cached=0):
+    """n_dec decodes, then n_pre prompts of `prompt` tokens each with `cached` tokens of
+    context already in the cache."""
+    T = n_dec + n_pre * prompt
+    lens = [1] * n_dec + [prompt + cached] * n_pre
+    return StarKVMetadata(num_actual_tokens=T, num_decodes=n_dec, num_decode_tokens=n_dec, num_prefills=n_pre,
+                          max_seq_len=10, seq_lens=torch.tensor(lens, dtype=torch.int32),
                           block_table=torch.zeros(n_dec + n_pre, 1, dtype=torch.int32),
-                          slot_mapping=torch.zeros(n_dec + n_pre, dtype=torch.int64))
+                          slot_mapping=torch.zeros(T, dtype=torch.int64),
+                          prefill_seq_lens_cpu=[prompt + cached] * n_pre,
+                          prefill_query_start_loc_cpu=[prompt * i for i in range(n_pre + 1)])
 
 
 def test_forward_profiling_run_and_rejections(layers):
@@ -81,7 +87,8 @@ def test_forward_profiling_run_and_rejections(layers):
     out = torch.full((3, 8 * 128), 5.0)
     assert impl.forward(None, out, out, out, out, None, out) is out
     assert not out.any()
-    with pytest.raises(NotImplementedError, match="prefill"):
-        impl.forward(None, out, out, out, out, _md(1, 2), out)
+    # Chunked prompts / cached context: raised before any work is enqueued (CPU tensors here).
+    with pytest.raises(NotImplementedError, match="every prompt in one step"):
+        impl.forward(None, out, out, out, out, _md(1, 1, prompt=2, cached=3), out)
     with pytest.raises(NotImplementedError, match="output quantization"):
         impl.forward(None, out, out, out, out, _md(3, 0), out, output_scale=1.0)

@@ -15,6 +15,9 @@ Checks:
 - padding rows (slot -1, length 0) write only the null block 0 and give finite
   outputs;
 - output rows past the batch's tokens are untouched.
+
+A mixed batch (decodes, then whole prompts) checks the dense prefill as well: the
+prompts' outputs against the float64 dense-prefill oracle over the step's own codes.
 """
 import types
 
@@ -26,7 +29,7 @@ from oracle import ref
 from starkv_serve import checkpoint as ck
 from starkv_serve import workloads as W
 from starkv_serve.attention import StarKVAttentionImpl, StarKVMetadata
-from test_gpu_decode import assert_close
+from test_gpu_decode import assert_close, metrics
 
 pytestmark = pytest.mark.gpu
 
@@ -103,3 +106,75 @@ def test_forward_decode_step(cuda, tmp_path, quant, num_heads, in_graph):
                                    impl.k_up.float().cpu().numpy(), RANKS, w.k_head_offsets.tolist(), impl.k_width,
                                    impl.v_up_by_q.float().cpu().numpy(), cs.float().cpu().numpy(), impl.scale)
     assert_close(out[:n], truth, f"forward quant={quant} in_graph={in_graph}")
+
+
+@pytest.mark.parametrize("quant,num_heads", [(False, 16), (True, 8)])
+def test_forward_mixed_decode_and_prefill(cuda, tmp_path, quant, num_heads):
+    """Decodes first, then whole prompts (attention.py:194-217): the decodes against the
+    decode oracle over the cache the step wrote, the prompts against the dense-prefill
+    oracle over the step's own codes."""
+    print(f"\n[attention mixed] quant={quant} heads={num_heads}", flush=True)
+    path = str(tmp_path / "fused_weights.pt")
+    ck.write_fused_checkpoint(path, 1, len(RANKS), 128, HIDDEN, {0: (RANKS, V_RANK)}, seed=31)
+    w = ck.load_fused_checkpoint(path, 1, len(RANKS), 128, dtype=torch.bfloat16, kv_quant=quant).layers[0]
+    g = torch.Generator().manual_seed(32)
+    cs = W.cos_sin_table(MAX_MODEL_LEN, torch.bfloat16, cuda)
+    impl = StarKVAttentionImpl(num_heads, 128, 128 ** -0.5, len(RANKS), starkv_layer=w,
+                               rotary_emb=types.SimpleNamespace(cos_sin_cache=cs), max_model_len=MAX_MODEL_LEN)
+    impl.to_device(cuda, torch.bfloat16)
+    dec_lens, prompts = [200, 17, 1], [37, 100, 1]
+    lengths = dec_lens + prompts
+    bt, nblk = W._page_layout(lengths, g)
+    width = impl.row.nbytes // 2 if quant else w.cache_width
+    kv_cache = torch.zeros(nblk, 1, W.BLOCK_SIZE, width, dtype=torch.bfloat16, device=cuda)
+    nd, npf = len(dec_lens), len(prompts)
+    # The decodes' earlier tokens, through the fused write.
+    blocks, slots = W._token_slots([L - 1 for L in dec_lens], bt[:nd])
+    x = torch.randn(blocks.numel(), HIDDEN, generator=g).to(torch.bfloat16).to(cuda)
+    impl.write_from_hidden(x, kv_cache, (blocks * W.BLOCK_SIZE + slots).to(cuda))
+    # This step: one token per decode (position L - 1), then every prompt token.
+    pos = torch.tensor([L - 1 for L in dec_lens])
+    dslots = bt[torch.arange(nd), pos // W.BLOCK_SIZE].long() * W.BLOCK_SIZE + pos % W.BLOCK_SIZE
+    pb, ps = W._token_slots(prompts, bt[nd:])
+    slot_mapping = torch.cat([dslots, pb * W.BLOCK_SIZE + ps]).to(cuda)
+    T = nd + sum(prompts)
+    hidden = torch.randn(T, HIDDEN, generator=g).to(torch.bfloat16).to(cuda)
+    codes = hidden @ impl.kv_down.T
+    key, value = codes[:, :impl.k_width], codes[:, impl.k_width:]
+    query = torch.randn(T, num_heads * 128, generator=g).to(torch.bfloat16).to(cuda)
+    qsl = [0]
+    for L in prompts:
+        qsl.append(qsl[-1] + L)
+    md = StarKVMetadata(num_actual_tokens=T, num_decodes=nd, num_decode_tokens=nd, num_prefills=npf,
+                        max_seq_len=max(lengths), seq_lens=torch.tensor(lengths, dtype=torch.int32, device=cuda),
+                        block_table=bt.to(cuda), slot_mapping=slot_mapping, prefill_seq_lens_cpu=list(prompts),
+                        prefill_query_start_loc_cpu=qsl)
+    output = torch.full((T, num_heads * 128), 7.0, dtype=torch.bfloat16, device=cuda)
+    impl.forward(None, query, key, value, kv_cache, md, output)
+    torch.cuda.synchronize()
+    out = output.view(T, num_heads, 128)
+    assert torch.isfinite(out).all()
+
+    cache = kv_cache.squeeze(1)
+    q = query.view(T, num_heads, 128).float().cpu().numpy()
+    if quant:
+        lay = ref.row_layout(impl.k_width, len(RANKS), w.v_rank)
+        dtruth = ref.quant_decode(q[:nd], cache.view(torch.uint8).cpu().numpy(), bt[:nd].numpy(),
+                                  np.array(dec_lens), max(dec_lens), lay, RANKS, impl.k_up.float().cpu().numpy(),
+                                  impl.v_up_by_q.float().cpu().numpy(), cs.float().cpu().numpy(), impl.scale)
+    else:
+        dtruth = ref.lowrank_decode(q[:nd], cache.float().cpu().numpy(), bt[:nd].numpy(), np.array(dec_lens),
+                                    max(dec_lens), impl.k_up.float().cpu().numpy(), RANKS, w.k_head_offsets.tolist(),
+                                    impl.k_width, impl.v_up_by_q.float().cpu().numpy(), cs.float().cpu().numpy(),
+                                    impl.scale)
+    assert_close(out[:nd], dtruth, f"mixed: decodes quant={quant}")
+    c = codes.float().cpu().numpy()
+    ptruth = ref.dense_prefill(q[nd:], c[nd:, :impl.k_width], c[nd:, impl.k_width:], qsl, w.k_up.float().numpy(),
+                               RANKS, w.k_head_offsets.tolist(), w.v_up.float().numpy(), cs.float().cpu().numpy(),
+                               impl.scale)
+    # Prefill tolerance: the fused attention takes bf16 q, K, V and multiplies bf16 P by V,
+    # as the reference's FlashAttention does (each a relative rounding of up to 2^-9), so
+    # mean-rel is bounded by 4e-3 here instead of the decode's 1e-3; max-abs stays 2e-2.
+    m = metrics(out[nd:], ptruth)
+    print(f"mixed: prompts quant={quant}: {m}", flush=True)
+    assert m["finite"] and m["max_abs"] <= 2e-2 and m["mean_rel"] <= 4e-3, m
