@@ -26,6 +26,10 @@ extern "C" {
 #define STARKV_F16 1
 #define STARKV_BF16 2
 
+/* Cache kinds of starkv_decode_workspace_bytes / starkv_decode_two_pass: STARKV_BF16 or
+ * STARKV_F16 low-rank codes, or the 3.2-bit QuantRow cache. */
+#define STARKV_CACHE_Q3_2 16
+
 #define STARKV_OK 0
 #define STARKV_ERR_ARG 1
 #define STARKV_ERR_HIP 2
@@ -122,12 +126,32 @@ int starkv_fold_q(void *stream, const void *q, int64_t q_s0, int64_t q_s1, int q
 int starkv_decode_grid(int n, int max_seq_len);
 
 /*
- * Workspace bytes a decode call needs: the rank-tile table, the token prefix sums,
- * the q-folded bases (n * k_tiles * 4 KiB) and the split-K partials. k_tiles is the
- * number of 16-lane rank tiles over all query heads:
- * (num_heads / num_kv_heads) * k_width / 16.
+ * Workspace bytes a decode call needs: the token prefix sums, the wave plan, the
+ * q-folded bases (4 KiB per request and 16-lane rank tile), the split-K partials
+ * ((grid + n) x num_heads x (v_rank + 2) fp32) and, for the two-pass form, the logits
+ * (n x num_heads x max_seq_len rounded up to 16, fp32). cache_kind: STARKV_BF16,
+ * STARKV_F16 or STARKV_CACHE_Q3_2 (num_kv_heads = num_heads). 0 for invalid sizes.
  */
-size_t starkv_decode_workspace_bytes(int n, int num_heads, int k_tiles, int v_rank, int grid);
+size_t starkv_decode_workspace_bytes(int cache_kind, int n, int num_heads, int num_kv_heads, int k_width,
+                                     int v_rank, int max_seq_len, int grid);
+
+/*
+ * 1 if a decode of this layer shape runs in two passes, else 0. The one-pass decode
+ * keeps P @ V in the decode kernel and takes v_rank <= 256 (bf16/fp16) or up to five
+ * 64-lane blocks of outlier (padded to 4) plus inlier columns (3.2-bit). Wider V
+ * ranks (up to 4096) run a logits pass and a P @ V pass, as the reference's
+ * paged_decode.py:199-219 / paged_quant.py:390-407 split their V pass. Both forms
+ * give the same results to within rounding.
+ */
+int starkv_decode_two_pass(int cache_kind, int num_heads, int k_width, int v_rank);
+
+/*
+ * Forces the decode form for the calls that follow (process-wide, not thread-safe; for
+ * tests and benchmarks that compare the two): 0 = automatic (default), 1 = one-pass
+ * only (shapes it cannot take are refused), 2 = two-pass always. Returns the previous
+ * mode, or -1 for an invalid mode. No counterpart in the reference.
+ */
+int starkv_decode_set_path(int mode);
 
 /*
  * bf16/fp16 low-rank paged decode. Replaces
@@ -140,21 +164,24 @@ size_t starkv_decode_workspace_bytes(int n, int num_heads, int k_tiles, int v_ra
  *   kv_cache    [num_blocks, block_size, k_width + v_rank], element strides c_s0, c_s1,
  *               last dim contiguous; code_dtype bf16 or fp16; block_size 16 * 2^s
  *   block_table [n, max_blocks] int32 (strides bt_s0, bt_s1); seq_lens [n] int32
- *   k_up        [k_width, 128] (row stride ku_s0), k_ranks / k_head_offsets [H_kv] int32
- *   v_up_by_q   [H_q, v_rank, 128] (strides vu_s0, vu_s1)
- *   cos_sin     [>= max_seq_len, 128] = cat(cos, sin) (row stride cs_s0)
+ *   k_up        [k_width, 128] (row stride ku_s0, dtype w_dtype), k_ranks /
+ *               k_head_offsets [H_kv] int32
+ *   v_up_by_q   [H_q, v_rank, 128] (strides vu_s0, vu_s1, dtype vu_dtype; v_rank <= 4096)
+ *   cos_sin     [>= max_seq_len, 128] = cat(cos, sin) (row stride cs_s0), fp16
  *   out         [n, H_q, 128] (strides o_s0, o_s1), dtype out_dtype
- *   workspace   >= starkv_decode_workspace_bytes(n, H_q, k_tiles, v_rank, grid) bytes,
- *               256-byte aligned; grid from starkv_decode_grid(n, max_seq_len) (or any
- *               grid >= 1)
+ *   workspace   >= starkv_decode_workspace_bytes(code_dtype, n, H_q, H_kv, k_width, v_rank,
+ *               max_seq_len, grid) bytes, 256-byte aligned; grid from
+ *               starkv_decode_grid(n, max_seq_len) (or any grid >= 1)
+ * A request with no tokens (seq_lens <= 0) gets NaN rows, as the reference's softmax
+ * over an empty row does.
  */
 int starkv_lowrank_decode(void *stream, const void *query, int64_t q_s0, int64_t q_s1, int q_dtype,
                           const void *kv_cache, int64_t c_s0, int64_t c_s1, int code_dtype, int block_size,
                           const int32_t *block_table, int64_t bt_s0, int64_t bt_s1, const int32_t *seq_lens,
                           int n, int num_heads, int num_kv_heads, int max_seq_len, const void *k_up,
                           int64_t ku_s0, int w_dtype, const int32_t *k_ranks, const int32_t *k_head_offsets,
-                          int k_width, const void *v_up_by_q, int64_t vu_s0, int64_t vu_s1, int v_rank,
-                          const void *cos_sin, int64_t cs_s0, int cs_dtype, float scale, void *out,
+                          int k_width, const void *v_up_by_q, int64_t vu_s0, int64_t vu_s1, int vu_dtype,
+                          int v_rank, const void *cos_sin, int64_t cs_s0, int cs_dtype, float scale, void *out,
                           int64_t o_s0, int64_t o_s1, int out_dtype, void *workspace, size_t workspace_bytes,
                           int grid);
 
@@ -164,6 +191,8 @@ int starkv_lowrank_decode(void *stream, const void *query, int64_t q_s0, int64_t
  * _paged_abx_z, softmax, _paged_pv_fold, lift). MHA, head_dim 128.
  *   kv_cache    uint8 [num_blocks, block_size, row_bytes], byte strides c_s0, c_s1
  *   tile_head / tile_nout / tile_last  [k_width / 16] int32 (k_tables' per-16-lane tiles)
+ *   workspace   >= starkv_decode_workspace_bytes(STARKV_CACHE_Q3_2, n, H, H, k_width, v_rank,
+ *               max_seq_len, grid) bytes
  *   other arguments as starkv_lowrank_decode.
  */
 int starkv_quant_decode(void *stream, const void *query, int64_t q_s0, int64_t q_s1, int q_dtype,
@@ -172,9 +201,9 @@ int starkv_quant_decode(void *stream, const void *query, int64_t q_s0, int64_t q
                         int n, int num_heads, int max_seq_len, int k_width, int v_rank, int row_bytes,
                         const void *k_up, int64_t ku_s0, int w_dtype, const int32_t *tile_head,
                         const int32_t *tile_nout, const int32_t *tile_last, const void *v_up_by_q,
-                        int64_t vu_s0, int64_t vu_s1, const void *cos_sin, int64_t cs_s0, int cs_dtype,
-                        float scale, void *out, int64_t o_s0, int64_t o_s1, int out_dtype, void *workspace,
-                        size_t workspace_bytes, int grid);
+                        int64_t vu_s0, int64_t vu_s1, int vu_dtype, const void *cos_sin, int64_t cs_s0,
+                        int cs_dtype, float scale, void *out, int64_t o_s0, int64_t o_s1, int out_dtype,
+                        void *workspace, size_t workspace_bytes, int grid);
 
 /*
  * Timing of the decode kernel alone, for benchmarks (no counterpart in the

@@ -33,6 +33,12 @@
 //    one page behind over a V table expanded once per page.
 // 3. merge: per (request, head) log-sum-exp of the partials, then the lift through
 //    v_up_by_q.
+// V ranks too wide for the decode kernel's P @ V (bf16/fp16 above 256, 3.2-bit above
+// five 64-lane blocks) take the two-pass form of decode_wide.hip instead: the decode
+// kernels run as a logits pass (K side and softmax statistics, logits stored in the
+// workspace), a P @ V pass reads the logits and the V bytes, and a merge of its own
+// lifts the result. Both forms take the same arguments and give the same outputs to
+// within rounding.
 #include <vector>
 
 #include "decode_common.hpp"
@@ -636,7 +642,7 @@ struct CommonArgs {
     const void* k_up; int64_t ku_s0; int w_dt;
     const int32_t* k_ranks; const int32_t* k_offsets;
     const int32_t* t_head; const int32_t* t_nout; const int32_t* t_last;
-    const void* vup; int64_t vu_s0, vu_s1; int v_rank;
+    const void* vup; int64_t vu_s0, vu_s1; int vu_dt; int v_rank;
     const void* cs; int64_t cs_s0; int cs_dt;
     float scale;
     void* out; int64_t o_s0, o_s1; int out_dt;
@@ -660,6 +666,43 @@ static int launch_merge(dim3 grid, size_t lds, hipStream_t stream, const DecodeP
     return STARKV_OK;
 }
 
+// Which decode form runs: 0 = the one-pass kernels where the shape fits them, else the
+// two-pass form; 1 = one-pass only (shapes it cannot take are refused); 2 = two-pass
+// always. Set by starkv_decode_set_path (tests and benchmarks compare the two).
+static int g_path = 0;
+
+// Whether the one-pass kernel takes a layer of this shape.
+static bool one_pass_fits(int fmt, int k_width, int v_rank, int row_bytes, int v_nout) {
+    if (fmt == FMT_Q4) {
+        const int qnb = quant_v_blocks(v_rank, v_nout);
+        return qnb > 0 && quant_copies(row_bytes) > 0 && quant_lds_bytes(row_bytes, qnb) <= quant_lds_limit();
+    }
+    const int nb = (v_rank + 63) / 64;
+    return nb <= 4 && lowrank_copies(k_width, nb) > 0;
+}
+
+static bool use_two_pass(int fmt, int k_width, int v_rank, int row_bytes, int v_nout) {
+    return g_path == 2 || (g_path == 0 && !one_pass_fits(fmt, k_width, v_rank, row_bytes, v_nout));
+}
+
+static int lcap_of(int max_seq_len) { return (max_seq_len + TILE_TOK - 1) / TILE_TOK * TILE_TOK; }
+
+// QuantRow (paged_quant.py:71-111) offsets of a 3.2-bit row.
+struct QRow {
+    int v_nout, v_nbo, ks_off, vs_off, vq_off, v_bytes, nbytes;
+};
+static QRow qrow(int k_width, int num_heads, int v_rank) {
+    QRow r;
+    r.v_nout = (int)(0.2 * (double)v_rank);
+    r.v_nbo = (r.v_nout + 1) / 2;
+    r.ks_off = k_width / 2;
+    r.vs_off = r.ks_off + 4 * num_heads;
+    r.vq_off = r.vs_off + 4;
+    r.v_bytes = r.v_nbo + (v_rank - r.v_nout + 1) / 2;
+    r.nbytes = (r.vq_off + r.v_bytes + 15) / 16 * 16;
+    return r;
+}
+
 static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_bytes, int TT, hipStream_t stream) {
     SKV_CHECK(a.n >= 1 && a.n <= MAX_REQ_PER_CALL, "decode: n=%d requests (1..%d per call)", a.n, MAX_REQ_PER_CALL);
     SKV_CHECK(a.Hq >= 1 && a.Hq <= MAX_H, "decode: num_heads=%d (1..%d)", a.Hq, MAX_H);
@@ -668,7 +711,9 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     SKV_CHECK(a.grid >= 1, "decode: grid must be >= 1");
     SKV_CHECK(TT >= 1 && TT <= MAX_TT, "decode: %d rank tiles (1..%d: k_width x heads per kv head <= %d)", TT,
               MAX_TT, MAX_TT * 16);
-    const WsLayout wl = ws_layout(a.n, a.Hq, TT, a.v_rank, a.grid);
+    const bool two = use_two_pass(fmt, p.k_width, a.v_rank, row_bytes, p.v_nout);
+    const int lcap = two ? lcap_of(a.max_seq_len) : 0;
+    const WsLayout wl = ws_layout(a.n, a.Hq, TT, a.v_rank, a.grid, lcap);
     SKV_CHECK(a.ws_bytes >= wl.total, "decode: workspace %zu bytes < %zu needed", a.ws_bytes, wl.total);
     SKV_CHECK(((uintptr_t)a.ws % 256) == 0, "decode: workspace must be 256-byte aligned");
     SKV_CHECK(p.bs_shift >= 0, "decode: block_size must be 16 times a power of two");
@@ -684,8 +729,9 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     SKV_CHECK(p.c_s1 * TILE_TOK < ((int64_t)1 << 31), "decode: 16 slots span %lld bytes (>= 2^31)",
               (long long)(p.c_s1 * TILE_TOK));
     SKV_CHECK(a.q_dt >= STARKV_F32 && a.q_dt <= STARKV_BF16 && a.w_dt >= STARKV_F32 && a.w_dt <= STARKV_BF16 &&
-                  a.out_dt >= STARKV_F32 && a.out_dt <= STARKV_BF16,
-              "decode: query, k_up / v_up_by_q and output dtypes must be bf16, fp16 or fp32");
+                  a.vu_dt >= STARKV_F32 && a.vu_dt <= STARKV_BF16 && a.out_dt >= STARKV_F32 &&
+                  a.out_dt <= STARKV_BF16,
+              "decode: query, k_up, v_up_by_q and output dtypes must be bf16, fp16 or fp32");
     SKV_CHECK(a.cs_dt == STARKV_F16, "decode: cos_sin must be fp16 (convert the table once; it is exact for bf16)");
     SKV_CHECK(a.cs_s0 % 8 == 0 && a.cs_s0 >= 128 && a.cs_s0 * 2 * TILE_TOK < ((int64_t)1 << 31) &&
                   ((uintptr_t)a.cs % 16) == 0,
@@ -694,8 +740,10 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
               "decode: query rows must be 16-byte aligned (strides multiples of 8)");
     SKV_CHECK(a.ku_s0 % 8 == 0 && ((uintptr_t)a.k_up % 16) == 0, "decode: k_up rows must be 16-byte aligned");
     const int nb = (a.v_rank + 63) / 64;
-    SKV_CHECK(nb <= 4, "decode: v_rank %d > 256", a.v_rank);
-    const int wsz = a.w_dt == STARKV_F32 ? 4 : 2;
+    SKV_CHECK(two || one_pass_fits(fmt, p.k_width, a.v_rank, row_bytes, p.v_nout),
+              "decode: v_rank %d does not fit the one-pass decode (the two-pass form is switched off)", a.v_rank);
+    SKV_CHECK(!two || a.v_rank <= MAX_V_RANK_TWO_PASS, "decode: v_rank %d > %d", a.v_rank, MAX_V_RANK_TWO_PASS);
+    const int wsz = a.vu_dt == STARKV_F32 ? 4 : 2;
     SKV_CHECK(((uintptr_t)a.vup % 16) == 0 && (a.vu_s0 * wsz) % 16 == 0 && (a.vu_s1 * wsz) % 16 == 0,
               "decode: v_up_by_q rows must be 16-byte aligned");
 
@@ -704,23 +752,39 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     p.cs = (const uint8_t*)a.cs; p.cs_s0b = (int)(a.cs_s0 * 2);
     p.row_g = row_bytes / 16;
     int qnb = 0;
-    if (fmt == FMT_Q4) {
+    if (two) {
+        // The logits pass copies only what the K side reads: the cos/sin rows and the K
+        // codes (bf16/fp16), or the K nibbles and scales (3.2-bit).
+        SKV_CHECK((int64_t)a.n * a.Hq * lcap < ((int64_t)1 << 31), "decode: %d x %d x %d logits exceed 2^31", a.n,
+                  a.Hq, lcap);
+        SKV_CHECK(pv_fits(fmt, p.k_width, a.v_rank, p.vs_off, p.vq_off, p.v_nout,
+                          p.v_nbo + (a.v_rank - p.v_nout + 1) / 2),
+                  "decode: no P @ V window of v_rank %d fits in LDS", a.v_rank);
+        if (fmt == FMT_Q4) {
+            const int rk = (p.vs_off + 15) / 16 * 16;
+            SKV_CHECK(quant_copies(rk) > 0 && quant_lds_bytes(rk, 0) <= quant_lds_limit(),
+                      "decode: a 3.2-bit page of %d K bytes per row does not fit in LDS", rk);
+            p.row_g = rk / 16;
+            p.nch = quant_chunks(rk);
+            p.lds_bytes = quant_lds_bytes(rk, 0);
+        } else {
+            SKV_CHECK(lowrank_copies(p.k_width, 0) > 0, "decode: a page of k_width %d does not fit in LDS",
+                      p.k_width);
+            p.nch = lowrank_chunks(p.k_width, 0);
+            p.lds_bytes = lowrank_lds_bytes(p.k_width, 0);
+        }
+    } else if (fmt == FMT_Q4) {
         qnb = quant_v_blocks(a.v_rank, p.v_nout);
-        SKV_CHECK(qnb > 0, "decode: v_rank %d needs more than 5 P @ V blocks", a.v_rank);
-        SKV_CHECK(quant_copies(row_bytes) > 0 && quant_lds_bytes(row_bytes, qnb) <= quant_lds_limit(),
-                  "decode: a 3.2-bit page of %d-byte rows (v_rank %d) does not fit in LDS", row_bytes, a.v_rank);
         p.nch = quant_chunks(row_bytes);
         p.lds_bytes = quant_lds_bytes(row_bytes, qnb);
     } else {
-        SKV_CHECK(lowrank_copies(p.k_width, nb) > 0,
-                  "decode: a page of k_width %d and v_rank %d needs more than 64 KB of LDS", p.k_width,
-                  a.v_rank);
         p.nch = lowrank_chunks(p.k_width, nb);
         p.lds_bytes = lowrank_lds_bytes(p.k_width, nb);
     }
     p.ws = (uint8_t*)a.ws;
     p.ws_plan = wl.plan; p.ws_ab = wl.ab;
     p.ws_m = wl.m; p.ws_l = wl.l; p.ws_acc = wl.acc;
+    p.ws_lg = wl.lg; p.lcap = lcap;
 
     PrepArgs pa;
     pa.seq_lens = a.seq_lens; pa.n = a.n; pa.max_seq_len = a.max_seq_len; pa.grid = a.grid;
@@ -737,17 +801,31 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     SKV_HIP(hipGetLastError());
     const bool timed = g_prof.on && 2 * g_prof.used + 1 < (int)g_prof.ev.size();
     if (timed) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
-    int rc = fmt == FMT_Q4 ? launch_quant(p, qnb, a.grid, stream) : launch_lowrank(p, fmt, nb, a.grid, stream);
+    int rc;
+    if (two) {
+        rc = fmt == FMT_Q4 ? launch_quant(p, 0, a.grid, stream) : launch_lowrank(p, fmt, 0, a.grid, stream);
+        if (rc) return rc;
+        SKV_HIP(hipGetLastError());
+        rc = launch_pv(p, fmt, a.grid, stream);
+    } else {
+        rc = fmt == FMT_Q4 ? launch_quant(p, qnb, a.grid, stream) : launch_lowrank(p, fmt, nb, a.grid, stream);
+    }
     if (rc) return rc;
     SKV_HIP(hipGetLastError());
     if (timed) {
         SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used + 1], stream));
         ++g_prof.used;
     }
+    if (two) {
+        rc = launch_merge_wide(p, a.vu_dt, a.vup, a.vu_s0, a.vu_s1, a.out, a.o_s0, a.o_s1, a.out_dt, stream);
+        if (rc) return rc;
+        SKV_HIP(hipGetLastError());
+        return STARKV_OK;
+    }
     const dim3 mgrid((a.n + MERGE_REQ - 1) / MERGE_REQ, a.Hq);
-    const size_t mlds = merge_lds_bytes(a.v_rank, a.w_dt);
-    if (a.w_dt == STARKV_BF16) return launch_merge<uint16_t>(mgrid, mlds, stream, p, wl, a);
-    if (a.w_dt == STARKV_F16) return launch_merge<_Float16>(mgrid, mlds, stream, p, wl, a);
+    const size_t mlds = merge_lds_bytes(a.v_rank, a.vu_dt);
+    if (a.vu_dt == STARKV_BF16) return launch_merge<uint16_t>(mgrid, mlds, stream, p, wl, a);
+    if (a.vu_dt == STARKV_F16) return launch_merge<_Float16>(mgrid, mlds, stream, p, wl, a);
     return launch_merge<float>(mgrid, mlds, stream, p, wl, a);
 }
 
@@ -788,8 +866,43 @@ int starkv_profile_end(double* decode_ms_sum, int* calls) {
     return STARKV_OK;
 }
 
-size_t starkv_decode_workspace_bytes(int n, int num_heads, int k_tiles, int v_rank, int grid) {
-    return ws_layout(n, num_heads, k_tiles, v_rank, grid).total;
+size_t starkv_decode_workspace_bytes(int cache_kind, int n, int num_heads, int num_kv_heads, int k_width, int v_rank,
+                                     int max_seq_len, int grid) {
+    if (n < 1 || num_heads < 1 || num_kv_heads < 1 || k_width < 16 || v_rank < 1 || max_seq_len < 1 || grid < 1)
+        return 0;
+    int fmt, row_bytes, v_nout = 0, TT;
+    if (cache_kind == STARKV_CACHE_Q3_2) {
+        const QRow r = qrow(k_width, num_heads, v_rank);
+        fmt = FMT_Q4;
+        row_bytes = r.nbytes;
+        v_nout = r.v_nout;
+        TT = k_width / 16;
+    } else {
+        fmt = cache_kind == STARKV_F16 ? FMT_F16 : FMT_BF16;
+        row_bytes = (k_width + v_rank) * 2;
+        TT = (num_heads / num_kv_heads) * (k_width / 16);
+    }
+    const bool two = use_two_pass(fmt, k_width, v_rank, row_bytes, v_nout);
+    return ws_layout(n, num_heads, TT, v_rank, grid, two ? lcap_of(max_seq_len) : 0).total;
+}
+
+int starkv_decode_set_path(int mode) {
+    clear_error();
+    if (mode < 0 || mode > 2) {
+        set_error("decode_set_path: mode %d (0 auto, 1 one-pass, 2 two-pass)", mode);
+        return -1;
+    }
+    const int prev = g_path;
+    g_path = mode;
+    return prev;
+}
+
+int starkv_decode_two_pass(int cache_kind, int num_heads, int k_width, int v_rank) {
+    if (cache_kind == STARKV_CACHE_Q3_2) {
+        const QRow r = qrow(k_width, num_heads, v_rank);
+        return use_two_pass(FMT_Q4, k_width, v_rank, r.nbytes, r.v_nout);
+    }
+    return use_two_pass(cache_kind == STARKV_F16 ? FMT_F16 : FMT_BF16, k_width, v_rank, (k_width + v_rank) * 2, 0);
 }
 
 int starkv_fold_q(void* stream, const void* q, int64_t q_s0, int64_t q_s1, int q_dtype, const void* k_up,
@@ -811,9 +924,9 @@ int starkv_lowrank_decode(void* stream, const void* query, int64_t q_s0, int64_t
                           const int32_t* block_table, int64_t bt_s0, int64_t bt_s1, const int32_t* seq_lens, int n,
                           int num_heads, int num_kv_heads, int max_seq_len, const void* k_up, int64_t ku_s0,
                           int w_dtype, const int32_t* k_ranks, const int32_t* k_head_offsets, int k_width,
-                          const void* v_up_by_q, int64_t vu_s0, int64_t vu_s1, int v_rank, const void* cos_sin,
-                          int64_t cs_s0, int cs_dtype, float scale, void* out, int64_t o_s0, int64_t o_s1,
-                          int out_dtype, void* workspace, size_t workspace_bytes, int grid) {
+                          const void* v_up_by_q, int64_t vu_s0, int64_t vu_s1, int vu_dtype, int v_rank,
+                          const void* cos_sin, int64_t cs_s0, int cs_dtype, float scale, void* out, int64_t o_s0,
+                          int64_t o_s1, int out_dtype, void* workspace, size_t workspace_bytes, int grid) {
     clear_error();
     SKV_CHECK(code_dtype == STARKV_BF16 || code_dtype == STARKV_F16, "lowrank_decode: codes must be bf16 or fp16");
     SKV_CHECK(num_kv_heads >= 1 && num_heads % num_kv_heads == 0, "lowrank_decode: num_heads %% num_kv_heads != 0");
@@ -831,8 +944,8 @@ int starkv_lowrank_decode(void* stream, const void* query, int64_t q_s0, int64_t
     p.k_width = k_width;
     CommonArgs a{query, q_s0, q_s1, q_dtype, block_table, bt_s0, bt_s1, seq_lens, n, num_heads, num_kv_heads,
                  max_seq_len, k_up, ku_s0, w_dtype, k_ranks, k_head_offsets, nullptr, nullptr, nullptr,
-                 v_up_by_q, vu_s0, vu_s1, v_rank, cos_sin, cs_s0, cs_dtype, scale, out, o_s0, o_s1, out_dtype,
-                 workspace, workspace_bytes, grid};
+                 v_up_by_q, vu_s0, vu_s1, vu_dtype, v_rank, cos_sin, cs_s0, cs_dtype, scale, out, o_s0, o_s1,
+                 out_dtype, workspace, workspace_bytes, grid};
     const int TT = (num_heads / num_kv_heads) * (k_width / 16);
     return decode_common(p, a, code_dtype == STARKV_BF16 ? FMT_BF16 : FMT_F16, (k_width + v_rank) * 2, TT,
                          (hipStream_t)stream);
@@ -844,8 +957,9 @@ int starkv_quant_decode(void* stream, const void* query, int64_t q_s0, int64_t q
                         int num_heads, int max_seq_len, int k_width, int v_rank, int row_bytes, const void* k_up,
                         int64_t ku_s0, int w_dtype, const int32_t* tile_head, const int32_t* tile_nout,
                         const int32_t* tile_last, const void* v_up_by_q, int64_t vu_s0, int64_t vu_s1,
-                        const void* cos_sin, int64_t cs_s0, int cs_dtype, float scale, void* out, int64_t o_s0,
-                        int64_t o_s1, int out_dtype, void* workspace, size_t workspace_bytes, int grid) {
+                        int vu_dtype, const void* cos_sin, int64_t cs_s0, int cs_dtype, float scale, void* out,
+                        int64_t o_s0, int64_t o_s1, int out_dtype, void* workspace, size_t workspace_bytes,
+                        int grid) {
     clear_error();
     SKV_CHECK(k_width >= 16 && k_width % 16 == 0, "quant_decode: k_width %d must be a positive multiple of 16",
               k_width);
@@ -859,19 +973,18 @@ int starkv_quant_decode(void* stream, const void* query, int64_t q_s0, int64_t q
     p.c_s1 = c_s1;
     p.bs_shift = block_shift(block_size);
     p.k_width = k_width;
-    const int v_nout = (int)(0.2 * (double)v_rank);
-    p.v_nout = v_nout;
-    p.v_nbo = (v_nout + 1) / 2;
-    p.ks_off = k_width / 2;
-    p.vs_off = p.ks_off + 4 * num_heads;
-    p.vq_off = p.vs_off + 4;
-    const int v_bytes = p.v_nbo + (v_rank - v_nout + 1) / 2;
-    const int nbytes = (p.vq_off + v_bytes + 15) / 16 * 16;
-    SKV_CHECK(row_bytes == nbytes, "quant_decode: row_bytes %d != QuantRow.nbytes %d", row_bytes, nbytes);
+    SKV_CHECK(num_heads >= 1 && v_rank >= 1, "quant_decode: num_heads %d, v_rank %d", num_heads, v_rank);
+    const QRow r = qrow(k_width, num_heads, v_rank);
+    p.v_nout = r.v_nout;
+    p.v_nbo = r.v_nbo;
+    p.ks_off = r.ks_off;
+    p.vs_off = r.vs_off;
+    p.vq_off = r.vq_off;
+    SKV_CHECK(row_bytes == r.nbytes, "quant_decode: row_bytes %d != QuantRow.nbytes %d", row_bytes, r.nbytes);
     CommonArgs a{query, q_s0, q_s1, q_dtype, block_table, bt_s0, bt_s1, seq_lens, n, num_heads, num_heads,
                  max_seq_len, k_up, ku_s0, w_dtype, nullptr, nullptr, tile_head, tile_nout, tile_last,
-                 v_up_by_q, vu_s0, vu_s1, v_rank, cos_sin, cs_s0, cs_dtype, scale, out, o_s0, o_s1, out_dtype,
-                 workspace, workspace_bytes, grid};
+                 v_up_by_q, vu_s0, vu_s1, vu_dtype, v_rank, cos_sin, cs_s0, cs_dtype, scale, out, o_s0, o_s1,
+                 out_dtype, workspace, workspace_bytes, grid};
     return decode_common(p, a, FMT_Q4, row_bytes, k_width / 16, (hipStream_t)stream);
 }
 

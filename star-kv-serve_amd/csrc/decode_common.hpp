@@ -43,6 +43,9 @@ constexpr float LAZY_MAX = 8.f;             // log2 headroom before the running 
 //   ab     fp16  [n][TT][4][64][8]
 //   m, l   fp32  [slots][Hq]  (log2-domain reference max and sum per partial)
 //   acc    fp32  [slots][Hq][v_rank]
+//   lg     fp32  [n][Hq][lcap]  (two-pass calls only) log2-domain logits, token l of
+//                               request b at (b Hq + h) lcap + l, lcap = max_seq_len
+//                               rounded up to 16
 // Slot word: everything a decode kernel needs of one of its slots, so that its prologue
 // reads a wave's slots with a few wide scalar loads: the code tile (first cache lane /
 // 16), the tile's outlier ranks (3.2-bit), the slot's partial-logit row, its local head
@@ -61,12 +64,13 @@ __device__ __forceinline__ int sw_head(uint32_t w) { return (int)((w >> 23) & 3)
 __device__ __forceinline__ int sw_tile(uint32_t w) { return (int)(w >> 25); }
 
 struct WsLayout {
-    size_t hdr, plan, ab, m, l, acc, total;
+    size_t hdr, plan, ab, m, l, acc, lg, total;
 };
 
 static inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-static WsLayout ws_layout(int n, int Hq, int TT, int v_rank, int grid) {
+// lcap = 0: the one-pass decode (no logits buffer).
+static WsLayout ws_layout(int n, int Hq, int TT, int v_rank, int grid, int lcap) {
     WsLayout w;
     const size_t slots = (size_t)grid + n;
     size_t o = 0;
@@ -76,6 +80,7 @@ static WsLayout ws_layout(int n, int Hq, int TT, int v_rank, int grid) {
     w.m = o; o = al256(o + slots * Hq * 4);
     w.l = o; o = al256(o + slots * Hq * 4);
     w.acc = o; o = al256(o + slots * Hq * (size_t)v_rank * 4);
+    w.lg = o; o = al256(o + (size_t)n * Hq * (size_t)lcap * 4);
     w.total = o;
     return w;
 }
@@ -91,6 +96,7 @@ struct DecodeParams {
     const uint8_t* cs; int cs_s0b;                 // fp16 cos/sin table, row stride in bytes
     uint8_t* ws;
     size_t ws_plan, ws_ab, ws_m, ws_l, ws_acc;
+    size_t ws_lg; int lcap;                        // two-pass calls: logits buffer, row length
 };
 
 __device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -212,9 +218,10 @@ struct SmState {
 // heads into partial slot `slot`, then reset. The wave's query-head ids come from LDS:
 // a vector load here would leave a tracked load in flight at the loop's join, and the
 // compiler would then drain every copy before the next page's first LDS read.
+// NB = 0 (the logits pass of a two-pass call): m and l only.
 template <int NB>
-__device__ __forceinline__ void flush_partial(const DecodeParams& p, SmState& sm, f32x4_t (&acc)[NB], int nh,
-                                              int slot, const int* sqh, int lane) {
+__device__ __forceinline__ void flush_partial(const DecodeParams& p, SmState& sm, f32x4_t (&acc)[NB > 0 ? NB : 1],
+                                              int nh, int slot, const int* sqh, int lane) {
     const int ln = opaque(lane);
     const int kh = ln >> 4, lr = ln & 15;
     const int64_t base = (int64_t)slot * p.Hq;
@@ -254,6 +261,15 @@ int lowrank_copies(int k_width, int nb);
 // (v_rank, v_nout) (0 if too many), 1 KB chunks copied per page and copies per wave (0 if
 // a page does not fit) for a row of row_bytes, dynamic LDS bytes, the LDS limit.
 int launch_quant(const DecodeParams& p, int nb, int grid, hipStream_t stream);
+
+// The two-pass decode (decode_wide.hip): the P @ V pass over the logits the K pass
+// stored (one launch per column window), whether its pages fit in LDS, and the merge of
+// its partials with the lift through v_up_by_q (of dtype w_dt).
+int launch_pv(const DecodeParams& p, int fmt, int grid, hipStream_t stream);
+bool pv_fits(int fmt, int k_width, int v_rank, int vs_off, int vq_off, int v_nout, int v_bytes);
+int launch_merge_wide(const DecodeParams& p, int w_dt, const void* vup, int64_t vu_s0, int64_t vu_s1, void* out,
+                      int64_t o_s0, int64_t o_s1, int out_dt, hipStream_t stream);
+constexpr int MAX_V_RANK_TWO_PASS = 4096;  // H x head_dim of a 32-head MHA layer: a full-rank V
 int quant_v_blocks(int v_rank, int v_nout);
 int quant_chunks(int row_bytes);
 int quant_copies(int row_bytes);

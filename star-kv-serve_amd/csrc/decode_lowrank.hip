@@ -25,6 +25,11 @@
 // Copy i of wave w moves chunk 8 i + w; lane q's offset inside the page depends only on
 // (chunk, q) and is computed once (`doff`). Copies past the page's chunks land in a
 // 1 KB dummy block after the buffers and read nothing.
+//
+// NB = 0 is the logits pass of a two-pass call (V ranks too wide for P @ V in this
+// kernel): no V chunks, no V table and no P @ V; the softmax stores each valid logit
+// (log2 domain, fp32) into the workspace logits buffer and keeps m and l for the
+// split-K partials, and decode_wide.hip's pass runs P @ V from those logits.
 
 #include "decode_pages.hpp"
 
@@ -49,7 +54,8 @@ struct LaneAddr {
     uint32_t cs[4];               // B operand: row lr, granule 4 ks + lg
     uint32_t k[MTV];              // slot i: 8 code bytes of row lr, ranks 4 lg .. 4 lg + 3
     uint32_t vt;                  // V table entry (0, lane)
-    uint32_t cv_rd[NB], cv_wr[NB];  // V transpose: the two codes read, the entry written
+    uint32_t cv_rd[NB > 0 ? NB : 1], cv_wr[NB > 0 ? NB : 1];  // V transpose: the two codes read, the entry written
+    int lg;                       // NB = 0: this lane's logit offset in a request's rows (q head x lcap + token)
     uint32_t st[(MTV + 3) / 4];   // partial-logit row of this lane's slot in each group of 4
     uint32_t sm;                  // softmax: first of the 4 rows of head lane >> 4
     uint32_t pw, pr;              // P: write (head lane >> 4, token lane & 15), read (head lane & 3)
@@ -136,10 +142,11 @@ __device__ __forceinline__ void k_side(const DecodeParams& p, const LaneAddr<MTV
 
 // Online softmax of the wave's heads (head lane >> 4 on a 16-lane row, token lane & 15).
 // Returns true when some head's reference max moved (acc needs rescaling by alpha).
-template <int FMT>
+// LG (the logits pass): no P; each valid logit goes to lgd instead.
+template <int FMT, bool LG = false>
 __device__ __forceinline__ bool softmax_page(SmState& sm, const uint32_t sm_addr, bool fast, uint32_t sp, int nh,
                                              uint32_t pw_addr, uint32_t plo_off, uint32_t salpha, int lane, int tok0,
-                                             int lo, int hi) {
+                                             int lo, int hi, float* lgd = nullptr) {
     const int kh = lane >> 4, lr = lane & 15;
     float s;
     if (fast) {
@@ -150,7 +157,9 @@ __device__ __forceinline__ bool softmax_page(SmState& sm, const uint32_t sm_addr
         for (int t = 0; t < sm.hn; ++t) s += lds_ld<float>(sp + (uint32_t)((sm.hf + t) * TILE_TOK + lr) * 4);
     }
     const int tok = tok0 + lr;
-    s = tok >= lo && tok < hi && kh < nh ? s : -INFINITY;
+    const bool valid = tok >= lo && tok < hi && kh < nh;
+    s = valid ? s : -INFINITY;
+    if (LG && valid) *lgd = s;
     float alpha = 1.f;
     bool moved = false;
     if (__builtin_amdgcn_ballot_w64(s > sm.m + LAZY_MAX) != 0) {
@@ -158,10 +167,11 @@ __device__ __forceinline__ bool softmax_page(SmState& sm, const uint32_t sm_addr
         alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(sm.m - mn);
         sm.m = mn;
         moved = true;
-        if (lr == 0) lds_st<float>(salpha + 4 * kh, alpha);
+        if (!LG && lr == 0) lds_st<float>(salpha + 4 * kh, alpha);
     }
     const float pe = s == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - sm.m);
     sm.l = fmaf(sm.l, alpha, pe);
+    if (LG) return moved;
     if (FMT == FMT_BF16) {
         // P = hi + lo in two bfloat16 parts: the P @ V product keeps ~16 bits of P.
         const __bf16 ph = (__bf16)pe;
@@ -192,7 +202,7 @@ __device__ __forceinline__ void lr_transpose_v(const uint32_t (&xv)[NB], const u
 // one K tile before the MFMAs that use them.
 template <int NB>
 struct PvStep {
-    uint2 ph, pl, b[NB];
+    uint2 ph, pl, b[NB > 0 ? NB : 1];
 };
 template <int FMT, int NB, int B, int NBUF>
 __device__ __forceinline__ void pv_load(PvStep<NB>& q, uint32_t pr, uint32_t plo_off, uint32_t vt, int s) {
@@ -202,7 +212,7 @@ __device__ __forceinline__ void pv_load(PvStep<NB>& q, uint32_t pr, uint32_t plo
     for (int nb = 0; nb < NB; ++nb) q.b[nb] = lds_ld2(vt + vt_step_offset<NB, NBUF>(s, nb) + B * 1024);
 }
 template <int FMT, int NB>
-__device__ __forceinline__ void pv_mfma(f32x4_t (&acc)[NB], const PvStep<NB>& q) {
+__device__ __forceinline__ void pv_mfma(f32x4_t (&acc)[NB > 0 ? NB : 1], const PvStep<NB>& q) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         if (FMT == FMT_BF16) {
@@ -219,7 +229,7 @@ __device__ __forceinline__ void pv_mfma(f32x4_t (&acc)[NB], const PvStep<NB>& q)
 
 // The whole P @ V of the page whose V table is in buffer B (the last page, after the loop).
 template <int FMT, int NB, int NBUF>
-__device__ __forceinline__ void pv_page(f32x4_t (&acc)[NB], uint32_t pr, uint32_t plo_off, uint32_t vt,
+__device__ __forceinline__ void pv_page(f32x4_t (&acc)[NB > 0 ? NB : 1], uint32_t pr, uint32_t plo_off, uint32_t vt,
                                         uint32_t salpha, bool rescale) {
     if (rescale) {
         const f32x4_t al = lds_ld<f32x4_t>(salpha);
@@ -249,7 +259,7 @@ struct LrLoop : PageLoop {
 // reads and the copies do not touch).
 template <int FMT, int MTV, int NB, int NLD, int BC, int BN, int NBUF>
 __device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const LaneAddr<MTV, NB>& la,
-                                        half8_t (&ab)[MTV][4], f32x4_t (&acc)[NB], SmState& sm,
+                                        half8_t (&ab)[MTV][4], f32x4_t (&acc)[NB > 0 ? NB : 1], SmState& sm,
                                         const uint32_t (&doff)[NLD], int ntw, int nh, bool fast, uint32_t sp,
                                         uint32_t plo_off, uint32_t salpha, const int* sqh, int lane, int wave) {
     const DecodeParams& p = params();
@@ -277,10 +287,10 @@ __device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const La
     // Page j's V codes for the transpose, read first; page j - 1's P @ V (its P was 0
     // before the first page) runs inside the K side: its rescale first, then one step
     // per tile.
-    uint32_t xv[NB];
+    uint32_t xv[NB > 0 ? NB : 1];
 #pragma unroll
     for (int k = 0; k < NB; ++k) xv[k] = lds_ld<uint32_t>(la.cv_rd[k] + BC * 1024);
-    if (st.pv_moved) {
+    if (NB > 0 && st.pv_moved) {
         const f32x4_t al = lds_ld<f32x4_t>(salpha);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
@@ -291,19 +301,32 @@ __device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const La
     if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
     PvStep<NB> pq;
     auto hook = [&](int i) {
-        if (i == 0) lr_transpose_v<NB, BC>(xv, la.cv_wr);
-        if (i >= 1 && i <= 4) pv_mfma<FMT, NB>(acc, pq);
-        if (i <= 3) pv_load<FMT, NB, BN, NBUF>(pq, la.pr, plo_off, la.vt, i);
+        if constexpr (NB > 0) {
+            if (i == 0) lr_transpose_v<NB, BC>(xv, la.cv_wr);
+            if (i >= 1 && i <= 4) pv_mfma<FMT, NB>(acc, pq);
+            if (i <= 3) pv_load<FMT, NB, BN, NBUF>(pq, la.pr, plo_off, la.vt, i);
+        }
     };
     k_side<FMT, MTV, NB, BC, NLD, BN, NBUF>(p, la, ab, ntw, nh, fast, sp, lane, wave, cc.b, dc, dp, doff, hook);
 #pragma unroll
     for (int i = MTV; i <= 4; ++i) hook(i);  // the P @ V steps a short K side left
-    if (st.pv_end) flush_partial<NB>(p, sm, acc, nh, st.pv_b + st.g, sqh, lane);
-    st.pv_moved = softmax_page<FMT>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, TILE_TOK * cc.k, cc.lo,
-                                    cc.hi);
+    if constexpr (NB > 0) {
+        if (st.pv_end) flush_partial<NB>(p, sm, acc, nh, st.pv_b + st.g, sqh, lane);
+        st.pv_moved = softmax_page<FMT>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, TILE_TOK * cc.k,
+                                        cc.lo, cc.hi);
+    } else {
+        // The logits pass: page j's logits into the request's rows, and its partial
+        // (m, l) flushed right away when page j ends the request.
+        float* lgd = (float*)(p.ws + p.ws_lg) + (int64_t)cc.b * p.Hq * p.lcap + TILE_TOK * cc.k + la.lg;
+        softmax_page<FMT, true>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, TILE_TOK * cc.k, cc.lo,
+                                cc.hi, lgd);
+    }
     copies_at<LrSched<MTV>, NLD, BN, NBUF>(MTV + 1, dc, dp, opaque_s(wave), doff);
     Cursor nx = cc;
     const bool seg_end = cur_next(nx, P, p.n, st.beg, st.end);
+    if constexpr (NB == 0) {
+        if (seg_end) flush_partial<0>(p, sm, acc, nh, cc.b + st.g, sqh, lane);
+    }
     st.pv_end = seg_end;
     st.pv_b = cc.b;
     st.cc = nx;
@@ -381,6 +404,7 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
             la.cv_rd[k] = base + (uint32_t)((C::V0 + (vb >> 10)) * page_stride<NBUF>() + (vb & 1023));
             la.cv_wr[k] = vt0 + vt_offset<NBUF>((((t >> 2) * 64 * NB + L) << 3) + (t & 3) * 2);
         }
+        la.lg = (lg < nh ? pw[32 + lg] : 0) * p.lcap + lr;
         const int rslot = ((lg & 1) << 1) | (lg >> 1);  // sum_rows4 puts inputs (a, b, c, d) in rows (0, 2, 1, 3)
 #pragma unroll
         for (int g = 0; g < (MTV + 3) / 4; ++g) {
@@ -426,9 +450,11 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
         if (ch < CS_CHUNKS) {
             off = cs_copy_offset(ch, lane, p.cs_s0b);
         } else if (ch < C::K0) {
-            const int vb = (ch - C::V0) * 1024 + 16 * lane;  // byte inside the V rows
-            const int row = vb / C::VPITCH, col = vb % C::VPITCH;
-            if (col < 2 * p.v_rank) off = (uint32_t)(row * (int)p.c_s1 + 2 * p.k_width + col);
+            if constexpr (NB > 0) {
+                const int vb = (ch - C::V0) * 1024 + 16 * lane;  // byte inside the V rows
+                const int row = vb / C::VPITCH, col = vb % C::VPITCH;
+                if (col < 2 * p.v_rank) off = (uint32_t)(row * (int)p.c_s1 + 2 * p.k_width + col);
+            }
         } else if (ch < p.nch) {
             const int Tc = 2 * (ch - C::K0) + (lane >> 5), r = (lane >> 1) & 15, h = lane & 1;
             if (Tc < p.k_width / 16) off = (uint32_t)(r * (int)p.c_s1 + 32 * Tc + 16 * h);
@@ -454,9 +480,9 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     st.nblk = page_block(dc, st.ld);
 
     half8_t ab[MTV][4];
-    f32x4_t acc[NB];
+    f32x4_t acc[NB > 0 ? NB : 1];
 #pragma unroll
-    for (int k = 0; k < NB; ++k) acc[k] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < (NB > 0 ? NB : 1); ++k) acc[k] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
     const int* sqh = &s_qh[wave][0];
     if (NBUF == 3) {
         while (true) {
@@ -482,13 +508,16 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     }
     // The last page's P @ V, once its V table is visible to every wave.
     SKV_WAIT_VM_LGKM0(0);  // also: no copy may land after the workgroup ends
-    lds_barrier();
-    pv_page<FMT, NB, NBUF>(acc, la.pr, plo_off, la.vt + (uint32_t)st.pv_buf * 1024u, salpha, st.pv_moved);
-    flush_partial<NB>(p, sm, acc, nh, st.pv_b + st.g, sqh, lane);
+    if constexpr (NB > 0) {
+        lds_barrier();
+        pv_page<FMT, NB, NBUF>(acc, la.pr, plo_off, la.vt + (uint32_t)st.pv_buf * 1024u, salpha, st.pv_moved);
+        flush_partial<NB>(p, sm, acc, nh, st.pv_b + st.g, sqh, lane);
+    }
 }
 
 template <int FMT, int MTV, int NLD, int NBUF>
 const void* pick_nb(int nb) {
+    if (nb <= 0) return (const void*)&lowrank_kernel<FMT, MTV, 0, NLD, NBUF>;
     if (nb <= 1) return (const void*)&lowrank_kernel<FMT, MTV, 1, NLD, NBUF>;
     if (nb <= 2) return (const void*)&lowrank_kernel<FMT, MTV, 2, NLD, NBUF>;
     return (const void*)&lowrank_kernel<FMT, MTV, 4, NLD, NBUF>;
@@ -508,7 +537,7 @@ const void* pick(int nbuf, int nld, int need, int nb) {
     return nld <= 3 ? pick_mtv<FMT, 3, 3>(need, nb) : pick_mtv<FMT, 6, 3>(need, nb);
 }
 
-int nb_blocks(int nb) { return nb <= 1 ? 1 : nb <= 2 ? 2 : 4; }
+int nb_blocks(int nb) { return nb <= 0 ? 0 : nb <= 1 ? 1 : nb <= 2 ? 2 : 4; }
 
 }  // namespace
 

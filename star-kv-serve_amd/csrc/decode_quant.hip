@@ -37,6 +37,10 @@
 //   nch .. nch + 2NB - 1  the expanded V table (not copied): entry (step s, lane-entry
 //                         L) is 4 tokens x fp16 at byte (s * 64 NB + L) * 8
 // then the 1 KB dummy block.
+//
+// NB = 0 is the logits pass of a two-pass call (V ranks too wide for P @ V here): no V
+// table and no P @ V; the softmax stores each valid logit (log2 domain, K scales
+// applied, fp32) into the workspace logits buffer and keeps m and l for the partials.
 
 #include <type_traits>
 
@@ -75,9 +79,10 @@ struct QLane {
     uint32_t so;                 // outlier-dot row of this lane's slot among kernel slots 0 .. 3
     uint32_t pw;                 // P * s_out write (head lane >> 4, token lane & 15); P * s_in at +128
     uint32_t vs;                 // the (outlier, inlier) V scales of row lane & 15
-    uint32_t pa[NB];             // P @ V A operand: P * s_out or P * s_in of head lane & 3
+    uint32_t pa[NB > 0 ? NB : 1];  // P @ V A operand: P * s_out or P * s_in of head lane & 3
     uint32_t vt;                 // V table entry (0, lane)
-    uint32_t cv_rd[NB], cv_wr[NB];  // V expansion: the byte read, the entry written
+    uint32_t cv_rd[NB > 0 ? NB : 1], cv_wr[NB > 0 ? NB : 1];  // V expansion: the byte read, the entry written
+    int lg;                      // NB = 0: this lane's logit offset in a request's rows (q head x lcap + token)
     uint32_t mk;                 // outlier masks of this lane's row group (table row 0)
     uint32_t sel;                // byte permute: bytes g, g + 4 -> bytes 0, 2
     uint32_t magic;              // 0x64006400
@@ -237,7 +242,7 @@ __device__ __forceinline__ void q_kside(const DecodeParams& p, const QLane<MTV, 
 template <int MTV, int NB>
 __device__ __forceinline__ bool q_softmax(SmState& sm, const QLane<MTV, NB>& la, bool fast, uint32_t sp, int nh,
                                           uint32_t ksw, uint32_t vsw, uint32_t salpha, int lane, int tok0, int lo,
-                                          int hi) {
+                                          int hi, float* lgd = nullptr) {
     const uint32_t sm_addr = la.sm, pw_addr = la.pw;
     const int kh = lane >> 4, lr = lane & 15;
     float s;
@@ -252,7 +257,9 @@ __device__ __forceinline__ bool q_softmax(SmState& sm, const QLane<MTV, NB>& la,
     const float si = __uint_as_float(ksw & 0xffff0000u);
     s = fmaf(__uint_as_float(ksw << 16) - si, lds_ld<float>(sm_addr + Q_EROW * TILE_TOK * 4), si * s);
     const int tok = tok0 + lr;
-    s = tok >= lo && tok < hi && kh < nh ? s : -INFINITY;
+    const bool valid = tok >= lo && tok < hi && kh < nh;
+    s = valid ? s : -INFINITY;
+    if (NB == 0 && valid) *lgd = s;
     float alpha = 1.f;
     bool moved = false;
     if (__builtin_amdgcn_ballot_w64(s > sm.m + LAZY_MAX) != 0) {
@@ -260,10 +267,11 @@ __device__ __forceinline__ bool q_softmax(SmState& sm, const QLane<MTV, NB>& la,
         alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(sm.m - mn);
         sm.m = mn;
         moved = true;
-        if (lr == 0) lds_st<float>(salpha + 4 * kh, alpha);
+        if (NB > 0 && lr == 0) lds_st<float>(salpha + 4 * kh, alpha);
     }
     const float pe = s == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - sm.m);
     sm.l = fmaf(sm.l, alpha, pe);
+    if (NB == 0) return moved;
     lds_st<uint16_t>(pw_addr, __builtin_bit_cast(uint16_t, (_Float16)(pe * __uint_as_float(vsw << 16))));
     lds_st<uint16_t>(pw_addr + 128, __builtin_bit_cast(uint16_t, (_Float16)(pe * __uint_as_float(vsw & 0xffff0000u))));
     return moved;
@@ -287,10 +295,10 @@ __device__ __forceinline__ void q_expand_v(const uint32_t (&xv)[NB], const uint3
 // are read one tile before the MFMA that uses them.
 template <int NB>
 struct PvStep {
-    uint2 a[NB], b[NB];
+    uint2 a[NB > 0 ? NB : 1], b[NB > 0 ? NB : 1];
 };
 template <int NB, int B>
-__device__ __forceinline__ void pv_load(PvStep<NB>& q, const uint32_t (&pa)[NB], uint32_t vt, int s) {
+__device__ __forceinline__ void pv_load(PvStep<NB>& q, const uint32_t (&pa)[NB > 0 ? NB : 1], uint32_t vt, int s) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         q.a[nb] = lds_ld2(pa[nb] + 8 * s);
@@ -298,7 +306,7 @@ __device__ __forceinline__ void pv_load(PvStep<NB>& q, const uint32_t (&pa)[NB],
     }
 }
 template <int NB>
-__device__ __forceinline__ void pv_mfma(f32x4_t (&acc)[NB], const PvStep<NB>& q) {
+__device__ __forceinline__ void pv_mfma(f32x4_t (&acc)[NB > 0 ? NB : 1], const PvStep<NB>& q) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
         acc[nb] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, q.a[nb]),
@@ -308,8 +316,8 @@ __device__ __forceinline__ void pv_mfma(f32x4_t (&acc)[NB], const PvStep<NB>& q)
 // acc[nb] = alpha * acc[nb] + (P * s)[4 heads, 16 tokens] @ V[16 tokens, lane-entries]
 // for the page whose V table is in buffer B, on v_mfma_f32_4x4x4_16b with a per-block A.
 template <int NB, int B>
-__device__ __forceinline__ void q_pv(f32x4_t (&acc)[NB], const uint32_t (&pa)[NB], uint32_t vt, uint32_t salpha,
-                                     bool rescale) {
+__device__ __forceinline__ void q_pv(f32x4_t (&acc)[NB > 0 ? NB : 1], const uint32_t (&pa)[NB > 0 ? NB : 1],
+                                     uint32_t vt, uint32_t salpha, bool rescale) {
     if (rescale) {
         const f32x4_t al = lds_ld<f32x4_t>(salpha);
 #pragma unroll
@@ -332,8 +340,8 @@ __device__ __forceinline__ void q_pv(f32x4_t (&acc)[NB], const uint32_t (&pa)[NB
 // The partial of a request: m, l and acc of this wave's heads into partial slot `slot`,
 // then reset. colv[nb] = the V column of this lane's entry in block nb (-1: none).
 template <int NB>
-__device__ __forceinline__ void q_flush(const DecodeParams& p, SmState& sm, f32x4_t (&acc)[NB], int nh, int slot,
-                                        const int* sqh, int lane, const int (&colv)[NB]) {
+__device__ __forceinline__ void q_flush(const DecodeParams& p, SmState& sm, f32x4_t (&acc)[NB > 0 ? NB : 1], int nh,
+                                        int slot, const int* sqh, int lane, const int (&colv)[NB > 0 ? NB : 1]) {
     const int ln = opaque(lane);
     const int kh = ln >> 4, lr = ln & 15;
     const int64_t base = (int64_t)slot * p.Hq;
@@ -370,11 +378,11 @@ struct QLoop : PageLoop {
 // which this iteration's P @ V reads.
 template <bool GEN, int MTV, int NB, int NLD, int BC, int BN>
 __device__ __forceinline__ bool q_iter(QLoop& st, const DmaConst& dc, const QLane<MTV, NB>& la,
-                                       half8_t (&ab)[MTV][4], const SlotPack<MTV>& sp8, f32x4_t (&acc)[NB],
-                                       SmState& sm,
+                                       half8_t (&ab)[MTV][4], const SlotPack<MTV>& sp8,
+                                       f32x4_t (&acc)[NB > 0 ? NB : 1], SmState& sm,
                                        const uint32_t (&doff)[NLD], int ntw, int nh, int nf, bool fast, uint32_t sp,
-                                       uint32_t salpha, uint32_t base, const int* sqh, const int (&colv)[NB], int lane,
-                                       int wave) {
+                                       uint32_t salpha, uint32_t base, const int* sqh,
+                                       const int (&colv)[NB > 0 ? NB : 1], int lane, int wave) {
     const DecodeParams& p = params();
     cint_p P = (cint_p)(p.ws + 4);
     if (!st.cc.valid) {
@@ -399,12 +407,12 @@ __device__ __forceinline__ bool q_iter(QLoop& st, const DmaConst& dc, const QLan
     // Reads of page j for the V expansion and the softmax, issued first: they complete
     // under the K side. Page j - 1's P @ V (its P was 0 before the first page) runs
     // inside the K side: its rescale first, then one step per tile.
-    uint32_t xv[NB];
+    uint32_t xv[NB > 0 ? NB : 1];
 #pragma unroll
     for (int k = 0; k < NB; ++k) xv[k] = lds_ld<uint8_t>(la.cv_rd[k] + BC * 1024);
     const uint32_t ksw = lds_ld<uint32_t>(la.ksm + BC * 1024);
-    const uint32_t vsw = lds_ld<uint32_t>(la.vs + BC * 1024);
-    if (st.pv_moved) {
+    const uint32_t vsw = NB > 0 ? lds_ld<uint32_t>(la.vs + BC * 1024) : 0u;
+    if (NB > 0 && st.pv_moved) {
         const f32x4_t al = lds_ld<f32x4_t>(salpha);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
@@ -415,19 +423,30 @@ __device__ __forceinline__ bool q_iter(QLoop& st, const DmaConst& dc, const QLan
     if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
     PvStep<NB> pq;
     auto hook = [&](int i) {
-        if (i == 0) q_expand_v<NB, BC>(xv, la.cv_wr);
-        if (i >= 1 && i <= 4) pv_mfma<NB>(acc, pq);
-        if (i <= 3) pv_load<NB, BN>(pq, la.pa, la.vt, i);
+        if constexpr (NB > 0) {
+            if (i == 0) q_expand_v<NB, BC>(xv, la.cv_wr);
+            if (i >= 1 && i <= 4) pv_mfma<NB>(acc, pq);
+            if (i <= 3) pv_load<NB, BN>(pq, la.pa, la.vt, i);
+        }
     };
     q_kside<GEN, MTV, NB, BC, NLD, BN>(p, la, ab, sp8, ntw, nh, nf, fast, sp, base, lane, wave, cc.b, dc, dp, doff,
                                        hook);
 #pragma unroll
     for (int i = MTV; i <= 4; ++i) hook(i);  // the P @ V steps a short K side left
-    if (st.pv_end) q_flush<NB>(p, sm, acc, nh, st.pv_b + st.g, sqh, lane, colv);
-    st.pv_moved = q_softmax<MTV, NB>(sm, la, fast, sp, nh, ksw, vsw, salpha, lane, TILE_TOK * cc.k, cc.lo, cc.hi);
+    if constexpr (NB > 0) {
+        if (st.pv_end) q_flush<NB>(p, sm, acc, nh, st.pv_b + st.g, sqh, lane, colv);
+        st.pv_moved = q_softmax<MTV, NB>(sm, la, fast, sp, nh, ksw, vsw, salpha, lane, TILE_TOK * cc.k, cc.lo, cc.hi);
+    } else {
+        // The logits pass: page j's logits into the request's rows.
+        float* lgd = (float*)(p.ws + p.ws_lg) + (int64_t)cc.b * p.Hq * p.lcap + TILE_TOK * cc.k + la.lg;
+        q_softmax<MTV, NB>(sm, la, fast, sp, nh, ksw, vsw, salpha, lane, TILE_TOK * cc.k, cc.lo, cc.hi, lgd);
+    }
     copies_at<QSched<MTV>, NLD, BN>(MTV + 1, dc, dp, opaque_s(wave), doff);
     Cursor nx = cc;
     const bool seg_end = cur_next(nx, P, p.n, st.beg, st.end);
+    if constexpr (NB == 0) {  // the request's partial (m, l) as soon as its last page is done
+        if (seg_end) flush_partial<0>(p, sm, acc, nh, cc.b + st.g, sqh, lane);
+    }
     st.pv = true;
     st.pv_end = seg_end;
     st.pv_b = cc.b;
@@ -527,6 +546,7 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
         for (int nb = 0; nb < NB; ++nb)
             la.pa[nb] = lds_addr(&s_pq[wave][64 * nb + lane < O4 ? 0 : 1][0]) + (uint32_t)(lane & 3) * TILE_TOK * 2;
         la.vt = vt0 + 8 * lane;
+        la.lg = (lg < nh ? pw[32 + lg] : 0) * p.lcap + lr;
         // V expansion: token t = tid % 16, lane-entries L, L + 1 with L = 2 (tid / 16) + 64 k.
         const int t = tid & 15;
 #pragma unroll
@@ -561,7 +581,7 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
             la.cv_wr[k] = vgpr_pin(la.cv_wr[k]);
         }
     }
-    int colv[NB];
+    int colv[NB > 0 ? NB : 1];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         const int L = 64 * nb + lane;
@@ -607,9 +627,9 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     st.nblk = page_block(dc, st.ld);
 
     half8_t ab[MTV][4];
-    f32x4_t acc[NB];
+    f32x4_t acc[NB > 0 ? NB : 1];
 #pragma unroll
-    for (int k = 0; k < NB; ++k) acc[k] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < (NB > 0 ? NB : 1); ++k) acc[k] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
     const int* sqh = &s_qh[wave][0];
     // The page loop, in one of two forms picked per wave (see q_kside).
     auto loop = [&](auto gen_tag) {
@@ -633,7 +653,7 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     // The last page's P @ V, once its V table is visible to every wave.
     SKV_WAIT_VM_LGKM0(0);  // also: no copy may land after the workgroup ends
     lds_barrier();
-    if (st.pv) {
+    if (NB > 0 && st.pv) {
         q_pv<NB, 0>(acc, la.pa, la.vt + (uint32_t)st.pv_buf * 1024u, salpha, st.pv_moved);
         q_flush<NB>(p, sm, acc, nh, st.pv_b + st.g, sqh, lane, colv);
     }
@@ -641,6 +661,7 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
 
 template <int MTV, int NLD>
 const void* q_pick_nb(int nb) {
+    if (nb <= 0) return (const void*)&quant_kernel<MTV, 0, NLD>;
     if (nb <= 1) return (const void*)&quant_kernel<MTV, 1, NLD>;
     if (nb <= 2) return (const void*)&quant_kernel<MTV, 2, NLD>;
     if (nb <= 3) return (const void*)&quant_kernel<MTV, 3, NLD>;
@@ -652,7 +673,7 @@ const void* q_pick_mtv(int need, int nb) {
     return need <= 4 ? q_pick_nb<4, NLD>(nb) : need <= 8 ? q_pick_nb<8, NLD>(nb) : q_pick_nb<10, NLD>(nb);
 }
 
-int q_nb_blocks(int nb) { return nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 3 ? 3 : 5; }
+int q_nb_blocks(int nb) { return nb <= 0 ? 0 : nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 3 ? 3 : 5; }
 
 }  // namespace
 

@@ -10,9 +10,10 @@ import os
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstarkv_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, F16, BF16 = 0, 1, 2
+CACHE_Q3_2 = 16  # cache kind of the 3.2-bit QuantRow cache
 _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 _P = ctypes.c_void_p
@@ -35,13 +36,15 @@ SIGNATURES = {
     "starkv_decode_grid": (_I, [_I, _I]),
     "starkv_profile_begin": (_I, [_I]),
     "starkv_profile_end": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
-    "starkv_decode_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
+    "starkv_decode_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I, _I, _I]),
+    "starkv_decode_two_pass": (_I, [_I, _I, _I, _I]),
+    "starkv_decode_set_path": (_I, [_I]),
     "starkv_lowrank_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _I, _P, _I64, _I64, _P, _I,
-                                   _I, _I, _I, _P, _I64, _I, _P, _P, _I, _P, _I64, _I64, _I, _P, _I64, _I,
-                                   _F, _P, _I64, _I64, _I, _P, _SZ, _I]),
+                                   _I, _I, _I, _P, _I64, _I, _P, _P, _I, _P, _I64, _I64, _I, _I, _P, _I64,
+                                   _I, _F, _P, _I64, _I64, _I, _P, _SZ, _I]),
     "starkv_quant_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _P, _I64, _I64, _P, _I, _I, _I,
-                                 _I, _I, _I, _P, _I64, _I, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I, _F, _P,
-                                 _I64, _I64, _I, _P, _SZ, _I]),
+                                 _I, _I, _I, _P, _I64, _I, _P, _P, _P, _P, _I64, _I64, _I, _P, _I64, _I, _F,
+                                 _P, _I64, _I64, _I, _P, _SZ, _I]),
 }
 
 _LIB = None
@@ -85,6 +88,14 @@ def stream_of(t: torch.Tensor) -> int:
 
 def ptr(t: torch.Tensor) -> int:
     return t.data_ptr()
+
+
+def set_decode_path(mode: int) -> int:
+    """0 = automatic (default), 1 = one-pass only, 2 = two-pass always; returns the previous mode."""
+    prev = lib().starkv_decode_set_path(int(mode))
+    if prev < 0:
+        check(1, "decode_set_path")
+    return prev
 
 
 def profile_begin(max_calls: int) -> None:

@@ -20,7 +20,7 @@ from dataclasses import dataclass
 import torch
 
 from starkv_serve import _hip
-from starkv_serve.kernels.paged_decode import MAX_REQUESTS_PER_LAUNCH, cos_sin_for_kernel
+from starkv_serve.kernels.paged_decode import _as_i32, cos_sin_for_kernel, rows_per_launch
 
 OUTLIER_RATIO = 0.2
 HADAMARD_SEED = 1234
@@ -140,8 +140,8 @@ def pack_kv(k_codes, v_codes, cache, slot_mapping, row: QuantRow, k_ranks, k_off
     if n == 0:
         return
     _hip.require_cuda(k_codes, v_codes, cache, slot_mapping, k_ranks, k_offsets, k_nouts)
-    k_ranks, k_offsets, k_nouts = (t if t.dtype == torch.int32 else t.to(torch.int32)
-                                   for t in (k_ranks, k_offsets, k_nouts))
+    k_ranks, k_offsets, k_nouts = (_as_i32(t) for t in (k_ranks, k_offsets, k_nouts))
+    slot_mapping = slot_mapping.contiguous()
     rc = _hip.lib().starkv_pack_kv(
         _hip.stream_of(cache), k_codes.data_ptr(), k_codes.stride(0), v_codes.data_ptr(), v_codes.stride(0),
         _hip.dtype_code(k_codes), cache.data_ptr(), cache.stride(0), cache.stride(1), cache.shape[1],
@@ -164,6 +164,7 @@ def fold_q(q, k_up, head_of_lane, scale):
     if n == 0 or W == 0:
         return ab
     _hip.require_cuda(q, k_up, head_of_lane)
+    head_of_lane = _as_i32(head_of_lane)
     rc = _hip.lib().starkv_fold_q(_hip.stream_of(q), q.data_ptr(), q.stride(0), q.stride(1), _hip.dtype_code(q),
                                   k_up.data_ptr(), k_up.stride(0), _hip.dtype_code(k_up), head_of_lane.data_ptr(),
                                   n, W, float(scale), ab.data_ptr())
@@ -205,17 +206,20 @@ def paged_quant_decode(
         return out
     L = _hip.lib()
     cs = cos_sin_for_kernel(cos_sin_cache)
-    block_table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
-    seq_lens = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
+    block_table = _as_i32(block_table)
+    seq_lens = _as_i32(seq_lens)
+    th, tn, tl = (_as_i32(t) for t in (th, tn, tl))
     k_tiles_n = row.k_width // 16
     assert th.numel() == k_tiles_n, "k_tiles must cover k_width / 16 tiles"
     stream = _hip.stream_of(query)
-    for s in range(0, n, MAX_REQUESTS_PER_LAUNCH):
-        e = min(n, s + MAX_REQUESTS_PER_LAUNCH)
+    step = rows_per_launch(_hip.CACHE_Q3_2, H, row.k_width, row.v_rank, int(max_seq_len))
+    for s in range(0, n, step):
+        e = min(n, s + step)
         m = e - s
         grid = L.starkv_decode_grid(m, int(max_seq_len))
-        ws = torch.empty(L.starkv_decode_workspace_bytes(m, H, k_tiles_n, row.v_rank, grid), dtype=torch.uint8,
-                         device=query.device)
+        ws = torch.empty(L.starkv_decode_workspace_bytes(_hip.CACHE_Q3_2, m, H, H, row.k_width, row.v_rank,
+                                                         int(max_seq_len), grid),
+                         dtype=torch.uint8, device=query.device)
         q, bt, o = query[s:e], block_table[s:e], out[s:e]
         rc = L.starkv_quant_decode(
             stream, q.data_ptr(), q.stride(0), q.stride(1), _hip.dtype_code(q),
@@ -223,7 +227,8 @@ def paged_quant_decode(
             bt.data_ptr(), bt.stride(0), bt.stride(1), seq_lens[s:e].data_ptr(), m, H, int(max_seq_len),
             row.k_width, row.v_rank, row.nbytes, k_up.data_ptr(), k_up.stride(0), _hip.dtype_code(k_up),
             th.data_ptr(), tn.data_ptr(), tl.data_ptr(), v_up_by_q.data_ptr(), v_up_by_q.stride(0),
-            v_up_by_q.stride(1), cs.data_ptr(), cs.stride(0), _hip.dtype_code(cs), float(scale), o.data_ptr(),
+            v_up_by_q.stride(1), _hip.dtype_code(v_up_by_q), cs.data_ptr(), cs.stride(0), _hip.dtype_code(cs),
+            float(scale), o.data_ptr(),
             o.stride(0), o.stride(1), _hip.dtype_code(o), ws.data_ptr(), ws.numel(), grid)
         _hip.check(rc, "paged_quant_decode")
     return out

@@ -20,7 +20,8 @@ def test_header_declares_the_api():
     names = declared()
     for n in ("starkv_lowrank_decode", "starkv_quant_decode", "starkv_pack_kv", "starkv_write_codes",
               "starkv_fold_q", "starkv_decode_grid", "starkv_decode_workspace_bytes", "starkv_last_error",
-              "starkv_abi_version", "starkv_write_kv", "starkv_write_kv_workspace_bytes"):
+              "starkv_abi_version", "starkv_write_kv", "starkv_write_kv_workspace_bytes",
+              "starkv_decode_two_pass", "starkv_decode_set_path"):
         assert n in names
 
 
@@ -49,9 +50,41 @@ def test_bad_arguments_return_errors():
 def test_workspace_size_is_a_host_function():
     from starkv_serve import _hip
     L = _hip.lib()
-    a = L.starkv_decode_workspace_bytes(64, 32, 80, 64, 256)
-    b = L.starkv_decode_workspace_bytes(64, 32, 80, 64, 128)
+    BF16, F16, Q = _hip.BF16, _hip.F16, _hip.CACHE_Q3_2
+    a = L.starkv_decode_workspace_bytes(BF16, 64, 32, 32, 1280, 64, 8192, 256)
+    b = L.starkv_decode_workspace_bytes(BF16, 64, 32, 32, 1280, 64, 8192, 128)
     assert a > b > 64 * 80 * 4096
+    # the one-pass form needs no logits buffer: the context length does not matter
+    assert L.starkv_decode_workspace_bytes(BF16, 64, 32, 32, 1280, 64, 100, 256) == a
+    assert L.starkv_decode_workspace_bytes(BF16, 0, 32, 32, 1280, 64, 100, 256) == 0
+
+
+def test_two_pass_selection():
+    """Which V ranks take the two-pass form (a host function of the layer shape)."""
+    from starkv_serve import _hip
+    L = _hip.lib()
+    BF16, F16, Q = _hip.BF16, _hip.F16, _hip.CACHE_Q3_2
+    assert L.starkv_decode_two_pass(BF16, 32, 1280, 64) == 0
+    assert L.starkv_decode_two_pass(BF16, 32, 1280, 256) == 0
+    assert L.starkv_decode_two_pass(BF16, 32, 880, 272) == 1
+    assert L.starkv_decode_two_pass(F16, 32, 880, 1280) == 1
+    assert L.starkv_decode_two_pass(Q, 32, 1280, 64) == 0
+    assert L.starkv_decode_two_pass(Q, 32, 880, 256) == 0      # 51 outliers (padded to 52) + 205 inliers: 5 blocks
+    assert L.starkv_decode_two_pass(Q, 32, 880, 1290) == 1
+    # two-pass workspaces add the fp32 logits [n, H, max_seq_len rounded up to 16]
+    one = L.starkv_decode_workspace_bytes(BF16, 64, 32, 32, 880, 1280, 8192, 256)
+    two = L.starkv_decode_workspace_bytes(BF16, 64, 32, 32, 880, 1280, 8200, 256)
+    assert two - one == 64 * 32 * 16 * 4
+    assert one >= 64 * 32 * 8192 * 4 + 320 * 32 * 1280 * 4
+    # forcing a form
+    assert _hip.set_decode_path(2) == 0
+    try:
+        assert L.starkv_decode_two_pass(BF16, 32, 1280, 64) == 1
+        assert L.starkv_decode_set_path(1) == 2
+        assert L.starkv_decode_two_pass(BF16, 32, 880, 1280) == 0
+        assert L.starkv_decode_set_path(7) == -1 and b"mode 7" in L.starkv_last_error()
+    finally:
+        _hip.set_decode_path(0)
 
 
 def test_write_kv_validation():

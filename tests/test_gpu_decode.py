@@ -64,17 +64,17 @@ def run_lowrank(wl_gpu, grid=None):
     tiles = (H // Hkv) * wl_gpu.k_width // 16
     out = torch.empty(n, H, 128, dtype=wl_gpu.v_up_by_q.dtype, device=q.device)
     L = _hip.lib()
-    ws = torch.empty(L.starkv_decode_workspace_bytes(n, H, tiles, wl_gpu.v_rank, grid), dtype=torch.uint8,
-                     device=q.device)
+    ws = torch.empty(L.starkv_decode_workspace_bytes(_hip.dtype_code(kv), n, H, Hkv, wl_gpu.k_width, wl_gpu.v_rank,
+                                                     wl_gpu.max_seq_len, grid), dtype=torch.uint8, device=q.device)
     cs, vq, U = cos_sin_for_kernel(wl_gpu.cos_sin_cache), wl_gpu.v_up_by_q, wl_gpu.k_up  # the ABI takes fp16
     rc = L.starkv_lowrank_decode(_hip.stream_of(q), q.data_ptr(), q.stride(0), q.stride(1), _hip.dtype_code(q),
                                  kv.data_ptr(), kv.stride(0), kv.stride(1), _hip.dtype_code(kv), kv.shape[1],
                                  bt.data_ptr(), bt.stride(0), bt.stride(1), sl.data_ptr(), n, H, Hkv,
                                  wl_gpu.max_seq_len, U.data_ptr(), U.stride(0), _hip.dtype_code(U),
                                  wl_gpu.k_ranks.data_ptr(), wl_gpu.k_head_offsets.data_ptr(), wl_gpu.k_width,
-                                 vq.data_ptr(), vq.stride(0), vq.stride(1), wl_gpu.v_rank, cs.data_ptr(), cs.stride(0),
-                                 _hip.dtype_code(cs), wl_gpu.scale, out.data_ptr(), out.stride(0), out.stride(1),
-                                 _hip.dtype_code(out), ws.data_ptr(), ws.numel(), grid)
+                                 vq.data_ptr(), vq.stride(0), vq.stride(1), _hip.dtype_code(vq), wl_gpu.v_rank,
+                                 cs.data_ptr(), cs.stride(0), _hip.dtype_code(cs), wl_gpu.scale, out.data_ptr(),
+                                 out.stride(0), out.stride(1), _hip.dtype_code(out), ws.data_ptr(), ws.numel(), grid)
     _hip.check(rc, "lowrank_decode")
     return out
 
@@ -274,3 +274,169 @@ def test_more_requests_than_one_launch(cuda, quant):
         out = paged_starkv_decode(*wl.decode_args())
         torch.cuda.synchronize()
         assert_close(out, lowrank_truth(wl), "chunked bf16")
+
+
+# ---------------------------------------------------------------------------
+# Two-pass form: V ranks wider than the one-pass kernels take (the reference
+# checkpoint's real shape, K width ~880 and V rank ~1290, train.py:360-362), and the
+# two-pass form forced on the one-pass edge cases.
+# ---------------------------------------------------------------------------
+
+@pytest.fixture
+def two_pass():
+    prev = _hip.set_decode_path(2)
+    yield
+    _hip.set_decode_path(prev)
+
+
+# K ranks of a 0.75-ratio layer: 880 lanes over 32 heads (widths multiples of 16).
+RANKS_880 = [32] * 23 + [16] * 9
+
+
+def subset_truth(wl, idx, quant):
+    """The oracle on the requests idx only (requests are independent)."""
+    sub = W.Workload(**{**wl.__dict__})
+    sub.query = wl.query[idx]
+    sub.block_table = wl.block_table[idx]
+    sub.seq_lens = wl.seq_lens[idx]
+    sub.lengths = [wl.lengths[i] for i in idx]
+    return quant_truth(sub) if quant else lowrank_truth(sub)
+
+
+@pytest.mark.parametrize("name", ["ragged_edges", "gqa_h32_kv8", "fp16", "strided_cache", "peaked_q",
+                                  "graph_span", "ranks_not_16", "block_128", "wide_k1376", "v_rank_256_h16"])
+def test_lowrank_two_pass_forced(cuda, two_pass, name):
+    lengths, kw = LOWRANK_CASES[name]
+    kw = dict(kw)
+    print(f"\n[lowrank two-pass] case={name} lengths={lengths[:8]} {kw}", flush=True)
+    nh = kw.pop("num_heads", 32)
+    wl = W.make_lowrank(lengths, num_heads=nh, seed=100 + len(name), **kw)
+    out = paged_starkv_decode(*wl.to(cuda).decode_args())
+    torch.cuda.synchronize()
+    assert_close(out, lowrank_truth(wl), name)
+
+
+@pytest.mark.parametrize("name", ["ragged_edges", "v_rank_32", "strided_cache", "graph_span", "fp16",
+                                  "block_64", "big_heads", "ranks_not_16", "v_rank_256_h8"])
+def test_quant_two_pass_forced(cuda, two_pass, name):
+    lengths, kw = QUANT_CASES[name]
+    kw = dict(kw)
+    print(f"\n[quant two-pass] case={name} lengths={lengths[:8]} {kw}", flush=True)
+    nh = kw.pop("num_heads", 32)
+    wl = W.make_quant(lengths, num_heads=nh, seed=200 + len(name), device=cuda, **kw)
+    out = paged_quant_decode(*wl.decode_args())
+    torch.cuda.synchronize()
+    assert_close(out, quant_truth(wl), name)
+
+
+def test_two_pass_grids_and_one_pass_agree(cuda, two_pass):
+    """The two passes split the tokens identically for any grid; results agree with the
+    one-pass form to within rounding."""
+    wl = W.make_lowrank([700, 33, 1500, 16], num_heads=32, seed=31)
+    g = wl.to(cuda)
+    truth = lowrank_truth(wl)
+    for grid in (1, 7, 300):
+        assert_close(run_lowrank(g, grid=grid), truth, f"two-pass grid={grid}")
+    two = paged_starkv_decode(*g.decode_args())
+    _hip.set_decode_path(1)
+    one = paged_starkv_decode(*g.decode_args())
+    torch.cuda.synchronize()
+    d = (two.float() - one.float()).abs().max().item()
+    print(f"two-pass vs one-pass max |diff| = {d:.3e}", flush=True)
+    assert d <= 2e-3
+
+
+WIDE_CASES = {
+    # name: (lengths, kwargs) -- V ranks the one-pass kernels do not take
+    "bf16_v272": ([300, 17, 1024], dict(v_rank=272)),
+    "bf16_v1024_w880": ([640, 129, 2000], dict(v_rank=1024, ranks=RANKS_880)),
+    "bf16_v1296_w880": ([1, 15, 16, 17, 999, 4096], dict(v_rank=1296, ranks=RANKS_880)),
+    "fp16_v1280_w880": ([513, 90, 2048], dict(v_rank=1280, ranks=RANKS_880, dtype=torch.float16)),
+    "bf16_v2048_gqa": ([700, 64], dict(v_rank=2048, num_kv_heads=8, ranks=[32] * 8)),
+    "bf16_v4096_h8": ([300, 31], dict(v_rank=4096, num_heads=8, ranks=[32] * 8)),  # two column windows
+    "bf16_v1280_strided": ([200, 31], dict(v_rank=1280, ranks=RANKS_880, col_pad=48)),
+    "bf16_v1280_graph_span": ([100, 37, 999], dict(v_rank=1280, ranks=RANKS_880, max_seq_len=4096)),
+}
+
+
+@pytest.mark.parametrize("name", list(WIDE_CASES))
+def test_lowrank_wide_v_vs_oracle(cuda, name):
+    lengths, kw = WIDE_CASES[name]
+    kw = dict(kw)
+    print(f"\n[lowrank wide] case={name} lengths={lengths[:8]} {kw}", flush=True)
+    nh = kw.pop("num_heads", 32)
+    wl = W.make_lowrank(lengths, num_heads=nh, seed=300 + len(name), **kw)
+    two = _hip.lib().starkv_decode_two_pass(_hip.dtype_code(wl.kv_cache), nh, wl.k_width, wl.v_rank)
+    assert two == 1, (wl.k_width, wl.v_rank)
+    out = paged_starkv_decode(*wl.to(cuda).decode_args())
+    torch.cuda.synchronize()
+    assert_close(out, lowrank_truth(wl), name)
+
+
+QUANT_WIDE_CASES = {
+    "v336": ([300, 17, 1024], dict(v_rank=336)),  # 67 outliers (padded to 68) + 269 inliers: 6 blocks
+    "v1290_w880": ([1, 15, 16, 17, 999, 4096], dict(v_rank=1290, ranks=RANKS_880)),
+    "v1024_w880_fp16": ([640, 129], dict(v_rank=1024, ranks=RANKS_880, dtype=torch.float16)),
+    "v1291_odd": ([500, 77], dict(v_rank=1291, ranks=RANKS_880)),  # odd outlier count and inlier bytes
+    "v4096_h8": ([300, 31], dict(v_rank=4096, num_heads=8, ranks=[32] * 8)),
+    "v1290_graph_span": ([100, 37, 999], dict(v_rank=1290, ranks=RANKS_880, max_seq_len=4096)),
+    "v1290_block64": ([900, 65, 3], dict(v_rank=1290, ranks=RANKS_880, block_size=64)),
+}
+
+
+@pytest.mark.parametrize("name", list(QUANT_WIDE_CASES))
+def test_quant_wide_v_vs_oracle(cuda, name):
+    lengths, kw = QUANT_WIDE_CASES[name]
+    kw = dict(kw)
+    print(f"\n[quant wide] case={name} lengths={lengths[:8]} {kw}", flush=True)
+    nh = kw.pop("num_heads", 32)
+    wl = W.make_quant(lengths, num_heads=nh, seed=400 + len(name), device=cuda, **kw)
+    two = _hip.lib().starkv_decode_two_pass(_hip.CACHE_Q3_2, nh, wl.k_width, wl.v_rank)
+    assert two == 1, (wl.k_width, wl.v_rank)
+    check_packed_rows(wl)
+    out = paged_quant_decode(*wl.decode_args())
+    torch.cuda.synchronize()
+    assert_close(out, quant_truth(wl), name)
+
+
+@pytest.mark.parametrize("quant", [False, True])
+def test_wide_v_bs64_ragged_full_size(cuda, quant):
+    """C1/C2-shaped batch (64 requests, lengths U[1024, 8192]) at the reference checkpoint's
+    shape: K width 880, V rank 1280 (bf16, padded to 16) / 1290 (3.2-bit). The kernels run
+    on all 64 requests; the oracle checks 8 of them (requests are independent), and a
+    physical page permutation leaves every output bit-identical."""
+    lengths = W.ragged_lengths(1006 + quant)
+    print(f"\n[wide bs64] quant={quant} {sum(lengths)} tokens", flush=True)
+    if quant:
+        wl = W.make_quant(lengths, num_heads=32, ranks=RANKS_880, v_rank=1290, seed=1006, device=cuda,
+                          gen_device=cuda)
+        wl.k_codes = wl.v_codes = None
+        out = paged_quant_decode(*wl.decode_args())
+    else:
+        wl = W.make_lowrank(lengths, num_heads=32, ranks=RANKS_880, v_rank=1280, seed=1006, gen_device=cuda).to(cuda)
+        out = paged_starkv_decode(*wl.decode_args())
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    idx = [0, 9, 17, 26, 35, 44, 53, 63]
+    assert_close(out[idx], subset_truth(wl, idx, quant), "wide bs64 subset")
+    nb = wl.kv_cache.shape[0]
+    perm = torch.cat([torch.zeros(1, dtype=torch.long), 1 + torch.randperm(nb - 1)]).to(cuda)
+    inv = torch.argsort(perm).to(torch.int32)
+    wl.kv_cache = wl.kv_cache[perm]
+    wl.block_table = inv[wl.block_table.long()]
+    out2 = paged_quant_decode(*wl.decode_args()) if quant else paged_starkv_decode(*wl.decode_args())
+    assert torch.equal(out, out2)
+
+
+def test_k_up_and_v_up_dtypes_independent(cuda):
+    """k_up fp32 with v_up_by_q bf16 (and the reverse): each is read with its own dtype."""
+    wl = W.make_lowrank([300, 17], num_heads=32, seed=41)
+    truth = lowrank_truth(wl)
+    g = wl.to(cuda)
+    g.k_up = g.k_up.float()
+    assert_close(paged_starkv_decode(*g.decode_args()), truth, "k_up fp32, v_up bf16")
+    g = wl.to(cuda)
+    g.v_up_by_q = g.v_up_by_q.float()
+    out = paged_starkv_decode(*g.decode_args())
+    assert out.dtype == torch.float32
+    assert_close(out.to(torch.bfloat16), truth, "k_up bf16, v_up fp32")
