@@ -210,6 +210,29 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0(int n) {
     }
 }
 
+// The same for counts up to 63 (rounded down to a multiple of 4 above 15, which only
+// waits for more).
+__device__ __forceinline__ void wait_vmcnt_lgkm0_wide(int n) {
+    if (n <= 15) {
+        wait_vmcnt_lgkm0(n);
+        return;
+    }
+    switch (min(n, 63) >> 2) {
+        case 4: SKV_WAIT_VM_LGKM0(16); break;
+        case 5: SKV_WAIT_VM_LGKM0(20); break;
+        case 6: SKV_WAIT_VM_LGKM0(24); break;
+        case 7: SKV_WAIT_VM_LGKM0(28); break;
+        case 8: SKV_WAIT_VM_LGKM0(32); break;
+        case 9: SKV_WAIT_VM_LGKM0(36); break;
+        case 10: SKV_WAIT_VM_LGKM0(40); break;
+        case 11: SKV_WAIT_VM_LGKM0(44); break;
+        case 12: SKV_WAIT_VM_LGKM0(48); break;
+        case 13: SKV_WAIT_VM_LGKM0(52); break;
+        case 14: SKV_WAIT_VM_LGKM0(56); break;
+        default: SKV_WAIT_VM_LGKM0(60); break;
+    }
+}
+
 // Workgroup barrier that does not drain outstanding global->LDS copies: the
 // caller has already waited for what it needs (lgkmcnt(0) included). The empty asm
 // keeps the compiler from moving LDS accesses across it (the barrier intrinsic itself

@@ -785,6 +785,7 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     p.ws_plan = wl.plan; p.ws_ab = wl.ab;
     p.ws_m = wl.m; p.ws_l = wl.l; p.ws_acc = wl.acc;
     p.ws_lg = wl.lg; p.lcap = lcap;
+    p.ws_o = wl.o; p.acc_ld = wl.ld;
 
     PrepArgs pa;
     pa.seq_lens = a.seq_lens; pa.n = a.n; pa.max_seq_len = a.max_seq_len; pa.grid = a.grid;

@@ -46,6 +46,8 @@ constexpr float LAZY_MAX = 8.f;             // log2 headroom before the running 
 //   lg     fp32  [n][Hq][lcap]  (two-pass calls only) log2-domain logits, token l of
 //                               request b at (b Hq + h) lcap + l, lcap = max_seq_len
 //                               rounded up to 16
+//   o      fp32  [n][Hq][ld]    (two-pass calls only) merged low-rank outputs
+// Two-pass calls pad acc and o rows to ld = v_rank rounded up to 4 (16-byte rows).
 // Slot word: everything a decode kernel needs of one of its slots, so that its prologue
 // reads a wave's slots with a few wide scalar loads: the code tile (first cache lane /
 // 16), the tile's outlier ranks (3.2-bit), the slot's partial-logit row, its local head
@@ -64,7 +66,8 @@ __device__ __forceinline__ int sw_head(uint32_t w) { return (int)((w >> 23) & 3)
 __device__ __forceinline__ int sw_tile(uint32_t w) { return (int)(w >> 25); }
 
 struct WsLayout {
-    size_t hdr, plan, ab, m, l, acc, lg, total;
+    size_t hdr, plan, ab, m, l, acc, lg, o, total;
+    int ld;  // floats per acc / o row
 };
 
 static inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -79,8 +82,10 @@ static WsLayout ws_layout(int n, int Hq, int TT, int v_rank, int grid, int lcap)
     w.ab = o; o = al256(o + ((size_t)n * TT + AB_SLACK_TILES) * AB_TILE_BYTES);
     w.m = o; o = al256(o + slots * Hq * 4);
     w.l = o; o = al256(o + slots * Hq * 4);
-    w.acc = o; o = al256(o + slots * Hq * (size_t)v_rank * 4);
+    w.ld = lcap > 0 ? (v_rank + 3) & ~3 : v_rank;
+    w.acc = o; o = al256(o + slots * Hq * (size_t)w.ld * 4);
     w.lg = o; o = al256(o + (size_t)n * Hq * (size_t)lcap * 4);
+    w.o = o; o = al256(o + (lcap > 0 ? (size_t)n * Hq * (size_t)w.ld * 4 : 0));
     w.total = o;
     return w;
 }
@@ -97,6 +102,7 @@ struct DecodeParams {
     uint8_t* ws;
     size_t ws_plan, ws_ab, ws_m, ws_l, ws_acc;
     size_t ws_lg; int lcap;                        // two-pass calls: logits buffer, row length
+    size_t ws_o; int acc_ld;                       // two-pass calls: merged outputs; acc / o row floats
 };
 
 __device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }

@@ -2,7 +2,7 @@
 // v_rank > 256, 3.2-bit codes with more than five 64-lane P @ V blocks), and the merge
 // of its partials. decode.hip runs, per call: prep, the logits pass (the one-pass
 // kernels with NB = 0: K side and softmax statistics only, every valid logit stored in
-// the workspace), then `pv_kernel` here, then `merge_wide_kernel` here.
+// the workspace), then `pv_kernel`, `merge_cols_kernel` and `lift_kernel` here.
 //
 // The reference splits its V pass the same way: logits first, then P @ V over
 // column blocks of at most 512 (paged_decode.py:105-147, 199-219) or 128 channels
@@ -17,19 +17,25 @@
 //   - the 16 logits of every head (2 KB) and the slot's reference max per head.
 // Since the reference max of a slot is final, P = exp2(logit - m) needs no rescaling.
 // P @ V runs on v_mfma_f32_32x32x16 (M = 32 heads, N = 32 columns, K = the page's 16
-// tokens): A = P (bf16 codes: P = hi + lo, two bf16 parts; fp16: P; 3.2-bit: P * s_out
-// for outlier blocks and P * s_in for inlier blocks, s the token's V scales, folded as
-// paged_quant.py:343-346 does), B = 16 tokens x 32 columns of V read with
-// ds_read_b64_tr_b16: a 16-lane group hands in 4 tokens x 16 columns and lane i gets
-// column i of the 4 tokens. 3.2-bit V nibbles are first expanded once per page, by
-// the whole workgroup, into an fp16 table of (n - 8) in that layout. Wave w owns the
-// 32-column blocks w, w + 8, ...; at the end of a request's tokens in the range it
-// stores its block of the slot's partial accumulator [Hq][v_rank] (fp32).
+// tokens) with A = P:
+//   - bf16 codes: P = hi + lo (two bf16 parts, two MFMAs); B = 16 tokens x 32 columns
+//     read with ds_read_b64_tr_b16 (a 16-lane group hands in 4 tokens x 16 columns and
+//     lane i gets column i of the 4 tokens); fp16 codes: P in fp16, the same B.
+//   - 3.2-bit codes: P in fp16. ds_read_b64_tr_b8 gives lane i byte-column i of 8
+//     tokens, i.e. the nibbles of two V columns; the lane turns the low nibbles into
+//     one fp16 B operand and the high nibbles into another (n - 8, exact), each scaled
+//     by the token's V scale of its column's kind (outlier or inlier: every byte holds
+//     one kind). So one 32-byte chunk of the row feeds two MFMAs, one for the even and
+//     one for the odd columns of its 64. The reference folds the scale into P instead
+//     (paged_quant.py:343-346); either way one product is rounded to 16 bits.
+// Wave w owns the blocks (chunks) w, w + 8, ...; at the end of a request's tokens in the
+// range it stores its columns of the slot's partial accumulator [Hq][ld] (fp32).
 //
-// LDS. Every 16-byte granule column G (8 code columns) holds the 16 tokens of a page,
-// token t in slot t ^ (4 (G & 1)), 256 bytes per granule column, so a page's V (or the
-// expanded table) is one 1 KB chunk per 32 columns, and a transposed read of 4 tokens
-// x 16 columns by 16 lanes touches 128 distinct bytes per bank group.
+// LDS. Every 16-byte granule column G (8 code columns, or 16 bytes of a 3.2-bit row)
+// holds the 16 tokens of a page, token t in slot t ^ (4 (G & 1)), 256 bytes per granule
+// column, so 32 bf16 columns (two granule columns each way) are one 1 KB chunk and a
+// transposed read of 4 tokens x 16 columns by 16 lanes touches 128 distinct bytes per
+// bank group.
 #include <algorithm>
 
 #include "decode_pages.hpp"
@@ -78,15 +84,15 @@ struct PvParams {
     int ng;          // 16-byte granules copied per row
     int vs_rel;      // 3.2-bit: V scales at this byte of the copied bytes
     int vq_rel;      // 3.2-bit: first V nibble byte (outlier nibbles), relative
-    int v_nout, v_nbo, o32;  // 3.2-bit: outlier columns, their bytes, outlier table columns (v_nout up to 32)
-    int c0, ncb;     // window: first (table) column, 32-column blocks
-    int nch;         // 1 KB chunks copied per page: V, then logits (2), then the slot's maxima (1)
+    int v_nout, v_nbo;  // 3.2-bit: outlier columns, their nibble bytes
+    int c0, ncb;     // window: bf16/fp16, first column and 32-column blocks; 3.2-bit, first
+                     // 32-byte chunk of the copied bytes and chunks
+    int nch;         // 1 KB chunks copied per page: logits (2), the slot's maxima (1), then V
     int nld;         // copies per wave per page
-    int nbuf;        // page buffers in flight (2 or 3)
+    int nbuf;        // page buffers (2 .. 8): nbuf - 1 pages in flight
     int buf_bytes;   // LDS bytes per page buffer (nch KB)
-    int tab;         // 3.2-bit: LDS byte of the expanded table
     int lds_bytes;
-    uint8_t* ws; size_t ws_plan, ws_m, ws_acc, ws_lg; int lcap;
+    uint8_t* ws; size_t ws_plan, ws_m, ws_acc, ws_lg; int lcap, acc_ld;
 };
 
 typedef const __attribute__((address_space(4))) PvParams kpv_t;
@@ -117,6 +123,10 @@ __device__ __forceinline__ PvPage pv_page_desc(const PvParams& p, const Cursor& 
     return d;
 }
 
+// LDS chunks of a page buffer: 0 and 1 the logits of heads 0-15 and 16-31, 2 the slot's
+// maxima, then the V granule columns.
+constexpr int PV_V0 = 3;
+
 // The copies of this wave for one page into the buffer at LDS byte `buf`: copy i moves
 // chunk 8 i + wave; chunks past nch go to the dummy block and read nothing.
 template <int NLD>
@@ -124,45 +134,29 @@ __device__ __forceinline__ void pv_copies(const PvParams& p, const PvPage& d, ui
                                           const uint32_t (&off)[NLD]) {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-        const int ch = i * NWAVE + wave;
         if (i >= p.nld) break;
+        const int ch = i * NWAVE + wave;
         const uint32_t m0 = ch < p.nch ? buf + (uint32_t)ch * 1024u : dummy;
-        if (ch < p.nch - 3)
-            lds_copy16(d.rv, m0, off[i]);
-        else if (ch < p.nch - 1)
-            lds_copy16(d.rl, m0, off[i]);
+        if (i == 0 && wave < PV_V0)
+            lds_copy16(wave < 2 ? d.rl : d.rm, m0, off[i]);
         else
-            lds_copy16(d.rm, m0, off[i]);
+            lds_copy16(d.rv, m0, off[i]);
     }
 }
 
-// Expands the 3.2-bit V nibbles of the page in buffer `buf` into the fp16 table of
-// (n - 8): table column tc < o32 is outlier column tc (nibbles from vq_rel), else
-// inlier column tc - o32 (nibbles from vq_rel + v_nbo); columns past the real ones
-// hold whatever bytes follow and are never stored.
-__device__ __forceinline__ void pv_expand(const PvParams& p, uint32_t buf, uint32_t tab, int tid) {
-    const int items = p.ncb * 4 * TILE_TOK;  // (table granule column, token)
-    const int lim = p.ng * 16 - 4;
-    for (int it = tid; it < items; it += NTHR) {
-        const int TG = it >> 4, t = it & 15;
-        const int tc = p.c0 + 8 * TG;
-        const int b = tc < p.o32 ? p.vq_rel + (tc >> 1) : p.vq_rel + p.v_nbo + ((tc - p.o32) >> 1);
-        // The 4 nibble bytes at b (any alignment): two aligned words, then a funnel shift.
-        const int b0 = min(b & ~3, lim), b1 = min((b & ~3) + 4, lim);
-        const uint32_t a0 = buf + (uint32_t)((((b0 >> 4) << 4) + gslot(b0 >> 4, t)) * 16 + (b0 & 15));
-        const uint32_t a1 = buf + (uint32_t)((((b1 >> 4) << 4) + gslot(b1 >> 4, t)) * 16 + (b1 & 15));
-        const uint32_t w0 = lds_ld<uint32_t>(a0), w1 = lds_ld<uint32_t>(a1);
-        const uint32_t w = __builtin_amdgcn_alignbyte(w1, w0, (uint32_t)(b & 3));
-        uint32_t r[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t byte = (w >> (8 * j)) & 0xFFu;
-            const uint32_t x = (byte & 0xFu) | ((byte << 12) & 0xF0000u) | 0x64006400u;  // fp16 (1024 + lo, 1024 + hi)
-            r[j] = h2_bits(as_h2(x) - (half2_t){(_Float16)1032.f, (_Float16)1032.f});
-        }
-        typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-        lds_st<u32x4_t>(tab + (uint32_t)((TG * 16 + gslot(TG, t)) * 16), (u32x4_t){r[0], r[1], r[2], r[3]});
-    }
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i_t* lds_v2p;
+
+// Byte-column (lane & 15) of 8 tokens x 16 bytes: byte e of the result is token e.
+__device__ __forceinline__ uint2 tr_read8(uint32_t addr) {
+    const v2i_t r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2p)(uintptr_t)addr);
+    return make_uint2((uint32_t)r[0], (uint32_t)r[1]);
+}
+
+// fp16 (n - 8) of two nibbles: bytes x and y of w (each 0 .. 15) with fp16 1024 (0x64)
+// as their high bytes, minus 1032 (all exact).
+__device__ __forceinline__ half2_t nib2(uint32_t w, uint32_t sel) {
+    return as_h2(__builtin_amdgcn_perm(0x64646464u, w, sel)) - (half2_t){(_Float16)1032.f, (_Float16)1032.f};
 }
 
 template <int FMT, int MB, int NLD>
@@ -189,34 +183,40 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
     for (int i = 0; i < NLD; ++i) {
         const int ch = i * NWAVE + wave;
         uint32_t o = 0x80000000u;  // past every descriptor: no access
-        const int nv = p.nch - 3;
-        if (ch < nv) {
-            const int G = 4 * ch + (lane >> 4), t = gslot(G, lane & 15);
-            if (G < p.ng) o = (uint32_t)(t * p.c_s1 + p.v_off + 16 * G);
-        } else if (ch < nv + 2) {
-            const int h = 16 * (ch - nv) + (lane >> 2);
+        if (ch < 2) {
+            const int h = 16 * ch + (lane >> 2);
             if (h < p.Hq) o = (uint32_t)((h * p.lcap) * 4 + 16 * (lane & 3));
-        } else if (ch == nv + 2) {
+        } else if (ch == 2) {
             if (4 * lane < p.Hq) o = (uint32_t)(16 * lane);
+        } else if (ch < p.nch) {
+            const int G = 4 * (ch - PV_V0) + (lane >> 4), t = gslot(G, lane & 15);
+            if (G < p.ng) o = (uint32_t)(t * p.c_s1 + p.v_off + 16 * G);
         }
         off[i] = o;
     }
 
-    // Lane roles. A operand: head am = lane & 31, tokens 8 ag .. 8 ag + 7 (ag = lane >> 5).
-    // B operand (transposed reads): 16-lane group q = lane >> 4 reads tokens 8 (q >> 1) +
-    // i / 4 (+ 4), columns 16 (q & 1) + 4 (i % 4) of the block, i = lane & 15.
+    // A operand: head am = lane & 31, tokens 8 ag .. 8 ag + 7 (ag = lane >> 5).
     const int am = lane & 31, ag = lane >> 5;
-    uint32_t trd0, trd1;  // byte offsets of this lane's two transposed reads inside block 0
+    // B operand reads of block (or chunk) 0, relative to the page buffer.
+    uint32_t trd0, trd1;
     {
         const int q = lane >> 4, i = lane & 15;
-        const int t = 8 * (q >> 1) + (i >> 2);
-        const int col = 16 * (q & 1) + 4 * (i & 3);
-        const int G = col >> 3, h = (col >> 2) & 1;
-        trd0 = (uint32_t)((G * 16 + gslot(G, t)) * 16 + 8 * h);
-        trd1 = (uint32_t)((G * 16 + gslot(G, t + 4)) * 16 + 8 * h);
+        if (FMT == FMT_Q4) {
+            // 16-lane group q: granule 2 c + (q & 1), tokens 8 (q >> 1) + i / 2, bytes 8 (i & 1).
+            const int G = q & 1, t = 8 * (q >> 1) + (i >> 1);
+            trd0 = (uint32_t)((G * 16 + gslot(G, t)) * 16 + 8 * (i & 1));
+            trd1 = 0;
+        } else {
+            // tokens 8 (q >> 1) + i / 4 (+ 4), columns 16 (q & 1) + 4 (i % 4).
+            const int t = 8 * (q >> 1) + (i >> 2);
+            const int col = 16 * (q & 1) + 4 * (i & 3);
+            const int G = col >> 3, h = (col >> 2) & 1;
+            trd0 = (uint32_t)((G * 16 + gslot(G, t)) * 16 + 8 * h);
+            trd1 = (uint32_t)((G * 16 + gslot(G, t + 4)) * 16 + 8 * h);
+        }
     }
-    const uint32_t lga = (uint32_t)((p.nch - 3) * 1024 + (am * 16 + 8 * ag) * 4);  // logits of (am, 8 ag ..)
-    const uint32_t mxa = (uint32_t)((p.nch - 1) * 1024 + am * 4);                   // the slot max of head am
+    const uint32_t lga = (uint32_t)((am * 16 + 8 * ag) * 4);  // logits of (am, 8 ag ..)
+    const uint32_t mxa = (uint32_t)(2 * 1024 + am * 4);         // the slot max of head am
     __syncthreads();
 
     f32x16_t acc[MB];
@@ -234,27 +234,22 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
         pv_copies<NLD>(p, pv_page_desc(p, ld, blk_of(ld), g), base + (uint32_t)(j * p.buf_bytes), dummy, wave, off);
         if (ld.valid) cur_next(ld, P, p.n, beg, end);
     }
+    // The cache block of the next page to copy, read one iteration ahead so that its
+    // load completes under the page barrier's wait.
+    int nblk = blk_of(ld);
     int jb = 0;  // buffer of the current page
     while (cc.valid) {
         // Page cc is in buffer jb; the copies of the nbuf - 2 pages after it may still run.
-        if (p.nbuf == 3)
-            wait_vmcnt_lgkm0(p.nld);
-        else
-            wait_vmcnt_lgkm0(0);
-        wait_lgkm0_barrier();  // every wave is done with the previous page's buffer and the table
+        wait_vmcnt_lgkm0_wide((p.nbuf - 2) * p.nld);
+        wait_lgkm0_barrier();  // every wave is done with the previous page's buffer
         {
             const int jn = jb == 0 ? p.nbuf - 1 : jb - 1;  // the buffer the previous page used
-            pv_copies<NLD>(p, pv_page_desc(p, ld, blk_of(ld), g), base + (uint32_t)(jn * p.buf_bytes), dummy, wave,
-                           off);
+            pv_copies<NLD>(p, pv_page_desc(p, ld, nblk, g), base + (uint32_t)(jn * p.buf_bytes), dummy, wave, off);
             if (ld.valid) cur_next(ld, P, p.n, beg, end);
+            nblk = blk_of(ld);
         }
         const uint32_t buf = base + (uint32_t)(jb * p.buf_bytes);
-        uint32_t src = buf;  // where the B operands are read: the page (bf16/fp16) or the table (3.2-bit)
-        if (FMT == FMT_Q4) {
-            src = base + (uint32_t)p.tab;
-            pv_expand(p, buf, src, tid);
-            wait_lgkm0_barrier();
-        }
+        const uint32_t vbuf = buf + PV_V0 * 1024;  // the page's V granule columns
         // A operand: P of head am at tokens 8 ag .. 8 ag + 7 of this page.
         const f32x4_t s0 = lds_ld<f32x4_t>(buf + lga), s1 = lds_ld<f32x4_t>(buf + lga + 16);
         const float mx = lds_ld<float>(buf + mxa);
@@ -266,43 +261,69 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
             const bool ok = am < p.Hq && tok0 + e >= cc.lo && tok0 + e < cc.hi;
             pe[e] = ok ? __builtin_amdgcn_exp2f(sv[e] - mx) : 0.f;
         }
-        bf16x8_t ahi, alo;
-        half8_t aho, ahi16;
-        if (FMT == FMT_BF16) {
+        if constexpr (FMT == FMT_BF16) {
             float lo[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) lo[e] = pe[e] - (float)(__bf16)pe[e];
-            ahi = to_bf16x8(pe);
-            alo = to_bf16x8(lo);
-        } else if (FMT == FMT_F16) {
-            aho = to_f16x8(pe);
-        } else {
-            float po[8], pi[8];
+            const bf16x8_t ahi = to_bf16x8(pe), alo = to_bf16x8(lo);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {  // the token's (outlier, inlier) V scales, bf16
-                const int t = 8 * ag + e;
-                const uint32_t sw = lds_ld<uint32_t>(buf + (uint32_t)(gslot(0, t) * 16 + p.vs_rel));
-                po[e] = pe[e] * __uint_as_float(sw << 16);
-                pi[e] = pe[e] * __uint_as_float(sw & 0xffff0000u);
-            }
-            aho = to_f16x8(po);
-            ahi16 = to_f16x8(pi);
-        }
-#pragma unroll
-        for (int i = 0; i < MB; ++i) {
-            const int cb = wave + NWAVE * i;
-            if (cb < p.ncb) {
-                const uint32_t a = src + (uint32_t)cb * 1024u;
-                const uint2 b0 = tr_read(a + trd0), b1 = tr_read(a + trd1);
-                const uint4 bw = make_uint4(b0.x, b0.y, b1.x, b1.y);
-                if (FMT == FMT_BF16) {
-                    const bf16x8_t bv = __builtin_bit_cast(bf16x8_t, bw);
+            for (int i = 0; i < MB; ++i) {
+                const int cb = wave + NWAVE * i;
+                if (cb < p.ncb) {
+                    const uint32_t a = vbuf + (uint32_t)cb * 1024u;
+                    const uint2 b0 = tr_read(a + trd0), b1 = tr_read(a + trd1);
+                    const bf16x8_t bv = __builtin_bit_cast(bf16x8_t, make_uint4(b0.x, b0.y, b1.x, b1.y));
                     acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi, bv, acc[i], 0, 0, 0);
                     acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(alo, bv, acc[i], 0, 0, 0);
-                } else {
-                    const half8_t bv = __builtin_bit_cast(half8_t, bw);
-                    const half8_t av = (FMT == FMT_Q4 && p.c0 + 32 * cb >= p.o32) ? ahi16 : aho;
+                }
+            }
+        } else if constexpr (FMT == FMT_F16) {
+            const half8_t av = to_f16x8(pe);
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                const int cb = wave + NWAVE * i;
+                if (cb < p.ncb) {
+                    const uint32_t a = vbuf + (uint32_t)cb * 1024u;
+                    const uint2 b0 = tr_read(a + trd0), b1 = tr_read(a + trd1);
+                    const half8_t bv = __builtin_bit_cast(half8_t, make_uint4(b0.x, b0.y, b1.x, b1.y));
                     acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[i], 0, 0, 0);
+                }
+            }
+        } else {
+            const half8_t av = to_f16x8(pe);
+            // This lane's 8 tokens' V scales as fp16 pairs (tokens 2j, 2j + 1), per kind.
+            uint32_t so[4], si[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int t = 8 * ag + 2 * j;
+                const uint32_t w0 = lds_ld<uint32_t>(vbuf + (uint32_t)(gslot(0, t) * 16 + p.vs_rel));
+                const uint32_t w1 = lds_ld<uint32_t>(vbuf + (uint32_t)(gslot(0, t + 1) * 16 + p.vs_rel));
+                so[j] = h2_bits(cvt_h2(__uint_as_float(w0 << 16), __uint_as_float(w1 << 16)));
+                si[j] = h2_bits(cvt_h2(__uint_as_float(w0 & 0xffff0000u), __uint_as_float(w1 & 0xffff0000u)));
+            }
+#pragma unroll
+            for (int i = 0; i < MB / 2; ++i) {
+                const int ch = wave + NWAVE * i;  // 32-byte chunk of the copied V bytes
+                if (ch < p.ncb) {
+                    const int c = p.c0 + ch;
+                    const uint2 w = tr_read8(vbuf + (uint32_t)c * 512u + trd0);
+                    // This lane's byte: outlier columns before v_nbo bytes of nibbles, inlier after.
+                    const bool inl = 32 * c + (lane & 31) - p.vq_rel >= p.v_nbo;
+                    const uint32_t l0 = w.x & 0x0F0F0F0Fu, l1 = w.y & 0x0F0F0F0Fu;
+                    const uint32_t h0 = (w.x >> 4) & 0x0F0F0F0Fu, h1 = (w.y >> 4) & 0x0F0F0F0Fu;
+                    half2_t sc[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) sc[j] = as_h2(inl ? si[j] : so[j]);
+                    const half2_t e0 = nib2(l0, 0x04010400u) * sc[0], e1 = nib2(l0, 0x04030402u) * sc[1];
+                    const half2_t e2 = nib2(l1, 0x04010400u) * sc[2], e3 = nib2(l1, 0x04030402u) * sc[3];
+                    const half2_t o0 = nib2(h0, 0x04010400u) * sc[0], o1 = nib2(h0, 0x04030402u) * sc[1];
+                    const half2_t o2 = nib2(h1, 0x04010400u) * sc[2], o3 = nib2(h1, 0x04030402u) * sc[3];
+                    const half8_t be = __builtin_bit_cast(
+                        half8_t, make_uint4(h2_bits(e0), h2_bits(e1), h2_bits(e2), h2_bits(e3)));
+                    const half8_t bo = __builtin_bit_cast(
+                        half8_t, make_uint4(h2_bits(o0), h2_bits(o1), h2_bits(o2), h2_bits(o3)));
+                    acc[2 * i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, be, acc[2 * i], 0, 0, 0);
+                    acc[2 * i + 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bo, acc[2 * i + 1], 0, 0, 0);
                 }
             }
         }
@@ -312,18 +333,30 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
             // This lane's column of each of its blocks, for the 16 heads
             // 8 (j / 4) + 4 (lane >> 5) + j % 4 of the 32x32 result.
             const int64_t slot = (int64_t)cc.b + g;
-            float* wa = (float*)(p.ws + p.ws_acc) + slot * p.Hq * p.v_rank;
+            float* wa = (float*)(p.ws + p.ws_acc) + slot * p.Hq * p.acc_ld;
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
-                const int cb = wave + NWAVE * i;
-                const int tc = p.c0 + 32 * cb + (lane & 31);
-                int col = tc;
-                if (FMT == FMT_Q4) col = tc < p.o32 ? (tc < p.v_nout ? tc : -1) : p.v_nout + tc - p.o32;
-                const bool okc = cb < p.ncb && col >= 0 && col < p.v_rank;
+                int col = -1;
+                if (FMT == FMT_Q4) {
+                    const int ch = wave + NWAVE * (i >> 1);
+                    const int rel = 32 * (p.c0 + ch) + (lane & 31) - p.vq_rel;  // nibble byte of this lane
+                    if (ch < p.ncb && rel >= 0) {
+                        if (rel < p.v_nbo) {
+                            col = 2 * rel + (i & 1);
+                            if (col >= p.v_nout) col = -1;
+                        } else {
+                            col = p.v_nout + 2 * (rel - p.v_nbo) + (i & 1);
+                        }
+                    }
+                } else {
+                    const int cb = wave + NWAVE * i;
+                    if (cb < p.ncb) col = p.c0 + 32 * cb + (lane & 31);
+                }
+                const bool okc = col >= 0 && col < p.v_rank;
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
                     const int h = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-                    if (okc && h < p.Hq) wa[(int64_t)h * p.v_rank + col] = acc[i][j];
+                    if (okc && h < p.Hq) wa[(int64_t)h * p.acc_ld + col] = acc[i][j];
                     acc[i][j] = 0.f;
                 }
             }
@@ -335,110 +368,139 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
 }
 
 // ---------------------------------------------------------------------------
-// Merge of the two-pass partials: per (request, head) the log-sum-exp of the slots'
-// (m, l), the weighted sum of their accumulators, then the lift through v_up_by_q[h].
-// A workgroup takes one head and MW_REQ requests: phase 1 merges request r into LDS
-// (wave w takes requests w and w + 4), phase 2 lifts all of them, each thread 8 output
-// columns over one sixteenth of the rank columns, and reduces over the sixteenths.
+// Merge of the two-pass partials, in two launches.
+// merge_cols_kernel: one workgroup per (request, head): the log-sum-exp weights of the
+//   request's slots, then every column's weighted sum of their accumulators, divided by
+//   the total, into o [n][Hq][ld] (NaN for a request with no tokens, as the reference's
+//   softmax over an empty row).
+// lift_kernel: one workgroup per (head, LIFT_REQ requests): out = o @ v_up_by_q[h], each
+//   thread 8 output columns over one sixteenth of the rank columns, then a reduction
+//   over the sixteenths.
 // ---------------------------------------------------------------------------
-constexpr int MW_REQ = 8;
-constexpr int MW_THR = 256;
+constexpr int MC_THR = 256;
+constexpr int LIFT_REQ = 8;
+constexpr int LIFT_THR = 512;
+constexpr int LIFT_WAVES = LIFT_THR / 64;
+constexpr int LIFT_U = 4;  // v_up_by_q rows per thread in flight
 
-static size_t merge_wide_lds(int v_rank) { return (size_t)MW_REQ * v_rank * 4 + (size_t)4 * MW_REQ * 128 * 4; }
-
-template <int DT>
-__global__ __launch_bounds__(MW_THR) void merge_wide_kernel(const uint8_t* __restrict__ ws, size_t ws_plan,
-                                                            size_t ws_m, size_t ws_l, size_t ws_acc, int n, int Hq,
-                                                            int v_rank, const void* __restrict__ vup, int64_t vu_s0,
-                                                            int64_t vu_s1, void* __restrict__ out, int64_t o_s0,
-                                                            int64_t o_s1, int out_dt) {
-    extern __shared__ __align__(16) uint8_t s_dyn[];
-    float* s_o = (float*)s_dyn;                                    // [MW_REQ][v_rank]
-    float* s_red = (float*)(s_dyn + (size_t)MW_REQ * v_rank * 4);  // [4 waves][MW_REQ][128]
-    __shared__ int s_live[MW_REQ];
-    const int h = blockIdx.x, b0 = blockIdx.y * MW_REQ;  // head in x: a head's workgroups share one XCD's L2
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+__global__ __launch_bounds__(MC_THR) void merge_cols_kernel(const uint8_t* __restrict__ ws, size_t ws_plan, size_t ws_m,
+                                                            size_t ws_l, size_t ws_acc, size_t ws_o, int n, int Hq,
+                                                            int v_rank, int ld) {
+    const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int* hdr = (const int*)ws;
     const float* wm = (const float*)(ws + ws_m);
     const float* wl = (const float*)(ws + ws_l);
     const float* wa = (const float*)(ws + ws_acc);
     const int S = hdr[0];
     const bool planned = ((const int*)(ws + ws_plan))[NWAVE * PLAN_STRIDE] != 0;
-
-    for (int rr = 0; rr < MW_REQ / 4; ++rr) {
-        const int r = w + 4 * rr, b = b0 + r;
-        const int pb = b < n ? hdr[1 + b] : 0, pe = b < n ? hdr[2 + b] : 0;
-        const bool live = b < n && pe > pb && S > 0 && planned;
-        const int k_lo = live ? pb / S : 0, nk = live ? (pe - 1) / S - k_lo + 1 : 0;
-        const int64_t s0 = (int64_t)(k_lo + b) * Hq + h;  // slot row of partial k: s0 + k Hq
-        float M = -INFINITY;
-        for (int k = lane; k < nk; k += 64) M = fmaxf(M, wm[s0 + (int64_t)k * Hq]);
-        M = wave_max(M);
-        const float wk = lane < nk ? exp2f(wm[s0 + (int64_t)lane * Hq] - M) : 0.f;
-        float l = lane < nk ? wl[s0 + (int64_t)lane * Hq] * wk : 0.f;
-        for (int k = lane + 64; k < nk; k += 64) {
+    const int pb = hdr[1 + b], pe = hdr[2 + b];
+    const bool live = pe > pb && S > 0 && planned;
+    const int k_lo = live ? pb / S : 0, nk = live ? (pe - 1) / S - k_lo + 1 : 0;
+    const int64_t s0 = (int64_t)(k_lo + b) * Hq + h;  // slot row of partial k: s0 + k Hq
+    // Every wave forms the same weights (the loads hit the same lines).
+    float M = -INFINITY;
+    for (int k = lane; k < nk; k += 64) M = fmaxf(M, wm[s0 + (int64_t)k * Hq]);
+    M = wave_max(M);
+    const float wk = lane < nk ? exp2f(wm[s0 + (int64_t)lane * Hq] - M) : 0.f;
+    float l = lane < nk ? wl[s0 + (int64_t)lane * Hq] * wk : 0.f;
+    for (int k = lane + 64; k < nk; k += 64) {
+        const int64_t sl = s0 + (int64_t)k * Hq;
+        l += wl[sl] * exp2f(wm[sl] - M);
+    }
+    l = wave_sum(l);
+    const float inv = live ? 1.f / l : __builtin_nanf("");
+    float* o = (float*)(ws + ws_o) + ((int64_t)b * Hq + h) * ld;
+    for (int c4 = 4 * tid; c4 < v_rank; c4 += 4 * MC_THR) {
+        f32x4_t a = {0.f, 0.f, 0.f, 0.f};
+        int k = 0;
+        for (; k + 4 <= nk; k += 4) {  // four partials' loads in flight
+            f32x4_t r[4];
+            float wt[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t sl = s0 + (int64_t)(k + u) * Hq;
+                r[u] = *(const f32x4_t*)(wa + sl * ld + c4);
+                wt[u] = k + u < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k + u))
+                                   : exp2f(wm[sl] - M);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) a += r[u] * wt[u];
+        }
+        for (; k < nk; ++k) {
             const int64_t sl = s0 + (int64_t)k * Hq;
-            l += wl[sl] * exp2f(wm[sl] - M);
+            const float wt = k < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k)) : exp2f(wm[sl] - M);
+            a += *(const f32x4_t*)(wa + sl * ld + c4) * wt;
         }
-        l = wave_sum(l);
-        const float inv = live ? 1.f / l : __builtin_nanf("");
-        for (int c0 = 0; c0 < v_rank; c0 += 256) {
-            float a[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int k = 0; k < nk; ++k) {
-                const int64_t sl = s0 + (int64_t)k * Hq;
-                const float wt = k < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k))
-                                        : exp2f(wm[sl] - M);
-                const float* row = wa + sl * v_rank;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int c = c0 + lane + 64 * j;
-                    if (c < v_rank) a[j] = fmaf(row[c], wt, a[j]);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int c = c0 + lane + 64 * j;
-                if (c < v_rank) s_o[r * v_rank + c] = a[j] * inv;
-            }
-        }
-        if (lane == 0) s_live[r] = live;
+        *(f32x4_t*)(o + c4) = a * inv;
     }
-    __syncthreads();
+}
 
-    // The lift: thread (dq, cp) takes output columns 8 dq .. 8 dq + 7 over rank columns
-    // c = cp (mod 16), for every request of the workgroup.
+template <int DT>
+__global__ __launch_bounds__(LIFT_THR) void lift_kernel(const uint8_t* __restrict__ ws, size_t ws_o, int n, int Hq,
+                                                        int v_rank, int ld, const void* __restrict__ vup,
+                                                        int64_t vu_s0, int64_t vu_s1, void* __restrict__ out,
+                                                        int64_t o_s0, int64_t o_s1, int out_dt) {
+    extern __shared__ __align__(16) uint8_t s_dyn[];
+    float* s_o = (float*)s_dyn;    // [LIFT_REQ][ld]
+    float* s_red = (float*)s_dyn;  // [LIFT_WAVES][LIFT_REQ][128], over s_o once the products are done
+    const int h = blockIdx.x, b0 = blockIdx.y * LIFT_REQ;  // head in x: a head's workgroups share one XCD's L2
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const float* og = (const float*)(ws + ws_o);
+    for (int i = 4 * tid; i < LIFT_REQ * ld; i += 4 * LIFT_THR) {
+        const int r = i / ld, c = i - r * ld;
+        f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+        if (b0 + r < n) v = *(const f32x4_t*)(og + ((int64_t)(b0 + r) * Hq + h) * ld + c);
+        *(f32x4_t*)(s_o + i) = v;
+    }
+    __syncthreads();
+    // Thread (dq, cp): output columns 8 dq .. 8 dq + 7 over rank columns c = cp (mod CP);
+    // LIFT_U rows of v_up_by_q are loaded before their products, so their latencies overlap.
+    constexpr int CP = LIFT_THR / 16;
     const int dq = tid & 15, cp = tid >> 4;
-    float o[MW_REQ][8];
+    float acc[LIFT_REQ][8];
 #pragma unroll
-    for (int r = 0; r < MW_REQ; ++r)
+    for (int r = 0; r < LIFT_REQ; ++r)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[r][e] = 0.f;
+        for (int e = 0; e < 8; ++e) acc[r][e] = 0.f;
     const int64_t vh = (int64_t)h * vu_s0 + 8 * dq;
-    for (int c = cp; c < v_rank; c += 16) {
-        float u[8];
-        load8_f(vup, vh + (int64_t)c * vu_s1, DT, u);
+    for (int c0 = cp; c0 < v_rank; c0 += CP * LIFT_U) {
+        float u[LIFT_U][8];
 #pragma unroll
-        for (int r = 0; r < MW_REQ; ++r) {
-            const float x = s_o[r * v_rank + c];
+        for (int j = 0; j < LIFT_U; ++j) {
+            const int c = min(c0 + CP * j, v_rank - 1);  // past the end: a valid row, weighted 0 below
+            load8_f(vup, vh + (int64_t)c * vu_s1, DT, u[j]);
+        }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[r][e] = fmaf(x, u[e], o[r][e]);
+        for (int j = 0; j < LIFT_U; ++j) {
+            const int c = c0 + CP * j;
+#pragma unroll
+            for (int r = 0; r < LIFT_REQ; ++r) {
+                const float x = c < v_rank ? s_o[r * ld + c] : 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[r][e] = fmaf(x, u[j][e], acc[r][e]);
+            }
         }
     }
-    // Sum over the wave's four sixteenths (lanes l, l ^ 16, l ^ 32, l ^ 48), then over the waves.
+    // Sum over the wave's four phases (lanes l, l ^ 16, l ^ 32, l ^ 48), then over the waves.
 #pragma unroll
-    for (int r = 0; r < MW_REQ; ++r)
+    for (int r = 0; r < LIFT_REQ; ++r)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float v = sum_rows(o[r][e]);
-            if (lane < 16) s_red[(w * MW_REQ + r) * 128 + 8 * dq + e] = v;
-        }
+        for (int e = 0; e < 8; ++e) acc[r][e] = sum_rows(acc[r][e]);
+    __syncthreads();  // every wave is done with s_o
+    if (lane < 16) {
+#pragma unroll
+        for (int r = 0; r < LIFT_REQ; ++r)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s_red[(w * LIFT_REQ + r) * 128 + 8 * dq + e] = acc[r][e];
+    }
     __syncthreads();
-    for (int i = tid; i < MW_REQ * 128; i += MW_THR) {
+    for (int i = tid; i < LIFT_REQ * 128; i += LIFT_THR) {
         const int r = i >> 7, d = i & 127, b = b0 + r;
         if (b >= n) continue;
-        float v = s_red[(0 * MW_REQ + r) * 128 + d] + s_red[(1 * MW_REQ + r) * 128 + d];
-        v += s_red[(2 * MW_REQ + r) * 128 + d] + s_red[(3 * MW_REQ + r) * 128 + d];
-        store_f(out, (int64_t)b * o_s0 + (int64_t)h * o_s1 + d, out_dt, s_live[r] ? v : __builtin_nanf(""));
+        float v = 0.f;
+#pragma unroll
+        for (int k = 0; k < LIFT_WAVES; ++k) v += s_red[(k * LIFT_REQ + r) * 128 + d];
+        store_f(out, (int64_t)b * o_s0 + (int64_t)h * o_s1 + d, out_dt, v);
     }
 }
 
@@ -448,6 +510,7 @@ __global__ __launch_bounds__(MW_THR) void merge_wide_kernel(const uint8_t* __res
 namespace {
 
 constexpr int PV_NLD = 12;  // copies per wave per page, at most (the plan keeps nch <= 96)
+constexpr int PV_INFLIGHT = 96 * 1024;  // page bytes in flight per workgroup the plan aims for
 
 template <int FMT>
 const void* pv_pick(int mb) {
@@ -467,59 +530,65 @@ int raise_lds(const void* fn, int bytes) {
     return STARKV_OK;
 }
 
+size_t lift_lds(int ld) { return std::max((size_t)LIFT_REQ * ld * 4, (size_t)LIFT_WAVES * LIFT_REQ * 128 * 4); }
+
 }  // namespace
 
-// The window plan of the P @ V pass: columns per launch (a multiple of 32) and the LDS
-// geometry. Table columns: bf16/fp16, the V columns; 3.2-bit, the outlier columns up to
-// a multiple of 32, then the inlier columns.
+// The plan of the P @ V pass: units (32-column blocks of bf16/fp16 codes, 32-byte chunks
+// of the copied 3.2-bit V bytes) per launch, at most 8 per wave's accumulators (64
+// MFMA blocks), and the LDS geometry.
 struct PvPlan {
-    int tcols;     // table columns in all
-    int cw;        // window width (columns per launch)
+    int units;      // in all
+    int per;        // per launch
     int nbuf, nch, nld, lds;
-    int ng, v_off; // per-launch copy geometry (bf16/fp16: per window; 3.2-bit: all V bytes)
+    int ng, v_off;  // copy geometry: granules per row (bf16/fp16: of one window) and the first byte
     bool ok;
 };
 
-static PvPlan pv_plan(int fmt, int k_width, int v_rank, int vs_off, int vq_off, int v_nout, int v_bytes) {
+static PvPlan pv_plan(int fmt, int k_width, int v_rank, int vs_off, int vq_off, int v_bytes) {
     PvPlan pl{};
-    const int o32 = (v_nout + 31) & ~31;
-    pl.tcols = fmt == FMT_Q4 ? o32 + (v_rank - v_nout) : v_rank;
-    const int ncb_all = (pl.tcols + 31) / 32;
-    // Candidate windows from wide to narrow; the first whose pages fit.
-    for (int cbw = std::min(ncb_all, 64); cbw >= 1; --cbw) {
-        const int cw = 32 * cbw;
-        int ng, v_off, tab = 0;
-        if (fmt == FMT_Q4) {
-            v_off = vs_off & ~15;
-            ng = (vq_off + v_bytes + 15) / 16 - v_off / 16;
-            tab = cbw * 1024;
-        } else {
-            v_off = 2 * k_width;
-            ng = cw / 8;
-        }
-        const int nch = (ng + 3) / 4 + 3;
-        for (int nbuf = 3; nbuf >= 2; --nbuf) {
-            const int lds = nbuf * nch * 1024 + tab + 1024;
-            if (lds <= PV_MAX_DYN_LDS && (nch + NWAVE - 1) / NWAVE <= 12) {
-                pl.cw = cw;
-                pl.nbuf = nbuf;
-                pl.nch = nch;
-                pl.nld = (nch + NWAVE - 1) / NWAVE;
-                pl.lds = lds;
-                pl.ng = ng;
-                pl.v_off = v_off;
-                pl.ok = true;
-                return pl;
-            }
+    int max_units;
+    if (fmt == FMT_Q4) {
+        pl.v_off = vs_off & ~15;
+        pl.ng = (vq_off + v_bytes + 15) / 16 - pl.v_off / 16;
+        pl.units = (pl.ng + 1) / 2;
+        max_units = 32;  // 2 blocks each
+    } else {
+        pl.v_off = 2 * k_width;
+        pl.units = (v_rank + 31) / 32;
+        max_units = 64;
+    }
+    // Fewest launches (each re-reads the logits) whose pages keep at least PV_INFLIGHT
+    // bytes in flight per workgroup, else the most bytes in flight.
+    const int lo = (pl.units + std::min(pl.units, max_units) - 1) / std::min(pl.units, max_units);
+    int best_score = -1;
+    for (int launches = lo; launches <= lo + 3; ++launches) {
+        const int per = (pl.units + launches - 1) / launches;
+        if (per > max_units || (fmt == FMT_Q4 && launches > lo)) continue;
+        const int ng = fmt == FMT_Q4 ? pl.ng : 4 * per;
+        const int nch = (ng + 3) / 4 + PV_V0;
+        if ((nch + NWAVE - 1) / NWAVE > PV_NLD) continue;
+        const int nbuf = std::min(8, (PV_MAX_DYN_LDS - 1024) / (nch * 1024));
+        if (nbuf < 2) continue;
+        const int inflight = (nbuf - 1) * nch * 1024;
+        const int score = inflight >= PV_INFLIGHT ? (1 << 30) - launches : inflight;
+        if (score > best_score) {
+            best_score = score;
+            pl.per = per;
+            pl.nbuf = nbuf;
+            pl.nch = nch;
+            pl.nld = (nch + NWAVE - 1) / NWAVE;
+            pl.lds = nbuf * nch * 1024 + 1024;
+            if (fmt != FMT_Q4) pl.ng = ng;
+            pl.ok = true;
         }
     }
-    pl.ok = false;
     return pl;
 }
 
 int launch_pv(const DecodeParams& p, int fmt, int grid, hipStream_t stream) {
     const int v_bytes = p.v_nbo + (p.v_rank - p.v_nout + 1) / 2;
-    const PvPlan pl = pv_plan(fmt, p.k_width, p.v_rank, p.vs_off, p.vq_off, p.v_nout, v_bytes);
+    const PvPlan pl = pv_plan(fmt, p.k_width, p.v_rank, p.vs_off, p.vq_off, v_bytes);
     SKV_CHECK(pl.ok, "decode: no P @ V window fits in LDS (v_rank %d)", p.v_rank);
     PvParams a;
     memset(&a, 0, sizeof(a));
@@ -529,16 +598,23 @@ int launch_pv(const DecodeParams& p, int fmt, int grid, hipStream_t stream) {
     a.ng = pl.ng;
     a.vs_rel = p.vs_off - pl.v_off;
     a.vq_rel = p.vq_off - pl.v_off;
-    a.v_nout = p.v_nout; a.v_nbo = p.v_nbo; a.o32 = (p.v_nout + 31) & ~31;
+    a.v_nout = p.v_nout; a.v_nbo = p.v_nbo;
     a.nch = pl.nch; a.nld = pl.nld; a.nbuf = pl.nbuf; a.buf_bytes = pl.nch * 1024;
-    a.tab = pl.nbuf * pl.nch * 1024;
     a.lds_bytes = pl.lds;
     a.ws = p.ws; a.ws_plan = p.ws_plan; a.ws_m = p.ws_m; a.ws_acc = p.ws_acc; a.ws_lg = p.ws_lg; a.lcap = p.lcap;
-    for (int c0 = 0; c0 < pl.tcols; c0 += pl.cw) {
-        a.c0 = c0;
-        a.ncb = (std::min(pl.cw, pl.tcols - c0) + 31) / 32;
-        a.v_off = fmt == FMT_Q4 ? pl.v_off : pl.v_off + 2 * c0;
-        const int mb = (a.ncb + NWAVE - 1) / NWAVE;
+    a.acc_ld = p.acc_ld;
+    for (int u0 = 0; u0 < pl.units; u0 += pl.per) {
+        a.ncb = std::min(pl.per, pl.units - u0);
+        int mb;
+        if (fmt == FMT_Q4) {
+            a.c0 = u0;
+            a.v_off = pl.v_off;
+            mb = 2 * ((a.ncb + NWAVE - 1) / NWAVE);
+        } else {
+            a.c0 = 32 * u0;
+            a.v_off = pl.v_off + 64 * u0;
+            mb = (a.ncb + NWAVE - 1) / NWAVE;
+        }
         const void* fn = fmt == FMT_BF16 ? pv_pick<FMT_BF16>(mb)
                          : fmt == FMT_F16 ? pv_pick<FMT_F16>(mb)
                                           : pv_pick<FMT_Q4>(mb);
@@ -551,26 +627,29 @@ int launch_pv(const DecodeParams& p, int fmt, int grid, hipStream_t stream) {
 }
 
 bool pv_fits(int fmt, int k_width, int v_rank, int vs_off, int vq_off, int v_nout, int v_bytes) {
-    return pv_plan(fmt, k_width, v_rank, vs_off, vq_off, v_nout, v_bytes).ok;
+    (void)v_nout;
+    return pv_plan(fmt, k_width, v_rank, vs_off, vq_off, v_bytes).ok &&
+           lift_lds((v_rank + 3) & ~3) <= (size_t)PV_MAX_DYN_LDS;
 }
 
 int launch_merge_wide(const DecodeParams& p, int w_dt, const void* vup, int64_t vu_s0, int64_t vu_s1, void* out,
                       int64_t o_s0, int64_t o_s1, int out_dt, hipStream_t stream) {
-    const size_t lds = merge_wide_lds(p.v_rank);
+    const size_t lds = lift_lds(p.acc_ld);
     SKV_CHECK(lds <= (size_t)PV_MAX_DYN_LDS, "decode: v_rank %d too large for the merge", p.v_rank);
-    const dim3 grid(p.Hq, (p.n + MW_REQ - 1) / MW_REQ);
-    const void* fn = w_dt == STARKV_BF16 ? (const void*)&merge_wide_kernel<STARKV_BF16>
-                     : w_dt == STARKV_F16 ? (const void*)&merge_wide_kernel<STARKV_F16>
-                                          : (const void*)&merge_wide_kernel<STARKV_F32>;
+    hipLaunchKernelGGL(merge_cols_kernel, dim3(p.n, p.Hq), dim3(MC_THR), 0, stream, (const uint8_t*)p.ws, p.ws_plan,
+                       p.ws_m, p.ws_l, p.ws_acc, p.ws_o, p.n, p.Hq, p.v_rank, p.acc_ld);
+    SKV_HIP(hipGetLastError());
+    const void* fn = w_dt == STARKV_BF16 ? (const void*)&lift_kernel<STARKV_BF16>
+                     : w_dt == STARKV_F16 ? (const void*)&lift_kernel<STARKV_F16>
+                                          : (const void*)&lift_kernel<STARKV_F32>;
     int rc = raise_lds(fn, PV_MAX_DYN_LDS);
     if (rc) return rc;
     const uint8_t* ws = p.ws;
-    size_t wp = p.ws_plan, wm = p.ws_m, wl = p.ws_l, wa = p.ws_acc;
-    int n = p.n, Hq = p.Hq, vr = p.v_rank;
-    void* args[] = {(void*)&ws, (void*)&wp, (void*)&wm, (void*)&wl, (void*)&wa, (void*)&n, (void*)&Hq, (void*)&vr,
-                    (void*)&vup, (void*)&vu_s0, (void*)&vu_s1, (void*)&out, (void*)&o_s0, (void*)&o_s1,
-                    (void*)&out_dt};
-    SKV_HIP(hipLaunchKernel(fn, grid, dim3(MW_THR), args, lds, stream));
+    size_t wo = p.ws_o;
+    int n = p.n, Hq = p.Hq, vr = p.v_rank, ld = p.acc_ld;
+    void* args[] = {(void*)&ws, (void*)&wo, (void*)&n, (void*)&Hq, (void*)&vr, (void*)&ld, (void*)&vup,
+                    (void*)&vu_s0, (void*)&vu_s1, (void*)&out, (void*)&o_s0, (void*)&o_s1, (void*)&out_dt};
+    SKV_HIP(hipLaunchKernel(fn, dim3(p.Hq, (p.n + LIFT_REQ - 1) / LIFT_REQ), dim3(LIFT_THR), args, lds, stream));
     return STARKV_OK;
 }
 
