@@ -146,6 +146,18 @@ size_t starkv_decode_workspace_bytes(int cache_kind, int n, int num_heads, int n
 int starkv_decode_two_pass(int cache_kind, int num_heads, int k_width, int v_rank);
 
 /*
+ * 1 if the decode entry points take a layer of this shape, else 0 (host function, no
+ * device access; call it at load time). k_ranks: host array of the num_kv_heads K ranks.
+ * A layer is refused when it has more than 32 query heads, more than 96 16-lane rank
+ * tiles over its query heads ((num_heads / num_kv_heads) x k_width / 16), a query head
+ * with more tiles than one of the decode kernel's 8 waves holds (16) after the wave plan
+ * balances whole heads, v_rank above 4096, or (3.2-bit) num_kv_heads != num_heads. The
+ * decode calls themselves return NaN rows for a layer whose heads do not fit the plan.
+ * No counterpart in the reference, whose Triton kernels take any head count.
+ */
+int starkv_decode_layer_fits(int cache_kind, int num_heads, int num_kv_heads, const int32_t *k_ranks, int v_rank);
+
+/*
  * Forces the decode form for the calls that follow (process-wide, not thread-safe; for
  * tests and benchmarks that compare the two): 0 = automatic (default), 1 = one-pass
  * only (shapes it cannot take are refused), 2 = two-pass always. Returns the previous

@@ -39,6 +39,7 @@
 // workspace), a P @ V pass reads the logits and the V bytes, and a merge of its own
 // lifts the result. Both forms take the same arguments and give the same outputs to
 // within rounding.
+#include <algorithm>
 #include <vector>
 
 #include "decode_common.hpp"
@@ -685,6 +686,53 @@ static bool use_two_pass(int fmt, int k_width, int v_rank, int row_bytes, int v_
     return g_path == 2 || (g_path == 0 && !one_pass_fits(fmt, k_width, v_rank, row_bytes, v_nout));
 }
 
+// Host restatement of the wave plan that workgroup 0 of prep_kernel builds
+// (prep_setup): query heads sorted by decreasing rank tiles (ties: lower head first),
+// dealt to the 8 decode waves in snake order, then the swap that lowers the most loaded
+// wave the most, while one does. True if every wave ends with at most MAX_SLOTS tiles,
+// which is when the decode kernels run the layer (otherwise they return NaN rows).
+static bool plan_fits(const int* tiles, int Hq, int TT) {
+    if (Hq < 1 || Hq > MAX_H || TT < 1 || TT > MAX_TT) return false;
+    int head_at[MAX_H], hsz[MAX_H], hwave[MAX_H], load[NWAVE] = {0};
+    for (int h = 0; h < Hq; ++h) {
+        int pos = 0;
+        for (int k = 0; k < Hq; ++k) pos += tiles[k] > tiles[h] || (tiles[k] == tiles[h] && k < h);
+        head_at[pos] = h;
+    }
+    for (int p = 0; p < Hq; ++p) {
+        hsz[p] = tiles[head_at[p]];
+        const int col = p % NWAVE;
+        hwave[p] = ((p / NWAVE) & 1) ? NWAVE - 1 - col : col;
+        load[hwave[p]] += hsz[p];
+    }
+    const int target = (TT + NWAVE - 1) / NWAVE;
+    for (int it = 0; it < 64; ++it) {
+        int A = 0;
+        for (int w = 1; w < NWAVE; ++w)
+            if (load[w] >= load[A]) A = w;  // the most loaded wave, ties to the higher index
+        const int la = load[A];
+        if (la <= target) break;
+        int best = 0x7fffffff;
+        for (int ha = 0; ha < Hq; ++ha) {
+            if (hwave[ha] != A) continue;
+            for (int hb = 0; hb < Hq; ++hb) {
+                if (hwave[hb] == A) continue;
+                const int d = hsz[ha] - hsz[hb], lb = load[hwave[hb]];
+                if (d > 0 && lb + d < la) best = std::min(best, (std::max(la - d, lb + d) << 16) | (ha << 8) | hb);
+            }
+        }
+        if (best == 0x7fffffff) break;
+        const int ha = (best >> 8) & 255, hb = best & 255, B = hwave[hb], d = hsz[ha] - hsz[hb];
+        hwave[ha] = B;
+        hwave[hb] = A;
+        load[A] -= d;
+        load[B] += d;
+    }
+    for (int w = 0; w < NWAVE; ++w)
+        if (load[w] > MAX_SLOTS) return false;
+    return true;
+}
+
 static int lcap_of(int max_seq_len) { return (max_seq_len + TILE_TOK - 1) / TILE_TOK * TILE_TOK; }
 
 // QuantRow (paged_quant.py:71-111) offsets of a 3.2-bit row.
@@ -885,6 +933,38 @@ size_t starkv_decode_workspace_bytes(int cache_kind, int n, int num_heads, int n
     }
     const bool two = use_two_pass(fmt, k_width, v_rank, row_bytes, v_nout);
     return ws_layout(n, num_heads, TT, v_rank, grid, two ? lcap_of(max_seq_len) : 0).total;
+}
+
+int starkv_decode_layer_fits(int cache_kind, int num_heads, int num_kv_heads, const int32_t* k_ranks, int v_rank) {
+    clear_error();
+    SKV_CHECK(k_ranks != nullptr, "decode_layer_fits: null k_ranks");
+    SKV_CHECK(num_heads >= 1 && num_kv_heads >= 1 && num_heads % num_kv_heads == 0,
+              "decode_layer_fits: %d query heads over %d kv heads", num_heads, num_kv_heads);
+    if (cache_kind == STARKV_CACHE_Q3_2 && num_heads != num_kv_heads) return 0;  // MHA only (paged_quant.py:374)
+    if (num_heads > MAX_H || v_rank < 1 || v_rank > MAX_V_RANK_TWO_PASS) return 0;
+    int tiles[MAX_H];
+    int TT = 0, k_width = 0;
+    const int grp = num_heads / num_kv_heads;
+    for (int kv = 0; kv < num_kv_heads; ++kv) {
+        const int r = k_ranks[kv];
+        if (r < 0) return 0;
+        k_width += (r + 15) / 16 * 16;
+        for (int j = 0; j < grp; ++j) tiles[kv * grp + j] = (r + 15) / 16;
+    }
+    for (int h = 0; h < num_heads; ++h) TT += tiles[h];
+    if (TT > MAX_TT) return 0;
+    if (!plan_fits(tiles, num_heads, TT)) return 0;
+    // The pages of the pass that reads K must fit in LDS.
+    if (cache_kind == STARKV_CACHE_Q3_2) {
+        const QRow r = qrow(k_width, num_heads, v_rank);
+        if (!use_two_pass(FMT_Q4, k_width, v_rank, r.nbytes, r.v_nout)) return 1;
+        const int rk = (r.vs_off + 15) / 16 * 16;
+        return quant_copies(rk) > 0 && quant_lds_bytes(rk, 0) <= quant_lds_limit() &&
+               pv_fits(FMT_Q4, k_width, v_rank, r.vs_off, r.vq_off, r.v_nout, r.v_bytes);
+    }
+    const int fmt = cache_kind == STARKV_F16 ? FMT_F16 : FMT_BF16;
+    if (!use_two_pass(fmt, k_width, v_rank, (k_width + v_rank) * 2, 0)) return 1;
+    return lowrank_copies(k_width, 0) > 0 && pv_fits(fmt, k_width, v_rank, 0, 0, 0, 0);
 }
 
 int starkv_decode_set_path(int mode) {

@@ -39,6 +39,7 @@ SIGNATURES = {
     "starkv_decode_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I, _I, _I]),
     "starkv_decode_two_pass": (_I, [_I, _I, _I, _I]),
     "starkv_decode_set_path": (_I, [_I]),
+    "starkv_decode_layer_fits": (_I, [_I, _I, _I, ctypes.POINTER(ctypes.c_int32), _I]),
     "starkv_lowrank_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _I, _P, _I64, _I64, _P, _I,
                                    _I, _I, _I, _P, _I64, _I, _P, _P, _I, _P, _I64, _I64, _I, _I, _P, _I64,
                                    _I, _F, _P, _I64, _I64, _I, _P, _SZ, _I]),
@@ -88,6 +89,12 @@ def stream_of(t: torch.Tensor) -> int:
 
 def ptr(t: torch.Tensor) -> int:
     return t.data_ptr()
+
+
+def layer_fits(cache_kind: int, num_heads: int, num_kv_heads: int, k_ranks, v_rank: int) -> bool:
+    """Whether the decode takes a layer of this shape (host-side; k_ranks a list of ints)."""
+    arr = (ctypes.c_int32 * len(k_ranks))(*[int(r) for r in k_ranks])
+    return bool(lib().starkv_decode_layer_fits(int(cache_kind), int(num_heads), int(num_kv_heads), arr, int(v_rank)))
 
 
 def set_decode_path(mode: int) -> int:

@@ -132,6 +132,8 @@ class StarKVAttentionImpl:
             idx[h * R + width:(h + 1) * R] = off
             k_up_pad[h, :width] = w.k_up[off:off + width]
         self.k_prefill_gather = idx.to(device)
+        # The decode kernels read an fp16 cos/sin table: converted once here, not per step.
+        self.cos_sin16 = self.rotary_emb.cos_sin_cache.to(device=device, dtype=torch.float16).contiguous()
         self.k_up_T = k_up_pad.to(device=device, dtype=torch.float32).contiguous()
         self.v_up = w.v_up.to(device=device, dtype=torch.float32).contiguous()  # [H * Hd, v_rank]
 
@@ -229,7 +231,9 @@ class StarKVAttentionImpl:
         span = self.max_model_len if full else max(md.max_seq_len, 1)
         # Padding rows have length 0; give them one (null-block) position to attend to.
         seq_lens = md.seq_lens[:nd].clamp(min=1)
-        cs = self.rotary_emb.cos_sin_cache
+        cs = getattr(self, "cos_sin16", None)
+        if cs is None:
+            cs = self.rotary_emb.cos_sin_cache
         if self.row is None:
             o = paged_starkv_decode(q, cache, md.block_table[:nd], seq_lens, span, self.k_up, self.k_ranks,
                                     self.k_head_offsets, self.k_width, self.v_up_by_q, cs, self.scale)

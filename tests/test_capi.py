@@ -114,3 +114,27 @@ def test_write_kv_validation():
     assert L.starkv_write_kv_workspace_bytes(64, 1344, 4096) == 16 * 64 * 1344 * 4
     assert L.starkv_write_kv_workspace_bytes(1024, 1344, 4096) == 1 * 1024 * 1344 * 4
     assert L.starkv_write_kv_workspace_bytes(0, 1344, 4096) == 0
+
+
+def test_layer_fits_host_plan():
+    """The host restatement of the wave plan accepts what the decode runs and refuses
+    what it cannot (more than 32 heads, more than 96 tiles, a head of more than 16
+    tiles, V rank above 4096, 3.2-bit GQA)."""
+    from starkv_serve import _hip
+    BF16, Q = _hip.BF16, _hip.CACHE_Q3_2
+    fits = _hip.layer_fits
+    assert fits(BF16, 32, 32, [16, 32, 48, 64] * 8, 64)
+    assert fits(Q, 32, 32, [16, 32, 48, 64] * 8, 64)
+    assert fits(BF16, 32, 32, [32] * 23 + [16] * 9, 1280)           # the 0.75-ratio shape, two-pass
+    assert fits(Q, 32, 32, [32] * 23 + [16] * 9, 1290)
+    assert fits(BF16, 32, 8, [32] * 8, 2048)                        # GQA 4: 64 tiles
+    assert fits(BF16, 4, 4, [256, 16, 100, 20], 64)                 # one head of 16 tiles
+    assert not fits(BF16, 4, 4, [272, 16, 16, 16], 64)              # a head of 17 tiles
+    assert not fits(BF16, 64, 64, [16] * 64, 64)                    # 64 query heads
+    assert not fits(BF16, 32, 8, [64] * 8, 64)                      # GQA 4 x 4 tiles x 8 = 128 tiles
+    assert not fits(BF16, 32, 32, [16] * 32, 4097)                  # V rank
+    assert not fits(Q, 32, 16, [16] * 16, 64)                       # 3.2-bit is MHA only
+    # eight heads of 12 tiles (96 in all) take one wave each; a ninth head passes the
+    # 96-tile cap
+    assert fits(BF16, 8, 8, [192] * 8, 64)
+    assert not fits(BF16, 9, 9, [192] * 8 + [16], 64)

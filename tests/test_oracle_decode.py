@@ -118,3 +118,23 @@ def test_quant_oracle_uses_all_stored_lanes():
     flat[1:].reshape(-1, Wd + 16)[:L] = np.concatenate([K, V], 1)
     want = ref.lowrank_decode(q, flat, bt, [L], L, U, [16, 32], offsets, Wd, vq, cs, 0.1)
     np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_reference_emulation_pinned_in_wide_dtypes():
+    """The reference-rounding emulation, run with float64 query and bases, equals the
+    float64 oracle to fp32 accuracy (its K lift and P @ V stay fp32): a dropped term, a
+    wrong head or offset, or a transposed operand in the emulation would not."""
+    wl = W.make_lowrank([37, 5, 200], num_heads=8, num_kv_heads=4, ranks=[16, 32, 20, 48], v_rank=32, seed=21,
+                        poison=False)
+    a = _lowrank_np(wl)
+    want = _oracle(wl, a)
+    got = ref.emulate_lowrank_reference(torch.from_numpy(a["q"]).double(), a["cache"], a["bt"], a["seq"],
+                                        wl.max_seq_len, a["U"], wl.ranks, wl.k_head_offsets.tolist(), wl.k_width,
+                                        torch.from_numpy(a["vq"]).double(), a["cs"], wl.scale)
+    err = np.abs(got - want).max() / np.abs(want).max()
+    assert err < 2e-6, err
+    # and with the model dtype it departs by the reference's own rounding (logits in bf16)
+    emu = ref.emulate_lowrank_reference(wl.query, wl.kv_cache, a["bt"], a["seq"], wl.max_seq_len, wl.k_up,
+                                        wl.ranks, wl.k_head_offsets.tolist(), wl.k_width, wl.v_up_by_q,
+                                        wl.cos_sin_cache, wl.scale)
+    assert 1e-4 < np.abs(emu - want).max() / np.abs(want).max() < 5e-2
