@@ -198,6 +198,28 @@ int starkv_lowrank_decode(void *stream, const void *query, int64_t q_s0, int64_t
                           int grid);
 
 /*
+ * starkv_lowrank_decode with no workspace argument and no allocation: the call's
+ * workspace is a fixed 64 MiB array of device memory inside the library (one per
+ * device, held until the process ends), so callers that cannot allocate (code under
+ * HIP graph capture, serving loops that forbid allocation) can decode. A call whose
+ * starkv_decode_workspace_bytes exceeds 64 MiB is refused with an error (for example
+ * 64 requests x 8192 tokens fit in one-pass form, k_width 1280 / v_rank 64: ~23 MiB).
+ * Every call on one device shares that array: calls that overlap on one device (other
+ * streams, other host threads) race, so serialize them. Nothing in it needs clearing
+ * between calls. No counterpart in the reference; it exists for callers that cannot
+ * allocate. Arguments as starkv_lowrank_decode.
+ */
+int starkv_lowrank_decode_noalloc(void *stream, const void *query, int64_t q_s0, int64_t q_s1, int q_dtype,
+                                  const void *kv_cache, int64_t c_s0, int64_t c_s1, int code_dtype,
+                                  int block_size, const int32_t *block_table, int64_t bt_s0, int64_t bt_s1,
+                                  const int32_t *seq_lens, int n, int num_heads, int num_kv_heads,
+                                  int max_seq_len, const void *k_up, int64_t ku_s0, int w_dtype,
+                                  const int32_t *k_ranks, const int32_t *k_head_offsets, int k_width,
+                                  const void *v_up_by_q, int64_t vu_s0, int64_t vu_s1, int vu_dtype, int v_rank,
+                                  const void *cos_sin, int64_t cs_s0, int cs_dtype, float scale, void *out,
+                                  int64_t o_s0, int64_t o_s1, int out_dtype, int grid);
+
+/*
  * 3.2-bit paged decode over the QuantRow cache. Replaces
  * starkv_serve/kernels/paged_quant.py:357-411 (paged_quant_decode: fold_q,
  * _paged_abx_z, softmax, _paged_pv_fold, lift). MHA, head_dim 128.

@@ -878,6 +878,28 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     return launch_merge<float>(mgrid, mlds, stream, p, wl, a);
 }
 
+// Workspace of starkv_lowrank_decode_noalloc: one array per device, held until the
+// process ends. Host code never uses the array's name as an address (on the host it
+// only stands for the symbol); it uses the device address hipGetSymbolAddress returns,
+// looked up once per device.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+static int scratch_address(void** out) {
+    static void* ptr[64] = {nullptr};
+    int dev = 0;
+    SKV_HIP(hipGetDevice(&dev));
+    SKV_CHECK(dev >= 0 && dev < 64, "decode_noalloc: device %d", dev);
+    if (!ptr[dev]) {
+        void* a = nullptr;
+        SKV_HIP(hipGetSymbolAddress(&a, HIP_SYMBOL(scratch)));
+        SKV_CHECK(a != nullptr && ((uintptr_t)a % 256) == 0, "decode_noalloc: scratch address");
+        ptr[dev] = a;
+    }
+    *out = ptr[dev];
+    return STARKV_OK;
+}
+
 }  // namespace starkv
 
 using namespace starkv;
@@ -1030,6 +1052,34 @@ int starkv_lowrank_decode(void* stream, const void* query, int64_t q_s0, int64_t
     const int TT = (num_heads / num_kv_heads) * (k_width / 16);
     return decode_common(p, a, code_dtype == STARKV_BF16 ? FMT_BF16 : FMT_F16, (k_width + v_rank) * 2, TT,
                          (hipStream_t)stream);
+}
+
+int starkv_lowrank_decode_noalloc(void* stream, const void* query, int64_t q_s0, int64_t q_s1, int q_dtype,
+                                  const void* kv_cache, int64_t c_s0, int64_t c_s1, int code_dtype, int block_size,
+                                  const int32_t* block_table, int64_t bt_s0, int64_t bt_s1, const int32_t* seq_lens,
+                                  int n, int num_heads, int num_kv_heads, int max_seq_len, const void* k_up,
+                                  int64_t ku_s0, int w_dtype, const int32_t* k_ranks, const int32_t* k_head_offsets,
+                                  int k_width, const void* v_up_by_q, int64_t vu_s0, int64_t vu_s1, int vu_dtype,
+                                  int v_rank, const void* cos_sin, int64_t cs_s0, int cs_dtype, float scale,
+                                  void* out, int64_t o_s0, int64_t o_s1, int out_dtype, int grid) {
+    clear_error();
+    SKV_CHECK(code_dtype == STARKV_BF16 || code_dtype == STARKV_F16,
+              "lowrank_decode_noalloc: codes must be bf16 or fp16");
+    const size_t need = starkv_decode_workspace_bytes(code_dtype, n, num_heads, num_kv_heads, k_width, v_rank,
+                                                      max_seq_len, grid);
+    SKV_CHECK(need > 0, "lowrank_decode_noalloc: invalid sizes");
+    SKV_CHECK(need <= NOALLOC_SCRATCH_BYTES,
+              "lowrank_decode_noalloc: this call needs %zu workspace bytes, more than the %zu of the "
+              "library's fixed scratch (use starkv_lowrank_decode with a workspace, or fewer requests)",
+              need, NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    const int rc = scratch_address(&ws);
+    if (rc) return rc;
+    return starkv_lowrank_decode(stream, query, q_s0, q_s1, q_dtype, kv_cache, c_s0, c_s1, code_dtype, block_size,
+                                 block_table, bt_s0, bt_s1, seq_lens, n, num_heads, num_kv_heads, max_seq_len, k_up,
+                                 ku_s0, w_dtype, k_ranks, k_head_offsets, k_width, v_up_by_q, vu_s0, vu_s1,
+                                 vu_dtype, v_rank, cos_sin, cs_s0, cs_dtype, scale, out, o_s0, o_s1, out_dtype, ws,
+                                 NOALLOC_SCRATCH_BYTES, grid);
 }
 
 int starkv_quant_decode(void* stream, const void* query, int64_t q_s0, int64_t q_s1, int q_dtype,

@@ -43,6 +43,9 @@ SIGNATURES = {
     "starkv_lowrank_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _I, _P, _I64, _I64, _P, _I,
                                    _I, _I, _I, _P, _I64, _I, _P, _P, _I, _P, _I64, _I64, _I, _I, _P, _I64,
                                    _I, _F, _P, _I64, _I64, _I, _P, _SZ, _I]),
+    "starkv_lowrank_decode_noalloc": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _I, _P, _I64, _I64, _P,
+                                           _I, _I, _I, _I, _P, _I64, _I, _P, _P, _I, _P, _I64, _I64, _I, _I, _P,
+                                           _I64, _I, _F, _P, _I64, _I64, _I, _I]),
     "starkv_quant_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _P, _I64, _I64, _P, _I, _I, _I,
                                  _I, _I, _I, _P, _I64, _I, _P, _P, _P, _P, _I64, _I64, _I, _P, _I64, _I, _F,
                                  _P, _I64, _I64, _I, _P, _SZ, _I]),
