@@ -2,20 +2,27 @@
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 
-A step is one decode call (one layer) over the whole batch. The headline workload
-is the reference metric's configuration: bf16/low-rank codes, batch 64, every
-request at 8192 tokens of context, 32 heads x head_dim 128, page size 16, K ranks
-per head drawn from {16, 32, 48, 64}, V rank 64, physical pages shuffled. The cache
-(1.25 GB) is larger than the 256 MB Infinity Cache, so every step streams it from
-HBM. `value` = algorithmic bytes per step / wall time per step (whole call: prep,
-decode and merge launches). `roofline.achieved` = the same bytes / the decode
-kernel's own average duration (HIP events around that launch, in a second pass of
-the same steps). Each workload's warmup runs 60 ms of back-to-back calls after a
-first round of 10 (--min-warmup-ms), so that the timed steps see the GPU's settled
-clocks. The
-3.2-bit kernel at the same shape (three rotating cache copies, 1.3 GB) and the ragged reference
-configurations are reported under "extra". `cpu_baseline` times the float64 CPU
-oracle on a bounded sample of the same workload on this host.
+A step is one decode call (one layer) over the whole batch. The headline workload is
+the reference metric's configuration: bf16 low-rank codes, batch 64, every request at
+8192 tokens of context, 32 heads x head_dim 128, page size 16, K ranks per head drawn
+from {16, 32, 48, 64}, V rank 64, physical pages shuffled. The cache (1.25 GB) is
+larger than the 256 MB Infinity Cache, so every step streams it from HBM.
+
+Timing, per workload, after W warm-up calls continued until 60 ms of back-to-back calls
+have settled the clocks (--min-warmup-ms):
+  - `ms_per_step` / `value`: K calls between two synchronizations, one event pair around
+    them (the whole call: prep, decode and merge launches), value = algorithmic bytes per
+    step / that mean time;
+  - `call_us_median`: the median over K more calls of the whole call, from event pairs
+    the library records around each call;
+  - `decode_kernel_us`: the median over K more calls of the decode kernels alone (the
+    roofline figure: `roofline.achieved` = bytes / this time).
+Extra workloads: the 3.2-bit kernel at the same shape (three rotating cache copies),
+the ragged U[1024, 8192] configurations, batch 1 x 4096, 16 x 32768 3.2-bit with the
+fused cache write in each step, the reference checkpoint's shape (K width 880, V rank
+1280 / 1290: the two-pass form), the fused cache write, and uncompressed attention
+(torch SDPA and the 100 %-HBM bound). `cpu_baseline` times the reference's math restated
+in fp32 PyTorch (oracle/torch_ref.py) on this host's cores, median of 5 runs after 1.
 
 One JSON line is printed on stdout.
 """
@@ -23,6 +30,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -33,10 +41,12 @@ for _p in (ROOT, os.path.join(ROOT, "star-kv-serve_amd")):
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_PEAK_F16_TFLOPS = 2500.0  # dense fp16/bf16
-METRIC = "decode-attn \u00b5s & HBM GB/s (% peak) at bs64\u00d78K; TPOT, tok/s at max sessions"
-# HBM bytes per decode-kernel launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
-# scaled by the same counters on a copy of known size); written by hand from the runs.
+METRIC = "decode-attn µs & HBM GB/s (% peak) at bs64×8K; TPOT, tok/s at max sessions"
+# HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by
+# the same counters on a copy of known size); written by hand from the runs.
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_kernel_hbm_traffic.md")
+# K ranks of a 0.75-ratio layer of the reference checkpoint: 880 lanes over 32 heads.
+RANKS_880 = [32] * 23 + [16] * 9
 
 
 def log(*a):
@@ -69,11 +79,12 @@ def warm_up(fn, warmup):
             return i
 
 
-def time_steps(fn, steps, warmup):
-    """Warmup, then `steps` timed calls bracketed by synchronizes (ms per step, the
-    whole call), then `steps` more calls with HIP events around each decode launch
-    (decode-kernel ms per call). The events sit in a pass of their own: each record
-    holds the stream for a few microseconds, which would count in the whole-call time."""
+def time_decode(fn, steps, warmup):
+    """Decode calls: warmup; `steps` calls bracketed by synchronizes (mean ms per call, the
+    contract figure); `steps` calls with the library's per-call events around the whole
+    call (median); `steps` calls with its events around the decode kernels (median). The
+    three passes are separate because each event record holds the stream a few
+    microseconds."""
     import torch
     from starkv_serve import _hip
     warm_up(fn, warmup)
@@ -83,43 +94,130 @@ def time_steps(fn, steps, warmup):
         fn(i)
     stop.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / steps
-    _hip.profile_begin(steps)
+    mean_ms = start.elapsed_time(stop) / steps
+    out = dict(ms=mean_ms)
+    for key, whole in (("call_ms", True), ("kern_ms", False)):
+        _hip.profile_begin(steps, whole_call=whole)
+        for i in range(steps):
+            fn(i)
+        torch.cuda.synchronize()
+        t = _hip.profile_end()
+        out[key] = statistics.median(t) if t else float("nan")
+    return out
+
+
+def time_events(fn, steps, warmup):
+    """Other work (writes, stock attention, write + decode steps): warmup, then `steps`
+    calls with an event pair around each; (mean, median) ms per call."""
+    import torch
+    warm_up(fn, warmup)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     for i in range(steps):
+        ev[i][0].record()
         fn(i)
+        ev[i][1].record()
     torch.cuda.synchronize()
-    kern_ms, calls = _hip.profile_end()
-    return ms, kern_ms / max(calls, 1)
+    t = [a.elapsed_time(b) for a, b in ev]
+    return sum(t) / len(t), statistics.median(t)
 
 
-def bench_lowrank(lengths, steps, warmup, seed, v_rank=64):
+def decode_args_fp16_cs(wl):
+    """The workload's decode arguments with the cos/sin table in fp16, as
+    StarKVAttentionImpl.to_device converts it once at load time."""
+    from starkv_serve.kernels.paged_decode import cos_sin_for_kernel
+    args = list(wl.decode_args())
+    args[10] = cos_sin_for_kernel(args[10])
+    return args
+
+
+def bench_lowrank(lengths, steps, warmup, seed, v_rank=64, ranks=None):
     import torch
     from starkv_serve import workloads as W
     from starkv_serve.kernels.paged_decode import paged_starkv_decode
     dev = torch.device("cuda", 0)
-    wl = W.make_lowrank(lengths, num_heads=32, v_rank=v_rank, seed=seed, gen_device=dev).to(dev)
-    args = wl.decode_args()
-    ms, kern = time_steps(lambda i: paged_starkv_decode(*args), steps, warmup)
-    return wl, ms, kern
+    wl = W.make_lowrank(lengths, num_heads=32, v_rank=v_rank, ranks=ranks, seed=seed, gen_device=dev).to(dev)
+    args = decode_args_fp16_cs(wl)
+    return wl, time_decode(lambda i: paged_starkv_decode(*args), steps, warmup)
 
 
-def bench_quant(lengths, steps, warmup, seed, copies, v_rank=64):
+def bench_quant(lengths, steps, warmup, seed, copies, v_rank=64, ranks=None):
     import torch
     from starkv_serve import workloads as W
     from starkv_serve.kernels.paged_quant import paged_quant_decode
     dev = torch.device("cuda", 0)
-    wl = W.make_quant(lengths, num_heads=32, v_rank=v_rank, seed=seed, device=dev, gen_device=dev)
+    wl = W.make_quant(lengths, num_heads=32, v_rank=v_rank, ranks=ranks, seed=seed, device=dev, gen_device=dev)
     wl.k_codes = wl.v_codes = None
     torch.cuda.empty_cache()
     caches = [wl.kv_cache] + [wl.kv_cache.clone() for _ in range(copies - 1)]
-    base = list(wl.decode_args())
+    base = decode_args_fp16_cs(wl)
 
     def step(i):
         base[1] = caches[i % len(caches)]
         return paged_quant_decode(*base)
 
-    ms, kern = time_steps(step, steps, warmup)
-    return wl, ms, kern
+    return wl, time_decode(step, steps, warmup)
+
+
+def summarize(wl, t):
+    b = wl.bytes_per_step()
+    f = wl.flops_per_step()
+    k = t["kern_ms"]
+    return dict(us_per_step=round(t["ms"] * 1e3, 2), call_us_median=round(t["call_ms"] * 1e3, 2),
+                decode_kernel_us=round(k * 1e3, 2), GBps=round(b / (t["ms"] * 1e-3) / 1e9, 1),
+                kernel_GBps=round(b / (k * 1e-3) / 1e9, 1), hbm_frac=round(b / (k * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                mfma_frac=round(f / (k * 1e-3) / 1e12 / MFMA_PEAK_F16_TFLOPS, 4), bytes_per_step=int(b),
+                flops_per_step=int(f), tokens=wl.tokens, requests=wl.n, k_width=wl.k_width, v_rank=wl.v_rank)
+
+
+def bench_c3(steps_per_pass, passes, warmup_passes=1, n_req=16, context=32768, hidden=4096, seed=3003):
+    """Config 3: 16 requests at context 32768, 3.2-bit, each step writing one token per
+    request through the fused write (kv_down GEMM + quantize + scatter) and then decoding
+    with the lengths one longer, 32 steps per pass, max_seq_len = the context (a full
+    graph's span). Median per step over the timed passes."""
+    import torch
+    from starkv_serve import checkpoint as ck
+    from starkv_serve import workloads as W
+    from starkv_serve.kernels.kv_write import write_kv
+    from starkv_serve.kernels.paged_quant import paged_quant_decode
+    import tempfile
+    dev = torch.device("cuda", 0)
+    wl = W.make_quant([context] * n_req, num_heads=32, v_rank=64, seed=seed, device=dev, gen_device=dev)
+    wl.k_codes = wl.v_codes = None
+    torch.cuda.empty_cache()
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "fused_weights.pt")
+        ck.write_fused_checkpoint(path, 1, 32, 128, hidden, {0: (wl.ranks, wl.v_rank)}, seed=seed + 1)
+        w = ck.load_fused_checkpoint(path, 1, 32, 128, dtype=torch.bfloat16, kv_quant=True).layers[0]
+    ops = ck.layer_operands(w, 32, dev, torch.bfloat16)
+    from starkv_serve.kernels.paged_decode import cos_sin_for_kernel
+    cs = cos_sin_for_kernel(wl.cos_sin_cache)
+    g = torch.Generator(device=dev).manual_seed(seed + 2)
+    hid = torch.randn(steps_per_pass, n_req, hidden, generator=g, device=dev).to(torch.bfloat16)
+    qs = torch.randn(steps_per_pass, n_req, 32, 128, generator=g, device=dev).to(torch.bfloat16)
+    rows = torch.arange(n_req, device=dev)
+    slots_all, lens_all = [], []
+    for st in range(steps_per_pass):
+        pos = context - steps_per_pass + st
+        slots_all.append(wl.block_table[rows, pos // 16].long() * 16 + pos % 16)
+        lens_all.append(torch.full((n_req,), pos + 1, dtype=torch.int32, device=dev))
+
+    def step(i):
+        st = i % steps_per_pass
+        write_kv(hid[st], ops.kv_down, wl.kv_cache, slots_all[st], ops.k_width, row=ops.row, k_ranks=ops.k_ranks,
+                 k_offsets=ops.k_head_offsets, k_nouts=ops.k_nouts)
+        return paged_quant_decode(qs[st], wl.kv_cache, wl.block_table, lens_all[st], context, ops.row, ops.k_up,
+                                  ops.head_of_lane, ops.k_tiles, ops.v_up_by_q, cs, wl.scale)
+
+    mean, med = time_events(step, steps_per_pass * passes, steps_per_pass * warmup_passes)
+    tok = sum(context - steps_per_pass + st + 1 for st in range(steps_per_pass)) * n_req / steps_per_pass
+    dec_bytes = tok * ops.row.nbytes + n_req * 32 * 128 * 4 + ops.k_up.numel() * 2 + ops.v_up_by_q.numel() * 2
+    wr_bytes = ops.kv_down.numel() * 2 + n_req * hidden * 2 + n_req * ops.row.nbytes
+    b = dec_bytes + wr_bytes
+    return dict(requests=n_req, context=context, steps=steps_per_pass * passes, us_per_step=round(mean * 1e3, 2),
+                us_per_step_median=round(med * 1e3, 2), bytes_per_step=int(b),
+                GBps=round(b / (med * 1e-3) / 1e9, 1), hbm_frac=round(b / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                k_width=ops.k_width, v_rank=ops.v_rank,
+                step="fused write (16 tokens: kv_down GEMM, quantize, scatter) + 3.2-bit decode, span 32768")
 
 
 def bench_stock(n, context, steps, warmup, num_heads=32):
@@ -127,7 +225,8 @@ def bench_stock(n, context, steps, warmup, num_heads=32):
     "stock" attention: torch's fused SDPA (flash or memory-efficient kernels only,
     never the unfused math path) over contiguous K/V [n, H, context, 128]. Stock
     paged attention reads the same K/V bytes through a block table, so this
-    contiguous read is the more favourable case for the comparator."""
+    contiguous read is the more favourable case for the comparator. Also the bound
+    of any such kernel: its K/V bytes at 100 % of HBM peak."""
     import torch
     import torch.nn.functional as F
     from torch.nn.attention import SDPBackend, sdpa_kernel
@@ -135,23 +234,18 @@ def bench_stock(n, context, steps, warmup, num_heads=32):
     q = torch.randn(n, num_heads, 1, 128, generator=g, device="cuda").to(torch.bfloat16)
     k = torch.randn(n, num_heads, context, 128, generator=g, device="cuda").to(torch.bfloat16)
     v = torch.randn(n, num_heads, context, 128, generator=g, device="cuda").to(torch.bfloat16)
+    b = 2 * k.numel() * 2 + 2 * q.numel() * 2
+    res = dict(bytes_per_step=int(b), hbm_bound_us=round(b / (HBM_PEAK_GBS * 1e9) * 1e6, 1))
     try:
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-            fn = lambda: F.scaled_dot_product_attention(q, k, v)
-            warm_up(lambda i: fn(), warmup)
-            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record()
-            for _ in range(steps):
-                fn()
-            stop.record()
-            torch.cuda.synchronize()
+            mean, med = time_events(lambda i: F.scaled_dot_product_attention(q, k, v), steps, warmup)
     except RuntimeError as e:  # no fused kernel for this shape/device
-        return dict(error=str(e)[:200])
-    ms = start.elapsed_time(stop) / steps
-    b = 2 * k.numel() * 2 + 2 * q.numel() * 2
-    return dict(us_per_step=round(ms * 1e3, 2), GBps=round(b / (ms * 1e-3) / 1e9, 1),
-                hbm_frac=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), bytes_per_step=int(b),
-                kernel="torch SDPA (flash / memory-efficient), contiguous bf16 K/V, no paging")
+        res["error"] = str(e)[:200]
+        return res
+    res.update(us_per_step=round(mean * 1e3, 2), us_per_step_median=round(med * 1e3, 2),
+               GBps=round(b / (med * 1e-3) / 1e9, 1), hbm_frac=round(b / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+               kernel="torch SDPA (flash / memory-efficient), contiguous bf16 K/V, no paging")
+    return res
 
 
 def bench_write(n, quant, steps, warmup, seed=1004, layers=24, hidden=4096, num_heads=32, v_rank=64):
@@ -181,7 +275,7 @@ def bench_write(n, quant, steps, warmup, seed=1004, layers=24, hidden=4096, num_
         nouts, _, _ = k_tables(ranks, dev)
         cache = torch.zeros(nb, 16, row.nbytes, dtype=torch.uint8, device=dev)
         row_bytes = row.nbytes
-        fused = lambda i: write_kv(x, kv_down[i % layers], cache, slots, k_width, row=row, k_ranks=k_ranks,
+        fused = lambda i: write_kv(x, kv_down[i % layers], cache, slots, k_width, row=row, k_ranks=k_ranks,  # noqa: E731
                                    k_offsets=offsets, k_nouts=nouts)
 
         def unfused(i):
@@ -190,26 +284,17 @@ def bench_write(n, quant, steps, warmup, seed=1004, layers=24, hidden=4096, num_
     else:
         cache = torch.zeros(nb, 16, width, dtype=torch.bfloat16, device=dev)
         row_bytes = 2 * width
-        fused = lambda i: write_kv(x, kv_down[i % layers], cache, slots, k_width)
+        fused = lambda i: write_kv(x, kv_down[i % layers], cache, slots, k_width)  # noqa: E731
 
         def unfused(i):
             c = F.linear(x, kv_down[i % layers])
             write_codes(c[:, :k_width], c[:, k_width:], cache, slots)
 
-    def timed(fn):
-        warm_up(fn, warmup)
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for i in range(steps):
-            fn(i)
-        b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / steps * 1e3
-
-    fu, un = timed(fused), timed(unfused)
+    fu = time_events(fused, steps, warmup)[1] * 1e3
+    un = time_events(unfused, steps, warmup)[1] * 1e3
     by = width * hidden * 2 + n * hidden * 2 + n * row_bytes + n * 8
     return dict(tokens=n, cache="3.2-bit" if quant else "bf16", hidden=hidden, k_width=k_width, v_rank=v_rank,
-                fused_us=round(fu, 2), unfused_us=round(un, 2), bytes_per_step=by,
+                fused_us_median=round(fu, 2), unfused_us_median=round(un, 2), bytes_per_step=by,
                 GBps=round(by / (fu * 1e-6) / 1e9, 1), hbm_frac=round(by / (fu * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
 
 
@@ -236,68 +321,95 @@ def copy_probe(gib, reps):
     print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "reps": reps}), flush=True)
 
 
-def summarize(wl, ms, kern):
-    b = wl.bytes_per_step()
-    f = wl.flops_per_step()
-    return dict(us_per_step=round(ms * 1e3, 2), decode_kernel_us=round(kern * 1e3, 2),
-                GBps=round(b / (ms * 1e-3) / 1e9, 1), kernel_GBps=round(b / (kern * 1e-3) / 1e9, 1),
-                hbm_frac=round(b / (kern * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                mfma_frac=round(f / (kern * 1e-3) / 1e12 / MFMA_PEAK_F16_TFLOPS, 4),
-                bytes_per_step=int(b), flops_per_step=int(f), tokens=wl.tokens, k_width=wl.k_width,
-                v_rank=wl.v_rank)
+# ---------------------------------------------------------------------------
+# CPU baseline: the reference's math in fp32 PyTorch on this host (oracle/torch_ref.py)
+# ---------------------------------------------------------------------------
 
-
-def cpu_baseline(wl, budget_s=12.0):
-    """The float64 oracle (numpy) on whole requests of the workload until ~budget_s."""
-    import numpy as np
-    import torch
-    from threadpoolctl import threadpool_info
-
-    from oracle import ref
-    cores = len(os.sched_getaffinity(0))
-    blas = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
-    q = wl.query.float().cpu().numpy()
-    bt = wl.block_table.cpu().numpy()
-    U = wl.k_up.float().cpu().numpy()
-    vq = wl.v_up_by_q.float().cpu().numpy()
-    cs = wl.cos_sin_cache.float().cpu().numpy()
-    row_bytes = (wl.k_width + wl.v_rank) * wl.kv_cache.element_size()
-    done_tokens, done_bytes, t_total, reqs = 0, 0, 0.0, 0
-    for b in range(wl.n):
-        L = int(wl.lengths[b])
-        pages = (L + 15) // 16
-        blocks = torch.from_numpy(bt[b, :pages]).long().to(wl.kv_cache.device)
-        rows = wl.kv_cache[blocks].float().cpu().numpy()         # [pages, 16, width] of this request
-        local_bt = np.arange(pages, dtype=np.int32)[None, :]
+def _cpu_median(fn, runs=5):
+    fn()  # warm-up
+    t = []
+    for _ in range(runs):
         t0 = time.perf_counter()
-        ref.lowrank_decode(q[b:b + 1], rows, local_bt, [L], wl.max_seq_len, U, wl.ranks,
-                           wl.k_head_offsets.tolist(), wl.k_width, vq, cs, wl.scale)
-        t_total += time.perf_counter() - t0
-        done_tokens += L
-        done_bytes += L * row_bytes
-        reqs += 1
-        if t_total >= budget_s:
-            break
-    return dict(value=round(done_bytes / t_total / 1e9, 3), unit="GB/s", cores=blas[0] if blas else cores,
-                kind="port",
-                sample=f"float64 numpy oracle (oracle/ref.py lowrank_decode) on {reqs} of the {wl.n} requests "
-                       f"({done_tokens} tokens, {t_total:.1f} s), GB/s of cache rows attended; "
-                       f"host affinity {cores} cores")
+        fn()
+        t.append(time.perf_counter() - t0)
+    return statistics.median(t)
+
+
+def _cpu_subset(wl, idx):
+    """The workload restricted to requests idx, on the CPU (the cache whole)."""
+    from starkv_serve import workloads as W
+    sub = W.Workload(**{**wl.__dict__})
+    for k in ("query", "block_table", "seq_lens"):
+        setattr(sub, k, getattr(wl, k)[idx].cpu())
+    for k in ("kv_cache", "k_up", "v_up_by_q", "cos_sin_cache"):
+        setattr(sub, k, getattr(wl, k).cpu())
+    sub.lengths = [wl.lengths[i] for i in idx]
+    return sub
+
+
+def cpu_decode_run(wl):
+    """A callable running the fp32 restatement of the workload's decode on the CPU."""
+    from oracle import ref, torch_ref
+    if wl.quant:
+        lay = ref.row_layout(wl.k_width, len(wl.ranks), wl.v_rank)
+        return lambda: torch_ref.quant_decode(wl.query, wl.kv_cache, wl.block_table, wl.seq_lens, wl.max_seq_len,
+                                              lay, wl.ranks, wl.k_up, wl.v_up_by_q, wl.cos_sin_cache, wl.scale)
+    return lambda: torch_ref.lowrank_decode(wl.query, wl.kv_cache, wl.block_table, wl.seq_lens, wl.max_seq_len,
+                                            wl.k_up, wl.ranks, wl.k_head_offsets.tolist(), wl.k_width,
+                                            wl.v_up_by_q, wl.cos_sin_cache, wl.scale)
+
+
+def cpu_measure(wl, idx, label):
+    import torch
+    sub = _cpu_subset(wl, idx)
+    t = _cpu_median(cpu_decode_run(sub))
+    b = sub.bytes_per_step()
+    return dict(value=round(b / t / 1e9, 3), unit="GB/s", seconds_median=round(t, 4), requests=len(idx),
+                tokens=sub.tokens, threads=torch.get_num_threads(),
+                sample=f"{label}: fp32 PyTorch restatement (oracle/torch_ref.py) on {len(idx)} of the {wl.n} "
+                       f"requests ({sub.tokens} tokens), median of 5 runs after 1, GB/s of the same "
+                       f"algorithmic bytes")
+
+
+def cpu_c3_step(n_req=16, context=32768, decode_requests=2, hidden=4096, seed=3003):
+    """One config-3 step on the CPU: the 16-token cache write (GEMM, quantize, pack,
+    scatter) and the decode of `decode_requests` of the 16 requests."""
+    import torch
+    from oracle import ref, torch_ref
+    from starkv_serve import workloads as W
+    wl = W.make_quant([context] * decode_requests, num_heads=32, v_rank=64, seed=seed, device="cpu")
+    wl.k_codes = wl.v_codes = None
+    lay = ref.row_layout(wl.k_width, 32, wl.v_rank)
+    g = torch.Generator().manual_seed(seed + 1)
+    kv_down = (torch.randn(wl.k_width + wl.v_rank, hidden, generator=g) * hidden ** -0.5).to(torch.bfloat16)
+    hid = torch.randn(n_req, hidden, generator=g).to(torch.bfloat16)
+    slots = torch.arange(n_req, dtype=torch.long)
+    dec = cpu_decode_run(wl)
+
+    def step():
+        torch_ref.write_step(hid, kv_down, wl.k_width, lay, wl.ranks, wl.kv_cache, slots)
+        dec()
+
+    t = _cpu_median(step)
+    per_req = context * wl.row.nbytes
+    return dict(seconds_median=round(t, 3), threads=torch.get_num_threads(),
+                GBps=round((decode_requests * per_req + kv_down.numel() * 2) / t / 1e9, 3),
+                sample=f"16-token write + decode of {decode_requests} of the 16 requests at {context} tokens, "
+                       f"median of 5 runs after 1; the full step would decode 16")
 
 
 def main():
     global MIN_WARMUP_MS
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=30)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--min-warmup-ms", type=float, default=MIN_WARMUP_MS,
                     help="each workload's warmup continues until this many ms of back-to-back calls")
-    ap.add_argument("--no-extra", action="store_true", help="skip the 3.2-bit and ragged configurations")
+    ap.add_argument("--no-extra", action="store_true", help="skip every workload but the headline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["bf16", "quant", "write", "short"], default=None,
-                    help="profile runs: time one workload only (bs64 x 8192; short: 64 requests x 16 "
-                         "tokens, bf16) and print its summary")
+    ap.add_argument("--only", choices=["bf16", "quant", "write", "short", "wide", "wide_quant", "c0", "c3"],
+                    default=None, help="profile runs: time one workload only and print its summary")
     ap.add_argument("--copy-probe", type=float, default=0.0, metavar="GIB",
                     help="profile runs: only copy GIB GiB device to device 5 times (counter scaling)")
     args = ap.parse_args()
@@ -314,71 +426,88 @@ def main():
         copy_probe(args.copy_probe, 5)
         return
 
+    from starkv_serve import workloads as W
     lengths = [8192] * 64
-    if args.only == "write":
-        for n_tok in (16, 64):
-            for quant in (True, False):
-                print(json.dumps(bench_write(n_tok, quant, args.steps, args.warmup)), flush=True)
-        return
-    if args.only == "short":
-        ws_, mss, ks = bench_lowrank([16] * 64, args.steps, args.warmup, seed=1005)
-        print(json.dumps(summarize(ws_, mss, ks)), flush=True)
-        return
-    if args.only == "quant":
-        wq, msq, kq = bench_quant(lengths, args.steps, args.warmup, seed=1003, copies=3)
-        print(json.dumps(summarize(wq, msq, kq)), flush=True)
+    K, Wm = args.steps, args.warmup
+    only = {
+        "write": lambda: [bench_write(n, q, K, Wm) for n in (16, 64) for q in (True, False)],
+        "short": lambda: summarize(*bench_lowrank([16] * 64, K, Wm, seed=1005)),
+        "quant": lambda: summarize(*bench_quant(lengths, K, Wm, seed=1003, copies=3)),
+        "wide": lambda: summarize(*bench_lowrank(lengths, K, Wm, seed=1007, v_rank=1280, ranks=RANKS_880)),
+        "wide_quant": lambda: summarize(*bench_quant(lengths, K, Wm, seed=1008, copies=3, v_rank=1290,
+                                                     ranks=RANKS_880)),
+        "c0": lambda: summarize(*bench_lowrank([4096], K, Wm, seed=1000)),
+        "c3": lambda: bench_c3(32, 2),
+    }
+    if args.only in only:
+        print(json.dumps(only[args.only]()), flush=True)
         return
     log("headline: bf16 low-rank, 64 x 8192")
-    wl, ms, kern = bench_lowrank(lengths, args.steps, args.warmup, seed=1001)
-    head = summarize(wl, ms, kern)
+    wl, th = bench_lowrank(lengths, K, Wm, seed=1001)
+    head = summarize(wl, th)
     log(json.dumps(head))
     if args.only == "bf16":
         print(json.dumps(head), flush=True)
         return
 
     extra = {}
+
+    def run(key, what, fn):
+        log(what)
+        extra[key] = fn()
+        log(json.dumps(extra[key]))
+        torch.cuda.empty_cache()
+
     if not args.no_extra:
-        from starkv_serve import workloads as W
-        log("3.2-bit, 64 x 8192 (3 rotating caches)")
-        wq, msq, kq = bench_quant(lengths, args.steps, args.warmup, seed=1003, copies=3)
-        extra["quant_bs64x8k"] = summarize(wq, msq, kq)
+        run("quant_bs64x8k", "3.2-bit, 64 x 8192 (3 rotating caches)", only["quant"])
         extra["quant_bs64x8k"]["hbm_traffic_bytes"] = measured_traffic("quant_bs64x8k")
-        log(json.dumps(extra["quant_bs64x8k"]))
-        del wq
-        torch.cuda.empty_cache()
-        log("bf16 low-rank, 64 requests, lengths U[1024, 8192]")
-        w1, ms1, k1 = bench_lowrank(W.ragged_lengths(1001), args.steps, args.warmup, seed=1001)
-        extra["lowrank_bs64_ragged_1k_8k"] = summarize(w1, ms1, k1)
-        log(json.dumps(extra["lowrank_bs64_ragged_1k_8k"]))
-        del w1
-        torch.cuda.empty_cache()
-        log("3.2-bit, 64 requests, lengths U[1024, 8192] (3 rotating caches)")
-        w2, ms2, k2 = bench_quant(W.ragged_lengths(1002), args.steps, args.warmup, seed=1002, copies=3)
-        extra["quant_bs64_ragged_1k_8k"] = summarize(w2, ms2, k2)
-        log(json.dumps(extra["quant_bs64_ragged_1k_8k"]))
-        del w2
-        torch.cuda.empty_cache()
+        run("lowrank_bs64_ragged_1k_8k", "bf16 low-rank, 64 requests, lengths U[1024, 8192] (config 1)",
+            lambda: summarize(*bench_lowrank(W.ragged_lengths(1001), K, Wm, seed=1001)))
+        run("quant_bs64_ragged_1k_8k", "3.2-bit, 64 requests, lengths U[1024, 8192] (config 2, 3 rotating caches)",
+            lambda: summarize(*bench_quant(W.ragged_lengths(1002), K, Wm, seed=1002, copies=3)))
+        run("lowrank_b1x4096", "bf16 low-rank, 1 x 4096 (config 0)", only["c0"])
+        run("quant_bs16x32k_write_decode", "3.2-bit, 16 x 32768, fused write + decode per step (config 3)",
+            only["c3"])
+        run("lowrank_bs64x8k_w880_v1280", "bf16 low-rank, 64 x 8192, K width 880, V rank 1280 (two-pass)",
+            only["wide"])
+        run("quant_bs64x8k_w880_v1290", "3.2-bit, 64 x 8192, K width 880, V rank 1290 (two-pass, 3 caches)",
+            only["wide_quant"])
         for n_tok in (16, 64):
             for quant in (True, False):
-                key = f"write_{'quant' if quant else 'bf16'}_n{n_tok}"
-                log(f"cache write, {n_tok} tokens, {'3.2-bit' if quant else 'bf16'} (fused vs unfused)")
-                extra[key] = bench_write(n_tok, quant, args.steps, args.warmup)
-                log(json.dumps(extra[key]))
-        torch.cuda.empty_cache()
+                run(f"write_{'quant' if quant else 'bf16'}_n{n_tok}",
+                    f"cache write, {n_tok} tokens, {'3.2-bit' if quant else 'bf16'} (fused vs unfused)",
+                    lambda: bench_write(n_tok, quant, K, Wm))
         log("uncompressed bf16 attention (torch fused SDPA), 64 x 8192")
-        stock = bench_stock(64, 8192, args.steps, args.warmup)
-        if "us_per_step" in stock:
-            stock["starkv_bf16_speedup"] = round(stock["us_per_step"] / head["us_per_step"], 2)
-            stock["starkv_quant_speedup"] = round(stock["us_per_step"] / extra["quant_bs64x8k"]["us_per_step"], 2)
-        extra["stock_bf16_sdpa_bs64x8k"] = stock
+        stock = bench_stock(64, 8192, K, Wm)
+        for key, name in (("bf16", head), ("quant", extra["quant_bs64x8k"])):
+            if "us_per_step" in stock:
+                stock[f"starkv_{key}_speedup_vs_sdpa"] = round(stock["us_per_step"] / name["us_per_step"], 2)
+            stock[f"starkv_{key}_speedup_vs_hbm_bound"] = round(stock["hbm_bound_us"] / name["us_per_step"], 2)
+        extra["stock_bf16_bs64x8k"] = stock
         log(json.dumps(stock))
         torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
-        log("cpu baseline")
-        cpu = cpu_baseline(wl)
+        torch.set_num_threads(len(os.sched_getaffinity(0)))
+        log(f"cpu baseline ({torch.get_num_threads()} threads)")
+        cpu = cpu_measure(wl, list(range(0, 64, 4)), "bf16 64 x 8192")
+        cpu.update(cores=torch.get_num_threads(), kind="port")
         log(json.dumps(cpu))
+        if not args.no_extra:
+            cpu_extra = {}
+            w0 = W.make_lowrank([4096], num_heads=32, seed=1000)
+            cpu_extra["lowrank_b1x4096"] = cpu_measure(w0, [0], "config 0")
+            w1 = W.make_lowrank(W.ragged_lengths(1001), num_heads=32, seed=1001, poison=False)
+            cpu_extra["lowrank_bs64_ragged_1k_8k"] = cpu_measure(w1, list(range(0, 64, 4)), "config 1")
+            del w1
+            w2 = W.make_quant(W.ragged_lengths(1002)[::4], num_heads=32, seed=1002, device="cpu")
+            w2.k_codes = w2.v_codes = None
+            cpu_extra["quant_bs64_ragged_1k_8k"] = cpu_measure(w2, list(range(16)), "config 2 (16 of its 64 lengths)")
+            del w2
+            cpu_extra["quant_bs16x32k_write_decode"] = cpu_c3_step()
+            extra["cpu_fp32_torch"] = cpu_extra
+            log(json.dumps(cpu_extra))
 
     out = {
         "metric": METRIC,
@@ -387,7 +516,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
+        "ms_per_step": round(th["ms"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -396,10 +525,11 @@ def main():
         "config": {"workload": "bf16 low-rank paged decode, one layer, batch 64 x context 8192",
                    "batch": 64, "context": 8192, "num_heads": 32, "head_dim": 128, "page_size": 16,
                    "k_width": wl.k_width, "v_rank": wl.v_rank, "k_ranks": "uniform {16,32,48,64} per head",
-                   "decode_us": head["us_per_step"], "min_warmup_ms": MIN_WARMUP_MS},
+                   "decode_us": head["us_per_step"], "call_us_median": head["call_us_median"],
+                   "min_warmup_ms": MIN_WARMUP_MS},
         "roofline": {"bound": "hbm", "achieved": head["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": head["hbm_frac"], "traffic": measured_traffic("bf16_bs64x8k"),
-                     "kernel": "lowrank_kernel (bf16 decode)", "kernel_us": head["decode_kernel_us"],
+                     "kernel": "lowrank_kernel (bf16 decode)", "kernel_us_median": head["decode_kernel_us"],
                      "bytes_per_launch": head["bytes_per_step"], "mfma_frac_fp16": head["mfma_frac"]},
         "cpu_baseline": cpu,
         "extra": extra,

@@ -240,15 +240,19 @@ int starkv_quant_decode(void *stream, const void *query, int64_t q_s0, int64_t q
                         void *workspace, size_t workspace_bytes, int grid);
 
 /*
- * Timing of the decode kernel alone, for benchmarks (no counterpart in the
- * reference, whose benchmark reads profiler traces instead, bench_serving.py:71-115).
- * starkv_profile_begin arms up to max_calls event pairs; each following decode call
- * records one pair around its decode kernel on its stream. starkv_profile_end
- * synchronizes those events, returns the summed milliseconds and the number of
- * timed calls, and disarms. Not for use under graph capture.
+ * Timing for benchmarks (no counterpart in the reference, whose benchmark reads profiler
+ * traces instead, bench_serving.py:71-115). starkv_profile_begin arms up to max_calls
+ * event pairs; each following decode call records one pair on its stream, around its
+ * decode kernels (mode 0: the one-pass kernel, or the logits and P @ V passes) or around
+ * the whole call (mode 1: from the prep launch to the merge). The events are created
+ * without the system-scope fence. starkv_profile_end synchronizes them, returns the
+ * summed milliseconds and the number of timed calls, and disarms; starkv_profile_times
+ * then copies up to max per-call milliseconds and returns how many. Not for use under
+ * graph capture.
  */
-int starkv_profile_begin(int max_calls);
+int starkv_profile_begin(int max_calls, int mode);
 int starkv_profile_end(double *decode_ms_sum, int *calls);
+int starkv_profile_times(double *ms, int max);
 
 #ifdef __cplusplus
 }

@@ -619,12 +619,15 @@ static int grid_for(int n, int max_seq_len) {
     return want < 1 ? 1 : (int)want;
 }
 
-// Optional timing of the decode kernel alone (benchmarks): when armed, each call records
-// a HIP event pair around the decode launch on the caller's stream.
+// Optional timing for benchmarks: when armed, each call records a HIP event pair on the
+// caller's stream, around its decode kernels (mode 0: the one-pass kernel, or the logits
+// and P @ V passes) or around the whole call (mode 1: prep to merge).
 struct DecodeProfile {
     bool on = false;
+    int mode = 0;
     int used = 0;
     std::vector<hipEvent_t> ev;
+    std::vector<double> ms;  // per-call durations of the last profile_end
 };
 static DecodeProfile g_prof;
 
@@ -835,6 +838,8 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     p.ws_lg = wl.lg; p.lcap = lcap;
     p.ws_o = wl.o; p.acc_ld = wl.ld;
 
+    const bool timed = g_prof.on && 2 * g_prof.used + 1 < (int)g_prof.ev.size();
+    if (timed && g_prof.mode == 1) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
     PrepArgs pa;
     pa.seq_lens = a.seq_lens; pa.n = a.n; pa.max_seq_len = a.max_seq_len; pa.grid = a.grid;
     pa.Hq = a.Hq; pa.Hkv = a.Hkv; pa.TT = TT; pa.k_rows = p.k_width;
@@ -848,8 +853,7 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     const int prep_grid = 1 + pa.tile_pairs * ((a.n + PREP_REQ - 1) / PREP_REQ);
     hipLaunchKernelGGL(prep_kernel, dim3(prep_grid), dim3(PREP_THR), 0, stream, pa);
     SKV_HIP(hipGetLastError());
-    const bool timed = g_prof.on && 2 * g_prof.used + 1 < (int)g_prof.ev.size();
-    if (timed) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
+    if (timed && g_prof.mode == 0) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
     int rc;
     if (two) {
         rc = fmt == FMT_Q4 ? launch_quant(p, 0, a.grid, stream) : launch_lowrank(p, fmt, 0, a.grid, stream);
@@ -861,21 +865,21 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     }
     if (rc) return rc;
     SKV_HIP(hipGetLastError());
-    if (timed) {
-        SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used + 1], stream));
-        ++g_prof.used;
-    }
+    if (timed && g_prof.mode == 0) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used + 1], stream));
     if (two) {
         rc = launch_merge_wide(p, a.vu_dt, a.vup, a.vu_s0, a.vu_s1, a.out, a.o_s0, a.o_s1, a.out_dt, stream);
-        if (rc) return rc;
-        SKV_HIP(hipGetLastError());
-        return STARKV_OK;
+    } else {
+        const dim3 mgrid((a.n + MERGE_REQ - 1) / MERGE_REQ, a.Hq);
+        const size_t mlds = merge_lds_bytes(a.v_rank, a.vu_dt);
+        rc = a.vu_dt == STARKV_BF16  ? launch_merge<uint16_t>(mgrid, mlds, stream, p, wl, a)
+             : a.vu_dt == STARKV_F16 ? launch_merge<_Float16>(mgrid, mlds, stream, p, wl, a)
+                                     : launch_merge<float>(mgrid, mlds, stream, p, wl, a);
     }
-    const dim3 mgrid((a.n + MERGE_REQ - 1) / MERGE_REQ, a.Hq);
-    const size_t mlds = merge_lds_bytes(a.v_rank, a.vu_dt);
-    if (a.vu_dt == STARKV_BF16) return launch_merge<uint16_t>(mgrid, mlds, stream, p, wl, a);
-    if (a.vu_dt == STARKV_F16) return launch_merge<_Float16>(mgrid, mlds, stream, p, wl, a);
-    return launch_merge<float>(mgrid, mlds, stream, p, wl, a);
+    if (rc) return rc;
+    SKV_HIP(hipGetLastError());
+    if (timed && g_prof.mode == 1) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used + 1], stream));
+    if (timed) ++g_prof.used;
+    return STARKV_OK;
 }
 
 // Workspace of starkv_lowrank_decode_noalloc: one array per device, held until the
@@ -908,9 +912,11 @@ extern "C" {
 
 int starkv_decode_grid(int n, int max_seq_len) { return grid_for(n, max_seq_len); }
 
-int starkv_profile_begin(int max_calls) {
+int starkv_profile_begin(int max_calls, int mode) {
     clear_error();
     SKV_CHECK(max_calls >= 1 && max_calls <= 100000, "profile_begin: max_calls %d", max_calls);
+    SKV_CHECK(mode == 0 || mode == 1, "profile_begin: mode %d (0 decode kernels, 1 whole call)", mode);
+    g_prof.mode = mode;
     for (hipEvent_t e : g_prof.ev) (void)hipEventDestroy(e);
     g_prof.ev.assign(2 * (size_t)max_calls, nullptr);
     // Timing-only events: without the system-scope fence a record does not write back
@@ -925,16 +931,26 @@ int starkv_profile_end(double* decode_ms_sum, int* calls) {
     clear_error();
     g_prof.on = false;
     double sum = 0.0;
+    g_prof.ms.assign(g_prof.used, 0.0);
     for (int i = 0; i < g_prof.used; ++i) {
         SKV_HIP(hipEventSynchronize(g_prof.ev[2 * i + 1]));
         float ms = 0.f;
         SKV_HIP(hipEventElapsedTime(&ms, g_prof.ev[2 * i], g_prof.ev[2 * i + 1]));
+        g_prof.ms[i] = ms;
         sum += ms;
     }
     if (decode_ms_sum) *decode_ms_sum = sum;
     if (calls) *calls = g_prof.used;
     g_prof.used = 0;
     return STARKV_OK;
+}
+
+int starkv_profile_times(double* ms, int max) {
+    clear_error();
+    SKV_CHECK(ms != nullptr && max >= 0, "profile_times: null output");
+    const int k = std::min(max, (int)g_prof.ms.size());
+    for (int i = 0; i < k; ++i) ms[i] = g_prof.ms[i];
+    return k;
 }
 
 size_t starkv_decode_workspace_bytes(int cache_kind, int n, int num_heads, int num_kv_heads, int k_width, int v_rank,

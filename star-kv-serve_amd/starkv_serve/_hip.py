@@ -34,8 +34,9 @@ SIGNATURES = {
     "starkv_write_kv": (_I, [_P, _P, _I64, _P, _I64, _I, _I, _I, _I, _I, _P, _I64, _I64, _I, _I, _I64, _P, _I,
                              _I, _P, _P, _P, _I, _P, _I64, _P, _SZ]),
     "starkv_decode_grid": (_I, [_I, _I]),
-    "starkv_profile_begin": (_I, [_I]),
+    "starkv_profile_begin": (_I, [_I, _I]),
     "starkv_profile_end": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
+    "starkv_profile_times": (_I, [ctypes.POINTER(ctypes.c_double), _I]),
     "starkv_decode_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I, _I, _I]),
     "starkv_decode_two_pass": (_I, [_I, _I, _I, _I]),
     "starkv_decode_set_path": (_I, [_I]),
@@ -108,17 +109,20 @@ def set_decode_path(mode: int) -> int:
     return prev
 
 
-def profile_begin(max_calls: int) -> None:
-    """Arm event timing of the decode kernel for the next `max_calls` decode calls."""
-    check(lib().starkv_profile_begin(int(max_calls)), "profile_begin")
+def profile_begin(max_calls: int, whole_call: bool = False) -> None:
+    """Arm event timing for the next `max_calls` decode calls: of their decode kernels, or
+    of the whole call (prep to merge) with whole_call."""
+    check(lib().starkv_profile_begin(int(max_calls), 1 if whole_call else 0), "profile_begin")
 
 
-def profile_end() -> tuple:
-    """(summed decode-kernel milliseconds, timed calls); disarms the timing."""
+def profile_end() -> list:
+    """Per-call milliseconds of the timed calls; disarms the timing."""
     ms = ctypes.c_double(0.0)
     calls = ctypes.c_int(0)
     check(lib().starkv_profile_end(ctypes.byref(ms), ctypes.byref(calls)), "profile_end")
-    return ms.value, calls.value
+    buf = (ctypes.c_double * max(calls.value, 1))()
+    k = lib().starkv_profile_times(buf, calls.value)
+    return [buf[i] for i in range(k)]
 
 
 def require_cuda(*ts: torch.Tensor) -> None:
