@@ -240,6 +240,25 @@ int starkv_quant_decode(void *stream, const void *query, int64_t q_s0, int64_t q
                         void *workspace, size_t workspace_bytes, int grid);
 
 /*
+ * Uncompressed paged decode attention over bf16/fp16 K and V caches
+ * [num_blocks, block_size, num_kv_heads, 128] (element strides c_s0, c_s1, c_s2, last
+ * dimension contiguous): out[b, h] = softmax(scale q[b, h] . K[b, :L]) V[b, :L], L =
+ * min(seq_lens[b], max_seq_len) (NaN rows for L = 0). It stands in for the stock
+ * attention backend the reference runs its uncompressed layers on
+ * (starkv_serve/model.py:77-81 builds vLLM's LlamaAttention for them; the reference has
+ * no code of its own for it), and is the stock bf16 comparator of the benchmarks.
+ * num_heads / num_kv_heads in {1, 2, 4, 8}; block_size 16 * 2^s; workspace >=
+ * starkv_stock_decode_workspace_bytes(n, num_heads, num_kv_heads, max_seq_len) bytes.
+ */
+size_t starkv_stock_decode_workspace_bytes(int n, int num_heads, int num_kv_heads, int max_seq_len);
+int starkv_stock_decode(void *stream, const void *query, int64_t q_s0, int64_t q_s1, int q_dtype,
+                        const void *k_cache, const void *v_cache, int64_t c_s0, int64_t c_s1, int64_t c_s2,
+                        int cache_dtype, int block_size, const int32_t *block_table, int64_t bt_s0,
+                        int64_t bt_s1, const int32_t *seq_lens, int n, int num_heads, int num_kv_heads,
+                        int max_seq_len, float scale, void *out, int64_t o_s0, int64_t o_s1, int out_dtype,
+                        void *workspace, size_t workspace_bytes);
+
+/*
  * Timing for benchmarks (no counterpart in the reference, whose benchmark reads profiler
  * traces instead, bench_serving.py:71-115). starkv_profile_begin arms up to max_calls
  * event pairs; each following decode call records one pair on its stream, around its

@@ -223,6 +223,32 @@ class StarKVAttentionImpl:
         return write_kv(hidden, self.kv_down, cache, slot_mapping, self.k_width, row=self.row, k_ranks=self.k_ranks,
                         k_offsets=self.k_head_offsets, k_nouts=self.k_nouts, return_codes=return_codes)
 
+    def forward_from_hidden(self, query: torch.Tensor, hidden: torch.Tensor, kv_cache: torch.Tensor,
+                            attn_metadata: Optional[StarKVMetadata], output: torch.Tensor,
+                            in_full_graph: Optional[bool] = None) -> torch.Tensor:
+        """``forward`` with the codes' GEMM fused into the write: the layer's input
+        `hidden` [T, hidden_size] instead of `key` / `value` codes (model.py:71 + the
+        write of attention.py:179-188), then the same decode and prefill."""
+        if attn_metadata is None:  # profiling run
+            return output.fill_(0)
+        md = attn_metadata
+        n = md.num_actual_tokens
+        if md.num_prefills:
+            codes = self.write_from_hidden(hidden[:n], kv_cache, md.slot_mapping[:n], return_codes=True)
+            key, value = codes[:, :self.k_width], codes[:, self.k_width:]
+            query_lens = self._prefill_lens(md)
+        else:
+            self.write_from_hidden(hidden[:n], kv_cache, md.slot_mapping[:n])
+        Hq, Hd = self.num_heads, self.head_size
+        nd = md.num_decode_tokens
+        if nd:
+            self._decode(query[:nd].view(nd, Hq, Hd), self._cache(kv_cache), md, output[:nd].view(nd, Hq, Hd),
+                         in_full_graph)
+        if md.num_prefills:
+            self._dense_prefill(query_lens, query[nd:n].view(n - nd, Hq, Hd), key[nd:n], value[nd:n],
+                                output[nd:n].view(n - nd, Hq, Hd))
+        return output
+
     def _decode(self, q: torch.Tensor, cache: torch.Tensor, md: StarKVMetadata, out: torch.Tensor,
                 in_full_graph: Optional[bool]) -> None:
         nd = q.shape[0]
