@@ -298,6 +298,124 @@ def bench_write(n, quant, steps, warmup, seed=1004, layers=24, hidden=4096, num_
                 GBps=round(by / (fu * 1e-6) / 1e9, 1), hbm_frac=round(by / (fu * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
 
 
+def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, modes=("stock", "bf16", "quant")):
+    """Config 4: decode steps of a random-init Llama-2-7B-shaped model (32 layers, 32 heads
+    x 128, hidden 4096, MLP 11008, vocab 32000). STAR-KV modes keep layers 0, 1, 2 and 31
+    uncompressed and compress the others at the 0.75 ratio (K ranks, multiples of 16, keep
+    ~21.5 % of K; V rank, a multiple of 32, ~31.5 % of V: 880 and 1280 here), their factors
+    written to a fused checkpoint and read back with load_fused_checkpoint; "stock" keeps
+    every layer uncompressed. Sessions hold `context` tokens of synthetic cache rows (the
+    3.2-bit rows packed from random hidden states through the write path) and decode
+    `steps` tokens each, one token per session per step, eager. Concurrency 1 and the most
+    sessions whose caches fit in the GPU's free memory (less `reserve_gb`). Per mode and
+    concurrency: TPOT (median step), tok/s = sessions / TPOT, and attention per step (the
+    KV writes and attention of all 32 layers, timed on their own, as bench_serving.py:62-115
+    sums them)."""
+    import tempfile
+    import torch
+    from starkv_serve import checkpoint as ck
+    from starkv_serve import model as M
+    dev = torch.device("cuda", 0)
+    shape = M.LLAMA2_7B
+    g = torch.Generator().manual_seed(seed)
+    full = (0, 1, 2, shape.num_layers - 1)
+    comp = {li: (M.ranks_for_ratio(32, 128, 0.215, 16, g), M.v_rank_for_ratio(32, 128, 0.315, 32))
+            for li in range(shape.num_layers) if li not in full}
+    # Block-table rows cover every position a step writes: the context, then warm + steps tokens.
+    pages = (context + warm + steps + 15) // 16
+    assert context + warm + steps <= 16 * pages
+    res = dict(model="Llama-2-7B shape, random init", context=context, decode_steps=steps,
+               uncompressed_layers=list(full), k_width=sum(next(iter(comp.values()))[0]),
+               v_rank=next(iter(comp.values()))[1])
+
+    def run(model, n):
+        model.allocate_kv_cache(n * pages + 1)
+        gg = torch.Generator(device=dev).manual_seed(seed + n)
+        bt = (torch.randperm(n * pages, device=dev, generator=gg) + 1).to(torch.int32).view(n, pages)
+        for li, layer in enumerate(model.layers):
+            c = model.kv_caches[li]
+            if not layer.compressed:
+                c[0].normal_(generator=gg)
+                c[1].normal_(generator=gg)
+            elif layer.impl.row is None:
+                c.normal_(generator=gg)
+            else:  # valid 3.2-bit rows: session 0's context through the write path, copied to the others
+                pc = (context + 15) // 16
+                pos = torch.arange(context, device=dev)
+                slots = bt[0, pos // 16].long() * 16 + pos % 16
+                for a in range(0, context, 4096):
+                    hid = torch.randn(min(4096, context - a), shape.hidden_size, device=dev, generator=gg)
+                    layer.impl.write_from_hidden(hid.to(torch.bfloat16), c, slots[a:a + 4096])
+                for sess in range(1, n):
+                    c[bt[sess, :pc].long()] = c[bt[0, :pc].long()]
+        tokens = torch.randint(0, shape.vocab_size, (n,), device=dev, generator=gg)
+        torch.cuda.synchronize()
+        times = []
+        for t in range(warm + steps):
+            positions = torch.full((n,), context + t, device=dev, dtype=torch.long)
+            md = M.decode_metadata(bt, positions, 16, context + t + 1)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            tokens = model.decode_step(tokens, positions, md).argmax(-1)
+            b.record()
+            if t >= warm:
+                times.append((a, b))
+        torch.cuda.synchronize()
+        tpot = statistics.median([a.elapsed_time(b) for a, b in times])
+        positions = torch.full((n,), context + warm + steps - 1, device=dev, dtype=torch.long)
+        md = M.decode_metadata(bt, positions, 16, context + warm + steps)
+        hid = torch.randn(n, shape.hidden_size, device=dev, generator=gg).to(torch.bfloat16)
+        at = []
+        for r in range(6):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            model.attention_only(hid, positions, md)
+            b.record()
+            if r:
+                at.append((a, b))
+        torch.cuda.synchronize()
+        attn = statistics.median([a.elapsed_time(b) for a, b in at])
+        out = dict(sessions=n, tpot_ms=round(tpot, 3), tok_per_s=round(n / tpot * 1e3, 1),
+                   attention_us_per_step=round(attn * 1e3, 1),
+                   kv_cache_gb=round(n * pages * 16 * model.cache_bytes_per_token() / 1e9, 2))
+        model.kv_caches = []
+        torch.cuda.empty_cache()
+        return out
+
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "fused_weights.pt")
+        ck.write_fused_checkpoint(path, shape.num_layers, shape.num_kv_heads, shape.head_dim, shape.hidden_size,
+                                  comp, seed=seed)
+        for mode in modes:
+            try:
+                c = None if mode == "stock" else ck.load_fused_checkpoint(
+                    path, shape.num_layers, shape.num_kv_heads, shape.head_dim, dtype=torch.bfloat16,
+                    kv_quant=mode == "quant")
+                model = M.StarKVLlamaForCausalLM(shape, c, max_model_len=context + warm + steps + 16, device=dev,
+                                                 seed=seed + 1, stock=mode == "stock")
+                per_tok = model.cache_bytes_per_token()
+                free, _ = torch.cuda.mem_get_info()
+                n_max = max(1, int((free - reserve_gb * 1e9) // (pages * 16 * per_tok)))
+                r = dict(kv_bytes_per_token=per_tok)
+                for key, n in (("c1", 1), ("max_sessions", n_max)):
+                    log(f"config 4 {mode}: {n} sessions x {context}")
+                    r[key] = run(model, n)
+                    log(json.dumps(r[key]))
+                res[mode] = r
+                del model
+            except RuntimeError as e:  # e.g. out of memory: record it, keep the rest of the bench
+                res[mode] = dict(error=str(e)[:300])
+            torch.cuda.empty_cache()
+    st = res.get("stock", {})
+    for mode in ("bf16", "quant"):
+        r = res.get(mode, {})
+        for key in ("c1", "max_sessions"):
+            if key in r and key in st:
+                r[key]["tpot_speedup_vs_stock"] = round(st[key]["tpot_ms"] / r[key]["tpot_ms"], 3)
+                r[key]["throughput_gain_vs_stock"] = round(r[key]["tok_per_s"] / st[key]["tok_per_s"], 3)
+    return res
+
+
 def measured_traffic(key):
     """HBM bytes per launch for `key` from the committed counter summary, or None."""
     import re
@@ -408,7 +526,8 @@ def main():
                     help="each workload's warmup continues until this many ms of back-to-back calls")
     ap.add_argument("--no-extra", action="store_true", help="skip every workload but the headline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["bf16", "quant", "write", "short", "wide", "wide_quant", "c0", "c3"],
+    ap.add_argument("--only", choices=["bf16", "quant", "write", "short", "wide", "wide_quant", "c0", "c3",
+                                       "model"],
                     default=None, help="profile runs: time one workload only and print its summary")
     ap.add_argument("--copy-probe", type=float, default=0.0, metavar="GIB",
                     help="profile runs: only copy GIB GiB device to device 5 times (counter scaling)")
@@ -438,6 +557,7 @@ def main():
                                                      ranks=RANKS_880)),
         "c0": lambda: summarize(*bench_lowrank([4096], K, Wm, seed=1000)),
         "c3": lambda: bench_c3(32, 2),
+        "model": lambda: bench_model(),
     }
     if args.only in only:
         print(json.dumps(only[args.only]()), flush=True)
@@ -477,6 +597,7 @@ def main():
                 run(f"write_{'quant' if quant else 'bf16'}_n{n_tok}",
                     f"cache write, {n_tok} tokens, {'3.2-bit' if quant else 'bf16'} (fused vs unfused)",
                     lambda: bench_write(n_tok, quant, K, Wm))
+        run("model_llama2_7b_16k", "config 4: Llama-2-7B-shaped decode steps at 16K context", only["model"])
         log("uncompressed bf16 attention (torch fused SDPA), 64 x 8192")
         stock = bench_stock(64, 8192, K, Wm)
         for key, name in (("bf16", head), ("quant", extra["quant_bs64x8k"])):

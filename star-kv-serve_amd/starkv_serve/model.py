@@ -207,6 +207,9 @@ def decode_metadata(block_table: torch.Tensor, positions: torch.Tensor, block_si
     """A decode-only batch's metadata: request b's new token at positions[b] (slot from its
     block-table row), seq_lens = positions + 1."""
     n = positions.shape[0]
+    if max_seq_len > block_table.shape[1] * block_size:
+        raise ValueError(f"positions up to {max_seq_len - 1} need more than the block table's "
+                         f"{block_table.shape[1]} blocks of {block_size}")
     rows = torch.arange(n, device=positions.device)
     slots = block_table[rows, positions // block_size].long() * block_size + positions % block_size
     return StarKVMetadata(num_actual_tokens=n, num_decodes=n, num_decode_tokens=n, num_prefills=0,
