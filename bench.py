@@ -245,6 +245,23 @@ def bench_stock(n, context, steps, warmup, num_heads=32):
     res.update(us_per_step=round(mean * 1e3, 2), us_per_step_median=round(med * 1e3, 2),
                GBps=round(b / (med * 1e-3) / 1e9, 1), hbm_frac=round(b / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                kernel="torch SDPA (flash / memory-efficient), contiguous bf16 K/V, no paging")
+    # The same K/V through a shuffled block table, with this library's uncompressed paged
+    # decode (the kernel of the full layers in the model harness).
+    from starkv_serve.kernels.stock_decode import paged_decode_full
+    del k, v
+    torch.cuda.empty_cache()
+    bs, pages = 16, context // 16
+    kc = torch.randn(n * pages + 1, bs, num_heads, 128, generator=g, device="cuda", dtype=torch.bfloat16)
+    vc = torch.randn(n * pages + 1, bs, num_heads, 128, generator=g, device="cuda", dtype=torch.bfloat16)
+    perm = torch.randperm(n * pages, generator=torch.Generator().manual_seed(8)) + 1
+    bt = perm.view(n, pages).to(torch.int32).cuda()
+    seq = torch.full((n,), context, dtype=torch.int32, device="cuda")
+    q3 = q[:, :, 0, :].contiguous()
+    pmean, pmed = time_events(lambda i: paged_decode_full(q3, kc, vc, bt, seq, context, 128 ** -0.5), steps, warmup)
+    res.update(paged_us_per_step=round(pmean * 1e3, 2), paged_us_per_step_median=round(pmed * 1e3, 2),
+               paged_GBps=round(b / (pmed * 1e-3) / 1e9, 1),
+               paged_hbm_frac=round(b / (pmed * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+               paged_kernel="stock_decode_kernel + stock_merge_kernel, bf16 K/V [blocks, 16, 32, 128], shuffled pages")
     return res
 
 
@@ -306,11 +323,14 @@ def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, mod
     written to a fused checkpoint and read back with load_fused_checkpoint; "stock" keeps
     every layer uncompressed. Sessions hold `context` tokens of synthetic cache rows (the
     3.2-bit rows packed from random hidden states through the write path) and decode
-    `steps` tokens each, one token per session per step, eager. Concurrency 1 and the most
+    `steps` tokens each, one token per session per step. Concurrency 1 and the most
     sessions whose caches fit in the GPU's free memory (less `reserve_gb`). Per mode and
     concurrency: TPOT (median step), tok/s = sessions / TPOT, and attention per step (the
     KV writes and attention of all 32 layers, timed on their own, as bench_serving.py:62-115
-    sums them)."""
+    sums them). Each figure twice: with each step (or each attention pass) replayed from one
+    HIP graph (`tpot_ms`, `tok_per_s`, `attention_us_per_step`: GPU time without host launch
+    gaps, the reference's attention figure being summed kernel time) and eager (`*_eager`:
+    every launch from the host)."""
     import tempfile
     import torch
     from starkv_serve import checkpoint as ck
@@ -348,35 +368,48 @@ def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, mod
                     layer.impl.write_from_hidden(hid.to(torch.bfloat16), c, slots[a:a + 4096])
                 for sess in range(1, n):
                     c[bt[sess, :pc].long()] = c[bt[0, :pc].long()]
-        tokens = torch.randint(0, shape.vocab_size, (n,), device=dev, generator=gg)
+        tokens0 = torch.randint(0, shape.vocab_size, (n,), device=dev, generator=gg)
+        pos0 = torch.full((n,), context, device=dev, dtype=torch.long)
         torch.cuda.synchronize()
-        times = []
-        for t in range(warm + steps):
-            positions = torch.full((n,), context + t, device=dev, dtype=torch.long)
-            md = M.decode_metadata(bt, positions, 16, context + t + 1)
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            tokens = model.decode_step(tokens, positions, md).argmax(-1)
-            b.record()
-            if t >= warm:
-                times.append((a, b))
-        torch.cuda.synchronize()
-        tpot = statistics.median([a.elapsed_time(b) for a, b in times])
-        positions = torch.full((n,), context + warm + steps - 1, device=dev, dtype=torch.long)
-        md = M.decode_metadata(bt, positions, 16, context + warm + steps)
+
+        def timed(fn, count):
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(count)]
+            for a, b in ev:
+                a.record()
+                fn()
+                b.record()
+            torch.cuda.synchronize()
+            return statistics.median([a.elapsed_time(b) for a, b in ev[warm:]])
+
+        # Eager steps: every launch from the host, lengths read on the host.
+        st = dict(tokens=tokens0.clone(), pos=pos0.clone())
+
+        def eager_step():
+            md = M.decode_metadata(bt, st["pos"], 16, int(context + st["t"]) + 1)
+            st["tokens"] = model.decode_step(st["tokens"], st["pos"], md).argmax(-1)
+            st["pos"] = st["pos"] + 1
+            st["t"] += 1
+
+        st["t"] = 0
+        tpot_eager = timed(eager_step, warm + steps)
+        # The same steps from one HIP graph per step (decode over the span max_model_len).
+        dg = M.DecodeGraph(model, bt, tokens0, pos0)
+        tpot = timed(dg.replay, warm + steps)
+        del dg
+        # Attention per step: the KV writes and attention of the 32 layers, in a graph of
+        # their own (their GPU time without host launch gaps), and eager.
+        positions = pos0 + warm + steps - 1
+        md = M.decode_metadata(bt, positions, 16, int(context + warm + steps))
         hid = torch.randn(n, shape.hidden_size, device=dev, generator=gg).to(torch.bfloat16)
-        at = []
-        for r in range(6):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            model.attention_only(hid, positions, md)
-            b.record()
-            if r:
-                at.append((a, b))
-        torch.cuda.synchronize()
-        attn = statistics.median([a.elapsed_time(b) for a, b in at])
+        attn_eager = timed(lambda: model.attention_only(hid, positions, md), warm + 5)
+        ag = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(ag):
+            model.attention_only(hid, positions, md, in_graph=True)
+        attn = timed(ag.replay, warm + 5)
+        del ag
         out = dict(sessions=n, tpot_ms=round(tpot, 3), tok_per_s=round(n / tpot * 1e3, 1),
-                   attention_us_per_step=round(attn * 1e3, 1),
+                   attention_us_per_step=round(attn * 1e3, 1), tpot_ms_eager=round(tpot_eager, 3),
+                   tok_per_s_eager=round(n / tpot_eager * 1e3, 1), attention_us_per_step_eager=round(attn_eager * 1e3, 1),
                    kv_cache_gb=round(n * pages * 16 * model.cache_bytes_per_token() / 1e9, 2))
         model.kv_caches = []
         torch.cuda.empty_cache()
@@ -391,7 +424,7 @@ def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, mod
                 c = None if mode == "stock" else ck.load_fused_checkpoint(
                     path, shape.num_layers, shape.num_kv_heads, shape.head_dim, dtype=torch.bfloat16,
                     kv_quant=mode == "quant")
-                model = M.StarKVLlamaForCausalLM(shape, c, max_model_len=context + warm + steps + 16, device=dev,
+                model = M.StarKVLlamaForCausalLM(shape, c, max_model_len=16 * pages, device=dev,
                                                  seed=seed + 1, stock=mode == "stock")
                 per_tok = model.cache_bytes_per_token()
                 free, _ = torch.cuda.mem_get_info()
@@ -527,7 +560,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip every workload but the headline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["bf16", "quant", "write", "short", "wide", "wide_quant", "c0", "c3",
-                                       "model"],
+                                       "model", "stock"],
                     default=None, help="profile runs: time one workload only and print its summary")
     ap.add_argument("--copy-probe", type=float, default=0.0, metavar="GIB",
                     help="profile runs: only copy GIB GiB device to device 5 times (counter scaling)")
@@ -558,6 +591,7 @@ def main():
         "c0": lambda: summarize(*bench_lowrank([4096], K, Wm, seed=1000)),
         "c3": lambda: bench_c3(32, 2),
         "model": lambda: bench_model(),
+        "stock": lambda: bench_stock(64, 8192, K, Wm),
     }
     if args.only in only:
         print(json.dumps(only[args.only]()), flush=True)
@@ -603,6 +637,8 @@ def main():
         for key, name in (("bf16", head), ("quant", extra["quant_bs64x8k"])):
             if "us_per_step" in stock:
                 stock[f"starkv_{key}_speedup_vs_sdpa"] = round(stock["us_per_step"] / name["us_per_step"], 2)
+            if "paged_us_per_step" in stock:
+                stock[f"starkv_{key}_speedup_vs_paged"] = round(stock["paged_us_per_step"] / name["us_per_step"], 2)
             stock[f"starkv_{key}_speedup_vs_hbm_bound"] = round(stock["hbm_bound_us"] / name["us_per_step"], 2)
         extra["stock_bf16_bs64x8k"] = stock
         log(json.dumps(stock))

@@ -121,9 +121,20 @@ int starkv_fold_q(void *stream, const void *q, int64_t q_s0, int64_t q_s1, int q
 
 /*
  * Grid (workgroups) the decode calls below use on the current device for n
- * requests bounded by max_seq_len. A pure function of (device, n, max_seq_len).
+ * requests bounded by max_seq_len: min(CUs, max(n, ceil(n * max_seq_len / 256))).
+ * A pure function of (device, n, max_seq_len).
  */
 int starkv_decode_grid(int n, int max_seq_len);
+
+/*
+ * The grid for one layer's calls: starkv_decode_grid's rule with 256 tokens per
+ * workgroup when the layer decodes in two passes (V ranks too wide for one pass; see
+ * starkv_decode_two_pass), 64 otherwise. A pure function of its arguments and the device.
+ * This build's Python wrappers take their grid from it (no counterpart in the
+ * reference, whose Triton launches size their own grids, paged_decode.py:192-219).
+ */
+int starkv_decode_grid_for(int cache_kind, int n, int num_heads, int num_kv_heads, int k_width, int v_rank,
+                           int max_seq_len);
 
 /*
  * Workspace bytes a decode call needs: the token prefix sums, the wave plan, the
@@ -183,7 +194,7 @@ int starkv_decode_set_path(int mode);
  *   out         [n, H_q, 128] (strides o_s0, o_s1), dtype out_dtype
  *   workspace   >= starkv_decode_workspace_bytes(code_dtype, n, H_q, H_kv, k_width, v_rank,
  *               max_seq_len, grid) bytes, 256-byte aligned; grid from
- *               starkv_decode_grid(n, max_seq_len) (or any grid >= 1)
+ *               starkv_decode_grid_for(...) (or any grid >= 1)
  * A request with no tokens (seq_lens <= 0) gets NaN rows, as the reference's softmax
  * over an empty row does.
  */

@@ -539,14 +539,27 @@ __global__ __launch_bounds__(MERGE_THR) void merge_kernel(const uint8_t* __restr
 #pragma unroll
         for (int j = 0; j < MERGE_CB; ++j) acc[j] = fmaf(pre[k][j], w, acc[j]);
     }
-    for (int k = MERGE_PRE; k < nk; ++k) {  // requests spread over more than MERGE_PRE workgroups
-        const int64_t sl = s0 + (int64_t)k * Hq;
-        const float w = k < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k))
-                               : exp2f(wm[sl] - M);
+    // Requests spread over more than MERGE_PRE workgroups: MERGE_PRE partials' rows in
+    // flight at a time (columns past v_rank read column 0 and are never stored).
+    for (int k0 = MERGE_PRE; k0 < nk; k0 += MERGE_PRE) {
+        float v[MERGE_PRE][MERGE_CB];
 #pragma unroll
-        for (int j = 0; j < MERGE_CB; ++j) {
-            const int c = lane + 64 * j;
-            if (c < v_rank) acc[j] = fmaf(wa[sl * v_rank + c], w, acc[j]);
+        for (int u = 0; u < MERGE_PRE; ++u) {
+            const int64_t sl = s0 + (int64_t)min(k0 + u, nk - 1) * Hq;
+#pragma unroll
+            for (int j = 0; j < MERGE_CB; ++j) {
+                const int c = lane + 64 * j;
+                v[u][j] = wa[sl * v_rank + (c < v_rank ? c : 0)];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < MERGE_PRE; ++u) {
+            const int k = k0 + u;
+            if (k >= nk) break;
+            const float w = k < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k))
+                                   : exp2f(wm[s0 + (int64_t)k * Hq] - M);
+#pragma unroll
+            for (int j = 0; j < MERGE_CB; ++j) acc[j] = fmaf(v[u][j], w, acc[j]);
         }
     }
     const float inv = 1.f / l;
@@ -595,7 +608,7 @@ __global__ __launch_bounds__(256) void fold_q_kernel(const void* __restrict__ q,
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-static int device_cus() {
+int device_cus() {
     static int cus[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
@@ -607,9 +620,14 @@ static int device_cus() {
     return cus[dev];
 }
 
-static int grid_for(int n, int max_seq_len) {
+// tok_per_wg: tokens per workgroup the split aims for (at most the device's CUs
+// workgroups). 256 (16 pages) for two-pass calls, whose fp32 partial accumulators of
+// H x v_rank per workgroup and request would otherwise cost as much traffic as the V
+// codes they sum; 64 for one-pass calls, whose partials are small, so that a short batch
+// (one request of 4096 tokens) still spreads over many CUs.
+static int grid_for(int n, int max_seq_len, int tok_per_wg = 256) {
     const int64_t tokens = (int64_t)n * (int64_t)(max_seq_len > 0 ? max_seq_len : 1);
-    int64_t want = (tokens + 255) / 256;  // at least ~16 pages per workgroup
+    int64_t want = (tokens + tok_per_wg - 1) / tok_per_wg;
     // Each request a workgroup moves on to costs a reload of that request's folded query
     // tiles (about as long as 2-3 pages), so short requests get a workgroup each where the
     // device has one to spare.
@@ -867,7 +885,7 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     SKV_HIP(hipGetLastError());
     if (timed && g_prof.mode == 0) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used + 1], stream));
     if (two) {
-        rc = launch_merge_wide(p, a.vu_dt, a.vup, a.vu_s0, a.vu_s1, a.out, a.o_s0, a.o_s1, a.out_dt, stream);
+        rc = launch_merge_wide(p, a.grid, a.vu_dt, a.vup, a.vu_s0, a.vu_s1, a.out, a.o_s0, a.o_s1, a.out_dt, stream);
     } else {
         const dim3 mgrid((a.n + MERGE_REQ - 1) / MERGE_REQ, a.Hq);
         const size_t mlds = merge_lds_bytes(a.v_rank, a.vu_dt);
@@ -911,6 +929,19 @@ using namespace starkv;
 extern "C" {
 
 int starkv_decode_grid(int n, int max_seq_len) { return grid_for(n, max_seq_len); }
+
+int starkv_decode_grid_for(int cache_kind, int n, int num_heads, int num_kv_heads, int k_width, int v_rank,
+                           int max_seq_len) {
+    if (n < 1 || num_heads < 1 || num_kv_heads < 1 || k_width < 16 || v_rank < 1) return grid_for(n, max_seq_len);
+    bool two;
+    if (cache_kind == STARKV_CACHE_Q3_2) {
+        const QRow r = qrow(k_width, num_heads, v_rank);
+        two = use_two_pass(FMT_Q4, k_width, v_rank, r.nbytes, r.v_nout);
+    } else {
+        two = use_two_pass(cache_kind == STARKV_F16 ? FMT_F16 : FMT_BF16, k_width, v_rank, (k_width + v_rank) * 2, 0);
+    }
+    return grid_for(n, max_seq_len, two ? 256 : 64);
+}
 
 int starkv_profile_begin(int max_calls, int mode) {
     clear_error();

@@ -271,10 +271,12 @@ int launch_quant(const DecodeParams& p, int nb, int grid, hipStream_t stream);
 // The two-pass decode (decode_wide.hip): the P @ V pass over the logits the K pass
 // stored (one launch per column window), whether its pages fit in LDS, and the merge of
 // its partials with the lift through v_up_by_q (of dtype w_dt).
+// Compute units of the current device (cached per device).
+int device_cus();
 int launch_pv(const DecodeParams& p, int fmt, int grid, hipStream_t stream);
 bool pv_fits(int fmt, int k_width, int v_rank, int vs_off, int vq_off, int v_nout, int v_bytes);
-int launch_merge_wide(const DecodeParams& p, int w_dt, const void* vup, int64_t vu_s0, int64_t vu_s1, void* out,
-                      int64_t o_s0, int64_t o_s1, int out_dt, hipStream_t stream);
+int launch_merge_wide(const DecodeParams& p, int grid, int w_dt, const void* vup, int64_t vu_s0, int64_t vu_s1,
+                      void* out, int64_t o_s0, int64_t o_s1, int out_dt, hipStream_t stream);
 constexpr int MAX_V_RANK_TWO_PASS = 4096;  // H x head_dim of a 32-head MHA layer: a full-rank V
 int quant_v_blocks(int v_rank, int v_nout);
 int quant_chunks(int row_bytes);

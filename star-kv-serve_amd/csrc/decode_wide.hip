@@ -12,8 +12,9 @@
 // that partial slot (request b, workgroup g) = b + g matches the (m, l) the logits pass
 // stored for it. Per page of 16 tokens the workgroup copies into LDS, with buffer loads
 // that write LDS directly (16 bytes per lane):
-//   - the V bytes of the 16 rows: bf16/fp16, the columns [c0, c0 + cw) of this launch's
-//     window; 3.2-bit, every V byte (scales, outlier and inlier nibbles);
+//   - the V bytes of the 16 rows: bf16/fp16, the columns of the workgroup's window
+//     (grid.y: windows run side by side); 3.2-bit, every V byte (scales, outlier and
+//     inlier nibbles);
 //   - the 16 logits of every head (2 KB) and the slot's reference max per head.
 // Since the reference max of a slot is final, P = exp2(logit - m) needs no rescaling.
 // P @ V runs on v_mfma_f32_32x32x16 (M = 32 heads, N = 32 columns, K = the page's 16
@@ -85,8 +86,9 @@ struct PvParams {
     int vs_rel;      // 3.2-bit: V scales at this byte of the copied bytes
     int vq_rel;      // 3.2-bit: first V nibble byte (outlier nibbles), relative
     int v_nout, v_nbo;  // 3.2-bit: outlier columns, their nibble bytes
-    int c0, ncb;     // window: bf16/fp16, first column and 32-column blocks; 3.2-bit, first
-                     // 32-byte chunk of the copied bytes and chunks
+    int per, units;  // window y (blockIdx.y) = units [y per, min((y + 1) per, units)): bf16/fp16,
+                     // 32-column blocks (the copies start 64 y per bytes further); 3.2-bit,
+                     // 32-byte chunks of the copied bytes (one window: every V byte is copied)
     int nch;         // 1 KB chunks copied per page: logits (2), the slot's maxima (1), then V
     int nld;         // copies per wave per page
     int nbuf;        // page buffers (2 .. 8): nbuf - 1 pages in flight
@@ -171,6 +173,11 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
     const int T = P[p.n];
     const int beg = min(g * S_tok, T), end = min(beg + S_tok, T);
     if (beg >= end) return;
+    // This workgroup's column window.
+    const int u0 = (int)blockIdx.y * p.per;
+    const int ncb = min(p.per, p.units - u0);
+    const int c0 = FMT == FMT_Q4 ? u0 : 32 * u0;
+    const int v_off = p.v_off + (FMT == FMT_Q4 ? 0 : 64 * u0);
 
     const uint32_t base = lds_addr(s_pv);
     const uint32_t dummy = base + (uint32_t)(p.lds_bytes - 1024);
@@ -190,7 +197,7 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
             if (4 * lane < p.Hq) o = (uint32_t)(16 * lane);
         } else if (ch < p.nch) {
             const int G = 4 * (ch - PV_V0) + (lane >> 4), t = gslot(G, lane & 15);
-            if (G < p.ng) o = (uint32_t)(t * p.c_s1 + p.v_off + 16 * G);
+            if (G < p.ng) o = (uint32_t)(t * p.c_s1 + v_off + 16 * G);
         }
         off[i] = o;
     }
@@ -259,7 +266,7 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const bool ok = am < p.Hq && tok0 + e >= cc.lo && tok0 + e < cc.hi;
-            pe[e] = ok ? __builtin_amdgcn_exp2f(sv[e] - mx) : 0.f;
+            pe[e] = __builtin_amdgcn_exp2f(ok ? sv[e] - mx : -INFINITY);  // no branch: exp2(-inf) = 0
         }
         if constexpr (FMT == FMT_BF16) {
             float lo[8];
@@ -269,7 +276,7 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
                 const int cb = wave + NWAVE * i;
-                if (cb < p.ncb) {
+                if (cb < ncb) {
                     const uint32_t a = vbuf + (uint32_t)cb * 1024u;
                     const uint2 b0 = tr_read(a + trd0), b1 = tr_read(a + trd1);
                     const bf16x8_t bv = __builtin_bit_cast(bf16x8_t, make_uint4(b0.x, b0.y, b1.x, b1.y));
@@ -282,7 +289,7 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
                 const int cb = wave + NWAVE * i;
-                if (cb < p.ncb) {
+                if (cb < ncb) {
                     const uint32_t a = vbuf + (uint32_t)cb * 1024u;
                     const uint2 b0 = tr_read(a + trd0), b1 = tr_read(a + trd1);
                     const half8_t bv = __builtin_bit_cast(half8_t, make_uint4(b0.x, b0.y, b1.x, b1.y));
@@ -301,12 +308,17 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
                 so[j] = h2_bits(cvt_h2(__uint_as_float(w0 << 16), __uint_as_float(w1 << 16)));
                 si[j] = h2_bits(cvt_h2(__uint_as_float(w0 & 0xffff0000u), __uint_as_float(w1 & 0xffff0000u)));
             }
+            // Every chunk's bytes first (chunks past the window reread the last one, unused).
+            uint2 wv[MB / 2];
+#pragma unroll
+            for (int i = 0; i < MB / 2; ++i)
+                wv[i] = tr_read8(vbuf + (uint32_t)(c0 + min(wave + NWAVE * i, ncb - 1)) * 512u + trd0);
 #pragma unroll
             for (int i = 0; i < MB / 2; ++i) {
                 const int ch = wave + NWAVE * i;  // 32-byte chunk of the copied V bytes
-                if (ch < p.ncb) {
-                    const int c = p.c0 + ch;
-                    const uint2 w = tr_read8(vbuf + (uint32_t)c * 512u + trd0);
+                if (ch < ncb) {
+                    const int c = c0 + ch;
+                    const uint2 w = wv[i];
                     // This lane's byte: outlier columns before v_nbo bytes of nibbles, inlier after.
                     const bool inl = 32 * c + (lane & 31) - p.vq_rel >= p.v_nbo;
                     const uint32_t l0 = w.x & 0x0F0F0F0Fu, l1 = w.y & 0x0F0F0F0Fu;
@@ -339,8 +351,8 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
                 int col = -1;
                 if (FMT == FMT_Q4) {
                     const int ch = wave + NWAVE * (i >> 1);
-                    const int rel = 32 * (p.c0 + ch) + (lane & 31) - p.vq_rel;  // nibble byte of this lane
-                    if (ch < p.ncb && rel >= 0) {
+                    const int rel = 32 * (c0 + ch) + (lane & 31) - p.vq_rel;  // nibble byte of this lane
+                    if (ch < ncb && rel >= 0) {
                         if (rel < p.v_nbo) {
                             col = 2 * rel + (i & 1);
                             if (col >= p.v_nout) col = -1;
@@ -350,7 +362,7 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
                     }
                 } else {
                     const int cb = wave + NWAVE * i;
-                    if (cb < p.ncb) col = p.c0 + 32 * cb + (lane & 31);
+                    if (cb < ncb) col = c0 + 32 * cb + (lane & 31);
                 }
                 const bool okc = col >= 0 && col < p.v_rank;
 #pragma unroll
@@ -369,24 +381,29 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
 
 // ---------------------------------------------------------------------------
 // Merge of the two-pass partials, in two launches.
-// merge_cols_kernel: one workgroup per (request, head): the log-sum-exp weights of the
-//   request's slots, then every column's weighted sum of their accumulators, divided by
-//   the total, into o [n][Hq][ld] (NaN for a request with no tokens, as the reference's
-//   softmax over an empty row).
-// lift_kernel: one workgroup per (head, LIFT_REQ requests): out = o @ v_up_by_q[h], each
-//   thread 8 output columns over one sixteenth of the rank columns, then a reduction
-//   over the sixteenths.
+// merge_cols_kernel<MCW>: one workgroup per (request, head, column block): the
+//   log-sum-exp weights of the request's slots, then each column's weighted sum of their
+//   accumulators, four loads in flight, divided by the total, into o [n][Hq][ld] (NaN for
+//   a request with no tokens, as the reference's softmax over an empty row). MCW = 1: the
+//   four waves take different columns (1024 per workgroup), each over every slot; MCW = 4,
+//   for requests split over many workgroups (a few long requests): wave w sums slots w,
+//   w + 4, ... of 256 columns, then the four waves' sums are added.
+// lift_kernel<DT, REQ, THR>: one workgroup per (head, REQ requests): out = o @ v_up_by_q[h],
+//   each thread 8 output columns over a THR / 16-th of the rank columns, LIFT_U rows in
+//   flight, then a reduction over those parts. 8 requests x 512 threads; for at most 8
+//   requests, 2 x 1024 (more rows in flight per workgroup, more workgroups).
 // ---------------------------------------------------------------------------
 constexpr int MC_THR = 256;
-constexpr int LIFT_REQ = 8;
-constexpr int LIFT_THR = 512;
-constexpr int LIFT_WAVES = LIFT_THR / 64;
-constexpr int LIFT_U = 4;  // v_up_by_q rows per thread in flight
+constexpr int LIFT_U = 8;  // v_up_by_q rows per thread in flight
 
+template <int MCW>
 __global__ __launch_bounds__(MC_THR) void merge_cols_kernel(const uint8_t* __restrict__ ws, size_t ws_plan, size_t ws_m,
                                                             size_t ws_l, size_t ws_acc, size_t ws_o, int n, int Hq,
                                                             int v_rank, int ld) {
+    constexpr int CPW = 4 * MC_THR / MCW;  // columns per workgroup
+    __shared__ f32x4_t s_sum[MCW][64];
     const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int w = MCW > 1 ? __builtin_amdgcn_readfirstlane(tid >> 6) : 0;  // slot phase
     const int* hdr = (const int*)ws;
     const float* wm = (const float*)(ws + ws_m);
     const float* wl = (const float*)(ws + ws_l);
@@ -410,36 +427,49 @@ __global__ __launch_bounds__(MC_THR) void merge_cols_kernel(const uint8_t* __res
     l = wave_sum(l);
     const float inv = live ? 1.f / l : __builtin_nanf("");
     float* o = (float*)(ws + ws_o) + ((int64_t)b * Hq + h) * ld;
-    for (int c4 = 4 * tid; c4 < v_rank; c4 += 4 * MC_THR) {
-        f32x4_t a = {0.f, 0.f, 0.f, 0.f};
-        int k = 0;
-        for (; k + 4 <= nk; k += 4) {  // four partials' loads in flight
+    const int c4 = blockIdx.z * CPW + 4 * (MCW > 1 ? lane : tid);
+    f32x4_t a = {0.f, 0.f, 0.f, 0.f};
+    if (c4 < v_rank) {
+        int k = w;  // wave-uniform
+        for (; k + 3 * MCW < nk; k += 4 * MCW) {  // four partials' loads in flight
             f32x4_t r[4];
             float wt[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const int64_t sl = s0 + (int64_t)(k + u) * Hq;
+                const int ku = k + u * MCW;
+                const int64_t sl = s0 + (int64_t)ku * Hq;
                 r[u] = *(const f32x4_t*)(wa + sl * ld + c4);
-                wt[u] = k + u < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k + u))
-                                   : exp2f(wm[sl] - M);
+                wt[u] = ku < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), ku)) : exp2f(wm[sl] - M);
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) a += r[u] * wt[u];
         }
-        for (; k < nk; ++k) {
+        for (; k < nk; k += MCW) {
             const int64_t sl = s0 + (int64_t)k * Hq;
             const float wt = k < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k)) : exp2f(wm[sl] - M);
             a += *(const f32x4_t*)(wa + sl * ld + c4) * wt;
         }
-        *(f32x4_t*)(o + c4) = a * inv;
+    }
+    if constexpr (MCW == 1) {
+        if (c4 < v_rank) *(f32x4_t*)(o + c4) = a * inv;
+    } else {
+        s_sum[w][lane] = a;
+        __syncthreads();
+        if (w == 0 && c4 < v_rank) {
+            f32x4_t t = s_sum[0][lane];
+#pragma unroll
+            for (int k = 1; k < MCW; ++k) t += s_sum[k][lane];
+            *(f32x4_t*)(o + c4) = t * inv;
+        }
     }
 }
 
-template <int DT>
+template <int DT, int LIFT_REQ, int LIFT_THR>
 __global__ __launch_bounds__(LIFT_THR) void lift_kernel(const uint8_t* __restrict__ ws, size_t ws_o, int n, int Hq,
                                                         int v_rank, int ld, const void* __restrict__ vup,
                                                         int64_t vu_s0, int64_t vu_s1, void* __restrict__ out,
                                                         int64_t o_s0, int64_t o_s1, int out_dt) {
+    constexpr int LIFT_WAVES = LIFT_THR / 64;
     extern __shared__ __align__(16) uint8_t s_dyn[];
     float* s_o = (float*)s_dyn;    // [LIFT_REQ][ld]
     float* s_red = (float*)s_dyn;  // [LIFT_WAVES][LIFT_REQ][128], over s_o once the products are done
@@ -530,7 +560,11 @@ int raise_lds(const void* fn, int bytes) {
     return STARKV_OK;
 }
 
-size_t lift_lds(int ld) { return std::max((size_t)LIFT_REQ * ld * 4, (size_t)LIFT_WAVES * LIFT_REQ * 128 * 4); }
+// Dynamic LDS of lift_kernel<DT, req, thr>: the rows o [req][ld], then (over them) the
+// per-wave sums [thr / 64][req][128].
+size_t lift_lds(int ld, int req = 8, int thr = 512) {
+    return std::max((size_t)req * ld * 4, (size_t)(thr / 64) * req * 128 * 4);
+}
 
 }  // namespace
 
@@ -539,13 +573,14 @@ size_t lift_lds(int ld) { return std::max((size_t)LIFT_REQ * ld * 4, (size_t)LIF
 // MFMA blocks), and the LDS geometry.
 struct PvPlan {
     int units;      // in all
-    int per;        // per launch
+    int per;        // per window
     int nbuf, nch, nld, lds;
     int ng, v_off;  // copy geometry: granules per row (bf16/fp16: of one window) and the first byte
     bool ok;
 };
 
-static PvPlan pv_plan(int fmt, int k_width, int v_rank, int vs_off, int vq_off, int v_bytes) {
+// min_windows (bf16/fp16): at least this many column windows, when each can keep 4 blocks.
+static PvPlan pv_plan(int fmt, int k_width, int v_rank, int vs_off, int vq_off, int v_bytes, int min_windows = 1) {
     PvPlan pl{};
     int max_units;
     if (fmt == FMT_Q4) {
@@ -558,9 +593,10 @@ static PvPlan pv_plan(int fmt, int k_width, int v_rank, int vs_off, int vq_off, 
         pl.units = (v_rank + 31) / 32;
         max_units = 64;
     }
-    // Fewest launches (each re-reads the logits) whose pages keep at least PV_INFLIGHT
+    // Fewest windows (each re-reads the logits) whose pages keep at least PV_INFLIGHT
     // bytes in flight per workgroup, else the most bytes in flight.
-    const int lo = (pl.units + std::min(pl.units, max_units) - 1) / std::min(pl.units, max_units);
+    int lo = (pl.units + std::min(pl.units, max_units) - 1) / std::min(pl.units, max_units);
+    if (fmt != FMT_Q4) lo = std::max(lo, std::min(min_windows, pl.units / 4));
     int best_score = -1;
     for (int launches = lo; launches <= lo + 3; ++launches) {
         const int per = (pl.units + launches - 1) / launches;
@@ -588,7 +624,10 @@ static PvPlan pv_plan(int fmt, int k_width, int v_rank, int vs_off, int vq_off, 
 
 int launch_pv(const DecodeParams& p, int fmt, int grid, hipStream_t stream) {
     const int v_bytes = p.v_nbo + (p.v_rank - p.v_nout + 1) / 2;
-    const PvPlan pl = pv_plan(fmt, p.k_width, p.v_rank, p.vs_off, p.vq_off, v_bytes);
+    // A grid short of the CUs (few requests) takes more, narrower windows side by side.
+    const int cus = device_cus();
+    PvPlan pl = pv_plan(fmt, p.k_width, p.v_rank, p.vs_off, p.vq_off, v_bytes, (cus + grid - 1) / grid);
+    if (!pl.ok) pl = pv_plan(fmt, p.k_width, p.v_rank, p.vs_off, p.vq_off, v_bytes);
     SKV_CHECK(pl.ok, "decode: no P @ V window fits in LDS (v_rank %d)", p.v_rank);
     PvParams a;
     memset(&a, 0, sizeof(a));
@@ -603,26 +642,19 @@ int launch_pv(const DecodeParams& p, int fmt, int grid, hipStream_t stream) {
     a.lds_bytes = pl.lds;
     a.ws = p.ws; a.ws_plan = p.ws_plan; a.ws_m = p.ws_m; a.ws_acc = p.ws_acc; a.ws_lg = p.ws_lg; a.lcap = p.lcap;
     a.acc_ld = p.acc_ld;
-    for (int u0 = 0; u0 < pl.units; u0 += pl.per) {
-        a.ncb = std::min(pl.per, pl.units - u0);
-        int mb;
-        if (fmt == FMT_Q4) {
-            a.c0 = u0;
-            a.v_off = pl.v_off;
-            mb = 2 * ((a.ncb + NWAVE - 1) / NWAVE);
-        } else {
-            a.c0 = 32 * u0;
-            a.v_off = pl.v_off + 64 * u0;
-            mb = (a.ncb + NWAVE - 1) / NWAVE;
-        }
-        const void* fn = fmt == FMT_BF16 ? pv_pick<FMT_BF16>(mb)
-                         : fmt == FMT_F16 ? pv_pick<FMT_F16>(mb)
-                                          : pv_pick<FMT_Q4>(mb);
-        int rc = raise_lds(fn, PV_MAX_DYN_LDS);
-        if (rc) return rc;
-        void* args[] = {(void*)&a};
-        SKV_HIP(hipLaunchKernel(fn, dim3(grid), dim3(NTHR), args, (size_t)a.lds_bytes, stream));
-    }
+    // The windows run side by side in one launch (grid.y): each re-reads the page logits.
+    a.per = pl.per;
+    a.units = pl.units;
+    a.v_off = pl.v_off;
+    const int windows = (pl.units + pl.per - 1) / pl.per;
+    const int mb = fmt == FMT_Q4 ? 2 * ((pl.per + NWAVE - 1) / NWAVE) : (pl.per + NWAVE - 1) / NWAVE;
+    const void* fn = fmt == FMT_BF16 ? pv_pick<FMT_BF16>(mb)
+                     : fmt == FMT_F16 ? pv_pick<FMT_F16>(mb)
+                                      : pv_pick<FMT_Q4>(mb);
+    int rc = raise_lds(fn, PV_MAX_DYN_LDS);
+    if (rc) return rc;
+    void* args[] = {(void*)&a};
+    SKV_HIP(hipLaunchKernel(fn, dim3(grid, windows), dim3(NTHR), args, (size_t)a.lds_bytes, stream));
     return STARKV_OK;
 }
 
@@ -632,24 +664,38 @@ bool pv_fits(int fmt, int k_width, int v_rank, int vs_off, int vq_off, int v_nou
            lift_lds((v_rank + 3) & ~3) <= (size_t)PV_MAX_DYN_LDS;
 }
 
-int launch_merge_wide(const DecodeParams& p, int w_dt, const void* vup, int64_t vu_s0, int64_t vu_s1, void* out,
-                      int64_t o_s0, int64_t o_s1, int out_dt, hipStream_t stream) {
+int launch_merge_wide(const DecodeParams& p, int grid, int w_dt, const void* vup, int64_t vu_s0, int64_t vu_s1,
+                      void* out, int64_t o_s0, int64_t o_s1, int out_dt, hipStream_t stream) {
     const size_t lds = lift_lds(p.acc_ld);
     SKV_CHECK(lds <= (size_t)PV_MAX_DYN_LDS, "decode: v_rank %d too large for the merge", p.v_rank);
-    hipLaunchKernelGGL(merge_cols_kernel, dim3(p.n, p.Hq), dim3(MC_THR), 0, stream, (const uint8_t*)p.ws, p.ws_plan,
-                       p.ws_m, p.ws_l, p.ws_acc, p.ws_o, p.n, p.Hq, p.v_rank, p.acc_ld);
+    // Slots per request: about grid / n + 1. Many (a few long requests): split them over waves.
+    if (grid >= 8 * p.n)
+        hipLaunchKernelGGL(merge_cols_kernel<4>, dim3(p.n, p.Hq, (p.v_rank + 255) / 256), dim3(MC_THR), 0, stream,
+                           (const uint8_t*)p.ws, p.ws_plan, p.ws_m, p.ws_l, p.ws_acc, p.ws_o, p.n, p.Hq, p.v_rank,
+                           p.acc_ld);
+    else
+        hipLaunchKernelGGL(merge_cols_kernel<1>, dim3(p.n, p.Hq, (p.v_rank + 1023) / 1024), dim3(MC_THR), 0, stream,
+                           (const uint8_t*)p.ws, p.ws_plan, p.ws_m, p.ws_l, p.ws_acc, p.ws_o, p.n, p.Hq, p.v_rank,
+                           p.acc_ld);
     SKV_HIP(hipGetLastError());
-    const void* fn = w_dt == STARKV_BF16 ? (const void*)&lift_kernel<STARKV_BF16>
-                     : w_dt == STARKV_F16 ? (const void*)&lift_kernel<STARKV_F16>
-                                          : (const void*)&lift_kernel<STARKV_F32>;
+    const bool small = p.n <= 8;
+    const int req = small ? 2 : 8, thr = small ? 1024 : 512;
+    const void* fn = small ? (w_dt == STARKV_BF16 ? (const void*)&lift_kernel<STARKV_BF16, 2, 1024>
+                              : w_dt == STARKV_F16 ? (const void*)&lift_kernel<STARKV_F16, 2, 1024>
+                                                   : (const void*)&lift_kernel<STARKV_F32, 2, 1024>)
+                           : (w_dt == STARKV_BF16 ? (const void*)&lift_kernel<STARKV_BF16, 8, 512>
+                              : w_dt == STARKV_F16 ? (const void*)&lift_kernel<STARKV_F16, 8, 512>
+                                                   : (const void*)&lift_kernel<STARKV_F32, 8, 512>);
     int rc = raise_lds(fn, PV_MAX_DYN_LDS);
     if (rc) return rc;
+    const size_t lds2 = lift_lds(p.acc_ld, req, thr);
+    SKV_CHECK(lds2 <= (size_t)PV_MAX_DYN_LDS, "decode: v_rank %d too large for the lift", p.v_rank);
     const uint8_t* ws = p.ws;
     size_t wo = p.ws_o;
     int n = p.n, Hq = p.Hq, vr = p.v_rank, ld = p.acc_ld;
     void* args[] = {(void*)&ws, (void*)&wo, (void*)&n, (void*)&Hq, (void*)&vr, (void*)&ld, (void*)&vup,
                     (void*)&vu_s0, (void*)&vu_s1, (void*)&out, (void*)&o_s0, (void*)&o_s1, (void*)&out_dt};
-    SKV_HIP(hipLaunchKernel(fn, dim3(p.Hq, (p.n + LIFT_REQ - 1) / LIFT_REQ), dim3(LIFT_THR), args, lds, stream));
+    SKV_HIP(hipLaunchKernel(fn, dim3(p.Hq, (p.n + req - 1) / req), dim3(thr), args, lds2, stream));
     return STARKV_OK;
 }
 

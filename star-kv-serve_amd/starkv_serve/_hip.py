@@ -34,6 +34,7 @@ SIGNATURES = {
     "starkv_write_kv": (_I, [_P, _P, _I64, _P, _I64, _I, _I, _I, _I, _I, _P, _I64, _I64, _I, _I, _I64, _P, _I,
                              _I, _P, _P, _P, _I, _P, _I64, _P, _SZ]),
     "starkv_decode_grid": (_I, [_I, _I]),
+    "starkv_decode_grid_for": (_I, [_I, _I, _I, _I, _I, _I, _I]),
     "starkv_stock_decode_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "starkv_stock_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _P, _I64, _I64, _I64, _I, _I, _P, _I64, _I64, _P,
                                  _I, _I, _I, _I, _F, _P, _I64, _I64, _I, _P, _SZ]),

@@ -138,7 +138,7 @@ def paged_starkv_decode(
     for s in range(0, n, step):
         e = min(n, s + step)
         m = e - s
-        grid = L.starkv_decode_grid(m, int(max_seq_len))
+        grid = L.starkv_decode_grid_for(kind, m, num_heads, num_kv_heads, int(k_width), v_rank, int(max_seq_len))
         ws = torch.empty(L.starkv_decode_workspace_bytes(kind, m, num_heads, num_kv_heads, int(k_width), v_rank,
                                                          int(max_seq_len), grid),
                          dtype=torch.uint8, device=query.device)

@@ -216,7 +216,7 @@ def paged_quant_decode(
     for s in range(0, n, step):
         e = min(n, s + step)
         m = e - s
-        grid = L.starkv_decode_grid(m, int(max_seq_len))
+        grid = L.starkv_decode_grid_for(_hip.CACHE_Q3_2, m, H, H, row.k_width, row.v_rank, int(max_seq_len))
         ws = torch.empty(L.starkv_decode_workspace_bytes(_hip.CACHE_Q3_2, m, H, H, row.k_width, row.v_rank,
                                                          int(max_seq_len), grid),
                          dtype=torch.uint8, device=query.device)

@@ -155,14 +155,16 @@ class StarKVLlamaForCausalLM:
 
     # -- the step ---------------------------------------------------------------------------
     def _attention(self, li: int, h: torch.Tensor, positions: torch.Tensor, md: StarKVMetadata,
-                   capture: Optional[list]) -> torch.Tensor:
+                   capture: Optional[list], in_graph: bool = False) -> torch.Tensor:
+        """Inside a graph (`in_graph`) no launch depends on the step's lengths: every layer
+        decodes over the span max_model_len, the lengths are read on the device."""
         s, layer = self.shape, self.layers[li]
         T = h.shape[0]
         H, Hkv, D = s.num_heads, s.num_kv_heads, s.head_dim
         if layer.compressed:
             q = self.rotary.apply(positions, F.linear(h, layer.q_proj).view(T, H, D))
             out = torch.empty(T, H * D, dtype=self.dtype, device=self.device)
-            layer.impl.forward_from_hidden(q.view(T, H * D), h, self.kv_caches[li], md, out, in_full_graph=False)
+            layer.impl.forward_from_hidden(q.view(T, H * D), h, self.kv_caches[li], md, out, in_full_graph=in_graph)
         else:
             qkv = F.linear(h, layer.qkv_proj)
             q, k, v = qkv.split([H * D, Hkv * D, Hkv * D], dim=-1)
@@ -172,22 +174,24 @@ class StarKVLlamaForCausalLM:
             slots = md.slot_mapping[:T].clamp(min=0)
             kc[slots // self.block_size, slots % self.block_size] = k
             vc[slots // self.block_size, slots % self.block_size] = v.reshape(T, Hkv, D)
-            out = paged_decode_full(q, kc, vc, md.block_table[:T], md.seq_lens[:T], max(md.max_seq_len, 1),
-                                    self.scale).view(T, H * D)
+            span = self.max_model_len if in_graph else max(md.max_seq_len, 1)
+            out = paged_decode_full(q, kc, vc, md.block_table[:T], md.seq_lens[:T], span, self.scale).view(T, H * D)
         if capture is not None:
             capture.append(dict(layer=li, q=q.view(T, H, D), out=out.view(T, H, D)))
         return F.linear(out, layer.o_proj)
 
-    def attention_only(self, hidden: torch.Tensor, positions: torch.Tensor, md: StarKVMetadata) -> None:
+    @torch.no_grad()
+    def attention_only(self, hidden: torch.Tensor, positions: torch.Tensor, md: StarKVMetadata,
+                       in_graph: bool = False) -> None:
         """The KV writes and attention of every layer for one step with the same input
         (the "attention per step" figure: cache write + attention summed over the layers,
         as the reference's benchmark sums them, bench_serving.py:62-115)."""
         for li in range(len(self.layers)):
-            self._attention(li, hidden, positions, md, None)
+            self._attention(li, hidden, positions, md, None, in_graph)
 
     @torch.no_grad()
     def decode_step(self, tokens: torch.Tensor, positions: torch.Tensor, md: StarKVMetadata,
-                    capture: Optional[list] = None) -> torch.Tensor:
+                    capture: Optional[list] = None, in_graph: bool = False) -> torch.Tensor:
         """Logits [n, vocab] for one new token per request: tokens [n] at `positions` [n];
         `md` has every row as a decode (seq_lens = positions + 1, slot_mapping the new
         tokens' slots)."""
@@ -195,11 +199,50 @@ class StarKVLlamaForCausalLM:
         x = self.embed[tokens]
         for li, layer in enumerate(self.layers):
             h = F.rms_norm(x, (s.hidden_size,), layer.ln1, s.rms_norm_eps)
-            x = x + self._attention(li, h, positions, md, capture)
+            x = x + self._attention(li, h, positions, md, capture, in_graph)
             h = F.rms_norm(x, (s.hidden_size,), layer.ln2, s.rms_norm_eps)
             gate, up = F.linear(h, layer.gate_up).chunk(2, dim=-1)
             x = x + F.linear(F.silu(gate) * up, layer.down)
         return F.linear(F.rms_norm(x, (s.hidden_size,), self.norm, s.rms_norm_eps), self.lm_head)
+
+
+class DecodeGraph:
+    """Greedy decode steps of `n` sessions captured once in a HIP graph: each replay runs
+    one whole step (metadata from the positions, the 32 layers, the LM head, argmax) and
+    advances the static tokens and positions in place, so consecutive replays decode
+    consecutive tokens with no host work between them; `logits` holds the last replay's
+    logits. The block table is static: its rows must cover every position the replays
+    reach (up to max_model_len - 1)."""
+
+    def __init__(self, model: StarKVLlamaForCausalLM, block_table: torch.Tensor, tokens: torch.Tensor,
+                 positions: torch.Tensor):
+        if model.max_model_len > block_table.shape[1] * model.block_size:
+            raise ValueError("the block table's rows must cover max_model_len positions")
+        self.model, self.block_table = model, block_table
+        self.tokens = tokens.clone()
+        self.positions = positions.clone().long()
+        self.graph = torch.cuda.CUDAGraph()
+        self._body()  # eager first: every lazy initialisation outside the capture
+        self.tokens.copy_(tokens)
+        self.positions.copy_(positions)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(self.graph):
+            self._body()
+
+    @torch.no_grad()
+    def _body(self) -> None:
+        m = self.model
+        md = decode_metadata(self.block_table, self.positions, m.block_size, m.max_model_len)
+        self.logits = m.decode_step(self.tokens, self.positions, md, in_graph=True)
+        self.tokens.copy_(self.logits.argmax(-1))
+        self.positions.add_(1)
+
+    def reset(self, tokens: torch.Tensor, positions: torch.Tensor) -> None:
+        self.tokens.copy_(tokens)
+        self.positions.copy_(positions)
+
+    def replay(self) -> None:
+        self.graph.replay()
 
 
 def decode_metadata(block_table: torch.Tensor, positions: torch.Tensor, block_size: int,

@@ -7,7 +7,8 @@ float64 oracle over the cache as it stands after that step's write: compressed l
 with oracle/ref.py's decode (bf16 codes or the 3.2-bit rows), full layers with plain
 softmax attention over the gathered K/V. Tolerance as the decode tests (max-abs 2e-2,
 mean-rel 1e-3). Also the stock model (every layer full) and the uncompressed-attention
-kernel alone against the oracle, with GQA."""
+kernel alone against the oracle, with GQA, and the step captured in a HIP graph
+(DecodeGraph) against the same steps run eagerly over the same span."""
 import numpy as np
 import pytest
 import torch
@@ -56,7 +57,8 @@ def build(cuda, tmp_path, kv_quant, stock=False):
     pages = [(L + STEPS + 15) // 16 for L in PROMPTS]
     g = torch.Generator().manual_seed(13)
     perm = (torch.randperm(sum(pages), generator=g) + 1).to(torch.int32)
-    bt = torch.zeros(len(PROMPTS), max(pages), dtype=torch.int32)
+    # Rows cover max_model_len (512) positions; columns past a request's pages hold the null block.
+    bt = torch.zeros(len(PROMPTS), 512 // 16, dtype=torch.int32)
     o = 0
     for b, p in enumerate(pages):
         bt[b, :p] = perm[o:o + p]
@@ -158,3 +160,35 @@ def test_stock_model_and_gqa_kernel(cuda, tmp_path):
                 p = np.exp(s - s.max())
                 truth[b, h] = (p / p.sum()) @ V[:, h // (Hq // Hkv)]
         assert_close(out, truth, f"stock kernel Hq={Hq} Hkv={Hkv} lens={lens} bs={bs}")
+
+
+@pytest.mark.parametrize("mode", ["bf16", "quant", "stock"])
+def test_decode_graph_replays_match_eager(cuda, tmp_path, mode):
+    """Three greedy steps replayed from one captured step equal three eager steps over the
+    graph's span bit for bit (logits and tokens), with eager work and synchronizations
+    between the replays; then a reset and a replay repeat the first step."""
+    print(f"\n[model graph] {mode}", flush=True)
+    model, bt = build(cuda, tmp_path, mode == "quant", stock=mode == "stock")
+    tokens = torch.tensor([5, 17, 999], device=cuda)
+    positions = torch.tensor(PROMPTS, device=cuda)
+    dg = M.DecodeGraph(model, bt, tokens, positions)
+    want, tok, pos = [], tokens.clone(), positions.clone()
+    for _ in range(3):
+        md = M.decode_metadata(bt, pos, 16, model.max_model_len)
+        logits = model.decode_step(tok, pos, md, in_graph=True)
+        tok = logits.argmax(-1)
+        pos = pos + 1
+        want.append((logits.clone(), tok.clone()))
+    torch.cuda.synchronize()
+    dg.reset(tokens, positions)
+    for step, (lw, tw) in enumerate(want):
+        dg.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(dg.logits, lw), f"step {step}"
+        assert torch.equal(dg.tokens, tw), f"step {step}"
+        assert torch.equal(dg.positions, positions + step + 1)
+        torch.randn(1000, device=cuda).sum().item()  # eager work between replays
+    dg.reset(tokens, positions)
+    dg.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(dg.logits, want[0][0])
