@@ -196,18 +196,36 @@ __global__ __launch_bounds__(ST_THR) void stock_decode_kernel(const StockParams 
     }
 }
 
+// One workgroup per (query head, request): the splits' maxima and sums first (thread s
+// reads split s), then every dimension's weighted sum, eight splits' loads in flight.
+constexpr int ST_MAX_SPLITS = 128;
 __global__ __launch_bounds__(128) void stock_merge_kernel(const StockParams p) {
-    const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    __shared__ float s_e[ST_MAX_SPLITS];
+    __shared__ float s_red[2][2];  // per wave: max, then weighted sum
+    const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x, w = d >> 6;
     const float* pp = p.part + ((int64_t)b * p.Hq + hq) * p.splits * 130;
-    float M = -INFINITY;
-    for (int s = 0; s < p.splits; ++s) M = fmaxf(M, pp[s * 130]);
-    float lt = 0.f, a = 0.f;
-    for (int s = 0; s < p.splits; ++s) {
-        const float ms = pp[s * 130];
-        const float e = ms == -INFINITY ? 0.f : exp2f(ms - M);
-        lt = fmaf(pp[s * 130 + 1], e, lt);
-        a = fmaf(pp[s * 130 + 2 + d], e, a);
+    const float ms = d < p.splits ? pp[d * 130] : -INFINITY;
+    const float ls = d < p.splits ? pp[d * 130 + 1] : 0.f;
+    const float mw = wave_max(ms);
+    if ((d & 63) == 0) s_red[w][0] = mw;
+    __syncthreads();
+    const float M = fmaxf(s_red[0][0], s_red[1][0]);
+    const float e = ms == -INFINITY ? 0.f : exp2f(ms - M);
+    const float lw = wave_sum(ls * e);
+    if ((d & 63) == 0) s_red[w][1] = lw;
+    if (d < p.splits) s_e[d] = e;
+    __syncthreads();
+    const float lt = s_red[0][1] + s_red[1][1];
+    float a = 0.f;
+    int s = 0;
+    for (; s + 8 <= p.splits; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = pp[(s + u) * 130 + 2 + d];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a = fmaf(v[u], s_e[s + u], a);
     }
+    for (; s < p.splits; ++s) a = fmaf(pp[s * 130 + 2 + d], s_e[s], a);
     store_f(p.out, (int64_t)b * p.o_s0 + (int64_t)hq * p.o_s1 + d, p.out_dt, a / lt);
 }
 
@@ -218,8 +236,8 @@ const void* stock_pick(int gw) {
     return gw == 1 ? (const void*)&stock_decode_kernel<CDT, 1> : (const void*)&stock_decode_kernel<CDT, 2>;
 }
 
-// Splits per (request, head group): enough workgroups to fill the device (about 4 per
-// CU), at least 8 pages per split. groups = workgroups per request and split.
+// Splits per (request, head group): enough workgroups to fill the device (3 per CU), at
+// least 8 pages per split, at most ST_MAX_SPLITS. groups = workgroups per request and split.
 int stock_splits(int n, int groups, int max_seq_len) {
     const int pages = (max_seq_len + 15) / 16;
     int dev = 0, cus = 256;
@@ -228,7 +246,11 @@ int stock_splits(int n, int groups, int max_seq_len) {
         if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0) cus = c;
     }
     const int64_t wgs = (int64_t)n * groups;
-    int s = (int)std::min<int64_t>((4 * (int64_t)cus + wgs - 1) / wgs, (int64_t)(pages + 7) / 8);
+    // Three workgroups of the kernel fit a CU at once (its registers): splits that make the
+    // grid one such round of the device, or a whole number of them, avoid a part-full last
+    // round.
+    int s = (int)std::min<int64_t>((3 * (int64_t)cus + wgs - 1) / wgs, (int64_t)(pages + 7) / 8);
+    s = std::min(s, ST_MAX_SPLITS);
     return s < 1 ? 1 : s;
 }
 
