@@ -401,10 +401,11 @@ def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, mod
         positions = pos0 + warm + steps - 1
         md = M.decode_metadata(bt, positions, 16, int(context + warm + steps))
         hid = torch.randn(n, shape.hidden_size, device=dev, generator=gg).to(torch.bfloat16)
-        attn_eager = timed(lambda: model.attention_only(hid, positions, md), warm + 5)
+        ins = model.attention_inputs(hid, positions)
+        attn_eager = timed(lambda: model.attention_only(hid, ins, md), warm + 5)
         ag = torch.cuda.CUDAGraph()
         with torch.cuda.graph(ag):
-            model.attention_only(hid, positions, md, in_graph=True)
+            model.attention_only(hid, ins, md, in_graph=True)
         attn = timed(ag.replay, warm + 5)
         del ag
         out = dict(sessions=n, tpot_ms=round(tpot, 3), tok_per_s=round(n / tpot * 1e3, 1),

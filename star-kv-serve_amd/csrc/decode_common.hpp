@@ -43,8 +43,10 @@ constexpr float LAZY_MAX = 8.f;             // log2 headroom before the running 
 //   ab     fp16  [n][TT][4][64][8]
 //   m, l   fp32  [slots][Hq]  (log2-domain reference max and sum per partial)
 //   acc    fp32  [slots][Hq][v_rank]
-//   lg     fp32  [n][Hq][lcap]  (two-pass calls only) log2-domain logits, token l of
-//                               request b at (b Hq + h) lcap + l, lcap = max_seq_len
+//   lg     fp32  [n][lcap/16][Hq][16]  (two-pass calls only) log2-domain logits, page
+//                               major: token l of request b, head h at
+//                               ((b lcap/16 + l/16) Hq + h) 16 + l % 16 (a page's logits of
+//                               every head are one 2 KB block), lcap = max_seq_len
 //                               rounded up to 16
 //   o      fp32  [n][Hq][ld]    (two-pass calls only) merged low-rank outputs
 // Two-pass calls pad acc and o rows to ld = v_rank rounded up to 4 (16-byte rows).

@@ -55,7 +55,7 @@ struct LaneAddr {
     uint32_t k[MTV];              // slot i: 8 code bytes of row lr, ranks 4 lg .. 4 lg + 3
     uint32_t vt;                  // V table entry (0, lane)
     uint32_t cv_rd[NB > 0 ? NB : 1], cv_wr[NB > 0 ? NB : 1];  // V transpose: the two codes read, the entry written
-    int lg;                       // NB = 0: this lane's logit offset in a request's rows (q head x lcap + token)
+    int lg;                       // NB = 0: this lane's logit offset in a page's block (q head x 16 + token)
     uint32_t st[(MTV + 3) / 4];   // partial-logit row of this lane's slot in each group of 4
     uint32_t sm;                  // softmax: first of the 4 rows of head lane >> 4
     uint32_t pw, pr;              // P: write (head lane >> 4, token lane & 15), read (head lane & 3)
@@ -317,7 +317,7 @@ __device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const La
     } else {
         // The logits pass: page j's logits into the request's rows, and its partial
         // (m, l) flushed right away when page j ends the request.
-        float* lgd = (float*)(p.ws + p.ws_lg) + (int64_t)cc.b * p.Hq * p.lcap + TILE_TOK * cc.k + la.lg;
+        float* lgd = (float*)(p.ws + p.ws_lg) + ((int64_t)cc.b * (p.lcap / TILE_TOK) + cc.k) * p.Hq * TILE_TOK + la.lg;
         softmax_page<FMT, true>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, TILE_TOK * cc.k, cc.lo,
                                 cc.hi, lgd);
     }
@@ -404,7 +404,7 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
             la.cv_rd[k] = base + (uint32_t)((C::V0 + (vb >> 10)) * page_stride<NBUF>() + (vb & 1023));
             la.cv_wr[k] = vt0 + vt_offset<NBUF>((((t >> 2) * 64 * NB + L) << 3) + (t & 3) * 2);
         }
-        la.lg = (lg < nh ? pw[32 + lg] : 0) * p.lcap + lr;
+        la.lg = (lg < nh ? pw[32 + lg] : 0) * TILE_TOK + lr;
         const int rslot = ((lg & 1) << 1) | (lg >> 1);  // sum_rows4 puts inputs (a, b, c, d) in rows (0, 2, 1, 3)
 #pragma unroll
         for (int g = 0; g < (MTV + 3) / 4; ++g) {

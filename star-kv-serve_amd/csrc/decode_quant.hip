@@ -82,7 +82,7 @@ struct QLane {
     uint32_t pa[NB > 0 ? NB : 1];  // P @ V A operand: P * s_out or P * s_in of head lane & 3
     uint32_t vt;                 // V table entry (0, lane)
     uint32_t cv_rd[NB > 0 ? NB : 1], cv_wr[NB > 0 ? NB : 1];  // V expansion: the byte read, the entry written
-    int lg;                      // NB = 0: this lane's logit offset in a request's rows (q head x lcap + token)
+    int lg;                      // NB = 0: this lane's logit offset in a page's block (q head x 16 + token)
     uint32_t mk;                 // outlier masks of this lane's row group (table row 0)
     uint32_t sel;                // byte permute: bytes g, g + 4 -> bytes 0, 2
     uint32_t magic;              // 0x64006400
@@ -438,7 +438,7 @@ __device__ __forceinline__ bool q_iter(QLoop& st, const DmaConst& dc, const QLan
         st.pv_moved = q_softmax<MTV, NB>(sm, la, fast, sp, nh, ksw, vsw, salpha, lane, TILE_TOK * cc.k, cc.lo, cc.hi);
     } else {
         // The logits pass: page j's logits into the request's rows.
-        float* lgd = (float*)(p.ws + p.ws_lg) + (int64_t)cc.b * p.Hq * p.lcap + TILE_TOK * cc.k + la.lg;
+        float* lgd = (float*)(p.ws + p.ws_lg) + ((int64_t)cc.b * (p.lcap / TILE_TOK) + cc.k) * p.Hq * TILE_TOK + la.lg;
         q_softmax<MTV, NB>(sm, la, fast, sp, nh, ksw, vsw, salpha, lane, TILE_TOK * cc.k, cc.lo, cc.hi, lgd);
     }
     copies_at<QSched<MTV>, NLD, BN>(MTV + 1, dc, dp, opaque_s(wave), doff);
@@ -546,7 +546,7 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
         for (int nb = 0; nb < NB; ++nb)
             la.pa[nb] = lds_addr(&s_pq[wave][64 * nb + lane < O4 ? 0 : 1][0]) + (uint32_t)(lane & 3) * TILE_TOK * 2;
         la.vt = vt0 + 8 * lane;
-        la.lg = (lg < nh ? pw[32 + lg] : 0) * p.lcap + lr;
+        la.lg = (lg < nh ? pw[32 + lg] : 0) * TILE_TOK + lr;
         // V expansion: token t = tid % 16, lane-entries L, L + 1 with L = 2 (tid / 16) + 64 k.
         const int t = tid & 15;
 #pragma unroll

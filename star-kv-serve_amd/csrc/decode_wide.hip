@@ -118,8 +118,8 @@ __device__ __forceinline__ PvPage pv_page_desc(const PvParams& p, const Cursor& 
     const uint8_t* page = p.cache + (int64_t)blk * p.c_s0 + (int64_t)row0 * p.c_s1;
     const int rows = v ? min(TILE_TOK, c.len - TILE_TOK * k) : 0;
     d.rv = buffer_rsrc(page, rows * p.c_s1);
-    const uint8_t* lg = p.ws + p.ws_lg + ((int64_t)(v ? c.b : 0) * p.Hq * p.lcap + TILE_TOK * k) * 4;
-    d.rl = buffer_rsrc(lg, v ? ((p.Hq - 1) * p.lcap + TILE_TOK) * 4 : 0);
+    const uint8_t* lg = p.ws + p.ws_lg + (((int64_t)(v ? c.b : 0) * (p.lcap / TILE_TOK) + k) * p.Hq * TILE_TOK) * 4;
+    d.rl = buffer_rsrc(lg, v ? p.Hq * TILE_TOK * 4 : 0);
     const uint8_t* m = p.ws + p.ws_m + (int64_t)(v ? c.b + g : 0) * p.Hq * 4;
     d.rm = buffer_rsrc(m, v ? ((p.Hq * 4 + 15) & ~15) : 0);
     return d;
@@ -192,7 +192,7 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
         uint32_t o = 0x80000000u;  // past every descriptor: no access
         if (ch < 2) {
             const int h = 16 * ch + (lane >> 2);
-            if (h < p.Hq) o = (uint32_t)((h * p.lcap) * 4 + 16 * (lane & 3));
+            if (h < p.Hq) o = (uint32_t)(h * 64 + 16 * (lane & 3));
         } else if (ch == 2) {
             if (4 * lane < p.Hq) o = (uint32_t)(16 * lane);
         } else if (ch < p.nch) {

@@ -181,13 +181,46 @@ class StarKVLlamaForCausalLM:
         return F.linear(out, layer.o_proj)
 
     @torch.no_grad()
-    def attention_only(self, hidden: torch.Tensor, positions: torch.Tensor, md: StarKVMetadata,
+    def attention_inputs(self, hidden: torch.Tensor, positions: torch.Tensor) -> List[tuple]:
+        """Per layer, what its attention op takes for one step with input `hidden`: the
+        rotated queries, and for an uncompressed layer the rotated keys and the values (a
+        compressed layer takes `hidden` itself: its write computes the codes)."""
+        s = self.shape
+        T = hidden.shape[0]
+        H, Hkv, D = s.num_heads, s.num_kv_heads, s.head_dim
+        res = []
+        for layer in self.layers:
+            if layer.compressed:
+                q = self.rotary.apply(positions, F.linear(hidden, layer.q_proj).view(T, H, D))
+                res.append((q.reshape(T, H * D), None, None))
+            else:
+                q, k, v = F.linear(hidden, layer.qkv_proj).split([H * D, Hkv * D, Hkv * D], dim=-1)
+                res.append((self.rotary.apply(positions, q.reshape(T, H, D)),
+                            self.rotary.apply(positions, k.reshape(T, Hkv, D)), v.reshape(T, Hkv, D).contiguous()))
+        return res
+
+    @torch.no_grad()
+    def attention_only(self, hidden: torch.Tensor, inputs: List[tuple], md: StarKVMetadata,
                        in_graph: bool = False) -> None:
-        """The KV writes and attention of every layer for one step with the same input
-        (the "attention per step" figure: cache write + attention summed over the layers,
-        as the reference's benchmark sums them, bench_serving.py:62-115)."""
-        for li in range(len(self.layers)):
-            self._attention(li, hidden, positions, md, None, in_graph)
+        """The attention ops of every layer for one step (the "attention per step" figure:
+        the cache write and the attention, summed over the layers, as the reference's
+        benchmark sums its two attention ops, bench_serving.py:62-115; the projections and
+        RoPE are outside, as there). `inputs` from attention_inputs. A compressed layer's
+        write includes its codes' GEMM (hidden @ kv_down^T), which the reference runs
+        outside the attention op (model.py:71)."""
+        T = hidden.shape[0]
+        for li, layer in enumerate(self.layers):
+            q, k, v = inputs[li]
+            if layer.compressed:
+                out = torch.empty(T, q.shape[1], dtype=self.dtype, device=self.device)
+                layer.impl.forward_from_hidden(q, hidden, self.kv_caches[li], md, out, in_full_graph=in_graph)
+            else:
+                kc, vc = self.kv_caches[li]
+                slots = md.slot_mapping[:T].clamp(min=0)
+                kc[slots // self.block_size, slots % self.block_size] = k
+                vc[slots // self.block_size, slots % self.block_size] = v
+                span = self.max_model_len if in_graph else max(md.max_seq_len, 1)
+                paged_decode_full(q, kc, vc, md.block_table[:T], md.seq_lens[:T], span, self.scale)
 
     @torch.no_grad()
     def decode_step(self, tokens: torch.Tensor, positions: torch.Tensor, md: StarKVMetadata,
