@@ -29,8 +29,14 @@ Differences from the reference, by design:
   prefill cannot serve (chunked prompts, cached context) raises before any work is
   enqueued, where the reference raises after the cache write.
 - The reference splits large decode batches so that its logits buffer stays under
-  2^26 floats (attention.py:52, 198-199). These kernels keep logits on chip and need
-  no such buffer; the decode wrappers only split batches above 1024 requests.
+  2^26 floats (attention.py:52, 198-199). The one-pass kernels keep logits on chip; the
+  decode wrappers split batches above 1024 requests, and two-pass layers (wide V) so that
+  a call's logits buffer stays under the same 2^26 floats.
+
+The rest of the reference's backend module is here too: ``build_metadata`` is its
+metadata builder's ``build`` (attention.py:80-103) on plain values, and where vLLM is
+importable, ``StarKVMetadataBuilder``, ``StarKVAttentionBackend`` and ``StarKVAttention``
+(attention.py:71-79, 254-316) wrap this implementation for vLLM.
 """
 from dataclasses import dataclass
 from typing import List, Optional
@@ -75,6 +81,51 @@ def _vllm_max_model_len() -> Optional[int]:
 
 def _vllm_in_full_graph() -> bool:
     return _HAVE_VLLM and get_forward_context().cudagraph_runtime_mode == CUDAGraphMode.FULL
+
+
+def split_decodes_and_prefills(query_start_loc_cpu, num_tokens: int, decode_threshold: int = 1):
+    """(num_decodes, num_prefills, num_decode_tokens, num_prefill_tokens) of a batch whose
+    requests are ordered decodes first: the leading requests with at most
+    `decode_threshold` query tokens are decodes. The restatement of vLLM's
+    ``split_decodes_and_prefills`` (vllm/v1/attention/backends/utils.py), which the
+    reference's builder calls (attention.py:83-84); raises ValueError if a decode follows
+    a prefill (the builder asks vLLM to reorder the batch so that none does)."""
+    qsl = [int(x) for x in query_start_loc_cpu]
+    num_reqs = len(qsl) - 1
+    lens = [qsl[i + 1] - qsl[i] for i in range(num_reqs)]
+    nd = 0
+    while nd < num_reqs and lens[nd] <= decode_threshold:
+        nd += 1
+    if any(q <= decode_threshold for q in lens[nd:]):
+        raise ValueError("decode requests must come before prefills")
+    return nd, num_reqs - nd, qsl[nd], num_tokens - qsl[nd]
+
+
+def build_metadata(num_actual_tokens: int, query_start_loc_cpu, max_seq_len: int, seq_lens: torch.Tensor,
+                   block_table: torch.Tensor, slot_mapping: torch.Tensor,
+                   seq_lens_cpu_upper_bound=None) -> StarKVMetadata:
+    """One step's StarKVMetadata from vLLM's common attention metadata (the reference's
+    ``StarKVMetadataBuilder.build``, attention.py:80-103): decodes and prefills split as
+    above; for the prefills, their query offsets rebased to 0 and their lengths (host lists,
+    as the dense prefill needs them)."""
+    nd, npf, ndt, _ = split_decodes_and_prefills(query_start_loc_cpu, num_actual_tokens, 1)
+    prefill_lens = prefill_qsl = None
+    if npf:
+        qsl = [int(x) for x in query_start_loc_cpu[nd:nd + npf + 1]]
+        prefill_qsl = [x - qsl[0] for x in qsl]
+        if seq_lens_cpu_upper_bound is not None:
+            prefill_lens = [int(x) for x in seq_lens_cpu_upper_bound[nd:nd + npf]]
+    return StarKVMetadata(num_actual_tokens=num_actual_tokens, num_decodes=nd, num_decode_tokens=ndt,
+                          num_prefills=npf, max_seq_len=int(max_seq_len), seq_lens=seq_lens,
+                          block_table=block_table, slot_mapping=slot_mapping,
+                          prefill_seq_lens_cpu=prefill_lens, prefill_query_start_loc_cpu=prefill_qsl)
+
+
+def cache_bytes_per_token(layer: StarKVLayerWeights, elem_size: int) -> int:
+    """The bytes per token a compressed layer's cache row takes: what the reference's
+    ``StarKVAttention.get_kv_cache_spec`` declares as the row of its one head slot
+    (attention.py:289-299, checkpoint.py:58-62)."""
+    return layer.cache_bytes(elem_size)
 
 
 def _attn_type_name(attn_type) -> str:
@@ -267,3 +318,81 @@ class StarKVAttentionImpl:
             o = paged_quant_decode(q, cache, md.block_table[:nd], seq_lens, span, self.row, self.k_up,
                                    self.head_of_lane, self.k_tiles, self.v_up_by_q, cs, self.scale)
         out.copy_(o)
+
+
+if _HAVE_VLLM:  # pragma: no cover - vLLM is not installed in this image
+    from typing import ClassVar
+
+    from vllm.model_executor.layers.attention.attention import (Attention, _encode_layer_name,
+                                                                unified_attention_with_output)
+    from vllm.v1.attention.backend import (AttentionBackend, AttentionCGSupport, AttentionMetadataBuilder,
+                                           CommonAttentionMetadata)
+    from vllm.v1.kv_cache_interface import FullAttentionSpec
+
+    class StarKVMetadataBuilder(AttentionMetadataBuilder[StarKVMetadata]):
+        """attention.py:71-103: decodes first; pure single-token decode batches are
+        captured whole in HIP graphs."""
+        _cudagraph_support: ClassVar[AttentionCGSupport] = AttentionCGSupport.UNIFORM_SINGLE_TOKEN_DECODE
+
+        def __init__(self, kv_cache_spec, layer_names, vllm_config, device):
+            super().__init__(kv_cache_spec, layer_names, vllm_config, device)
+            self._init_reorder_batch_threshold(1)
+
+        def build(self, common_prefix_len: int, common_attn_metadata: CommonAttentionMetadata,
+                  fast_build: bool = False) -> StarKVMetadata:
+            m = common_attn_metadata
+            return build_metadata(m.num_actual_tokens, m.query_start_loc_cpu, m.max_seq_len, m.seq_lens,
+                                  m.block_table_tensor, m.slot_mapping, m.seq_lens_cpu_upper_bound)
+
+    class StarKVAttentionBackend(AttentionBackend):
+        """attention.py:254-268."""
+        forward_includes_kv_cache_update: bool = True
+        supported_dtypes: ClassVar[List[torch.dtype]] = [torch.float16, torch.bfloat16]
+
+        @staticmethod
+        def get_name() -> str:
+            return "CUSTOM"  # registered as AttentionBackendEnum.CUSTOM by the plugin
+
+        @staticmethod
+        def get_impl_cls():
+            return StarKVAttentionImpl
+
+        @staticmethod
+        def get_builder_cls():
+            return StarKVMetadataBuilder
+
+    class StarKVAttention(Attention):
+        """An ``Attention`` whose K and V inputs are STAR-KV codes (attention.py:271-316)."""
+
+        def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int,
+                     starkv_layer: StarKVLayerWeights, rotary_emb, qkv_proj, cache_config=None, prefix: str = ""):
+            super().__init__(num_heads, head_size, scale, num_kv_heads=num_kv_heads, cache_config=cache_config,
+                             prefix=prefix, attn_backend=StarKVAttentionBackend, starkv_layer=starkv_layer,
+                             rotary_emb=rotary_emb)
+            self.starkv_layer = starkv_layer
+            self._qkv_proj = (qkv_proj,)  # not registered a second time as a child module
+
+        def get_kv_cache_spec(self, vllm_config) -> FullAttentionSpec:
+            dtype = self.kv_cache_torch_dtype
+            elem = torch.empty((), dtype=dtype).element_size()
+            return FullAttentionSpec(block_size=vllm_config.cache_config.block_size, num_kv_heads=self.num_kv_heads,
+                                     head_size=self.head_size, dtype=dtype, num_head_slots=1,
+                                     state_content_bytes=cache_bytes_per_token(self.starkv_layer, elem))
+
+        def forward(self, query, key, value, output_shape=None, output_dtype=None):
+            output = torch.empty((query.shape[0], self.num_heads * self.head_size), dtype=output_dtype or query.dtype,
+                                 device=query.device)
+            if self.use_direct_call:
+                unified_attention_with_output(query, key, value, output, self.layer_name)
+            else:
+                torch.ops.vllm.unified_attention_with_output(query, key, value, output,
+                                                             _encode_layer_name(self.layer_name))
+            return output
+
+        def process_weights_after_loading(self, act_dtype: torch.dtype):
+            super().process_weights_after_loading(act_dtype)
+            qkv = self._qkv_proj[0]
+            q_size = self.num_heads * self.head_size
+            if qkv.weight.shape[0] != q_size:  # the K/V rows are dead: the codes come from kv_down
+                qkv.weight = torch.nn.Parameter(qkv.weight.data[:q_size].contiguous(), requires_grad=False)
+            self.impl.to_device(qkv.weight.device, act_dtype)
