@@ -251,6 +251,21 @@ int starkv_quant_decode(void *stream, const void *query, int64_t q_s0, int64_t q
                         void *workspace, size_t workspace_bytes, int grid);
 
 /*
+ * The step's K and V of uncompressed layers into vLLM's paged caches
+ * [num_blocks, block_size, H_kv, 128] (what vLLM's reshape_and_cache does before its
+ * paged attention, the reference's stock layers: starkv_serve/model.py:77-81):
+ *   key, value    [n, H_kv, 128] bf16/fp16 (element strides k_s0, k_s1 / v_s0, v_s1;
+ *                 head dim contiguous), dtype as the caches'
+ *   k_cache, v_cache  element strides c_s0 (block), c_s1 (slot), c_s2 (head)
+ *   slot_mapping  [n] int32 or int64 (slot_bits 32 / 64); slot -1 writes nothing
+ * One launch for both caches.
+ */
+int starkv_stock_write(void *stream, const void *key, int64_t k_s0, int64_t k_s1, const void *value, int64_t v_s0,
+                       int64_t v_s1, int dtype, void *k_cache, void *v_cache, int64_t c_s0, int64_t c_s1,
+                       int64_t c_s2, int block_size, int64_t num_blocks, const void *slot_mapping, int slot_bits,
+                       int n, int num_kv_heads);
+
+/*
  * Uncompressed paged decode attention over bf16/fp16 K and V caches
  * [num_blocks, block_size, num_kv_heads, 128] (element strides c_s0, c_s1, c_s2, last
  * dimension contiguous): out[b, h] = softmax(scale q[b, h] . K[b, :L]) V[b, :L], L =

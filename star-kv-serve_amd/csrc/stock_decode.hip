@@ -229,6 +229,33 @@ __global__ __launch_bounds__(128) void stock_merge_kernel(const StockParams p) {
     store_f(p.out, (int64_t)b * p.o_s0 + (int64_t)hq * p.o_s1 + d, p.out_dt, a / lt);
 }
 
+// The step's K and V rows into their slots (what vLLM's reshape_and_cache does for the
+// uncompressed layers): one workgroup per token, both caches, 16 bytes per thread and
+// pass. Slot -1 (a padding token) and slots past the cache write nothing.
+struct StockWriteParams {
+    const uint8_t* key; const uint8_t* value; int64_t k_s0, k_s1, v_s0, v_s1;  // bytes
+    uint8_t* kc; uint8_t* vc; int64_t c_s0, c_s1, c_s2;                        // bytes
+    int slot_shift; int64_t num_blocks;  // slot_shift = log2(block_size)
+    const void* slots; int slot64;
+    int Hkv;
+};
+constexpr int SW_THR = 256;
+
+__global__ __launch_bounds__(SW_THR) void stock_write_kernel(const StockWriteParams p) {
+    const int t = blockIdx.x;
+    const int64_t slot = p.slot64 ? ((const int64_t*)p.slots)[t] : (int64_t)((const int32_t*)p.slots)[t];
+    if (slot < 0 || (slot >> p.slot_shift) >= p.num_blocks) return;
+    const int64_t row = (slot >> p.slot_shift) * p.c_s0 + (slot & ((1 << p.slot_shift) - 1)) * p.c_s1;
+    const int per = p.Hkv * 16;  // 16-byte granules per token and cache (256 bytes per head)
+    for (int i = threadIdx.x; i < 2 * per; i += SW_THR) {
+        const bool v = i >= per;
+        const int j = v ? i - per : i, h = j >> 4, g = j & 15;
+        const uint8_t* src = (v ? p.value + t * p.v_s0 + h * p.v_s1 : p.key + t * p.k_s0 + h * p.k_s1) + 16 * g;
+        uint8_t* dst = (v ? p.vc : p.kc) + row + h * p.c_s2 + 16 * g;
+        *(uint4*)dst = *(const uint4*)src;
+    }
+}
+
 // Query heads per workgroup: 1 (MHA) or 2 (wider groups take several workgroups per KV
 // head, whose rows they read again from L2).
 template <int CDT>
@@ -315,6 +342,35 @@ int starkv_stock_decode(void* stream, const void* query, int64_t q_s0, int64_t q
         hipLaunchKernelGGL(stock_merge_kernel, dim3(num_heads, n), dim3(128), 0, (hipStream_t)stream, p);
         SKV_HIP(hipGetLastError());
     }
+    return STARKV_OK;
+}
+
+int starkv_stock_write(void* stream, const void* key, int64_t k_s0, int64_t k_s1, const void* value, int64_t v_s0,
+                       int64_t v_s1, int dtype, void* k_cache, void* v_cache, int64_t c_s0, int64_t c_s1, int64_t c_s2,
+                       int block_size, int64_t num_blocks, const void* slot_mapping, int slot_bits, int n,
+                       int num_kv_heads) {
+    clear_error();
+    SKV_CHECK(n >= 0 && num_kv_heads >= 1, "stock_write: n=%d num_kv_heads=%d", n, num_kv_heads);
+    if (n == 0) return STARKV_OK;
+    SKV_CHECK(key && value && k_cache && v_cache && slot_mapping, "stock_write: null pointer");
+    SKV_CHECK(dtype == STARKV_BF16 || dtype == STARKV_F16, "stock_write: K/V must be bf16 or fp16");
+    SKV_CHECK(slot_bits == 32 || slot_bits == 64, "stock_write: slot_mapping must be int32 or int64");
+    int bs_shift = -1;
+    for (int sft = 0; sft < 16; ++sft)
+        if (block_size == (16 << sft)) bs_shift = sft;
+    SKV_CHECK(bs_shift >= 0, "stock_write: block_size must be 16 times a power of two");
+    const uintptr_t al = (uintptr_t)key | (uintptr_t)value | (uintptr_t)k_cache | (uintptr_t)v_cache;
+    SKV_CHECK(al % 16 == 0 && (k_s0 | k_s1 | v_s0 | v_s1 | c_s0 | c_s1 | c_s2) % 8 == 0,
+              "stock_write: rows must be 16-byte aligned");
+    StockWriteParams p;
+    p.key = (const uint8_t*)key; p.value = (const uint8_t*)value;
+    p.k_s0 = 2 * k_s0; p.k_s1 = 2 * k_s1; p.v_s0 = 2 * v_s0; p.v_s1 = 2 * v_s1;
+    p.kc = (uint8_t*)k_cache; p.vc = (uint8_t*)v_cache; p.c_s0 = 2 * c_s0; p.c_s1 = 2 * c_s1; p.c_s2 = 2 * c_s2;
+    p.slot_shift = bs_shift + 4; p.num_blocks = num_blocks;  // block_size = 16 << bs_shift
+    p.slots = slot_mapping; p.slot64 = slot_bits == 64;
+    p.Hkv = num_kv_heads;
+    hipLaunchKernelGGL(stock_write_kernel, dim3(n), dim3(SW_THR), 0, (hipStream_t)stream, p);
+    SKV_HIP(hipGetLastError());
     return STARKV_OK;
 }
 

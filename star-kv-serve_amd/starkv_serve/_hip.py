@@ -38,6 +38,8 @@ SIGNATURES = {
     "starkv_stock_decode_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "starkv_stock_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _P, _I64, _I64, _I64, _I, _I, _P, _I64, _I64, _P,
                                  _I, _I, _I, _I, _F, _P, _I64, _I64, _I, _P, _SZ]),
+    "starkv_stock_write": (_I, [_P, _P, _I64, _I64, _P, _I64, _I64, _I, _P, _P, _I64, _I64, _I64, _I, _I64, _P, _I,
+                                _I, _I]),
     "starkv_profile_begin": (_I, [_I, _I]),
     "starkv_profile_end": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "starkv_profile_times": (_I, [ctypes.POINTER(ctypes.c_double), _I]),

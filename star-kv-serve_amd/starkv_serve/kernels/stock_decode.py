@@ -37,3 +37,27 @@ def paged_decode_full(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch
         out.stride(0), out.stride(1), _hip.dtype_code(out), ws.data_ptr(), ws.numel())
     _hip.check(rc, "paged_decode_full")
     return out
+
+
+def write_kv_full(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  slot_mapping: torch.Tensor) -> None:
+    """The step's ``key`` / ``value`` [n, H_kv, 128] into the paged caches
+    [num_blocks, block_size, H_kv, 128] at ``slot_mapping`` [n] (slot -1: nothing), as
+    vLLM's reshape_and_cache does for uncompressed layers; one launch."""
+    n = key.shape[0]
+    assert key.shape == value.shape and key.shape[1:] == k_cache.shape[2:] and k_cache.shape == v_cache.shape
+    assert key.dtype == value.dtype == k_cache.dtype == v_cache.dtype and k_cache.stride() == v_cache.stride()
+    assert key.stride(-1) == 1 and value.stride(-1) == 1 and k_cache.stride(-1) == 1
+    if n == 0:
+        return
+    _hip.require_cuda(key, value, k_cache, v_cache, slot_mapping)
+    slots = slot_mapping.contiguous()
+    bits = 64 if slots.dtype == torch.int64 else 32
+    if bits == 32:
+        slots = _as_i32(slots)
+    rc = _hip.lib().starkv_stock_write(
+        _hip.stream_of(key), key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0),
+        value.stride(1), _hip.dtype_code(key), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
+        k_cache.stride(1), k_cache.stride(2), k_cache.shape[1], k_cache.shape[0], slots.data_ptr(), bits, n,
+        key.shape[1])
+    _hip.check(rc, "write_kv_full")

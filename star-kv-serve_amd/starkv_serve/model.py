@@ -11,8 +11,9 @@ keep full K/V.
   ``hidden @ [k_down; v_down]^T`` fused with the scatter or 3.2-bit pack), then the
   decode runs over the paged cache.
 - An uncompressed layer is vLLM's LlamaAttention (model.py:77-81 there): QKV, RoPE on q
-  and k, k and v into paged key / value caches [num_blocks, block_size, H_kv, 128], and
-  paged decode attention over them (``paged_decode_full``).
+  and k, k and v into paged key / value caches [num_blocks, block_size, H_kv, 128]
+  (``write_kv_full``, one launch, as vLLM's reshape_and_cache), and paged decode
+  attention over them (``paged_decode_full``).
 - Everything else is the stock Llama decoder: RMSNorm, SiLU-gated MLP, residuals, the
   final norm and the LM head.
 
@@ -32,7 +33,7 @@ import torch.nn.functional as F
 
 from starkv_serve.attention import StarKVAttentionImpl, StarKVMetadata
 from starkv_serve.checkpoint import StarKVCheckpoint
-from starkv_serve.kernels.stock_decode import paged_decode_full
+from starkv_serve.kernels.stock_decode import paged_decode_full, write_kv_full
 from starkv_serve.workloads import cos_sin_table
 
 
@@ -171,9 +172,7 @@ class StarKVLlamaForCausalLM:
             q = self.rotary.apply(positions, q.reshape(T, H, D))
             k = self.rotary.apply(positions, k.reshape(T, Hkv, D))
             kc, vc = self.kv_caches[li]
-            slots = md.slot_mapping[:T].clamp(min=0)
-            kc[slots // self.block_size, slots % self.block_size] = k
-            vc[slots // self.block_size, slots % self.block_size] = v.reshape(T, Hkv, D)
+            write_kv_full(k, v.reshape(T, Hkv, D), kc, vc, md.slot_mapping[:T])
             span = self.max_model_len if in_graph else max(md.max_seq_len, 1)
             out = paged_decode_full(q, kc, vc, md.block_table[:T], md.seq_lens[:T], span, self.scale).view(T, H * D)
         if capture is not None:
@@ -216,9 +215,7 @@ class StarKVLlamaForCausalLM:
                 layer.impl.forward_from_hidden(q, hidden, self.kv_caches[li], md, out, in_full_graph=in_graph)
             else:
                 kc, vc = self.kv_caches[li]
-                slots = md.slot_mapping[:T].clamp(min=0)
-                kc[slots // self.block_size, slots % self.block_size] = k
-                vc[slots // self.block_size, slots % self.block_size] = v
+                write_kv_full(k, v, kc, vc, md.slot_mapping[:T])
                 span = self.max_model_len if in_graph else max(md.max_seq_len, 1)
                 paged_decode_full(q, kc, vc, md.block_table[:T], md.seq_lens[:T], span, self.scale)
 

@@ -16,7 +16,7 @@ import torch
 from oracle import ref
 from starkv_serve import checkpoint as ck
 from starkv_serve import model as M
-from starkv_serve.kernels.stock_decode import paged_decode_full
+from starkv_serve.kernels.stock_decode import paged_decode_full, write_kv_full
 from test_gpu_decode import assert_close
 
 pytestmark = pytest.mark.gpu
@@ -192,3 +192,28 @@ def test_decode_graph_replays_match_eager(cuda, tmp_path, mode):
     dg.replay()
     torch.cuda.synchronize()
     assert torch.equal(dg.logits, want[0][0])
+
+
+@pytest.mark.parametrize("slot_dtype", [torch.int32, torch.int64])
+def test_stock_write_matches_index_put(cuda, slot_dtype):
+    """write_kv_full against torch's index_put on the same caches: bit-exact, slot -1
+    writes nothing, strided key/value rows (views of one QKV output), block size 32."""
+    print(f"\n[stock write] slots {slot_dtype}", flush=True)
+    g = torch.Generator().manual_seed(31)
+    nb, bs, Hkv, n = 9, 32, 4, 12
+    qkv = torch.randn(n, (8 + 2 * Hkv) * 128, generator=g).to(torch.bfloat16).to(cuda)
+    k = qkv[:, 8 * 128:(8 + Hkv) * 128].view(n, Hkv, 128)
+    v = qkv[:, (8 + Hkv) * 128:].view(n, Hkv, 128)
+    slots = torch.randperm(nb * bs, generator=g)[:n].to(slot_dtype)
+    slots[3] = -1
+    slots = slots.to(cuda)
+    kc = torch.randn(nb, bs, Hkv, 128, generator=g).to(torch.bfloat16).to(cuda)
+    vc = torch.randn(nb, bs, Hkv, 128, generator=g).to(torch.bfloat16).to(cuda)
+    want_k, want_v = kc.clone(), vc.clone()
+    ok = slots >= 0
+    s = slots[ok].long()
+    want_k[s // bs, s % bs] = k[ok]
+    want_v[s // bs, s % bs] = v[ok]
+    write_kv_full(k, v, kc, vc, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(kc, want_k) and torch.equal(vc, want_v)
