@@ -171,3 +171,26 @@ def test_writer_statistics(tmp_path):
     k0 = codes[:, :64] @ w.k_up[:64]
     assert 0.8 < k0.std().item() < 1.2
     assert sd["model.layers.0.self_attn.k_proj.head_ranks"].dtype == torch.int32
+
+
+def test_layer_the_decode_cannot_run_is_refused_at_load(tmp_path):
+    """layer_operands replays the decode's wave plan on the host: 32 heads of rank 64
+    (128 rank tiles, above the 96 one call takes) raise NotImplementedError at load time
+    instead of decoding to NaN rows."""
+    path = str(tmp_path / "wide_k.pt")
+    ck.write_fused_checkpoint(path, 1, 32, HD, 256, {0: ([64] * 32, 64)}, seed=9)
+    w = ck.load_fused_checkpoint(path, 1, 32, HD, dtype=torch.bfloat16).layers[0]
+    with pytest.raises(NotImplementedError):
+        ck.layer_operands(w, 32, torch.device("cpu"), torch.bfloat16)
+
+
+def test_side_tensors_normalised_to_contiguous_int32():
+    """The decode wrappers pass side tensors (lengths, block tables, ranks, tile tables)
+    as plain int32 arrays: strided or int64 inputs are converted, not misread."""
+    from starkv_serve.kernels.paged_decode import _as_i32
+    base = torch.arange(20, dtype=torch.int64)
+    strided = base[::2]
+    out = _as_i32(strided)
+    assert out.dtype == torch.int32 and out.is_contiguous() and torch.equal(out, strided.to(torch.int32))
+    same = torch.arange(5, dtype=torch.int32)
+    assert _as_i32(same) is same
