@@ -16,12 +16,15 @@ have settled the clocks (--min-warmup-ms):
   - `call_us_median`: the median over K more calls of the whole call, from event pairs
     the library records around each call;
   - `decode_kernel_us`: the median over K more calls of the decode kernels alone (the
-    roofline figure: `roofline.achieved` = bytes / this time).
+    roofline figure: `roofline.achieved` = bytes / this time);
+  - `call_us_graph`: the call captured once in a HIP graph, K replays back to back (mean;
+    no host work between launches, as a serving engine runs uniform decode steps).
 Extra workloads: the 3.2-bit kernel at the same shape (three rotating cache copies),
-the ragged U[1024, 8192] configurations, batch 1 x 4096, 16 x 32768 3.2-bit with the
-fused cache write in each step, the reference checkpoint's shape (K width 880, V rank
-1280 / 1290: the two-pass form), the fused cache write, and uncompressed attention
-(torch SDPA and the 100 %-HBM bound). `cpu_baseline` times the reference's math restated
+the ragged U[1024, 8192] configurations, batch 1 x 4096, 64 requests x 16 tokens, 16 x
+32768 3.2-bit with the fused cache write in each step, the reference checkpoint's shape
+(K width 880, V rank 1280 / 1290: the two-pass form), the fused cache write, uncompressed
+attention (torch SDPA, this library's paged stock kernel, the 100 %-HBM bound) and the
+Llama-2-7B-shaped model (config 4). `cpu_baseline` times the reference's math restated
 in fp32 PyTorch (oracle/torch_ref.py) on this host's cores, median of 5 runs after 1.
 
 One JSON line is printed on stdout.
@@ -103,6 +106,20 @@ def time_decode(fn, steps, warmup):
         torch.cuda.synchronize()
         t = _hip.profile_end()
         out[key] = statistics.median(t) if t else float("nan")
+    # The same call captured once in a HIP graph and replayed `steps` times back to back
+    # (how a serving engine runs uniform decode steps): no host work between the launches.
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn(0)
+    for _ in range(warmup):
+        g.replay()
+    start.record()
+    for _ in range(steps):
+        g.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    out["graph_ms"] = start.elapsed_time(stop) / steps
+    del g
     return out
 
 
@@ -163,6 +180,7 @@ def summarize(wl, t):
     f = wl.flops_per_step()
     k = t["kern_ms"]
     return dict(us_per_step=round(t["ms"] * 1e3, 2), call_us_median=round(t["call_ms"] * 1e3, 2),
+                call_us_graph=round(t["graph_ms"] * 1e3, 2),
                 decode_kernel_us=round(k * 1e3, 2), GBps=round(b / (t["ms"] * 1e-3) / 1e9, 1),
                 kernel_GBps=round(b / (k * 1e-3) / 1e9, 1), hbm_frac=round(b / (k * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                 mfma_frac=round(f / (k * 1e-3) / 1e12 / MFMA_PEAK_F16_TFLOPS, 4), bytes_per_step=int(b),
@@ -621,6 +639,8 @@ def main():
         run("quant_bs64_ragged_1k_8k", "3.2-bit, 64 requests, lengths U[1024, 8192] (config 2, 3 rotating caches)",
             lambda: summarize(*bench_quant(W.ragged_lengths(1002), K, Wm, seed=1002, copies=3)))
         run("lowrank_b1x4096", "bf16 low-rank, 1 x 4096 (config 0)", only["c0"])
+        run("lowrank_64x16_short", "bf16 low-rank, 64 requests x 16 tokens (host-bound: eager vs graph)",
+            only["short"])
         run("quant_bs16x32k_write_decode", "3.2-bit, 16 x 32768, fused write + decode per step (config 3)",
             only["c3"])
         run("lowrank_bs64x8k_w880_v1280", "bf16 low-rank, 64 x 8192, K width 880, V rank 1280 (two-pass)",
