@@ -184,8 +184,14 @@ int starkv_decode_set_path(int mode);
  *   KV head kv = h / (H_q / H_kv) at lane k_head_offsets[kv] of the token's cache row,
  *   out[b,h] = (softmax(logit) @ V_codes) @ v_up_by_q[h].
  *   query       [n, H_q, 128] (element strides q_s0, q_s1; last dim contiguous)
- *   kv_cache    [num_blocks, block_size, k_width + v_rank], element strides c_s0, c_s1,
- *               last dim contiguous; code_dtype bf16 or fp16; block_size 16 * 2^s
+ *   kv_cache    [num_blocks, block_size, >= v_col + v_rank], element strides c_s0, c_s1,
+ *               last dim contiguous; code_dtype bf16 or fp16; block_size 16 * 2^s. From
+ *               the pointer, a row holds the K lanes the call reads (k_width of them, at
+ *               k_head_offsets) and the V codes at lane v_col: v_col = k_width for a
+ *               [K | V] row; a caller that splits a layer's KV heads over calls (more than
+ *               32 query heads or 96 rank tiles) advances the pointer to a group's first
+ *               K lane and passes the distance from there to V (v_col >= k_width,
+ *               a multiple of 8)
  *   block_table [n, max_blocks] int32 (strides bt_s0, bt_s1); seq_lens [n] int32
  *   k_up        [k_width, 128] (row stride ku_s0, dtype w_dtype), k_ranks /
  *               k_head_offsets [H_kv] int32
@@ -203,10 +209,10 @@ int starkv_lowrank_decode(void *stream, const void *query, int64_t q_s0, int64_t
                           const int32_t *block_table, int64_t bt_s0, int64_t bt_s1, const int32_t *seq_lens,
                           int n, int num_heads, int num_kv_heads, int max_seq_len, const void *k_up,
                           int64_t ku_s0, int w_dtype, const int32_t *k_ranks, const int32_t *k_head_offsets,
-                          int k_width, const void *v_up_by_q, int64_t vu_s0, int64_t vu_s1, int vu_dtype,
-                          int v_rank, const void *cos_sin, int64_t cs_s0, int cs_dtype, float scale, void *out,
-                          int64_t o_s0, int64_t o_s1, int out_dtype, void *workspace, size_t workspace_bytes,
-                          int grid);
+                          int k_width, int v_col, const void *v_up_by_q, int64_t vu_s0, int64_t vu_s1,
+                          int vu_dtype, int v_rank, const void *cos_sin, int64_t cs_s0, int cs_dtype, float scale,
+                          void *out, int64_t o_s0, int64_t o_s1, int out_dtype, void *workspace,
+                          size_t workspace_bytes, int grid);
 
 /*
  * starkv_lowrank_decode with no workspace argument and no allocation: the call's
@@ -225,7 +231,7 @@ int starkv_lowrank_decode_noalloc(void *stream, const void *query, int64_t q_s0,
                                   int block_size, const int32_t *block_table, int64_t bt_s0, int64_t bt_s1,
                                   const int32_t *seq_lens, int n, int num_heads, int num_kv_heads,
                                   int max_seq_len, const void *k_up, int64_t ku_s0, int w_dtype,
-                                  const int32_t *k_ranks, const int32_t *k_head_offsets, int k_width,
+                                  const int32_t *k_ranks, const int32_t *k_head_offsets, int k_width, int v_col,
                                   const void *v_up_by_q, int64_t vu_s0, int64_t vu_s1, int vu_dtype, int v_rank,
                                   const void *cos_sin, int64_t cs_s0, int cs_dtype, float scale, void *out,
                                   int64_t o_s0, int64_t o_s1, int out_dtype, int grid);

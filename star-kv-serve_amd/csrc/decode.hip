@@ -1074,7 +1074,7 @@ int starkv_lowrank_decode(void* stream, const void* query, int64_t q_s0, int64_t
                           const int32_t* block_table, int64_t bt_s0, int64_t bt_s1, const int32_t* seq_lens, int n,
                           int num_heads, int num_kv_heads, int max_seq_len, const void* k_up, int64_t ku_s0,
                           int w_dtype, const int32_t* k_ranks, const int32_t* k_head_offsets, int k_width,
-                          const void* v_up_by_q, int64_t vu_s0, int64_t vu_s1, int vu_dtype, int v_rank,
+                          int v_col, const void* v_up_by_q, int64_t vu_s0, int64_t vu_s1, int vu_dtype, int v_rank,
                           const void* cos_sin, int64_t cs_s0, int cs_dtype, float scale, void* out, int64_t o_s0,
                           int64_t o_s1, int out_dtype, void* workspace, size_t workspace_bytes, int grid) {
     clear_error();
@@ -1082,6 +1082,8 @@ int starkv_lowrank_decode(void* stream, const void* query, int64_t q_s0, int64_t
     SKV_CHECK(num_kv_heads >= 1 && num_heads % num_kv_heads == 0, "lowrank_decode: num_heads %% num_kv_heads != 0");
     SKV_CHECK(k_width >= 16 && k_width % 16 == 0, "lowrank_decode: k_width %d must be a positive multiple of 16",
               k_width);
+    SKV_CHECK(v_col >= k_width && v_col % 8 == 0, "lowrank_decode: v_col %d must be >= k_width %d and a multiple of 8",
+              v_col, k_width);
     SKV_CHECK(query && kv_cache && block_table && seq_lens && k_up && k_ranks && k_head_offsets && v_up_by_q &&
                   cos_sin && out && workspace,
               "lowrank_decode: null pointer");
@@ -1092,12 +1094,14 @@ int starkv_lowrank_decode(void* stream, const void* query, int64_t q_s0, int64_t
     p.c_s1 = c_s1 * 2;
     p.bs_shift = block_shift(block_size);
     p.k_width = k_width;
+    p.v_col = v_col;
     CommonArgs a{query, q_s0, q_s1, q_dtype, block_table, bt_s0, bt_s1, seq_lens, n, num_heads, num_kv_heads,
                  max_seq_len, k_up, ku_s0, w_dtype, k_ranks, k_head_offsets, nullptr, nullptr, nullptr,
                  v_up_by_q, vu_s0, vu_s1, vu_dtype, v_rank, cos_sin, cs_s0, cs_dtype, scale, out, o_s0, o_s1,
                  out_dtype, workspace, workspace_bytes, grid};
     const int TT = (num_heads / num_kv_heads) * (k_width / 16);
-    return decode_common(p, a, code_dtype == STARKV_BF16 ? FMT_BF16 : FMT_F16, (k_width + v_rank) * 2, TT,
+    // A row holds, from the cache pointer, the K lanes read and then the V codes at v_col.
+    return decode_common(p, a, code_dtype == STARKV_BF16 ? FMT_BF16 : FMT_F16, (v_col + v_rank) * 2, TT,
                          (hipStream_t)stream);
 }
 
@@ -1106,7 +1110,8 @@ int starkv_lowrank_decode_noalloc(void* stream, const void* query, int64_t q_s0,
                                   const int32_t* block_table, int64_t bt_s0, int64_t bt_s1, const int32_t* seq_lens,
                                   int n, int num_heads, int num_kv_heads, int max_seq_len, const void* k_up,
                                   int64_t ku_s0, int w_dtype, const int32_t* k_ranks, const int32_t* k_head_offsets,
-                                  int k_width, const void* v_up_by_q, int64_t vu_s0, int64_t vu_s1, int vu_dtype,
+                                  int k_width, int v_col, const void* v_up_by_q, int64_t vu_s0, int64_t vu_s1,
+                                  int vu_dtype,
                                   int v_rank, const void* cos_sin, int64_t cs_s0, int cs_dtype, float scale,
                                   void* out, int64_t o_s0, int64_t o_s1, int out_dtype, int grid) {
     clear_error();
@@ -1124,7 +1129,7 @@ int starkv_lowrank_decode_noalloc(void* stream, const void* query, int64_t q_s0,
     if (rc) return rc;
     return starkv_lowrank_decode(stream, query, q_s0, q_s1, q_dtype, kv_cache, c_s0, c_s1, code_dtype, block_size,
                                  block_table, bt_s0, bt_s1, seq_lens, n, num_heads, num_kv_heads, max_seq_len, k_up,
-                                 ku_s0, w_dtype, k_ranks, k_head_offsets, k_width, v_up_by_q, vu_s0, vu_s1,
+                                 ku_s0, w_dtype, k_ranks, k_head_offsets, k_width, v_col, v_up_by_q, vu_s0, vu_s1,
                                  vu_dtype, v_rank, cos_sin, cs_s0, cs_dtype, scale, out, o_s0, o_s1, out_dtype, ws,
                                  NOALLOC_SCRATCH_BYTES, grid);
 }

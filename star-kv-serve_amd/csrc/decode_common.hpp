@@ -97,6 +97,7 @@ struct DecodeParams {
     int bs_shift;                                  // block_size = 16 << bs_shift
     const int32_t* bt; int bt_s0, bt_s1;
     int n, Hq, TT, k_width, v_rank;
+    int v_col;                                     // bf16/fp16: first V lane of a row (from the cache pointer)
     int ks_off, vs_off, vq_off, v_nout, v_nbo;     // QuantRow (3.2-bit)
     int row_g;                                     // row granules (16 B)
     int nch, lds_bytes;                            // 1 KB chunks copied per page, dynamic LDS bytes

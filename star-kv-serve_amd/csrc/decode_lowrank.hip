@@ -453,7 +453,7 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
             if constexpr (NB > 0) {
                 const int vb = (ch - C::V0) * 1024 + 16 * lane;  // byte inside the V rows
                 const int row = vb / C::VPITCH, col = vb % C::VPITCH;
-                if (col < 2 * p.v_rank) off = (uint32_t)(row * (int)p.c_s1 + 2 * p.k_width + col);
+                if (col < 2 * p.v_rank) off = (uint32_t)(row * (int)p.c_s1 + 2 * p.v_col + col);
             }
         } else if (ch < p.nch) {
             const int Tc = 2 * (ch - C::K0) + (lane >> 5), r = (lane >> 1) & 15, h = lane & 1;

@@ -580,7 +580,8 @@ struct PvPlan {
 };
 
 // min_windows (bf16/fp16): at least this many column windows, when each can keep 4 blocks.
-static PvPlan pv_plan(int fmt, int k_width, int v_rank, int vs_off, int vq_off, int v_bytes, int min_windows = 1) {
+// v_col (bf16/fp16): the first V lane of a row.
+static PvPlan pv_plan(int fmt, int v_col, int v_rank, int vs_off, int vq_off, int v_bytes, int min_windows = 1) {
     PvPlan pl{};
     int max_units;
     if (fmt == FMT_Q4) {
@@ -589,7 +590,7 @@ static PvPlan pv_plan(int fmt, int k_width, int v_rank, int vs_off, int vq_off, 
         pl.units = (pl.ng + 1) / 2;
         max_units = 32;  // 2 blocks each
     } else {
-        pl.v_off = 2 * k_width;
+        pl.v_off = 2 * v_col;
         pl.units = (v_rank + 31) / 32;
         max_units = 64;
     }
@@ -626,8 +627,8 @@ int launch_pv(const DecodeParams& p, int fmt, int grid, hipStream_t stream) {
     const int v_bytes = p.v_nbo + (p.v_rank - p.v_nout + 1) / 2;
     // A grid short of the CUs (few requests) takes more, narrower windows side by side.
     const int cus = device_cus();
-    PvPlan pl = pv_plan(fmt, p.k_width, p.v_rank, p.vs_off, p.vq_off, v_bytes, (cus + grid - 1) / grid);
-    if (!pl.ok) pl = pv_plan(fmt, p.k_width, p.v_rank, p.vs_off, p.vq_off, v_bytes);
+    PvPlan pl = pv_plan(fmt, p.v_col, p.v_rank, p.vs_off, p.vq_off, v_bytes, (cus + grid - 1) / grid);
+    if (!pl.ok) pl = pv_plan(fmt, p.v_col, p.v_rank, p.vs_off, p.vq_off, v_bytes);
     SKV_CHECK(pl.ok, "decode: no P @ V window fits in LDS (v_rank %d)", p.v_rank);
     PvParams a;
     memset(&a, 0, sizeof(a));

@@ -10,7 +10,7 @@ import os
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstarkv_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 F32, F16, BF16 = 0, 1, 2
 CACHE_Q3_2 = 16  # cache kind of the 3.2-bit QuantRow cache
@@ -48,11 +48,11 @@ SIGNATURES = {
     "starkv_decode_set_path": (_I, [_I]),
     "starkv_decode_layer_fits": (_I, [_I, _I, _I, ctypes.POINTER(ctypes.c_int32), _I]),
     "starkv_lowrank_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _I, _P, _I64, _I64, _P, _I,
-                                   _I, _I, _I, _P, _I64, _I, _P, _P, _I, _P, _I64, _I64, _I, _I, _P, _I64,
+                                   _I, _I, _I, _P, _I64, _I, _P, _P, _I, _I, _P, _I64, _I64, _I, _I, _P, _I64,
                                    _I, _F, _P, _I64, _I64, _I, _P, _SZ, _I]),
     "starkv_lowrank_decode_noalloc": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _I, _P, _I64, _I64, _P,
-                                           _I, _I, _I, _I, _P, _I64, _I, _P, _P, _I, _P, _I64, _I64, _I, _I, _P,
-                                           _I64, _I, _F, _P, _I64, _I64, _I, _I]),
+                                           _I, _I, _I, _I, _P, _I64, _I, _P, _P, _I, _I, _P, _I64, _I64, _I, _I,
+                                           _P, _I64, _I, _F, _P, _I64, _I64, _I, _I]),
     "starkv_quant_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _P, _I64, _I64, _P, _I, _I, _I,
                                  _I, _I, _I, _P, _I64, _I, _P, _P, _P, _P, _I64, _I64, _I, _P, _I64, _I, _F,
                                  _P, _I64, _I64, _I, _P, _SZ, _I]),

@@ -36,6 +36,7 @@ import torch
 
 from starkv_serve import _hip
 
+from starkv_serve.kernels.paged_decode import kv_head_groups
 from starkv_serve.kernels.paged_quant import HADAMARD_SEED, QuantRow, block_hadamard, k_tables, n_outlier
 
 K_ALIGN = 16  # stored K width per head: rank rounded up to this (one MFMA rank tile)
@@ -196,16 +197,18 @@ def layer_operands(w: StarKVLayerWeights, num_heads: int, device, dtype: torch.d
     if num_heads % H:
         raise ValueError(f"{num_heads} query heads for {H} KV heads")
     # Refuse at load time a layer the decode kernels cannot run (rather than NaN rows
-    # at serving time): the test the library applies (starkv_decode_layer_fits). A 3.2-bit
-    # GQA layer is refused by StarKVAttentionImpl itself, as the reference does
-    # (attention.py:116-117).
-    kind = _hip.CACHE_Q3_2 if w.kv_quant else _hip.BF16
-    if (not w.kv_quant or num_heads == H) and not _hip.layer_fits(kind, num_heads, H, w.k_head_ranks.tolist(),
-                                                                   w.v_rank):
+    # at serving time): the test the library applies (starkv_decode_layer_fits). A bf16/fp16
+    # layer beyond one call runs as KV-head groups (kv_head_groups raises when a single KV
+    # head does not fit). A 3.2-bit GQA layer is refused by StarKVAttentionImpl itself, as
+    # the reference does (attention.py:116-117).
+    ranks = w.k_head_ranks.tolist()
+    if not w.kv_quant:
+        kv_head_groups(_hip.BF16, num_heads, ranks, w.v_rank)
+    elif num_heads == H and not _hip.layer_fits(_hip.CACHE_Q3_2, num_heads, H, ranks, w.v_rank):
         raise NotImplementedError(
-            f"STAR-KV HIP decode: layer with {num_heads} query heads over K ranks {w.k_head_ranks.tolist()} and "
-            f"V rank {w.v_rank} does not fit the decode kernels (at most 32 query heads, 96 rank tiles of 16, "
-            f"16 tiles per decode wave after whole-head balancing, V rank 4096)")
+            f"STAR-KV HIP decode: 3.2-bit layer with {num_heads} heads over K ranks {ranks} and "
+            f"V rank {w.v_rank} does not fit the decode kernels (at most 32 heads, 96 rank tiles of 16, "
+            f"16 tiles per decode wave after whole-head balancing)")
     Hd = w.k_up.shape[1]
     v_up = w.v_up.to(device=device, dtype=dtype)
     v_up_by_q = (v_up.view(H, Hd, w.v_rank).repeat_interleave(num_heads // H, dim=0)

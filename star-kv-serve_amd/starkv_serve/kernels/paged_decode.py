@@ -6,8 +6,14 @@ dtype). The work runs in the HIP library (``libstarkv_hip.so``) on the current
 stream: a prep launch (token prefix sums and wave plan in one workgroup, the query
 folded into each head's basis in the others), one persistent decode kernel that
 streams every cache page once through LDS with the K logits on MFMA and split-K
-partials, and a merge that also lifts the low-rank output through ``v_up_by_q``. No host synchronisation; the grid
-is a function of ``(n, max_seq_len)`` only, so the call can be graph-captured.
+partials, and a merge that also lifts the low-rank output through ``v_up_by_q``. No host
+synchronisation; the grid is a function of ``(n, max_seq_len)`` only, so the call can be
+graph-captured.
+
+One library call takes at most 32 query heads and 96 rank tiles (a rank tile is 16 K lanes
+seen by one query head). A larger layer (48- or 64-head MHA, wide GQA) is decoded as
+groups of consecutive KV heads, one call per group: each call reads its group's K lanes
+and the whole V code block, and writes its group's query heads (``kv_head_groups``).
 
 Layout contract (reference paged_decode.py:150-174, attention.py:158-160):
   query          [n, H_q, 128], RoPE applied
@@ -46,10 +52,14 @@ MAX_LOGITS_PER_LAUNCH = 1 << 26
 _cs_cache = {}  # id(table) -> (weak reference to the table, its version, fp16 copy)
 
 
-def _forget(key, r):
-    entry = _cs_cache.get(key)
+def _forget_in(cache, key, r):
+    entry = cache.get(key)
     if entry is not None and entry[0] is r:
-        del _cs_cache[key]
+        del cache[key]
+
+
+def _forget(key, r):
+    _forget_in(_cs_cache, key, r)
 
 
 def cos_sin_for_kernel(cos_sin_cache: torch.Tensor) -> torch.Tensor:
@@ -84,6 +94,64 @@ def rows_per_launch(cache_kind: int, num_heads: int, k_width: int, v_rank: int, 
         lcap = (int(max_seq_len) + 15) // 16 * 16
         rows = max(1, min(rows, MAX_LOGITS_PER_LAUNCH // (num_heads * lcap)))
     return rows
+
+
+def kv_head_groups(cache_kind: int, num_heads: int, k_ranks, v_rank: int) -> list:
+    """KV-head ranges ``[(g0, g1), ...]`` decoded by one library call each: the whole layer
+    when one call takes it, else greedy runs of consecutive KV heads, each as long as one
+    call takes it. Raises NotImplementedError when a single KV head does not fit (more than
+    32 query heads per KV head, or a rank above 1536 / heads per KV head)."""
+    ranks = [int(r) for r in k_ranks]
+    hkv = len(ranks)
+    if _hip.layer_fits(cache_kind, num_heads, hkv, ranks, v_rank):
+        return [(0, hkv)]
+    per = num_heads // hkv
+    groups, g0 = [], 0
+    while g0 < hkv:
+        if not _hip.layer_fits(cache_kind, per, 1, ranks[g0:g0 + 1], v_rank):
+            raise NotImplementedError(f"STAR-KV HIP decode: KV head {g0} (rank {ranks[g0]}, {per} query heads, "
+                                      f"v_rank {v_rank}) does not fit one decode call")
+        g1 = g0 + 1
+        while g1 < hkv and _hip.layer_fits(cache_kind, per * (g1 + 1 - g0), g1 + 1 - g0, ranks[g0:g1 + 1], v_rank):
+            g1 += 1
+        groups.append((g0, g1))
+        g0 = g1
+    return groups
+
+
+MAX_HEADS_PER_CALL = 32
+MAX_TILES_PER_CALL = 96
+
+# Host copies of device int tensors (KV-head ranks and offsets of a layer split into
+# groups), keyed like the cos/sin copies: the split needs them on the host, and reading
+# them once per layer keeps the decode free of host synchronisation afterwards.
+_host_cache = {}  # id(tensor) -> (weak reference, its version, list of ints)
+_groups_cache = {}  # (kind, H, ranks, v_rank) -> kv_head_groups(...)
+
+
+def _host_ints(t: torch.Tensor) -> list:
+    if not t.is_cuda:
+        return [int(x) for x in t.tolist()]
+    key = id(t)
+    hit = _host_cache.get(key)
+    if hit is not None and hit[0]() is t and hit[1] == t._version:
+        return hit[2]
+    vals = [int(x) for x in t.tolist()]
+    _host_cache[key] = (weakref.ref(t, lambda r, k=key: _forget_in(_host_cache, k, r)), t._version, vals)
+    return vals
+
+
+def _groups_for(kind, num_heads, num_kv_heads, k_width, k_ranks, v_rank):
+    # A layer within one call's heads and tiles runs as one call without reading its
+    # ranks on the host (the library reports a wave plan that does not fit as NaN rows).
+    if num_heads <= MAX_HEADS_PER_CALL and num_heads // num_kv_heads * (k_width // 16) <= MAX_TILES_PER_CALL:
+        return [(0, num_kv_heads)]
+    ranks = _host_ints(k_ranks)
+    key = (kind, num_heads, tuple(ranks), v_rank)
+    g = _groups_cache.get(key)
+    if g is None:
+        g = _groups_cache[key] = kv_head_groups(kind, num_heads, ranks, v_rank)
+    return g
 
 
 def paged_starkv_decode(
@@ -130,26 +198,41 @@ def paged_starkv_decode(
     cs = cos_sin_for_kernel(cos_sin_cache)
     block_table = _as_i32(block_table)
     seq_lens = _as_i32(seq_lens)
-    k_ranks = _as_i32(k_ranks)
-    k_head_offsets = _as_i32(k_head_offsets)
     kind = _hip.dtype_code(kv_cache)
-    step = rows_per_launch(kind, num_heads, int(k_width), v_rank, int(max_seq_len))
     stream = _hip.stream_of(query)
-    for s in range(0, n, step):
-        e = min(n, s + step)
-        m = e - s
-        grid = L.starkv_decode_grid_for(kind, m, num_heads, num_kv_heads, int(k_width), v_rank, int(max_seq_len))
-        ws = torch.empty(L.starkv_decode_workspace_bytes(kind, m, num_heads, num_kv_heads, int(k_width), v_rank,
-                                                         int(max_seq_len), grid),
-                         dtype=torch.uint8, device=query.device)
-        q, bt, o = query[s:e], block_table[s:e], out[s:e]
-        rc = L.starkv_lowrank_decode(
-            stream, q.data_ptr(), q.stride(0), q.stride(1), _hip.dtype_code(q),
-            kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1), kind, kv_cache.shape[1],
-            bt.data_ptr(), bt.stride(0), bt.stride(1), seq_lens[s:e].data_ptr(), m, num_heads, num_kv_heads,
-            int(max_seq_len), k_up.data_ptr(), k_up.stride(0), _hip.dtype_code(k_up), k_ranks.data_ptr(),
-            k_head_offsets.data_ptr(), int(k_width), v_up_by_q.data_ptr(), v_up_by_q.stride(0), v_up_by_q.stride(1),
-            _hip.dtype_code(v_up_by_q), v_rank, cs.data_ptr(), cs.stride(0), _hip.dtype_code(cs), float(scale),
-            o.data_ptr(), o.stride(0), o.stride(1), _hip.dtype_code(o), ws.data_ptr(), ws.numel(), grid)
-        _hip.check(rc, "paged_starkv_decode")
+    k_width, max_seq_len = int(k_width), int(max_seq_len)
+    per = num_heads // num_kv_heads
+    groups = _groups_for(kind, num_heads, num_kv_heads, k_width, k_ranks, v_rank)
+    if len(groups) == 1:
+        parts = [(query, out, kv_cache, k_up, _as_i32(k_ranks), _as_i32(k_head_offsets), v_up_by_q, num_heads,
+                  num_kv_heads, k_width)]
+    else:
+        offs = _host_ints(k_head_offsets)
+        ranks = _host_ints(k_ranks)
+        parts = []
+        for g0, g1 in groups:
+            lo = offs[g0]
+            kw = sum((r + 15) // 16 * 16 for r in ranks[g0:g1])
+            parts.append((query[:, per * g0:per * g1], out[:, per * g0:per * g1], kv_cache[..., lo:],
+                          k_up[lo:lo + kw], _as_i32(k_ranks[g0:g1]), _as_i32(k_head_offsets[g0:g1] - lo),
+                          v_up_by_q[per * g0:per * g1], per * (g1 - g0), g1 - g0, kw))
+    for qg, og, cg, kug, krg, kog, vug, hq, hkv, kw in parts:
+        v_col = k_width - (cg.data_ptr() - kv_cache.data_ptr()) // kv_cache.element_size()
+        step = rows_per_launch(kind, hq, kw, v_rank, max_seq_len)
+        for s in range(0, n, step):
+            e = min(n, s + step)
+            m = e - s
+            grid = L.starkv_decode_grid_for(kind, m, hq, hkv, kw, v_rank, max_seq_len)
+            ws = torch.empty(L.starkv_decode_workspace_bytes(kind, m, hq, hkv, kw, v_rank, max_seq_len, grid),
+                             dtype=torch.uint8, device=query.device)
+            q, bt, o = qg[s:e], block_table[s:e], og[s:e]
+            rc = L.starkv_lowrank_decode(
+                stream, q.data_ptr(), q.stride(0), q.stride(1), _hip.dtype_code(q),
+                cg.data_ptr(), cg.stride(0), cg.stride(1), kind, cg.shape[1],
+                bt.data_ptr(), bt.stride(0), bt.stride(1), seq_lens[s:e].data_ptr(), m, hq, hkv,
+                max_seq_len, kug.data_ptr(), kug.stride(0), _hip.dtype_code(kug), krg.data_ptr(),
+                kog.data_ptr(), kw, v_col, vug.data_ptr(), vug.stride(0), vug.stride(1),
+                _hip.dtype_code(vug), v_rank, cs.data_ptr(), cs.stride(0), _hip.dtype_code(cs), float(scale),
+                o.data_ptr(), o.stride(0), o.stride(1), _hip.dtype_code(o), ws.data_ptr(), ws.numel(), grid)
+            _hip.check(rc, "paged_starkv_decode")
     return out

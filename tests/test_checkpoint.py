@@ -174,14 +174,49 @@ def test_writer_statistics(tmp_path):
 
 
 def test_layer_the_decode_cannot_run_is_refused_at_load(tmp_path):
-    """layer_operands replays the decode's wave plan on the host: 32 heads of rank 64
-    (128 rank tiles, above the 96 one call takes) raise NotImplementedError at load time
-    instead of decoding to NaN rows."""
+    """layer_operands replays the decode's wave plan on the host: a head of rank 272
+    (17 rank tiles, above the 16 a decode wave holds) raises NotImplementedError at load
+    time instead of decoding to NaN rows; 32 heads of rank 64 (128 rank tiles, above the
+    96 one call takes) load, as KV-head groups."""
     path = str(tmp_path / "wide_k.pt")
-    ck.write_fused_checkpoint(path, 1, 32, HD, 256, {0: ([64] * 32, 64)}, seed=9)
-    w = ck.load_fused_checkpoint(path, 1, 32, HD, dtype=torch.bfloat16).layers[0]
+    ck.write_fused_checkpoint(path, 2, 32, HD, 256, {0: ([272] + [16] * 31, 64), 1: ([64] * 32, 64)}, seed=9)
+    layers = ck.load_fused_checkpoint(path, 2, 32, HD, dtype=torch.bfloat16).layers
     with pytest.raises(NotImplementedError):
-        ck.layer_operands(w, 32, torch.device("cpu"), torch.bfloat16)
+        ck.layer_operands(layers[0], 32, torch.device("cpu"), torch.bfloat16)
+    ck.layer_operands(layers[1], 32, torch.device("cpu"), torch.bfloat16)
+
+
+@pytest.mark.parametrize("H,ranks,v_rank,want", [
+    (32, [32] * 8, 64, None),                              # 64 tiles: fits one call
+    (32, [64] * 32, 64, [(0, 24), (24, 32)]),              # MHA, 128 tiles: 96 + 32
+    (32, [64] * 8, 64, [(0, 6), (6, 8)]),                  # GQA 4 heads per KV head, 128 tiles
+    (48, [16] * 48, 64, [(0, 32), (32, 48)]),              # 48 heads: 32 + 16
+    (64, [32] * 64, 1280, [(0, 32), (32, 64)]),            # two-pass layers split the same way
+    (32, [128] * 8, 64, [(0, 3), (3, 6), (6, 8)]),         # GQA 4 heads per KV head of 8 tiles: 96 tiles a call
+])
+def test_kv_head_groups_partition(H, ranks, v_rank, want):
+    """kv_head_groups: consecutive KV-head runs that cover the layer once, each a shape one
+    library call takes (the host test the library applies), each as long as possible."""
+    from starkv_serve import _hip
+    from starkv_serve.kernels.paged_decode import kv_head_groups
+    g = kv_head_groups(_hip.BF16, H, ranks, v_rank)
+    hkv = len(ranks)
+    per = H // hkv
+    assert g == (want or [(0, hkv)])
+    assert g[0][0] == 0 and g[-1][1] == hkv and all(a[1] == b[0] for a, b in zip(g, g[1:]))
+    for g0, g1 in g:
+        assert _hip.layer_fits(_hip.BF16, per * (g1 - g0), g1 - g0, ranks[g0:g1], v_rank)
+        if g1 < hkv:  # one more KV head would not fit
+            assert not _hip.layer_fits(_hip.BF16, per * (g1 + 1 - g0), g1 + 1 - g0, ranks[g0:g1 + 1], v_rank)
+
+
+def test_kv_head_groups_refuses_a_kv_head_that_does_not_fit():
+    from starkv_serve import _hip
+    from starkv_serve.kernels.paged_decode import kv_head_groups
+    with pytest.raises(NotImplementedError):
+        kv_head_groups(_hip.BF16, 64, [16], 64)               # 64 query heads on one KV head
+    with pytest.raises(NotImplementedError):
+        kv_head_groups(_hip.BF16, 32, [208] * 4, 64)          # 8 heads x 13 tiles = 104 > 96
 
 
 def test_side_tensors_normalised_to_contiguous_int32():

@@ -72,7 +72,7 @@ def run_lowrank(wl_gpu, grid=None):
                                  bt.data_ptr(), bt.stride(0), bt.stride(1), sl.data_ptr(), n, H, Hkv,
                                  wl_gpu.max_seq_len, U.data_ptr(), U.stride(0), _hip.dtype_code(U),
                                  wl_gpu.k_ranks.data_ptr(), wl_gpu.k_head_offsets.data_ptr(), wl_gpu.k_width,
-                                 vq.data_ptr(), vq.stride(0), vq.stride(1), _hip.dtype_code(vq), wl_gpu.v_rank,
+                                 wl_gpu.k_width, vq.data_ptr(), vq.stride(0), vq.stride(1), _hip.dtype_code(vq), wl_gpu.v_rank,
                                  cs.data_ptr(), cs.stride(0), _hip.dtype_code(cs), wl_gpu.scale, out.data_ptr(),
                                  out.stride(0), out.stride(1), _hip.dtype_code(out), ws.data_ptr(), ws.numel(), grid)
     _hip.check(rc, "lowrank_decode")
@@ -96,6 +96,12 @@ LOWRANK_CASES = {
     # pages too large for three LDS buffers: the two-buffer layout
     "wide_k1376": ([300, 17, 1024], dict(ranks=[48] * 22 + [32] * 10)),
     "wide_k1536_v256": ([150, 33], dict(ranks=[48] * 32, v_rank=256)),
+    # beyond one call's 32 heads / 96 rank tiles: KV-head groups (v_col past the group's K)
+    "groups_mha_rank64": ([250, 31, 1], dict(ranks=[64] * 32)),
+    "groups_gqa_kv8_rank64": ([300, 17, 64], dict(num_kv_heads=8, ranks=[64] * 8)),
+    "groups_mha_h48": ([200, 33, 5], dict(num_heads=48)),
+    "groups_mha_h48_strided": ([120, 16], dict(num_heads=48, col_pad=40)),
+    "groups_mha_h64_two_pass": ([150, 17], dict(num_heads=64, ranks=[32] * 40 + [16] * 24, v_rank=1280)),
 }
 
 

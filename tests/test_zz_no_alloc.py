@@ -23,7 +23,7 @@ def decode(g, noalloc):
     args = [_hip.stream_of(q), q.data_ptr(), q.stride(0), q.stride(1), _hip.dtype_code(q), kv.data_ptr(),
             kv.stride(0), kv.stride(1), _hip.dtype_code(kv), kv.shape[1], bt.data_ptr(), bt.stride(0), bt.stride(1),
             sl.data_ptr(), n, H, Hkv, g.max_seq_len, U.data_ptr(), U.stride(0), _hip.dtype_code(U),
-            g.k_ranks.data_ptr(), g.k_head_offsets.data_ptr(), g.k_width, vq.data_ptr(), vq.stride(0), vq.stride(1),
+            g.k_ranks.data_ptr(), g.k_head_offsets.data_ptr(), g.k_width, g.k_width, vq.data_ptr(), vq.stride(0), vq.stride(1),
             _hip.dtype_code(vq), g.v_rank, cs.data_ptr(), cs.stride(0), _hip.dtype_code(cs), g.scale, out.data_ptr(),
             out.stride(0), out.stride(1), _hip.dtype_code(out)]
     if noalloc:
@@ -58,6 +58,6 @@ def test_noalloc_refuses_oversized_calls(cuda):
     rc = L.starkv_lowrank_decode_noalloc(_hip.stream_of(q), q.data_ptr(), 0, 0, _hip.BF16, g.kv_cache.data_ptr(), 0,
                                          0, _hip.BF16, 16, g.block_table.data_ptr(), 0, 0, g.seq_lens.data_ptr(),
                                          1024, 32, 32, 32768, g.k_up.data_ptr(), 128, _hip.BF16, g.k_ranks.data_ptr(),
-                                         g.k_head_offsets.data_ptr(), 1280, g.v_up_by_q.data_ptr(), 0, 0, _hip.BF16,
-                                         1280, 0, 128, _hip.F16, 1.0, 0, 0, 0, _hip.BF16, 256)
+                                         g.k_head_offsets.data_ptr(), 1280, 1280, g.v_up_by_q.data_ptr(), 0, 0,
+                                         _hip.BF16, 1280, 0, 128, _hip.F16, 1.0, 0, 0, 0, _hip.BF16, 256)
     assert rc != 0 and b"fixed scratch" in L.starkv_last_error()
