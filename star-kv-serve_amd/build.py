@@ -1,8 +1,10 @@
-"""Build the HIP library in-tree: csrc/*.hip -> starkv_serve/libstarkv_hip.so (gfx950).
+"""Build the HIP library in-tree: csrc/*.hip -> starkv_serve/libstarkv_hip.so (gfx950),
+then the torch operator library csrc/torch_ops.cpp -> starkv_serve/libstarkv_torch.so
+(torch.ops.starkv, linked against libstarkv_hip.so).
 
     python star-kv-serve_amd/build.py
 
-Each source compiles in its own hipcc process (in parallel), then one link step.
+Each HIP source compiles in its own hipcc process (in parallel), then one link step.
 """
 import os
 import subprocess
@@ -12,6 +14,8 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "starkv_serve", "libstarkv_hip.so")
+OPS_OUT = os.path.join(HERE, "starkv_serve", "libstarkv_torch.so")
+CXX = os.environ.get("CXX", "g++")
 BUILD = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -39,14 +43,36 @@ def build(verbose: bool = True) -> str:
     with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = OUT + ".tmp%d" % os.getpid()
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-soname,libstarkv_hip.so", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, OUT)
     if verbose:
         print(f"built {OUT}")
+    build_ops(verbose)
     return OUT
+
+
+def build_ops(verbose: bool = True) -> str:
+    """torch_ops.cpp -> libstarkv_torch.so: host C++ over torch's headers (no device code),
+    linked against libstarkv_hip.so found beside it at load time."""
+    import torch
+    tdir = os.path.dirname(torch.__file__)
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = OPS_OUT + ".tmp%d" % os.getpid()
+    cmd = [CXX, "-std=c++17", "-O2", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", f"-I{tdir}/include", f"-I{tdir}/include/torch/csrc/api/include",
+           "-I/opt/rocm/include", os.path.join(CSRC, "torch_ops.cpp"), "-o", tmp,
+           f"-L{os.path.dirname(OUT)}", "-lstarkv_hip", f"-L{tdir}/lib", "-lc10", "-ltorch_cpu", "-lc10_hip",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tdir}/lib"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"torch_ops.cpp failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, OPS_OUT)
+    if verbose:
+        print(f"built {OPS_OUT}")
+    return OPS_OUT
 
 
 if __name__ == "__main__":

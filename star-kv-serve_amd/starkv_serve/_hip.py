@@ -1,8 +1,16 @@
-"""ctypes binding of libstarkv_hip.so, the C ABI declared in include/starkv_hip.h.
+"""Bindings of libstarkv_hip.so, the C ABI declared in include/starkv_hip.h.
 
-Tensors cross the boundary as data pointers, strides and dtype codes; streams as
-the current HIP stream handle. There is no fallback: if the library is missing
-or fails to load, every entry point raises.
+Two routes, one library instance:
+- ``ops()``: ``torch.ops.starkv``, the operator library libstarkv_torch.so
+  (csrc/torch_ops.cpp). The kernel wrappers launch through it: tensors go in as
+  tensors, the workspace comes from torch's caching allocator and the launch goes on
+  the current HIP stream.
+- ``lib()``: ctypes over the C ABI itself, for the host-only queries (grids,
+  workspace sizes, layer checks, the decode-form switch, timing) and for tests that
+  drive the C ABI directly. Tensors cross it as data pointers, strides and dtype codes.
+
+There is no fallback: if either library is missing or fails to load, every entry
+point raises.
 """
 import ctypes
 import os
@@ -10,6 +18,7 @@ import os
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstarkv_hip.so")
+OPS_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstarkv_torch.so")
 ABI_VERSION = 3
 
 F32, F16, BF16 = 0, 1, 2
@@ -79,6 +88,24 @@ def lib():
     return _LIB
 
 
+_OPS = None
+
+
+def ops():
+    """``torch.ops.starkv``; raises RuntimeError if the operator library is missing. The C
+    library is loaded first, so both routes share its state (decode-form switch, timing):
+    the operator library binds to the already-loaded libstarkv_hip.so by its soname."""
+    global _OPS
+    if _OPS is None:
+        lib()
+        if not os.path.exists(OPS_PATH):
+            raise RuntimeError(f"STAR-KV operator library not built: {OPS_PATH} is missing "
+                               "(run `python star-kv-serve_amd/build.py`)")
+        torch.ops.load_library(OPS_PATH)
+        _OPS = torch.ops.starkv
+    return _OPS
+
+
 def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = lib().starkv_last_error().decode(errors="replace")
@@ -107,11 +134,16 @@ def layer_fits(cache_kind: int, num_heads: int, num_kv_heads: int, k_ranks, v_ra
     return bool(lib().starkv_decode_layer_fits(int(cache_kind), int(num_heads), int(num_kv_heads), arr, int(v_rank)))
 
 
+decode_path_epoch = 0  # bumped by set_decode_path: host caches of the decode form key on it
+
+
 def set_decode_path(mode: int) -> int:
     """0 = automatic (default), 1 = one-pass only, 2 = two-pass always; returns the previous mode."""
+    global decode_path_epoch
     prev = lib().starkv_decode_set_path(int(mode))
     if prev < 0:
         check(1, "decode_set_path")
+    decode_path_epoch += 1
     return prev
 
 

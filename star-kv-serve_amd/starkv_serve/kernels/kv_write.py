@@ -14,6 +14,7 @@ from typing import Optional
 import torch
 
 from starkv_serve import _hip
+from starkv_serve.kernels.paged_decode import _as_i32
 from starkv_serve.kernels.paged_quant import QuantRow
 
 
@@ -58,24 +59,15 @@ def write_kv(hidden: torch.Tensor, kv_down: torch.Tensor, kv_cache: torch.Tensor
     if n == 0:
         return codes
     _hip.require_cuda(hidden, kv_down, kv_cache, slot_mapping)
-    L = _hip.lib()
-    ws = torch.empty(L.starkv_write_kv_workspace_bytes(n, width, hs), dtype=torch.uint8, device=hidden.device)
+    _slot_bits(slot_mapping)
     if row is not None:
         _hip.require_cuda(k_ranks, k_offsets, k_nouts)
-        k_ranks, k_offsets, k_nouts = (t if t.dtype == torch.int32 else t.to(torch.int32)
-                                       for t in (k_ranks, k_offsets, k_nouts))
+        k_ranks, k_offsets, k_nouts = (_as_i32(t) for t in (k_ranks, k_offsets, k_nouts))
         heads, rb = row.num_kv_heads, row.nbytes
-        pr, po, pn = k_ranks.data_ptr(), k_offsets.data_ptr(), k_nouts.data_ptr()
     else:
-        heads, rb, pr, po, pn = 0, 0, None, None, None
-    rc = L.starkv_write_kv(
-        _hip.stream_of(hidden), hidden.data_ptr(), hidden.stride(0), kv_down.data_ptr(), kv_down.stride(0),
-        _hip.dtype_code(hidden), n, hs, k_width, v_rank, kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1),
-        _hip.dtype_code(kv_cache) if row is None else 0, kv_cache.shape[1], kv_cache.shape[0],
-        slot_mapping.data_ptr(), _slot_bits(slot_mapping), heads, pr, po, pn, rb,
-        codes.data_ptr() if codes is not None else None, codes.stride(0) if codes is not None else 0,
-        ws.data_ptr(), ws.numel())
-    _hip.check(rc, "write_kv")
+        heads, rb = 0, 0
+    _hip.ops().write_kv(hidden, kv_down, int(k_width), kv_cache, slot_mapping.contiguous(), heads, k_ranks, k_offsets,
+                        k_nouts, rb, codes)
     return codes
 
 
@@ -88,9 +80,5 @@ def write_codes(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor, 
     if n == 0:
         return
     _hip.require_cuda(key, value, kv_cache, slot_mapping)
-    rc = _hip.lib().starkv_write_codes(
-        _hip.stream_of(kv_cache), key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
-        _hip.dtype_code(key), kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1), _hip.dtype_code(kv_cache),
-        kv_cache.shape[1], kv_cache.shape[0], slot_mapping.data_ptr(), _slot_bits(slot_mapping), n, key.shape[1],
-        value.shape[1])
-    _hip.check(rc, "write_codes")
+    _slot_bits(slot_mapping)
+    _hip.ops().write_codes(key, value, kv_cache, slot_mapping.contiguous())

@@ -2,8 +2,8 @@
 
 Drop-in for the reference's ``starkv_serve/kernels/paged_decode.py``: same function,
 same arguments and meaning, same result (``[n, H_q, head_dim]`` in ``v_up_by_q``'s
-dtype). The work runs in the HIP library (``libstarkv_hip.so``) on the current
-stream: a prep launch (token prefix sums and wave plan in one workgroup, the query
+dtype). The work runs in the HIP library (``libstarkv_hip.so``, launched through
+``torch.ops.starkv.lowrank_decode``) on the current stream: a prep launch (token prefix sums and wave plan in one workgroup, the query
 folded into each head's basis in the others), one persistent decode kernel that
 streams every cache page once through LDS with the K logits on MFMA and split-K
 partials, and a merge that also lifts the low-rank output through ``v_up_by_q``. No host
@@ -89,11 +89,18 @@ def _as_i32(t: torch.Tensor) -> torch.Tensor:
 def rows_per_launch(cache_kind: int, num_heads: int, k_width: int, v_rank: int, max_seq_len: int) -> int:
     """Requests per library call: at most 1024, and for two-pass decodes at most
     MAX_LOGITS_PER_LAUNCH logits."""
+    key = (cache_kind, num_heads, k_width, v_rank, _hip.decode_path_epoch)
+    two = _two_pass.get(key)
+    if two is None:
+        two = _two_pass[key] = bool(_hip.lib().starkv_decode_two_pass(cache_kind, num_heads, k_width, v_rank))
     rows = MAX_REQUESTS_PER_LAUNCH
-    if _hip.lib().starkv_decode_two_pass(cache_kind, num_heads, k_width, v_rank):
+    if two:
         lcap = (int(max_seq_len) + 15) // 16 * 16
         rows = max(1, min(rows, MAX_LOGITS_PER_LAUNCH // (num_heads * lcap)))
     return rows
+
+
+_two_pass = {}  # (cache kind, H, k_width, v_rank, path epoch) -> which decode form the library picks
 
 
 def kv_head_groups(cache_kind: int, num_heads: int, k_ranks, v_rank: int) -> list:
@@ -194,13 +201,12 @@ def paged_starkv_decode(
     out = torch.empty((n, num_heads, head_dim), dtype=v_up_by_q.dtype, device=query.device)
     if n == 0:
         return out
-    L = _hip.lib()
+    ops = _hip.ops()
     cs = cos_sin_for_kernel(cos_sin_cache)
     block_table = _as_i32(block_table)
     seq_lens = _as_i32(seq_lens)
     kind = _hip.dtype_code(kv_cache)
-    stream = _hip.stream_of(query)
-    k_width, max_seq_len = int(k_width), int(max_seq_len)
+    k_width, max_seq_len, scale = int(k_width), int(max_seq_len), float(scale)
     per = num_heads // num_kv_heads
     groups = _groups_for(kind, num_heads, num_kv_heads, k_width, k_ranks, v_rank)
     if len(groups) == 1:
@@ -219,20 +225,12 @@ def paged_starkv_decode(
     for qg, og, cg, kug, krg, kog, vug, hq, hkv, kw in parts:
         v_col = k_width - (cg.data_ptr() - kv_cache.data_ptr()) // kv_cache.element_size()
         step = rows_per_launch(kind, hq, kw, v_rank, max_seq_len)
+        if step >= n:
+            ops.lowrank_decode(qg, cg, block_table, seq_lens, max_seq_len, kug, krg, kog, kw, v_col, vug, cs, scale,
+                               og)
+            continue
         for s in range(0, n, step):
             e = min(n, s + step)
-            m = e - s
-            grid = L.starkv_decode_grid_for(kind, m, hq, hkv, kw, v_rank, max_seq_len)
-            ws = torch.empty(L.starkv_decode_workspace_bytes(kind, m, hq, hkv, kw, v_rank, max_seq_len, grid),
-                             dtype=torch.uint8, device=query.device)
-            q, bt, o = qg[s:e], block_table[s:e], og[s:e]
-            rc = L.starkv_lowrank_decode(
-                stream, q.data_ptr(), q.stride(0), q.stride(1), _hip.dtype_code(q),
-                cg.data_ptr(), cg.stride(0), cg.stride(1), kind, cg.shape[1],
-                bt.data_ptr(), bt.stride(0), bt.stride(1), seq_lens[s:e].data_ptr(), m, hq, hkv,
-                max_seq_len, kug.data_ptr(), kug.stride(0), _hip.dtype_code(kug), krg.data_ptr(),
-                kog.data_ptr(), kw, v_col, vug.data_ptr(), vug.stride(0), vug.stride(1),
-                _hip.dtype_code(vug), v_rank, cs.data_ptr(), cs.stride(0), _hip.dtype_code(cs), float(scale),
-                o.data_ptr(), o.stride(0), o.stride(1), _hip.dtype_code(o), ws.data_ptr(), ws.numel(), grid)
-            _hip.check(rc, "paged_starkv_decode")
+            ops.lowrank_decode(qg[s:e], cg, block_table[s:e], seq_lens[s:e], max_seq_len, kug, krg, kog, kw, v_col,
+                               vug, cs, scale, og[s:e])
     return out

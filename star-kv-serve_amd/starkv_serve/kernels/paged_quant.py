@@ -142,12 +142,9 @@ def pack_kv(k_codes, v_codes, cache, slot_mapping, row: QuantRow, k_ranks, k_off
     _hip.require_cuda(k_codes, v_codes, cache, slot_mapping, k_ranks, k_offsets, k_nouts)
     k_ranks, k_offsets, k_nouts = (_as_i32(t) for t in (k_ranks, k_offsets, k_nouts))
     slot_mapping = slot_mapping.contiguous()
-    rc = _hip.lib().starkv_pack_kv(
-        _hip.stream_of(cache), k_codes.data_ptr(), k_codes.stride(0), v_codes.data_ptr(), v_codes.stride(0),
-        _hip.dtype_code(k_codes), cache.data_ptr(), cache.stride(0), cache.stride(1), cache.shape[1],
-        cache.shape[0], slot_mapping.data_ptr(), _slot_bits(slot_mapping), n, row.num_kv_heads, k_ranks.data_ptr(),
-        k_offsets.data_ptr(), k_nouts.data_ptr(), row.k_width, row.v_rank, row.nbytes)
-    _hip.check(rc, "pack_kv")
+    _slot_bits(slot_mapping)
+    _hip.ops().pack_kv(k_codes, v_codes, cache, slot_mapping, row.num_kv_heads, k_ranks, k_offsets, k_nouts,
+                       row.k_width, row.v_rank, row.nbytes)
 
 
 def fold_q(q, k_up, head_of_lane, scale):
@@ -164,11 +161,7 @@ def fold_q(q, k_up, head_of_lane, scale):
     if n == 0 or W == 0:
         return ab
     _hip.require_cuda(q, k_up, head_of_lane)
-    head_of_lane = _as_i32(head_of_lane)
-    rc = _hip.lib().starkv_fold_q(_hip.stream_of(q), q.data_ptr(), q.stride(0), q.stride(1), _hip.dtype_code(q),
-                                  k_up.data_ptr(), k_up.stride(0), _hip.dtype_code(k_up), head_of_lane.data_ptr(),
-                                  n, W, float(scale), ab.data_ptr())
-    _hip.check(rc, "fold_q")
+    _hip.ops().fold_q(q, k_up, _as_i32(head_of_lane), float(scale), ab)
     return ab
 
 
@@ -204,31 +197,17 @@ def paged_quant_decode(
     out = torch.empty((n, H, D), dtype=v_up_by_q.dtype, device=query.device)
     if n == 0:
         return out
-    L = _hip.lib()
+    ops = _hip.ops()
     cs = cos_sin_for_kernel(cos_sin_cache)
     block_table = _as_i32(block_table)
     seq_lens = _as_i32(seq_lens)
     th, tn, tl = (_as_i32(t) for t in (th, tn, tl))
     k_tiles_n = row.k_width // 16
     assert th.numel() == k_tiles_n, "k_tiles must cover k_width / 16 tiles"
-    stream = _hip.stream_of(query)
-    step = rows_per_launch(_hip.CACHE_Q3_2, H, row.k_width, row.v_rank, int(max_seq_len))
+    max_seq_len, scale = int(max_seq_len), float(scale)
+    step = rows_per_launch(_hip.CACHE_Q3_2, H, row.k_width, row.v_rank, max_seq_len)
     for s in range(0, n, step):
         e = min(n, s + step)
-        m = e - s
-        grid = L.starkv_decode_grid_for(_hip.CACHE_Q3_2, m, H, H, row.k_width, row.v_rank, int(max_seq_len))
-        ws = torch.empty(L.starkv_decode_workspace_bytes(_hip.CACHE_Q3_2, m, H, H, row.k_width, row.v_rank,
-                                                         int(max_seq_len), grid),
-                         dtype=torch.uint8, device=query.device)
-        q, bt, o = query[s:e], block_table[s:e], out[s:e]
-        rc = L.starkv_quant_decode(
-            stream, q.data_ptr(), q.stride(0), q.stride(1), _hip.dtype_code(q),
-            kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1), kv_cache.shape[1],
-            bt.data_ptr(), bt.stride(0), bt.stride(1), seq_lens[s:e].data_ptr(), m, H, int(max_seq_len),
-            row.k_width, row.v_rank, row.nbytes, k_up.data_ptr(), k_up.stride(0), _hip.dtype_code(k_up),
-            th.data_ptr(), tn.data_ptr(), tl.data_ptr(), v_up_by_q.data_ptr(), v_up_by_q.stride(0),
-            v_up_by_q.stride(1), _hip.dtype_code(v_up_by_q), cs.data_ptr(), cs.stride(0), _hip.dtype_code(cs),
-            float(scale), o.data_ptr(),
-            o.stride(0), o.stride(1), _hip.dtype_code(o), ws.data_ptr(), ws.numel(), grid)
-        _hip.check(rc, "paged_quant_decode")
+        ops.quant_decode(query[s:e], kv_cache, block_table[s:e], seq_lens[s:e], max_seq_len, row.k_width, row.v_rank,
+                         row.nbytes, k_up, th, tn, tl, v_up_by_q, cs, scale, out[s:e])
     return out

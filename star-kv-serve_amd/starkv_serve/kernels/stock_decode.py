@@ -25,17 +25,8 @@ def paged_decode_full(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch
     if n == 0:
         return out
     _hip.require_cuda(query, k_cache, v_cache, block_table, seq_lens)
-    L = _hip.lib()
     block_table, seq_lens = _as_i32(block_table), _as_i32(seq_lens)
-    ws = torch.empty(L.starkv_stock_decode_workspace_bytes(n, Hq, Hkv, int(max_seq_len)), dtype=torch.uint8,
-                     device=query.device)
-    rc = L.starkv_stock_decode(
-        _hip.stream_of(query), query.data_ptr(), query.stride(0), query.stride(1), _hip.dtype_code(query),
-        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
-        _hip.dtype_code(k_cache), k_cache.shape[1], block_table.data_ptr(), block_table.stride(0),
-        block_table.stride(1), seq_lens.data_ptr(), n, Hq, Hkv, int(max_seq_len), float(scale), out.data_ptr(),
-        out.stride(0), out.stride(1), _hip.dtype_code(out), ws.data_ptr(), ws.numel())
-    _hip.check(rc, "paged_decode_full")
+    _hip.ops().stock_decode(query, k_cache, v_cache, block_table, seq_lens, int(max_seq_len), float(scale), out)
     return out
 
 
@@ -52,12 +43,6 @@ def write_kv_full(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
         return
     _hip.require_cuda(key, value, k_cache, v_cache, slot_mapping)
     slots = slot_mapping.contiguous()
-    bits = 64 if slots.dtype == torch.int64 else 32
-    if bits == 32:
+    if slots.dtype != torch.int64:
         slots = _as_i32(slots)
-    rc = _hip.lib().starkv_stock_write(
-        _hip.stream_of(key), key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0),
-        value.stride(1), _hip.dtype_code(key), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
-        k_cache.stride(1), k_cache.stride(2), k_cache.shape[1], k_cache.shape[0], slots.data_ptr(), bits, n,
-        key.shape[1])
-    _hip.check(rc, "write_kv_full")
+    _hip.ops().stock_write(key, value, k_cache, v_cache, slots)

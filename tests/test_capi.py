@@ -138,3 +138,40 @@ def test_layer_fits_host_plan():
     # 96-tile cap
     assert fits(BF16, 8, 8, [192] * 8, 64)
     assert not fits(BF16, 9, 9, [192] * 8 + [16], 64)
+
+
+OPS = {
+    "lowrank_decode": "(Tensor query, Tensor kv_cache, Tensor block_table, Tensor seq_lens, SymInt max_seq_len",
+    "quant_decode": "(Tensor query, Tensor kv_cache, Tensor block_table, Tensor seq_lens, SymInt max_seq_len",
+    "pack_kv": "(Tensor k_codes, Tensor v_codes, Tensor(a!) cache, Tensor slot_mapping",
+    "write_codes": "(Tensor key, Tensor value, Tensor(a!) kv_cache, Tensor slot_mapping)",
+    "write_kv": "(Tensor hidden, Tensor kv_down, SymInt k_width, Tensor(a!) kv_cache",
+    "fold_q": "(Tensor q, Tensor k_up, Tensor head_of_lane, float scale, Tensor(a!) ab)",
+    "stock_decode": "(Tensor query, Tensor k_cache, Tensor v_cache, Tensor block_table",
+    "stock_write": "(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor slot_mapping)",
+}
+
+
+def test_operator_library_registers_every_op():
+    """torch.ops.starkv (libstarkv_torch.so over the C ABI): every launch entry point is an
+    operator with a schema that marks the tensors it writes."""
+    import torch
+    from starkv_serve import _hip
+    ops = _hip.ops()
+    for name, head in OPS.items():
+        schema = str(getattr(ops, name).default._schema)
+        assert schema.startswith(f"starkv::{name}"), schema
+        assert head.replace("SymInt", "int") in schema.replace("SymInt", "int"), schema
+    assert "Tensor(a!) out" in str(ops.lowrank_decode.default._schema)
+    del torch
+
+
+def test_operators_refuse_cpu_tensors():
+    """The operators are registered for the GPU only: CPU tensors find no kernel and raise
+    (no CPU fallback)."""
+    import torch
+    from starkv_serve import _hip
+    t = torch.zeros(4, dtype=torch.bfloat16)
+    s = torch.zeros(1, dtype=torch.int64)
+    with pytest.raises(NotImplementedError, match="CPU"):
+        _hip.ops().write_codes(t.view(1, 4), t.view(1, 4), t.view(1, 1, 4), s)
