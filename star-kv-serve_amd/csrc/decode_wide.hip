@@ -540,7 +540,12 @@ __global__ __launch_bounds__(LIFT_THR) void lift_kernel(const uint8_t* __restric
 namespace {
 
 constexpr int PV_NLD = 12;  // copies per wave per page, at most (the plan keeps nch <= 96)
-constexpr int PV_INFLIGHT = 96 * 1024;  // page bytes in flight per workgroup the plan aims for
+// Page bytes in flight per workgroup the plan aims for, with at least two pages in flight.
+// A page costs about the same time whatever its width (its barrier, P and copy issue), so
+// the plan takes the fewest windows that keep this much in flight: at V rank 1280 one
+// window of 40 blocks (86 KB in flight) runs 64 x 8192 in 286 us where two windows of 20
+// (115 KB) took 346 us.
+constexpr int PV_INFLIGHT = 64 * 1024;
 
 template <int FMT>
 const void* pv_pick(int mb) {
@@ -608,7 +613,7 @@ static PvPlan pv_plan(int fmt, int v_col, int v_rank, int vs_off, int vq_off, in
         const int nbuf = std::min(8, (PV_MAX_DYN_LDS - 1024) / (nch * 1024));
         if (nbuf < 2) continue;
         const int inflight = (nbuf - 1) * nch * 1024;
-        const int score = inflight >= PV_INFLIGHT ? (1 << 30) - launches : inflight;
+        const int score = inflight >= PV_INFLIGHT && nbuf >= 3 ? (1 << 30) - launches : inflight;
         if (score > best_score) {
             best_score = score;
             pl.per = per;
