@@ -468,6 +468,52 @@ def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, mod
     return res
 
 
+def bench_prefill(steps, warmup, num_heads=32):
+    """Dense causal prefill attention (the attention half of the STAR-KV layer's
+    prefill, attention.py:219-251): this library's prefill kernel over fp16 K / V, next
+    to torch's fused SDPA (flash or memory-efficient kernels) over the same bf16 q and
+    K / V per prompt. Shapes: one 16,384-token prompt (config 4's prompts) and 8 prompts
+    of 2,048, 32 heads x 128. FLOPs: the causal half of QK^T and PV, 2 L (L + 1) 128 H."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from starkv_serve.kernels.prefill import prefill_attention
+    res = {}
+    g = torch.Generator(device="cuda").manual_seed(11)
+    for name, lens in (("1x16384", [16384]), ("8x2048", [2048] * 8)):
+        T = sum(lens)
+        q = torch.randn(T, num_heads, 128, generator=g, device="cuda").to(torch.bfloat16)
+        k = torch.randn(T, num_heads, 128, generator=g, device="cuda").to(torch.float16)
+        v = torch.randn(T, num_heads, 128, generator=g, device="cuda").to(torch.float16)
+        out = torch.empty_like(q)
+        flops = sum(2 * L * (L + 1) * 128 * num_heads for L in lens)
+        mean, med = time_events(lambda i: prefill_attention(q, k, v, lens, 128 ** -0.5, out=out), steps, warmup)
+        r = dict(prompts=len(lens), tokens=T, flops=int(flops), us_median=round(med * 1e3, 1),
+                 TFLOPs=round(flops / (med * 1e-3) / 1e12, 1),
+                 mfma_frac=round(flops / (med * 1e-3) / 1e12 / MFMA_PEAK_F16_TFLOPS, 4))
+        kb, vb = k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+        def sdpa(i):
+            a = 0
+            for L in lens:
+                qi = q[a:a + L].transpose(0, 1).unsqueeze(0)
+                ki = kb[a:a + L].transpose(0, 1).unsqueeze(0)
+                vi = vb[a:a + L].transpose(0, 1).unsqueeze(0)
+                F.scaled_dot_product_attention(qi, ki, vi, is_causal=True)
+                a += L
+        try:
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                smean, smed = time_events(sdpa, steps, warmup)
+            r.update(sdpa_us_median=round(smed * 1e3, 1), sdpa_TFLOPs=round(flops / (smed * 1e-3) / 1e12, 1),
+                     speedup_vs_sdpa=round(smed / med, 2))
+        except RuntimeError as e:
+            r["sdpa_error"] = str(e)[:200]
+        res[name] = r
+        del q, k, v, kb, vb, out
+        torch.cuda.empty_cache()
+    return res
+
+
 def measured_traffic(key):
     """HBM bytes per launch for `key` from the committed counter summary, or None."""
     import re
@@ -579,7 +625,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip every workload but the headline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["bf16", "quant", "write", "short", "wide", "wide_quant", "c0", "c3",
-                                       "model", "stock"],
+                                       "model", "stock", "prefill"],
                     default=None, help="profile runs: time one workload only and print its summary")
     ap.add_argument("--copy-probe", type=float, default=0.0, metavar="GIB",
                     help="profile runs: only copy GIB GiB device to device 5 times (counter scaling)")
@@ -611,6 +657,7 @@ def main():
         "c3": lambda: bench_c3(32, 2),
         "model": lambda: bench_model(),
         "stock": lambda: bench_stock(64, 8192, K, Wm),
+        "prefill": lambda: bench_prefill(min(K, 10), min(Wm, 3)),
     }
     if args.only in only:
         print(json.dumps(only[args.only]()), flush=True)
@@ -653,6 +700,7 @@ def main():
                     f"cache write, {n_tok} tokens, {'3.2-bit' if quant else 'bf16'} (fused vs unfused)",
                     lambda: bench_write(n_tok, quant, K, Wm))
         run("model_llama2_7b_16k", "config 4: Llama-2-7B-shaped decode steps at 16K context", only["model"])
+        run("prefill", "dense causal prefill attention (prefill kernel vs torch SDPA)", only["prefill"])
         log("uncompressed bf16 attention (torch fused SDPA), 64 x 8192")
         stock = bench_stock(64, 8192, K, Wm)
         for key, name in (("bf16", head), ("quant", extra["quant_bs64x8k"])):

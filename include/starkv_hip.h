@@ -291,6 +291,27 @@ int starkv_stock_decode(void *stream, const void *query, int64_t q_s0, int64_t q
                         void *workspace, size_t workspace_bytes);
 
 /*
+ * Dense causal prefill attention of a STAR-KV layer: the attention half of the reference's
+ * _dense_prefill (starkv_serve/attention.py:219-251, its flash_attn_varlen_func call with
+ * causal=True, attention.py:243-249), over K and V already lifted from the step's codes.
+ * Every prompt attends to itself only (no cached context): for token t of the prompt that
+ * starts at s, out[t, h] = softmax(scale q[t, h] . K[s .. t, h / G]) V[s .. t, h / G] with
+ * G = num_heads / num_kv_heads. query [T, num_heads, 128] (bf16, fp16 or fp32, element
+ * strides q_s0, q_s1); key and value [T, num_kv_heads, 128] fp16 sharing element strides
+ * (kv_s0, kv_s1); cu_seqlens [num_prompts + 1] int32 on the device (the prompts' first
+ * tokens, then T); out [T, num_heads, 128] (element strides o_s0, o_s1). head_size 128.
+ * blocks: num_blocks (prompt, 128-row query block) pairs on the device, as
+ * starkv_prefill_block_list writes them on the host from a host copy of cu_seqlens
+ * (it returns the count and writes at most `capacity` pairs; -1 for a bad prefix).
+ */
+int starkv_prefill_block_list(const int32_t *cu_seqlens, int num_prompts, int32_t *blocks, int capacity);
+int starkv_prefill_attention(void *stream, const void *query, int64_t q_s0, int64_t q_s1, int q_dtype,
+                             const void *key, const void *value, int64_t kv_s0, int64_t kv_s1, int kv_dtype,
+                             const int32_t *cu_seqlens, const int32_t *blocks, int num_blocks, int num_heads,
+                             int num_kv_heads, int head_size, float scale, void *out, int64_t o_s0, int64_t o_s1,
+                             int out_dtype);
+
+/*
  * Timing for benchmarks (no counterpart in the reference, whose benchmark reads profiler
  * traces instead, bench_serving.py:71-115). starkv_profile_begin arms up to max_calls
  * event pairs; each following decode call records one pair on its stream, around its

@@ -21,6 +21,10 @@ something other than itself) -- see tests/test_oracle_*.py:
                                       the same codes; a first token returns its own V
                                       lifted; causality (a later token changes no
                                       earlier output)
+  causal_attention                    torch's float64 CPU scaled_dot_product_attention
+                                      (is_causal) per prompt and head; a first token
+                                      returns its own V; dense_prefill equals it over
+                                      the lifted K and V
 """
 import math
 
@@ -280,6 +284,31 @@ def dense_prefill(q, k_codes, v_codes, query_start_loc, k_up, k_ranks, k_offsets
                 p = np.exp(logits - logits.max(axis=1, keepdims=True))
                 p /= p.sum(axis=1, keepdims=True)
                 out[a:b, h] = p @ V
+    return out
+
+
+def causal_attention(q, k, v, query_start_loc, scale):
+    """float64 truth for the prefill kernel's attention over given K and V (the
+    flash_attn_varlen_func call of attention.py:243-249, causal=True): per prompt (tokens
+    query_start_loc[i] .. query_start_loc[i + 1]), softmax(q . k * scale) @ v over the
+    prompt's tokens up to the query's own; query head h reads KV head h // (H_q / H_kv).
+    q [T, H_q, D], k and v [T, H_kv, D]. Returns [T, H_q, D]."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    T, Hq, D = q.shape
+    G = Hq // k.shape[1]
+    out = np.zeros((T, Hq, D))
+    qsl = [int(x) for x in query_start_loc]
+    for i in range(len(qsl) - 1):
+        a, b = qsl[i], qsl[i + 1]
+        if b <= a:
+            continue
+        causal = np.tril(np.ones((b - a, b - a), bool))
+        for h in range(Hq):
+            logits = np.where(causal, (q[a:b, h] @ k[a:b, h // G].T) * scale, -np.inf)
+            p = np.exp(logits - logits.max(axis=1, keepdims=True))
+            out[a:b, h] = (p / p.sum(axis=1, keepdims=True)) @ v[a:b, h // G]
     return out
 
 

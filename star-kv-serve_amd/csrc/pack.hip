@@ -90,7 +90,7 @@ using namespace starkv;
 
 extern "C" {
 
-int starkv_abi_version(void) { return 3; }
+int starkv_abi_version(void) { return 4; }
 
 const char* starkv_last_error(void) { return g_err; }
 

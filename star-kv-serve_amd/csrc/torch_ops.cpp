@@ -189,6 +189,20 @@ void stock_write(const at::Tensor& key, const at::Tensor& value, const at::Tenso
           "stock_write");
 }
 
+// Dense causal prefill attention over lifted K / V (attention.py:219-251's attention).
+void prefill(const at::Tensor& query, const at::Tensor& key, const at::Tensor& value, const at::Tensor& cu_seqlens,
+             const at::Tensor& blocks, double scale, const at::Tensor& out) {
+    const c10::DeviceGuard guard(query.device());
+    TORCH_CHECK(key.strides() == value.strides(), "starkv.prefill: K and V must share strides");
+    TORCH_CHECK(blocks.dim() == 2 && blocks.size(1) == 2, "starkv.prefill: blocks must be [num_blocks, 2]");
+    check(starkv_prefill_attention(stream_of(query), query.data_ptr(), query.stride(0), query.stride(1),
+                                   dtype_code(query), key.data_ptr(), value.data_ptr(), key.stride(0), key.stride(1),
+                                   dtype_code(key), i32(cu_seqlens, "cu_seqlens"), i32(blocks, "blocks"),
+                                   (int)blocks.size(0), (int)query.size(1), (int)key.size(1), (int)query.size(2),
+                                   (float)scale, out.data_ptr(), out.stride(0), out.stride(1), dtype_code(out)),
+          "prefill");
+}
+
 }  // namespace
 
 TORCH_LIBRARY(starkv, m) {
@@ -208,6 +222,8 @@ TORCH_LIBRARY(starkv, m) {
     m.def("stock_decode(Tensor query, Tensor k_cache, Tensor v_cache, Tensor block_table, Tensor seq_lens, "
           "int max_seq_len, float scale, Tensor(a!) out) -> ()");
     m.def("stock_write(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor slot_mapping) -> ()");
+    m.def("prefill(Tensor query, Tensor key, Tensor value, Tensor cu_seqlens, Tensor blocks, float scale, "
+          "Tensor(a!) out) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(starkv, CUDA, m) {
@@ -219,4 +235,5 @@ TORCH_LIBRARY_IMPL(starkv, CUDA, m) {
     m.impl("fold_q", &fold_q);
     m.impl("stock_decode", &stock_decode);
     m.impl("stock_write", &stock_write);
+    m.impl("prefill", &prefill);
 }

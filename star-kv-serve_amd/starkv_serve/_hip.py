@@ -19,7 +19,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstarkv_hip.so")
 OPS_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstarkv_torch.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 F32, F16, BF16 = 0, 1, 2
 CACHE_Q3_2 = 16  # cache kind of the 3.2-bit QuantRow cache
@@ -49,6 +49,9 @@ SIGNATURES = {
                                  _I, _I, _I, _I, _F, _P, _I64, _I64, _I, _P, _SZ]),
     "starkv_stock_write": (_I, [_P, _P, _I64, _I64, _P, _I64, _I64, _I, _P, _P, _I64, _I64, _I64, _I, _I64, _P, _I,
                                 _I, _I]),
+    "starkv_prefill_block_list": (_I, [ctypes.POINTER(ctypes.c_int32), _I, ctypes.POINTER(ctypes.c_int32), _I]),
+    "starkv_prefill_attention": (_I, [_P, _P, _I64, _I64, _I, _P, _P, _I64, _I64, _I, _P, _P, _I, _I, _I, _I, _F,
+                                      _P, _I64, _I64, _I]),
     "starkv_profile_begin": (_I, [_I, _I]),
     "starkv_profile_end": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "starkv_profile_times": (_I, [ctypes.POINTER(ctypes.c_double), _I]),

@@ -48,6 +48,7 @@ from starkv_serve.checkpoint import StarKVLayerWeights, layer_operands
 from starkv_serve.kernels.kv_write import write_codes, write_kv
 from starkv_serve.kernels.paged_decode import paged_starkv_decode
 from starkv_serve.kernels.paged_quant import HEAD_DIM, pack_kv, paged_quant_decode
+from starkv_serve.kernels.prefill import prefill_attention
 
 DECODER = "decoder"  # AttentionType.DECODER
 
@@ -240,29 +241,20 @@ class StarKVAttentionImpl:
     def _dense_prefill(self, query_lens: List[int], q: torch.Tensor, k_codes: torch.Tensor, v_codes: torch.Tensor,
                        out: torch.Tensor) -> None:
         """STAR-KV's prefill (attention.py:219-251): K = RoPE(codes @ U) and V = codes @
-        v_up for this step's tokens (positions from 0 in every prompt), then causal
-        attention of every prompt to itself. q and out [T, H_q, 128]."""
-        from torch.nn.attention import SDPBackend, sdpa_kernel
+        v_up for this step's tokens (positions from 0 in every prompt), lifted in fp32 and
+        rounded once to fp16, then causal attention of every prompt to itself on this
+        library's prefill kernel. q and out [T, H_q, 128]."""
         T = q.shape[0]
         H, R, Hd = self.num_kv_heads, self.w.k_max_rank, self.head_size
-        G = self.num_heads // H
         pos = torch.cat([torch.arange(L) for L in query_lens]).to(q.device)
         kp = k_codes[:, self.k_prefill_gather].float().view(T, H, R).transpose(0, 1).contiguous()
         k = torch.bmm(kp, self.k_up_T).transpose(0, 1)                                     # [T, H, Hd] fp32
         cos, sin = self.rotary_emb.cos_sin_cache[pos].float().chunk(2, dim=-1)
         cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
         k1, k2 = k.chunk(2, dim=-1)
-        k = torch.cat([k1 * cos - k2 * sin, k2 * cos + k1 * sin], dim=-1).to(q.dtype)
-        v = F.linear(v_codes.float(), self.v_up).view(T, H, Hd).to(q.dtype)
-        a = 0
-        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-            for L in query_lens:
-                qi = q[a:a + L].transpose(0, 1).unsqueeze(0).contiguous()                  # [1, H_q, L, Hd]
-                ki = k[a:a + L].repeat_interleave(G, dim=1).transpose(0, 1).unsqueeze(0).contiguous()
-                vi = v[a:a + L].repeat_interleave(G, dim=1).transpose(0, 1).unsqueeze(0).contiguous()
-                o = F.scaled_dot_product_attention(qi, ki, vi, is_causal=True, scale=self.scale)
-                out[a:a + L] = o[0].transpose(0, 1)
-                a += L
+        k = torch.cat([k1 * cos - k2 * sin, k2 * cos + k1 * sin], dim=-1).to(torch.float16)
+        v = F.linear(v_codes.float(), self.v_up).view(T, H, Hd).to(torch.float16)
+        prefill_attention(q, k, v, query_lens, self.scale, out=out)
 
     def write_from_hidden(self, hidden: torch.Tensor, kv_cache: torch.Tensor, slot_mapping: torch.Tensor,
                           return_codes: bool = False) -> Optional[torch.Tensor]:

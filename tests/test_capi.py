@@ -4,6 +4,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -175,3 +176,23 @@ def test_operators_refuse_cpu_tensors():
     s = torch.zeros(1, dtype=torch.int64)
     with pytest.raises(NotImplementedError, match="CPU"):
         _hip.ops().write_codes(t.view(1, 4), t.view(1, 4), t.view(1, 1, 4), s)
+
+
+def test_prefill_block_list_host():
+    """starkv_prefill_block_list (C, host) and the wrapper's block_list agree: one
+    (prompt, 128-row block) pair per query block, empty prompts skipped; a bad prefix is
+    refused; the prefill entry point checks its arguments before launching."""
+    from starkv_serve import _hip
+    from starkv_serve.kernels.prefill import block_list
+    L = _hip.lib()
+    lens = [1, 0, 128, 129, 300, 0, 5]
+    cu = (ctypes.c_int32 * (len(lens) + 1))(*np.concatenate([[0], np.cumsum(lens)]).astype(int).tolist())
+    n = L.starkv_prefill_block_list(cu, len(lens), None, 0)
+    buf = (ctypes.c_int32 * (2 * n))()
+    assert L.starkv_prefill_block_list(cu, len(lens), buf, n) == n == 1 + 1 + 2 + 3 + 1
+    assert list(buf) == block_list(lens)
+    bad = (ctypes.c_int32 * 3)(0, 5, 2)
+    assert L.starkv_prefill_block_list(bad, 2, None, 0) == -1
+    rc = L.starkv_prefill_attention(None, None, 0, 0, 2, None, None, 0, 0, 1, None, None, 1, 32, 32, 64, 0.1, None,
+                                    0, 0, 2)
+    assert rc != 0 and b"null pointer" in L.starkv_last_error()

@@ -80,3 +80,39 @@ def test_causal_and_prompts_independent():
     np.testing.assert_array_equal(out[:11], base[:11])
     np.testing.assert_array_equal(out[12:], base[12:])
     assert not np.allclose(out[11], base[11])
+
+
+def test_causal_attention_matches_torch_sdpa():
+    """causal_attention (the prefill kernel's truth) against torch's float64 CPU
+    scaled_dot_product_attention, per prompt, with GQA."""
+    import torch
+    rng = np.random.default_rng(7)
+    lengths, Hq, Hkv = [5, 1, 70], 8, 2
+    T = sum(lengths)
+    q, k, v = rng.standard_normal((T, Hq, D)), rng.standard_normal((T, Hkv, D)), rng.standard_normal((T, Hkv, D))
+    qsl = np.concatenate([[0], np.cumsum(lengths)])
+    out = ref.causal_attention(q, k, v, qsl, 0.09)
+    G = Hq // Hkv
+    for i in range(len(lengths)):
+        a, b = qsl[i], qsl[i + 1]
+        qt = torch.from_numpy(q[a:b]).transpose(0, 1)
+        kt = torch.from_numpy(k[a:b]).repeat_interleave(G, dim=1).transpose(0, 1)
+        vt = torch.from_numpy(v[a:b]).repeat_interleave(G, dim=1).transpose(0, 1)
+        o = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, is_causal=True, scale=0.09)
+        np.testing.assert_allclose(out[a:b], o.transpose(0, 1).numpy(), rtol=1e-12, atol=1e-12)
+    # a prompt's first token attends to itself alone
+    np.testing.assert_allclose(out[qsl[:-1].astype(int)], v[qsl[:-1].astype(int)].repeat(G, axis=1), atol=1e-14)
+
+
+def test_dense_prefill_is_causal_attention_over_lifted_kv():
+    """dense_prefill = causal_attention over RoPE(codes @ U) and codes @ v_up^T."""
+    c = _case([9, 33], [16, 32], 4, 64, 11)
+    T = c["q"].shape[0]
+    k = np.zeros((T, c["Hkv"], D))
+    for h, (r, off) in enumerate(zip(c["ranks"], c["offsets"])):
+        lifted = c["k_codes"][:, off:off + r] @ c["k_up"][off:off + r]
+        for i in range(len(c["qsl"]) - 1):
+            a, b = int(c["qsl"][i]), int(c["qsl"][i + 1])
+            k[a:b, h] = ref._rope(lifted[a:b], c["cs"][:b - a])
+    v = (c["v_codes"] @ c["v_up"].T).reshape(T, c["Hkv"], D)
+    np.testing.assert_allclose(ref.causal_attention(c["q"], k, v, c["qsl"], c["scale"]), _prefill(c), atol=1e-12)
