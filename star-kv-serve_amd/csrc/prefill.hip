@@ -56,7 +56,7 @@ struct PrefillParams {
 // Physical byte of (row, 16-byte granule g) in a K or V tile: granules XOR-swizzled by the row.
 __device__ __forceinline__ uint32_t pf_addr(int row, int g) { return (uint32_t)(row * 256 + ((g ^ (row & 15)) << 4)); }
 
-// 8 query dimensions as fp16 (zeros past the prompt).
+// 8 query dimensions times scale * log2(e), as fp16 (zeros past the prompt).
 template <int QDT>
 __device__ __forceinline__ half8_t pf_load_q(const PrefillParams& p, int64_t tok, int hq, int d0, bool ok) {
     half8_t r;
@@ -66,20 +66,25 @@ __device__ __forceinline__ half8_t pf_load_q(const PrefillParams& p, int64_t tok
         return r;
     }
     const int64_t off = tok * p.q_s0 + (int64_t)hq * p.q_s1 + d0;
-    if (QDT == STARKV_F16) return *(const half8_t*)((const _Float16*)p.q + off);
-    if (QDT == STARKV_BF16) {
+    float f[8];
+    if (QDT == STARKV_F16) {
+        const half8_t x = *(const half8_t*)((const _Float16*)p.q + off);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = (float)x[e];
+    } else if (QDT == STARKV_BF16) {
         const uint4 w = *(const uint4*)((const uint16_t*)p.q + off);
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            r[2 * k] = (_Float16)__uint_as_float(ws[k] << 16);
-            r[2 * k + 1] = (_Float16)__uint_as_float(ws[k] & 0xffff0000u);
+            f[2 * k] = __uint_as_float(ws[k] << 16);
+            f[2 * k + 1] = __uint_as_float(ws[k] & 0xffff0000u);
         }
-        return r;
-    }
-    const float* f = (const float*)p.q + off;
+    } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = (_Float16)f[e];
+        for (int e = 0; e < 8; ++e) f[e] = ((const float*)p.q)[off + e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (_Float16)(f[e] * p.sc);
     return r;
 }
 
@@ -187,17 +192,23 @@ __global__ __launch_bounds__(PF_THR) __attribute__((amdgpu_waves_per_eu(2))) voi
                     sc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds_ld<half8_t>(kb + 8192u * mb + ka[ks]), qb[ks],
                                                                    sc[mb], 0, 0, 0);
             }
-            // Scores of this lane's query: key k0 + 32 mb + 8 (r / 4) + 4 h + r % 4.
+            // Scores of this lane's query (already scaled through q): key k0 + 32 mb + 8 (r / 4) +
+            // 4 h + r % 4. Only a tile that reaches past the wave's first query or the prompt's
+            // end needs the causal / end mask.
+            if (k0 + PF_KT - 1 > qw || k0 + PF_KT > L) {
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = k0 + 32 * mb + 8 * (r >> 2) + 4 * h + (r & 3);
+                        if (!(key <= qi && key < L)) sc[mb][r] = -INFINITY;
+                    }
+            }
             float mx = -INFINITY;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = k0 + 32 * mb + 8 * (r >> 2) + 4 * h + (r & 3);
-                    const float v = key <= qi && key < L ? sc[mb][r] * p.sc : -INFINITY;
-                    sc[mb][r] = v;
-                    mx = fmaxf(mx, v);
-                }
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[mb][r]);
             {  // with the partner lane's half: x[0] holds lane l % 32's value, x[1] lane 32 + l % 32's
                 const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
                 mx = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
