@@ -12,7 +12,8 @@
 // prefill_kernel: one workgroup of 4 waves per (query block of 128 rows, query head); wave
 // w takes query rows 32 w .. 32 w + 31 of the block. Keys go by tiles of 64, K and V of a
 // tile copied global->LDS by all waves (buffer loads that write LDS, bounded to the
-// prompt's rows), two tiles in flight. Per tile and wave, on v_mfma_f32_32x32x16_f16:
+// prompt's rows), the next tile in flight while one is used. The block list puts the
+// blocks with the most keys first. Per tile and wave, on v_mfma_f32_32x32x16_f16:
 //   S^T = K Q^T: M = 32 keys (two blocks per tile), N = the wave's 32 queries, K = the 128
 //     head dimensions (8 steps); A = a K row's 8 dimensions (ds_read_b128 from a row whose
 //     16-byte granules are XOR-swizzled by the row, so 16 rows hit distinct banks), B = Q
@@ -27,6 +28,10 @@
 //     the same key order, read with ds_read_b64_tr_b16 (4 key rows x 16 dimensions per
 //     16-lane group, lane i receiving dimension i).
 // At the end the two halves of each query's sum are added and O / l is written.
+#include <algorithm>
+#include <array>
+#include <vector>
+
 #include "decode_pages.hpp"
 
 namespace starkv {
@@ -39,6 +44,8 @@ constexpr int PF_QB = 32 * PF_WAVES;      // query rows per workgroup
 constexpr int PF_KT = 64;                 // keys per tile
 constexpr int PF_TILE = PF_KT * 256;      // bytes of K (or V) per tile: 64 rows x 128 fp16
 constexpr int PF_BUF = 2 * PF_TILE;       // K then V
+constexpr int PF_NBUF = 2;                // tile buffers: the next tile lands while one is used
+constexpr int PF_CPW = 32 / PF_WAVES;     // 1 KB copies per wave per tile
 constexpr float PF_LAZY = 8.f;            // log2 headroom of the reference max
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -116,22 +123,22 @@ __global__ __launch_bounds__(PF_THR) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qb[ks] = pf_load_q<QDT>(p, (int64_t)s + qi, hq, 16 * ks + 8 * h, qi < L);
 
-    // Copies: a tile is 32 KB (K rows then V rows), 32 copies of 1 KB, 8 per wave. Copy c
-    // of wave w moves LDS bytes [1024 (4 c + w), + 1024): K (or V, past 16 KB) rows
-    // 4 (4 c + w) % 64 .. + 3; lane j writes physical granule j % 16 of row (j / 16) of
-    // them, i.e. logical granule (j % 16) ^ (row & 15).
+    // Copies: a tile is 32 KB (K rows then V rows), 32 copies of 1 KB, PF_CPW per wave.
+    // Copy c of wave w moves LDS bytes [1024 (PF_WAVES c + w), + 1024): K (or V, past
+    // 16 KB) rows 4 ((PF_WAVES c + w) % 16) .. + 3; lane j writes physical granule j % 16
+    // of row (j / 16) of them, i.e. logical granule (j % 16) ^ (row & 15).
     const uint32_t base = lds_addr(s_kv);
-    uint32_t coff[8];
+    uint32_t coff[PF_CPW];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const int ch = 4 * c + wave;              // 1 KB chunk of the tile
+    for (int c = 0; c < PF_CPW; ++c) {
+        const int ch = PF_WAVES * c + wave;       // 1 KB chunk of the tile
         const int row = (ch % 16) * 4 + (lane >> 4);
         const int g = (lane & 15) ^ (row & 15);
         coff[c] = (uint32_t)(row * p.kv_s0 + 16 * g);
     }
     const int64_t head_off = (int64_t)hk * p.kv_s1;
-    auto issue = [&](int t) {  // tile t's copies into buffer t % 2
-        const uint32_t buf = base + (uint32_t)((t & 1) * PF_BUF);
+    auto issue = [&](int t) {  // tile t's copies into buffer t % PF_NBUF
+        const uint32_t buf = base + (uint32_t)((t % PF_NBUF) * PF_BUF);
         const int r0 = t * PF_KT;
         const int rows = max(0, min(PF_KT, L - r0));
         int4v_t rk = buffer_rsrc(p.k + ((int64_t)s + r0) * p.kv_s0 + head_off, (int)(rows * p.kv_s0));
@@ -142,9 +149,9 @@ __global__ __launch_bounds__(PF_THR) __attribute__((amdgpu_waves_per_eu(2))) voi
             rv[e] = rfl(rv[e]);
         }
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {  // chunks 4 c + wave: K for c < 4, V after
-            const uint32_t m0 = buf + (uint32_t)(4 * c + wave) * 1024u;
-            if (c < 4)
+        for (int c = 0; c < PF_CPW; ++c) {  // chunks PF_WAVES c + wave: K for the first 16, V after
+            const uint32_t m0 = buf + (uint32_t)(PF_WAVES * c + wave) * 1024u;
+            if (c < PF_CPW / 2)
                 lds_copy16(rk, m0, coff[c]);
             else
                 lds_copy16(rv, m0, coff[c]);
@@ -175,14 +182,16 @@ __global__ __launch_bounds__(PF_THR) __attribute__((amdgpu_waves_per_eu(2))) voi
     for (int md = 0; md < 4; ++md) o[md] = (f32x16_t){};
     float m = -INFINITY, l = 0.f;
 
+    // Two workgroups share a CU (64 KB of LDS each): with three tile buffers and 8 waves per
+    // workgroup instead, one 16K-token prompt took 3.54 ms against 3.18 here.
     issue(0);
     for (int t = 0; t < ntile; ++t) {
         SKV_WAIT_VM_LGKM0(0);  // tile t has landed (this wave's copies)
         lds_barrier();         // every wave's copies of tile t; every wave done with tile t - 1
-        if (t + 1 < ntile) issue(t + 1);
+        if (t + 1 < ntile) issue(t + 1);  // into tile t - 1's buffer
         const int k0 = t * PF_KT;
         if (nq > 0 && k0 <= qw + nq - 1) {  // some key of the tile is visible to the wave
-            const uint32_t kb = base + (uint32_t)((t & 1) * PF_BUF), vb = kb + PF_TILE;
+            const uint32_t kb = base + (uint32_t)((t % PF_NBUF) * PF_BUF), vb = kb + PF_TILE;
             f32x16_t sc[2];
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) {
@@ -291,20 +300,25 @@ using namespace starkv;
 extern "C" {
 
 int starkv_prefill_block_list(const int32_t* cu_seqlens, int num_prompts, int32_t* blocks, int capacity) {
+    // (keys, prompt, block) of every 128-row query block, the most keys first (ties in
+    // prompt then block order): the longest causal rows start first and the short ones
+    // fill the tail.
     if (!cu_seqlens || num_prompts < 0) return -1;
-    int nb = 0;
+    std::vector<std::array<int, 3>> all;
     for (int i = 0; i < num_prompts; ++i) {
         const int L = cu_seqlens[i + 1] - cu_seqlens[i];
         if (L < 0) return -1;
-        for (int b = 0; b * PF_QB < L; ++b) {
-            if (blocks && nb < capacity) {
-                blocks[2 * nb] = i;
-                blocks[2 * nb + 1] = b;
-            }
-            ++nb;
-        }
+        for (int b = 0; b * PF_QB < L; ++b) all.push_back({std::min(L, PF_QB * (b + 1)), i, b});
     }
-    return nb;
+    std::stable_sort(all.begin(), all.end(), [](const std::array<int, 3>& x, const std::array<int, 3>& y) {
+        return x[0] > y[0];
+    });
+    if (blocks)
+        for (int k = 0; k < (int)all.size() && k < capacity; ++k) {
+            blocks[2 * k] = all[k][1];
+            blocks[2 * k + 1] = all[k][2];
+        }
+    return (int)all.size();
 }
 
 int starkv_prefill_attention(void* stream, const void* query, int64_t q_s0, int64_t q_s1, int q_dtype,
@@ -340,7 +354,7 @@ int starkv_prefill_attention(void* stream, const void* query, int64_t q_s0, int6
     const void* fn = q_dtype == STARKV_F32 ? pf_pick<STARKV_F32>(out_dtype)
                      : q_dtype == STARKV_F16 ? pf_pick<STARKV_F16>(out_dtype)
                                              : pf_pick<STARKV_BF16>(out_dtype);
-    const int lds = 2 * PF_BUF;
+    const int lds = PF_NBUF * PF_BUF;
     static const void* raised[16];
     static int nraised = 0;
     bool seen = false;

@@ -4,6 +4,7 @@ The attention half of the STAR-KV layer's prefill (starkv_serve/attention.py:219
 the reference, which hands the lifted K and V to vLLM's flash_attn_varlen_func with
 causal=True): every prompt attends to itself, no cached context.
 """
+import ctypes
 from typing import List, Optional
 
 import torch
@@ -12,14 +13,21 @@ from starkv_serve import _hip
 
 
 def block_list(query_lens: List[int]) -> List[int]:
-    """The kernel's workgroup rows as a flat list (prompt, 128-row query block, ...),
-    the host-side order of starkv_prefill_block_list."""
-    out = []
-    for i, L in enumerate(query_lens):
+    """The kernel's workgroup rows, (prompt, query block) pairs flattened, from the
+    library's host helper starkv_prefill_block_list (the query block size is the
+    kernel's): the blocks with the most keys first."""
+    cu = [0]
+    for L in query_lens:
         if L < 0:
             raise ValueError(f"negative prompt length {L}")
-        out += [v for b in range((L + 127) // 128) for v in (i, b)]
-    return out
+        cu.append(cu[-1] + int(L))
+    lib = _hip.lib()
+    cu_c = (ctypes.c_int32 * len(cu))(*cu)
+    n = lib.starkv_prefill_block_list(cu_c, len(query_lens), None, 0)
+    buf = (ctypes.c_int32 * (2 * max(n, 1)))()
+    if n < 0 or lib.starkv_prefill_block_list(cu_c, len(query_lens), buf, n) != n:
+        raise RuntimeError("starkv_prefill_block_list failed")
+    return list(buf)[:2 * n]
 
 
 def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, query_lens: List[int], scale: float,

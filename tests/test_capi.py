@@ -178,19 +178,29 @@ def test_operators_refuse_cpu_tensors():
         _hip.ops().write_codes(t.view(1, 4), t.view(1, 4), t.view(1, 1, 4), s)
 
 
+def _block_list_restated(lens, qb=128):
+    """starkv_prefill_block_list restated: every (prompt, qb-row block), the blocks with
+    the most keys (min(L, qb (b + 1))) first, ties in prompt then block order."""
+    blocks = [(min(L, qb * (b + 1)), i, b) for i, L in enumerate(lens) for b in range((L + qb - 1) // qb)]
+    blocks.sort(key=lambda t: (-t[0], t[1], t[2]))
+    return [v for _, i, b in blocks for v in (i, b)]
+
+
 def test_prefill_block_list_host():
-    """starkv_prefill_block_list (C, host) and the wrapper's block_list agree: one
-    (prompt, 128-row block) pair per query block, empty prompts skipped; a bad prefix is
-    refused; the prefill entry point checks its arguments before launching."""
+    """starkv_prefill_block_list (C, host) against its restatement: one (prompt, 128-row
+    query block) pair per query block, empty prompts skipped, the longest causal rows
+    first; a bad prefix is refused; the prefill entry point checks its arguments before
+    launching."""
     from starkv_serve import _hip
     from starkv_serve.kernels.prefill import block_list
     L = _hip.lib()
-    lens = [1, 0, 128, 129, 300, 0, 5]
+    lens = [1, 0, 128, 129, 300, 0, 5, 257]
     cu = (ctypes.c_int32 * (len(lens) + 1))(*np.concatenate([[0], np.cumsum(lens)]).astype(int).tolist())
     n = L.starkv_prefill_block_list(cu, len(lens), None, 0)
     buf = (ctypes.c_int32 * (2 * n))()
-    assert L.starkv_prefill_block_list(cu, len(lens), buf, n) == n == 1 + 1 + 2 + 3 + 1
-    assert list(buf) == block_list(lens)
+    assert L.starkv_prefill_block_list(cu, len(lens), buf, n) == n == 1 + 1 + 2 + 3 + 1 + 3
+    assert list(buf) == _block_list_restated(lens) == block_list(lens)
+    assert list(buf)[:2] == [4, 2]  # the 300-token prompt's third block: 300 keys
     bad = (ctypes.c_int32 * 3)(0, 5, 2)
     assert L.starkv_prefill_block_list(bad, 2, None, 0) == -1
     rc = L.starkv_prefill_attention(None, None, 0, 0, 2, None, None, 0, 0, 1, None, None, 1, 32, 32, 64, 0.1, None,

@@ -38,7 +38,7 @@ CASES = {
     # name: (lengths, Hq, Hkv, q dtype)
     "one_token": ([1], 32, 32, torch.bfloat16),
     "tile_edges": ([63, 64, 65], 8, 8, torch.bfloat16),
-    "block_edges": ([127, 128, 129, 256], 4, 2, torch.bfloat16),
+    "block_edges": ([127, 128, 129, 255, 256, 257], 4, 2, torch.bfloat16),
     "ragged_gqa4": ([300, 17, 1000, 5], 32, 8, torch.bfloat16),
     "gqa8_fp16": ([200, 333], 16, 2, torch.float16),
     "fp32_query": ([150, 40], 8, 4, torch.float32),
