@@ -621,10 +621,12 @@ int device_cus() {
 }
 
 // tok_per_wg: tokens per workgroup the split aims for (at most the device's CUs
-// workgroups). 256 (16 pages) for two-pass calls, whose fp32 partial accumulators of
-// H x v_rank per workgroup and request would otherwise cost as much traffic as the V
-// codes they sum; 64 for one-pass calls, whose partials are small, so that a short batch
-// (one request of 4096 tokens) still spreads over many CUs.
+// workgroups). 128 (8 pages) for two-pass calls, whose fp32 partial accumulators of
+// H x v_rank per workgroup and request cost about as much traffic as the V codes they
+// sum when a workgroup has few pages (one request of 16384 tokens at V rank 1280: 77 us a
+// call at 256 tokens per workgroup, 67 at 128, 71 at 64); 64 for one-pass calls, whose
+// partials are small, so that a short batch (one request of 4096 tokens) still spreads
+// over many CUs.
 static int grid_for(int n, int max_seq_len, int tok_per_wg = 256) {
     const int64_t tokens = (int64_t)n * (int64_t)(max_seq_len > 0 ? max_seq_len : 1);
     int64_t want = (tokens + tok_per_wg - 1) / tok_per_wg;
@@ -940,7 +942,7 @@ int starkv_decode_grid_for(int cache_kind, int n, int num_heads, int num_kv_head
     } else {
         two = use_two_pass(cache_kind == STARKV_F16 ? FMT_F16 : FMT_BF16, k_width, v_rank, (k_width + v_rank) * 2, 0);
     }
-    return grid_for(n, max_seq_len, two ? 256 : 64);
+    return grid_for(n, max_seq_len, two ? 128 : 64);
 }
 
 int starkv_profile_begin(int max_calls, int mode) {
