@@ -44,6 +44,7 @@ CASES = {
     "fp32_query": ([150, 40], 8, 4, torch.float32),
     "empty_prompt": ([5, 0, 77, 0], 4, 4, torch.bfloat16),
     "long": ([2500], 4, 1, torch.bfloat16),
+    "gqa3": ([90, 200], 6, 2, torch.bfloat16),
 }
 
 
