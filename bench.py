@@ -333,7 +333,8 @@ def bench_write(n, quant, steps, warmup, seed=1004, layers=24, hidden=4096, num_
                 GBps=round(by / (fu * 1e-6) / 1e9, 1), hbm_frac=round(by / (fu * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
 
 
-def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, modes=("stock", "bf16", "quant")):
+def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, modes=("stock", "bf16", "quant"),
+                max_sessions=True):
     """Config 4: decode steps of a random-init Llama-2-7B-shaped model (32 layers, 32 heads
     x 128, hidden 4096, MLP 11008, vocab 32000). STAR-KV modes keep layers 0, 1, 2 and 31
     uncompressed and compress the others at the 0.75 ratio (K ranks, multiples of 16, keep
@@ -345,8 +346,9 @@ def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, mod
     sessions whose caches fit in the GPU's free memory (less `reserve_gb`). Per mode and
     concurrency: TPOT (median step), tok/s = sessions / TPOT, and attention per step (the
     KV writes and attention of all 32 layers, timed on their own, as bench_serving.py:62-115
-    sums them). Each figure twice: with each step (or each attention pass) replayed from one
-    HIP graph (`tpot_ms`, `tok_per_s`, `attention_us_per_step`: GPU time without host launch
+    sums them; `max_sessions` False: concurrency 1 only). Each figure twice: with each step
+    (or each attention pass) replayed from one HIP graph (`tpot_ms`, `tok_per_s`,
+    `attention_us_per_step`: GPU time without host launch
     gaps, the reference's attention figure being summed kernel time) and eager (`*_eager`:
     every launch from the host)."""
     import tempfile
@@ -449,7 +451,7 @@ def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, mod
                 free, _ = torch.cuda.mem_get_info()
                 n_max = max(1, int((free - reserve_gb * 1e9) // (pages * 16 * per_tok)))
                 r = dict(kv_bytes_per_token=per_tok)
-                for key, n in (("c1", 1), ("max_sessions", n_max)):
+                for key, n in (("c1", 1), ("max_sessions", n_max))[:2 if max_sessions else 1]:
                     log(f"config 4 {mode}: {n} sessions x {context}")
                     r[key] = run(model, n)
                     log(json.dumps(r[key]))
@@ -625,7 +627,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip every workload but the headline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["bf16", "quant", "write", "short", "wide", "wide_quant", "c0", "c3",
-                                       "model", "stock", "prefill"],
+                                       "model", "model_c1", "stock", "prefill"],
                     default=None, help="profile runs: time one workload only and print its summary")
     ap.add_argument("--copy-probe", type=float, default=0.0, metavar="GIB",
                     help="profile runs: only copy GIB GiB device to device 5 times (counter scaling)")
@@ -656,6 +658,7 @@ def main():
         "c0": lambda: summarize(*bench_lowrank([4096], K, Wm, seed=1000)),
         "c3": lambda: bench_c3(32, 2),
         "model": lambda: bench_model(),
+        "model_c1": lambda: bench_model(max_sessions=False),
         "stock": lambda: bench_stock(64, 8192, K, Wm),
         "prefill": lambda: bench_prefill(min(K, 10), min(Wm, 3)),
     }

@@ -7,9 +7,9 @@
 //   out   = (softmax(logit) @ V_codes) @ v_up_by_q[h]  paged_decode.py:105-147, 220-226
 //
 // MI355X design, three launches per call (all grids are functions of host ints):
-// 1. prep: workgroup 0 writes the prefix sums of the request lengths and the wave
-//    plan: whole query heads dealt to the 8 waves of a decode workgroup, so every wave
-//    owns a balanced set of rank tiles and every head lives in one wave. The other
+// 1. prep: workgroup 0 writes the prefix sums of the request lengths, workgroup 1 the
+//    wave plan: whole query heads dealt to the 8 waves of a decode workgroup, so every
+//    wave owns a balanced set of rank tiles and every head lives in one wave. The other
 //    workgroups fold AB for every (request, rank tile) in fp16, written in the
 //    A-operand lane order of v_mfma_f32_16x16x32_f16, so the decode kernel loads it
 //    straight into its final registers.
@@ -47,10 +47,11 @@
 namespace starkv {
 // ---------------------------------------------------------------------------
 // 1. prep: one launch of PREP_THR-thread workgroups. Workgroup 0 writes the prefix
-//    sums of the request lengths and the wave plan; every other workgroup folds AB for
-//    two rank tiles and up to PREP_REQ requests. Both read the rank-tile table, which
-//    each workgroup builds in LDS from the per-head ranks (bf16/fp16) or the per-tile
-//    arrays (3.2-bit).
+//    sums of the request lengths, workgroup 1 the wave plan (the two side by side: the
+//    plan is the longer chain); every other workgroup folds AB for two rank tiles and up
+//    to PREP_REQ requests. The plan and the folds read the rank-tile table, which each
+//    workgroup builds in LDS from the per-head ranks (bf16/fp16) or the per-tile arrays
+//    (3.2-bit).
 // ---------------------------------------------------------------------------
 constexpr int PREP_THR = 256;
 constexpr int PREP_REQ = 8;  // requests per fold workgroup
@@ -160,21 +161,12 @@ __device__ __forceinline__ int wave_min_i(int v) {
 }
 
 // Workgroup 0 of prep. Writes hdr[0] = tokens per decode workgroup, hdr[1 + b] = first
-// token of request b in the concatenation, and the plan: per wave (PLAN_STRIDE ints)
-// [0] its tiles, [1] its heads, [2] its heads with tiles, [3] whether every head of it
-// has at most 4 tiles, [8 + s] the tile of slot s, [32 + k], [40 + k], [48 + k] head k's
-// query head, first slot and tile count, [PW_SLOTS + s] the slot words; then one int,
-// 1 if the heads fit the waves (every wave at most MAX_SLOTS tiles).
-__device__ void prep_setup(const PrepArgs& a, const TileTable& tt, int tid, int (&v)[4]) {
+// token of request b in the concatenation (v: this thread's requests 4 tid .. 4 tid + 3).
+__device__ void prep_prefix(const PrepArgs& a, int tid, int (&v)[4]) {
     __shared__ int s_wsum[PREP_THR / 64];
-    __shared__ int s_byp[MAX_H];   // query head at each position of the size order
-    __shared__ int s_load[NWAVE];  // tiles per decode wave
-    __shared__ int s_plan[NWAVE * PLAN_STRIDE + 1];
     const int lane = tid & 63, wave = tid >> 6;
     int* hdr = (int*)a.ws;
-
-    // Prefix sums of min(max(seq_len, 0), max_seq_len); thread tid takes requests
-    // 4 tid .. 4 tid + 3.
+    // Prefix sums of min(max(seq_len, 0), max_seq_len).
     int s = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -188,16 +180,6 @@ __device__ void prep_setup(const PrepArgs& a, const TileTable& tt, int tid, int 
         if (lane >= o) incl += y;
     }
     if (lane == 63) s_wsum[wave] = incl;
-    // Heads by decreasing tile count (ties: lower head first).
-    if (tid < a.Hq) {
-        const int mine = tt.hn[tid];
-        int pos = 0;
-#pragma unroll 8
-        for (int h = 0; h < a.Hq; ++h) pos += tt.hn[h] > mine || (tt.hn[h] == mine && h < tid);
-        s_byp[pos] = tid;
-    }
-    for (int i = tid; i < NWAVE * PLAN_STRIDE + 1; i += PREP_THR) s_plan[i] = 0;
-    if (tid < NWAVE) s_load[tid] = 0;
     __syncthreads();
     int run = incl - s;
 #pragma unroll
@@ -209,6 +191,29 @@ __device__ void prep_setup(const PrepArgs& a, const TileTable& tt, int tid, int 
     }
     if (tid == PREP_THR - 1) hdr[0] = (run + a.grid - 1) / a.grid;
     if (tid == 0) hdr[1] = 0;
+}
+
+// Workgroup 1 of prep: the wave plan. Per wave (PLAN_STRIDE ints) [0] its tiles, [1] its
+// heads, [2] its heads with tiles, [3] whether every head of it has at most 4 tiles,
+// [8 + s] the tile of slot s, [32 + k], [40 + k], [48 + k] head k's query head, first slot
+// and tile count, [PW_SLOTS + s] the slot words; then one int, 1 if the heads fit the
+// waves (every wave at most MAX_SLOTS tiles).
+__device__ void prep_plan(const PrepArgs& a, const TileTable& tt, int tid) {
+    __shared__ int s_byp[MAX_H];   // query head at each position of the size order
+    __shared__ int s_load[NWAVE];  // tiles per decode wave
+    __shared__ int s_plan[NWAVE * PLAN_STRIDE + 1];
+    const int lane = tid & 63, wave = tid >> 6;
+    // Heads by decreasing tile count (ties: lower head first).
+    if (tid < a.Hq) {
+        const int mine = tt.hn[tid];
+        int pos = 0;
+#pragma unroll 8
+        for (int h = 0; h < a.Hq; ++h) pos += tt.hn[h] > mine || (tt.hn[h] == mine && h < tid);
+        s_byp[pos] = tid;
+    }
+    for (int i = tid; i < NWAVE * PLAN_STRIDE + 1; i += PREP_THR) s_plan[i] = 0;
+    if (tid < NWAVE) s_load[tid] = 0;
+    __syncthreads();
 
     // Wave plan, in wave 0 with lane p holding the head at position p of the size order.
     // Heads are dealt to the 8 waves in snake order (0..7, 7..0, 0..7, ...), so every
@@ -420,19 +425,21 @@ __global__ __launch_bounds__(PREP_THR) void prep_kernel(PrepArgs a) {
     __shared__ TileTable tt;
     const int tid = threadIdx.x;
     if (blockIdx.x == 0) {
-        int v[4];  // request lengths, read before the table's barriers
+        int v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = 4 * tid + i < a.n ? a.seq_lens[4 * tid + i] : 0;
-        tile_table(a, tt, tid);
-        prep_setup(a, tt, tid, v);
+        prep_prefix(a, tid, v);
+        return;
+    }
+    tile_table(a, tt, tid);
+    if (blockIdx.x == 1) {
+        prep_plan(a, tt, tid);
+    } else if (a.q_dt == STARKV_BF16) {
+        prep_fold_q<STARKV_BF16>(a, tt, tid, blockIdx.x - 2);
+    } else if (a.q_dt == STARKV_F16) {
+        prep_fold_q<STARKV_F16>(a, tt, tid, blockIdx.x - 2);
     } else {
-        tile_table(a, tt, tid);
-        if (a.q_dt == STARKV_BF16)
-            prep_fold_q<STARKV_BF16>(a, tt, tid, blockIdx.x - 1);
-        else if (a.q_dt == STARKV_F16)
-            prep_fold_q<STARKV_F16>(a, tt, tid, blockIdx.x - 1);
-        else
-            prep_fold_q<STARKV_F32>(a, tt, tid, blockIdx.x - 1);
+        prep_fold_q<STARKV_F32>(a, tt, tid, blockIdx.x - 2);
     }
 }
 
@@ -446,7 +453,7 @@ __global__ __launch_bounds__(PREP_THR) void prep_kernel(PrepArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int MERGE_REQ = 4;
 constexpr int MERGE_THR = 64 * MERGE_REQ;
-constexpr int MERGE_PRE = 8;  // partials per request whose accumulator rows are read in the second round
+constexpr int MERGE_PRE = 16;  // partials per request whose accumulator rows are read in the second round
 constexpr int MERGE_CB = 4;   // column blocks of 64: v_rank <= 256
 
 // LDS of one merge workgroup: v_up_by_q[h] (v_rank x 128 WT), then the merged
@@ -709,8 +716,8 @@ static bool use_two_pass(int fmt, int k_width, int v_rank, int row_bytes, int v_
     return g_path == 2 || (g_path == 0 && !one_pass_fits(fmt, k_width, v_rank, row_bytes, v_nout));
 }
 
-// Host restatement of the wave plan that workgroup 0 of prep_kernel builds
-// (prep_setup): query heads sorted by decreasing rank tiles (ties: lower head first),
+// Host restatement of the wave plan that workgroup 1 of prep_kernel builds
+// (prep_plan): query heads sorted by decreasing rank tiles (ties: lower head first),
 // dealt to the 8 decode waves in snake order, then the swap that lowers the most loaded
 // wave the most, while one does. True if every wave ends with at most MAX_SLOTS tiles,
 // which is when the decode kernels run the layer (otherwise they return NaN rows).
@@ -870,7 +877,7 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     pa.sc = a.scale * LOG2E;
     pa.ws = p.ws; pa.ws_plan = wl.plan; pa.ws_ab = wl.ab;
     pa.tile_pairs = (TT + 1) / 2;
-    const int prep_grid = 1 + pa.tile_pairs * ((a.n + PREP_REQ - 1) / PREP_REQ);
+    const int prep_grid = 2 + pa.tile_pairs * ((a.n + PREP_REQ - 1) / PREP_REQ);
     hipLaunchKernelGGL(prep_kernel, dim3(prep_grid), dim3(PREP_THR), 0, stream, pa);
     SKV_HIP(hipGetLastError());
     if (timed && g_prof.mode == 0) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));

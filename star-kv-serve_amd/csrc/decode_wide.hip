@@ -381,22 +381,26 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
 
 // ---------------------------------------------------------------------------
 // Merge of the two-pass partials, in two launches.
-// merge_cols_kernel<MCW>: one workgroup per (request, head, column block): the
-//   log-sum-exp weights of the request's slots, then each column's weighted sum of their
-//   accumulators, four loads in flight, divided by the total, into o [n][Hq][ld] (NaN for
-//   a request with no tokens, as the reference's softmax over an empty row). MCW = 1: the
-//   four waves take different columns (1024 per workgroup), each over every slot; MCW = 4,
-//   for requests split over many workgroups (a few long requests): wave w sums slots w,
-//   w + 4, ... of 256 columns, then the four waves' sums are added.
-// lift_kernel<DT, REQ, THR>: one workgroup per (head, REQ requests): out = o @ v_up_by_q[h],
-//   each thread 8 output columns over a THR / 16-th of the rank columns, LIFT_U rows in
-//   flight, then a reduction over those parts. 8 requests x 512 threads; for at most 8
-//   requests, 2 x 1024 (more rows in flight per workgroup, more workgroups).
+// merge_cols_kernel<MCW, U>: one workgroup per (request, head, column block): the
+//   log-sum-exp weights of the request's slots (the first 256 kept in registers), then each
+//   column's weighted sum of their accumulators, U partials' loads in flight, divided by the
+//   total, into o [n][Hq][ld] (NaN for a request with no tokens, as the reference's softmax
+//   over an empty row). MCW = 1: the four waves take different columns (1024 per
+//   workgroup), each over every slot; MCW = 4, for requests split over many workgroups (a
+//   few long requests): wave w sums slots w, w + 4, ... of 256 columns, then the four
+//   waves' sums are added.
+// lift_kernel<DT, REQ, THR, DQ>: one workgroup per (head, REQ requests, 8 DQ output
+//   columns): out = o @ v_up_by_q[h], each thread 8 output columns over a THR / DQ-th of the
+//   rank columns, LIFT_U rows in flight, then a reduction over those parts. 8 requests x
+//   512 threads x all 128 columns; for at most 8 requests, 2 x 1024 threads x 32 columns
+//   (four workgroups per head and request pair: one request's v_up_by_q rows are read by
+//   128 workgroups instead of 32).
 // ---------------------------------------------------------------------------
 constexpr int MC_THR = 256;
-constexpr int LIFT_U = 8;  // v_up_by_q rows per thread in flight
+constexpr int MC_WREG = 4;  // slot weights held in registers: 64 MC_WREG slots
+constexpr int LIFT_U = 8;   // v_up_by_q rows per thread in flight
 
-template <int MCW>
+template <int MCW, int U>
 __global__ __launch_bounds__(MC_THR) void merge_cols_kernel(const uint8_t* __restrict__ ws, size_t ws_plan, size_t ws_m,
                                                             size_t ws_l, size_t ws_acc, size_t ws_o, int n, int Hq,
                                                             int v_rank, int ld) {
@@ -414,13 +418,27 @@ __global__ __launch_bounds__(MC_THR) void merge_cols_kernel(const uint8_t* __res
     const bool live = pe > pb && S > 0 && planned;
     const int k_lo = live ? pb / S : 0, nk = live ? (pe - 1) / S - k_lo + 1 : 0;
     const int64_t s0 = (int64_t)(k_lo + b) * Hq + h;  // slot row of partial k: s0 + k Hq
-    // Every wave forms the same weights (the loads hit the same lines).
-    float M = -INFINITY;
-    for (int k = lane; k < nk; k += 64) M = fmaxf(M, wm[s0 + (int64_t)k * Hq]);
+    // Every wave forms the same weights (the loads hit the same lines). Slot k < 64 MC_WREG:
+    // its max in lane k % 64 of mk[k / 64], its weight in wk[k / 64].
+    float mk[MC_WREG], lk[MC_WREG];
+#pragma unroll
+    for (int j = 0; j < MC_WREG; ++j) {
+        const int k = lane + 64 * j;
+        mk[j] = k < nk ? wm[s0 + (int64_t)k * Hq] : -INFINITY;
+        lk[j] = k < nk ? wl[s0 + (int64_t)k * Hq] : 0.f;
+    }
+    float M = mk[0];
+#pragma unroll
+    for (int j = 1; j < MC_WREG; ++j) M = fmaxf(M, mk[j]);
+    for (int k = lane + 64 * MC_WREG; k < nk; k += 64) M = fmaxf(M, wm[s0 + (int64_t)k * Hq]);
     M = wave_max(M);
-    const float wk = lane < nk ? exp2f(wm[s0 + (int64_t)lane * Hq] - M) : 0.f;
-    float l = lane < nk ? wl[s0 + (int64_t)lane * Hq] * wk : 0.f;
-    for (int k = lane + 64; k < nk; k += 64) {
+    float wk[MC_WREG], l = 0.f;
+#pragma unroll
+    for (int j = 0; j < MC_WREG; ++j) {
+        wk[j] = lane + 64 * j < nk ? exp2f(mk[j] - M) : 0.f;
+        l = fmaf(lk[j], wk[j], l);
+    }
+    for (int k = lane + 64 * MC_WREG; k < nk; k += 64) {
         const int64_t sl = s0 + (int64_t)k * Hq;
         l += wl[sl] * exp2f(wm[sl] - M);
     }
@@ -428,26 +446,34 @@ __global__ __launch_bounds__(MC_THR) void merge_cols_kernel(const uint8_t* __res
     const float inv = live ? 1.f / l : __builtin_nanf("");
     float* o = (float*)(ws + ws_o) + ((int64_t)b * Hq + h) * ld;
     const int c4 = blockIdx.z * CPW + 4 * (MCW > 1 ? lane : tid);
+    // Weight of slot k (wave-uniform k). The lane reads come from wk as formed above, with
+    // every lane active (inside the column branch below some lanes are not).
+    auto weight = [&](int k, int64_t sl) -> float {
+        if (k < 64 * MC_WREG) {
+            float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk[0]), k & 63));
+#pragma unroll
+            for (int j = 1; j < MC_WREG; ++j)
+                if (k >= 64 * j) x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk[j]), k & 63));
+            return x;
+        }
+        return exp2f(wm[sl] - M);
+    };
     f32x4_t a = {0.f, 0.f, 0.f, 0.f};
     if (c4 < v_rank) {
         int k = w;  // wave-uniform
-        for (; k + 3 * MCW < nk; k += 4 * MCW) {  // four partials' loads in flight
-            f32x4_t r[4];
-            float wt[4];
+        for (; k + (U - 1) * MCW < nk; k += U * MCW) {  // U partials' loads in flight
+            f32x4_t r[U];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < U; ++u) r[u] = *(const f32x4_t*)(wa + (s0 + (int64_t)(k + u * MCW) * Hq) * ld + c4);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
                 const int ku = k + u * MCW;
-                const int64_t sl = s0 + (int64_t)ku * Hq;
-                r[u] = *(const f32x4_t*)(wa + sl * ld + c4);
-                wt[u] = ku < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), ku)) : exp2f(wm[sl] - M);
+                a += r[u] * weight(ku, s0 + (int64_t)ku * Hq);
             }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) a += r[u] * wt[u];
         }
         for (; k < nk; k += MCW) {
             const int64_t sl = s0 + (int64_t)k * Hq;
-            const float wt = k < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k)) : exp2f(wm[sl] - M);
-            a += *(const f32x4_t*)(wa + sl * ld + c4) * wt;
+            a += *(const f32x4_t*)(wa + sl * ld + c4) * weight(k, sl);
         }
     }
     if constexpr (MCW == 1) {
@@ -464,18 +490,36 @@ __global__ __launch_bounds__(MC_THR) void merge_cols_kernel(const uint8_t* __res
     }
 }
 
-template <int DT, int LIFT_REQ, int LIFT_THR>
+template <int DT, int LIFT_REQ, int LIFT_THR, int DQ>
 __global__ __launch_bounds__(LIFT_THR) void lift_kernel(const uint8_t* __restrict__ ws, size_t ws_o, int n, int Hq,
                                                         int v_rank, int ld, const void* __restrict__ vup,
                                                         int64_t vu_s0, int64_t vu_s1, void* __restrict__ out,
                                                         int64_t o_s0, int64_t o_s1, int out_dt) {
+    static_assert(DQ == 16 || DQ == 4, "8 DQ output columns per workgroup: 128 or 32");
     constexpr int LIFT_WAVES = LIFT_THR / 64;
+    constexpr int DW = 8 * DQ;  // output columns of this workgroup
     extern __shared__ __align__(16) uint8_t s_dyn[];
     float* s_o = (float*)s_dyn;    // [LIFT_REQ][ld]
-    float* s_red = (float*)s_dyn;  // [LIFT_WAVES][LIFT_REQ][128], over s_o once the products are done
+    float* s_red = (float*)s_dyn;  // [LIFT_WAVES][LIFT_REQ][DW], over s_o once the products are done
     const int h = blockIdx.x, b0 = blockIdx.y * LIFT_REQ;  // head in x: a head's workgroups share one XCD's L2
+    const int d0 = blockIdx.z * DW;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const float* og = (const float*)(ws + ws_o);
+    // Thread (dq, cp): output columns d0 + 8 dq .. + 7 over rank columns c = cp (mod CP);
+    // LIFT_U rows of v_up_by_q are loaded before their products, so their latencies overlap
+    // (the first LIFT_U before the rows o are staged).
+    constexpr int CP = LIFT_THR / DQ;
+    const int dq = tid % DQ, cp = tid / DQ;
+    const int64_t vh = (int64_t)h * vu_s0 + d0 + 8 * dq;
+    float u[LIFT_U][8];
+    auto load_rows = [&](int c0) {
+#pragma unroll
+        for (int j = 0; j < LIFT_U; ++j) {
+            const int c = min(c0 + CP * j, v_rank - 1);  // past the end: a valid row, weighted 0 below
+            load8_f(vup, vh + (int64_t)c * vu_s1, DT, u[j]);
+        }
+    };
+    load_rows(cp);
     for (int i = 4 * tid; i < LIFT_REQ * ld; i += 4 * LIFT_THR) {
         const int r = i / ld, c = i - r * ld;
         f32x4_t v = {0.f, 0.f, 0.f, 0.f};
@@ -483,23 +527,13 @@ __global__ __launch_bounds__(LIFT_THR) void lift_kernel(const uint8_t* __restric
         *(f32x4_t*)(s_o + i) = v;
     }
     __syncthreads();
-    // Thread (dq, cp): output columns 8 dq .. 8 dq + 7 over rank columns c = cp (mod CP);
-    // LIFT_U rows of v_up_by_q are loaded before their products, so their latencies overlap.
-    constexpr int CP = LIFT_THR / 16;
-    const int dq = tid & 15, cp = tid >> 4;
     float acc[LIFT_REQ][8];
 #pragma unroll
     for (int r = 0; r < LIFT_REQ; ++r)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[r][e] = 0.f;
-    const int64_t vh = (int64_t)h * vu_s0 + 8 * dq;
     for (int c0 = cp; c0 < v_rank; c0 += CP * LIFT_U) {
-        float u[LIFT_U][8];
-#pragma unroll
-        for (int j = 0; j < LIFT_U; ++j) {
-            const int c = min(c0 + CP * j, v_rank - 1);  // past the end: a valid row, weighted 0 below
-            load8_f(vup, vh + (int64_t)c * vu_s1, DT, u[j]);
-        }
+        if (c0 != cp) load_rows(c0);
 #pragma unroll
         for (int j = 0; j < LIFT_U; ++j) {
             const int c = c0 + CP * j;
@@ -511,26 +545,35 @@ __global__ __launch_bounds__(LIFT_THR) void lift_kernel(const uint8_t* __restric
             }
         }
     }
-    // Sum over the wave's four phases (lanes l, l ^ 16, l ^ 32, l ^ 48), then over the waves.
+    // Sum over the lanes of the wave with the same dq (lane = dq + DQ k): for DQ = 4 first
+    // over lanes l, l ^ 4, l ^ 8, l ^ 12 of each row (row rotations by 8 and 4), then over
+    // the four rows; then over the waves.
 #pragma unroll
     for (int r = 0; r < LIFT_REQ; ++r)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[r][e] = sum_rows(acc[r][e]);
+        for (int e = 0; e < 8; ++e) {
+            float v = acc[r][e];
+            if constexpr (DQ == 4) {
+                v += dpp_f<0x128>(v);  // row_ror:8
+                v += dpp_f<0x124>(v);  // row_ror:4
+            }
+            acc[r][e] = sum_rows(v);
+        }
     __syncthreads();  // every wave is done with s_o
-    if (lane < 16) {
+    if (lane < DQ) {
 #pragma unroll
         for (int r = 0; r < LIFT_REQ; ++r)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) s_red[(w * LIFT_REQ + r) * 128 + 8 * dq + e] = acc[r][e];
+            for (int e = 0; e < 8; ++e) s_red[(w * LIFT_REQ + r) * DW + 8 * dq + e] = acc[r][e];
     }
     __syncthreads();
-    for (int i = tid; i < LIFT_REQ * 128; i += LIFT_THR) {
-        const int r = i >> 7, d = i & 127, b = b0 + r;
+    for (int i = tid; i < LIFT_REQ * DW; i += LIFT_THR) {
+        const int r = i / DW, d = i % DW, b = b0 + r;
         if (b >= n) continue;
         float v = 0.f;
 #pragma unroll
-        for (int k = 0; k < LIFT_WAVES; ++k) v += s_red[(k * LIFT_REQ + r) * 128 + d];
-        store_f(out, (int64_t)b * o_s0 + (int64_t)h * o_s1 + d, out_dt, v);
+        for (int k = 0; k < LIFT_WAVES; ++k) v += s_red[(k * LIFT_REQ + r) * DW + d];
+        store_f(out, (int64_t)b * o_s0 + (int64_t)h * o_s1 + d0 + d, out_dt, v);
     }
 }
 
@@ -565,10 +608,10 @@ int raise_lds(const void* fn, int bytes) {
     return STARKV_OK;
 }
 
-// Dynamic LDS of lift_kernel<DT, req, thr>: the rows o [req][ld], then (over them) the
-// per-wave sums [thr / 64][req][128].
-size_t lift_lds(int ld, int req = 8, int thr = 512) {
-    return std::max((size_t)req * ld * 4, (size_t)(thr / 64) * req * 128 * 4);
+// Dynamic LDS of lift_kernel<DT, req, thr, dq>: the rows o [req][ld], then (over them)
+// the per-wave sums [thr / 64][req][8 dq].
+size_t lift_lds(int ld, int req = 8, int thr = 512, int dq = 16) {
+    return std::max((size_t)req * ld * 4, (size_t)(thr / 64) * req * 8 * dq * 4);
 }
 
 }  // namespace
@@ -676,32 +719,32 @@ int launch_merge_wide(const DecodeParams& p, int grid, int w_dt, const void* vup
     SKV_CHECK(lds <= (size_t)PV_MAX_DYN_LDS, "decode: v_rank %d too large for the merge", p.v_rank);
     // Slots per request: about grid / n + 1. Many (a few long requests): split them over waves.
     if (grid >= 8 * p.n)
-        hipLaunchKernelGGL(merge_cols_kernel<4>, dim3(p.n, p.Hq, (p.v_rank + 255) / 256), dim3(MC_THR), 0, stream,
-                           (const uint8_t*)p.ws, p.ws_plan, p.ws_m, p.ws_l, p.ws_acc, p.ws_o, p.n, p.Hq, p.v_rank,
-                           p.acc_ld);
+        hipLaunchKernelGGL((merge_cols_kernel<4, 16>), dim3(p.n, p.Hq, (p.v_rank + 255) / 256), dim3(MC_THR), 0,
+                           stream, (const uint8_t*)p.ws, p.ws_plan, p.ws_m, p.ws_l, p.ws_acc, p.ws_o, p.n, p.Hq,
+                           p.v_rank, p.acc_ld);
     else
-        hipLaunchKernelGGL(merge_cols_kernel<1>, dim3(p.n, p.Hq, (p.v_rank + 1023) / 1024), dim3(MC_THR), 0, stream,
-                           (const uint8_t*)p.ws, p.ws_plan, p.ws_m, p.ws_l, p.ws_acc, p.ws_o, p.n, p.Hq, p.v_rank,
-                           p.acc_ld);
+        hipLaunchKernelGGL((merge_cols_kernel<1, 8>), dim3(p.n, p.Hq, (p.v_rank + 1023) / 1024), dim3(MC_THR), 0,
+                           stream, (const uint8_t*)p.ws, p.ws_plan, p.ws_m, p.ws_l, p.ws_acc, p.ws_o, p.n, p.Hq,
+                           p.v_rank, p.acc_ld);
     SKV_HIP(hipGetLastError());
     const bool small = p.n <= 8;
-    const int req = small ? 2 : 8, thr = small ? 1024 : 512;
-    const void* fn = small ? (w_dt == STARKV_BF16 ? (const void*)&lift_kernel<STARKV_BF16, 2, 1024>
-                              : w_dt == STARKV_F16 ? (const void*)&lift_kernel<STARKV_F16, 2, 1024>
-                                                   : (const void*)&lift_kernel<STARKV_F32, 2, 1024>)
-                           : (w_dt == STARKV_BF16 ? (const void*)&lift_kernel<STARKV_BF16, 8, 512>
-                              : w_dt == STARKV_F16 ? (const void*)&lift_kernel<STARKV_F16, 8, 512>
-                                                   : (const void*)&lift_kernel<STARKV_F32, 8, 512>);
+    const int req = small ? 2 : 8, thr = small ? 1024 : 512, dq = small ? 4 : 16;
+    const void* fn = small ? (w_dt == STARKV_BF16 ? (const void*)&lift_kernel<STARKV_BF16, 2, 1024, 4>
+                              : w_dt == STARKV_F16 ? (const void*)&lift_kernel<STARKV_F16, 2, 1024, 4>
+                                                   : (const void*)&lift_kernel<STARKV_F32, 2, 1024, 4>)
+                           : (w_dt == STARKV_BF16 ? (const void*)&lift_kernel<STARKV_BF16, 8, 512, 16>
+                              : w_dt == STARKV_F16 ? (const void*)&lift_kernel<STARKV_F16, 8, 512, 16>
+                                                   : (const void*)&lift_kernel<STARKV_F32, 8, 512, 16>);
     int rc = raise_lds(fn, PV_MAX_DYN_LDS);
     if (rc) return rc;
-    const size_t lds2 = lift_lds(p.acc_ld, req, thr);
+    const size_t lds2 = lift_lds(p.acc_ld, req, thr, dq);
     SKV_CHECK(lds2 <= (size_t)PV_MAX_DYN_LDS, "decode: v_rank %d too large for the lift", p.v_rank);
     const uint8_t* ws = p.ws;
     size_t wo = p.ws_o;
     int n = p.n, Hq = p.Hq, vr = p.v_rank, ld = p.acc_ld;
     void* args[] = {(void*)&ws, (void*)&wo, (void*)&n, (void*)&Hq, (void*)&vr, (void*)&ld, (void*)&vup,
                     (void*)&vu_s0, (void*)&vu_s1, (void*)&out, (void*)&o_s0, (void*)&o_s1, (void*)&out_dt};
-    SKV_HIP(hipLaunchKernel(fn, dim3(p.Hq, (p.n + req - 1) / req), dim3(thr), args, lds2, stream));
+    SKV_HIP(hipLaunchKernel(fn, dim3(p.Hq, (p.n + req - 1) / req, 128 / (8 * dq)), dim3(thr), args, lds2, stream));
     return STARKV_OK;
 }
 

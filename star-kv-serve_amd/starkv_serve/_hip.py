@@ -166,6 +166,21 @@ def profile_end() -> list:
     return [buf[i] for i in range(k)]
 
 
+def output_for(out, shape, dtype, device) -> torch.Tensor:
+    """The decode's output: a new tensor of `shape` and `dtype`, or the caller's `out`
+    (any of bf16 / fp16 / fp32, last dimension contiguous), which the kernels write in
+    place."""
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    if tuple(out.shape) != tuple(shape):
+        raise ValueError(f"out has shape {tuple(out.shape)}, expected {tuple(shape)}")
+    if out.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError(f"out dtype {out.dtype} (bf16, fp16 or fp32)")
+    if out.device != torch.device(device) or out.stride(-1) != 1:
+        raise ValueError("out must be on the query's device with a contiguous last dimension")
+    return out
+
+
 def require_cuda(*ts: torch.Tensor) -> None:
     dev = ts[0].device
     for t in ts:

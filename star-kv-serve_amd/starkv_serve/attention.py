@@ -67,6 +67,15 @@ class StarKVMetadata:
     prefill_seq_lens_cpu: Optional[List[int]] = None
     prefill_query_start_loc_cpu: Optional[List[int]] = None
 
+    def decode_lens(self, nd: int) -> torch.Tensor:
+        """seq_lens[:nd] with padding rows (length 0) given one (null-block) position to
+        attend to: formed once per step and shared by every layer."""
+        c = self.__dict__.get("_decode_lens")
+        if c is None or c[0] != nd:
+            c = (nd, self.seq_lens[:nd].clamp(min=1))
+            self.__dict__["_decode_lens"] = c
+        return c[1]
+
 
 try:  # looked up once: forward runs every layer of every step
     from vllm.config import CUDAGraphMode, get_current_vllm_config
@@ -298,18 +307,17 @@ class StarKVAttentionImpl:
         full = _vllm_in_full_graph() if in_full_graph is None else in_full_graph
         # Inside a full graph nothing may depend on the step's lengths: the span is fixed.
         span = self.max_model_len if full else max(md.max_seq_len, 1)
-        # Padding rows have length 0; give them one (null-block) position to attend to.
-        seq_lens = md.seq_lens[:nd].clamp(min=1)
+        seq_lens = md.decode_lens(nd)
         cs = getattr(self, "cos_sin16", None)
         if cs is None:
             cs = self.rotary_emb.cos_sin_cache
+        # The kernels write `out` in its own dtype and strides (no copy of the result).
         if self.row is None:
-            o = paged_starkv_decode(q, cache, md.block_table[:nd], seq_lens, span, self.k_up, self.k_ranks,
-                                    self.k_head_offsets, self.k_width, self.v_up_by_q, cs, self.scale)
+            paged_starkv_decode(q, cache, md.block_table[:nd], seq_lens, span, self.k_up, self.k_ranks,
+                                self.k_head_offsets, self.k_width, self.v_up_by_q, cs, self.scale, out=out)
         else:
-            o = paged_quant_decode(q, cache, md.block_table[:nd], seq_lens, span, self.row, self.k_up,
-                                   self.head_of_lane, self.k_tiles, self.v_up_by_q, cs, self.scale)
-        out.copy_(o)
+            paged_quant_decode(q, cache, md.block_table[:nd], seq_lens, span, self.row, self.k_up,
+                               self.head_of_lane, self.k_tiles, self.v_up_by_q, cs, self.scale, out=out)
 
 
 if _HAVE_VLLM:  # pragma: no cover - vLLM is not installed in this image

@@ -25,6 +25,7 @@ Layout contract (reference paged_decode.py:150-174, attention.py:158-160):
   cos_sin_cache  [>= max_seq_len, 128] = cat(cos, sin)
 """
 import weakref
+from typing import Optional
 
 import torch
 
@@ -175,11 +176,15 @@ def paged_starkv_decode(
     cos_sin_cache: torch.Tensor,
     scale: float,
     v_programs: int = TARGET_V_PROGRAMS,
+    *,
+    out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attention output per query head, ``[n, H_q, head_dim]`` (paged_decode.py:150-226).
 
     ``v_programs`` is accepted for API compatibility; the split-K layout is chosen
-    by the library from the device and ``(n, max_seq_len)``.
+    by the library from the device and ``(n, max_seq_len)``. ``out`` (keyword only, not in
+    the reference's signature): a tensor of that shape, bf16 / fp16 / fp32, written in place
+    and returned (the attention layer hands over its output rows, saving a copy).
     """
     del v_programs
     n, num_heads, head_dim = query.shape
@@ -198,7 +203,7 @@ def paged_starkv_decode(
     if kv_cache.stride(-1) != 1 or query.stride(-1) != 1 or k_up.stride(-1) != 1 or v_up_by_q.stride(-1) != 1:
         raise ValueError("STAR-KV HIP decode: the last dimension of every operand must be contiguous")
 
-    out = torch.empty((n, num_heads, head_dim), dtype=v_up_by_q.dtype, device=query.device)
+    out = _hip.output_for(out, (n, num_heads, head_dim), v_up_by_q.dtype, query.device)
     if n == 0:
         return out
     ops = _hip.ops()

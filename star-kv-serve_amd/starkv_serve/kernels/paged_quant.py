@@ -16,6 +16,7 @@ K logits on MFMA and split-K partials merged and lifted at the end.
 """
 import math
 from dataclasses import dataclass
+from typing import Optional
 
 import torch
 
@@ -179,11 +180,15 @@ def paged_quant_decode(
     cos_sin_cache: torch.Tensor,
     scale: float,
     target_v_programs: int = 2048,
+    *,
+    out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attention output per query head, ``[n, H, 128]`` (paged_quant.py:357-411). MHA only.
 
     ``head_of_lane`` and ``target_v_programs`` are accepted for API compatibility; the
-    per-tile table ``k_tiles`` is what the kernel reads.
+    per-tile table ``k_tiles`` is what the kernel reads. ``out`` (keyword only, not in the
+    reference's signature): a tensor of that shape, bf16 / fp16 / fp32, written in place and
+    returned.
     """
     del head_of_lane, target_v_programs
     n, H, D = query.shape
@@ -194,7 +199,7 @@ def paged_quant_decode(
     _hip.require_cuda(query, kv_cache, block_table, seq_lens, k_up, th, tn, tl, v_up_by_q, cos_sin_cache)
     if kv_cache.stride(-1) != 1 or query.stride(-1) != 1 or k_up.stride(-1) != 1 or v_up_by_q.stride(-1) != 1:
         raise ValueError("STAR-KV HIP decode: the last dimension of every operand must be contiguous")
-    out = torch.empty((n, H, D), dtype=v_up_by_q.dtype, device=query.device)
+    out = _hip.output_for(out, (n, H, D), v_up_by_q.dtype, query.device)
     if n == 0:
         return out
     ops = _hip.ops()

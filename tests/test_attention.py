@@ -92,3 +92,31 @@ def test_forward_profiling_run_and_rejections(layers):
         impl.forward(None, out, out, out, out, _md(1, 1, prompt=2, cached=3), out)
     with pytest.raises(NotImplementedError, match="output quantization"):
         impl.forward(None, out, out, out, out, _md(3, 0), out, output_scale=1.0)
+
+
+def test_decode_lens_formed_once_per_step():
+    """Padding rows (length 0) get one position; the clamped lengths are formed once per
+    step and shared by every layer's decode."""
+    md = StarKVMetadata(num_actual_tokens=3, num_decodes=3, num_decode_tokens=3, num_prefills=0, max_seq_len=9,
+                        seq_lens=torch.tensor([5, 0, 9, 7], dtype=torch.int32),
+                        block_table=torch.zeros(4, 1, dtype=torch.int32),
+                        slot_mapping=torch.zeros(3, dtype=torch.int64))
+    a = md.decode_lens(3)
+    assert a.tolist() == [5, 1, 9] and a.dtype == torch.int32
+    assert md.decode_lens(3) is a
+    assert md.decode_lens(2).tolist() == [5, 1]
+
+
+def test_decode_output_argument_checked():
+    """`out=` of the decode wrappers: shape, dtype and layout are checked before any launch."""
+    from starkv_serve import _hip
+    fresh = _hip.output_for(None, (2, 4, 128), torch.bfloat16, "cpu")
+    assert fresh.shape == (2, 4, 128) and fresh.dtype == torch.bfloat16
+    ok = torch.empty(2, 4, 128, dtype=torch.float32)
+    assert _hip.output_for(ok, (2, 4, 128), torch.bfloat16, "cpu") is ok
+    with pytest.raises(ValueError, match="shape"):
+        _hip.output_for(torch.empty(2, 5, 128), (2, 4, 128), torch.bfloat16, "cpu")
+    with pytest.raises(ValueError, match="dtype"):
+        _hip.output_for(torch.empty(2, 4, 128, dtype=torch.int32), (2, 4, 128), torch.bfloat16, "cpu")
+    with pytest.raises(ValueError, match="contiguous"):
+        _hip.output_for(torch.empty(2, 128, 4).transpose(1, 2), (2, 4, 128), torch.bfloat16, "cpu")

@@ -440,6 +440,26 @@ def test_wide_v_bs64_ragged_full_size(cuda, quant):
     assert torch.equal(out, out2)
 
 
+def test_out_written_in_place(cuda):
+    """`out=`: the kernels write the caller's rows (here fp32 columns of a wider, strided
+    tensor) in place, bit-identical to a fresh output of the same dtype."""
+    wl = W.make_lowrank([300, 17, 900], num_heads=32, seed=43).to(cuda)
+    ref_out = paged_starkv_decode(*wl.decode_args()).float()
+    wide = torch.full((3, 40, 128), float("nan"), dtype=torch.float32, device=cuda)
+    got = paged_starkv_decode(*wl.decode_args(), out=wide[:, 4:36])
+    assert got.data_ptr() == wide[:, 4:36].data_ptr()
+    fresh = torch.empty(3, 32, 128, dtype=torch.float32, device=cuda)
+    paged_starkv_decode(*wl.decode_args(), out=fresh)
+    torch.cuda.synchronize()
+    assert torch.equal(wide[:, 4:36], fresh)
+    assert torch.isnan(wide[:, :4]).all() and torch.isnan(wide[:, 36:]).all()
+    assert torch.equal(fresh.to(torch.bfloat16).float(), ref_out)  # same values, rounded once
+    wq = W.make_quant([300, 17], num_heads=32, seed=44, device=cuda)
+    oq = torch.empty(2, 32, 128, dtype=wq.v_up_by_q.dtype, device=cuda)
+    assert paged_quant_decode(*wq.decode_args(), out=oq) is oq
+    assert torch.equal(oq, paged_quant_decode(*wq.decode_args()))
+
+
 def test_k_up_and_v_up_dtypes_independent(cuda):
     """k_up fp32 with v_up_by_q bf16 (and the reverse): each is read with its own dtype."""
     wl = W.make_lowrank([300, 17], num_heads=32, seed=41)
