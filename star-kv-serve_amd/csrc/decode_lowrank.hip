@@ -352,6 +352,16 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     const int lg = lane >> 4, lr = lane & 15;
     cint_p P = (cint_p)(p.ws + 4);
     cint_p plan = (cint_p)(p.ws + p.ws_plan);
+    // Page buffers and partial-logit rows start zeroed: rows past a request's end are
+    // never copied and must hold finite values (P is 0 there); a head's partial rows
+    // past its slots are summed as zeros. Done first: it overlaps the header loads.
+    for (int i = tid; i < p.lds_bytes / 16; i += NTHR) ((uint4*)s_pages)[i] = make_uint4(0, 0, 0, 0);
+    for (int i = tid; i < NWAVE * (MAX_SLOTS + 1) * TILE_TOK; i += NTHR) (&s_part[0][0])[i] = 0.f;
+    if (tid < NWAVE * 4) (&s_alpha[0][0])[tid] = 1.f;
+    for (int i = tid; i < NWAVE * 4 * TILE_TOK; i += NTHR) {  // P before the first page
+        (&s_p[0][0])[i] = 0;
+        if (FMT == FMT_BF16) (&s_plo[0][0])[i] = 0;
+    }
     if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
     LrLoop st;
     st.g = xcd_range(blockIdx.x, gridDim.x);
@@ -360,17 +370,6 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     st.beg = min(st.g * S_tok, T);
     st.end = min(st.beg + S_tok, T);
     if (st.beg >= st.end) return;
-
-    // Page buffers and partial-logit rows start zeroed: rows past a request's end are
-    // never copied and must hold finite values (P is 0 there); a head's partial rows
-    // past its slots are summed as zeros.
-    for (int i = tid; i < p.lds_bytes / 16; i += NTHR) ((uint4*)s_pages)[i] = make_uint4(0, 0, 0, 0);
-    for (int i = tid; i < NWAVE * (MAX_SLOTS + 1) * TILE_TOK; i += NTHR) (&s_part[0][0])[i] = 0.f;
-    if (tid < NWAVE * 4) (&s_alpha[0][0])[tid] = 1.f;
-    for (int i = tid; i < NWAVE * 4 * TILE_TOK; i += NTHR) {  // P before the first page
-        (&s_p[0][0])[i] = 0;
-        if (FMT == FMT_BF16) (&s_plo[0][0])[i] = 0;
-    }
 
     // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
     cint_p pw = plan + wave * PLAN_STRIDE;

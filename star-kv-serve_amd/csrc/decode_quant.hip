@@ -470,18 +470,9 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     const int lg = lane >> 4, lr = lane & 15;
     cint_p P = (cint_p)(p.ws + 4);
     cint_p plan = (cint_p)(p.ws + p.ws_plan);
-    if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
-    QLoop st;
-    st.g = xcd_range(blockIdx.x, gridDim.x);
-    const int S_tok = ((cint_p)p.ws)[0];
-    const int T = P[p.n];
-    st.beg = min(st.g * S_tok, T);
-    st.end = min(st.beg + S_tok, T);
-    if (st.beg >= st.end) return;
-
     // Page buffers and partial-logit rows start zeroed: rows past a request's end are
     // never copied and must hold finite values (P is 0 there); a head's partial rows
-    // past its slots are summed as zeros.
+    // past its slots are summed as zeros. Done first: it overlaps the header loads.
     for (int i = tid; i < p.lds_bytes / 16; i += NTHR) ((uint4*)s_pages)[i] = make_uint4(0, 0, 0, 0);
     for (int i = tid; i < NWAVE * Q_PART_ROWS * TILE_TOK; i += NTHR) (&s_part[0][0])[i] = 0.f;
     if (tid < NWAVE * 4) (&s_alpha[0][0])[tid] = 1.f;
@@ -492,6 +483,14 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
         const uint32_t mb = (2 * g + 1 < c ? 0x0000ffffu : 0u) | (2 * g + 9 < c ? 0xffff0000u : 0u);
         s_omask[c][g] = make_uint2(ma, mb);
     }
+    if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
+    QLoop st;
+    st.g = xcd_range(blockIdx.x, gridDim.x);
+    const int S_tok = ((cint_p)p.ws)[0];
+    const int T = P[p.n];
+    st.beg = min(st.g * S_tok, T);
+    st.end = min(st.beg + S_tok, T);
+    if (st.beg >= st.end) return;
 
     // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
     cint_p pw = plan + wave * PLAN_STRIDE;

@@ -167,6 +167,9 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
     const PvParams& p = pv_params();
     const int tid = threadIdx.x, lane = tid & 63, wave = rfl(tid >> 6);
     cint_p P = (cint_p)(p.ws + 4);
+    // Buffers start zeroed: rows past a request's end are never copied and must be finite.
+    // Done first: it overlaps the header loads.
+    for (int i = tid; i < p.lds_bytes / 16; i += NTHR) ((uint4*)s_pv)[i] = make_uint4(0, 0, 0, 0);
     if (((cint_p)(p.ws + p.ws_plan))[NWAVE * PLAN_STRIDE] == 0) return;  // no plan: the merge reports NaN
     const int g = xcd_range(blockIdx.x, gridDim.x);
     const int S_tok = ((cint_p)p.ws)[0];
@@ -181,8 +184,6 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
 
     const uint32_t base = lds_addr(s_pv);
     const uint32_t dummy = base + (uint32_t)(p.lds_bytes - 1024);
-    // Buffers start zeroed: rows past a request's end are never copied and must be finite.
-    for (int i = tid; i < p.lds_bytes / 16; i += NTHR) ((uint4*)s_pv)[i] = make_uint4(0, 0, 0, 0);
 
     // Copy offsets of this lane inside a page, per copy i (chunk 8 i + wave).
     uint32_t off[NLD];
