@@ -127,9 +127,11 @@ int starkv_fold_q(void *stream, const void *q, int64_t q_s0, int64_t q_s1, int q
 int starkv_decode_grid(int n, int max_seq_len);
 
 /*
- * The grid for one layer's calls: starkv_decode_grid's rule with 256 tokens per
- * workgroup when the layer decodes in two passes (V ranks too wide for one pass; see
- * starkv_decode_two_pass), 64 otherwise. A pure function of its arguments and the device.
+ * The grid for one layer's calls: starkv_decode_grid's rule with 64 tokens per
+ * workgroup. For a layer that decodes in two passes (V ranks too wide for one pass; see
+ * starkv_decode_two_pass) this is the logits pass's grid; the P @ V pass takes ranges of
+ * R of its ranges (R from the cache kind, n, max_seq_len and the grid, 1 to 4). A pure
+ * function of its arguments and the device.
  * This build's Python wrappers take their grid from it (no counterpart in the
  * reference, whose Triton launches size their own grids, paged_decode.py:192-219).
  */

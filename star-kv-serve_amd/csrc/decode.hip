@@ -160,7 +160,8 @@ __device__ __forceinline__ int wave_min_i(int v) {
     return min(min(r0, r1), min(r2, r3));
 }
 
-// Workgroup 0 of prep. Writes hdr[0] = tokens per decode workgroup, hdr[1 + b] = first
+// Workgroup 0 of prep. Writes hdr[0] = tokens per decode workgroup (a multiple of 16;
+// the last workgroups may have none), hdr[1 + b] = first
 // token of request b in the concatenation (v: this thread's requests 4 tid .. 4 tid + 3).
 __device__ void prep_prefix(const PrepArgs& a, int tid, int (&v)[4]) {
     __shared__ int s_wsum[PREP_THR / 64];
@@ -189,7 +190,9 @@ __device__ void prep_prefix(const PrepArgs& a, int tid, int (&v)[4]) {
         run += v[i];
         if (4 * tid + i < a.n) hdr[2 + 4 * tid + i] = run;
     }
-    if (tid == PREP_THR - 1) hdr[0] = (run + a.grid - 1) / a.grid;
+    // Tokens per decode workgroup: a multiple of 16, so that a single request's ranges
+    // start on its pages (no page is copied by two workgroups).
+    if (tid == PREP_THR - 1) hdr[0] = ((run + a.grid - 1) / a.grid + TILE_TOK - 1) / TILE_TOK * TILE_TOK;
     if (tid == 0) hdr[1] = 0;
 }
 
@@ -628,12 +631,9 @@ int device_cus() {
 }
 
 // tok_per_wg: tokens per workgroup the split aims for (at most the device's CUs
-// workgroups). 128 (8 pages) for two-pass calls, whose fp32 partial accumulators of
-// H x v_rank per workgroup and request cost about as much traffic as the V codes they
-// sum when a workgroup has few pages (one request of 16384 tokens at V rank 1280: 77 us a
-// call at 256 tokens per workgroup, 67 at 128, 71 at 64); 64 for one-pass calls, whose
+// workgroups). 64 for the one-pass kernels and the logits pass of two-pass calls, whose
 // partials are small, so that a short batch (one request of 4096 tokens) still spreads
-// over many CUs.
+// over many CUs; PV_TOK for the P @ V pass of two-pass calls (pv_ratio).
 static int grid_for(int n, int max_seq_len, int tok_per_wg = 256) {
     const int64_t tokens = (int64_t)n * (int64_t)(max_seq_len > 0 ? max_seq_len : 1);
     int64_t want = (tokens + tok_per_wg - 1) / tok_per_wg;
@@ -644,6 +644,23 @@ static int grid_for(int n, int max_seq_len, int tok_per_wg = 256) {
     const int cus = device_cus();
     if (want > cus) want = cus;
     return want < 1 ? 1 : (int)want;
+}
+
+// Two-pass calls: the P @ V pass runs over ranges of R consecutive logits-pass ranges. Its
+// fp32 partial accumulators of H x v_rank per workgroup and request cost about as much
+// traffic as the V codes they sum when a workgroup has few pages, while the logits pass's
+// partials are two floats per head: with few requests the logits pass takes every CU and
+// the bf16/fp16 P @ V pass fewer, longer ranges in two column windows side by side. R = the
+// logits grid over the grid at PV_TOK tokens per workgroup, rounded (1 to 4); 1 for
+// 3.2-bit codes, whose P @ V pass copies every V byte in one window and so keeps more
+// workgroups busy with R = 1. One request of 16419 tokens at V rank 1280 / 1290 (config 4
+// at concurrency 1): bf16 P @ V + merge 36.7 us at R = 2, 37.6 at R = 1; 3.2-bit 39.3 at
+// R = 1, 42.6 at R = 2.
+constexpr int PV_TOK = 128;
+static int pv_ratio(int fmt, int n, int max_seq_len, int grid) {
+    if (fmt == FMT_Q4) return 1;
+    const int gp = grid_for(n, max_seq_len, PV_TOK);
+    return std::max(1, std::min(4, (grid + gp / 2) / gp));
 }
 
 // Optional timing for benchmarks: when armed, each call records a HIP event pair on the
@@ -791,7 +808,8 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
               MAX_TT, MAX_TT * 16);
     const bool two = use_two_pass(fmt, p.k_width, a.v_rank, row_bytes, p.v_nout);
     const int lcap = two ? lcap_of(a.max_seq_len) : 0;
-    const WsLayout wl = ws_layout(a.n, a.Hq, TT, a.v_rank, a.grid, lcap);
+    const int pv_r = two ? pv_ratio(fmt, a.n, a.max_seq_len, a.grid) : 1;
+    const WsLayout wl = ws_layout(a.n, a.Hq, TT, a.v_rank, a.grid, lcap, pv_r);
     SKV_CHECK(a.ws_bytes >= wl.total, "decode: workspace %zu bytes < %zu needed", a.ws_bytes, wl.total);
     SKV_CHECK(((uintptr_t)a.ws % 256) == 0, "decode: workspace must be 256-byte aligned");
     SKV_CHECK(p.bs_shift >= 0, "decode: block_size must be 16 times a power of two");
@@ -864,6 +882,7 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     p.ws_m = wl.m; p.ws_l = wl.l; p.ws_acc = wl.acc;
     p.ws_lg = wl.lg; p.lcap = lcap;
     p.ws_o = wl.o; p.acc_ld = wl.ld;
+    p.pv_r = pv_r;
 
     const bool timed = g_prof.on && 2 * g_prof.used + 1 < (int)g_prof.ev.size();
     if (timed && g_prof.mode == 1) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
@@ -942,14 +961,8 @@ int starkv_decode_grid(int n, int max_seq_len) { return grid_for(n, max_seq_len)
 int starkv_decode_grid_for(int cache_kind, int n, int num_heads, int num_kv_heads, int k_width, int v_rank,
                            int max_seq_len) {
     if (n < 1 || num_heads < 1 || num_kv_heads < 1 || k_width < 16 || v_rank < 1) return grid_for(n, max_seq_len);
-    bool two;
-    if (cache_kind == STARKV_CACHE_Q3_2) {
-        const QRow r = qrow(k_width, num_heads, v_rank);
-        two = use_two_pass(FMT_Q4, k_width, v_rank, r.nbytes, r.v_nout);
-    } else {
-        two = use_two_pass(cache_kind == STARKV_F16 ? FMT_F16 : FMT_BF16, k_width, v_rank, (k_width + v_rank) * 2, 0);
-    }
-    return grid_for(n, max_seq_len, two ? 128 : 64);
+    (void)cache_kind;  // the one-pass kernels and the logits pass of two-pass calls split alike
+    return grid_for(n, max_seq_len, 64);
 }
 
 int starkv_profile_begin(int max_calls, int mode) {
@@ -1010,7 +1023,9 @@ size_t starkv_decode_workspace_bytes(int cache_kind, int n, int num_heads, int n
         TT = (num_heads / num_kv_heads) * (k_width / 16);
     }
     const bool two = use_two_pass(fmt, k_width, v_rank, row_bytes, v_nout);
-    return ws_layout(n, num_heads, TT, v_rank, grid, two ? lcap_of(max_seq_len) : 0).total;
+    return ws_layout(n, num_heads, TT, v_rank, grid, two ? lcap_of(max_seq_len) : 0,
+                     two ? pv_ratio(fmt, n, max_seq_len, grid) : 1)
+        .total;
 }
 
 int starkv_decode_layer_fits(int cache_kind, int num_heads, int num_kv_heads, const int32_t* k_ranks, int v_rank) {

@@ -6,6 +6,8 @@
 
 #include <stdio.h>
 
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace starkv {
@@ -49,7 +51,11 @@ constexpr float LAZY_MAX = 8.f;             // log2 headroom before the running 
 //                               every head are one 2 KB block), lcap = max_seq_len
 //                               rounded up to 16
 //   o      fp32  [n][Hq][ld]    (two-pass calls only) merged low-rank outputs
-// Two-pass calls pad acc and o rows to ld = v_rank rounded up to 4 (16-byte rows).
+// Two-pass calls pad acc and o rows to ld = v_rank rounded up to 4 (16-byte rows). Their
+// P @ V pass runs over ranges of R consecutive logits-pass ranges (R >= 1, for few
+// requests: the logits pass then spreads over more workgroups than the P @ V pass, whose
+// partials are wide): pv slots = ceil(grid / R) + n, the acc rows are per pv slot, and m
+// and l hold R ceil(grid / R) + n slots (the ranges past grid are never written).
 // Slot word: everything a decode kernel needs of one of its slots, so that its prologue
 // reads a wave's slots with a few wide scalar loads: the code tile (first cache lane /
 // 16), the tile's outlier ranks (3.2-bit), the slot's partial-logit row, its local head
@@ -74,10 +80,12 @@ struct WsLayout {
 
 static inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// lcap = 0: the one-pass decode (no logits buffer).
-static WsLayout ws_layout(int n, int Hq, int TT, int v_rank, int grid, int lcap) {
+// lcap = 0: the one-pass decode (no logits buffer). pv_r: the P @ V pass's R.
+static WsLayout ws_layout(int n, int Hq, int TT, int v_rank, int grid, int lcap, int pv_r = 1) {
     WsLayout w;
-    const size_t slots = (size_t)grid + n;
+    const size_t gp = lcap > 0 ? ((size_t)grid + pv_r - 1) / pv_r : (size_t)grid;
+    const size_t slots = (lcap > 0 ? std::max((size_t)grid, gp * pv_r) : (size_t)grid) + n;
+    const size_t pslots = gp + n;
     size_t o = 0;
     w.hdr = o; o = al256(o + (size_t)(n + 2) * 4);
     w.plan = o; o = al256(o + (size_t)(NWAVE * PLAN_STRIDE + 1) * 4);
@@ -85,7 +93,7 @@ static WsLayout ws_layout(int n, int Hq, int TT, int v_rank, int grid, int lcap)
     w.m = o; o = al256(o + slots * Hq * 4);
     w.l = o; o = al256(o + slots * Hq * 4);
     w.ld = lcap > 0 ? (v_rank + 3) & ~3 : v_rank;
-    w.acc = o; o = al256(o + slots * Hq * (size_t)w.ld * 4);
+    w.acc = o; o = al256(o + pslots * Hq * (size_t)w.ld * 4);
     w.lg = o; o = al256(o + (size_t)n * Hq * (size_t)lcap * 4);
     w.o = o; o = al256(o + (lcap > 0 ? (size_t)n * Hq * (size_t)w.ld * 4 : 0));
     w.total = o;
@@ -106,6 +114,7 @@ struct DecodeParams {
     size_t ws_plan, ws_ab, ws_m, ws_l, ws_acc;
     size_t ws_lg; int lcap;                        // two-pass calls: logits buffer, row length
     size_t ws_o; int acc_ld;                       // two-pass calls: merged outputs; acc / o row floats
+    int pv_r;                                      // two-pass calls: logits-pass ranges per P @ V range
 };
 
 __device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }

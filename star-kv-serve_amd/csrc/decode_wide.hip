@@ -8,15 +8,17 @@
 // column blocks of at most 512 (paged_decode.py:105-147, 199-219) or 128 channels
 // inside one outlier/inlier block (paged_quant.py:311-354, 390-407).
 //
-// pv_kernel. The same persistent workgroups and token ranges as the logits pass, so
-// that partial slot (request b, workgroup g) = b + g matches the (m, l) the logits pass
-// stored for it. Per page of 16 tokens the workgroup copies into LDS, with buffer loads
-// that write LDS directly (16 bytes per lane):
+// pv_kernel. Persistent workgroups whose token range g is R consecutive ranges of the
+// logits pass (R = 1 unless few requests; MULTI: R > 1), partial slot (request b, range
+// g) = b + g. Its reference max for request b is the largest of the logits pass's maxima
+// in slots b + R g + j that hold tokens of b (merge_cols forms the same max). Per page of
+// 16 tokens the workgroup copies into LDS, with buffer loads that write LDS directly (16
+// bytes per lane):
 //   - the V bytes of the 16 rows: bf16/fp16, the columns of the workgroup's window
 //     (grid.y: windows run side by side); 3.2-bit, every V byte (scales, outlier and
 //     inlier nibbles);
-//   - the 16 logits of every head (2 KB) and the slot's reference max per head.
-// Since the reference max of a slot is final, P = exp2(logit - m) needs no rescaling.
+//   - the 16 logits of every head (2 KB) and the R slots' maxima per head.
+// Since the reference max is final, P = exp2(logit - m) needs no rescaling.
 // P @ V runs on v_mfma_f32_32x32x16 (M = 32 heads, N = 32 columns, K = the page's 16
 // tokens) with A = P:
 //   - bf16 codes: P = hi + lo (two bf16 parts, two MFMAs); B = 16 tokens x 32 columns
@@ -95,6 +97,7 @@ struct PvParams {
     int buf_bytes;   // LDS bytes per page buffer (nch KB)
     int lds_bytes;
     uint8_t* ws; size_t ws_plan, ws_m, ws_acc, ws_lg; int lcap, acc_ld;
+    int r;           // this pass's range = R consecutive logits-pass ranges
 };
 
 typedef const __attribute__((address_space(4))) PvParams kpv_t;
@@ -105,7 +108,7 @@ __device__ __forceinline__ const PvParams& pv_params() {
 }
 
 // Copy descriptors of one page: its rows, its logits rows (request b, tokens 16 k ..,
-// every head), the slot's reference maxima.
+// every head), the reference maxima of the R logits-pass slots b + R g + j.
 struct PvPage {
     int4v_t rv, rl, rm;
 };
@@ -120,13 +123,14 @@ __device__ __forceinline__ PvPage pv_page_desc(const PvParams& p, const Cursor& 
     d.rv = buffer_rsrc(page, rows * p.c_s1);
     const uint8_t* lg = p.ws + p.ws_lg + (((int64_t)(v ? c.b : 0) * (p.lcap / TILE_TOK) + k) * p.Hq * TILE_TOK) * 4;
     d.rl = buffer_rsrc(lg, v ? p.Hq * TILE_TOK * 4 : 0);
-    const uint8_t* m = p.ws + p.ws_m + (int64_t)(v ? c.b + g : 0) * p.Hq * 4;
-    d.rm = buffer_rsrc(m, v ? ((p.Hq * 4 + 15) & ~15) : 0);
+    const uint8_t* m = p.ws + p.ws_m + (int64_t)(v ? c.b + p.r * g : 0) * p.Hq * 4;
+    d.rm = buffer_rsrc(m, v ? ((p.r * p.Hq * 4 + 15) & ~15) : 0);
     return d;
 }
 
-// LDS chunks of a page buffer: 0 and 1 the logits of heads 0-15 and 16-31, 2 the slot's
-// maxima, then the V granule columns.
+// LDS chunks of a page buffer: 0 and 1 the logits of heads 0-15 and 16-31, 2 the R
+// logits-pass slots' maxima (slot j head h at byte 4 (j Hq + h)), then the V granule
+// columns.
 constexpr int PV_V0 = 3;
 
 // The copies of this wave for one page into the buffer at LDS byte `buf`: copy i moves
@@ -161,7 +165,7 @@ __device__ __forceinline__ half2_t nib2(uint32_t w, uint32_t sel) {
     return as_h2(__builtin_amdgcn_perm(0x64646464u, w, sel)) - (half2_t){(_Float16)1032.f, (_Float16)1032.f};
 }
 
-template <int FMT, int MB, int NLD>
+template <int FMT, int MB, int NLD, bool MULTI>
 __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
     extern __shared__ __attribute__((aligned(16))) uint8_t s_pv[];
     const PvParams& p = pv_params();
@@ -172,9 +176,9 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
     for (int i = tid; i < p.lds_bytes / 16; i += NTHR) ((uint4*)s_pv)[i] = make_uint4(0, 0, 0, 0);
     if (((cint_p)(p.ws + p.ws_plan))[NWAVE * PLAN_STRIDE] == 0) return;  // no plan: the merge reports NaN
     const int g = xcd_range(blockIdx.x, gridDim.x);
-    const int S_tok = ((cint_p)p.ws)[0];
+    const int S_tok = ((cint_p)p.ws)[0];  // tokens per logits-pass range
     const int T = P[p.n];
-    const int beg = min(g * S_tok, T), end = min(beg + S_tok, T);
+    const int beg = min(g * p.r * S_tok, T), end = min(beg + p.r * S_tok, T);
     if (beg >= end) return;
     // This workgroup's column window.
     const int u0 = (int)blockIdx.y * p.per;
@@ -195,7 +199,7 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
             const int h = 16 * ch + (lane >> 2);
             if (h < p.Hq) o = (uint32_t)(h * 64 + 16 * (lane & 3));
         } else if (ch == 2) {
-            if (4 * lane < p.Hq) o = (uint32_t)(16 * lane);
+            if (4 * lane < p.r * p.Hq) o = (uint32_t)(16 * lane);
         } else if (ch < p.nch) {
             const int G = 4 * (ch - PV_V0) + (lane >> 4), t = gslot(G, lane & 15);
             if (G < p.ng) o = (uint32_t)(t * p.c_s1 + v_off + 16 * G);
@@ -224,7 +228,7 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
         }
     }
     const uint32_t lga = (uint32_t)((am * 16 + 8 * ag) * 4);  // logits of (am, 8 ag ..)
-    const uint32_t mxa = (uint32_t)(2 * 1024 + am * 4);         // the slot max of head am
+    const uint32_t mxa = (uint32_t)(2 * 1024 + am * 4);         // slot 0's max of head am
     __syncthreads();
 
     f32x16_t acc[MB];
@@ -246,6 +250,21 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
     // load completes under the page barrier's wait.
     int nblk = blk_of(ld);
     int jb = 0;  // buffer of the current page
+    // The logits-pass ranges R g + j holding tokens of the request of page c: bit j. This
+    // pass's reference max of the request is the largest of theirs (slots of other
+    // ranges hold other requests' values, or none).
+    auto sub_mask = [&](const Cursor& c) -> int {
+        if (!MULTI || !c.valid) return 1;  // R = 1: the one range is this workgroup's
+        const int pb = P[c.b];
+        const int lo = pb + c.lo, hi = pb + c.hi;
+        int msk = 0;
+        for (int j = 0; j < p.r; ++j) {
+            const int r0 = (p.r * g + j) * S_tok;
+            if (max(r0, lo) < min(r0 + S_tok, hi)) msk |= 1 << j;
+        }
+        return msk;
+    };
+    int msk = sub_mask(cc);  // of the current request, redone when the request changes
     while (cc.valid) {
         // Page cc is in buffer jb; the copies of the nbuf - 2 pages after it may still run.
         wait_vmcnt_lgkm0_wide((p.nbuf - 2) * p.nld);
@@ -260,7 +279,19 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
         const uint32_t vbuf = buf + PV_V0 * 1024;  // the page's V granule columns
         // A operand: P of head am at tokens 8 ag .. 8 ag + 7 of this page.
         const f32x4_t s0 = lds_ld<f32x4_t>(buf + lga), s1 = lds_ld<f32x4_t>(buf + lga + 16);
-        const float mx = lds_ld<float>(buf + mxa);
+        // R = 1: the slot's max. Else the largest of the R slots' maxima (all four read:
+        // the slots past R are in the chunk too), those of other requests' ranges left out.
+        float mx;
+        if constexpr (MULTI) {
+            mx = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float mj = lds_ld<float>(buf + mxa + (uint32_t)(4 * j * p.Hq));
+                mx = (msk >> j) & 1 ? fmaxf(mx, mj) : mx;
+            }
+        } else {
+            mx = lds_ld<float>(buf + mxa);
+        }
         const float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
         const int tok0 = TILE_TOK * cc.k + 8 * ag;
         float pe[8];
@@ -375,6 +406,7 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
             }
         }
         cc = nx;
+        if (MULTI && seg_end) msk = sub_mask(cc);
         jb = jb + 1 == p.nbuf ? 0 : jb + 1;
     }
     wait_vmcnt_lgkm0(0);  // no copy may land after the workgroup ends
@@ -387,9 +419,9 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
 //   column's weighted sum of their accumulators, U partials' loads in flight, divided by the
 //   total, into o [n][Hq][ld] (NaN for a request with no tokens, as the reference's softmax
 //   over an empty row). MCW = 1: the four waves take different columns (1024 per
-//   workgroup), each over every slot; MCW = 4, for requests split over many workgroups (a
-//   few long requests): wave w sums slots w, w + 4, ... of 256 columns, then the four
-//   waves' sums are added.
+//   workgroup), each over every slot; MCW = 8 (eight waves), for requests split over many
+//   workgroups (a few long requests): wave w sums slots w, w + 8, ... of 256 columns, then
+//   the waves' sums are added.
 // lift_kernel<DT, REQ, THR, DQ>: one workgroup per (head, REQ requests, 8 DQ output
 //   columns): out = o @ v_up_by_q[h], each thread 8 output columns over a THR / DQ-th of the
 //   rank columns, LIFT_U rows in flight, then a reduction over those parts. 8 requests x
@@ -401,11 +433,11 @@ constexpr int MC_THR = 256;
 constexpr int MC_WREG = 4;  // slot weights held in registers: 64 MC_WREG slots
 constexpr int LIFT_U = 8;   // v_up_by_q rows per thread in flight
 
-template <int MCW, int U>
-__global__ __launch_bounds__(MC_THR) void merge_cols_kernel(const uint8_t* __restrict__ ws, size_t ws_plan, size_t ws_m,
+template <int MCW, int U, int THR>
+__global__ __launch_bounds__(THR) void merge_cols_kernel(const uint8_t* __restrict__ ws, size_t ws_plan, size_t ws_m,
                                                             size_t ws_l, size_t ws_acc, size_t ws_o, int n, int Hq,
-                                                            int v_rank, int ld) {
-    constexpr int CPW = 4 * MC_THR / MCW;  // columns per workgroup
+                                                            int v_rank, int ld, int pv_r) {
+    constexpr int CPW = 4 * THR / MCW;  // columns per workgroup
     __shared__ f32x4_t s_sum[MCW][64];
     const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int w = MCW > 1 ? __builtin_amdgcn_readfirstlane(tid >> 6) : 0;  // slot phase
@@ -413,43 +445,80 @@ __global__ __launch_bounds__(MC_THR) void merge_cols_kernel(const uint8_t* __res
     const float* wm = (const float*)(ws + ws_m);
     const float* wl = (const float*)(ws + ws_l);
     const float* wa = (const float*)(ws + ws_acc);
-    const int S = hdr[0];
+    const int SL = hdr[0];        // tokens per logits-pass range
+    const int S = SL * pv_r;      // tokens per P @ V range
     const bool planned = ((const int*)(ws + ws_plan))[NWAVE * PLAN_STRIDE] != 0;
     const int pb = hdr[1 + b], pe = hdr[2 + b];
     const bool live = pe > pb && S > 0 && planned;
+    // The request's logits-pass slots b + r_lo + i (i < nr) and P @ V slots b + k_lo + k (k < nk).
+    const int r_lo = live ? pb / SL : 0, nr = live ? (pe - 1) / SL - r_lo + 1 : 0;
     const int k_lo = live ? pb / S : 0, nk = live ? (pe - 1) / S - k_lo + 1 : 0;
-    const int64_t s0 = (int64_t)(k_lo + b) * Hq + h;  // slot row of partial k: s0 + k Hq
-    // Every wave forms the same weights (the loads hit the same lines). Slot k < 64 MC_WREG:
-    // its max in lane k % 64 of mk[k / 64], its weight in wk[k / 64].
-    float mk[MC_WREG], lk[MC_WREG];
+    const int64_t s0 = (int64_t)(k_lo + b) * Hq + h;  // P @ V slot row of partial k: s0 + k Hq
+    const int64_t r0 = (int64_t)(r_lo + b) * Hq + h;  // logits-pass slot row i: r0 + i Hq
+    // Every wave forms the same weights (the loads hit the same lines): the request's max M
+    // and sum l over its logits-pass slots; P @ V partial k weighs 2^(M_k - M), M_k its
+    // reference max: the largest of the logits-pass maxima of its range's R slots that
+    // hold tokens of the request (as the P @ V pass formed it). The first 64 MC_WREG
+    // logits-pass slots' maxima are held in registers (slot i in lane i % 64 of mr[i / 64]),
+    // and so are the weights of the first 64 MC_WREG partials (wk).
+    float mr[MC_WREG], lr[MC_WREG];
 #pragma unroll
     for (int j = 0; j < MC_WREG; ++j) {
-        const int k = lane + 64 * j;
-        mk[j] = k < nk ? wm[s0 + (int64_t)k * Hq] : -INFINITY;
-        lk[j] = k < nk ? wl[s0 + (int64_t)k * Hq] : 0.f;
+        const int i = lane + 64 * j;
+        mr[j] = i < nr ? wm[r0 + (int64_t)i * Hq] : -INFINITY;
+        lr[j] = i < nr ? wl[r0 + (int64_t)i * Hq] : 0.f;
     }
-    float M = mk[0];
+    float M = mr[0];
 #pragma unroll
-    for (int j = 1; j < MC_WREG; ++j) M = fmaxf(M, mk[j]);
-    for (int k = lane + 64 * MC_WREG; k < nk; k += 64) M = fmaxf(M, wm[s0 + (int64_t)k * Hq]);
+    for (int j = 1; j < MC_WREG; ++j) M = fmaxf(M, mr[j]);
+    for (int i = lane + 64 * MC_WREG; i < nr; i += 64) M = fmaxf(M, wm[r0 + (int64_t)i * Hq]);
     M = wave_max(M);
-    float wk[MC_WREG], l = 0.f;
+    float l = 0.f;
 #pragma unroll
-    for (int j = 0; j < MC_WREG; ++j) {
-        wk[j] = lane + 64 * j < nk ? exp2f(mk[j] - M) : 0.f;
-        l = fmaf(lk[j], wk[j], l);
-    }
-    for (int k = lane + 64 * MC_WREG; k < nk; k += 64) {
-        const int64_t sl = s0 + (int64_t)k * Hq;
+    for (int j = 0; j < MC_WREG; ++j) l = fmaf(lr[j], lane + 64 * j < nr ? exp2f(mr[j] - M) : 0.f, l);
+    for (int i = lane + 64 * MC_WREG; i < nr; i += 64) {
+        const int64_t sl = r0 + (int64_t)i * Hq;
         l += wl[sl] * exp2f(wm[sl] - M);
     }
     l = wave_sum(l);
+    // M_k from memory (partials past 64 MC_WREG, under divergent lanes).
+    auto slot_max = [&](int k) -> float {
+        float x = -INFINITY;
+        for (int t = 0; t < pv_r; ++t) {
+            const int i = pv_r * (k_lo + k) + t - r_lo;
+            if (i >= 0 && i < nr) x = fmaxf(x, wm[r0 + (int64_t)i * Hq]);
+        }
+        return x;
+    };
+    float wk[MC_WREG];
+    if (pv_r == 1) {  // partial k is logits-pass slot k
+#pragma unroll
+        for (int j = 0; j < MC_WREG; ++j) wk[j] = lane + 64 * j < nk ? exp2f(mr[j] - M) : 0.f;
+    } else {  // every lane active: the maxima are read across lanes
+#pragma unroll
+        for (int j = 0; j < MC_WREG; ++j) {
+            const int k = lane + 64 * j;
+            float x = -INFINITY;
+            for (int t = 0; t < pv_r; ++t) {
+                const int i = pv_r * (k_lo + k) + t - r_lo;
+                float v = -INFINITY;
+#pragma unroll
+                for (int jj = 0; jj < MC_WREG; ++jj) {
+                    const float y = __shfl(mr[jj], i & 63, 64);
+                    v = (i >> 6) == jj ? y : v;
+                }
+                if (i >= 64 * MC_WREG) v = i < nr ? wm[r0 + (int64_t)i * Hq] : -INFINITY;
+                x = i >= 0 && i < nr ? fmaxf(x, v) : x;
+            }
+            wk[j] = k < nk ? exp2f(x - M) : 0.f;
+        }
+    }
     const float inv = live ? 1.f / l : __builtin_nanf("");
     float* o = (float*)(ws + ws_o) + ((int64_t)b * Hq + h) * ld;
     const int c4 = blockIdx.z * CPW + 4 * (MCW > 1 ? lane : tid);
     // Weight of slot k (wave-uniform k). The lane reads come from wk as formed above, with
     // every lane active (inside the column branch below some lanes are not).
-    auto weight = [&](int k, int64_t sl) -> float {
+    auto weight = [&](int k) -> float {
         if (k < 64 * MC_WREG) {
             float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk[0]), k & 63));
 #pragma unroll
@@ -457,7 +526,7 @@ __global__ __launch_bounds__(MC_THR) void merge_cols_kernel(const uint8_t* __res
                 if (k >= 64 * j) x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk[j]), k & 63));
             return x;
         }
-        return exp2f(wm[sl] - M);
+        return exp2f(slot_max(k) - M);
     };
     f32x4_t a = {0.f, 0.f, 0.f, 0.f};
     if (c4 < v_rank) {
@@ -469,12 +538,12 @@ __global__ __launch_bounds__(MC_THR) void merge_cols_kernel(const uint8_t* __res
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int ku = k + u * MCW;
-                a += r[u] * weight(ku, s0 + (int64_t)ku * Hq);
+                a += r[u] * weight(ku);
             }
         }
         for (; k < nk; k += MCW) {
             const int64_t sl = s0 + (int64_t)k * Hq;
-            a += *(const f32x4_t*)(wa + sl * ld + c4) * weight(k, sl);
+            a += *(const f32x4_t*)(wa + sl * ld + c4) * weight(k);
         }
     }
     if constexpr (MCW == 1) {
@@ -591,12 +660,17 @@ constexpr int PV_NLD = 12;  // copies per wave per page, at most (the plan keeps
 // (115 KB) took 346 us.
 constexpr int PV_INFLIGHT = 64 * 1024;
 
-template <int FMT>
+template <int FMT, bool MULTI>
 const void* pv_pick(int mb) {
-    if (mb <= 2) return (const void*)&pv_kernel<FMT, 2, PV_NLD>;
-    if (mb <= 4) return (const void*)&pv_kernel<FMT, 4, PV_NLD>;
-    if (mb <= 6) return (const void*)&pv_kernel<FMT, 6, PV_NLD>;
-    return (const void*)&pv_kernel<FMT, 8, PV_NLD>;
+    if (mb <= 2) return (const void*)&pv_kernel<FMT, 2, PV_NLD, MULTI>;
+    if (mb <= 4) return (const void*)&pv_kernel<FMT, 4, PV_NLD, MULTI>;
+    if (mb <= 6) return (const void*)&pv_kernel<FMT, 6, PV_NLD, MULTI>;
+    return (const void*)&pv_kernel<FMT, 8, PV_NLD, MULTI>;
+}
+
+template <int FMT>
+const void* pv_pick_r(int mb, int r) {
+    return r > 1 ? pv_pick<FMT, true>(mb) : pv_pick<FMT, false>(mb);
 }
 
 int raise_lds(const void* fn, int bytes) {
@@ -676,7 +750,8 @@ int launch_pv(const DecodeParams& p, int fmt, int grid, hipStream_t stream) {
     const int v_bytes = p.v_nbo + (p.v_rank - p.v_nout + 1) / 2;
     // A grid short of the CUs (few requests) takes more, narrower windows side by side.
     const int cus = device_cus();
-    PvPlan pl = pv_plan(fmt, p.v_col, p.v_rank, p.vs_off, p.vq_off, v_bytes, (cus + grid - 1) / grid);
+    const int gp = (grid + p.pv_r - 1) / p.pv_r;  // this pass's ranges
+    PvPlan pl = pv_plan(fmt, p.v_col, p.v_rank, p.vs_off, p.vq_off, v_bytes, (cus + gp - 1) / gp);
     if (!pl.ok) pl = pv_plan(fmt, p.v_col, p.v_rank, p.vs_off, p.vq_off, v_bytes);
     SKV_CHECK(pl.ok, "decode: no P @ V window fits in LDS (v_rank %d)", p.v_rank);
     PvParams a;
@@ -692,19 +767,20 @@ int launch_pv(const DecodeParams& p, int fmt, int grid, hipStream_t stream) {
     a.lds_bytes = pl.lds;
     a.ws = p.ws; a.ws_plan = p.ws_plan; a.ws_m = p.ws_m; a.ws_acc = p.ws_acc; a.ws_lg = p.ws_lg; a.lcap = p.lcap;
     a.acc_ld = p.acc_ld;
+    a.r = p.pv_r;
     // The windows run side by side in one launch (grid.y): each re-reads the page logits.
     a.per = pl.per;
     a.units = pl.units;
     a.v_off = pl.v_off;
     const int windows = (pl.units + pl.per - 1) / pl.per;
     const int mb = fmt == FMT_Q4 ? 2 * ((pl.per + NWAVE - 1) / NWAVE) : (pl.per + NWAVE - 1) / NWAVE;
-    const void* fn = fmt == FMT_BF16 ? pv_pick<FMT_BF16>(mb)
-                     : fmt == FMT_F16 ? pv_pick<FMT_F16>(mb)
-                                      : pv_pick<FMT_Q4>(mb);
+    const void* fn = fmt == FMT_BF16 ? pv_pick_r<FMT_BF16>(mb, p.pv_r)
+                     : fmt == FMT_F16 ? pv_pick_r<FMT_F16>(mb, p.pv_r)
+                                      : pv_pick_r<FMT_Q4>(mb, p.pv_r);
     int rc = raise_lds(fn, PV_MAX_DYN_LDS);
     if (rc) return rc;
     void* args[] = {(void*)&a};
-    SKV_HIP(hipLaunchKernel(fn, dim3(grid, windows), dim3(NTHR), args, (size_t)a.lds_bytes, stream));
+    SKV_HIP(hipLaunchKernel(fn, dim3(gp, windows), dim3(NTHR), args, (size_t)a.lds_bytes, stream));
     return STARKV_OK;
 }
 
@@ -718,15 +794,16 @@ int launch_merge_wide(const DecodeParams& p, int grid, int w_dt, const void* vup
                       void* out, int64_t o_s0, int64_t o_s1, int out_dt, hipStream_t stream) {
     const size_t lds = lift_lds(p.acc_ld);
     SKV_CHECK(lds <= (size_t)PV_MAX_DYN_LDS, "decode: v_rank %d too large for the merge", p.v_rank);
-    // Slots per request: about grid / n + 1. Many (a few long requests): split them over waves.
-    if (grid >= 8 * p.n)
-        hipLaunchKernelGGL((merge_cols_kernel<4, 16>), dim3(p.n, p.Hq, (p.v_rank + 255) / 256), dim3(MC_THR), 0,
+    // Slots per request: about gp / n + 1. Many (a few long requests): split them over waves.
+    const int gp = (grid + p.pv_r - 1) / p.pv_r;
+    if (gp >= 8 * p.n)
+        hipLaunchKernelGGL((merge_cols_kernel<8, 16, 512>), dim3(p.n, p.Hq, (p.v_rank + 255) / 256), dim3(512), 0,
                            stream, (const uint8_t*)p.ws, p.ws_plan, p.ws_m, p.ws_l, p.ws_acc, p.ws_o, p.n, p.Hq,
-                           p.v_rank, p.acc_ld);
+                           p.v_rank, p.acc_ld, p.pv_r);
     else
-        hipLaunchKernelGGL((merge_cols_kernel<1, 8>), dim3(p.n, p.Hq, (p.v_rank + 1023) / 1024), dim3(MC_THR), 0,
+        hipLaunchKernelGGL((merge_cols_kernel<1, 8, MC_THR>), dim3(p.n, p.Hq, (p.v_rank + 1023) / 1024), dim3(MC_THR), 0,
                            stream, (const uint8_t*)p.ws, p.ws_plan, p.ws_m, p.ws_l, p.ws_acc, p.ws_o, p.n, p.Hq,
-                           p.v_rank, p.acc_ld);
+                           p.v_rank, p.acc_ld, p.pv_r);
     SKV_HIP(hipGetLastError());
     const bool small = p.n <= 8;
     const int req = small ? 2 : 8, thr = small ? 1024 : 512, dq = small ? 4 : 16;
