@@ -120,20 +120,6 @@ __device__ __forceinline__ uint32_t vgpr_pin(uint32_t v) {
     return v;
 }
 
-// ---------------------------------------------------------------------------
-// Wave64 reductions
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
 
 // Reductions over the 16 lanes of a row (lanes 16r .. 16r+15) with DPP: quad_perm
 // [1,0,3,2] (0xB1), quad_perm [2,3,0,1] (0x4E), row_half_mirror (0x141), row_mirror
@@ -180,6 +166,19 @@ __device__ __forceinline__ float sum_rows4(float a, float b, float c, float d) {
     const auto z = __builtin_amdgcn_permlane16_swap(__float_as_uint(X), __float_as_uint(Y), false, false);
     return __uint_as_float(z[0]) + __uint_as_float(z[1]);           // {a, c, b, d}
 }
+
+// Max over the 4 rows of a wave (lanes l, l^16, l^32, l^48), as sum_rows.
+__device__ __forceinline__ float max_rows(float v) {
+    const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float s = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
+    const auto y = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return fmaxf(__uint_as_float(y[0]), __uint_as_float(y[1]));
+}
+
+// Wave64 reductions (every lane active, every lane gets the result): within each row of
+// 16 with DPP, then over the rows with the lane swaps.
+__device__ __forceinline__ float wave_max(float v) { return max_rows(row16_max(v)); }
+__device__ __forceinline__ float wave_sum(float v) { return sum_rows(row16_sum(v)); }
 
 // ---------------------------------------------------------------------------
 // s_waitcnt with a run-time count (the instruction takes an immediate).

@@ -16,7 +16,11 @@
 //    every code to the model dtype (the dtype F.linear returns, round-to-nearest-even),
 //    optionally writes the rounded codes out, and stores the row: the codes themselves
 //    (bf16/fp16 cache) or the packed 3.2-bit row, the packers reading the rounded codes
-//    from LDS exactly as pack_kv reads them from memory.
+//    from LDS exactly as pack_kv reads them from memory. For at most 16 tokens of a
+//    3.2-bit cache, `groups` workgroups per token (each forming the codes) share its H K
+//    blocks and V block, one block per wave.
+#include <algorithm>
+
 #include "pack_rows.hpp"
 
 namespace starkv {
@@ -122,6 +126,7 @@ struct KvStoreParams {
     int quant;                        // 1: 3.2-bit rows
     int H; const int32_t* ranks; const int32_t* offsets; const int32_t* nouts;
     RowLayout row;
+    int groups;                       // 3.2-bit rows: workgroups per token (grid.y) sharing its H + 1 blocks
 };
 
 template <int DT>
@@ -163,7 +168,7 @@ __global__ __launch_bounds__(KVS_THR) void kv_store_kernel(const KvStoreParams p
             if (c < p.width) {
                 const uint16_t r = round_code<DT>(a);
                 s_code[c] = code_value<DT>(r);
-                if (p.codes) p.codes[(int64_t)i * p.co_s0 + c] = r;
+                if (p.codes && blockIdx.y == 0) p.codes[(int64_t)i * p.co_s0 + c] = r;
                 if (!p.quant && store) ((uint16_t*)p.cache)[row + c] = r;
             }
         }
@@ -172,7 +177,8 @@ __global__ __launch_bounds__(KVS_THR) void kv_store_kernel(const KvStoreParams p
     __syncthreads();
     const int lane = tid & 63;
     uint8_t* dst = (uint8_t*)p.cache + row;
-    for (int u = tid >> 6; u <= p.H; u += KVS_THR / 64) {
+    // Blocks u = y + groups (w + 16 k) of workgroup y, wave w (the H K blocks, then V).
+    for (int u = blockIdx.y + p.groups * (tid >> 6); u <= p.H; u += p.groups * (KVS_THR / 64)) {
         if (u < p.H) {
             const float* src = s_code + p.offsets[u];
             pack_k_block([&](int l) { return src[l]; }, p.ranks[u], p.nouts[u], p.offsets[u], u, p.row.ks_off, dst,
@@ -259,17 +265,20 @@ int starkv_write_kv(void* stream, const void* hidden, int64_t h_s0, const void* 
     s.slots = slot_mapping; s.slot_bits = slot_bits;
     s.quant = quant; s.H = num_kv_heads; s.ranks = k_ranks; s.offsets = k_offsets; s.nouts = k_nouts;
     s.row = rl;
+    // Few tokens: a token's H + 1 blocks are packed by several workgroups (each one forms
+    // the token's codes), one block per wave.
+    s.groups = quant && n <= 16 ? std::max(1, std::min(8, (num_kv_heads + 1 + KVS_THR / 64 - 1) / (KVS_THR / 64))) : 1;
     const size_t lds = (size_t)width * sizeof(float);
     SKV_CHECK(lds <= 64 * 1024, "write_kv: %d codes per token exceed the 64 KB LDS block", width);
     hipStream_t st = (hipStream_t)stream;
     if (w_dtype == STARKV_BF16) {
         hipLaunchKernelGGL(kv_gemm_kernel<STARKV_BF16>, ggrid, dim3(KVW_THR), 0, st, g);
         SKV_HIP(hipGetLastError());
-        hipLaunchKernelGGL(kv_store_kernel<STARKV_BF16>, dim3(n), dim3(KVS_THR), lds, st, s);
+        hipLaunchKernelGGL(kv_store_kernel<STARKV_BF16>, dim3(n, s.groups), dim3(KVS_THR), lds, st, s);
     } else {
         hipLaunchKernelGGL(kv_gemm_kernel<STARKV_F16>, ggrid, dim3(KVW_THR), 0, st, g);
         SKV_HIP(hipGetLastError());
-        hipLaunchKernelGGL(kv_store_kernel<STARKV_F16>, dim3(n), dim3(KVS_THR), lds, st, s);
+        hipLaunchKernelGGL(kv_store_kernel<STARKV_F16>, dim3(n, s.groups), dim3(KVS_THR), lds, st, s);
     }
     SKV_HIP(hipGetLastError());
     return STARKV_OK;
