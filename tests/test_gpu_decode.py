@@ -358,6 +358,23 @@ def test_two_pass_grids_and_one_pass_agree(cuda, two_pass):
     assert d <= 2e-3
 
 
+def test_two_pass_pv_ranges_over_logits_ranges(cuda, two_pass):
+    """The P @ V pass over ranges of R = 1 .. 4 logits-pass ranges (the grid sets R: it is
+    the grid over the split at 128 tokens per workgroup, here 47 for these lengths): every
+    R against the oracle, with an empty request and requests that start and end inside
+    the ranges."""
+    wl = W.make_lowrank([700, 0, 1500, 16], num_heads=32, seed=33)
+    g = wl.to(cuda)
+    truth = lowrank_truth(wl)
+    for grid in (47, 94, 141, 188, 200):
+        print(f"\n[two-pass R] grid={grid}", flush=True)
+        out = run_lowrank(g, grid=grid)
+        torch.cuda.synchronize()
+        o, t = out.float().cpu().numpy(), truth
+        assert np.isnan(o[1]).all()  # the empty request: softmax over no tokens
+        assert_close(out[[0, 2, 3]], t[[0, 2, 3]], f"two-pass grid={grid}")
+
+
 WIDE_CASES = {
     # name: (lengths, kwargs) -- V ranks the one-pass kernels do not take
     "bf16_v272": ([300, 17, 1024], dict(v_rank=272)),
