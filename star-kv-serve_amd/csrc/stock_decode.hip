@@ -113,16 +113,20 @@ __global__ __launch_bounds__(ST_THR) void stock_decode_kernel(const StockParams 
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            float d = 0.f;
+            // q . k over this lane's 32 dimensions (four chains), then over the 4 lanes of
+            // the token (quad permutes), then the page max over the 16 tokens: lanes of the
+            // same dimension chunk are l, l + 4, l + 8, l + 12 of each row (row rotations),
+            // then the 4 rows (lane swaps).
+            float dd[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < 32; ++i) d = fmaf(qv[g][i], kf[i], d);
-            d += __shfl_xor(d, 1, 64);
-            d += __shfl_xor(d, 2, 64);
+            for (int i = 0; i < 32; ++i) dd[i & 3] = fmaf(qv[g][i], kf[i], dd[i & 3]);
+            float d = (dd[0] + dd[1]) + (dd[2] + dd[3]);
+            d += dpp_f<0xB1>(d);  // quad_perm [1,0,3,2]
+            d += dpp_f<0x4E>(d);  // quad_perm [2,3,0,1]
             const float sv = ok ? d : -INFINITY;
-            float mx = fmaxf(sv, __shfl_xor(sv, 4, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            float mx = fmaxf(sv, dpp_f<0x128>(sv));  // row_ror:8
+            mx = fmaxf(mx, dpp_f<0x124>(mx));        // row_ror:4
+            mx = max_rows(mx);
             const float mn = fmaxf(m[g], mx);
             const float alpha = mn == -INFINITY ? 1.f : exp2f(m[g] - mn);
             const float pe = ok ? exp2f(sv - mn) : 0.f;
