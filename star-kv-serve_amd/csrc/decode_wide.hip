@@ -797,7 +797,7 @@ int launch_merge_wide(const DecodeParams& p, int grid, int w_dt, const void* vup
     // Slots per request: about gp / n + 1. Many (a few long requests): split them over waves.
     const int gp = (grid + p.pv_r - 1) / p.pv_r;
     if (gp >= 8 * p.n)
-        hipLaunchKernelGGL((merge_cols_kernel<8, 16, 512>), dim3(p.n, p.Hq, (p.v_rank + 255) / 256), dim3(512), 0,
+        hipLaunchKernelGGL((merge_cols_kernel<16, 8, 1024>), dim3(p.n, p.Hq, (p.v_rank + 255) / 256), dim3(1024), 0,
                            stream, (const uint8_t*)p.ws, p.ws_plan, p.ws_m, p.ws_l, p.ws_acc, p.ws_o, p.n, p.Hq,
                            p.v_rank, p.acc_ld, p.pv_r);
     else
