@@ -375,6 +375,21 @@ def test_two_pass_pv_ranges_over_logits_ranges(cuda, two_pass):
         assert_close(out[[0, 2, 3]], t[[0, 2, 3]], f"two-pass grid={grid}")
 
 
+def test_two_pass_long_request_many_partials(cuda):
+    """One request of 20,000 tokens at W 880, V rank 1280: the merge of its P @ V partials
+    with every wave's batched loads in use (default grid: 157 partials, R = 2), and at grid
+    1300 (16 tokens per logits range, R = 4: 313 partials) past the weights it keeps in
+    registers (256), where it reads the ranges' maxima from memory."""
+    wl = W.make_lowrank([20000], num_heads=32, seed=41, v_rank=1280, ranks=RANKS_880)
+    g = wl.to(cuda)
+    truth = lowrank_truth(wl)
+    for grid in (None, 1300):
+        print(f"\n[two-pass long] grid={grid}", flush=True)
+        out = run_lowrank(g, grid=grid)
+        torch.cuda.synchronize()
+        assert_close(out, truth, f"two-pass long grid={grid}")
+
+
 WIDE_CASES = {
     # name: (lengths, kwargs) -- V ranks the one-pass kernels do not take
     "bf16_v272": ([300, 17, 1024], dict(v_rank=272)),
