@@ -425,6 +425,9 @@ QUANT_WIDE_CASES = {
     "v4096_h8": ([300, 31], dict(v_rank=4096, num_heads=8, ranks=[32] * 8)),
     "v1290_graph_span": ([100, 37, 999], dict(v_rank=1290, ranks=RANKS_880, max_seq_len=4096)),
     "v1290_block64": ([900, 65, 3], dict(v_rank=1290, ranks=RANKS_880, block_size=64)),
+    # one long request: 313 P @ V partials (3.2-bit: one per logits range), past the 256
+    # merge weights held in registers
+    "v1290_long": ([20000], dict(v_rank=1290, ranks=RANKS_880)),
 }
 
 
