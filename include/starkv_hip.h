@@ -159,16 +159,32 @@ size_t starkv_decode_workspace_bytes(int cache_kind, int n, int num_heads, int n
 int starkv_decode_two_pass(int cache_kind, int num_heads, int k_width, int v_rank);
 
 /*
- * 1 if the decode entry points take a layer of this shape, else 0 (host function, no
- * device access; call it at load time). k_ranks: host array of the num_kv_heads K ranks.
- * A layer is refused when it has more than 32 query heads, more than 96 16-lane rank
- * tiles over its query heads ((num_heads / num_kv_heads) x k_width / 16), a query head
- * with more tiles than one of the decode kernel's 8 waves holds (16) after the wave plan
- * balances whole heads, v_rank above 4096, or (3.2-bit) num_kv_heads != num_heads. The
- * decode calls themselves return NaN rows for a layer whose heads do not fit the plan.
- * No counterpart in the reference, whose Triton kernels take any head count.
+ * 1 if one decode call takes a layer of this shape, else 0 (host function, no device
+ * access; call it at load time). k_ranks: host array of the num_kv_heads K ranks. One
+ * call is refused when it has more than 32 query heads, more than 96 16-lane rank tiles
+ * over its query heads ((num_heads / num_kv_heads) x k_width / 16), a wave of the decode
+ * kernel's 8 that would hold more than 16 tiles after the wave plan balances whole heads,
+ * v_rank above 4096, or (3.2-bit) num_kv_heads != num_heads. A decode call over a shape
+ * refused here returns NaN rows; starkv_decode_layer_groups splits such a layer into
+ * calls that fit. No counterpart in the reference, whose Triton kernels take any head
+ * count.
  */
 int starkv_decode_layer_fits(int cache_kind, int num_heads, int num_kv_heads, const int32_t *k_ranks, int v_rank);
+
+/*
+ * How a layer is decoded: as `count` calls over consecutive KV-head ranges, written to
+ * groups[2 i], groups[2 i + 1] = [first, end) for i < count (host function, no device
+ * access; call it at load time). Returns count >= 1 (1: the whole layer in one call),
+ * 0 if some single KV head does not fit one call (or more than max_groups ranges are
+ * needed), -1 for invalid arguments. Ranges are greedy: each as long as one call takes
+ * (starkv_decode_layer_fits' limits on that range). bf16/fp16 calls over a range get
+ * the cache pointer advanced to its first K lane and its V codes through v_col
+ * (starkv_lowrank_decode); 3.2-bit calls go through starkv_quant_decode_group. No
+ * counterpart in the reference, whose Triton kernels take any head count
+ * (paged_quant.py:357-411 sizes its V block by next_pow2(H), :407).
+ */
+int starkv_decode_layer_groups(int cache_kind, int num_heads, int num_kv_heads, const int32_t *k_ranks, int v_rank,
+                               int32_t *groups, int max_groups);
 
 /*
  * Forces the decode form for the calls that follow (process-wide, not thread-safe; for
@@ -257,6 +273,39 @@ int starkv_quant_decode(void *stream, const void *query, int64_t q_s0, int64_t q
                         int64_t vu_s0, int64_t vu_s1, int vu_dtype, const void *cos_sin, int64_t cs_s0,
                         int cs_dtype, float scale, void *out, int64_t o_s0, int64_t o_s1, int out_dtype,
                         void *workspace, size_t workspace_bytes, int grid);
+
+/*
+ * starkv_quant_decode over query heads [head0, head0 + num_heads) of a layer whose rows
+ * are QuantRow(row_k_width, row_num_heads, v_rank) (row_bytes its nbytes): the heads' K
+ * nibbles start at K lane k_lane0 (a multiple of 16) and span k_width lanes. kv_cache
+ * points at the rows (as for the whole layer); query, k_up (the group's k_width rows),
+ * tile_head / tile_nout / tile_last (from the group's first tile: tile_head values are
+ * the layer's head indices), v_up_by_q and out cover the group's heads only. The call
+ * reads its heads' K nibbles and K scales and the whole V block. The whole-layer call
+ * is row_k_width = k_width, row_num_heads = num_heads, head0 = k_lane0 = 0.
+ *   workspace   >= starkv_quant_group_workspace_bytes(...) bytes
+ * Layers beyond one call's limits (more than 32 heads or 96 rank tiles) run as such
+ * groups (starkv_decode_layer_groups); the reference's Triton path takes them in one
+ * launch (paged_quant.py:357-411).
+ */
+int starkv_quant_decode_group(void *stream, const void *query, int64_t q_s0, int64_t q_s1, int q_dtype,
+                              const uint8_t *kv_cache, int64_t c_s0, int64_t c_s1, int block_size,
+                              const int32_t *block_table, int64_t bt_s0, int64_t bt_s1, const int32_t *seq_lens,
+                              int n, int num_heads, int max_seq_len, int k_width, int v_rank, int row_bytes,
+                              const void *k_up, int64_t ku_s0, int w_dtype, const int32_t *tile_head,
+                              const int32_t *tile_nout, const int32_t *tile_last, const void *v_up_by_q,
+                              int64_t vu_s0, int64_t vu_s1, int vu_dtype, const void *cos_sin, int64_t cs_s0,
+                              int cs_dtype, float scale, void *out, int64_t o_s0, int64_t o_s1, int out_dtype,
+                              void *workspace, size_t workspace_bytes, int grid, int row_k_width,
+                              int row_num_heads, int head0, int k_lane0);
+
+/* Workspace bytes of starkv_quant_decode_group (0 for invalid sizes). */
+size_t starkv_quant_group_workspace_bytes(int n, int row_k_width, int row_num_heads, int v_rank, int head0,
+                                          int num_heads, int k_lane0, int k_width, int max_seq_len, int grid);
+
+/* 1 if starkv_quant_decode_group over this group runs in two passes, else 0. */
+int starkv_quant_group_two_pass(int row_k_width, int row_num_heads, int v_rank, int head0, int num_heads,
+                                int k_lane0, int k_width);
 
 /*
  * The step's K and V of uncompressed layers into vLLM's paged caches

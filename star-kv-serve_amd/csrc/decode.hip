@@ -61,6 +61,7 @@ struct PrepArgs {
     int n, max_seq_len, grid, Hq, Hkv, TT, k_rows;
     const int32_t* k_ranks; const int32_t* k_offsets;                       // bf16/fp16
     const int32_t* t_head; const int32_t* t_nout; const int32_t* t_last;  // 3.2-bit (t_head set)
+    int head0, code0;  // 3.2-bit head groups: the group's first head, code tile of its first tile
     const void* q; int64_t q_s0, q_s1; int q_dt;
     const void* k_up; int64_t ku_s0; int ku_dt;
     float sc;  // scale * log2(e)
@@ -80,14 +81,15 @@ struct TileTable {
 // Fills `tt` (every thread of the workgroup calls it; it ends with a barrier).
 //   bf16/fp16: query head h (kv head h / (Hq / Hkv)) has ceil(rank / 16) tiles; the
 //     heads' tiles are laid out head after head, k_up rows from the kv head's offset.
-//   3.2-bit: tile t belongs to head t_head[t], k_up rows 16 t .. 16 t + 15 (lanes
-//     contiguous), outlier ranks t_nout[t].
+//   3.2-bit: tile t belongs to head t_head[t] - head0 (a call over a group of heads
+//     gets the tables from the group's first tile on), k_up rows 16 t .. 16 t + 15
+//     (lanes contiguous), outlier ranks t_nout[t], code tile code0 + t.
 __device__ void tile_table(const PrepArgs& a, TileTable& tt, int tid) {
     int h = 0, hp = -1, nout = 0;  // 3.2-bit: tile tid's head, tile tid - 1's head, outlier ranks
     if (a.t_head) {
         if (tid < a.TT) {
-            h = min(max(a.t_head[tid], 0), a.Hq - 1);
-            if (tid > 0) hp = min(max(a.t_head[tid - 1], 0), a.Hq - 1);
+            h = min(max(a.t_head[tid] - a.head0, 0), a.Hq - 1);
+            if (tid > 0) hp = min(max(a.t_head[tid - 1] - a.head0, 0), a.Hq - 1);
             nout = min(max(a.t_nout[tid], 0), 16);
         }
     } else if (tid < a.Hkv) {
@@ -110,7 +112,7 @@ __device__ void tile_table(const PrepArgs& a, TileTable& tt, int tid) {
             tt.head[tid] = h;
             tt.row[tid] = 16 * tid;
             tt.valid[tid] = 16;
-            tt.word[tid] = tid | (nout << 13);
+            tt.word[tid] = (a.code0 + tid) | (nout << 13);
             atomicAdd(&tt.hn[h], 1);
             if (hp != h) tt.hf[h] = tid;  // a head's tiles are contiguous
         }
@@ -690,6 +692,7 @@ struct CommonArgs {
     const void* k_up; int64_t ku_s0; int w_dt;
     const int32_t* k_ranks; const int32_t* k_offsets;
     const int32_t* t_head; const int32_t* t_nout; const int32_t* t_last;
+    int head0, code0;
     const void* vup; int64_t vu_s0, vu_s1; int vu_dt; int v_rank;
     const void* cs; int64_t cs_s0; int cs_dt;
     float scale;
@@ -784,10 +787,11 @@ static int lcap_of(int max_seq_len) { return (max_seq_len + TILE_TOK - 1) / TILE
 
 // QuantRow (paged_quant.py:71-111) offsets of a 3.2-bit row.
 struct QRow {
-    int v_nout, v_nbo, ks_off, vs_off, vq_off, v_bytes, nbytes;
+    int v_rank, v_nout, v_nbo, ks_off, vs_off, vq_off, v_bytes, nbytes;
 };
 static QRow qrow(int k_width, int num_heads, int v_rank) {
     QRow r;
+    r.v_rank = v_rank;
     r.v_nout = (int)(0.2 * (double)v_rank);
     r.v_nbo = (r.v_nout + 1) / 2;
     r.ks_off = k_width / 2;
@@ -796,6 +800,92 @@ static QRow qrow(int k_width, int num_heads, int v_rank) {
     r.v_bytes = r.v_nbo + (v_rank - r.v_nout + 1) / 2;
     r.nbytes = (r.vq_off + r.v_bytes + 15) / 16 * 16;
     return r;
+}
+
+// A 3.2-bit call over query heads [head0, head0 + heads) of a layer whose rows are
+// QuantRow(row_k_width, row_heads, v_rank), the heads' K lanes starting at lane0 (a
+// multiple of 16). Its cache pointer is advanced to the 16-byte granule `base` holding
+// the group's first K nibble byte; every offset below is relative to it. The copies of
+// a page take the bytes from there to the row's end (one pass) or to the group's last K
+// scale (the logits pass of two-pass calls).
+struct QGroup {
+    QRow row;       // the layer's row
+    int base;       // bytes the cache pointer advances
+    int code0;      // code tile (8 bytes) of the group's first tile, from base
+    int ks_off, vs_off, vq_off;
+    int extent;     // bytes from base to the row's end (a multiple of 16)
+    int k_extent;   // bytes from base through the group's K scales, rounded up to 16
+};
+static QGroup qgroup(int row_k_width, int row_heads, int v_rank, int head0, int heads, int lane0) {
+    QGroup g;
+    g.row = qrow(row_k_width, row_heads, v_rank);
+    const int kb = lane0 / 2;
+    g.base = kb & ~15;
+    g.code0 = (kb - g.base) / 8;
+    g.ks_off = g.row.ks_off + 4 * head0 - g.base;
+    g.vs_off = g.row.vs_off - g.base;
+    g.vq_off = g.row.vq_off - g.base;
+    g.extent = g.row.nbytes - g.base;
+    g.k_extent = (g.ks_off + 4 * heads + 15) / 16 * 16;
+    return g;
+}
+
+static bool qgroup_args_ok(int row_k_width, int row_heads, int v_rank, int head0, int heads, int lane0,
+                           int k_width) {
+    return row_k_width >= 16 && row_k_width % 16 == 0 && row_heads >= 1 && v_rank >= 1 && head0 >= 0 &&
+           heads >= 1 && head0 + heads <= row_heads && lane0 >= 0 && lane0 % 16 == 0 && k_width >= 16 &&
+           k_width % 16 == 0 && lane0 + k_width <= row_k_width;
+}
+
+// Whether a 3.2-bit call over this group takes the two-pass form.
+static bool qgroup_two_pass(const QGroup& g) {
+    return use_two_pass(FMT_Q4, 0, g.row.v_rank, g.extent, g.row.v_nout);
+}
+
+// Whether one 3.2-bit call takes query heads [h0, h1) of an MHA layer of H heads with K
+// ranks `ranks`: at most 32 heads and 96 rank tiles, a wave plan in which every wave
+// holds at most 16 tiles, and pages (from the group's first K byte) that fit in LDS.
+static bool quant_group_fits(const int32_t* ranks, int H, int v_rank, int h0, int h1) {
+    const int heads = h1 - h0;
+    if (heads < 1 || heads > MAX_H || h0 < 0 || h1 > H || v_rank < 1 || v_rank > MAX_V_RANK_TWO_PASS) return false;
+    int tiles[MAX_H];
+    int TT = 0, lane0 = 0, kw = 0, row_kw = 0;
+    for (int h = 0; h < H; ++h) {
+        if (ranks[h] < 0 || ranks[h] > 16 * MAX_TT) return false;
+        const int w = (ranks[h] + 15) / 16 * 16;
+        if (h < h0) lane0 += w;
+        if (h >= h0 && h < h1) {
+            kw += w;
+            tiles[h - h0] = w / 16;
+            TT += w / 16;
+        }
+        row_kw += w;
+    }
+    if (TT < 1 || TT > MAX_TT || !plan_fits(tiles, heads, TT)) return false;
+    const QGroup g = qgroup(row_kw, H, v_rank, h0, heads, lane0);
+    if (!qgroup_two_pass(g)) return true;
+    return quant_copies(g.k_extent) > 0 && quant_lds_bytes(g.k_extent, 0) <= quant_lds_limit() &&
+           pv_fits(FMT_Q4, kw, v_rank, g.vs_off, g.vq_off, g.row.v_nout, g.row.v_bytes);
+}
+
+// Whether one bf16/fp16 call takes KV heads with K ranks ranks[0 .. hkv) and `per` query
+// heads each: the call reads their K lanes and the V codes.
+static bool codes_group_fits(int cache_kind, int per, const int32_t* ranks, int hkv, int v_rank) {
+    const int Hq = per * hkv;
+    if (Hq < 1 || Hq > MAX_H || v_rank < 1 || v_rank > MAX_V_RANK_TWO_PASS) return false;
+    int tiles[MAX_H];
+    int TT = 0, k_width = 0;
+    for (int kv = 0; kv < hkv; ++kv) {
+        const int r = ranks[kv];
+        if (r < 0 || r > 16 * MAX_TT) return false;
+        k_width += (r + 15) / 16 * 16;
+        for (int j = 0; j < per; ++j) tiles[kv * per + j] = (r + 15) / 16;
+    }
+    for (int h = 0; h < Hq; ++h) TT += tiles[h];
+    if (TT < 1 || TT > MAX_TT || !plan_fits(tiles, Hq, TT)) return false;
+    const int fmt = cache_kind == STARKV_F16 ? FMT_F16 : FMT_BF16;
+    if (!use_two_pass(fmt, k_width, v_rank, (k_width + v_rank) * 2, 0)) return true;
+    return lowrank_copies(k_width, 0) > 0 && pv_fits(fmt, k_width, v_rank, 0, 0, 0, 0);
 }
 
 static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_bytes, int TT, hipStream_t stream) {
@@ -857,7 +947,7 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
                           p.v_nbo + (a.v_rank - p.v_nout + 1) / 2),
                   "decode: no P @ V window of v_rank %d fits in LDS", a.v_rank);
         if (fmt == FMT_Q4) {
-            const int rk = (p.vs_off + 15) / 16 * 16;
+            const int rk = (p.ks_off + 4 * a.Hq + 15) / 16 * 16;
             SKV_CHECK(quant_copies(rk) > 0 && quant_lds_bytes(rk, 0) <= quant_lds_limit(),
                       "decode: a 3.2-bit page of %d K bytes per row does not fit in LDS", rk);
             p.row_g = rk / 16;
@@ -891,6 +981,7 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     pa.Hq = a.Hq; pa.Hkv = a.Hkv; pa.TT = TT; pa.k_rows = p.k_width;
     pa.k_ranks = a.k_ranks; pa.k_offsets = a.k_offsets;
     pa.t_head = a.t_head; pa.t_nout = a.t_nout; pa.t_last = a.t_last;
+    pa.head0 = a.head0; pa.code0 = a.code0;
     pa.q = a.q; pa.q_s0 = a.q_s0; pa.q_s1 = a.q_s1; pa.q_dt = a.q_dt;
     pa.k_up = a.k_up; pa.ku_s0 = a.ku_s0; pa.ku_dt = a.w_dt;
     pa.sc = a.scale * LOG2E;
@@ -1012,11 +1103,9 @@ size_t starkv_decode_workspace_bytes(int cache_kind, int n, int num_heads, int n
         return 0;
     int fmt, row_bytes, v_nout = 0, TT;
     if (cache_kind == STARKV_CACHE_Q3_2) {
-        const QRow r = qrow(k_width, num_heads, v_rank);
-        fmt = FMT_Q4;
-        row_bytes = r.nbytes;
-        v_nout = r.v_nout;
-        TT = k_width / 16;
+        if (k_width % 16) return 0;
+        return starkv_quant_group_workspace_bytes(n, k_width, num_heads, v_rank, 0, num_heads, 0, k_width,
+                                                  max_seq_len, grid);
     } else {
         fmt = cache_kind == STARKV_F16 ? FMT_F16 : FMT_BF16;
         row_bytes = (k_width + v_rank) * 2;
@@ -1033,31 +1122,39 @@ int starkv_decode_layer_fits(int cache_kind, int num_heads, int num_kv_heads, co
     SKV_CHECK(k_ranks != nullptr, "decode_layer_fits: null k_ranks");
     SKV_CHECK(num_heads >= 1 && num_kv_heads >= 1 && num_heads % num_kv_heads == 0,
               "decode_layer_fits: %d query heads over %d kv heads", num_heads, num_kv_heads);
-    if (cache_kind == STARKV_CACHE_Q3_2 && num_heads != num_kv_heads) return 0;  // MHA only (paged_quant.py:374)
-    if (num_heads > MAX_H || v_rank < 1 || v_rank > MAX_V_RANK_TWO_PASS) return 0;
-    int tiles[MAX_H];
-    int TT = 0, k_width = 0;
-    const int grp = num_heads / num_kv_heads;
-    for (int kv = 0; kv < num_kv_heads; ++kv) {
-        const int r = k_ranks[kv];
-        if (r < 0) return 0;
-        k_width += (r + 15) / 16 * 16;
-        for (int j = 0; j < grp; ++j) tiles[kv * grp + j] = (r + 15) / 16;
+    if (cache_kind == STARKV_CACHE_Q3_2)
+        return num_heads == num_kv_heads && quant_group_fits(k_ranks, num_heads, v_rank, 0, num_heads);
+    return codes_group_fits(cache_kind, num_heads / num_kv_heads, k_ranks, num_kv_heads, v_rank);
+}
+
+int starkv_decode_layer_groups(int cache_kind, int num_heads, int num_kv_heads, const int32_t* k_ranks, int v_rank,
+                               int32_t* groups, int max_groups) {
+    clear_error();
+    if (k_ranks == nullptr || groups == nullptr || max_groups < 1 || num_heads < 1 || num_kv_heads < 1 ||
+        num_heads % num_kv_heads != 0) {
+        set_error("decode_layer_groups: %d query heads over %d kv heads, %d group slots", num_heads, num_kv_heads,
+                  max_groups);
+        return -1;
     }
-    for (int h = 0; h < num_heads; ++h) TT += tiles[h];
-    if (TT > MAX_TT) return 0;
-    if (!plan_fits(tiles, num_heads, TT)) return 0;
-    // The pages of the pass that reads K must fit in LDS.
-    if (cache_kind == STARKV_CACHE_Q3_2) {
-        const QRow r = qrow(k_width, num_heads, v_rank);
-        if (!use_two_pass(FMT_Q4, k_width, v_rank, r.nbytes, r.v_nout)) return 1;
-        const int rk = (r.vs_off + 15) / 16 * 16;
-        return quant_copies(rk) > 0 && quant_lds_bytes(rk, 0) <= quant_lds_limit() &&
-               pv_fits(FMT_Q4, k_width, v_rank, r.vs_off, r.vq_off, r.v_nout, r.v_bytes);
+    const bool quant = cache_kind == STARKV_CACHE_Q3_2;
+    if (quant && num_heads != num_kv_heads) return 0;  // MHA only (paged_quant.py:374)
+    const int per = num_heads / num_kv_heads;
+    auto fits = [&](int g0, int g1) {
+        return quant ? quant_group_fits(k_ranks, num_kv_heads, v_rank, g0, g1)
+                     : codes_group_fits(cache_kind, per, k_ranks + g0, g1 - g0, v_rank);
+    };
+    int count = 0;
+    for (int g0 = 0; g0 < num_kv_heads;) {
+        if (!fits(g0, g0 + 1)) return 0;
+        int g1 = g0 + 1;
+        while (g1 < num_kv_heads && fits(g0, g1 + 1)) ++g1;
+        if (count == max_groups) return 0;
+        groups[2 * count] = g0;
+        groups[2 * count + 1] = g1;
+        ++count;
+        g0 = g1;
     }
-    const int fmt = cache_kind == STARKV_F16 ? FMT_F16 : FMT_BF16;
-    if (!use_two_pass(fmt, k_width, v_rank, (k_width + v_rank) * 2, 0)) return 1;
-    return lowrank_copies(k_width, 0) > 0 && pv_fits(fmt, k_width, v_rank, 0, 0, 0, 0);
+    return count;
 }
 
 int starkv_decode_set_path(int mode) {
@@ -1072,10 +1169,8 @@ int starkv_decode_set_path(int mode) {
 }
 
 int starkv_decode_two_pass(int cache_kind, int num_heads, int k_width, int v_rank) {
-    if (cache_kind == STARKV_CACHE_Q3_2) {
-        const QRow r = qrow(k_width, num_heads, v_rank);
-        return use_two_pass(FMT_Q4, k_width, v_rank, r.nbytes, r.v_nout);
-    }
+    if (cache_kind == STARKV_CACHE_Q3_2)
+        return starkv_quant_group_two_pass(k_width, num_heads, v_rank, 0, num_heads, 0, k_width);
     return use_two_pass(cache_kind == STARKV_F16 ? FMT_F16 : FMT_BF16, k_width, v_rank, (k_width + v_rank) * 2, 0);
 }
 
@@ -1120,7 +1215,7 @@ int starkv_lowrank_decode(void* stream, const void* query, int64_t q_s0, int64_t
     p.k_width = k_width;
     p.v_col = v_col;
     CommonArgs a{query, q_s0, q_s1, q_dtype, block_table, bt_s0, bt_s1, seq_lens, n, num_heads, num_kv_heads,
-                 max_seq_len, k_up, ku_s0, w_dtype, k_ranks, k_head_offsets, nullptr, nullptr, nullptr,
+                 max_seq_len, k_up, ku_s0, w_dtype, k_ranks, k_head_offsets, nullptr, nullptr, nullptr, 0, 0,
                  v_up_by_q, vu_s0, vu_s1, vu_dtype, v_rank, cos_sin, cs_s0, cs_dtype, scale, out, o_s0, o_s1,
                  out_dtype, workspace, workspace_bytes, grid};
     const int TT = (num_heads / num_kv_heads) * (k_width / 16);
@@ -1158,6 +1253,46 @@ int starkv_lowrank_decode_noalloc(void* stream, const void* query, int64_t q_s0,
                                  NOALLOC_SCRATCH_BYTES, grid);
 }
 
+int starkv_quant_decode_group(void* stream, const void* query, int64_t q_s0, int64_t q_s1, int q_dtype,
+                              const uint8_t* kv_cache, int64_t c_s0, int64_t c_s1, int block_size,
+                              const int32_t* block_table, int64_t bt_s0, int64_t bt_s1, const int32_t* seq_lens, int n,
+                              int num_heads, int max_seq_len, int k_width, int v_rank, int row_bytes,
+                              const void* k_up, int64_t ku_s0, int w_dtype, const int32_t* tile_head,
+                              const int32_t* tile_nout, const int32_t* tile_last, const void* v_up_by_q,
+                              int64_t vu_s0, int64_t vu_s1, int vu_dtype, const void* cos_sin, int64_t cs_s0,
+                              int cs_dtype, float scale, void* out, int64_t o_s0, int64_t o_s1, int out_dtype,
+                              void* workspace, size_t workspace_bytes, int grid, int row_k_width, int row_num_heads,
+                              int head0, int k_lane0) {
+    clear_error();
+    SKV_CHECK(qgroup_args_ok(row_k_width, row_num_heads, v_rank, head0, num_heads, k_lane0, k_width),
+              "quant_decode: heads [%d, %d) with K lanes [%d, %d) of a layer of %d heads and K width %d "
+              "(widths multiples of 16)",
+              head0, head0 + num_heads, k_lane0, k_lane0 + k_width, row_num_heads, row_k_width);
+    SKV_CHECK(query && kv_cache && block_table && seq_lens && k_up && tile_head && tile_nout && tile_last &&
+                  v_up_by_q && cos_sin && out && workspace,
+              "quant_decode: null pointer");
+    const QGroup g = qgroup(row_k_width, row_num_heads, v_rank, head0, num_heads, k_lane0);
+    SKV_CHECK(row_bytes == g.row.nbytes, "quant_decode: row_bytes %d != QuantRow.nbytes %d", row_bytes,
+              g.row.nbytes);
+    DecodeParams p;
+    memset(&p, 0, sizeof(p));
+    p.cache = kv_cache + g.base;
+    p.c_s0 = c_s0;
+    p.c_s1 = c_s1;
+    p.bs_shift = block_shift(block_size);
+    p.k_width = k_width;
+    p.v_nout = g.row.v_nout;
+    p.v_nbo = g.row.v_nbo;
+    p.ks_off = g.ks_off;
+    p.vs_off = g.vs_off;
+    p.vq_off = g.vq_off;
+    CommonArgs a{query, q_s0, q_s1, q_dtype, block_table, bt_s0, bt_s1, seq_lens, n, num_heads, num_heads,
+                 max_seq_len, k_up, ku_s0, w_dtype, nullptr, nullptr, tile_head, tile_nout, tile_last, head0, g.code0,
+                 v_up_by_q, vu_s0, vu_s1, vu_dtype, v_rank, cos_sin, cs_s0, cs_dtype, scale, out, o_s0, o_s1,
+                 out_dtype, workspace, workspace_bytes, grid};
+    return decode_common(p, a, FMT_Q4, g.extent, k_width / 16, (hipStream_t)stream);
+}
+
 int starkv_quant_decode(void* stream, const void* query, int64_t q_s0, int64_t q_s1, int q_dtype,
                         const uint8_t* kv_cache, int64_t c_s0, int64_t c_s1, int block_size,
                         const int32_t* block_table, int64_t bt_s0, int64_t bt_s1, const int32_t* seq_lens, int n,
@@ -1167,32 +1302,29 @@ int starkv_quant_decode(void* stream, const void* query, int64_t q_s0, int64_t q
                         int vu_dtype, const void* cos_sin, int64_t cs_s0, int cs_dtype, float scale, void* out,
                         int64_t o_s0, int64_t o_s1, int out_dtype, void* workspace, size_t workspace_bytes,
                         int grid) {
-    clear_error();
-    SKV_CHECK(k_width >= 16 && k_width % 16 == 0, "quant_decode: k_width %d must be a positive multiple of 16",
-              k_width);
-    SKV_CHECK(query && kv_cache && block_table && seq_lens && k_up && tile_head && tile_nout && tile_last &&
-                  v_up_by_q && cos_sin && out && workspace,
-              "quant_decode: null pointer");
-    DecodeParams p;
-    memset(&p, 0, sizeof(p));
-    p.cache = kv_cache;
-    p.c_s0 = c_s0;
-    p.c_s1 = c_s1;
-    p.bs_shift = block_shift(block_size);
-    p.k_width = k_width;
-    SKV_CHECK(num_heads >= 1 && v_rank >= 1, "quant_decode: num_heads %d, v_rank %d", num_heads, v_rank);
-    const QRow r = qrow(k_width, num_heads, v_rank);
-    p.v_nout = r.v_nout;
-    p.v_nbo = r.v_nbo;
-    p.ks_off = r.ks_off;
-    p.vs_off = r.vs_off;
-    p.vq_off = r.vq_off;
-    SKV_CHECK(row_bytes == r.nbytes, "quant_decode: row_bytes %d != QuantRow.nbytes %d", row_bytes, r.nbytes);
-    CommonArgs a{query, q_s0, q_s1, q_dtype, block_table, bt_s0, bt_s1, seq_lens, n, num_heads, num_heads,
-                 max_seq_len, k_up, ku_s0, w_dtype, nullptr, nullptr, tile_head, tile_nout, tile_last,
-                 v_up_by_q, vu_s0, vu_s1, vu_dtype, v_rank, cos_sin, cs_s0, cs_dtype, scale, out, o_s0, o_s1,
-                 out_dtype, workspace, workspace_bytes, grid};
-    return decode_common(p, a, FMT_Q4, row_bytes, k_width / 16, (hipStream_t)stream);
+    return starkv_quant_decode_group(stream, query, q_s0, q_s1, q_dtype, kv_cache, c_s0, c_s1, block_size,
+                                     block_table, bt_s0, bt_s1, seq_lens, n, num_heads, max_seq_len, k_width, v_rank,
+                                     row_bytes, k_up, ku_s0, w_dtype, tile_head, tile_nout, tile_last, v_up_by_q,
+                                     vu_s0, vu_s1, vu_dtype, cos_sin, cs_s0, cs_dtype, scale, out, o_s0, o_s1,
+                                     out_dtype, workspace, workspace_bytes, grid, k_width, num_heads, 0, 0);
+}
+
+size_t starkv_quant_group_workspace_bytes(int n, int row_k_width, int row_num_heads, int v_rank, int head0,
+                                          int num_heads, int k_lane0, int k_width, int max_seq_len, int grid) {
+    if (n < 1 || max_seq_len < 1 || grid < 1 ||
+        !qgroup_args_ok(row_k_width, row_num_heads, v_rank, head0, num_heads, k_lane0, k_width))
+        return 0;
+    const QGroup g = qgroup(row_k_width, row_num_heads, v_rank, head0, num_heads, k_lane0);
+    const bool two = qgroup_two_pass(g);
+    return ws_layout(n, num_heads, k_width / 16, v_rank, grid, two ? lcap_of(max_seq_len) : 0,
+                     two ? pv_ratio(FMT_Q4, n, max_seq_len, grid) : 1)
+        .total;
+}
+
+int starkv_quant_group_two_pass(int row_k_width, int row_num_heads, int v_rank, int head0, int num_heads,
+                                int k_lane0, int k_width) {
+    if (!qgroup_args_ok(row_k_width, row_num_heads, v_rank, head0, num_heads, k_lane0, k_width)) return 0;
+    return qgroup_two_pass(qgroup(row_k_width, row_num_heads, v_rank, head0, num_heads, k_lane0));
 }
 
 }  // extern "C"

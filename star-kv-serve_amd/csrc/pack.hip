@@ -90,7 +90,7 @@ using namespace starkv;
 
 extern "C" {
 
-int starkv_abi_version(void) { return 4; }
+int starkv_abi_version(void) { return 5; }
 
 const char* starkv_last_error(void) { return g_err; }
 

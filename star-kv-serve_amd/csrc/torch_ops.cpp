@@ -78,23 +78,28 @@ void quant_decode(const at::Tensor& query, const at::Tensor& kv_cache, const at:
                   const at::Tensor& seq_lens, int64_t max_seq_len, int64_t k_width, int64_t v_rank, int64_t row_bytes,
                   const at::Tensor& k_up, const at::Tensor& tile_head, const at::Tensor& tile_nout,
                   const at::Tensor& tile_last, const at::Tensor& v_up_by_q, const at::Tensor& cos_sin, double scale,
-                  const at::Tensor& out) {
+                  const at::Tensor& out, int64_t row_k_width, int64_t row_num_heads, int64_t head0, int64_t k_lane0) {
     const c10::DeviceGuard guard(query.device());
     TORCH_CHECK(kv_cache.scalar_type() == at::kByte, "starkv.quant_decode: the cache is uint8 rows");
     const int n = (int)query.size(0), H = (int)query.size(1);
     const int grid = starkv_decode_grid_for(STARKV_CACHE_Q3_2, n, H, H, (int)k_width, (int)v_rank, (int)max_seq_len);
     TORCH_CHECK(grid > 0, "starkv.quant_decode: no grid for ", n, " requests");
-    const at::Tensor ws = workspace(query, starkv_decode_workspace_bytes(STARKV_CACHE_Q3_2, n, H, H, (int)k_width,
-                                                                         (int)v_rank, (int)max_seq_len, grid));
-    check(starkv_quant_decode(stream_of(query), query.data_ptr(), query.stride(0), query.stride(1), dtype_code(query),
-                              kv_cache.data_ptr<uint8_t>(), kv_cache.stride(0), kv_cache.stride(1),
-                              (int)kv_cache.size(1), i32(block_table, "block_table"), block_table.stride(0),
-                              block_table.stride(1), i32(seq_lens, "seq_lens"), n, H, (int)max_seq_len, (int)k_width,
-                              (int)v_rank, (int)row_bytes, k_up.data_ptr(), k_up.stride(0), dtype_code(k_up),
-                              i32(tile_head, "tile_head"), i32(tile_nout, "tile_nout"), i32(tile_last, "tile_last"),
-                              v_up_by_q.data_ptr(), v_up_by_q.stride(0), v_up_by_q.stride(1), dtype_code(v_up_by_q),
-                              cos_sin.data_ptr(), cos_sin.stride(0), dtype_code(cos_sin), (float)scale, out.data_ptr(),
-                              out.stride(0), out.stride(1), dtype_code(out), ws.data_ptr(), (size_t)ws.numel(), grid),
+    const size_t need = starkv_quant_group_workspace_bytes(n, (int)row_k_width, (int)row_num_heads, (int)v_rank,
+                                                           (int)head0, H, (int)k_lane0, (int)k_width,
+                                                           (int)max_seq_len, grid);
+    TORCH_CHECK(need > 0, "starkv.quant_decode: heads [", head0, ", ", head0 + H, ") with K lanes [", k_lane0, ", ",
+                k_lane0 + k_width, ") do not fit a layer of ", row_num_heads, " heads and K width ", row_k_width);
+    const at::Tensor ws = workspace(query, need);
+    check(starkv_quant_decode_group(
+              stream_of(query), query.data_ptr(), query.stride(0), query.stride(1), dtype_code(query),
+              kv_cache.data_ptr<uint8_t>(), kv_cache.stride(0), kv_cache.stride(1), (int)kv_cache.size(1),
+              i32(block_table, "block_table"), block_table.stride(0), block_table.stride(1), i32(seq_lens, "seq_lens"),
+              n, H, (int)max_seq_len, (int)k_width, (int)v_rank, (int)row_bytes, k_up.data_ptr(), k_up.stride(0),
+              dtype_code(k_up), i32(tile_head, "tile_head"), i32(tile_nout, "tile_nout"), i32(tile_last, "tile_last"),
+              v_up_by_q.data_ptr(), v_up_by_q.stride(0), v_up_by_q.stride(1), dtype_code(v_up_by_q),
+              cos_sin.data_ptr(), cos_sin.stride(0), dtype_code(cos_sin), (float)scale, out.data_ptr(), out.stride(0),
+              out.stride(1), dtype_code(out), ws.data_ptr(), (size_t)ws.numel(), grid, (int)row_k_width,
+              (int)row_num_heads, (int)head0, (int)k_lane0),
           "quant_decode");
 }
 
@@ -211,7 +216,8 @@ TORCH_LIBRARY(starkv, m) {
           "Tensor cos_sin, float scale, Tensor(a!) out) -> ()");
     m.def("quant_decode(Tensor query, Tensor kv_cache, Tensor block_table, Tensor seq_lens, int max_seq_len, "
           "int k_width, int v_rank, int row_bytes, Tensor k_up, Tensor tile_head, Tensor tile_nout, "
-          "Tensor tile_last, Tensor v_up_by_q, Tensor cos_sin, float scale, Tensor(a!) out) -> ()");
+          "Tensor tile_last, Tensor v_up_by_q, Tensor cos_sin, float scale, Tensor(a!) out, int row_k_width, "
+          "int row_num_heads, int head0, int k_lane0) -> ()");
     m.def("pack_kv(Tensor k_codes, Tensor v_codes, Tensor(a!) cache, Tensor slot_mapping, int num_kv_heads, "
           "Tensor k_ranks, Tensor k_offsets, Tensor k_nouts, int k_width, int v_rank, int row_bytes) -> ()");
     m.def("write_codes(Tensor key, Tensor value, Tensor(a!) kv_cache, Tensor slot_mapping) -> ()");

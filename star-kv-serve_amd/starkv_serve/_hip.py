@@ -19,7 +19,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstarkv_hip.so")
 OPS_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstarkv_torch.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 F32, F16, BF16 = 0, 1, 2
 CACHE_Q3_2 = 16  # cache kind of the 3.2-bit QuantRow cache
@@ -68,6 +68,13 @@ SIGNATURES = {
     "starkv_quant_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _P, _I64, _I64, _P, _I, _I, _I,
                                  _I, _I, _I, _P, _I64, _I, _P, _P, _P, _P, _I64, _I64, _I, _P, _I64, _I, _F,
                                  _P, _I64, _I64, _I, _P, _SZ, _I]),
+    "starkv_quant_decode_group": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _P, _I64, _I64, _P, _I, _I,
+                                       _I, _I, _I, _I, _P, _I64, _I, _P, _P, _P, _P, _I64, _I64, _I, _P, _I64, _I,
+                                       _F, _P, _I64, _I64, _I, _P, _SZ, _I, _I, _I, _I, _I]),
+    "starkv_quant_group_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _I]),
+    "starkv_quant_group_two_pass": (_I, [_I, _I, _I, _I, _I, _I, _I]),
+    "starkv_decode_layer_groups": (_I, [_I, _I, _I, ctypes.POINTER(ctypes.c_int32), _I,
+                                        ctypes.POINTER(ctypes.c_int32), _I]),
 }
 
 _LIB = None
@@ -135,6 +142,21 @@ def layer_fits(cache_kind: int, num_heads: int, num_kv_heads: int, k_ranks, v_ra
     """Whether the decode takes a layer of this shape (host-side; k_ranks a list of ints)."""
     arr = (ctypes.c_int32 * len(k_ranks))(*[int(r) for r in k_ranks])
     return bool(lib().starkv_decode_layer_fits(int(cache_kind), int(num_heads), int(num_kv_heads), arr, int(v_rank)))
+
+
+def layer_groups(cache_kind: int, num_heads: int, num_kv_heads: int, k_ranks, v_rank: int) -> list:
+    """KV-head ranges ``[(g0, g1), ...]``, one decode call each (``starkv_decode_layer_groups``;
+    host-side, k_ranks a list of ints); an empty list when some single KV head does not fit
+    one call."""
+    ranks = [int(r) for r in k_ranks]
+    arr = (ctypes.c_int32 * max(len(ranks), 1))(*ranks)
+    cap = max(len(ranks), 1)
+    out = (ctypes.c_int32 * (2 * cap))()
+    k = lib().starkv_decode_layer_groups(int(cache_kind), int(num_heads), int(num_kv_heads), arr, int(v_rank), out,
+                                         cap)
+    if k < 0:
+        check(1, "decode_layer_groups")
+    return [(out[2 * i], out[2 * i + 1]) for i in range(k)]
 
 
 decode_path_epoch = 0  # bumped by set_decode_path: host caches of the decode form key on it

@@ -11,10 +11,10 @@ errors, the same ``to_device`` attributes and the same ``forward`` contract:
 - ``write_from_hidden`` is the fused route for the codes' own GEMM (model.py:71 + the
   write): one ``write_kv`` call from the layer's hidden states.
 - Prefill is dense, as in the reference (attention.py:219-251): this step's codes are
-  lifted back to K (RoPE applied) and V, and every prompt attends causally to itself
-  through torch's fused attention (flash or memory-efficient kernels only, never the
-  unfused math path). It is the one part of the layer that is not a kernel of this
-  library.
+  lifted back to K (RoPE applied) and V in float32 (torch GEMMs), rounded once to fp16,
+  and every prompt attends causally to itself on this library's prefill kernel
+  (``prefill_attention``, MFMA flash attention; the reference hands bf16 K / V to
+  FlashAttention).
 
 vLLM is not needed to import or run this module. The two values the reference reads
 from vLLM are taken from it when it is importable, else from arguments:
@@ -179,6 +179,7 @@ class StarKVAttentionImpl:
         self.v_up_by_q = ops.v_up_by_q
         self.kv_down = ops.kv_down
         self.row = ops.row
+        self.kv_groups = ops.kv_groups
         if self.row is not None:
             self.k_nouts, self.head_of_lane, self.k_tiles = ops.k_nouts, ops.head_of_lane, ops.k_tiles
         # Prefill lifts every KV head in one batched product, which needs one width: the
@@ -314,10 +315,12 @@ class StarKVAttentionImpl:
         # The kernels write `out` in its own dtype and strides (no copy of the result).
         if self.row is None:
             paged_starkv_decode(q, cache, md.block_table[:nd], seq_lens, span, self.k_up, self.k_ranks,
-                                self.k_head_offsets, self.k_width, self.v_up_by_q, cs, self.scale, out=out)
+                                self.k_head_offsets, self.k_width, self.v_up_by_q, cs, self.scale, out=out,
+                                kv_groups=self.kv_groups)
         else:
             paged_quant_decode(q, cache, md.block_table[:nd], seq_lens, span, self.row, self.k_up,
-                               self.head_of_lane, self.k_tiles, self.v_up_by_q, cs, self.scale, out=out)
+                               self.head_of_lane, self.k_tiles, self.v_up_by_q, cs, self.scale, out=out,
+                               kv_groups=self.kv_groups)
 
 
 if _HAVE_VLLM:  # pragma: no cover - vLLM is not installed in this image

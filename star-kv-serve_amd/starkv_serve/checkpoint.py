@@ -188,6 +188,7 @@ class LayerOperands:
     k_nouts: Optional[torch.Tensor] = None
     head_of_lane: Optional[torch.Tensor] = None
     k_tiles: Optional[tuple] = None
+    kv_groups: Optional[list] = None  # KV-head ranges, one decode call each (kv_head_groups)
 
 
 def layer_operands(w: StarKVLayerWeights, num_heads: int, device, dtype: torch.dtype) -> LayerOperands:
@@ -196,19 +197,19 @@ def layer_operands(w: StarKVLayerWeights, num_heads: int, device, dtype: torch.d
     H = w.k_head_ranks.numel()
     if num_heads % H:
         raise ValueError(f"{num_heads} query heads for {H} KV heads")
-    # Refuse at load time a layer the decode kernels cannot run (rather than NaN rows
-    # at serving time): the test the library applies (starkv_decode_layer_fits). A bf16/fp16
-    # layer beyond one call runs as KV-head groups (kv_head_groups raises when a single KV
-    # head does not fit). A 3.2-bit GQA layer is refused by StarKVAttentionImpl itself, as
-    # the reference does (attention.py:116-117).
+    # How the decode runs the layer, decided once here with the library's own rule
+    # (starkv_decode_layer_groups): one call, or one call per range of consecutive KV heads
+    # when the layer exceeds one call's heads, rank tiles or wave plan. A layer where a
+    # single KV head does not fit one call is refused here (NotImplementedError), not at
+    # serving time. The library must be built: these operands exist to be handed to it.
+    # A 3.2-bit GQA layer is refused by StarKVAttentionImpl itself, as the reference does
+    # (attention.py:116-117).
     ranks = w.k_head_ranks.tolist()
+    groups = None
     if not w.kv_quant:
-        kv_head_groups(_hip.BF16, num_heads, ranks, w.v_rank)
-    elif num_heads == H and not _hip.layer_fits(_hip.CACHE_Q3_2, num_heads, H, ranks, w.v_rank):
-        raise NotImplementedError(
-            f"STAR-KV HIP decode: 3.2-bit layer with {num_heads} heads over K ranks {ranks} and "
-            f"V rank {w.v_rank} does not fit the decode kernels (at most 32 heads, 96 rank tiles of 16, "
-            f"16 tiles per decode wave after whole-head balancing)")
+        groups = kv_head_groups(_hip.BF16, num_heads, ranks, w.v_rank)
+    elif num_heads == H:
+        groups = kv_head_groups(_hip.CACHE_Q3_2, num_heads, ranks, w.v_rank)
     Hd = w.k_up.shape[1]
     v_up = w.v_up.to(device=device, dtype=dtype)
     v_up_by_q = (v_up.view(H, Hd, w.v_rank).repeat_interleave(num_heads // H, dim=0)
@@ -217,7 +218,7 @@ def layer_operands(w: StarKVLayerWeights, num_heads: int, device, dtype: torch.d
                         k_width=w.k_width, k_up=w.k_up.to(device=device, dtype=dtype).contiguous(),
                         v_up_by_q=v_up_by_q,
                         kv_down=torch.cat([w.k_down, w.v_down]).to(device=device, dtype=dtype).contiguous(),
-                        v_rank=w.v_rank)
+                        v_rank=w.v_rank, kv_groups=groups)
     if w.kv_quant:
         ops.row = QuantRow(w.k_width, H, w.v_rank)
         ops.k_nouts, ops.head_of_lane, ops.k_tiles = k_tables(w.k_head_ranks.tolist(), device)

@@ -87,6 +87,14 @@ def _as_i32(t: torch.Tensor) -> torch.Tensor:
     return (t if t.dtype == torch.int32 else t.to(torch.int32)).contiguous()
 
 
+def _rows_for(two: bool, num_heads: int, max_seq_len: int) -> int:
+    rows = MAX_REQUESTS_PER_LAUNCH
+    if two:
+        lcap = (int(max_seq_len) + 15) // 16 * 16
+        rows = max(1, min(rows, MAX_LOGITS_PER_LAUNCH // (num_heads * lcap)))
+    return rows
+
+
 def rows_per_launch(cache_kind: int, num_heads: int, k_width: int, v_rank: int, max_seq_len: int) -> int:
     """Requests per library call: at most 1024, and for two-pass decodes at most
     MAX_LOGITS_PER_LAUNCH logits."""
@@ -94,11 +102,7 @@ def rows_per_launch(cache_kind: int, num_heads: int, k_width: int, v_rank: int, 
     two = _two_pass.get(key)
     if two is None:
         two = _two_pass[key] = bool(_hip.lib().starkv_decode_two_pass(cache_kind, num_heads, k_width, v_rank))
-    rows = MAX_REQUESTS_PER_LAUNCH
-    if two:
-        lcap = (int(max_seq_len) + 15) // 16 * 16
-        rows = max(1, min(rows, MAX_LOGITS_PER_LAUNCH // (num_heads * lcap)))
-    return rows
+    return _rows_for(two, num_heads, max_seq_len)
 
 
 _two_pass = {}  # (cache kind, H, k_width, v_rank, path epoch) -> which decode form the library picks
@@ -107,32 +111,22 @@ _two_pass = {}  # (cache kind, H, k_width, v_rank, path epoch) -> which decode f
 def kv_head_groups(cache_kind: int, num_heads: int, k_ranks, v_rank: int) -> list:
     """KV-head ranges ``[(g0, g1), ...]`` decoded by one library call each: the whole layer
     when one call takes it, else greedy runs of consecutive KV heads, each as long as one
-    call takes it. Raises NotImplementedError when a single KV head does not fit (more than
-    32 query heads per KV head, or a rank above 1536 / heads per KV head)."""
+    call takes (``starkv_decode_layer_groups``, the library's own limits: 32 query heads,
+    96 rank tiles and a wave plan of at most 16 tiles per wave per call). Raises
+    NotImplementedError when a single KV head does not fit one call (more than 32 query
+    heads per KV head, or more rank tiles over its query heads than those limits allow)."""
     ranks = [int(r) for r in k_ranks]
-    hkv = len(ranks)
-    if _hip.layer_fits(cache_kind, num_heads, hkv, ranks, v_rank):
-        return [(0, hkv)]
-    per = num_heads // hkv
-    groups, g0 = [], 0
-    while g0 < hkv:
-        if not _hip.layer_fits(cache_kind, per, 1, ranks[g0:g0 + 1], v_rank):
-            raise NotImplementedError(f"STAR-KV HIP decode: KV head {g0} (rank {ranks[g0]}, {per} query heads, "
-                                      f"v_rank {v_rank}) does not fit one decode call")
-        g1 = g0 + 1
-        while g1 < hkv and _hip.layer_fits(cache_kind, per * (g1 + 1 - g0), g1 + 1 - g0, ranks[g0:g1 + 1], v_rank):
-            g1 += 1
-        groups.append((g0, g1))
-        g0 = g1
+    groups = _hip.layer_groups(cache_kind, num_heads, len(ranks), ranks, v_rank)
+    if not groups:
+        raise NotImplementedError(f"STAR-KV HIP decode: a KV head of this layer ({num_heads} query heads over K ranks "
+                                  f"{ranks}, v_rank {v_rank}) does not fit one decode call")
     return groups
 
 
-MAX_HEADS_PER_CALL = 32
-MAX_TILES_PER_CALL = 96
-
-# Host copies of device int tensors (KV-head ranks and offsets of a layer split into
-# groups), keyed like the cos/sin copies: the split needs them on the host, and reading
-# them once per layer keeps the decode free of host synchronisation afterwards.
+# Host copies of device int tensors (a layer's KV-head ranks and offsets, the 3.2-bit tile
+# table), keyed like the cos/sin copies: the head grouping needs them on the host, and
+# reading them once per tensor keeps the decode free of host synchronisation afterwards.
+# StarKVAttentionImpl computes its groups at load time and passes them in (kv_groups).
 _host_cache = {}  # id(tensor) -> (weak reference, its version, list of ints)
 _groups_cache = {}  # (kind, H, ranks, v_rank) -> kv_head_groups(...)
 
@@ -144,17 +138,16 @@ def _host_ints(t: torch.Tensor) -> list:
     hit = _host_cache.get(key)
     if hit is not None and hit[0]() is t and hit[1] == t._version:
         return hit[2]
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("STAR-KV HIP decode: the layer's head grouping is computed from its ranks on the host, "
+                           "which cannot happen during graph capture: pass kv_groups, or run one decode of the "
+                           "layer before capturing")
     vals = [int(x) for x in t.tolist()]
     _host_cache[key] = (weakref.ref(t, lambda r, k=key: _forget_in(_host_cache, k, r)), t._version, vals)
     return vals
 
 
-def _groups_for(kind, num_heads, num_kv_heads, k_width, k_ranks, v_rank):
-    # A layer within one call's heads and tiles runs as one call without reading its
-    # ranks on the host (the library reports a wave plan that does not fit as NaN rows).
-    if num_heads <= MAX_HEADS_PER_CALL and num_heads // num_kv_heads * (k_width // 16) <= MAX_TILES_PER_CALL:
-        return [(0, num_kv_heads)]
-    ranks = _host_ints(k_ranks)
+def _groups_for(kind, num_heads, ranks, v_rank):
     key = (kind, num_heads, tuple(ranks), v_rank)
     g = _groups_cache.get(key)
     if g is None:
@@ -178,13 +171,16 @@ def paged_starkv_decode(
     v_programs: int = TARGET_V_PROGRAMS,
     *,
     out: Optional[torch.Tensor] = None,
+    kv_groups: Optional[list] = None,
 ) -> torch.Tensor:
     """Attention output per query head, ``[n, H_q, head_dim]`` (paged_decode.py:150-226).
 
     ``v_programs`` is accepted for API compatibility; the split-K layout is chosen
-    by the library from the device and ``(n, max_seq_len)``. ``out`` (keyword only, not in
-    the reference's signature): a tensor of that shape, bf16 / fp16 / fp32, written in place
-    and returned (the attention layer hands over its output rows, saving a copy).
+    by the library from the device and ``(n, max_seq_len)``. Keyword-only extensions, not
+    in the reference's signature: ``out``, a tensor of that shape, bf16 / fp16 / fp32,
+    written in place and returned (the attention layer hands over its output rows, saving
+    a copy); ``kv_groups``, the layer's ``kv_head_groups`` computed once at load time (else
+    they are computed here from a host copy of ``k_ranks``, read once per tensor).
     """
     del v_programs
     n, num_heads, head_dim = query.shape
@@ -213,8 +209,8 @@ def paged_starkv_decode(
     kind = _hip.dtype_code(kv_cache)
     k_width, max_seq_len, scale = int(k_width), int(max_seq_len), float(scale)
     per = num_heads // num_kv_heads
-    groups = _groups_for(kind, num_heads, num_kv_heads, k_width, k_ranks, v_rank)
-    if len(groups) == 1:
+    groups = kv_groups if kv_groups is not None else _groups_for(kind, num_heads, _host_ints(k_ranks), v_rank)
+    if len(groups) == 1 and tuple(groups[0]) == (0, num_kv_heads):
         parts = [(query, out, kv_cache, k_up, _as_i32(k_ranks), _as_i32(k_head_offsets), v_up_by_q, num_heads,
                   num_kv_heads, k_width)]
     else:

@@ -21,7 +21,7 @@ from typing import Optional
 import torch
 
 from starkv_serve import _hip
-from starkv_serve.kernels.paged_decode import _as_i32, cos_sin_for_kernel, rows_per_launch
+from starkv_serve.kernels.paged_decode import _as_i32, _groups_for, _host_ints, _rows_for, cos_sin_for_kernel
 
 OUTLIER_RATIO = 0.2
 HADAMARD_SEED = 1234
@@ -182,13 +182,18 @@ def paged_quant_decode(
     target_v_programs: int = 2048,
     *,
     out: Optional[torch.Tensor] = None,
+    kv_groups: Optional[list] = None,
 ) -> torch.Tensor:
     """Attention output per query head, ``[n, H, 128]`` (paged_quant.py:357-411). MHA only.
 
     ``head_of_lane`` and ``target_v_programs`` are accepted for API compatibility; the
-    per-tile table ``k_tiles`` is what the kernel reads. ``out`` (keyword only, not in the
-    reference's signature): a tensor of that shape, bf16 / fp16 / fp32, written in place and
-    returned.
+    per-tile table ``k_tiles`` is what the kernel reads. Keyword-only extensions, not in the
+    reference's signature: ``out``, a tensor of that shape, bf16 / fp16 / fp32, written in
+    place and returned; ``kv_groups``, the layer's head ranges (``kv_head_groups`` over the
+    heads' K widths), computed once at load time; else they are computed here from a host
+    copy of the tile table, read once per tensor. A layer beyond one library call (more
+    than 32 heads or 96 rank tiles) runs as one call per head range, each reading its
+    heads' K nibbles and scales and the whole V block.
     """
     del head_of_lane, target_v_programs
     n, H, D = query.shape
@@ -210,9 +215,40 @@ def paged_quant_decode(
     k_tiles_n = row.k_width // 16
     assert th.numel() == k_tiles_n, "k_tiles must cover k_width / 16 tiles"
     max_seq_len, scale = int(max_seq_len), float(scale)
-    step = rows_per_launch(_hip.CACHE_Q3_2, H, row.k_width, row.v_rank, max_seq_len)
-    for s in range(0, n, step):
-        e = min(n, s + step)
-        ops.quant_decode(query[s:e], kv_cache, block_table[s:e], seq_lens[s:e], max_seq_len, row.k_width, row.v_rank,
-                         row.nbytes, k_up, th, tn, tl, v_up_by_q, cs, scale, out[s:e])
+    if kv_groups is None:
+        kv_groups = _groups_for(_hip.CACHE_Q3_2, H, head_widths(_host_ints(th), H), row.v_rank)
+    if len(kv_groups) == 1 and tuple(kv_groups[0]) == (0, H):
+        parts = [(0, H, 0, row.k_width)]
+    else:
+        widths = head_widths(_host_ints(th), H)
+        parts = [(h0, h1, sum(widths[:h0]), sum(widths[h0:h1])) for h0, h1 in kv_groups]
+    for h0, h1, lane0, kw in parts:
+        t0, t1 = lane0 // 16, (lane0 + kw) // 16
+        qg, og, kug, vug = query[:, h0:h1], out[:, h0:h1], k_up[lane0:lane0 + kw], v_up_by_q[h0:h1]
+        thg, tng, tlg = th[t0:t1], tn[t0:t1], tl[t0:t1]
+        step = _rows_for(bool(_quant_two_pass(row, h0, h1, lane0, kw)), h1 - h0, max_seq_len)
+        for s in range(0, n, step):
+            e = min(n, s + step)
+            ops.quant_decode(qg[s:e], kv_cache, block_table[s:e], seq_lens[s:e], max_seq_len, kw, row.v_rank,
+                             row.nbytes, kug, thg, tng, tlg, vug, cs, scale, og[s:e], row.k_width, H, h0, lane0)
     return out
+
+
+def head_widths(tile_head, num_heads: int) -> list:
+    """Per-head K widths (16 lanes per tile) from the per-tile head table."""
+    w = [0] * num_heads
+    for h in tile_head:
+        w[int(h)] += 16
+    return w
+
+
+_qtwo = {}  # (row, group, path epoch) -> whether the group's decode takes two passes
+
+
+def _quant_two_pass(row: QuantRow, h0: int, h1: int, lane0: int, kw: int) -> bool:
+    key = (row.k_width, row.num_kv_heads, row.v_rank, h0, h1, lane0, kw, _hip.decode_path_epoch)
+    two = _qtwo.get(key)
+    if two is None:
+        two = _qtwo[key] = bool(_hip.lib().starkv_quant_group_two_pass(row.k_width, row.num_kv_heads, row.v_rank, h0,
+                                                                       h1 - h0, lane0, kw))
+    return two

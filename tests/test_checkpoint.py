@@ -229,3 +229,131 @@ def test_side_tensors_normalised_to_contiguous_int32():
     assert out.dtype == torch.int32 and out.is_contiguous() and torch.equal(out, strided.to(torch.int32))
     same = torch.arange(5, dtype=torch.int32)
     assert _as_i32(same) is same
+
+
+def _plan_fits_restated(tiles):
+    """The decode's wave plan, restated: heads sorted by decreasing tiles (ties: lower
+    head first) dealt to 8 waves in snake order, then, while the most loaded wave (ties:
+    the higher index) is above ceil(total / 8), the head swap that lowers it the most
+    (smallest resulting maximum, then lowest head indices); fits if no wave holds more
+    than 16 tiles."""
+    Hq, TT = len(tiles), sum(tiles)
+    if not 1 <= Hq <= 32 or not 1 <= TT <= 96:
+        return False
+    order = sorted(range(Hq), key=lambda h: (-tiles[h], h))
+    size = [tiles[h] for h in order]
+    wave = [(p % 8) if (p // 8) % 2 == 0 else 7 - p % 8 for p in range(Hq)]
+    load = [0] * 8
+    for p in range(Hq):
+        load[wave[p]] += size[p]
+    target = (TT + 7) // 8
+    for _ in range(64):
+        A = max(range(8), key=lambda w: (load[w], w))
+        if load[A] <= target:
+            break
+        best = None
+        for a in range(Hq):
+            if wave[a] != A:
+                continue
+            for b in range(Hq):
+                if wave[b] == A:
+                    continue
+                d, lb = size[a] - size[b], load[wave[b]]
+                if d > 0 and lb + d < load[A]:
+                    cand = (max(load[A] - d, lb + d), a, b)
+                    best = cand if best is None or cand < best else best
+        if best is None:
+            break
+        _, a, b = best
+        B, d = wave[b], size[a] - size[b]
+        wave[a], wave[b] = B, A
+        load[A] -= d
+        load[B] += d
+    return max(load) <= 16
+
+
+def test_wave_plan_rule_matches_its_restatement():
+    """starkv_decode_layer_fits (bf16, narrow V: only the plan and the caps decide) against
+    an independent restatement of the wave plan, over random head-rank mixes around the
+    limits, and the shape a too-simple tile count would accept (95 tiles, nine heads of 8)."""
+    from starkv_serve import _hip
+    g = torch.Generator().manual_seed(11)
+    cases = [[128] * 9 + [16] * 23, [128] * 8 + [16] * 32, [256, 16, 100, 20], [192] * 8 + [16]]
+    for _ in range(300):
+        Hh = int(torch.randint(1, 33, (1,), generator=g))
+        top = int(torch.randint(2, 17, (1,), generator=g))
+        cases.append([16 * int(t) for t in torch.randint(1, top + 1, (Hh,), generator=g)])
+    agree = 0
+    for ranks in cases:
+        want = _plan_fits_restated([(r + 15) // 16 for r in ranks])
+        got = _hip.layer_fits(_hip.BF16, len(ranks), len(ranks), ranks, 64)
+        assert got == want, ranks
+        agree += got
+    assert not _plan_fits_restated([8] * 9 + [1] * 23)
+    assert 0 < agree < len(cases)  # both outcomes occur
+
+
+@pytest.mark.parametrize("quant,H,ranks,v_rank,want", [
+    (True, 32, [16, 32, 48, 64] * 8, 64, [(0, 32)]),
+    (True, 32, [32] * 23 + [16] * 9, 1290, [(0, 32)]),             # the 0.75-ratio layer: one call
+    (True, 32, [64] * 32, 64, [(0, 24), (24, 32)]),                # W 2048: 128 tiles
+    (True, 32, [64] * 16 + [48] * 16, 1290, [(0, 26), (26, 32)]),  # W 1792, two-pass: 64 + 30 tiles
+    (True, 40, [16, 32, 48, 64] * 10, 64, [(0, 32), (32, 40)]),    # 40 heads
+    (True, 32, [128] * 9 + [16] * 23, 64, [(0, 23), (23, 32)]),    # 95 tiles, plan does not fit
+    (False, 32, [128] * 9 + [16] * 23, 64, [(0, 23), (23, 32)]),
+    (True, 64, [64] * 64, 1290, [(0, 24), (24, 48), (48, 64)]),
+])
+def test_head_groups_known_answers(quant, H, ranks, v_rank, want):
+    """starkv_decode_layer_groups: greedy consecutive ranges, one call each; a layer that
+    fits one call is one range, and the whole-layer check agrees."""
+    from starkv_serve import _hip
+    from starkv_serve.kernels.paged_decode import kv_head_groups
+    kind = _hip.CACHE_Q3_2 if quant else _hip.BF16
+    g = kv_head_groups(kind, H, ranks, v_rank)
+    assert g == want
+    assert g[0][0] == 0 and g[-1][1] == len(ranks) and all(a[1] == b[0] for a, b in zip(g, g[1:]))
+    assert _hip.layer_fits(kind, H, len(ranks), ranks, v_rank) == (g == [(0, len(ranks))])
+
+
+def test_quant_group_geometry_matches_whole_layer_queries():
+    """The 3.2-bit group entry points, over the whole layer, size the workspace and pick the
+    decode form exactly as the whole-layer queries do."""
+    from starkv_serve import _hip
+    L = _hip.lib()
+    for H_, W, rv in [(32, 1232, 64), (32, 880, 1290), (8, 512, 256), (4, 400, 32)]:
+        for n, span, grid in [(64, 8192, 256), (1, 16448, 256), (3, 100, 7)]:
+            assert (L.starkv_quant_group_workspace_bytes(n, W, H_, rv, 0, H_, 0, W, span, grid) ==
+                    L.starkv_decode_workspace_bytes(_hip.CACHE_Q3_2, n, H_, H_, W, rv, span, grid))
+        assert (L.starkv_quant_group_two_pass(W, H_, rv, 0, H_, 0, W) ==
+                L.starkv_decode_two_pass(_hip.CACHE_Q3_2, H_, W, rv))
+    # a group past the layer's heads or lanes, or a lane offset that is not a tile, is refused
+    assert L.starkv_quant_group_workspace_bytes(1, 1232, 32, 64, 30, 4, 0, 64, 100, 1) == 0
+    assert L.starkv_quant_group_workspace_bytes(1, 1232, 32, 64, 0, 4, 8, 64, 100, 1) == 0
+    assert L.starkv_quant_group_workspace_bytes(1, 1232, 32, 64, 0, 4, 1200, 64, 100, 1) == 0
+
+
+@pytest.mark.parametrize("quant", [False, True])
+def test_decode_uses_the_load_time_groups(tmp_path, quant):
+    """The groups the decode wrappers compute from host ranks equal the ones layer_operands
+    stores at load time, for a layer whose 95 tiles pass the tile cap but not the wave plan
+    (one call over it would return NaN rows); a 40-head 3.2-bit layer now loads as two
+    groups."""
+    from starkv_serve import _hip
+    from starkv_serve.kernels import paged_decode as pd
+    from starkv_serve.kernels import paged_quant as pq
+    ranks = [128] * 9 + [16] * 23
+    path = str(tmp_path / "plan.pt")
+    ck.write_fused_checkpoint(path, 1, 32, HD, 64, {0: (ranks, 64)}, seed=3)
+    layer = ck.load_fused_checkpoint(path, 1, 32, HD, dtype=torch.bfloat16, kv_quant=quant).layers[0]
+    ops = ck.layer_operands(layer, 32, torch.device("cpu"), torch.bfloat16)
+    kind = _hip.CACHE_Q3_2 if quant else _hip.BF16
+    assert ops.kv_groups == [(0, 23), (23, 32)]
+    assert pd._groups_for(kind, 32, pd._host_ints(ops.k_ranks), 64) == ops.kv_groups
+    if quant:
+        widths = pq.head_widths(pd._host_ints(ops.k_tiles[0]), 32)
+        assert widths == [128] * 9 + [16] * 23
+        assert pd._groups_for(kind, 32, widths, 64) == ops.kv_groups
+        path40 = str(tmp_path / "h40.pt")
+        ck.write_fused_checkpoint(path40, 1, 40, HD, 64, {0: ([16, 32, 48, 64] * 10, 64)}, seed=4)
+        l40 = ck.load_fused_checkpoint(path40, 1, 40, HD, dtype=torch.bfloat16, kv_quant=True).layers[0]
+        assert ck.layer_operands(l40, 40, torch.device("cpu"), torch.bfloat16).kv_groups == [(0, 32), (32, 40)]

@@ -102,6 +102,9 @@ LOWRANK_CASES = {
     "groups_mha_h48": ([200, 33, 5], dict(num_heads=48)),
     "groups_mha_h48_strided": ([120, 16], dict(num_heads=48, col_pad=40)),
     "groups_mha_h64_two_pass": ([150, 17], dict(num_heads=64, ranks=[32] * 40 + [16] * 24, v_rank=1280)),
+    # 95 rank tiles, but nine heads of 8 tiles cannot share 8 waves of 16 tiles: the wave
+    # plan splits the layer into groups (one call as a whole would return NaN rows)
+    "groups_plan_w1520": ([250, 31], dict(ranks=[128] * 9 + [16] * 23)),
 }
 
 
@@ -243,6 +246,14 @@ QUANT_CASES = {
     # V lane maps over 3 and 5 blocks of 64 (outlier columns padded to 4)
     "v_rank_128": ([300, 45], dict(v_rank=128)),
     "v_rank_256_h8": ([200, 31], dict(v_rank=256, num_heads=8)),
+    # beyond one call's 32 heads / 96 rank tiles / wave plan: head groups, each call
+    # reading its heads' K nibbles and scales and the whole V block
+    "groups_rank64_w2048": ([250, 31, 1], dict(ranks=[64] * 32)),
+    "groups_w1792_v1290": ([150, 17], dict(ranks=[64] * 16 + [48] * 16, v_rank=1290)),
+    "groups_h40": ([200, 33, 5], dict(num_heads=40)),
+    # a group whose first K nibble sits 8 bytes into a 16-byte granule
+    "groups_code_offset": ([120, 47], dict(ranks=[16] + [64] * 31)),
+    "groups_plan_w1520": ([250, 31], dict(ranks=[128] * 9 + [16] * 23)),
 }
 
 
