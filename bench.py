@@ -108,11 +108,12 @@ def time_decode(fn, steps, warmup):
         out[key] = statistics.median(t) if t else float("nan")
     # The same call captured once in a HIP graph and replayed `steps` times back to back
     # (how a serving engine runs uniform decode steps): no host work between the launches.
+    # The replays get the same warm-up as the eager calls: the capture leaves the GPU idle,
+    # and the clock transient that follows (above) would otherwise fall in the timed ones.
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         fn(0)
-    for _ in range(warmup):
-        g.replay()
+    warm_up(lambda i: g.replay(), warmup)
     start.record()
     for _ in range(steps):
         g.replay()

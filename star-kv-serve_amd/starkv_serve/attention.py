@@ -148,7 +148,7 @@ class StarKVAttentionImpl:
     def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: Optional[int] = None,
                  alibi_slopes=None, sliding_window=None, kv_cache_dtype: str = "auto", logits_soft_cap=None,
                  attn_type=DECODER, kv_sharing_target_layer_name=None, *, starkv_layer: StarKVLayerWeights,
-                 rotary_emb, max_model_len: Optional[int] = None):
+                 rotary_emb, max_model_len: Optional[int] = None, fused_write: bool = False):
         if alibi_slopes is not None or sliding_window is not None or logits_soft_cap:
             raise NotImplementedError("STAR-KV attention: no alibi, sliding window or softcap")
         if _attn_type_name(attn_type) != DECODER or kv_sharing_target_layer_name is not None:
@@ -164,6 +164,9 @@ class StarKVAttentionImpl:
         self.kv_cache_dtype = kv_cache_dtype
         self.w = starkv_layer
         self.rotary_emb = rotary_emb
+        # fused_write: `forward` receives the layer's input as `key` (value unused) and
+        # writes the cache row from it (forward_from_hidden).
+        self.fused_write = fused_write
         vllm_len = _vllm_max_model_len()
         self.max_model_len = vllm_len if vllm_len is not None else max_model_len
         if self.max_model_len is None:
@@ -211,6 +214,8 @@ class StarKVAttentionImpl:
         defaults to vLLM's forward context (False without vLLM)."""
         if output_scale is not None or output_block_scale is not None:
             raise NotImplementedError("STAR-KV attention: fused output quantization")
+        if self.fused_write:
+            return self.forward_from_hidden(query, key, kv_cache, attn_metadata, output, in_full_graph)
         if attn_metadata is None:  # profiling run
             return output.fill_(0)
         md = attn_metadata
@@ -368,11 +373,16 @@ if _HAVE_VLLM:  # pragma: no cover - vLLM is not installed in this image
         """An ``Attention`` whose K and V inputs are STAR-KV codes (attention.py:271-316)."""
 
         def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int,
-                     starkv_layer: StarKVLayerWeights, rotary_emb, qkv_proj, cache_config=None, prefix: str = ""):
+                     starkv_layer: StarKVLayerWeights, rotary_emb, qkv_proj=None, cache_config=None, prefix: str = "",
+                     fused_write: bool = False):
+            """`qkv_proj`: a stacked QKV projection whose K/V rows are dropped after loading
+            (the codes replace them), or None for a Q-only layer. `fused_write`: `key` is the
+            layer's input and the write forms the codes (forward_from_hidden)."""
             super().__init__(num_heads, head_size, scale, num_kv_heads=num_kv_heads, cache_config=cache_config,
                              prefix=prefix, attn_backend=StarKVAttentionBackend, starkv_layer=starkv_layer,
-                             rotary_emb=rotary_emb)
+                             rotary_emb=rotary_emb, fused_write=fused_write)
             self.starkv_layer = starkv_layer
+            self.fused_write = fused_write
             self._qkv_proj = (qkv_proj,)  # not registered a second time as a child module
 
         def get_kv_cache_spec(self, vllm_config) -> FullAttentionSpec:
@@ -385,6 +395,8 @@ if _HAVE_VLLM:  # pragma: no cover - vLLM is not installed in this image
         def forward(self, query, key, value, output_shape=None, output_dtype=None):
             output = torch.empty((query.shape[0], self.num_heads * self.head_size), dtype=output_dtype or query.dtype,
                                  device=query.device)
+            if value is None:  # fused write: key is the layer's input, value is not read
+                value = key.new_empty(0)
             if self.use_direct_call:
                 unified_attention_with_output(query, key, value, output, self.layer_name)
             else:
@@ -396,6 +408,6 @@ if _HAVE_VLLM:  # pragma: no cover - vLLM is not installed in this image
             super().process_weights_after_loading(act_dtype)
             qkv = self._qkv_proj[0]
             q_size = self.num_heads * self.head_size
-            if qkv.weight.shape[0] != q_size:  # the K/V rows are dead: the codes come from kv_down
+            if qkv is not None and qkv.weight.shape[0] != q_size:  # the K/V rows are dead: the codes come from kv_down
                 qkv.weight = torch.nn.Parameter(qkv.weight.data[:q_size].contiguous(), requires_grad=False)
             self.impl.to_device(qkv.weight.device, act_dtype)

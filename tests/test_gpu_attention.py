@@ -40,10 +40,13 @@ LENGTHS = [300, 77, 16, 1]  # after this step
 PAD = 2                     # graph-padding rows
 
 
-@pytest.mark.parametrize("quant,num_heads,in_graph", [(False, 16, False), (False, 16, True), (True, 8, False),
-                                                      (True, 8, True)])
-def test_forward_decode_step(cuda, tmp_path, quant, num_heads, in_graph):
-    print(f"\n[attention forward] quant={quant} heads={num_heads} in_graph={in_graph}", flush=True)
+@pytest.mark.parametrize("quant,num_heads,in_graph,fused", [(False, 16, False, False), (False, 16, True, False),
+                                                            (True, 8, False, False), (True, 8, True, False),
+                                                            (False, 16, False, True), (True, 8, True, True)])
+def test_forward_decode_step(cuda, tmp_path, quant, num_heads, in_graph, fused):
+    """`fused`: the layer is built with fused_write (the vLLM model's compressed layers):
+    forward receives the layer's input as key and the write kernel forms the codes."""
+    print(f"\n[attention forward] quant={quant} heads={num_heads} in_graph={in_graph} fused={fused}", flush=True)
     path = str(tmp_path / "fused_weights.pt")
     ck.write_fused_checkpoint(path, 1, len(RANKS), 128, HIDDEN, {0: (RANKS, V_RANK)}, seed=21)
     w = ck.load_fused_checkpoint(path, 1, len(RANKS), 128, dtype=torch.bfloat16, kv_quant=quant).layers[0]
@@ -52,7 +55,7 @@ def test_forward_decode_step(cuda, tmp_path, quant, num_heads, in_graph):
     cs = W.cos_sin_table(MAX_MODEL_LEN, torch.bfloat16, cuda)
     rope = types.SimpleNamespace(cos_sin_cache=cs)
     impl = StarKVAttentionImpl(num_heads, 128, 128 ** -0.5, len(RANKS), starkv_layer=w, rotary_emb=rope,
-                               max_model_len=MAX_MODEL_LEN)
+                               max_model_len=MAX_MODEL_LEN, fused_write=fused)
     impl.to_device(cuda, torch.bfloat16)
 
     bt, nblk = W._page_layout(LENGTHS, g)
@@ -84,7 +87,10 @@ def test_forward_decode_step(cuda, tmp_path, quant, num_heads, in_graph):
                         slot_mapping=slot_mapping)
     output = torch.full((n + PAD + 3, num_heads * 128), 7.0, dtype=torch.bfloat16, device=cuda)
     null_before = kv_cache[0].clone()
-    impl.forward(None, query, key, value, kv_cache, md, output, in_full_graph=in_graph)
+    if fused:
+        impl.forward(None, query, hidden, hidden.new_empty(0), kv_cache, md, output, in_full_graph=in_graph)
+    else:
+        impl.forward(None, query, key, value, kv_cache, md, output, in_full_graph=in_graph)
     torch.cuda.synchronize()
 
     assert torch.all(output[n + PAD:] == 7.0)
@@ -105,7 +111,7 @@ def test_forward_decode_step(cuda, tmp_path, quant, num_heads, in_graph):
         truth = ref.lowrank_decode(q, cache.float().cpu().numpy(), bt.numpy(), np.array(LENGTHS), max(LENGTHS),
                                    impl.k_up.float().cpu().numpy(), RANKS, w.k_head_offsets.tolist(), impl.k_width,
                                    impl.v_up_by_q.float().cpu().numpy(), cs.float().cpu().numpy(), impl.scale)
-    assert_close(out[:n], truth, f"forward quant={quant} in_graph={in_graph}")
+    assert_close(out[:n], truth, f"forward quant={quant} in_graph={in_graph} fused={fused}")
 
 
 @pytest.mark.parametrize("quant,num_heads", [(False, 16), (True, 8)])
