@@ -67,7 +67,14 @@ struct PrepArgs {
     float sc;  // scale * log2(e)
     uint8_t* ws; size_t ws_plan, ws_ab;
     int tile_pairs;  // ceil(TT / 2): fold workgroups per group of PREP_REQ requests
+    int fold_wgs;    // fold workgroups (after workgroups 0 and 1); the page-record ones follow
+    // Page records (PageRec, one per page of every request) for the decode launches.
+    PageRec* pages;
+    const uint8_t* cache; int64_t c_s0, c_s1;  // bytes
+    int bs_shift;
+    const int32_t* bt; int64_t bt_s0, bt_s1;
 };
+constexpr int PREP_RECS = 4 * PREP_THR;  // page records per record workgroup
 
 // Rank-tile table: per tile its query head, first k_up row, valid ranks (rows past them
 // fold to zero) and code word (slot_word's code tile | outlier ranks << 13); per query
@@ -162,18 +169,20 @@ __device__ __forceinline__ int wave_min_i(int v) {
     return min(min(r0, r1), min(r2, r3));
 }
 
-// Workgroup 0 of prep. Writes hdr[0] = tokens per decode workgroup (a multiple of 16;
-// the last workgroups may have none), hdr[1 + b] = first
-// token of request b in the concatenation (v: this thread's requests 4 tid .. 4 tid + 3).
-__device__ void prep_prefix(const PrepArgs& a, int tid, int (&v)[4]) {
+// The requests' page counts, min(max(seq_len, 0), max_seq_len) tokens in pages of 16, as
+// an inclusive prefix: s_pp[b + 1] = pages of requests 0 .. b, s_pp[0] = 0; s_len[b] the
+// clamped lengths. Every thread of the workgroup calls it (requests 4 tid .. 4 tid + 3);
+// it ends with a barrier.
+__device__ void page_prefix(const PrepArgs& a, int tid, int* s_pp, int* s_len) {
     __shared__ int s_wsum[PREP_THR / 64];
     const int lane = tid & 63, wave = tid >> 6;
-    int* hdr = (int*)a.ws;
-    // Prefix sums of min(max(seq_len, 0), max_seq_len).
-    int s = 0;
+    int v[4], s = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        v[i] = min(max(v[i], 0), a.max_seq_len);
+        const int b = 4 * tid + i;
+        const int L = b < a.n ? min(max(a.seq_lens[b], 0), a.max_seq_len) : 0;
+        if (b < a.n) s_len[b] = L;
+        v[i] = (L + TILE_TOK - 1) / TILE_TOK;
         s += v[i];
     }
     int incl = s;
@@ -190,12 +199,45 @@ __device__ void prep_prefix(const PrepArgs& a, int tid, int (&v)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         run += v[i];
-        if (4 * tid + i < a.n) hdr[2 + 4 * tid + i] = run;
+        if (4 * tid + i < a.n) s_pp[4 * tid + i + 1] = run;
     }
-    // Tokens per decode workgroup: a multiple of 16, so that a single request's ranges
-    // start on its pages (no page is copied by two workgroups).
-    if (tid == PREP_THR - 1) hdr[0] = ((run + a.grid - 1) / a.grid + TILE_TOK - 1) / TILE_TOK * TILE_TOK;
-    if (tid == 0) hdr[1] = 0;
+    if (tid == 0) s_pp[0] = 0;
+    __syncthreads();
+}
+
+// Workgroup 0 of prep: hdr[0] = pages per decode workgroup (the last workgroups may have
+// none), hdr[1 + b] = first page of request b in the concatenation, hdr[1 + n] = all pages.
+__device__ void prep_prefix(const PrepArgs& a, int tid, int* s_pp, int* s_len) {
+    page_prefix(a, tid, s_pp, s_len);
+    int* hdr = (int*)a.ws;
+    for (int b = tid; b <= a.n; b += PREP_THR) hdr[1 + b] = s_pp[b];
+    if (tid == 0) hdr[0] = (s_pp[a.n] + a.grid - 1) / a.grid;
+}
+
+// Record workgroup w of prep: the records of pages w PREP_RECS .. (w + 1) PREP_RECS - 1
+// (those that exist), thread tid taking pages w PREP_RECS + tid + PREP_THR i.
+__device__ void prep_records(const PrepArgs& a, int tid, int w, int* s_pp, int* s_len) {
+    page_prefix(a, tid, s_pp, s_len);
+    const int total = s_pp[a.n];
+    const int mask = (1 << a.bs_shift) - 1;
+#pragma unroll
+    for (int i = 0; i < PREP_RECS / PREP_THR; ++i) {
+        const int gp = w * PREP_RECS + tid + PREP_THR * i;
+        if (gp >= total) break;
+        int lo = 0, hi = a.n - 1;  // the request of page gp: the largest b with s_pp[b] <= gp
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s_pp[mid] <= gp) lo = mid; else hi = mid - 1;
+        }
+        const int b = lo, k = gp - s_pp[b], L = s_len[b];
+        const int blk = a.bt[(int64_t)b * a.bt_s0 + (int64_t)(k >> a.bs_shift) * a.bt_s1];
+        PageRec r;
+        r.addr = (uint64_t)(uintptr_t)a.cache + (uint64_t)((int64_t)blk * a.c_s0 +
+                                                           (int64_t)((k & mask) * TILE_TOK) * a.c_s1);
+        r.k = k;
+        r.bits = pr_bits(b, min(TILE_TOK, L - TILE_TOK * k), TILE_TOK * (k + 1) >= L);
+        a.pages[gp] = r;
+    }
 }
 
 // Workgroup 1 of prep: the wave plan. Per wave (PLAN_STRIDE ints) [0] its tiles, [1] its
@@ -428,12 +470,14 @@ __device__ void prep_fold_q(const PrepArgs& a, const TileTable& tt, int tid, int
 
 __global__ __launch_bounds__(PREP_THR) void prep_kernel(PrepArgs a) {
     __shared__ TileTable tt;
+    __shared__ int s_pp[MAX_REQ_PER_CALL + 1], s_len[MAX_REQ_PER_CALL];
     const int tid = threadIdx.x;
     if (blockIdx.x == 0) {
-        int v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = 4 * tid + i < a.n ? a.seq_lens[4 * tid + i] : 0;
-        prep_prefix(a, tid, v);
+        prep_prefix(a, tid, s_pp, s_len);
+        return;
+    }
+    if ((int)blockIdx.x >= 2 + a.fold_wgs) {
+        prep_records(a, tid, blockIdx.x - 2 - a.fold_wgs, s_pp, s_len);
         return;
     }
     tile_table(a, tt, tid);
@@ -899,7 +943,8 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     const bool two = use_two_pass(fmt, p.k_width, a.v_rank, row_bytes, p.v_nout);
     const int lcap = two ? lcap_of(a.max_seq_len) : 0;
     const int pv_r = two ? pv_ratio(fmt, a.n, a.max_seq_len, a.grid) : 1;
-    const WsLayout wl = ws_layout(a.n, a.Hq, TT, a.v_rank, a.grid, lcap, pv_r);
+    SKV_CHECK(a.max_seq_len <= (1 << 24), "decode: max_seq_len %d > 2^24", a.max_seq_len);
+    const WsLayout wl = ws_layout(a.n, a.Hq, TT, a.v_rank, a.grid, lcap, pv_r, pages_of(a.max_seq_len));
     SKV_CHECK(a.ws_bytes >= wl.total, "decode: workspace %zu bytes < %zu needed", a.ws_bytes, wl.total);
     SKV_CHECK(((uintptr_t)a.ws % 256) == 0, "decode: workspace must be 256-byte aligned");
     SKV_CHECK(p.bs_shift >= 0, "decode: block_size must be 16 times a power of two");
@@ -973,6 +1018,7 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     p.ws_lg = wl.lg; p.lcap = lcap;
     p.ws_o = wl.o; p.acc_ld = wl.ld;
     p.pv_r = pv_r;
+    p.ws_pages = wl.pages;
 
     const bool timed = g_prof.on && 2 * g_prof.used + 1 < (int)g_prof.ev.size();
     if (timed && g_prof.mode == 1) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
@@ -987,7 +1033,14 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     pa.sc = a.scale * LOG2E;
     pa.ws = p.ws; pa.ws_plan = wl.plan; pa.ws_ab = wl.ab;
     pa.tile_pairs = (TT + 1) / 2;
-    const int prep_grid = 2 + pa.tile_pairs * ((a.n + PREP_REQ - 1) / PREP_REQ);
+    pa.fold_wgs = pa.tile_pairs * ((a.n + PREP_REQ - 1) / PREP_REQ);
+    pa.pages = (PageRec*)(p.ws + wl.pages);
+    pa.cache = p.cache; pa.c_s0 = p.c_s0; pa.c_s1 = p.c_s1; pa.bs_shift = p.bs_shift;
+    pa.bt = a.bt; pa.bt_s0 = a.bt_s0; pa.bt_s1 = a.bt_s1;
+    const int64_t rec_wgs = ((int64_t)a.n * pages_of(a.max_seq_len) + PREP_RECS - 1) / PREP_RECS;
+    SKV_CHECK(2 + pa.fold_wgs + rec_wgs < ((int64_t)1 << 31), "decode: %d requests x %d tokens", a.n,
+              a.max_seq_len);
+    const int prep_grid = 2 + pa.fold_wgs + (int)rec_wgs;
     hipLaunchKernelGGL(prep_kernel, dim3(prep_grid), dim3(PREP_THR), 0, stream, pa);
     SKV_HIP(hipGetLastError());
     if (timed && g_prof.mode == 0) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
@@ -1113,7 +1166,7 @@ size_t starkv_decode_workspace_bytes(int cache_kind, int n, int num_heads, int n
     }
     const bool two = use_two_pass(fmt, k_width, v_rank, row_bytes, v_nout);
     return ws_layout(n, num_heads, TT, v_rank, grid, two ? lcap_of(max_seq_len) : 0,
-                     two ? pv_ratio(fmt, n, max_seq_len, grid) : 1)
+                     two ? pv_ratio(fmt, n, max_seq_len, grid) : 1, pages_of(max_seq_len))
         .total;
 }
 
@@ -1317,7 +1370,7 @@ size_t starkv_quant_group_workspace_bytes(int n, int row_k_width, int row_num_he
     const QGroup g = qgroup(row_k_width, row_num_heads, v_rank, head0, num_heads, k_lane0);
     const bool two = qgroup_two_pass(g);
     return ws_layout(n, num_heads, k_width / 16, v_rank, grid, two ? lcap_of(max_seq_len) : 0,
-                     two ? pv_ratio(FMT_Q4, n, max_seq_len, grid) : 1)
+                     two ? pv_ratio(FMT_Q4, n, max_seq_len, grid) : 1, pages_of(max_seq_len))
         .total;
 }
 

@@ -1,6 +1,6 @@
 // Shared definitions of the paged decode launches (decode.hip, decode_lowrank.hip,
 // decode_quant.hip):
-// constants, the workspace layout, the kernel parameter block, the token cursor, the
+// constants, the workspace layout and page records, the kernel parameter block, the
 // global->LDS copy primitive and the per-partial flush.
 #pragma once
 
@@ -36,7 +36,10 @@ constexpr int CS_CHUNKS = 4;                // 16 rows x 16 granules -> 4 copies
 constexpr float LAZY_MAX = 8.f;             // log2 headroom before the running max moves
 
 // Workspace layout, in bytes from the base (every region 256-byte aligned):
-//   hdr    int   [2 + n]      S (tokens per workgroup), P[0..n] (prefix of clamped lengths)
+//   hdr    int   [2 + n]      S (pages per decode workgroup), P[0..n] (prefix of the
+//                             requests' page counts ceil(min(len, max_seq_len) / 16))
+//   pages  PageRec [n * ceil(max_seq_len / 16)]  one record per page, request after
+//                             request (page P[b] + k is page k of request b)
 //   plan   int   [8][80] + 1  per wave: [0] tiles, [1] heads, [2] heads with tiles,
 //                             [3] 1 if every head has <= 4 tiles, [8 + s] tile of slot s,
 //                             [32 + k] q head of local head k, [40 + k] its first slot,
@@ -74,20 +77,43 @@ __device__ __forceinline__ int sw_head(uint32_t w) { return (int)((w >> 23) & 3)
 __device__ __forceinline__ int sw_tile(uint32_t w) { return (int)(w >> 25); }
 
 struct WsLayout {
-    size_t hdr, plan, ab, m, l, acc, lg, o, total;
+    size_t hdr, pages, plan, ab, m, l, acc, lg, o, total;
     int ld;  // floats per acc / o row
 };
 
 static inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// lcap = 0: the one-pass decode (no logits buffer). pv_r: the P @ V pass's R.
-static WsLayout ws_layout(int n, int Hq, int TT, int v_rank, int grid, int lcap, int pv_r = 1) {
+// Page record: where a page's rows are and what the decode needs to know of it. The
+// decode launches split the pages (not the tokens) into equal contiguous ranges, one per
+// workgroup, and read one record per page with a scalar load: no token cursor, block
+// table lookup or address arithmetic beyond one 64-bit add in the page loop.
+//   addr  byte address of the page's first row (cache + block * c_s0 + slot * c_s1)
+//   k     page index inside the request (its tokens are 16 k .. 16 k + rows - 1)
+//   bits  request b (bits 0-10) | rows - 1 (bits 11-14) | 1 << 15 if the page is the
+//         request's last
+struct PageRec {
+    uint64_t addr;
+    int k;
+    uint32_t bits;
+};
+constexpr uint32_t PR_LAST = 1u << 15;
+__host__ __device__ constexpr uint32_t pr_bits(int b, int rows, bool last) {
+    return (uint32_t)b | ((uint32_t)(rows - 1) << 11) | (last ? PR_LAST : 0u);
+}
+__device__ __forceinline__ int pr_b(uint32_t bits) { return (int)(bits & 0x7FF); }
+__device__ __forceinline__ int pr_rows(uint32_t bits) { return (int)((bits >> 11) & 15) + 1; }
+static inline int pages_of(int max_seq_len) { return (max_seq_len + 15) / 16; }
+
+// lcap = 0: the one-pass decode (no logits buffer). pv_r: the P @ V pass's R. maxp: page
+// records per request (pages_of(max_seq_len)).
+static WsLayout ws_layout(int n, int Hq, int TT, int v_rank, int grid, int lcap, int pv_r, int maxp) {
     WsLayout w;
     const size_t gp = lcap > 0 ? ((size_t)grid + pv_r - 1) / pv_r : (size_t)grid;
     const size_t slots = (lcap > 0 ? std::max((size_t)grid, gp * pv_r) : (size_t)grid) + n;
     const size_t pslots = gp + n;
     size_t o = 0;
     w.hdr = o; o = al256(o + (size_t)(n + 2) * 4);
+    w.pages = o; o = al256(o + (size_t)n * (size_t)maxp * sizeof(PageRec));
     w.plan = o; o = al256(o + (size_t)(NWAVE * PLAN_STRIDE + 1) * 4);
     w.ab = o; o = al256(o + ((size_t)n * TT + AB_SLACK_TILES) * AB_TILE_BYTES);
     w.m = o; o = al256(o + slots * Hq * 4);
@@ -115,56 +141,12 @@ struct DecodeParams {
     size_t ws_lg; int lcap;                        // two-pass calls: logits buffer, row length
     size_t ws_o; int acc_ld;                       // two-pass calls: merged outputs; acc / o row floats
     int pv_r;                                      // two-pass calls: logits-pass ranges per P @ V range
+    size_t ws_pages;                               // page records
 };
 
 __device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// ---------------------------------------------------------------------------
-// Token cursor: which (request, page) a workgroup visits next. P (the prefix of
-// the clamped lengths) is read with scalar loads from the workspace header.
-// ---------------------------------------------------------------------------
 typedef const __attribute__((address_space(4))) int32_t* cint_p;
-
-struct Cursor {
-    int b, k, lo, hi, len;  // request, page, request-local token range [lo, hi) of this workgroup, length
-    bool valid;
-};
-
-__device__ __forceinline__ void cur_set(Cursor& c, cint_p P, int beg, int end) {
-    const int pb = P[c.b], pe = P[c.b + 1];
-    c.lo = max(beg, pb) - pb;
-    c.hi = min(end, pe) - pb;
-    c.len = pe - pb;
-    c.k = c.lo / TILE_TOK;
-}
-
-__device__ __forceinline__ void cur_first(Cursor& c, cint_p P, int n, int beg, int end) {
-    int lo = 0, hi = n - 1;  // largest b with P[b] <= beg; then P[b + 1] > beg
-    while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (P[mid] <= beg) lo = mid; else hi = mid - 1;
-    }
-    c.b = lo;
-    c.valid = beg < end;
-    if (c.valid) cur_set(c, P, beg, end);
-}
-
-// Returns true when the next page starts a new request (the current one ended).
-__device__ __forceinline__ bool cur_next(Cursor& c, cint_p P, int n, int beg, int end) {
-    if (TILE_TOK * (c.k + 1) < c.hi) {
-        ++c.k;
-        return false;
-    }
-    int b = c.b + 1;
-    while (b < n && P[b + 1] == P[b]) ++b;
-    if (b >= n || P[b] >= end) {
-        c.valid = false;
-        return true;
-    }
-    c.b = b;
-    cur_set(c, P, beg, end);
-    return true;
-}
 
 // ---------------------------------------------------------------------------
 // Global -> LDS copies: raw buffer loads with the LDS bit, 16 bytes per lane.

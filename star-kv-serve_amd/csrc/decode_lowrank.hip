@@ -1,8 +1,8 @@
 // bf16/fp16 low-rank paged decode: the decode launch of starkv_lowrank_decode
 // (decode.hip holds the setup, fold and merge launches and the host entry points).
 //
-// One persistent workgroup of 8 waves per CU walks its contiguous token range page by
-// page (16 tokens). Each wave owns whole query heads and holds their rank tiles of AB
+// One persistent workgroup of 8 waves per CU walks its contiguous range of pages (16
+// tokens each), one page record per page. Each wave owns whole query heads and holds their rank tiles of AB
 // (q folded into U) in VGPRs. Per page: z = AB . [cos|sin]^T on MFMA, the lanes fold z
 // with the codes, the wave's heads run an online softmax, and P @ V accumulates on MFMA.
 //
@@ -263,16 +263,15 @@ __device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const La
                                         const uint32_t (&doff)[NLD], int ntw, int nh, bool fast, uint32_t sp,
                                         uint32_t plo_off, uint32_t salpha, const int* sqh, int lane, int wave) {
     const DecodeParams& p = params();
-    cint_p P = (cint_p)(p.ws + 4);
-    if (!st.cc.valid) {
+    if (st.j >= st.end) {
         st.pv_buf = BN;  // the last page's buffer: its P @ V runs after the loop
         return false;
     }
-    const Cursor cc = st.cc;
-    if (st.new_seg) {
+    const int b = pr_b(st.rc.bits), k = st.rc.k, rows = pr_rows(st.rc.bits);
+    if (page_starts_seg(st)) {
         // This request's AB into registers; slots past the wave's tiles load tile 0.
         cint_p pw = (cint_p)(p.ws + p.ws_plan) + wave * PLAN_STRIDE;
-        const half8_t* abp = (const half8_t*)(p.ws + p.ws_ab + (size_t)cc.b * p.TT * AB_TILE_BYTES);
+        const half8_t* abp = (const half8_t*)(p.ws + p.ws_ab + (size_t)b * p.TT * AB_TILE_BYTES);
 #pragma unroll
         for (int i = 0; i < MTV; ++i) {
             const int t = pw[8 + i];
@@ -283,13 +282,16 @@ __device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const La
     }
     SKV_WAIT_VM_LGKM0(NBUF == 3 ? NLD : 0);  // only the copies of page j + 1 may still be in flight
     lds_barrier();  // page j is in LDS, page j - 1's V table is complete; every wave is done with page j - 1
-    const DmaPage dp = dma_setup(dc, st.ld, st.nblk);
+    const int jl = st.j + NBUF - 1;  // the page whose copies issue now
+    const DmaPage dp = dma_setup(dc, NBUF == 3 ? st.r2 : st.r1, jl < st.end);
+    // The record of the page the next iteration copies: it arrives under the next wait.
+    const PageRec next = jl + 1 < st.end ? page_rec(p, jl + 1) : st.rc;
     // Page j's V codes for the transpose, read first; page j - 1's P @ V (its P was 0
     // before the first page) runs inside the K side: its rescale first, then one step
     // per tile.
     uint32_t xv[NB > 0 ? NB : 1];
 #pragma unroll
-    for (int k = 0; k < NB; ++k) xv[k] = lds_ld<uint32_t>(la.cv_rd[k] + BC * 1024);
+    for (int q = 0; q < NB; ++q) xv[q] = lds_ld<uint32_t>(la.cv_rd[q] + BC * 1024);
     if (NB > 0 && st.pv_moved) {
         const f32x4_t al = lds_ld<f32x4_t>(salpha);
 #pragma unroll
@@ -298,7 +300,6 @@ __device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const La
             for (int e = 0; e < 4; ++e) acc[nb][e] *= al[e];
     }
     copies_at<LrSched<MTV>, NLD, BN, NBUF>(0, dc, dp, opaque_s(wave), doff);
-    if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
     PvStep<NB> pq;
     auto hook = [&](int i) {
         if constexpr (NB > 0) {
@@ -307,33 +308,26 @@ __device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const La
             if (i <= 3) pv_load<FMT, NB, BN, NBUF>(pq, la.pr, plo_off, la.vt, i);
         }
     };
-    k_side<FMT, MTV, NB, BC, NLD, BN, NBUF>(p, la, ab, ntw, nh, fast, sp, lane, wave, cc.b, dc, dp, doff, hook);
+    k_side<FMT, MTV, NB, BC, NLD, BN, NBUF>(p, la, ab, ntw, nh, fast, sp, lane, wave, b, dc, dp, doff, hook);
 #pragma unroll
     for (int i = MTV; i <= 4; ++i) hook(i);  // the P @ V steps a short K side left
     if constexpr (NB > 0) {
         if (st.pv_end) flush_partial<NB>(p, sm, acc, nh, st.pv_b + st.g, sqh, lane);
-        st.pv_moved = softmax_page<FMT>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, TILE_TOK * cc.k,
-                                        cc.lo, cc.hi);
+        st.pv_moved = softmax_page<FMT>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, 0, 0, rows);
     } else {
         // The logits pass: page j's logits into the request's rows, and its partial
         // (m, l) flushed right away when page j ends the request.
-        float* lgd = (float*)(p.ws + p.ws_lg) + ((int64_t)cc.b * (p.lcap / TILE_TOK) + cc.k) * p.Hq * TILE_TOK + la.lg;
-        softmax_page<FMT, true>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, TILE_TOK * cc.k, cc.lo,
-                                cc.hi, lgd);
+        float* lgd = (float*)(p.ws + p.ws_lg) + ((int64_t)b * (p.lcap / TILE_TOK) + k) * p.Hq * TILE_TOK + la.lg;
+        softmax_page<FMT, true>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, 0, 0, rows, lgd);
     }
     copies_at<LrSched<MTV>, NLD, BN, NBUF>(MTV + 1, dc, dp, opaque_s(wave), doff);
-    Cursor nx = cc;
-    const bool seg_end = cur_next(nx, P, p.n, st.beg, st.end);
+    const bool seg_end = page_ends_seg(st);
     if constexpr (NB == 0) {
-        if (seg_end) flush_partial<0>(p, sm, acc, nh, cc.b + st.g, sqh, lane);
+        if (seg_end) flush_partial<0>(p, sm, acc, nh, b + st.g, sqh, lane);
     }
     st.pv_end = seg_end;
-    st.pv_b = cc.b;
-    st.cc = nx;
-    st.new_seg = seg_end;
-    // The block of the page the next iteration copies: its load completes under the
-    // wait at the next page's barrier.
-    st.nblk = page_block(dc, st.ld);
+    st.pv_b = b;
+    page_loop_next<NBUF>(st, next);
     return true;
 }
 
@@ -350,7 +344,6 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     const DecodeParams& p = params();
     const int tid = threadIdx.x, lane = tid & 63, wave = rfl(tid >> 6);
     const int lg = lane >> 4, lr = lane & 15;
-    cint_p P = (cint_p)(p.ws + 4);
     cint_p plan = (cint_p)(p.ws + p.ws_plan);
     // Page buffers and partial-logit rows start zeroed: rows past a request's end are
     // never copied and must hold finite values (P is 0 there); a head's partial rows
@@ -364,12 +357,7 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     }
     if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
     LrLoop st;
-    st.g = xcd_range(blockIdx.x, gridDim.x);
-    const int S_tok = ((cint_p)p.ws)[0];
-    const int T = P[p.n];
-    st.beg = min(st.g * S_tok, T);
-    st.end = min(st.beg + S_tok, T);
-    if (st.beg >= st.end) return;
+    if (!page_loop_init<NBUF>(st, p, xcd_range(blockIdx.x, gridDim.x))) return;
 
     // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
     cint_p pw = plan + wave * PLAN_STRIDE;
@@ -463,20 +451,12 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     const DmaConst dc = dma_const<NBUF>(p, base, wave, base + (uint32_t)((p.nch + 2 * NB) * page_stride<NBUF>()));
     __syncthreads();
 
-    cur_first(st.cc, P, p.n, st.beg, st.end);
-    st.ld = st.cc;
-    st.new_seg = true;
     st.pv_moved = false;
     st.pv_end = false;
     st.pv_b = 0;
     st.pv_buf = 0;
-    dma_page<NLD, 0, NBUF>(dc, st.ld, page_block(dc, st.ld), wave, doff);
-    cur_next(st.ld, P, p.n, st.beg, st.end);
-    if (NBUF == 3) {
-        dma_page<NLD, 1, NBUF>(dc, st.ld, page_block(dc, st.ld), wave, doff);
-        if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
-    }
-    st.nblk = page_block(dc, st.ld);
+    dma_page<NLD, 0, NBUF>(dc, st.rc, true, wave, doff);
+    if (NBUF == 3) dma_page<NLD, 1, NBUF>(dc, st.r1, st.beg + 1 < st.end, wave, doff);
 
     half8_t ab[MTV][4];
     f32x4_t acc[NB > 0 ? NB : 1];

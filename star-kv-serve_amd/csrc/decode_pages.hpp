@@ -64,8 +64,7 @@ __device__ __forceinline__ uint32_t cs_read_offset(int ks, int lg, int lr) {
 // Loop-invariant operands of the page copies, read once from the parameter block and
 // held in SGPRs.
 struct DmaConst {
-    const uint8_t* cache; int64_t c_s0; int c_s1;
-    const int32_t* bt; int bt_s0, bt_s1, bs_shift;
+    int c_s1;
     const uint8_t* cs; int cs_s0b;
     int nch;
     uint32_t m0w, m0dummy;  // LDS address of this wave's first chunk (buffer 0); the dummy block
@@ -74,8 +73,7 @@ struct DmaConst {
 template <int NBUF = 3>
 __device__ __forceinline__ DmaConst dma_const(const DecodeParams& p, uint32_t base, int wave, uint32_t dummy) {
     DmaConst dc;
-    dc.cache = p.cache; dc.c_s0 = p.c_s0; dc.c_s1 = (int)p.c_s1;
-    dc.bt = p.bt; dc.bt_s0 = p.bt_s0; dc.bt_s1 = p.bt_s1; dc.bs_shift = p.bs_shift;
+    dc.c_s1 = (int)p.c_s1;
     dc.cs = p.cs; dc.cs_s0b = p.cs_s0b;
     dc.nch = p.nch;
     dc.m0w = base + (uint32_t)(wave * page_stride<NBUF>());
@@ -83,28 +81,31 @@ __device__ __forceinline__ DmaConst dma_const(const DecodeParams& p, uint32_t ba
     return dc;
 }
 
-// Cache block of the page cursor c points at (0 past the range).
-__device__ __forceinline__ int page_block(const DmaConst& dc, const Cursor& c) {
-    return c.valid ? ((cint_p)dc.bt)[c.b * dc.bt_s0 + (c.k >> dc.bs_shift) * dc.bt_s1] : 0;
+// The page records, read with scalar loads (wave-uniform index): one s_load_dwordx4.
+typedef const __attribute__((address_space(4))) int4v_t* crec_p;
+__device__ __forceinline__ PageRec rec_of(int4v_t v) {
+    PageRec r;
+    r.addr = (uint64_t)(uint32_t)v[0] | ((uint64_t)(uint32_t)v[1] << 32);
+    r.k = v[2];
+    r.bits = (uint32_t)v[3];
+    return r;
+}
+__device__ __forceinline__ PageRec page_rec(const DecodeParams& p, int j) {
+    return rec_of(((crec_p)(p.ws + p.ws_pages))[j]);
 }
 
 // Buffer descriptors of one page: its rows and its cos/sin rows, bounded to the rows
 // the request has (rows past its end are not read). Past the end of the workgroup's
-// range both are empty: the copies still issue.
+// range (valid false) both are empty: the copies still issue.
 struct DmaPage {
     int4v_t rkv, rcs;
 };
 
-__device__ __forceinline__ DmaPage dma_setup(const DmaConst& dc, const Cursor& c, int blk) {
-    const bool v = c.valid;
-    const int k = v ? c.k : 0;
-    const int row0 = (k & ((1 << dc.bs_shift) - 1)) * TILE_TOK;  // first slot of the page in its block
-    const uint8_t* page = dc.cache + (int64_t)blk * dc.c_s0 + (int64_t)row0 * dc.c_s1;
-    const int tok0 = TILE_TOK * k;
-    const int rows = v ? min(TILE_TOK, c.len - tok0) : 0;
+__device__ __forceinline__ DmaPage dma_setup(const DmaConst& dc, const PageRec& r, bool valid) {
+    const int rows = valid ? pr_rows(r.bits) : 0;
     DmaPage d;
-    d.rkv = buffer_rsrc(page, rows * dc.c_s1);
-    d.rcs = buffer_rsrc(dc.cs + (int64_t)tok0 * dc.cs_s0b, rows * dc.cs_s0b);
+    d.rkv = buffer_rsrc((const void*)(uintptr_t)r.addr, rows * dc.c_s1);
+    d.rcs = buffer_rsrc(dc.cs + (int64_t)(valid ? r.k : 0) * (TILE_TOK * dc.cs_s0b), rows * dc.cs_s0b);
     return d;
 }
 
@@ -120,9 +121,9 @@ __device__ __forceinline__ void dma_one(const DmaConst& dc, const DmaPage& d, in
 }
 
 template <int NLD, int B, int NBUF = 3>
-__device__ __forceinline__ void dma_page(const DmaConst& dc, const Cursor& c, int blk, int wave,
+__device__ __forceinline__ void dma_page(const DmaConst& dc, const PageRec& r, bool valid, int wave,
                                          const uint32_t (&doff)[NLD]) {
-    const DmaPage d = dma_setup(dc, c, blk);
+    const DmaPage d = dma_setup(dc, r, valid);
 #pragma unroll
     for (int i = 0; i < NLD; ++i) dma_one<B, NBUF>(dc, d, i, wave, doff[i]);
 }
@@ -167,13 +168,51 @@ __device__ __forceinline__ int xcd_range(int x, int grid) {
     return grid % 8 == 0 ? (x % 8) * (grid / 8) + x / 8 : x;
 }
 
-// Page-loop state of a workgroup: the page being computed (cc), the page whose copies
-// issue next (ld, two pages ahead) and its cache block, loaded one page ahead.
+// Page-loop state of a workgroup over its pages [beg, end): the page being computed j and
+// the records of pages j (rc), j + 1 (r1) and j + 2 (r2; three page buffers: the page whose
+// copies issue in iteration j), each loaded one iteration before it is first used. Page j
+// starts a request's segment (its AB goes into registers first) when it is the range's
+// first page or the request's page 0, and ends it (the partial is flushed) when it is the
+// request's last page or the range's last.
 struct PageLoop {
-    Cursor cc, ld;
-    int beg, end, g;
-    int nblk;
-    bool new_seg;  // cc starts a new request: its AB goes into registers first
+    int j, beg, end, g;
+    PageRec rc, r1, r2;
 };
+
+__device__ __forceinline__ bool page_starts_seg(const PageLoop& st) { return st.j == st.beg || st.rc.k == 0; }
+__device__ __forceinline__ bool page_ends_seg(const PageLoop& st) {
+    return (st.rc.bits & PR_LAST) != 0 || st.j + 1 == st.end;
+}
+
+// The workgroup's page range from the header (pages per workgroup S, all pages) and the
+// records of its first NBUF pages; false if the range is empty.
+template <int NBUF>
+__device__ __forceinline__ bool page_loop_init(PageLoop& st, const DecodeParams& p, int g) {
+    cint_p hdr = (cint_p)p.ws;
+    const int S = hdr[0], total = hdr[1 + p.n];
+    st.g = g;
+    st.beg = min(g * S, total);
+    st.end = min(st.beg + S, total);
+    if (st.beg >= st.end) return false;
+    st.j = st.beg;
+    st.rc = page_rec(p, st.beg);
+    st.r1 = st.beg + 1 < st.end ? page_rec(p, st.beg + 1) : st.rc;
+    st.r2 = NBUF == 3 && st.beg + 2 < st.end ? page_rec(p, st.beg + 2) : st.r1;
+    return true;
+}
+
+// End of iteration j: the records move down one page; `next` is page j + NBUF's (loaded
+// during the iteration).
+template <int NBUF>
+__device__ __forceinline__ void page_loop_next(PageLoop& st, const PageRec& next) {
+    st.rc = st.r1;
+    if (NBUF == 3) {
+        st.r1 = st.r2;
+        st.r2 = next;
+    } else {
+        st.r1 = next;
+    }
+    ++st.j;
+}
 
 }  // namespace starkv

@@ -384,15 +384,14 @@ __device__ __forceinline__ bool q_iter(QLoop& st, const DmaConst& dc, const QLan
                                        uint32_t salpha, uint32_t base, const int* sqh,
                                        const int (&colv)[NB > 0 ? NB : 1], int lane, int wave) {
     const DecodeParams& p = params();
-    cint_p P = (cint_p)(p.ws + 4);
-    if (!st.cc.valid) {
+    if (st.j >= st.end) {
         st.pv_buf = BN;  // the last page's buffer: its P @ V runs after the loop
         return false;
     }
-    const Cursor cc = st.cc;
-    if (st.new_seg) {
+    const int b = pr_b(st.rc.bits), k = st.rc.k, rows = pr_rows(st.rc.bits);
+    if (page_starts_seg(st)) {
         // This request's AB into registers; slots past the wave's tiles load tile 0.
-        const half8_t* abp = (const half8_t*)(p.ws + p.ws_ab + (size_t)cc.b * p.TT * AB_TILE_BYTES);
+        const half8_t* abp = (const half8_t*)(p.ws + p.ws_ab + (size_t)b * p.TT * AB_TILE_BYTES);
 #pragma unroll
         for (int i = 0; i < MTV; ++i) {
             const int t = unpack8<MTV>(sp8.tile, i);
@@ -403,7 +402,9 @@ __device__ __forceinline__ bool q_iter(QLoop& st, const DmaConst& dc, const QLan
     }
     SKV_WAIT_VM_LGKM0(NLD);  // only the copies of page j + 1 may still be in flight
     lds_barrier();           // page j is in LDS, page j - 1's V table is complete; page j - 1 is done
-    const DmaPage dp = dma_setup(dc, st.ld, st.nblk);
+    const DmaPage dp = dma_setup(dc, st.r2, st.j + 2 < st.end);
+    // The record of the page the next iteration copies: it arrives under the next wait.
+    const PageRec next = st.j + 3 < st.end ? page_rec(p, st.j + 3) : st.rc;
     // Reads of page j for the V expansion and the softmax, issued first: they complete
     // under the K side. Page j - 1's P @ V (its P was 0 before the first page) runs
     // inside the K side: its rescale first, then one step per tile.
@@ -420,7 +421,6 @@ __device__ __forceinline__ bool q_iter(QLoop& st, const DmaConst& dc, const QLan
             for (int e = 0; e < 4; ++e) acc[nb][e] *= al[e];
     }
     copies_at<QSched<MTV>, NLD, BN>(0, dc, dp, opaque_s(wave), doff);
-    if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
     PvStep<NB> pq;
     auto hook = [&](int i) {
         if constexpr (NB > 0) {
@@ -429,30 +429,27 @@ __device__ __forceinline__ bool q_iter(QLoop& st, const DmaConst& dc, const QLan
             if (i <= 3) pv_load<NB, BN>(pq, la.pa, la.vt, i);
         }
     };
-    q_kside<GEN, MTV, NB, BC, NLD, BN>(p, la, ab, sp8, ntw, nh, nf, fast, sp, base, lane, wave, cc.b, dc, dp, doff,
+    q_kside<GEN, MTV, NB, BC, NLD, BN>(p, la, ab, sp8, ntw, nh, nf, fast, sp, base, lane, wave, b, dc, dp, doff,
                                        hook);
 #pragma unroll
     for (int i = MTV; i <= 4; ++i) hook(i);  // the P @ V steps a short K side left
     if constexpr (NB > 0) {
         if (st.pv_end) q_flush<NB>(p, sm, acc, nh, st.pv_b + st.g, sqh, lane, colv);
-        st.pv_moved = q_softmax<MTV, NB>(sm, la, fast, sp, nh, ksw, vsw, salpha, lane, TILE_TOK * cc.k, cc.lo, cc.hi);
+        st.pv_moved = q_softmax<MTV, NB>(sm, la, fast, sp, nh, ksw, vsw, salpha, lane, 0, 0, rows);
     } else {
         // The logits pass: page j's logits into the request's rows.
-        float* lgd = (float*)(p.ws + p.ws_lg) + ((int64_t)cc.b * (p.lcap / TILE_TOK) + cc.k) * p.Hq * TILE_TOK + la.lg;
-        q_softmax<MTV, NB>(sm, la, fast, sp, nh, ksw, vsw, salpha, lane, TILE_TOK * cc.k, cc.lo, cc.hi, lgd);
+        float* lgd = (float*)(p.ws + p.ws_lg) + ((int64_t)b * (p.lcap / TILE_TOK) + k) * p.Hq * TILE_TOK + la.lg;
+        q_softmax<MTV, NB>(sm, la, fast, sp, nh, ksw, vsw, salpha, lane, 0, 0, rows, lgd);
     }
     copies_at<QSched<MTV>, NLD, BN>(MTV + 1, dc, dp, opaque_s(wave), doff);
-    Cursor nx = cc;
-    const bool seg_end = cur_next(nx, P, p.n, st.beg, st.end);
+    const bool seg_end = page_ends_seg(st);
     if constexpr (NB == 0) {  // the request's partial (m, l) as soon as its last page is done
-        if (seg_end) flush_partial<0>(p, sm, acc, nh, cc.b + st.g, sqh, lane);
+        if (seg_end) flush_partial<0>(p, sm, acc, nh, b + st.g, sqh, lane);
     }
     st.pv = true;
     st.pv_end = seg_end;
-    st.pv_b = cc.b;
-    st.cc = nx;
-    st.new_seg = seg_end;
-    st.nblk = page_block(dc, st.ld);
+    st.pv_b = b;
+    page_loop_next<3>(st, next);
     return true;
 }
 
@@ -468,7 +465,6 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     const DecodeParams& p = params();
     const int tid = threadIdx.x, lane = tid & 63, wave = rfl(tid >> 6);
     const int lg = lane >> 4, lr = lane & 15;
-    cint_p P = (cint_p)(p.ws + 4);
     cint_p plan = (cint_p)(p.ws + p.ws_plan);
     // Page buffers and partial-logit rows start zeroed: rows past a request's end are
     // never copied and must hold finite values (P is 0 there); a head's partial rows
@@ -485,12 +481,7 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     }
     if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
     QLoop st;
-    st.g = xcd_range(blockIdx.x, gridDim.x);
-    const int S_tok = ((cint_p)p.ws)[0];
-    const int T = P[p.n];
-    st.beg = min(st.g * S_tok, T);
-    st.end = min(st.beg + S_tok, T);
-    if (st.beg >= st.end) return;
+    if (!page_loop_init<3>(st, p, xcd_range(blockIdx.x, gridDim.x))) return;
 
     // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
     cint_p pw = plan + wave * PLAN_STRIDE;
@@ -611,19 +602,13 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     const DmaConst dc = dma_const(p, base, wave, base + (uint32_t)((p.nch + 2 * NB) * PAGE_STRIDE));
     __syncthreads();
 
-    cur_first(st.cc, P, p.n, st.beg, st.end);
-    st.ld = st.cc;
-    st.new_seg = true;
     st.pv = false;
     st.pv_moved = false;
     st.pv_end = false;
     st.pv_b = 0;
     st.pv_buf = 0;
-    dma_page<NLD, 0>(dc, st.ld, page_block(dc, st.ld), wave, doff);
-    cur_next(st.ld, P, p.n, st.beg, st.end);
-    dma_page<NLD, 1>(dc, st.ld, page_block(dc, st.ld), wave, doff);
-    if (st.ld.valid) cur_next(st.ld, P, p.n, st.beg, st.end);
-    st.nblk = page_block(dc, st.ld);
+    dma_page<NLD, 0>(dc, st.rc, true, wave, doff);
+    dma_page<NLD, 1>(dc, st.r1, st.beg + 1 < st.end, wave, doff);
 
     half8_t ab[MTV][4];
     f32x4_t acc[NB > 0 ? NB : 1];

@@ -79,9 +79,7 @@ __device__ __forceinline__ half8_t to_f16x8(const float (&v)[8]) {
 
 // Kernel arguments of the P @ V pass (host ints and pointers only).
 struct PvParams {
-    const uint8_t* cache; int64_t c_s0; int c_s1;  // bytes
-    int bs_shift;
-    const int32_t* bt; int bt_s0, bt_s1;
+    int c_s1;        // row stride, bytes
     int n, Hq, v_rank;
     int v_off;       // byte of a row where the copied V bytes start (16-aligned)
     int ng;          // 16-byte granules copied per row
@@ -98,6 +96,7 @@ struct PvParams {
     int lds_bytes;
     uint8_t* ws; size_t ws_plan, ws_m, ws_acc, ws_lg; int lcap, acc_ld;
     int r;           // this pass's range = R consecutive logits-pass ranges
+    size_t ws_pages; // page records
 };
 
 typedef const __attribute__((address_space(4))) PvParams kpv_t;
@@ -107,25 +106,26 @@ __device__ __forceinline__ const PvParams& pv_params() {
     return *(const PvParams*)pp;
 }
 
-// Copy descriptors of one page: its rows, its logits rows (request b, tokens 16 k ..,
-// every head), the reference maxima of the R logits-pass slots b + R g + j.
+// Copy descriptors of one page (record r; valid false past the range: nothing is read):
+// its rows, its logits (request b, tokens 16 k .., every head), the reference maxima of the
+// R logits-pass slots b + R g + j.
 struct PvPage {
     int4v_t rv, rl, rm;
 };
 
-__device__ __forceinline__ PvPage pv_page_desc(const PvParams& p, const Cursor& c, int blk, int g) {
+__device__ __forceinline__ PvPage pv_page_desc(const PvParams& p, const PageRec& r, bool v, int g) {
     PvPage d;
-    const bool v = c.valid;
-    const int k = v ? c.k : 0;
-    const int row0 = (k & ((1 << p.bs_shift) - 1)) * TILE_TOK;
-    const uint8_t* page = p.cache + (int64_t)blk * p.c_s0 + (int64_t)row0 * p.c_s1;
-    const int rows = v ? min(TILE_TOK, c.len - TILE_TOK * k) : 0;
-    d.rv = buffer_rsrc(page, rows * p.c_s1);
-    const uint8_t* lg = p.ws + p.ws_lg + (((int64_t)(v ? c.b : 0) * (p.lcap / TILE_TOK) + k) * p.Hq * TILE_TOK) * 4;
+    const int b = v ? pr_b(r.bits) : 0, k = v ? r.k : 0;
+    d.rv = buffer_rsrc((const void*)(uintptr_t)r.addr, v ? pr_rows(r.bits) * p.c_s1 : 0);
+    const uint8_t* lg = p.ws + p.ws_lg + (((int64_t)b * (p.lcap / TILE_TOK) + k) * p.Hq * TILE_TOK) * 4;
     d.rl = buffer_rsrc(lg, v ? p.Hq * TILE_TOK * 4 : 0);
-    const uint8_t* m = p.ws + p.ws_m + (int64_t)(v ? c.b + p.r * g : 0) * p.Hq * 4;
+    const uint8_t* m = p.ws + p.ws_m + (int64_t)(b + p.r * g) * p.Hq * 4;
     d.rm = buffer_rsrc(m, v ? ((p.r * p.Hq * 4 + 15) & ~15) : 0);
     return d;
+}
+
+__device__ __forceinline__ PageRec pv_rec(const PvParams& p, int j) {
+    return rec_of(((crec_p)(p.ws + p.ws_pages))[j]);
 }
 
 // LDS chunks of a page buffer: 0 and 1 the logits of heads 0-15 and 16-31, 2 the R
@@ -170,15 +170,15 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
     extern __shared__ __attribute__((aligned(16))) uint8_t s_pv[];
     const PvParams& p = pv_params();
     const int tid = threadIdx.x, lane = tid & 63, wave = rfl(tid >> 6);
-    cint_p P = (cint_p)(p.ws + 4);
+    cint_p P = (cint_p)(p.ws + 4);  // P[b]: first page of request b
     // Buffers start zeroed: rows past a request's end are never copied and must be finite.
     // Done first: it overlaps the header loads.
     for (int i = tid; i < p.lds_bytes / 16; i += NTHR) ((uint4*)s_pv)[i] = make_uint4(0, 0, 0, 0);
     if (((cint_p)(p.ws + p.ws_plan))[NWAVE * PLAN_STRIDE] == 0) return;  // no plan: the merge reports NaN
     const int g = xcd_range(blockIdx.x, gridDim.x);
-    const int S_tok = ((cint_p)p.ws)[0];  // tokens per logits-pass range
-    const int T = P[p.n];
-    const int beg = min(g * p.r * S_tok, T), end = min(beg + p.r * S_tok, T);
+    const int S = ((cint_p)p.ws)[0];  // pages per logits-pass range
+    const int total = P[p.n];
+    const int beg = min(g * p.r * S, total), end = min(beg + p.r * S, total);
     if (beg >= end) return;
     // This workgroup's column window.
     const int u0 = (int)blockIdx.y * p.per;
@@ -235,46 +235,46 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc[i] = (f32x16_t){};
 
-    Cursor cc, ld;
-    cur_first(cc, P, p.n, beg, end);
-    ld = cc;
-    auto blk_of = [&](const Cursor& c) {
-        return c.valid ? ((cint_p)p.bt)[c.b * p.bt_s0 + (c.k >> p.bs_shift) * p.bt_s1] : 0;
-    };
-    // Prologue: pages 0 .. nbuf - 2 in flight.
+    // Records: the current page j (cur), j + 1 (ncur, loaded in iteration j), the page whose
+    // copies issue in iteration j (cpy = page j + nbuf - 1, loaded in iteration j - 1).
+    PageRec cur = pv_rec(p, beg);
+    // Prologue: pages beg .. beg + nbuf - 2 in flight.
     for (int j = 0; j < p.nbuf - 1; ++j) {
-        pv_copies<NLD>(p, pv_page_desc(p, ld, blk_of(ld), g), base + (uint32_t)(j * p.buf_bytes), dummy, wave, off);
-        if (ld.valid) cur_next(ld, P, p.n, beg, end);
+        const bool v = beg + j < end;
+        const PageRec r = v ? pv_rec(p, beg + j) : cur;
+        pv_copies<NLD>(p, pv_page_desc(p, r, v, g), base + (uint32_t)(j * p.buf_bytes), dummy, wave, off);
     }
-    // The cache block of the next page to copy, read one iteration ahead so that its
-    // load completes under the page barrier's wait.
-    int nblk = blk_of(ld);
+    int jc = beg + p.nbuf - 1;  // the page whose copies issue next
+    PageRec cpy = jc < end ? pv_rec(p, jc) : cur;
     int jb = 0;  // buffer of the current page
-    // The logits-pass ranges R g + j holding tokens of the request of page c: bit j. This
-    // pass's reference max of the request is the largest of theirs (slots of other
-    // ranges hold other requests' values, or none).
-    auto sub_mask = [&](const Cursor& c) -> int {
-        if (!MULTI || !c.valid) return 1;  // R = 1: the one range is this workgroup's
-        const int pb = P[c.b];
-        const int lo = pb + c.lo, hi = pb + c.hi;
+    // The logits-pass ranges R g + j holding pages of request b: bit j. This pass's
+    // reference max of the request is the largest of theirs (slots of other ranges hold
+    // other requests' values, or none).
+    auto sub_mask = [&](int b) -> int {
+        if (!MULTI) return 1;  // R = 1: the one range is this workgroup's
+        const int lo = P[b], hi = P[b + 1];
         int msk = 0;
         for (int j = 0; j < p.r; ++j) {
-            const int r0 = (p.r * g + j) * S_tok;
-            if (max(r0, lo) < min(r0 + S_tok, hi)) msk |= 1 << j;
+            const int r0 = (p.r * g + j) * S;
+            if (max(r0, lo) < min(r0 + S, hi)) msk |= 1 << j;
         }
         return msk;
     };
-    int msk = sub_mask(cc);  // of the current request, redone when the request changes
-    while (cc.valid) {
-        // Page cc is in buffer jb; the copies of the nbuf - 2 pages after it may still run.
+    int msk = sub_mask(pr_b(cur.bits));  // of the current request, redone when the request changes
+    for (int j = beg; j < end; ++j) {
+        // Page j is in buffer jb; the copies of the nbuf - 2 pages after it may still run.
         wait_vmcnt_lgkm0_wide((p.nbuf - 2) * p.nld);
         wait_lgkm0_barrier();  // every wave is done with the previous page's buffer
         {
             const int jn = jb == 0 ? p.nbuf - 1 : jb - 1;  // the buffer the previous page used
-            pv_copies<NLD>(p, pv_page_desc(p, ld, nblk, g), base + (uint32_t)(jn * p.buf_bytes), dummy, wave, off);
-            if (ld.valid) cur_next(ld, P, p.n, beg, end);
-            nblk = blk_of(ld);
+            pv_copies<NLD>(p, pv_page_desc(p, cpy, jc < end, g), base + (uint32_t)(jn * p.buf_bytes), dummy, wave,
+                           off);
         }
+        // The records of the next iteration: they arrive under its wait.
+        ++jc;
+        const PageRec ncpy = jc < end ? pv_rec(p, jc) : cur;
+        const PageRec ncur = j + 1 < end ? pv_rec(p, j + 1) : cur;
+        const int rows = pr_rows(cur.bits);
         const uint32_t buf = base + (uint32_t)(jb * p.buf_bytes);
         const uint32_t vbuf = buf + PV_V0 * 1024;  // the page's V granule columns
         // A operand: P of head am at tokens 8 ag .. 8 ag + 7 of this page.
@@ -293,11 +293,11 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
             mx = lds_ld<float>(buf + mxa);
         }
         const float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-        const int tok0 = TILE_TOK * cc.k + 8 * ag;
+        const int tok0 = 8 * ag;  // this lane's first token in the page
         float pe[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const bool ok = am < p.Hq && tok0 + e >= cc.lo && tok0 + e < cc.hi;
+            const bool ok = am < p.Hq && tok0 + e < rows;
             pe[e] = __builtin_amdgcn_exp2f(ok ? sv[e] - mx : -INFINITY);  // no branch: exp2(-inf) = 0
         }
         if constexpr (FMT == FMT_BF16) {
@@ -371,12 +371,11 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
                 }
             }
         }
-        Cursor nx = cc;
-        const bool seg_end = cur_next(nx, P, p.n, beg, end);
+        const bool seg_end = (cur.bits & PR_LAST) != 0 || j + 1 == end;
         if (seg_end) {
             // This lane's column of each of its blocks, for the 16 heads
             // 8 (j / 4) + 4 (lane >> 5) + j % 4 of the 32x32 result.
-            const int64_t slot = (int64_t)cc.b + g;
+            const int64_t slot = (int64_t)pr_b(cur.bits) + g;
             float* wa = (float*)(p.ws + p.ws_acc) + slot * p.Hq * p.acc_ld;
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
@@ -405,8 +404,9 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
                 }
             }
         }
-        cc = nx;
-        if (MULTI && seg_end) msk = sub_mask(cc);
+        cur = ncur;
+        cpy = ncpy;
+        if (MULTI && seg_end && j + 1 < end) msk = sub_mask(pr_b(cur.bits));
         jb = jb + 1 == p.nbuf ? 0 : jb + 1;
     }
     wait_vmcnt_lgkm0(0);  // no copy may land after the workgroup ends
@@ -756,8 +756,7 @@ int launch_pv(const DecodeParams& p, int fmt, int grid, hipStream_t stream) {
     SKV_CHECK(pl.ok, "decode: no P @ V window fits in LDS (v_rank %d)", p.v_rank);
     PvParams a;
     memset(&a, 0, sizeof(a));
-    a.cache = p.cache; a.c_s0 = p.c_s0; a.c_s1 = (int)p.c_s1; a.bs_shift = p.bs_shift;
-    a.bt = p.bt; a.bt_s0 = p.bt_s0; a.bt_s1 = p.bt_s1;
+    a.c_s1 = (int)p.c_s1;
     a.n = p.n; a.Hq = p.Hq; a.v_rank = p.v_rank;
     a.ng = pl.ng;
     a.vs_rel = p.vs_off - pl.v_off;
@@ -768,6 +767,7 @@ int launch_pv(const DecodeParams& p, int fmt, int grid, hipStream_t stream) {
     a.ws = p.ws; a.ws_plan = p.ws_plan; a.ws_m = p.ws_m; a.ws_acc = p.ws_acc; a.ws_lg = p.ws_lg; a.lcap = p.lcap;
     a.acc_ld = p.acc_ld;
     a.r = p.pv_r;
+    a.ws_pages = p.ws_pages;
     // The windows run side by side in one launch (grid.y): each re-reads the page logits.
     a.per = pl.per;
     a.units = pl.units;

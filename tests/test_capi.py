@@ -55,8 +55,10 @@ def test_workspace_size_is_a_host_function():
     a = L.starkv_decode_workspace_bytes(BF16, 64, 32, 32, 1280, 64, 8192, 256)
     b = L.starkv_decode_workspace_bytes(BF16, 64, 32, 32, 1280, 64, 8192, 128)
     assert a > b > 64 * 80 * 4096
-    # the one-pass form needs no logits buffer: the context length does not matter
-    assert L.starkv_decode_workspace_bytes(BF16, 64, 32, 32, 1280, 64, 100, 256) == a
+    # the one-pass form needs no logits buffer: the context length only sizes the page
+    # records, 16 bytes for every page a request of max_seq_len tokens can have
+    c = L.starkv_decode_workspace_bytes(BF16, 64, 32, 32, 1280, 64, 100, 256)
+    assert a - c == 64 * (8192 // 16 - (100 + 15) // 16) * 16
     assert L.starkv_decode_workspace_bytes(BF16, 0, 32, 32, 1280, 64, 100, 256) == 0
 
 
@@ -72,10 +74,11 @@ def test_two_pass_selection():
     assert L.starkv_decode_two_pass(Q, 32, 1280, 64) == 0
     assert L.starkv_decode_two_pass(Q, 32, 880, 256) == 0      # 51 outliers (padded to 52) + 205 inliers: 5 blocks
     assert L.starkv_decode_two_pass(Q, 32, 880, 1290) == 1
-    # two-pass workspaces add the fp32 logits [n, H, max_seq_len rounded up to 16]
+    # two-pass workspaces add the fp32 logits [n, H, max_seq_len rounded up to 16] (and a
+    # page record per request for the 17th page)
     one = L.starkv_decode_workspace_bytes(BF16, 64, 32, 32, 880, 1280, 8192, 256)
     two = L.starkv_decode_workspace_bytes(BF16, 64, 32, 32, 880, 1280, 8200, 256)
-    assert two - one == 64 * 32 * 16 * 4
+    assert two - one == 64 * 32 * 16 * 4 + 64 * 16
     assert one >= 64 * 32 * 8192 * 4 + 320 * 32 * 1280 * 4
     # forcing a form
     assert _hip.set_decode_path(2) == 0
