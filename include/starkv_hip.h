@@ -149,14 +149,16 @@ size_t starkv_decode_workspace_bytes(int cache_kind, int n, int num_heads, int n
                                      int v_rank, int max_seq_len, int grid);
 
 /*
- * 1 if a decode of this layer shape runs in two passes, else 0. The one-pass decode
- * keeps P @ V in the decode kernel and takes v_rank <= 256 (bf16/fp16) or up to five
- * 64-lane blocks of outlier (padded to 4) plus inlier columns (3.2-bit). Wider V
- * ranks (up to 4096) run a logits pass and a P @ V pass, as the reference's
- * paged_decode.py:199-219 / paged_quant.py:390-407 split their V pass. Both forms
- * give the same results to within rounding.
+ * 1 if a decode of this layer shape runs in two passes, else 0 (num_kv_heads = num_heads
+ * for the 3.2-bit cache). The one-pass decode keeps P @ V in the decode kernel and takes
+ * v_rank <= 256 (bf16/fp16) or up to five 64-lane blocks of outlier (padded to 4) plus
+ * inlier columns (3.2-bit), where a kernel instantiation holds the layer's rank tiles per
+ * wave (all but one of them at least) without scratch spills. Other V ranks (up to 4096)
+ * run a logits pass and a P @ V pass, as the reference's paged_decode.py:199-219 /
+ * paged_quant.py:390-407 split their V pass. Both forms give the same results to within
+ * rounding.
  */
-int starkv_decode_two_pass(int cache_kind, int num_heads, int k_width, int v_rank);
+int starkv_decode_two_pass(int cache_kind, int num_heads, int num_kv_heads, int k_width, int v_rank);
 
 /*
  * 1 if one decode call takes a layer of this shape, else 0 (host function, no device

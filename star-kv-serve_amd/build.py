@@ -7,6 +7,7 @@ then the torch operator library csrc/torch_ops.cpp -> starkv_serve/libstarkv_tor
 Each HIP source compiles in its own hipcc process (in parallel), then one link step.
 """
 import os
+import re
 import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
@@ -28,12 +29,31 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
+def _spills(report: str) -> list:
+    """Kernels of a -Rpass-analysis=kernel-resource-usage report that use scratch memory
+    (register spills): [(kernel, bytes per lane)]."""
+    out, name = [], None
+    for line in report.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and int(m.group(1)) > 0:
+            out.append((name, int(m.group(1))))
+    return out
+
+
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
+    # Every kernel of the library runs from registers: a kernel that spills to scratch is a
+    # build error (its instantiation must be dropped or its register use reduced).
+    spills = _spills(r.stderr)
+    if spills:
+        raise RuntimeError(f"{src}: kernels with scratch spills: {spills}")
     return obj
 
 

@@ -767,17 +767,20 @@ static int launch_merge(dim3 grid, size_t lds, hipStream_t stream, const DecodeP
 static int g_path = 0;
 
 // Whether the one-pass kernel takes a layer of this shape.
-static bool one_pass_fits(int fmt, int k_width, int v_rank, int row_bytes, int v_nout) {
+// TT: the call's rank tiles over its query heads (the tiles per wave the kernel must hold
+// decide whether a one-pass instantiation without scratch spills exists).
+static bool one_pass_fits(int fmt, int k_width, int v_rank, int row_bytes, int v_nout, int TT) {
     if (fmt == FMT_Q4) {
         const int qnb = quant_v_blocks(v_rank, v_nout);
-        return qnb > 0 && quant_copies(row_bytes) > 0 && quant_lds_bytes(row_bytes, qnb) <= quant_lds_limit();
+        return qnb > 0 && quant_copies(row_bytes) > 0 && quant_lds_bytes(row_bytes, qnb) <= quant_lds_limit() &&
+               quant_mtv(TT, qnb, row_bytes) > 0;
     }
     const int nb = (v_rank + 63) / 64;
-    return nb <= 4 && lowrank_copies(k_width, nb) > 0;
+    return nb <= 4 && lowrank_copies(k_width, nb) > 0 && lowrank_mtv(TT, nb) > 0;
 }
 
-static bool use_two_pass(int fmt, int k_width, int v_rank, int row_bytes, int v_nout) {
-    return g_path == 2 || (g_path == 0 && !one_pass_fits(fmt, k_width, v_rank, row_bytes, v_nout));
+static bool use_two_pass(int fmt, int k_width, int v_rank, int row_bytes, int v_nout, int TT) {
+    return g_path == 2 || (g_path == 0 && !one_pass_fits(fmt, k_width, v_rank, row_bytes, v_nout, TT));
 }
 
 // Host restatement of the wave plan that workgroup 1 of prep_kernel builds
@@ -882,8 +885,8 @@ static bool qgroup_args_ok(int row_k_width, int row_heads, int v_rank, int head0
 }
 
 // Whether a 3.2-bit call over this group takes the two-pass form.
-static bool qgroup_two_pass(const QGroup& g) {
-    return use_two_pass(FMT_Q4, 0, g.row.v_rank, g.extent, g.row.v_nout);
+static bool qgroup_two_pass(const QGroup& g, int k_width) {
+    return use_two_pass(FMT_Q4, 0, g.row.v_rank, g.extent, g.row.v_nout, k_width / 16);
 }
 
 // Whether one 3.2-bit call takes query heads [h0, h1) of an MHA layer of H heads with K
@@ -907,7 +910,7 @@ static bool quant_group_fits(const int32_t* ranks, int H, int v_rank, int h0, in
     }
     if (TT < 1 || TT > MAX_TT || !plan_fits(tiles, heads, TT)) return false;
     const QGroup g = qgroup(row_kw, H, v_rank, h0, heads, lane0);
-    if (!qgroup_two_pass(g)) return true;
+    if (!qgroup_two_pass(g, kw)) return true;
     return quant_copies(g.k_extent) > 0 && quant_lds_bytes(g.k_extent, 0) <= quant_lds_limit() &&
            pv_fits(FMT_Q4, kw, v_rank, g.vs_off, g.vq_off, g.row.v_nout, g.row.v_bytes);
 }
@@ -928,7 +931,7 @@ static bool codes_group_fits(int cache_kind, int per, const int32_t* ranks, int 
     for (int h = 0; h < Hq; ++h) TT += tiles[h];
     if (TT < 1 || TT > MAX_TT || !plan_fits(tiles, Hq, TT)) return false;
     const int fmt = cache_kind == STARKV_F16 ? FMT_F16 : FMT_BF16;
-    if (!use_two_pass(fmt, k_width, v_rank, (k_width + v_rank) * 2, 0)) return true;
+    if (!use_two_pass(fmt, k_width, v_rank, (k_width + v_rank) * 2, 0, TT)) return true;
     return lowrank_copies(k_width, 0) > 0 && pv_fits(fmt, k_width, v_rank, 0, 0, 0, 0);
 }
 
@@ -940,7 +943,7 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     SKV_CHECK(a.grid >= 1, "decode: grid must be >= 1");
     SKV_CHECK(TT >= 1 && TT <= MAX_TT, "decode: %d rank tiles (1..%d: k_width x heads per kv head <= %d)", TT,
               MAX_TT, MAX_TT * 16);
-    const bool two = use_two_pass(fmt, p.k_width, a.v_rank, row_bytes, p.v_nout);
+    const bool two = use_two_pass(fmt, p.k_width, a.v_rank, row_bytes, p.v_nout, TT);
     const int lcap = two ? lcap_of(a.max_seq_len) : 0;
     const int pv_r = two ? pv_ratio(fmt, a.n, a.max_seq_len, a.grid) : 1;
     SKV_CHECK(a.max_seq_len <= (1 << 24), "decode: max_seq_len %d > 2^24", a.max_seq_len);
@@ -971,7 +974,7 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
               "decode: query rows must be 16-byte aligned (strides multiples of 8)");
     SKV_CHECK(a.ku_s0 % 8 == 0 && ((uintptr_t)a.k_up % 16) == 0, "decode: k_up rows must be 16-byte aligned");
     const int nb = (a.v_rank + 63) / 64;
-    SKV_CHECK(two || one_pass_fits(fmt, p.k_width, a.v_rank, row_bytes, p.v_nout),
+    SKV_CHECK(two || one_pass_fits(fmt, p.k_width, a.v_rank, row_bytes, p.v_nout, TT),
               "decode: v_rank %d does not fit the one-pass decode (the two-pass form is switched off)", a.v_rank);
     SKV_CHECK(!two || a.v_rank <= MAX_V_RANK_TWO_PASS, "decode: v_rank %d > %d", a.v_rank, MAX_V_RANK_TWO_PASS);
     const int wsz = a.vu_dt == STARKV_F32 ? 4 : 2;
@@ -1164,7 +1167,7 @@ size_t starkv_decode_workspace_bytes(int cache_kind, int n, int num_heads, int n
         row_bytes = (k_width + v_rank) * 2;
         TT = (num_heads / num_kv_heads) * (k_width / 16);
     }
-    const bool two = use_two_pass(fmt, k_width, v_rank, row_bytes, v_nout);
+    const bool two = use_two_pass(fmt, k_width, v_rank, row_bytes, v_nout, TT);
     return ws_layout(n, num_heads, TT, v_rank, grid, two ? lcap_of(max_seq_len) : 0,
                      two ? pv_ratio(fmt, n, max_seq_len, grid) : 1, pages_of(max_seq_len))
         .total;
@@ -1221,10 +1224,12 @@ int starkv_decode_set_path(int mode) {
     return prev;
 }
 
-int starkv_decode_two_pass(int cache_kind, int num_heads, int k_width, int v_rank) {
+int starkv_decode_two_pass(int cache_kind, int num_heads, int num_kv_heads, int k_width, int v_rank) {
+    if (num_heads < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0 || k_width < 16) return 0;
     if (cache_kind == STARKV_CACHE_Q3_2)
         return starkv_quant_group_two_pass(k_width, num_heads, v_rank, 0, num_heads, 0, k_width);
-    return use_two_pass(cache_kind == STARKV_F16 ? FMT_F16 : FMT_BF16, k_width, v_rank, (k_width + v_rank) * 2, 0);
+    return use_two_pass(cache_kind == STARKV_F16 ? FMT_F16 : FMT_BF16, k_width, v_rank, (k_width + v_rank) * 2, 0,
+                        num_heads / num_kv_heads * (k_width / 16));
 }
 
 int starkv_fold_q(void* stream, const void* q, int64_t q_s0, int64_t q_s1, int q_dtype, const void* k_up,
@@ -1368,7 +1373,7 @@ size_t starkv_quant_group_workspace_bytes(int n, int row_k_width, int row_num_he
         !qgroup_args_ok(row_k_width, row_num_heads, v_rank, head0, num_heads, k_lane0, k_width))
         return 0;
     const QGroup g = qgroup(row_k_width, row_num_heads, v_rank, head0, num_heads, k_lane0);
-    const bool two = qgroup_two_pass(g);
+    const bool two = qgroup_two_pass(g, k_width);
     return ws_layout(n, num_heads, k_width / 16, v_rank, grid, two ? lcap_of(max_seq_len) : 0,
                      two ? pv_ratio(FMT_Q4, n, max_seq_len, grid) : 1, pages_of(max_seq_len))
         .total;
@@ -1377,7 +1382,7 @@ size_t starkv_quant_group_workspace_bytes(int n, int row_k_width, int row_num_he
 int starkv_quant_group_two_pass(int row_k_width, int row_num_heads, int v_rank, int head0, int num_heads,
                                 int k_lane0, int k_width) {
     if (!qgroup_args_ok(row_k_width, row_num_heads, v_rank, head0, num_heads, k_lane0, k_width)) return 0;
-    return qgroup_two_pass(qgroup(row_k_width, row_num_heads, v_rank, head0, num_heads, k_lane0));
+    return qgroup_two_pass(qgroup(row_k_width, row_num_heads, v_rank, head0, num_heads, k_lane0), k_width);
 }
 
 }  // extern "C"

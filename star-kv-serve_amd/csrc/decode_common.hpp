@@ -145,6 +145,7 @@ struct DecodeParams {
 };
 
 __device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int lds_ld_i32(uint32_t a) { return *(const __attribute__((address_space(3))) int*)(a); }
 
 typedef const __attribute__((address_space(4))) int32_t* cint_p;
 
@@ -211,8 +212,12 @@ __device__ __forceinline__ f32x4_t mfma_tile(const half8_t (&a)[4], const half8_
 // lane & 15.
 struct SmState {
     float m, l;   // log2-domain reference max (same on the head's 16 lanes), this lane's column sum
-    int hf, hn;   // the row's head: first slot, slots (0 for no head)
 };
+
+// A wave's heads' partial-logit rows for the softmax of heads with more than 4 slots (the
+// rare path): per local head k, its first slot | its slots << 8, kept in LDS rather than
+// registers (the common path never reads them).
+__device__ __forceinline__ int head_slots(uint32_t shfn, int lane) { return lds_ld_i32(shfn + 4 * (opaque(lane) >> 4)); }
 
 // The partial of the request that ends with this page: m, l and acc of this wave's
 // heads into partial slot `slot`, then reset. The wave's query-head ids come from LDS:
@@ -253,6 +258,10 @@ int launch_lowrank(const DecodeParams& p, int fmt, int nb, int grid, hipStream_t
 // per page, page buffers (3 or 2), dynamic LDS bytes, copies per wave per page (0 if a
 // page does not fit).
 int lowrank_chunks(int k_width, int nb);
+// Rank tiles per wave the bf16/fp16 kernel holds in VGPRs for TT rank tiles and nb V
+// blocks (nb = 0: the logits pass); 0 if no instantiation runs the one pass without
+// scratch spills.
+int lowrank_mtv(int TT, int nb);
 int lowrank_buffers(int k_width, int nb);
 int lowrank_lds_bytes(int k_width, int nb);
 int lowrank_copies(int k_width, int nb);
@@ -273,6 +282,7 @@ int launch_merge_wide(const DecodeParams& p, int grid, int w_dt, const void* vup
                       void* out, int64_t o_s0, int64_t o_s1, int out_dt, hipStream_t stream);
 constexpr int MAX_V_RANK_TWO_PASS = 4096;  // H x head_dim of a 32-head MHA layer: a full-rank V
 int quant_v_blocks(int v_rank, int v_nout);
+int quant_mtv(int TT, int nb, int row_bytes);  // as lowrank_mtv, for the 3.2-bit kernel
 int quant_chunks(int row_bytes);
 int quant_copies(int row_bytes);
 int quant_lds_bytes(int row_bytes, int nb);

@@ -145,7 +145,7 @@ __device__ __forceinline__ void k_side(const DecodeParams& p, const LaneAddr<MTV
 // LG (the logits pass): no P; each valid logit goes to lgd instead.
 template <int FMT, bool LG = false>
 __device__ __forceinline__ bool softmax_page(SmState& sm, const uint32_t sm_addr, bool fast, uint32_t sp, int nh,
-                                             uint32_t pw_addr, uint32_t plo_off, uint32_t salpha, int lane, int tok0,
+                                             uint32_t pw_addr, uint32_t plo_off, uint32_t salpha, uint32_t shfn, int lane, int tok0,
                                              int lo, int hi, float* lgd = nullptr) {
     const int kh = lane >> 4, lr = lane & 15;
     float s;
@@ -154,7 +154,8 @@ __device__ __forceinline__ bool softmax_page(SmState& sm, const uint32_t sm_addr
             (lds_ld<float>(sm_addr + 128) + lds_ld<float>(sm_addr + 192));
     } else {
         s = 0.f;
-        for (int t = 0; t < sm.hn; ++t) s += lds_ld<float>(sp + (uint32_t)((sm.hf + t) * TILE_TOK + lr) * 4);
+        const int hfn = head_slots(shfn, lane);
+        for (int t = 0; t < (hfn >> 8); ++t) s += lds_ld<float>(sp + (uint32_t)(((hfn & 255) + t) * TILE_TOK + lr) * 4);
     }
     const int tok = tok0 + lr;
     const bool valid = tok >= lo && tok < hi && kh < nh;
@@ -167,7 +168,7 @@ __device__ __forceinline__ bool softmax_page(SmState& sm, const uint32_t sm_addr
         alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(sm.m - mn);
         sm.m = mn;
         moved = true;
-        if (!LG && lr == 0) lds_st<float>(salpha + 4 * kh, alpha);
+        if (!LG && lr == 0) lds_st<float>(salpha + 4 * (opaque(lane) >> 4), alpha);
     }
     const float pe = s == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - sm.m);
     sm.l = fmaf(sm.l, alpha, pe);
@@ -261,7 +262,7 @@ template <int FMT, int MTV, int NB, int NLD, int BC, int BN, int NBUF>
 __device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const LaneAddr<MTV, NB>& la,
                                         half8_t (&ab)[MTV][4], f32x4_t (&acc)[NB > 0 ? NB : 1], SmState& sm,
                                         const uint32_t (&doff)[NLD], int ntw, int nh, bool fast, uint32_t sp,
-                                        uint32_t plo_off, uint32_t salpha, const int* sqh, int lane, int wave) {
+                                        uint32_t plo_off, uint32_t salpha, uint32_t shfn, const int* sqh, int lane, int wave) {
     const DecodeParams& p = params();
     if (st.j >= st.end) {
         st.pv_buf = BN;  // the last page's buffer: its P @ V runs after the loop
@@ -313,12 +314,12 @@ __device__ __forceinline__ bool lr_iter(LrLoop& st, const DmaConst& dc, const La
     for (int i = MTV; i <= 4; ++i) hook(i);  // the P @ V steps a short K side left
     if constexpr (NB > 0) {
         if (st.pv_end) flush_partial<NB>(p, sm, acc, nh, st.pv_b + st.g, sqh, lane);
-        st.pv_moved = softmax_page<FMT>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, 0, 0, rows);
+        st.pv_moved = softmax_page<FMT>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, shfn, lane, 0, 0, rows);
     } else {
         // The logits pass: page j's logits into the request's rows, and its partial
         // (m, l) flushed right away when page j ends the request.
         float* lgd = (float*)(p.ws + p.ws_lg) + ((int64_t)b * (p.lcap / TILE_TOK) + k) * p.Hq * TILE_TOK + la.lg;
-        softmax_page<FMT, true>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, lane, 0, 0, rows, lgd);
+        softmax_page<FMT, true>(sm, la.sm, fast, sp, nh, la.pw, plo_off, salpha, shfn, lane, 0, 0, rows, lgd);
     }
     copies_at<LrSched<MTV>, NLD, BN, NBUF>(MTV + 1, dc, dp, opaque_s(wave), doff);
     const bool seg_end = page_ends_seg(st);
@@ -339,6 +340,7 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     __shared__ __attribute__((aligned(16))) uint16_t s_plo[FMT == FMT_BF16 ? NWAVE : 1][4 * TILE_TOK];
     __shared__ __attribute__((aligned(16))) float s_alpha[NWAVE][4];
     __shared__ int s_qh[NWAVE][4];
+    __shared__ int s_hfn[NWAVE][4];  // per local head: first slot | slots << 8
     typedef LrChunks<NB> C;
 
     const DecodeParams& p = params();
@@ -423,8 +425,8 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     const uint32_t salpha = lds_addr(&s_alpha[wave][0]);
     if (lane < 4) s_qh[wave][lane] = lane < nh ? pw[32 + lane] : 0;
     SmState sm;
-    sm.hf = lg < nh ? pw[40 + lg] : 0;
-    sm.hn = lg < nh ? pw[48 + lg] : 0;
+    if (lane < 4) s_hfn[wave][lane] = lane < nh ? pw[40 + lane] | (pw[48 + lane] << 8) : 0;
+    const uint32_t shfn = lds_addr(&s_hfn[wave][0]);
     sm.m = -INFINITY;
     sm.l = 0.f;
 
@@ -465,23 +467,23 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     const int* sqh = &s_qh[wave][0];
     if (NBUF == 3) {
         while (true) {
-            if (!lr_iter<FMT, MTV, NB, NLD, 0, 2, NBUF>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, sqh,
+            if (!lr_iter<FMT, MTV, NB, NLD, 0, 2, NBUF>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, shfn, sqh,
                                                   lane, wave))
                 break;
-            if (!lr_iter<FMT, MTV, NB, NLD, 1, 0, NBUF>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, sqh,
+            if (!lr_iter<FMT, MTV, NB, NLD, 1, 0, NBUF>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, shfn, sqh,
                                                   lane, wave))
                 break;
-            if (!lr_iter<FMT, MTV, NB, NLD, 2, 1, NBUF>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, sqh,
+            if (!lr_iter<FMT, MTV, NB, NLD, 2, 1, NBUF>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha, shfn, sqh,
                                                   lane, wave))
                 break;
         }
     } else {  // two buffers: page j + 1 goes into the buffer page j - 1 left
         while (true) {
             if (!lr_iter<FMT, MTV, NB, NLD, 0, 1, NBUF>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha,
-                                                       sqh, lane, wave))
+                                                       shfn, sqh, lane, wave))
                 break;
             if (!lr_iter<FMT, MTV, NB, NLD, 1, 0, NBUF>(st, dc, la, ab, acc, sm, doff, ntw, nh, fast, sp, plo_off, salpha,
-                                                       sqh, lane, wave))
+                                                       shfn, sqh, lane, wave))
                 break;
         }
     }
@@ -494,26 +496,36 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     }
 }
 
+// The instantiations that run without scratch spills: MTV tiles per wave held in VGPRs
+// with NB V blocks. Only these are compiled (lowrank_mtv picks among them).
+constexpr bool lr_spill_free(int mtv, int nb) { return mtv <= 8 || (mtv == 9 && nb <= 2) || (mtv == 10 && nb <= 1); }
+
+template <int FMT, int MTV, int NB, int NLD, int NBUF>
+const void* inst() {
+    if constexpr (lr_spill_free(MTV, NB)) return (const void*)&lowrank_kernel<FMT, MTV, NB, NLD, NBUF>;
+    return nullptr;
+}
+
 template <int FMT, int MTV, int NLD, int NBUF>
 const void* pick_nb(int nb) {
-    if (nb <= 0) return (const void*)&lowrank_kernel<FMT, MTV, 0, NLD, NBUF>;
-    if (nb <= 1) return (const void*)&lowrank_kernel<FMT, MTV, 1, NLD, NBUF>;
-    if (nb <= 2) return (const void*)&lowrank_kernel<FMT, MTV, 2, NLD, NBUF>;
-    return (const void*)&lowrank_kernel<FMT, MTV, 4, NLD, NBUF>;
+    if (nb <= 0) return inst<FMT, MTV, 0, NLD, NBUF>();
+    if (nb <= 1) return inst<FMT, MTV, 1, NLD, NBUF>();
+    if (nb <= 2) return inst<FMT, MTV, 2, NLD, NBUF>();
+    return inst<FMT, MTV, 4, NLD, NBUF>();
 }
 
 template <int FMT, int NLD, int NBUF>
-const void* pick_mtv(int need, int nb) {
-    return need <= 4 ? pick_nb<FMT, 4, NLD, NBUF>(nb)
-           : need <= 8 ? pick_nb<FMT, 8, NLD, NBUF>(nb)
-           : need <= 9 ? pick_nb<FMT, 9, NLD, NBUF>(nb)
-                       : pick_nb<FMT, 10, NLD, NBUF>(nb);
+const void* pick_mtv(int mtv, int nb) {
+    return mtv == 4 ? pick_nb<FMT, 4, NLD, NBUF>(nb)
+           : mtv == 8 ? pick_nb<FMT, 8, NLD, NBUF>(nb)
+           : mtv == 9 ? pick_nb<FMT, 9, NLD, NBUF>(nb)
+                      : pick_nb<FMT, 10, NLD, NBUF>(nb);
 }
 
 template <int FMT>
-const void* pick(int nbuf, int nld, int need, int nb) {
-    if (nbuf == 2) return pick_mtv<FMT, 8, 2>(need, nb);
-    return nld <= 3 ? pick_mtv<FMT, 3, 3>(need, nb) : pick_mtv<FMT, 6, 3>(need, nb);
+const void* pick(int nbuf, int nld, int mtv, int nb) {
+    if (nbuf == 2) return pick_mtv<FMT, 8, 2>(mtv, nb);
+    return nld <= 3 ? pick_mtv<FMT, 3, 3>(mtv, nb) : pick_mtv<FMT, 6, 3>(mtv, nb);
 }
 
 int nb_blocks(int nb) { return nb <= 0 ? 0 : nb <= 1 ? 1 : nb <= 2 ? 2 : 4; }
@@ -544,13 +556,30 @@ int lowrank_lds_bytes(int k_width, int nb) {
     return (lowrank_chunks(k_width, nb) + 2 * nb_blocks(nb)) * lowrank_buffers(k_width, nb) * 1024 + 1024;
 }
 
-// Rank tiles per wave held in VGPRs: the wave plan balances whole heads to within a
-// tile of TT / 8, so MTV = ceil(TT / 8) covers every wave for the usual rank mixes (a
-// wave with more streams the rest of its tiles from L2).
+// Rank tiles per wave held in VGPRs for a layer of TT rank tiles and nb V blocks (the
+// one-pass kernel; nb = 0 the logits pass). The wave plan balances whole heads to within a
+// tile of TT / 8, so need = ceil(TT / 8) covers every wave for the usual rank mixes (a wave
+// with more streams the rest of its tiles from L2 on every page). The smallest compiled
+// size >= need, or, where that one would spill with nb V blocks, the next smaller one if
+// it still holds need - 1; 0 if neither runs without spills (the layer then takes the
+// two-pass form, whose logits pass has none: nb = 0 never returns 0).
+int lowrank_mtv(int TT, int nb) {
+    static const int sizes[4] = {4, 8, 9, 10};
+    const int need = (TT + NWAVE - 1) / NWAVE;
+    int i = 0;
+    while (i < 3 && sizes[i] < need) ++i;
+    const int nbv = nb_blocks(nb);
+    if (lr_spill_free(sizes[i], nbv)) return sizes[i];
+    if (i > 0 && sizes[i - 1] >= need - 1 && lr_spill_free(sizes[i - 1], nbv)) return sizes[i - 1];
+    return 0;
+}
+
 int launch_lowrank(const DecodeParams& p, int fmt, int nb, int grid, hipStream_t stream) {
-    const int need = (p.TT + NWAVE - 1) / NWAVE;
+    const int mtv = lowrank_mtv(p.TT, nb);
     const int nld = lowrank_copies(p.k_width, nb), nbuf = lowrank_buffers(p.k_width, nb);
-    const void* fn = fmt == FMT_BF16 ? pick<FMT_BF16>(nbuf, nld, need, nb) : pick<FMT_F16>(nbuf, nld, need, nb);
+    SKV_CHECK(mtv > 0, "decode: no spill-free kernel for %d rank tiles and %d V blocks", p.TT, nb);
+    const void* fn = fmt == FMT_BF16 ? pick<FMT_BF16>(nbuf, nld, mtv, nb) : pick<FMT_F16>(nbuf, nld, mtv, nb);
+    SKV_CHECK(fn != nullptr, "decode: no kernel for %d rank tiles and %d V blocks", p.TT, nb);
     static const void* raised[256];  // kernels whose dynamic-LDS limit was raised (host-side bookkeeping)
     static int nraised = 0;
     bool seen = false;

@@ -241,8 +241,8 @@ __device__ __forceinline__ void q_kside(const DecodeParams& p, const QLane<MTV, 
 // ksw, vsw: this lane's (outlier, inlier) K scales of its head and V scales, row lane & 15.
 template <int MTV, int NB>
 __device__ __forceinline__ bool q_softmax(SmState& sm, const QLane<MTV, NB>& la, bool fast, uint32_t sp, int nh,
-                                          uint32_t ksw, uint32_t vsw, uint32_t salpha, int lane, int tok0, int lo,
-                                          int hi, float* lgd = nullptr) {
+                                          uint32_t ksw, uint32_t vsw, uint32_t salpha, uint32_t shfn, int lane,
+                                          int tok0, int lo, int hi, float* lgd = nullptr) {
     const uint32_t sm_addr = la.sm, pw_addr = la.pw;
     const int kh = lane >> 4, lr = lane & 15;
     float s;
@@ -251,7 +251,8 @@ __device__ __forceinline__ bool q_softmax(SmState& sm, const QLane<MTV, NB>& la,
             (lds_ld<float>(sm_addr + 128) + lds_ld<float>(sm_addr + 192));
     } else {
         s = 0.f;
-        for (int t = 0; t < sm.hn; ++t) s += lds_ld<float>(sp + (uint32_t)((sm.hf + t) * TILE_TOK + lr) * 4);
+        const int hfn = head_slots(shfn, lane);
+        for (int t = 0; t < (hfn >> 8); ++t) s += lds_ld<float>(sp + (uint32_t)(((hfn & 255) + t) * TILE_TOK + lr) * 4);
     }
     // The head's K scales for this token: s_in * (all ranks) + (s_out - s_in) * (outlier ranks).
     const float si = __uint_as_float(ksw & 0xffff0000u);
@@ -267,7 +268,7 @@ __device__ __forceinline__ bool q_softmax(SmState& sm, const QLane<MTV, NB>& la,
         alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(sm.m - mn);
         sm.m = mn;
         moved = true;
-        if (NB > 0 && lr == 0) lds_st<float>(salpha + 4 * kh, alpha);
+        if (NB > 0 && lr == 0) lds_st<float>(salpha + 4 * (opaque(lane) >> 4), alpha);
     }
     const float pe = s == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - sm.m);
     sm.l = fmaf(sm.l, alpha, pe);
@@ -381,7 +382,7 @@ __device__ __forceinline__ bool q_iter(QLoop& st, const DmaConst& dc, const QLan
                                        half8_t (&ab)[MTV][4], const SlotPack<MTV>& sp8,
                                        f32x4_t (&acc)[NB > 0 ? NB : 1], SmState& sm,
                                        const uint32_t (&doff)[NLD], int ntw, int nh, int nf, bool fast, uint32_t sp,
-                                       uint32_t salpha, uint32_t base, const int* sqh,
+                                       uint32_t salpha, uint32_t shfn, uint32_t base, const int* sqh,
                                        const int (&colv)[NB > 0 ? NB : 1], int lane, int wave) {
     const DecodeParams& p = params();
     if (st.j >= st.end) {
@@ -435,11 +436,11 @@ __device__ __forceinline__ bool q_iter(QLoop& st, const DmaConst& dc, const QLan
     for (int i = MTV; i <= 4; ++i) hook(i);  // the P @ V steps a short K side left
     if constexpr (NB > 0) {
         if (st.pv_end) q_flush<NB>(p, sm, acc, nh, st.pv_b + st.g, sqh, lane, colv);
-        st.pv_moved = q_softmax<MTV, NB>(sm, la, fast, sp, nh, ksw, vsw, salpha, lane, 0, 0, rows);
+        st.pv_moved = q_softmax<MTV, NB>(sm, la, fast, sp, nh, ksw, vsw, salpha, shfn, lane, 0, 0, rows);
     } else {
         // The logits pass: page j's logits into the request's rows.
         float* lgd = (float*)(p.ws + p.ws_lg) + ((int64_t)b * (p.lcap / TILE_TOK) + k) * p.Hq * TILE_TOK + la.lg;
-        q_softmax<MTV, NB>(sm, la, fast, sp, nh, ksw, vsw, salpha, lane, 0, 0, rows, lgd);
+        q_softmax<MTV, NB>(sm, la, fast, sp, nh, ksw, vsw, salpha, shfn, lane, 0, 0, rows, lgd);
     }
     copies_at<QSched<MTV>, NLD, BN>(MTV + 1, dc, dp, opaque_s(wave), doff);
     const bool seg_end = page_ends_seg(st);
@@ -461,6 +462,7 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     __shared__ __attribute__((aligned(16))) float s_alpha[NWAVE][4];
     __shared__ __attribute__((aligned(16))) uint2 s_omask[17][4];  // [outlier ranks of the tile][row group]
     __shared__ int s_qh[NWAVE][4];
+    __shared__ int s_hfn[NWAVE][4];  // per local head: first slot | slots << 8
 
     const DecodeParams& p = params();
     const int tid = threadIdx.x, lane = tid & 63, wave = rfl(tid >> 6);
@@ -580,8 +582,8 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     const uint32_t salpha = lds_addr(&s_alpha[wave][0]);
     if (lane < 4) s_qh[wave][lane] = lane < nh ? pw[32 + lane] : 0;
     SmState sm;
-    sm.hf = lg < nh ? pw[40 + lg] : 0;
-    sm.hn = lg < nh ? pw[48 + lg] : 0;
+    if (lane < 4) s_hfn[wave][lane] = lane < nh ? pw[40 + lane] | (pw[48 + lane] << 8) : 0;
+    const uint32_t shfn = lds_addr(&s_hfn[wave][0]);
     sm.m = -INFINITY;
     sm.l = 0.f;
 
@@ -619,13 +621,13 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     auto loop = [&](auto gen_tag) {
         constexpr bool G = decltype(gen_tag)::value;
         while (true) {
-            if (!q_iter<G, MTV, NB, NLD, 0, 2>(st, dc, la, ab, sp8, acc, sm, doff, ntw, nh, nf, fast, sp, salpha, base, sqh,
+            if (!q_iter<G, MTV, NB, NLD, 0, 2>(st, dc, la, ab, sp8, acc, sm, doff, ntw, nh, nf, fast, sp, salpha, shfn, base, sqh,
                                                colv, lane, wave))
                 break;
-            if (!q_iter<G, MTV, NB, NLD, 1, 0>(st, dc, la, ab, sp8, acc, sm, doff, ntw, nh, nf, fast, sp, salpha, base, sqh,
+            if (!q_iter<G, MTV, NB, NLD, 1, 0>(st, dc, la, ab, sp8, acc, sm, doff, ntw, nh, nf, fast, sp, salpha, shfn, base, sqh,
                                                colv, lane, wave))
                 break;
-            if (!q_iter<G, MTV, NB, NLD, 2, 1>(st, dc, la, ab, sp8, acc, sm, doff, ntw, nh, nf, fast, sp, salpha, base, sqh,
+            if (!q_iter<G, MTV, NB, NLD, 2, 1>(st, dc, la, ab, sp8, acc, sm, doff, ntw, nh, nf, fast, sp, salpha, shfn, base, sqh,
                                                colv, lane, wave))
                 break;
         }
@@ -643,18 +645,34 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     }
 }
 
+// The instantiations that run without scratch spills (MTV tiles per wave in VGPRs, NB V
+// blocks, NLD copies per wave). Only these are compiled (quant_mtv picks among them).
+constexpr bool q_spill_free(int mtv, int nb, int nld) {
+    return mtv <= 4 || (mtv <= 8 && nb <= 3) || (mtv == 9 && nb <= (nld <= 3 ? 2 : 1)) ||
+           (mtv == 10 && nb <= (nld <= 3 ? 1 : 0));
+}
+
+template <int MTV, int NB, int NLD>
+const void* q_inst() {
+    if constexpr (q_spill_free(MTV, NB, NLD)) return (const void*)&quant_kernel<MTV, NB, NLD>;
+    return nullptr;
+}
+
 template <int MTV, int NLD>
 const void* q_pick_nb(int nb) {
-    if (nb <= 0) return (const void*)&quant_kernel<MTV, 0, NLD>;
-    if (nb <= 1) return (const void*)&quant_kernel<MTV, 1, NLD>;
-    if (nb <= 2) return (const void*)&quant_kernel<MTV, 2, NLD>;
-    if (nb <= 3) return (const void*)&quant_kernel<MTV, 3, NLD>;
-    return (const void*)&quant_kernel<MTV, 5, NLD>;
+    if (nb <= 0) return q_inst<MTV, 0, NLD>();
+    if (nb <= 1) return q_inst<MTV, 1, NLD>();
+    if (nb <= 2) return q_inst<MTV, 2, NLD>();
+    if (nb <= 3) return q_inst<MTV, 3, NLD>();
+    return q_inst<MTV, 5, NLD>();
 }
 
 template <int NLD>
-const void* q_pick_mtv(int need, int nb) {
-    return need <= 4 ? q_pick_nb<4, NLD>(nb) : need <= 8 ? q_pick_nb<8, NLD>(nb) : q_pick_nb<10, NLD>(nb);
+const void* q_pick_mtv(int mtv, int nb) {
+    return mtv == 4 ? q_pick_nb<4, NLD>(nb)
+           : mtv == 8 ? q_pick_nb<8, NLD>(nb)
+           : mtv == 9 ? q_pick_nb<9, NLD>(nb)
+                      : q_pick_nb<10, NLD>(nb);
 }
 
 int q_nb_blocks(int nb) { return nb <= 0 ? 0 : nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 3 ? 3 : 5; }
@@ -680,10 +698,25 @@ int quant_lds_bytes(int row_bytes, int nb) { return (quant_chunks(row_bytes) + 2
 
 int quant_lds_limit() { return Q_MAX_DYN_LDS; }
 
+// Rank tiles per wave held in VGPRs (as lowrank_mtv): the smallest compiled size >= need,
+// or the next smaller one if that one would spill and it still holds need - 1; 0 if
+// neither runs without spills with nb V blocks (the two-pass form then).
+int quant_mtv(int TT, int nb, int row_bytes) {
+    static const int sizes[4] = {4, 8, 9, 10};
+    const int need = (TT + NWAVE - 1) / NWAVE, nld = quant_copies(row_bytes), nbv = q_nb_blocks(nb);
+    int i = 0;
+    while (i < 3 && sizes[i] < need) ++i;
+    if (q_spill_free(sizes[i], nbv, nld)) return sizes[i];
+    if (i > 0 && sizes[i - 1] >= need - 1 && q_spill_free(sizes[i - 1], nbv, nld)) return sizes[i - 1];
+    return 0;
+}
+
 int launch_quant(const DecodeParams& p, int nb, int grid, hipStream_t stream) {
-    const int need = (p.TT + NWAVE - 1) / NWAVE;
+    const int mtv = quant_mtv(p.TT, nb, p.row_g * 16);
     const int nld = quant_copies(p.row_g * 16);
-    const void* fn = nld <= 3 ? q_pick_mtv<3>(need, nb) : q_pick_mtv<6>(need, nb);
+    SKV_CHECK(mtv > 0, "decode: no spill-free kernel for %d rank tiles and %d V blocks", p.TT, nb);
+    const void* fn = nld <= 3 ? q_pick_mtv<3>(mtv, nb) : q_pick_mtv<6>(mtv, nb);
+    SKV_CHECK(fn != nullptr, "decode: no kernel for %d rank tiles and %d V blocks", p.TT, nb);
     static const void* raised[256];  // kernels whose dynamic-LDS limit was raised (host-side bookkeeping)
     static int nraised = 0;
     bool seen = false;

@@ -56,7 +56,7 @@ SIGNATURES = {
     "starkv_profile_end": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "starkv_profile_times": (_I, [ctypes.POINTER(ctypes.c_double), _I]),
     "starkv_decode_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I, _I, _I]),
-    "starkv_decode_two_pass": (_I, [_I, _I, _I, _I]),
+    "starkv_decode_two_pass": (_I, [_I, _I, _I, _I, _I]),
     "starkv_decode_set_path": (_I, [_I]),
     "starkv_decode_layer_fits": (_I, [_I, _I, _I, ctypes.POINTER(ctypes.c_int32), _I]),
     "starkv_lowrank_decode": (_I, [_P, _P, _I64, _I64, _I, _P, _I64, _I64, _I, _I, _P, _I64, _I64, _P, _I,

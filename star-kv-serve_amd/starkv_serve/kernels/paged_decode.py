@@ -95,17 +95,19 @@ def _rows_for(two: bool, num_heads: int, max_seq_len: int) -> int:
     return rows
 
 
-def rows_per_launch(cache_kind: int, num_heads: int, k_width: int, v_rank: int, max_seq_len: int) -> int:
+def rows_per_launch(cache_kind: int, num_heads: int, num_kv_heads: int, k_width: int, v_rank: int,
+                    max_seq_len: int) -> int:
     """Requests per library call: at most 1024, and for two-pass decodes at most
     MAX_LOGITS_PER_LAUNCH logits."""
-    key = (cache_kind, num_heads, k_width, v_rank, _hip.decode_path_epoch)
+    key = (cache_kind, num_heads, num_kv_heads, k_width, v_rank, _hip.decode_path_epoch)
     two = _two_pass.get(key)
     if two is None:
-        two = _two_pass[key] = bool(_hip.lib().starkv_decode_two_pass(cache_kind, num_heads, k_width, v_rank))
+        two = _two_pass[key] = bool(_hip.lib().starkv_decode_two_pass(cache_kind, num_heads, num_kv_heads, k_width,
+                                                                      v_rank))
     return _rows_for(two, num_heads, max_seq_len)
 
 
-_two_pass = {}  # (cache kind, H, k_width, v_rank, path epoch) -> which decode form the library picks
+_two_pass = {}  # (cache kind, H, H_kv, k_width, v_rank, path epoch) -> which decode form the library picks
 
 
 def kv_head_groups(cache_kind: int, num_heads: int, k_ranks, v_rank: int) -> list:
@@ -225,7 +227,7 @@ def paged_starkv_decode(
                           v_up_by_q[per * g0:per * g1], per * (g1 - g0), g1 - g0, kw))
     for qg, og, cg, kug, krg, kog, vug, hq, hkv, kw in parts:
         v_col = k_width - (cg.data_ptr() - kv_cache.data_ptr()) // kv_cache.element_size()
-        step = rows_per_launch(kind, hq, kw, v_rank, max_seq_len)
+        step = rows_per_launch(kind, hq, hkv, kw, v_rank, max_seq_len)
         if step >= n:
             ops.lowrank_decode(qg, cg, block_table, seq_lens, max_seq_len, kug, krg, kog, kw, v_col, vug, cs, scale,
                                og)

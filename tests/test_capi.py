@@ -67,13 +67,21 @@ def test_two_pass_selection():
     from starkv_serve import _hip
     L = _hip.lib()
     BF16, F16, Q = _hip.BF16, _hip.F16, _hip.CACHE_Q3_2
-    assert L.starkv_decode_two_pass(BF16, 32, 1280, 64) == 0
-    assert L.starkv_decode_two_pass(BF16, 32, 1280, 256) == 0
-    assert L.starkv_decode_two_pass(BF16, 32, 880, 272) == 1
-    assert L.starkv_decode_two_pass(F16, 32, 880, 1280) == 1
-    assert L.starkv_decode_two_pass(Q, 32, 1280, 64) == 0
-    assert L.starkv_decode_two_pass(Q, 32, 880, 256) == 0      # 51 outliers (padded to 52) + 205 inliers: 5 blocks
-    assert L.starkv_decode_two_pass(Q, 32, 880, 1290) == 1
+    assert L.starkv_decode_two_pass(BF16, 32, 32, 1280, 64) == 0
+    # V rank 256 in one pass needs all of a wave's tiles in registers next to four V blocks:
+    # spill-free up to 8 tiles per wave (K width 1024), two passes at 10 (K width 1280)
+    assert L.starkv_decode_two_pass(BF16, 32, 32, 1024, 256) == 0
+    assert L.starkv_decode_two_pass(BF16, 32, 32, 1280, 256) == 1
+    assert L.starkv_decode_two_pass(BF16, 32, 32, 1120, 64) == 0      # 9 tiles per wave, one V block
+    assert L.starkv_decode_two_pass(Q, 32, 32, 1232, 64) == 0         # 10 tiles: 9 in registers, 1 streamed
+    assert L.starkv_decode_two_pass(BF16, 32, 32, 880, 272) == 1
+    assert L.starkv_decode_two_pass(F16, 32, 32, 880, 1280) == 1
+    assert L.starkv_decode_two_pass(Q, 32, 32, 1280, 64) == 0
+    # V rank 256: 51 outliers (padded to 52) + 205 inliers, 5 blocks: one pass with 4 tiles
+    # per wave (K width 512), two passes with 7 (K width 880: 8 tiles and 5 V blocks spill)
+    assert L.starkv_decode_two_pass(Q, 32, 32, 512, 256) == 0
+    assert L.starkv_decode_two_pass(Q, 32, 32, 880, 256) == 1
+    assert L.starkv_decode_two_pass(Q, 32, 32, 880, 1290) == 1
     # two-pass workspaces add the fp32 logits [n, H, max_seq_len rounded up to 16] (and a
     # page record per request for the 17th page)
     one = L.starkv_decode_workspace_bytes(BF16, 64, 32, 32, 880, 1280, 8192, 256)
@@ -83,9 +91,9 @@ def test_two_pass_selection():
     # forcing a form
     assert _hip.set_decode_path(2) == 0
     try:
-        assert L.starkv_decode_two_pass(BF16, 32, 1280, 64) == 1
+        assert L.starkv_decode_two_pass(BF16, 32, 32, 1280, 64) == 1
         assert L.starkv_decode_set_path(1) == 2
-        assert L.starkv_decode_two_pass(BF16, 32, 880, 1280) == 0
+        assert L.starkv_decode_two_pass(BF16, 32, 32, 880, 1280) == 0
         assert L.starkv_decode_set_path(7) == -1 and b"mode 7" in L.starkv_last_error()
     finally:
         _hip.set_decode_path(0)
@@ -209,3 +217,18 @@ def test_prefill_block_list_host():
     rc = L.starkv_prefill_attention(None, None, 0, 0, 2, None, None, 0, 0, 1, None, None, 1, 32, 32, 64, 0.1, None,
                                     0, 0, 2)
     assert rc != 0 and b"null pointer" in L.starkv_last_error()
+
+
+def test_build_rejects_kernels_that_spill():
+    """The build reads hipcc's kernel resource report and refuses scratch spills: the parse
+    finds the kernels with a nonzero ScratchSize and only those."""
+    import build
+    report = "\n".join([
+        "x.hip:1:1: remark: Function Name: _Z1av [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     VGPRs: 256 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     ScratchSize [bytes/lane]: 16 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark: Function Name: _Z1bv [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert build._spills(report) == [("_Z1av", 16)]
+    assert build._spills("") == []

@@ -325,7 +325,7 @@ def test_quant_group_geometry_matches_whole_layer_queries():
             assert (L.starkv_quant_group_workspace_bytes(n, W, H_, rv, 0, H_, 0, W, span, grid) ==
                     L.starkv_decode_workspace_bytes(_hip.CACHE_Q3_2, n, H_, H_, W, rv, span, grid))
         assert (L.starkv_quant_group_two_pass(W, H_, rv, 0, H_, 0, W) ==
-                L.starkv_decode_two_pass(_hip.CACHE_Q3_2, H_, W, rv))
+                L.starkv_decode_two_pass(_hip.CACHE_Q3_2, H_, H_, W, rv))
     # a group past the layer's heads or lanes, or a lane offset that is not a tile, is refused
     assert L.starkv_quant_group_workspace_bytes(1, 1232, 32, 64, 30, 4, 0, 64, 100, 1) == 0
     assert L.starkv_quant_group_workspace_bytes(1, 1232, 32, 64, 0, 4, 8, 64, 100, 1) == 0

@@ -421,7 +421,8 @@ def test_lowrank_wide_v_vs_oracle(cuda, name):
     print(f"\n[lowrank wide] case={name} lengths={lengths[:8]} {kw}", flush=True)
     nh = kw.pop("num_heads", 32)
     wl = W.make_lowrank(lengths, num_heads=nh, seed=300 + len(name), **kw)
-    two = _hip.lib().starkv_decode_two_pass(_hip.dtype_code(wl.kv_cache), nh, wl.k_width, wl.v_rank)
+    two = _hip.lib().starkv_decode_two_pass(_hip.dtype_code(wl.kv_cache), nh, wl.k_ranks.numel(), wl.k_width,
+                                            wl.v_rank)
     assert two == 1, (wl.k_width, wl.v_rank)
     out = paged_starkv_decode(*wl.to(cuda).decode_args())
     torch.cuda.synchronize()
@@ -449,7 +450,7 @@ def test_quant_wide_v_vs_oracle(cuda, name):
     print(f"\n[quant wide] case={name} lengths={lengths[:8]} {kw}", flush=True)
     nh = kw.pop("num_heads", 32)
     wl = W.make_quant(lengths, num_heads=nh, seed=400 + len(name), device=cuda, **kw)
-    two = _hip.lib().starkv_decode_two_pass(_hip.CACHE_Q3_2, nh, wl.k_width, wl.v_rank)
+    two = _hip.lib().starkv_decode_two_pass(_hip.CACHE_Q3_2, nh, nh, wl.k_width, wl.v_rank)
     assert two == 1, (wl.k_width, wl.v_rank)
     check_packed_rows(wl)
     out = paged_quant_decode(*wl.decode_args())
