@@ -139,8 +139,8 @@ int starkv_decode_grid_for(int cache_kind, int n, int num_heads, int num_kv_head
                            int max_seq_len);
 
 /*
- * Workspace bytes a decode call needs: the token prefix sums, the wave plan, the
- * q-folded bases (4 KiB per request and 16-lane rank tile), the split-K partials
+ * Workspace bytes a decode call needs: the page prefix sums, the page records (16 bytes
+ * per request and page of max_seq_len), the wave plan, the q-folded bases (4 KiB per request and 16-lane rank tile), the split-K partials
  * ((grid + n) x num_heads x (v_rank + 2) fp32) and, for the two-pass form, the logits
  * (n x num_heads x max_seq_len rounded up to 16, fp32). cache_kind: STARKV_BF16,
  * STARKV_F16 or STARKV_CACHE_Q3_2 (num_kv_heads = num_heads). 0 for invalid sizes.

@@ -3,10 +3,11 @@
 Drop-in for the reference's ``starkv_serve/kernels/paged_decode.py``: same function,
 same arguments and meaning, same result (``[n, H_q, head_dim]`` in ``v_up_by_q``'s
 dtype). The work runs in the HIP library (``libstarkv_hip.so``, launched through
-``torch.ops.starkv.lowrank_decode``) on the current stream: a prep launch (token prefix sums and wave plan in one workgroup, the query
-folded into each head's basis in the others), one persistent decode kernel that
-streams every cache page once through LDS with the K logits on MFMA and split-K
-partials, and a merge that also lifts the low-rank output through ``v_up_by_q``. No host
+``torch.ops.starkv.lowrank_decode``) on the current stream: a prep launch (page prefix
+sums, wave plan, the query folded into each head's basis, and one 16-byte record per
+cache page: its address, index and row count), one persistent decode kernel that streams
+every cache page once through LDS, equal page ranges per workgroup, with the K logits on
+MFMA and split-K partials, and a merge that also lifts the low-rank output through ``v_up_by_q``. No host
 synchronisation; the grid is a function of ``(n, max_seq_len)`` only, so the call can be
 graph-captured.
 
