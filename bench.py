@@ -341,9 +341,13 @@ def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, mod
     uncompressed and compress the others at the 0.75 ratio (K ranks, multiples of 16, keep
     ~21.5 % of K; V rank, a multiple of 32, ~31.5 % of V: 880 and 1280 here), their factors
     written to a fused checkpoint and read back with load_fused_checkpoint; "stock" keeps
-    every layer uncompressed. Sessions hold `context` tokens of synthetic cache rows (the
-    3.2-bit rows packed from random hidden states through the write path) and decode
-    `steps` tokens each, one token per session per step. Concurrency 1 and the most
+    every layer uncompressed. At concurrency 1 the session's cache comes from its prompt: one
+    prefill_step over `context` random tokens (TTFT = its median time over 2 runs after 1;
+    compressed layers write their codes and run the dense prefill, full layers write K/V and
+    run causal attention), and decoding starts from the prompt's greedy next token. At the
+    most sessions the caches hold `context` tokens of synthetic rows (the 3.2-bit rows
+    packed from random hidden states through the write path). Each session decodes `steps`
+    tokens, one token per session per step. Concurrency 1 and the most
     sessions whose caches fit in the GPU's free memory (less `reserve_gb`). Per mode and
     concurrency: TPOT (median step), tok/s = sessions / TPOT, and attention per step (the
     KV writes and attention of all 32 layers, timed on their own, as bench_serving.py:62-115
@@ -373,7 +377,22 @@ def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, mod
         model.allocate_kv_cache(n * pages + 1)
         gg = torch.Generator(device=dev).manual_seed(seed + n)
         bt = (torch.randperm(n * pages, device=dev, generator=gg) + 1).to(torch.int32).view(n, pages)
-        for li, layer in enumerate(model.layers):
+        prefill = {}
+        if n == 1:  # the session's cache from its prompt
+            prompt = torch.randint(0, shape.vocab_size, (context,), device=dev, generator=gg)
+            pmd, ppos = M.prefill_metadata(bt, [context], 16)
+            times = []
+            for i in range(3):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                plog = model.prefill_step(prompt, ppos, pmd)
+                b.record()
+                torch.cuda.synchronize()
+                times.append(a.elapsed_time(b))
+            ttft = statistics.median(times[1:])
+            prefill = dict(ttft_ms=round(ttft, 2), prefill_tok_per_s=round(context / ttft * 1e3, 1))
+            log(f"  prefill of one {context}-token prompt: {ttft:.1f} ms")
+        for li, layer in enumerate(model.layers if n > 1 else []):
             c = model.kv_caches[li]
             if not layer.compressed:
                 c[0].normal_(generator=gg)
@@ -389,7 +408,7 @@ def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, mod
                     layer.impl.write_from_hidden(hid.to(torch.bfloat16), c, slots[a:a + 4096])
                 for sess in range(1, n):
                     c[bt[sess, :pc].long()] = c[bt[0, :pc].long()]
-        tokens0 = torch.randint(0, shape.vocab_size, (n,), device=dev, generator=gg)
+        tokens0 = plog.argmax(-1) if n == 1 else torch.randint(0, shape.vocab_size, (n,), device=dev, generator=gg)
         pos0 = torch.full((n,), context, device=dev, dtype=torch.long)
         torch.cuda.synchronize()
 
@@ -429,7 +448,8 @@ def bench_model(context=16384, steps=32, warm=3, seed=4000, reserve_gb=24.0, mod
             model.attention_only(hid, ins, md, in_graph=True)
         attn = timed(ag.replay, warm + 5)
         del ag
-        out = dict(sessions=n, tpot_ms=round(tpot, 3), tok_per_s=round(n / tpot * 1e3, 1),
+        out = dict(sessions=n, cache_from="prompt prefill" if n == 1 else "synthetic rows", **prefill,
+                   tpot_ms=round(tpot, 3), tok_per_s=round(n / tpot * 1e3, 1),
                    attention_us_per_step=round(attn * 1e3, 1), tpot_ms_eager=round(tpot_eager, 3),
                    tok_per_s_eager=round(n / tpot_eager * 1e3, 1), attention_us_per_step_eager=round(attn_eager * 1e3, 1),
                    kv_cache_gb=round(n * pages * 16 * model.cache_bytes_per_token() / 1e9, 2))

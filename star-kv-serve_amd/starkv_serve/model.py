@@ -19,10 +19,13 @@ keep full K/V.
 
 The weights of everything but the attention factors are random-init here (the harness
 measures decode steps; there is no network for real checkpoints). The factors come from
-a fused checkpoint through ``load_fused_checkpoint``, as the reference loads them. Decode
-batches only: every request contributes its one next token (the reference serves
-prompts through its dense prefill, attention.py:219-251, which StarKVAttentionImpl also
-implements).
+a fused checkpoint through ``load_fused_checkpoint``, as the reference loads them.
+
+Two kinds of step: ``decode_step`` (every request contributes its one next token) and
+``prefill_step`` (whole prompts, each from position 0, as the reference serves them: a
+compressed layer writes the prompt's codes and runs its dense prefill,
+attention.py:219-251; a full layer writes K/V and runs causal attention over the prompt,
+here on this library's prefill kernel where vLLM would run FlashAttention).
 """
 import math
 from dataclasses import dataclass
@@ -33,6 +36,7 @@ import torch.nn.functional as F
 
 from starkv_serve.attention import StarKVAttentionImpl, StarKVMetadata
 from starkv_serve.checkpoint import StarKVCheckpoint
+from starkv_serve.kernels.prefill import prefill_attention
 from starkv_serve.kernels.stock_decode import paged_decode_full, write_kv_full
 from starkv_serve.workloads import cos_sin_table
 
@@ -162,6 +166,7 @@ class StarKVLlamaForCausalLM:
         s, layer = self.shape, self.layers[li]
         T = h.shape[0]
         H, Hkv, D = s.num_heads, s.num_kv_heads, s.head_dim
+        k = v = None
         if layer.compressed:
             q = self.rotary.apply(positions, F.linear(h, layer.q_proj).view(T, H, D))
             out = torch.empty(T, H * D, dtype=self.dtype, device=self.device)
@@ -171,12 +176,17 @@ class StarKVLlamaForCausalLM:
             q, k, v = qkv.split([H * D, Hkv * D, Hkv * D], dim=-1)
             q = self.rotary.apply(positions, q.reshape(T, H, D))
             k = self.rotary.apply(positions, k.reshape(T, Hkv, D))
+            v = v.reshape(T, Hkv, D)
             kc, vc = self.kv_caches[li]
-            write_kv_full(k, v.reshape(T, Hkv, D), kc, vc, md.slot_mapping[:T])
-            span = self.max_model_len if in_graph else max(md.max_seq_len, 1)
-            out = paged_decode_full(q, kc, vc, md.block_table[:T], md.seq_lens[:T], span, self.scale).view(T, H * D)
+            write_kv_full(k, v, kc, vc, md.slot_mapping[:T])
+            if md.num_prefills:  # whole prompts only (prefill_step): causal attention over each prompt
+                out = prefill_attention(q, k, v, md.prefill_seq_lens_cpu, self.scale).view(T, H * D)
+            else:
+                span = self.max_model_len if in_graph else max(md.max_seq_len, 1)
+                out = paged_decode_full(q, kc, vc, md.block_table[:T], md.seq_lens[:T], span,
+                                        self.scale).view(T, H * D)
         if capture is not None:
-            capture.append(dict(layer=li, q=q.view(T, H, D), out=out.view(T, H, D)))
+            capture.append(dict(layer=li, q=q.view(T, H, D), out=out.view(T, H, D), h=h, k=k, v=v))
         return F.linear(out, layer.o_proj)
 
     @torch.no_grad()
@@ -220,20 +230,40 @@ class StarKVLlamaForCausalLM:
                 paged_decode_full(q, kc, vc, md.block_table[:T], md.seq_lens[:T], span, self.scale)
 
     @torch.no_grad()
-    def decode_step(self, tokens: torch.Tensor, positions: torch.Tensor, md: StarKVMetadata,
-                    capture: Optional[list] = None, in_graph: bool = False) -> torch.Tensor:
-        """Logits [n, vocab] for one new token per request: tokens [n] at `positions` [n];
-        `md` has every row as a decode (seq_lens = positions + 1, slot_mapping the new
-        tokens' slots)."""
+    def _layers(self, x: torch.Tensor, positions: torch.Tensor, md: StarKVMetadata, capture: Optional[list],
+                in_graph: bool) -> torch.Tensor:
         s = self.shape
-        x = self.embed[tokens]
         for li, layer in enumerate(self.layers):
             h = F.rms_norm(x, (s.hidden_size,), layer.ln1, s.rms_norm_eps)
             x = x + self._attention(li, h, positions, md, capture, in_graph)
             h = F.rms_norm(x, (s.hidden_size,), layer.ln2, s.rms_norm_eps)
             gate, up = F.linear(h, layer.gate_up).chunk(2, dim=-1)
             x = x + F.linear(F.silu(gate) * up, layer.down)
+        return x
+
+    def _logits(self, x: torch.Tensor) -> torch.Tensor:
+        s = self.shape
         return F.linear(F.rms_norm(x, (s.hidden_size,), self.norm, s.rms_norm_eps), self.lm_head)
+
+    def decode_step(self, tokens: torch.Tensor, positions: torch.Tensor, md: StarKVMetadata,
+                    capture: Optional[list] = None, in_graph: bool = False) -> torch.Tensor:
+        """Logits [n, vocab] for one new token per request: tokens [n] at `positions` [n];
+        `md` has every row as a decode (seq_lens = positions + 1, slot_mapping the new
+        tokens' slots)."""
+        return self._logits(self._layers(self.embed[tokens], positions, md, capture, in_graph))
+
+    @torch.no_grad()
+    def prefill_step(self, tokens: torch.Tensor, positions: torch.Tensor, md: StarKVMetadata,
+                     capture: Optional[list] = None) -> torch.Tensor:
+        """Logits [P, vocab] at the last token of each of P whole prompts: tokens [T] and
+        positions [T] (0 .. L - 1 per prompt) laid end to end, `md` from
+        ``prefill_metadata``. Every layer writes the prompts' cache rows (compressed: the
+        codes through the fused write; full: K and V), so decode steps can follow."""
+        if md.num_decodes or not md.num_prefills:
+            raise ValueError("prefill_step: a prompts-only batch (prefill_metadata)")
+        x = self._layers(self.embed[tokens], positions, md, capture, False)
+        last = torch.tensor(md.prefill_query_start_loc_cpu[1:], device=x.device) - 1
+        return self._logits(x[last])
 
 
 class DecodeGraph:
@@ -288,6 +318,30 @@ def decode_metadata(block_table: torch.Tensor, positions: torch.Tensor, block_si
     return StarKVMetadata(num_actual_tokens=n, num_decodes=n, num_decode_tokens=n, num_prefills=0,
                           max_seq_len=int(max_seq_len), seq_lens=(positions + 1).to(torch.int32),
                           block_table=block_table, slot_mapping=slots)
+
+
+def prefill_metadata(block_table: torch.Tensor, prompt_lens: List[int], block_size: int):
+    """A prompts-only batch's metadata and positions: prompt b's tokens at positions
+    0 .. L_b - 1, their slots from block-table row b, laid end to end. Returns (md,
+    positions [T])."""
+    lens = [int(L) for L in prompt_lens]
+    if not lens or min(lens) < 1:
+        raise ValueError("prefill_metadata: every prompt needs at least one token")
+    if max(lens) > block_table.shape[1] * block_size:
+        raise ValueError(f"a prompt of {max(lens)} tokens needs more than the block table's "
+                         f"{block_table.shape[1]} blocks of {block_size}")
+    dev = block_table.device
+    rows = torch.cat([torch.full((L,), b, dtype=torch.long) for b, L in enumerate(lens)]).to(dev)
+    positions = torch.cat([torch.arange(L) for L in lens]).to(dev)
+    slots = block_table[rows, positions // block_size].long() * block_size + positions % block_size
+    qsl = [0]
+    for L in lens:
+        qsl.append(qsl[-1] + L)
+    md = StarKVMetadata(num_actual_tokens=qsl[-1], num_decodes=0, num_decode_tokens=0, num_prefills=len(lens),
+                        max_seq_len=max(lens), seq_lens=torch.tensor(lens, dtype=torch.int32, device=dev),
+                        block_table=block_table, slot_mapping=slots, prefill_seq_lens_cpu=lens,
+                        prefill_query_start_loc_cpu=qsl)
+    return md, positions
 
 
 def ranks_for_ratio(num_kv_heads: int, head_dim: int, keep: float, multiple: int, generator: torch.Generator):

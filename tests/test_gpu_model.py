@@ -46,6 +46,28 @@ def full_attention_truth(q, kc, vc, bt, seq_lens, scale):
     return out
 
 
+def decode_layer_truth(model, c, bt_host, seq):
+    """float64 truth of one layer's decode output `c` (a decode_step capture entry) over
+    the layer's cache as the step left it: oracle/ref.py's decode for a compressed layer
+    (bf16 codes or 3.2-bit rows), softmax attention over the gathered K/V for a full one."""
+    li, layer = c["layer"], model.layers[c["layer"]]
+    if not layer.compressed:
+        kc, vc = model.kv_caches[li]
+        return full_attention_truth(c["q"], kc, vc, bt_host, seq, model.scale)
+    imp = layer.impl
+    q = c["q"].float().cpu().numpy()
+    vq = imp.v_up_by_q.float().cpu().numpy()
+    cs = imp.rotary_emb.cos_sin_cache.float().cpu().numpy()
+    ranks = imp.w.k_head_ranks.tolist()
+    if imp.row is None:
+        cache = model.kv_caches[li].float().cpu().numpy()
+        return ref.lowrank_decode(q, cache, bt_host, seq, int(seq.max()), imp.k_up.float().cpu().numpy(), ranks,
+                                  imp.k_head_offsets.tolist(), imp.k_width, vq, cs, imp.scale)
+    lay = ref.row_layout(imp.k_width, len(ranks), imp.w.v_rank)
+    return ref.quant_decode(q, model.kv_caches[li].cpu().numpy(), bt_host, seq, int(seq.max()), lay, ranks,
+                            imp.k_up.float().cpu().numpy(), vq, cs, imp.scale)
+
+
 def build(cuda, tmp_path, kv_quant, stock=False):
     path = str(tmp_path / "fused_weights.pt")
     comp = {1: ([16, 32, 16, 48], 64), 2: ([32, 16, 16, 16], 96)}
@@ -96,26 +118,7 @@ def test_model_decode_steps_against_oracle(cuda, tmp_path, kv_quant):
         seq = (positions + 1).cpu().numpy()
         assert [c["layer"] for c in cap] == [0, 1, 2, 3]
         for c in cap:
-            li, layer = c["layer"], model.layers[c["layer"]]
-            if layer.compressed:
-                imp = layer.impl
-                q = c["q"].float().cpu().numpy()
-                vq = imp.v_up_by_q.float().cpu().numpy()
-                cs = imp.rotary_emb.cos_sin_cache.float().cpu().numpy()
-                if imp.row is None:
-                    cache = model.kv_caches[li].float().cpu().numpy()
-                    truth = ref.lowrank_decode(q, cache, bt_host, seq, int(seq.max()), imp.k_up.float().cpu().numpy(),
-                                               imp.w.k_head_ranks.tolist(), imp.k_head_offsets.tolist(), imp.k_width,
-                                               vq, cs, imp.scale)
-                else:
-                    lay = ref.row_layout(imp.k_width, 4, imp.w.v_rank)
-                    truth = ref.quant_decode(q, model.kv_caches[li].cpu().numpy(), bt_host, seq, int(seq.max()),
-                                             lay, imp.w.k_head_ranks.tolist(), imp.k_up.float().cpu().numpy(), vq,
-                                             cs, imp.scale)
-            else:
-                kc, vc = model.kv_caches[li]
-                truth = full_attention_truth(c["q"], kc, vc, bt_host, seq, model.scale)
-            assert_close(c["out"], truth, f"step {step} layer {li}")
+            assert_close(c["out"], decode_layer_truth(model, c, bt_host, seq), f"step {step} layer {c['layer']}")
         tokens = logits.argmax(-1)
 
 
