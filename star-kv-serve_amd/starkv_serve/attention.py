@@ -200,7 +200,8 @@ class StarKVAttentionImpl:
         # The decode kernels read an fp16 cos/sin table: converted once here, not per step.
         self.cos_sin16 = self.rotary_emb.cos_sin_cache.to(device=device, dtype=torch.float16).contiguous()
         self.k_up_T = k_up_pad.to(device=device, dtype=torch.float32).contiguous()
-        self.v_up = w.v_up.to(device=device, dtype=torch.float32).contiguous()  # [H * Hd, v_rank]
+        # V's lift runs as an fp16 GEMM (fp32 accumulation, the result rounded once to fp16).
+        self.v_up_f16 = w.v_up.to(device=device, dtype=torch.float16).contiguous()  # [H * Hd, v_rank]
 
     def _cache(self, kv_cache: torch.Tensor) -> torch.Tensor:
         cache = kv_cache.squeeze(1) if kv_cache.dim() == 4 else kv_cache  # [num_blocks, block_size, width]
@@ -256,8 +257,9 @@ class StarKVAttentionImpl:
     def _dense_prefill(self, query_lens: List[int], q: torch.Tensor, k_codes: torch.Tensor, v_codes: torch.Tensor,
                        out: torch.Tensor) -> None:
         """STAR-KV's prefill (attention.py:219-251): K = RoPE(codes @ U) and V = codes @
-        v_up for this step's tokens (positions from 0 in every prompt), lifted in fp32 and
-        rounded once to fp16, then causal attention of every prompt to itself on this
+        v_up for this step's tokens (positions from 0 in every prompt), each rounded once
+        to fp16 (K lifted and rotated in fp32; V as an fp16 GEMM of the codes and v_up in
+        fp16, accumulated in fp32), then causal attention of every prompt to itself on this
         library's prefill kernel. q and out [T, H_q, 128]."""
         T = q.shape[0]
         H, R, Hd = self.num_kv_heads, self.w.k_max_rank, self.head_size
@@ -268,7 +270,7 @@ class StarKVAttentionImpl:
         cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
         k1, k2 = k.chunk(2, dim=-1)
         k = torch.cat([k1 * cos - k2 * sin, k2 * cos + k1 * sin], dim=-1).to(torch.float16)
-        v = F.linear(v_codes.float(), self.v_up).view(T, H, Hd).to(torch.float16)
+        v = F.linear(v_codes.to(torch.float16), self.v_up_f16).view(T, H, Hd)
         prefill_attention(q, k, v, query_lens, self.scale, out=out)
 
     def write_from_hidden(self, hidden: torch.Tensor, kv_cache: torch.Tensor, slot_mapping: torch.Tensor,

@@ -8,7 +8,9 @@ Pins:
 - bf16/fp16 cache rows are those codes bit for bit; other slots are untouched;
 - 3.2-bit rows equal the C oracle's packing (bit for bit kv_quant._q) of those codes
   on [0, vq_off + v_bytes), and the pad bytes are 0;
-- slot -1 writes the null block 0; slots past the cache are skipped.
+- slot -1 writes the null block 0; slots past the cache are skipped;
+- the same for a prompt's many tokens (above FUSED_MAX_TOKENS: the codes from F.linear,
+  then the store kernels).
 """
 import math
 
@@ -65,7 +67,8 @@ def _slots(n, num_blocks, gen):
 
 @pytest.mark.parametrize("n,hidden,dtype", [(1, 4096, torch.bfloat16), (37, 4096, torch.bfloat16),
                                             (64, 4096, torch.bfloat16), (130, 4096, torch.bfloat16),
-                                            (9, 3072, torch.bfloat16), (21, 4096, torch.float16)])
+                                            (9, 3072, torch.bfloat16), (21, 4096, torch.float16),
+                                            (600, 4096, torch.bfloat16), (257, 4096, torch.float16)])
 def test_write_kv_codes_and_cache(cuda, n, hidden, dtype):
     print(f"\n[write_kv] n={n} hidden={hidden} dtype={dtype}", flush=True)
     w, ops = _layer(cuda, hidden, False, dtype)
@@ -91,7 +94,7 @@ def test_write_kv_codes_and_cache(cuda, n, hidden, dtype):
     assert torch.equal(flat[rest].view(torch.int16), before.reshape(-1, w.cache_width)[rest].view(torch.int16))
 
 
-@pytest.mark.parametrize("n", [1, 37, 64])
+@pytest.mark.parametrize("n", [1, 37, 64, 600])
 def test_write_kv_quant_rows(cuda, n):
     print(f"\n[write_kv quant] n={n}", flush=True)
     w, ops = _layer(cuda, 4096, True, torch.bfloat16)
