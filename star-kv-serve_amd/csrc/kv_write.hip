@@ -140,31 +140,32 @@ __device__ __forceinline__ float code_value(uint16_t r) {
     else return (float)__builtin_bit_cast(_Float16, r);
 }
 
-template <int DT>
+// S = the GEMM's K splits (a launch constant): exactly the S partials of each column load.
+// CPT columns per thread and pass (2, or 3 for rows wider than 2048 codes: one pass).
+template <int DT, int S, int CPT>
 __global__ __launch_bounds__(KVS_THR) void kv_store_kernel(const KvStoreParams p) {
     extern __shared__ float s_code[];  // [width]: the token's rounded codes
     const int i = blockIdx.x, tid = threadIdx.x;
     const int64_t slot = load_slot(p.slots, p.slot_bits, i);
     const bool store = slot < p.num_blocks * p.block_size;  // slots past the cache are skipped
     const int64_t row = (slot / p.block_size) * p.c_s0 + (slot % p.block_size) * p.c_s1;
-    // Columns c0 + tid and c0 + tid + KVS_THR: every split's partial of both is loaded
+    // Columns c0 + tid + j KVS_THR (j < CPT): every split's partial of each is loaded
     // before the first add (indices clamped, so no branch sits between the loads), then
     // summed in split order.
-    for (int c0 = 0; c0 < p.width; c0 += 2 * KVS_THR) {
-        float v[2][KVW_MAX_SPLIT];
+    for (int c0 = 0; c0 < p.width; c0 += CPT * KVS_THR) {
+        float v[CPT][S];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < CPT; ++j) {
             const int c = min(c0 + tid + j * KVS_THR, p.width - 1);
 #pragma unroll
-            for (int sp = 0; sp < KVW_MAX_SPLIT; ++sp)
-                v[j][sp] = p.part[((int64_t)min(sp, p.splits - 1) * p.n + i) * p.width + c];
+            for (int sp = 0; sp < S; ++sp) v[j][sp] = p.part[((int64_t)sp * p.n + i) * p.width + c];
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < CPT; ++j) {
             const int c = c0 + tid + j * KVS_THR;
             float a = v[j][0];
 #pragma unroll
-            for (int sp = 1; sp < KVW_MAX_SPLIT; ++sp) a = sp < p.splits ? a + v[j][sp] : a;
+            for (int sp = 1; sp < S; ++sp) a += v[j][sp];
             if (c < p.width) {
                 const uint16_t r = round_code<DT>(a);
                 s_code[c] = code_value<DT>(r);
@@ -189,6 +190,22 @@ __global__ __launch_bounds__(KVS_THR) void kv_store_kernel(const KvStoreParams p
                          p.row.vq_off, p.row.vs_off, p.row.nbytes, dst, lane);
         }
     }
+}
+
+template <int DT, int CPT>
+static const void* kv_store_pick_s(int splits) {
+    switch (splits) {
+        case 1: return (const void*)&kv_store_kernel<DT, 1, CPT>;
+        case 2: return (const void*)&kv_store_kernel<DT, 2, CPT>;
+        case 4: return (const void*)&kv_store_kernel<DT, 4, CPT>;
+        case 8: return (const void*)&kv_store_kernel<DT, 8, CPT>;
+        case 16: return (const void*)&kv_store_kernel<DT, 16, CPT>;
+        default: return nullptr;
+    }
+}
+template <int DT>
+static const void* kv_store_pick(int splits, int width) {
+    return width > 2 * KVS_THR ? kv_store_pick_s<DT, 3>(splits) : kv_store_pick_s<DT, 2>(splits);
 }
 
 // K splits: doubled while the GEMM grid has fewer than 256 workgroups (one per CU) and
@@ -271,16 +288,16 @@ int starkv_write_kv(void* stream, const void* hidden, int64_t h_s0, const void* 
     const size_t lds = (size_t)width * sizeof(float);
     SKV_CHECK(lds <= 64 * 1024, "write_kv: %d codes per token exceed the 64 KB LDS block", width);
     hipStream_t st = (hipStream_t)stream;
-    if (w_dtype == STARKV_BF16) {
+    if (w_dtype == STARKV_BF16)
         hipLaunchKernelGGL(kv_gemm_kernel<STARKV_BF16>, ggrid, dim3(KVW_THR), 0, st, g);
-        SKV_HIP(hipGetLastError());
-        hipLaunchKernelGGL(kv_store_kernel<STARKV_BF16>, dim3(n, s.groups), dim3(KVS_THR), lds, st, s);
-    } else {
+    else
         hipLaunchKernelGGL(kv_gemm_kernel<STARKV_F16>, ggrid, dim3(KVW_THR), 0, st, g);
-        SKV_HIP(hipGetLastError());
-        hipLaunchKernelGGL(kv_store_kernel<STARKV_F16>, dim3(n, s.groups), dim3(KVS_THR), lds, st, s);
-    }
     SKV_HIP(hipGetLastError());
+    const void* fn = w_dtype == STARKV_BF16 ? kv_store_pick<STARKV_BF16>(splits, width)
+                                            : kv_store_pick<STARKV_F16>(splits, width);
+    SKV_CHECK(fn != nullptr, "write_kv: %d K splits", splits);
+    void* args[] = {(void*)&s};
+    SKV_HIP(hipLaunchKernel(fn, dim3(n, s.groups), dim3(KVS_THR), args, lds, st));
     return STARKV_OK;
 }
 
