@@ -1,6 +1,6 @@
 """ORACLE -- test infrastructure only.
 
-CPU restatement of STAR-KV's paged decode path, used as the checker by ``tests/``,
+CPU restatement of STAR-KV's paged decode path, the reference results for ``tests/``,
 ``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py``. The product
 (``starkv_serve`` and its HIP library) never imports, links or calls anything here.
 

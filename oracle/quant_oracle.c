@@ -1,7 +1,7 @@
 /*
  * ORACLE -- test infrastructure only. Nothing in the product links, loads or
  * calls this file; only tests/, the smoke check and bench.py's CPU baseline do,
- * and only as the checker.
+ * and only as the reference the GPU results are compared with.
  *
  * Plain-C restatement of STAR-KV's 3.2-bit KV quantizer and its paged row
  * format, bit for bit:
