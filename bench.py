@@ -655,7 +655,7 @@ def main():
     args = ap.parse_args()
     MIN_WARMUP_MS = args.min_warmup_ms
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (decode shards by request; "
+        print("bench.py measures one GPU: the library has no multi-GPU path (decode shards by request; "
               "each GPU would run this same kernel on its own requests). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
