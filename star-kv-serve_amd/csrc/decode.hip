@@ -495,9 +495,11 @@ __global__ __launch_bounds__(PREP_THR) void prep_kernel(PrepArgs a) {
 // ---------------------------------------------------------------------------
 // 3. merge: per (request, head) the partials' log-sum-exp, then the lift through
 //    v_up_by_q. A workgroup takes one head and MERGE_REQ requests, one wave each, so
-//    every row of v_up_by_q[h] serves MERGE_REQ outputs. The loads come in two phases:
-//    the request's partial range (with v_up_by_q[h] staged into LDS meanwhile), then
-//    every partial's max and sum and the first MERGE_PRE partials' accumulator rows
+//    every row of v_up_by_q[h] serves MERGE_REQ outputs; a call of one or two requests
+//    gives each request 4 or 2 waves, which split its partials (partial k to wave k mod
+//    the waves) and add their rows before the lift. The loads come in two phases: the
+//    request's partial range (with v_up_by_q[h] staged into LDS meanwhile), then every
+//    partial's max and sum and the wave's first MERGE_PRE partials' accumulator rows
 //    together.
 // ---------------------------------------------------------------------------
 constexpr int MERGE_REQ = 4;
@@ -530,7 +532,10 @@ __global__ __launch_bounds__(MERGE_THR) void merge_kernel(const uint8_t* __restr
     WT* s_v = (WT*)s_dyn;                                     // [v_rank][128]
     float* s_o = (float*)(s_dyn + (size_t)v_rank * 128 * sizeof(WT));  // [MERGE_REQ][v_rank]
     __shared__ int s_live[MERGE_REQ];
-    const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, r = tid >> 6;
+    const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    // Requests per workgroup (grid.x is 1 when n < 3) and waves per request.
+    const int rpw = n >= 3 ? MERGE_REQ : n, wpr = MERGE_REQ / rpw;
+    const int r = (tid >> 6) / wpr, sub = (tid >> 6) % wpr;  // this wave's request and share
     const int b = blockIdx.x * MERGE_REQ + r;
     const int* hdr = (const int*)ws;
     const float* wm = (const float*)(ws + ws_m);
@@ -567,16 +572,16 @@ __global__ __launch_bounds__(MERGE_THR) void merge_kernel(const uint8_t* __restr
     const int64_t s0 = (int64_t)(k_lo + b) * Hq + h;  // slot index of partial k: s0 + k * Hq
 
     // Load phase 2: partial k = lane's max and sum, and lane's columns c = lane + 64 j of the
-    // first MERGE_PRE partials.
+    // wave's first MERGE_PRE partials (k = sub + wpr i).
     const float mk = lane < nk ? wm[s0 + (int64_t)lane * Hq] : -INFINITY;
     const float lk = lane < nk ? wl[s0 + (int64_t)lane * Hq] : 0.f;
     float pre[MERGE_PRE][MERGE_CB];
 #pragma unroll
-    for (int k = 0; k < MERGE_PRE; ++k)
+    for (int i = 0; i < MERGE_PRE; ++i)
 #pragma unroll
         for (int j = 0; j < MERGE_CB; ++j) {
-            const int c = lane + 64 * j;
-            pre[k][j] = k < nk && c < v_rank ? wa[(s0 + (int64_t)k * Hq) * v_rank + c] : 0.f;
+            const int c = lane + 64 * j, k = sub + wpr * i;
+            pre[i][j] = k < nk && c < v_rank ? wa[(s0 + (int64_t)k * Hq) * v_rank + c] : 0.f;
         }
     float M = mk;
     for (int k = lane + 64; k < nk; k += 64) M = fmaxf(M, wm[s0 + (int64_t)k * Hq]);
@@ -590,18 +595,20 @@ __global__ __launch_bounds__(MERGE_THR) void merge_kernel(const uint8_t* __restr
     l = wave_sum(l);
     float acc[MERGE_CB] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < MERGE_PRE; ++k) {
+    for (int i = 0; i < MERGE_PRE; ++i) {
+        const int k = sub + wpr * i;  // wave-uniform; below 64 (wpr <= 4)
         const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k));
 #pragma unroll
-        for (int j = 0; j < MERGE_CB; ++j) acc[j] = fmaf(pre[k][j], w, acc[j]);
+        for (int j = 0; j < MERGE_CB; ++j) acc[j] = fmaf(pre[i][j], w, acc[j]);
     }
-    // Requests spread over more than MERGE_PRE workgroups: MERGE_PRE partials' rows in
-    // flight at a time (columns past v_rank read column 0 and are never stored).
-    for (int k0 = MERGE_PRE; k0 < nk; k0 += MERGE_PRE) {
+    // Requests spread over more than wpr MERGE_PRE workgroups: MERGE_PRE of the wave's
+    // partials' rows in flight at a time (columns past v_rank read column 0 and are never
+    // stored).
+    for (int i0 = MERGE_PRE; sub + wpr * i0 < nk; i0 += MERGE_PRE) {
         float v[MERGE_PRE][MERGE_CB];
 #pragma unroll
         for (int u = 0; u < MERGE_PRE; ++u) {
-            const int64_t sl = s0 + (int64_t)min(k0 + u, nk - 1) * Hq;
+            const int64_t sl = s0 + (int64_t)min(sub + wpr * (i0 + u), nk - 1) * Hq;
 #pragma unroll
             for (int j = 0; j < MERGE_CB; ++j) {
                 const int c = lane + 64 * j;
@@ -610,7 +617,7 @@ __global__ __launch_bounds__(MERGE_THR) void merge_kernel(const uint8_t* __restr
         }
 #pragma unroll
         for (int u = 0; u < MERGE_PRE; ++u) {
-            const int k = k0 + u;
+            const int k = sub + wpr * (i0 + u);
             if (k >= nk) break;
             const float w = k < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k))
                                    : exp2f(wm[s0 + (int64_t)k * Hq] - M);
@@ -618,12 +625,30 @@ __global__ __launch_bounds__(MERGE_THR) void merge_kernel(const uint8_t* __restr
             for (int j = 0; j < MERGE_CB; ++j) acc[j] = fmaf(v[u][j], w, acc[j]);
         }
     }
+    // Row (tid >> 6) of s_o: this wave's share of request r, scaled; a request's wpr rows
+    // (rows r wpr + s) are added into row r before the lift.
     const float inv = 1.f / l;
 #pragma unroll
     for (int j = 0; j < MERGE_CB; ++j)
-        if (lane + 64 * j < v_rank) s_o[r * v_rank + lane + 64 * j] = acc[j] * inv;
-    if (lane == 0) s_live[r] = live;
+        if (lane + 64 * j < v_rank) s_o[(tid >> 6) * v_rank + lane + 64 * j] = acc[j] * inv;
+    if (lane == 0 && sub == 0) s_live[r] = live;
     __syncthreads();
+
+    if (wpr > 1) {  // rows r wpr .. r wpr + wpr - 1 into row r (r < rpw), column tid
+        float x0 = 0.f, x1 = 0.f;
+        if (tid < v_rank) {
+            for (int s2 = 0; s2 < wpr; ++s2) {
+                x0 += s_o[s2 * v_rank + tid];
+                if (rpw == 2) x1 += s_o[(wpr + s2) * v_rank + tid];
+            }
+        }
+        __syncthreads();
+        if (tid < v_rank) {
+            s_o[tid] = x0;
+            if (rpw == 2) s_o[v_rank + tid] = x1;
+        }
+        __syncthreads();
+    }
 
     // The lift through v_up_by_q[h]: thread (d, request pair) takes two requests' column d.
     const int d = tid & 127, r0 = 2 * (tid >> 7);
