@@ -82,7 +82,7 @@ constexpr int PREP_RECS = 4 * PREP_THR;  // page records per record workgroup
 struct TileTable {
     int head[MAX_TT], row[MAX_TT], valid[MAX_TT], word[MAX_TT];
     int hf[MAX_H], hn[MAX_H];
-    int rank[MAX_H], off[MAX_H];
+    int rank[MAX_H], off[MAX_H], t0[MAX_H];  // bf16/fp16 kv heads: t0 = tiles of the kv heads before
 };
 
 // Fills `tt` (every thread of the workgroup calls it; it ends with a barrier).
@@ -99,9 +99,22 @@ __device__ void tile_table(const PrepArgs& a, TileTable& tt, int tid) {
             if (tid > 0) hp = min(max(a.t_head[tid - 1] - a.head0, 0), a.Hq - 1);
             nout = min(max(a.t_nout[tid], 0), 16);
         }
-    } else if (tid < a.Hkv) {
-        tt.rank[tid] = min(max(a.k_ranks[tid], 0), 16 * MAX_TT);
-        tt.off[tid] = a.k_offsets[tid];
+    } else if (tid < 64) {
+        // Wave 0: the kv heads' ranks and offsets, and the tiles before each kv head (all
+        // its query heads'), an exclusive lane scan (Hkv <= 32 lanes).
+        const int R = tid < a.Hkv ? min(max(a.k_ranks[tid], 0), 16 * MAX_TT) : 0;
+        if (tid < a.Hkv) {
+            tt.rank[tid] = R;
+            tt.off[tid] = a.k_offsets[tid];
+        }
+        const int v = (a.Hq / a.Hkv) * ((R + 15) >> 4);
+        int incl = v;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (tid >= o) incl += y;
+        }
+        if (tid < a.Hkv) tt.t0[tid] = incl - v;
     }
     if (tid < MAX_TT) {
         tt.head[tid] = 0;
@@ -125,8 +138,7 @@ __device__ void tile_table(const PrepArgs& a, TileTable& tt, int tid) {
         }
     } else if (tid < a.Hq) {
         const int grp = a.Hq / a.Hkv, kv = tid / grp;
-        int t0 = 0;  // tiles of the query heads before this one: whole groups, then this group's
-        for (int k = 0; k < kv; ++k) t0 += grp * ((tt.rank[k] + 15) >> 4);
+        int t0 = tt.t0[kv];  // tiles of the query heads before this one: whole groups, then this group's
         const int R = tt.rank[kv], o = tt.off[kv];
         const int nt = (R + 15) >> 4;
         t0 += (tid - kv * grp) * nt;
@@ -250,13 +262,17 @@ __device__ void prep_plan(const PrepArgs& a, const TileTable& tt, int tid) {
     __shared__ int s_load[NWAVE];  // tiles per decode wave
     __shared__ int s_plan[NWAVE * PLAN_STRIDE + 1];
     const int lane = tid & 63, wave = tid >> 6;
-    // Heads by decreasing tile count (ties: lower head first).
-    if (tid < a.Hq) {
-        const int mine = tt.hn[tid];
+    // Heads by decreasing tile count (ties: lower head first): lane h of wave 0 counts
+    // the heads before head h, every head's count read across lanes.
+    if (wave == 0) {
+        const int mine = lane < a.Hq ? tt.hn[lane] : 0;
         int pos = 0;
-#pragma unroll 8
-        for (int h = 0; h < a.Hq; ++h) pos += tt.hn[h] > mine || (tt.hn[h] == mine && h < tid);
-        s_byp[pos] = tid;
+#pragma unroll 4
+        for (int h = 0; h < a.Hq; ++h) {
+            const int o = __builtin_amdgcn_readlane(mine, h);
+            pos += o > mine || (o == mine && h < lane);
+        }
+        if (lane < a.Hq) s_byp[pos] = lane;
     }
     for (int i = tid; i < NWAVE * PLAN_STRIDE + 1; i += PREP_THR) s_plan[i] = 0;
     if (tid < NWAVE) s_load[tid] = 0;
@@ -307,33 +323,40 @@ __device__ void prep_plan(const PrepArgs& a, const TileTable& tt, int tid) {
         // order: k = the heads before it, sl = their tiles, nfb = those of them with
         // tiles; over its whole wave: nfh heads with tiles, the largest head mxh (the
         // first). Lane w < 8 also takes wave w's heads, heads with tiles, largest head.
-        int k = 0, sl = 0, nfb = 0, nfh = 0, mxh = 0, nhw = 0, nfw = 0, mxw = 0;
+        // The counts run as inclusive lane scans (Hq <= 32 lanes) of 8-bit fields, wave w
+        // at bits 8 (w & 3) of word w >> 2 (a wave's tiles are at most MAX_TT < 256).
+        const int wv = act ? hwave : 0;
+        const uint32_t one = act ? 1u << (8 * (wv & 3)) : 0u;
+        uint32_t c0 = wv < 4 ? one : 0u, c1 = wv < 4 ? 0u : one;  // heads
+        uint32_t s0 = c0 * (uint32_t)hsz, s1 = c1 * (uint32_t)hsz;  // their tiles
+        uint32_t f0 = hsz > 0 ? c0 : 0u, f1 = hsz > 0 ? c1 : 0u;    // heads with tiles
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) {
+            const uint32_t y0 = __shfl_up(c0, o, 64), y1 = __shfl_up(c1, o, 64);
+            const uint32_t y2 = __shfl_up(s0, o, 64), y3 = __shfl_up(s1, o, 64);
+            const uint32_t y4 = __shfl_up(f0, o, 64), y5 = __shfl_up(f1, o, 64);
+            if (lane >= o) {
+                c0 += y0; c1 += y1;
+                s0 += y2; s1 += y3;
+                f0 += y4; f1 += y5;
+            }
+        }
+        auto fld = [](uint32_t x0, uint32_t x1, int w) -> int {
+            return (int)(((w < 4 ? x0 : x1) >> (8 * (w & 3))) & 255u);
+        };
+        // The last head's lane holds every wave's totals.
+        const uint32_t tc0 = __builtin_amdgcn_readlane(c0, a.Hq - 1), tc1 = __builtin_amdgcn_readlane(c1, a.Hq - 1);
+        const uint32_t tf0 = __builtin_amdgcn_readlane(f0, a.Hq - 1), tf1 = __builtin_amdgcn_readlane(f1, a.Hq - 1);
+        const int k = fld(c0, c1, wv) - 1, sl = fld(s0, s1, wv) - hsz, nfb = fld(f0, f1, wv) - (hsz > 0 ? 1 : 0);
+        const int nfh = fld(tf0, tf1, wv);
+        const int nhw = fld(tc0, tc1, lane & 7), nfw = fld(tf0, tf1, lane & 7);
+        int mxh = 0, mxw = 0;  // a wave's largest head is its first
+#pragma unroll
         for (int w = 0; w < NWAVE; ++w) {
-            uint64_t bw = __builtin_amdgcn_ballot_w64(act && hwave == w);
-            int cnt = 0, acc = 0, fb = 0, big = 0;
-            while (bw) {
-                const int h = __builtin_ctzll(bw);
-                bw &= bw - 1;
-                const int z = __builtin_amdgcn_readlane(hsz, h);
-                if (lane == h) {
-                    k = cnt;
-                    sl = acc;
-                    nfb = fb;
-                }
-                big = max(big, z);
-                ++cnt;
-                acc += z;
-                fb += z > 0;
-            }
-            if (act && hwave == w) {
-                nfh = fb;
-                mxh = big;
-            }
-            if (lane == w) {
-                nhw = cnt;
-                nfw = fb;
-                mxw = big;
-            }
+            const uint64_t bw = __builtin_amdgcn_ballot_w64(act && hwave == w);
+            const int big = bw ? __builtin_amdgcn_readlane(hsz, (int)__builtin_ctzll(bw)) : 0;
+            if (act && hwave == w) mxh = big;
+            if (lane == w) mxw = big;
         }
         const int nnb = sl - nfb;  // tiles past their first of the heads before this one
         if (act && ok) {
@@ -341,13 +364,16 @@ __device__ void prep_plan(const PrepArgs& a, const TileTable& tt, int tid) {
             pw[32 + k] = head;
             pw[40 + k] = sl;
             pw[48 + k] = hsz;
-            for (int j = 0; j < hsz; ++j) {
-                pw[8 + sl + j] = hfirst + j;
-                // The decode kernel's slot order: plan order, or for the 3.2-bit kernel the
-                // heads' first tiles first (the ones with outlier ranks), then the rest.
-                const int ks = a.t_head ? (j == 0 ? nfb : nfh + nnb + j - 1) : sl + j;
-                const int row = mxh <= 4 ? 4 * k + j : sl + j;  // the slot's partial-logit row
-                pw[PW_SLOTS + ks] = slot_word(tt.word[hfirst + j], row, k, hfirst + j);
+#pragma unroll
+            for (int j = 0; j < MAX_SLOTS; ++j) {  // hsz <= MAX_SLOTS: the plan fits
+                if (j < hsz) {
+                    pw[8 + sl + j] = hfirst + j;
+                    // The decode kernel's slot order: plan order, or for the 3.2-bit kernel the
+                    // heads' first tiles first (the ones with outlier ranks), then the rest.
+                    const int ks = a.t_head ? (j == 0 ? nfb : nfh + nnb + j - 1) : sl + j;
+                    const int row = mxh <= 4 ? 4 * k + j : sl + j;  // the slot's partial-logit row
+                    pw[PW_SLOTS + ks] = slot_word(tt.word[hfirst + j], row, k, hfirst + j);
+                }
             }
         }
         if (lane < NWAVE) {
@@ -356,8 +382,16 @@ __device__ void prep_plan(const PrepArgs& a, const TileTable& tt, int tid) {
             pw[1] = ok ? nhw : 0;
             pw[2] = ok ? nfw : 0;
             pw[3] = mxw <= 4;
-            for (int s2 = ok ? load : 0; s2 < MAX_SLOTS; ++s2)  // slots past the wave's tiles: tile 0, the spare row
-                pw[PW_SLOTS + s2] = slot_word(tt.word[0] & SW_CODE_MASK, MAX_SLOTS, 0, 0);
+        }
+        // Slots past each wave's tiles: tile 0, the spare row (lane i: slots i, i + 64 of
+        // the 8 x MAX_SLOTS).
+        const uint32_t spare = slot_word(tt.word[0] & SW_CODE_MASK, MAX_SLOTS, 0, 0);
+        static_assert(NWAVE * MAX_SLOTS % 64 == 0, "the spare slots fill whole passes of the wave");
+#pragma unroll
+        for (int i = 0; i < NWAVE * MAX_SLOTS; i += 64) {
+            const int w = (i + lane) / MAX_SLOTS, s2 = (i + lane) % MAX_SLOTS;
+            const int lw = __shfl(load, w, 64);
+            if (s2 >= (ok ? lw : 0)) s_plan[w * PLAN_STRIDE + PW_SLOTS + s2] = (int)spare;
         }
         if (lane == 0) s_plan[NWAVE * PLAN_STRIDE] = ok;
     }

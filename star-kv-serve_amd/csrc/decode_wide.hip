@@ -88,7 +88,11 @@ struct PvParams {
     int v_nout, v_nbo;  // 3.2-bit: outlier columns, their nibble bytes
     int per, units;  // window y (blockIdx.y) = units [y per, min((y + 1) per, units)): bf16/fp16,
                      // 32-column blocks (the copies start 64 y per bytes further); 3.2-bit,
-                     // 32-byte chunks of the copied bytes (one window: every V byte is copied)
+                     // 32-byte chunks of the row's V bytes from v_off
+    int q_u1;        // 3.2-bit: 0, one window copying every V byte (chunk c at LDS unit c); 1,
+                     // several windows: unit 0 (the V scales) at LDS unit 0, the window's chunk
+                     // u0 + k at LDS unit 1 + k (ng = 2 + 2 per granules copied)
+    int ng_all;      // 3.2-bit: granules of V bytes in a row from v_off
     int nch;         // 1 KB chunks copied per page: logits (2), the slot's maxima (1), then V
     int nld;         // copies per wave per page
     int nbuf;        // page buffers (2 .. 8): nbuf - 1 pages in flight
@@ -201,8 +205,10 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
         } else if (ch == 2) {
             if (4 * lane < p.r * p.Hq) o = (uint32_t)(16 * lane);
         } else if (ch < p.nch) {
+            // G: the granule column in LDS; ga: the row's granule it holds (same parity).
             const int G = 4 * (ch - PV_V0) + (lane >> 4), t = gslot(G, lane & 15);
-            if (G < p.ng) o = (uint32_t)(t * p.c_s1 + v_off + 16 * G);
+            const int ga = FMT == FMT_Q4 && p.q_u1 && G >= 2 ? G - 2 + 2 * u0 : G;
+            if (G < p.ng && (FMT != FMT_Q4 || ga < p.ng_all)) o = (uint32_t)(t * p.c_s1 + v_off + 16 * ga);
         }
         off[i] = o;
     }
@@ -344,7 +350,7 @@ __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
             uint2 wv[MB / 2];
 #pragma unroll
             for (int i = 0; i < MB / 2; ++i)
-                wv[i] = tr_read8(vbuf + (uint32_t)(c0 + min(wave + NWAVE * i, ncb - 1)) * 512u + trd0);
+                wv[i] = tr_read8(vbuf + (uint32_t)((p.q_u1 ? 1 : c0) + min(wave + NWAVE * i, ncb - 1)) * 512u + trd0);
 #pragma unroll
             for (int i = 0; i < MB / 2; ++i) {
                 const int ch = wave + NWAVE * i;  // 32-byte chunk of the copied V bytes
@@ -698,19 +704,21 @@ struct PvPlan {
     int units;      // in all
     int per;        // per window
     int nbuf, nch, nld, lds;
-    int ng, v_off;  // copy geometry: granules per row (bf16/fp16: of one window) and the first byte
+    int ng, v_off;  // copy geometry: granules copied per row (of one window) and the first byte
+    int ng_all;     // 3.2-bit: granules of V bytes per row
+    int q_u1;       // 3.2-bit: several windows (each copies unit 0, the V scales, then its own units)
     bool ok;
 };
 
-// min_windows (bf16/fp16): at least this many column windows, when each can keep 4 blocks.
+// min_windows: at least this many column windows, when each can keep 4 units.
 // v_col (bf16/fp16): the first V lane of a row.
 static PvPlan pv_plan(int fmt, int v_col, int v_rank, int vs_off, int vq_off, int v_bytes, int min_windows = 1) {
     PvPlan pl{};
     int max_units;
     if (fmt == FMT_Q4) {
         pl.v_off = vs_off & ~15;
-        pl.ng = (vq_off + v_bytes + 15) / 16 - pl.v_off / 16;
-        pl.units = (pl.ng + 1) / 2;
+        pl.ng_all = (vq_off + v_bytes + 15) / 16 - pl.v_off / 16;
+        pl.units = (pl.ng_all + 1) / 2;
         max_units = 32;  // 2 blocks each
     } else {
         pl.v_off = 2 * v_col;
@@ -720,12 +728,14 @@ static PvPlan pv_plan(int fmt, int v_col, int v_rank, int vs_off, int vq_off, in
     // Fewest windows (each re-reads the logits) whose pages keep at least PV_INFLIGHT
     // bytes in flight per workgroup, else the most bytes in flight.
     int lo = (pl.units + std::min(pl.units, max_units) - 1) / std::min(pl.units, max_units);
-    if (fmt != FMT_Q4) lo = std::max(lo, std::min(min_windows, pl.units / 4));
+    lo = std::max(lo, std::min(min_windows, pl.units / 4));
     int best_score = -1;
     for (int launches = lo; launches <= lo + 3; ++launches) {
         const int per = (pl.units + launches - 1) / launches;
-        if (per > max_units || (fmt == FMT_Q4 && launches > lo)) continue;
-        const int ng = fmt == FMT_Q4 ? pl.ng : 4 * per;
+        if (per > max_units) continue;
+        // 3.2-bit windows copy unit 0 (the V scales) and their own units.
+        const bool q_win = fmt == FMT_Q4 && per < pl.units;
+        const int ng = fmt == FMT_Q4 ? (q_win ? 2 + 2 * per : pl.ng_all) : 4 * per;
         const int nch = (ng + 3) / 4 + PV_V0;
         if ((nch + NWAVE - 1) / NWAVE > PV_NLD) continue;
         const int nbuf = std::min(8, (PV_MAX_DYN_LDS - 1024) / (nch * 1024));
@@ -739,7 +749,8 @@ static PvPlan pv_plan(int fmt, int v_col, int v_rank, int vs_off, int vq_off, in
             pl.nch = nch;
             pl.nld = (nch + NWAVE - 1) / NWAVE;
             pl.lds = nbuf * nch * 1024 + 1024;
-            if (fmt != FMT_Q4) pl.ng = ng;
+            pl.ng = ng;
+            pl.q_u1 = q_win ? 1 : 0;
             pl.ok = true;
         }
     }
@@ -759,6 +770,8 @@ int launch_pv(const DecodeParams& p, int fmt, int grid, hipStream_t stream) {
     a.c_s1 = (int)p.c_s1;
     a.n = p.n; a.Hq = p.Hq; a.v_rank = p.v_rank;
     a.ng = pl.ng;
+    a.ng_all = pl.ng_all;
+    a.q_u1 = pl.q_u1;
     a.vs_rel = p.vs_off - pl.v_off;
     a.vq_rel = p.vq_off - pl.v_off;
     a.v_nout = p.v_nout; a.v_nbo = p.v_nbo;
