@@ -79,7 +79,7 @@ constexpr int PREP_RECS = 4 * PREP_THR;  // page records per record workgroup
 // Rank-tile table: per tile its query head, first k_up row, valid ranks (rows past them
 // fold to zero) and code word (slot_word's code tile | outlier ranks << 13); per query
 // head its first tile and tile count.
-struct TileTable {
+struct alignas(16) TileTable {
     int head[MAX_TT], row[MAX_TT], valid[MAX_TT], word[MAX_TT];
     int hf[MAX_H], hn[MAX_H];
     int rank[MAX_H], off[MAX_H], t0[MAX_H];  // bf16/fp16 kv heads: t0 = tiles of the kv heads before
@@ -159,6 +159,16 @@ __device__ void tile_table(const PrepArgs& a, TileTable& tt, int tid) {
 template <int CTL>
 __device__ __forceinline__ int dpp_i(int v) {
     return __builtin_amdgcn_update_dpp(0, v, CTL, 0xF, 0xF, true);
+}
+
+// Inclusive scan over lanes 0 .. 31 (lanes 32 .. 63 get a scan of their own): row_shr 1, 2,
+// 4, 8 within each row of 16, then row 1 adds lane 15 (row_bcast:15 into rows 1 and 3).
+__device__ __forceinline__ void scan32(uint32_t& v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);
 }
 
 // Max over lanes 0 .. 7 (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror), as a
@@ -263,14 +273,21 @@ __device__ void prep_plan(const PrepArgs& a, const TileTable& tt, int tid) {
     __shared__ int s_plan[NWAVE * PLAN_STRIDE + 1];
     const int lane = tid & 63, wave = tid >> 6;
     // Heads by decreasing tile count (ties: lower head first): lane h of wave 0 counts
-    // the heads before head h, every head's count read across lanes.
+    // the heads before head h (every head's count read at once, four per LDS read).
     if (wave == 0) {
         const int mine = lane < a.Hq ? tt.hn[lane] : 0;
+        int4 hv[MAX_H / 4];
+#pragma unroll
+        for (int g = 0; g < MAX_H / 4; ++g) hv[g] = ((const int4*)tt.hn)[g];
         int pos = 0;
-#pragma unroll 4
-        for (int h = 0; h < a.Hq; ++h) {
-            const int o = __builtin_amdgcn_readlane(mine, h);
-            pos += o > mine || (o == mine && h < lane);
+#pragma unroll
+        for (int g = 0; g < MAX_H / 4; ++g) {
+            const int e[4] = {hv[g].x, hv[g].y, hv[g].z, hv[g].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int h = 4 * g + j;
+                pos += h < a.Hq && (e[j] > mine || (e[j] == mine && h < lane));
+            }
         }
         if (lane < a.Hq) s_byp[pos] = lane;
     }
@@ -330,17 +347,9 @@ __device__ void prep_plan(const PrepArgs& a, const TileTable& tt, int tid) {
         uint32_t c0 = wv < 4 ? one : 0u, c1 = wv < 4 ? 0u : one;  // heads
         uint32_t s0 = c0 * (uint32_t)hsz, s1 = c1 * (uint32_t)hsz;  // their tiles
         uint32_t f0 = hsz > 0 ? c0 : 0u, f1 = hsz > 0 ? c1 : 0u;    // heads with tiles
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) {
-            const uint32_t y0 = __shfl_up(c0, o, 64), y1 = __shfl_up(c1, o, 64);
-            const uint32_t y2 = __shfl_up(s0, o, 64), y3 = __shfl_up(s1, o, 64);
-            const uint32_t y4 = __shfl_up(f0, o, 64), y5 = __shfl_up(f1, o, 64);
-            if (lane >= o) {
-                c0 += y0; c1 += y1;
-                s0 += y2; s1 += y3;
-                f0 += y4; f1 += y5;
-            }
-        }
+        scan32(c0); scan32(c1);
+        scan32(s0); scan32(s1);
+        scan32(f0); scan32(f1);
         auto fld = [](uint32_t x0, uint32_t x1, int w) -> int {
             return (int)(((w < 4 ? x0 : x1) >> (8 * (w & 3))) & 255u);
         };
@@ -364,15 +373,18 @@ __device__ void prep_plan(const PrepArgs& a, const TileTable& tt, int tid) {
             pw[32 + k] = head;
             pw[40 + k] = sl;
             pw[48 + k] = hsz;
+            int wd[MAX_SLOTS];  // the head's tile words, read at once (hsz <= MAX_SLOTS: the plan fits)
 #pragma unroll
-            for (int j = 0; j < MAX_SLOTS; ++j) {  // hsz <= MAX_SLOTS: the plan fits
+            for (int j = 0; j < MAX_SLOTS; ++j) wd[j] = tt.word[min(hfirst + j, MAX_TT - 1)];
+#pragma unroll
+            for (int j = 0; j < MAX_SLOTS; ++j) {
                 if (j < hsz) {
                     pw[8 + sl + j] = hfirst + j;
                     // The decode kernel's slot order: plan order, or for the 3.2-bit kernel the
                     // heads' first tiles first (the ones with outlier ranks), then the rest.
                     const int ks = a.t_head ? (j == 0 ? nfb : nfh + nnb + j - 1) : sl + j;
                     const int row = mxh <= 4 ? 4 * k + j : sl + j;  // the slot's partial-logit row
-                    pw[PW_SLOTS + ks] = slot_word(tt.word[hfirst + j], row, k, hfirst + j);
+                    pw[PW_SLOTS + ks] = slot_word(wd[j], row, k, hfirst + j);
                 }
             }
         }
