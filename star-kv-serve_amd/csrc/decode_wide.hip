@@ -445,6 +445,7 @@ __global__ __launch_bounds__(THR) void merge_cols_kernel(const uint8_t* __restri
                                                             int v_rank, int ld, int pv_r) {
     constexpr int CPW = 4 * THR / MCW;  // columns per workgroup
     __shared__ f32x4_t s_sum[MCW][64];
+    __shared__ float s_mr[64 * MC_WREG];  // R > 1: the slots' maxima held in registers, for reads by index
     const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int w = MCW > 1 ? __builtin_amdgcn_readfirstlane(tid >> 6) : 0;  // slot phase
     const int* hdr = (const int*)ws;
@@ -500,21 +501,22 @@ __global__ __launch_bounds__(THR) void merge_cols_kernel(const uint8_t* __restri
     if (pv_r == 1) {  // partial k is logits-pass slot k
 #pragma unroll
         for (int j = 0; j < MC_WREG; ++j) wk[j] = lane + 64 * j < nk ? exp2f(mr[j] - M) : 0.f;
-    } else {  // every lane active: the maxima are read across lanes
+    } else {  // the maxima by slot index from LDS (every wave formed the same; wave 0 stores them)
+        if (tid < 64) {
+#pragma unroll
+            for (int j = 0; j < MC_WREG; ++j) s_mr[lane + 64 * j] = mr[j];
+        }
+        __syncthreads();
 #pragma unroll
         for (int j = 0; j < MC_WREG; ++j) {
             const int k = lane + 64 * j;
             float x = -INFINITY;
             for (int t = 0; t < pv_r; ++t) {
                 const int i = pv_r * (k_lo + k) + t - r_lo;
-                float v = -INFINITY;
-#pragma unroll
-                for (int jj = 0; jj < MC_WREG; ++jj) {
-                    const float y = __shfl(mr[jj], i & 63, 64);
-                    v = (i >> 6) == jj ? y : v;
-                }
-                if (i >= 64 * MC_WREG) v = i < nr ? wm[r0 + (int64_t)i * Hq] : -INFINITY;
-                x = i >= 0 && i < nr ? fmaxf(x, v) : x;
+                const float v = i < 0 || i >= nr           ? -INFINITY
+                                : i < 64 * MC_WREG ? s_mr[i]
+                                                   : wm[r0 + (int64_t)i * Hq];
+                x = fmaxf(x, v);
             }
             wk[j] = k < nk ? exp2f(x - M) : 0.f;
         }
