@@ -767,15 +767,15 @@ static int grid_for(int n, int max_seq_len, int tok_per_wg = 256) {
 // fp32 partial accumulators of H x v_rank per workgroup and request cost about as much
 // traffic as the V codes they sum when a workgroup has few pages, while the logits pass's
 // partials are two floats per head: with few requests the logits pass takes every CU and
-// the bf16/fp16 P @ V pass fewer, longer ranges in two column windows side by side. R = the
-// logits grid over the grid at PV_TOK tokens per workgroup, rounded (1 to 4); 1 for
-// 3.2-bit codes, whose P @ V pass copies every V byte in one window and so keeps more
-// workgroups busy with R = 1. One request of 16419 tokens at V rank 1280 / 1290 (config 4
-// at concurrency 1): bf16 P @ V + merge 36.7 us at R = 2, 37.6 at R = 1; 3.2-bit 39.3 at
-// R = 1, 42.6 at R = 2.
+// the P @ V pass fewer, longer ranges in column windows side by side. R = the logits grid
+// over the grid at PV_TOK tokens per workgroup, rounded (1 to 4). One request of 16419
+// tokens at V rank 1280 / 1290 (config 4 at concurrency 1), P @ V + merge: bf16 36.7 us at
+// R = 2, 37.6 at R = 1; 3.2-bit 34.6 us at R = 2, 35.4 at R = 1, 39.3 at R = 4 (a P @ V
+// page costs about the same at a quarter of the columns). Two such requests: R = 1 for
+// both, the fastest.
 constexpr int PV_TOK = 128;
 static int pv_ratio(int fmt, int n, int max_seq_len, int grid) {
-    if (fmt == FMT_Q4) return 1;
+    (void)fmt;
     const int gp = grid_for(n, max_seq_len, PV_TOK);
     return std::max(1, std::min(4, (grid + gp / 2) / gp));
 }

@@ -16,7 +16,8 @@
 // bytes per lane):
 //   - the V bytes of the 16 rows: bf16/fp16, the columns of the workgroup's window
 //     (grid.y: windows run side by side); 3.2-bit, every V byte (scales, outlier and
-//     inlier nibbles);
+//     inlier nibbles) with one window, or with several the 32 bytes holding the V scales
+//     and then the window's own 32-byte chunks;
 //   - the 16 logits of every head (2 KB) and the R slots' maxima per head.
 // Since the reference max is final, P = exp2(logit - m) needs no rescaling.
 // P @ V runs on v_mfma_f32_32x32x16 (M = 32 heads, N = 32 columns, K = the page's 16

@@ -386,6 +386,44 @@ def test_two_pass_pv_ranges_over_logits_ranges(cuda, two_pass):
         assert_close(out[[0, 2, 3]], t[[0, 2, 3]], f"two-pass grid={grid}")
 
 
+def run_quant(wl_gpu, grid):
+    """One 3.2-bit call through the C ABI with an explicit split."""
+    q, kv, bt, sl = wl_gpu.query, wl_gpu.kv_cache, wl_gpu.block_table, wl_gpu.seq_lens
+    n, H, _ = q.shape
+    L = _hip.lib()
+    out = torch.empty(n, H, 128, dtype=wl_gpu.v_up_by_q.dtype, device=q.device)
+    ws = torch.empty(L.starkv_decode_workspace_bytes(_hip.CACHE_Q3_2, n, H, H, wl_gpu.k_width, wl_gpu.v_rank,
+                                                     wl_gpu.max_seq_len, grid), dtype=torch.uint8, device=q.device)
+    cs, vq, U = cos_sin_for_kernel(wl_gpu.cos_sin_cache), wl_gpu.v_up_by_q, wl_gpu.k_up
+    th, tn, tl = wl_gpu.k_tiles
+    rc = L.starkv_quant_decode(_hip.stream_of(q), q.data_ptr(), q.stride(0), q.stride(1), _hip.dtype_code(q),
+                               kv.data_ptr(), kv.stride(0), kv.stride(1), kv.shape[1], bt.data_ptr(), bt.stride(0),
+                               bt.stride(1), sl.data_ptr(), n, H, wl_gpu.max_seq_len, wl_gpu.k_width, wl_gpu.v_rank,
+                               wl_gpu.row.nbytes, U.data_ptr(), U.stride(0), _hip.dtype_code(U), th.data_ptr(),
+                               tn.data_ptr(), tl.data_ptr(), vq.data_ptr(), vq.stride(0), vq.stride(1),
+                               _hip.dtype_code(vq), cs.data_ptr(), cs.stride(0), _hip.dtype_code(cs), wl_gpu.scale,
+                               out.data_ptr(), out.stride(0), out.stride(1), _hip.dtype_code(out), ws.data_ptr(),
+                               ws.numel(), grid)
+    _hip.check(rc, "quant_decode")
+    return out
+
+
+def test_quant_two_pass_pv_ranges_and_windows(cuda):
+    """3.2-bit P @ V over ranges of R = 1 .. 4 logits-pass ranges at V rank 1290 (W 880): the
+    grids give R = 1 .. 4 and, short of the device's CUs, 2-4 column windows, each copying the
+    V scales' bytes and its own chunks (the last window shorter); an empty request and
+    requests that start and end inside the ranges."""
+    wl = W.make_quant([700, 0, 1500, 16], num_heads=32, ranks=RANKS_880, v_rank=1290, seed=35, device=cuda)
+    truth = quant_truth(wl)
+    for grid in (47, 94, 141, 188, 200):
+        print(f"\n[quant two-pass R] grid={grid}", flush=True)
+        out = run_quant(wl, grid)
+        torch.cuda.synchronize()
+        o = out.float().cpu().numpy()
+        assert np.isnan(o[1]).all()
+        assert_close(out[[0, 2, 3]], truth[[0, 2, 3]], f"quant two-pass grid={grid}")
+
+
 def test_two_pass_long_request_many_partials(cuda):
     """One request of 20,000 tokens at W 880, V rank 1280: the merge of its P @ V partials
     with every wave's batched loads in use (default grid: 157 partials, R = 2), and at grid
