@@ -90,6 +90,31 @@ int starkv_write_kv(void *stream, const void *hidden, int64_t h_s0, const void *
                     int64_t co_s0, void *workspace, size_t workspace_bytes);
 
 /*
+ * starkv_write_kv with its launches deferred to the calling thread's next decode call on
+ * the same stream (starkv_lowrank_decode, starkv_quant_decode and their group and
+ * no-alloc forms): that call runs the write's code GEMM inside its own first launch (the
+ * page plan and query fold, which do not depend on the write), then the write's store,
+ * then its decode kernels, so a decode step's write and decode take one launch fewer.
+ * Same arguments, checks and results as starkv_write_kv; the reference has no
+ * counterpart (its write and decode are separate framework calls, attention.py:179-217).
+ * Until the write is launched, hidden, kv_down, the slot mapping, the head arrays and the
+ * workspace must stay valid and unchanged. A pending write is also launched, on its own
+ * stream and in its own launches, by the thread's next write call (deferred or not), by
+ * a decode call on another stream or one that fails its checks, and by
+ * starkv_flush_write. One write per thread can be pending.
+ */
+int starkv_write_kv_deferred(void *stream, const void *hidden, int64_t h_s0, const void *kv_down, int64_t w_s0,
+                             int w_dtype, int n, int hidden_size, int k_width, int v_rank, void *cache,
+                             int64_t c_s0, int64_t c_s1, int cache_dtype, int block_size, int64_t num_blocks,
+                             const void *slot_mapping, int slot_bits, int num_kv_heads, const int32_t *k_ranks,
+                             const int32_t *k_offsets, const int32_t *k_nouts, int row_bytes, void *codes_out,
+                             int64_t co_s0, void *workspace, size_t workspace_bytes);
+
+/* Launches the calling thread's deferred write, if one is pending (no counterpart in the
+ * reference: the pair of starkv_write_kv_deferred). */
+int starkv_flush_write(void);
+
+/*
  * 3.2-bit write path: quantize one row per token (per-KV-head 4-bit outlier /
  * 3-bit inlier K blocks with bf16 scales, then the head-shared V latent) and
  * scatter it into its slot, bit for bit kv_quant._q (IEEE fp32 division,

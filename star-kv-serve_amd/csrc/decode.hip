@@ -43,6 +43,7 @@
 #include <vector>
 
 #include "decode_common.hpp"
+#include "kv_gemm.hpp"
 
 namespace starkv {
 // ---------------------------------------------------------------------------
@@ -514,28 +515,49 @@ __device__ void prep_fold_q(const PrepArgs& a, const TileTable& tt, int tid, int
         prep_fold<QT, STARKV_F32>(a, tt, tid, bid);
 }
 
-__global__ __launch_bounds__(PREP_THR) void prep_kernel(PrepArgs a) {
+// Workgroup `bid` of prep's grid: 0 the prefix, 1 the plan, then the fold workgroups,
+// then the record workgroups.
+__device__ __forceinline__ void prep_block(const PrepArgs& a, int bid) {
     __shared__ TileTable tt;
     __shared__ int s_pp[MAX_REQ_PER_CALL + 1], s_len[MAX_REQ_PER_CALL];
     const int tid = threadIdx.x;
-    if (blockIdx.x == 0) {
+    if (bid == 0) {
         prep_prefix(a, tid, s_pp, s_len);
         return;
     }
-    if ((int)blockIdx.x >= 2 + a.fold_wgs) {
-        prep_records(a, tid, blockIdx.x - 2 - a.fold_wgs, s_pp, s_len);
+    if (bid >= 2 + a.fold_wgs) {
+        prep_records(a, tid, bid - 2 - a.fold_wgs, s_pp, s_len);
         return;
     }
     tile_table(a, tt, tid);
-    if (blockIdx.x == 1) {
+    if (bid == 1) {
         prep_plan(a, tt, tid);
     } else if (a.q_dt == STARKV_BF16) {
-        prep_fold_q<STARKV_BF16>(a, tt, tid, blockIdx.x - 2);
+        prep_fold_q<STARKV_BF16>(a, tt, tid, bid - 2);
     } else if (a.q_dt == STARKV_F16) {
-        prep_fold_q<STARKV_F16>(a, tt, tid, blockIdx.x - 2);
+        prep_fold_q<STARKV_F16>(a, tt, tid, bid - 2);
     } else {
-        prep_fold_q<STARKV_F32>(a, tt, tid, blockIdx.x - 2);
+        prep_fold_q<STARKV_F32>(a, tt, tid, bid - 2);
     }
+}
+
+__global__ __launch_bounds__(PREP_THR) void prep_kernel(PrepArgs a) { prep_block(a, blockIdx.x); }
+
+// prep with a deferred cache write's code GEMM in the same launch (the two are
+// independent: prep reads the query, lengths, tables and block table, the GEMM the
+// layer input and kv_down): prep's workgroups first, then the GEMM's (gx x gy x gz grid
+// flattened). The write's store follows as the next launch, before the decode kernels.
+static_assert(KVW_THR == PREP_THR, "the GEMM and prep workgroups share one launch");
+template <int DT>
+__global__ __launch_bounds__(PREP_THR) void write_prep_kernel(PrepArgs a, KvGemmParams g, int prep_wgs, int gx,
+                                                              int gy) {
+    const int bid = blockIdx.x;
+    if (bid < prep_wgs) {
+        prep_block(a, bid);
+        return;
+    }
+    const int gb = bid - prep_wgs;
+    kv_gemm_block<DT>(g, gb % gx, (gb / gx) % gy, gb / (gx * gy));
 }
 
 // ---------------------------------------------------------------------------
@@ -1006,7 +1028,18 @@ static bool codes_group_fits(int cache_kind, int per, const int32_t* ranks, int 
     return lowrank_copies(k_width, 0) > 0 && pv_fits(fmt, k_width, v_rank, 0, 0, 0, 0);
 }
 
+static int decode_common_body(DecodeParams& p, const CommonArgs& a, int fmt, int row_bytes, int TT,
+                              hipStream_t stream);
+
+// A call that fails its checks leaves no deferred write behind: it is launched on its own.
 static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_bytes, int TT, hipStream_t stream) {
+    const int rc = decode_common_body(p, a, fmt, row_bytes, TT, stream);
+    if (rc != STARKV_OK) flush_pending_write();
+    return rc;
+}
+
+static int decode_common_body(DecodeParams& p, const CommonArgs& a, int fmt, int row_bytes, int TT,
+                              hipStream_t stream) {
     SKV_CHECK(a.n >= 1 && a.n <= MAX_REQ_PER_CALL, "decode: n=%d requests (1..%d per call)", a.n, MAX_REQ_PER_CALL);
     SKV_CHECK(a.Hq >= 1 && a.Hq <= MAX_H, "decode: num_heads=%d (1..%d)", a.Hq, MAX_H);
     SKV_CHECK(a.max_seq_len >= 1, "decode: max_seq_len must be >= 1");
@@ -1115,7 +1148,27 @@ static int decode_common(DecodeParams& p, const CommonArgs& a, int fmt, int row_
     SKV_CHECK(2 + pa.fold_wgs + rec_wgs < ((int64_t)1 << 31), "decode: %d requests x %d tokens", a.n,
               a.max_seq_len);
     const int prep_grid = 2 + pa.fold_wgs + (int)rec_wgs;
-    hipLaunchKernelGGL(prep_kernel, dim3(prep_grid), dim3(PREP_THR), 0, stream, pa);
+    PendingGemm pg;
+    if (pending_write_on(stream, &pg)) {
+        // A deferred write on this stream: its GEMM rides in prep's launch, its store
+        // follows, and the decode kernels read the cache after both.
+        const int64_t gw = (int64_t)pg.gx * pg.gy * pg.gz;
+        SKV_CHECK(prep_grid + gw < ((int64_t)1 << 31), "decode: %d prep and %lld write workgroups", prep_grid,
+                  (long long)gw);
+        if (pg.w_dtype == STARKV_BF16)
+            hipLaunchKernelGGL(write_prep_kernel<STARKV_BF16>, dim3(prep_grid + (int)gw), dim3(PREP_THR), 0, stream,
+                               pa, pg.g, prep_grid, pg.gx, pg.gy);
+        else
+            hipLaunchKernelGGL(write_prep_kernel<STARKV_F16>, dim3(prep_grid + (int)gw), dim3(PREP_THR), 0, stream,
+                               pa, pg.g, prep_grid, pg.gx, pg.gy);
+        SKV_HIP(hipGetLastError());
+        const int wrc = launch_pending_store();
+        if (wrc) return wrc;
+    } else {
+        const int wrc = flush_pending_write();  // a deferred write on another stream: its own launches
+        if (wrc) return wrc;
+        hipLaunchKernelGGL(prep_kernel, dim3(prep_grid), dim3(PREP_THR), 0, stream, pa);
+    }
     SKV_HIP(hipGetLastError());
     if (timed && g_prof.mode == 0) SKV_HIP(hipEventRecord(g_prof.ev[2 * g_prof.used], stream));
     int rc;

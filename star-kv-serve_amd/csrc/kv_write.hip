@@ -21,99 +21,16 @@
 //    blocks and V block, one block per wave.
 #include <algorithm>
 
+#include "kv_gemm.hpp"
 #include "pack_rows.hpp"
 
 namespace starkv {
 
-constexpr int KVW_THR = 256;    // GEMM workgroup
 constexpr int KVS_THR = 1024;   // store workgroup (one token)
-constexpr int KVW_COLS = 64;    // codes per GEMM workgroup (4 waves x 16)
-constexpr int KVW_TOKENS = 64;  // tokens per GEMM workgroup (4 MFMA row tiles)
-constexpr int KVW_MAX_SPLIT = 16;
-constexpr int KVW_CHUNK = 8;     // K steps (of 32 channels) whose loads are in flight together
-
-struct KvGemmParams {
-    const uint16_t* hidden; int64_t h_s0;  // [n, hidden] elements
-    const uint16_t* w; int64_t w_s0;       // kv_down [width, hidden]
-    int n, width, ksteps, splits;           // ksteps = hidden / 32
-    float* part;                            // [splits][n][width]
-};
-
-template <int DT>
-__device__ __forceinline__ f32x4_t mfma_16x16x32(uint4 a, uint4 b, f32x4_t c) {
-    if constexpr (DT == STARKV_BF16)
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                       c, 0, 0, 0);
-    else
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c,
-                                                      0, 0, 0);
-}
-
-// K steps [k0, k1) of one wave: TILES row tiles (uniform per workgroup) x 16 codes.
-// The channel sum is order-free, so the channels go to MFMA steps in an order that
-// reads whole lines: over steps 2m and 2m + 1, lane group g (lane / 16) supplies
-// channels 64 m + 16 g .. + 8 and then + 8 .. + 16 of its row, 32 contiguous bytes,
-// and the 4 groups cover the row's 128 bytes; A (hidden) and B (kv_down) use the same
-// order. Every load of a chunk of KVW_CHUNK steps is issued before its first MFMA; pairs
-// past the split's end reload its last pair with B zeroed (no branch between loads).
-template <int DT, int TILES>
-__device__ __forceinline__ void kv_gemm_steps(const uint16_t* wr, const uint16_t* const (&ar)[4], int k0, int k1,
-                                              f32x4_t (&acc)[4]) {
-    for (int kc = k0; kc < k1; kc += KVW_CHUNK) {
-        uint4 b[KVW_CHUNK], a[KVW_CHUNK][TILES];
-#pragma unroll
-        for (int j = 0; j < KVW_CHUNK; j += 2) {
-            const int m = min(kc + j, k1 - 2) >> 1;  // the pair's 64-channel block
-            b[j] = *(const uint4*)(wr + 64 * m);
-            b[j + 1] = *(const uint4*)(wr + 64 * m + 8);
-#pragma unroll
-            for (int t = 0; t < TILES; ++t) {
-                a[j][t] = *(const uint4*)(ar[t] + 64 * m);
-                a[j + 1][t] = *(const uint4*)(ar[t] + 64 * m + 8);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < KVW_CHUNK; ++j) {
-            const uint4 bj = kc + j < k1 ? b[j] : make_uint4(0, 0, 0, 0);
-#pragma unroll
-            for (int t = 0; t < TILES; ++t) acc[t] = mfma_16x16x32<DT>(a[j][t], bj, acc[t]);
-        }
-    }
-}
 
 template <int DT>
 __global__ __launch_bounds__(KVW_THR) void kv_gemm_kernel(const KvGemmParams p) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int s = blockIdx.y, m0 = KVW_TOKENS * blockIdx.z;
-    const int col = KVW_COLS * blockIdx.x + 16 * wave + (lane & 15);  // this lane's B column (code)
-    const int kq = 16 * (lane >> 4);                                   // its 16 channels of each 64
-    // Splits cover whole pairs of K steps (ksteps is even: hidden is a multiple of 64).
-    const int k0 = 2 * (s * (p.ksteps / 2) / p.splits), k1 = 2 * ((s + 1) * (p.ksteps / 2) / p.splits);
-    const int tiles = min(4, (p.n - m0 + 15) / 16);  // row tiles with tokens (uniform)
-    // Rows past the code or token range read row width - 1 / n - 1 (valid memory);
-    // their products are never stored.
-    const uint16_t* wr = p.w + (int64_t)min(col, p.width - 1) * p.w_s0 + kq;
-    const uint16_t* ar[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) ar[t] = p.hidden + (int64_t)min(m0 + 16 * t + (lane & 15), p.n - 1) * p.h_s0 + kq;
-    f32x4_t acc[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    switch (tiles) {
-        case 1: kv_gemm_steps<DT, 1>(wr, ar, k0, k1, acc); break;
-        case 2: kv_gemm_steps<DT, 2>(wr, ar, k0, k1, acc); break;
-        case 3: kv_gemm_steps<DT, 3>(wr, ar, k0, k1, acc); break;
-        default: kv_gemm_steps<DT, 4>(wr, ar, k0, k1, acc); break;
-    }
-    if (col >= p.width) return;
-    // acc[t][e] = code `col` of token m0 + 16 t + 4 (lane >> 4) + e.
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int m = m0 + 16 * t + 4 * (lane >> 4) + e;
-            if (t < tiles && m < p.n) p.part[((int64_t)s * p.n + m) * p.width + col] = acc[t][e];
-        }
+    kv_gemm_block<DT>(p, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 struct KvStoreParams {
@@ -229,12 +146,32 @@ size_t starkv_write_kv_workspace_bytes(int n, int width, int hidden) {
     return (size_t)kv_splits(n, width, hidden) * n * width * sizeof(float);
 }
 
-int starkv_write_kv(void* stream, const void* hidden, int64_t h_s0, const void* kv_down, int64_t w_s0, int w_dtype,
-                    int n, int hidden_size, int k_width, int v_rank, void* cache, int64_t c_s0, int64_t c_s1,
-                    int cache_dtype, int block_size, int64_t num_blocks, const void* slot_mapping, int slot_bits,
-                    int num_kv_heads, const int32_t* k_ranks, const int32_t* k_offsets, const int32_t* k_nouts,
-                    int row_bytes, void* codes_out, int64_t co_s0, void* workspace, size_t workspace_bytes) {
-    clear_error();
+}  // extern "C"
+
+namespace starkv {
+
+// One write's launches: the GEMM grid and parameters, then the store's.
+struct WriteLaunch {
+    hipStream_t stream;
+    int w_dtype;
+    KvGemmParams g;
+    dim3 ggrid;
+    KvStoreParams s;
+    const void* store_fn;
+    size_t lds;
+};
+
+// The calling thread's deferred write (starkv_write_kv_deferred), launched by its next
+// decode call on the same stream, by its next write, or by starkv_flush_write.
+static thread_local WriteLaunch t_pending;
+static thread_local bool t_has_pending = false;
+
+static int prepare_write(WriteLaunch& w, void* stream, const void* hidden, int64_t h_s0, const void* kv_down,
+                         int64_t w_s0, int w_dtype, int n, int hidden_size, int k_width, int v_rank, void* cache,
+                         int64_t c_s0, int64_t c_s1, int cache_dtype, int block_size, int64_t num_blocks,
+                         const void* slot_mapping, int slot_bits, int num_kv_heads, const int32_t* k_ranks,
+                         const int32_t* k_offsets, const int32_t* k_nouts, int row_bytes, void* codes_out,
+                         int64_t co_s0, void* workspace, size_t workspace_bytes) {
     SKV_CHECK(n >= 0 && k_width > 0 && v_rank > 0 && hidden_size > 0, "write_kv: bad sizes");
     SKV_CHECK(w_dtype == STARKV_BF16 || w_dtype == STARKV_F16, "write_kv: hidden and kv_down must be bf16 or fp16");
     SKV_CHECK(hidden_size % 64 == 0, "write_kv: hidden size %d must be a multiple of 64", hidden_size);
@@ -287,18 +224,98 @@ int starkv_write_kv(void* stream, const void* hidden, int64_t h_s0, const void* 
     s.groups = quant && n <= 16 ? std::max(1, std::min(8, (num_kv_heads + 1 + KVS_THR / 64 - 1) / (KVS_THR / 64))) : 1;
     const size_t lds = (size_t)width * sizeof(float);
     SKV_CHECK(lds <= 64 * 1024, "write_kv: %d codes per token exceed the 64 KB LDS block", width);
-    hipStream_t st = (hipStream_t)stream;
-    if (w_dtype == STARKV_BF16)
-        hipLaunchKernelGGL(kv_gemm_kernel<STARKV_BF16>, ggrid, dim3(KVW_THR), 0, st, g);
-    else
-        hipLaunchKernelGGL(kv_gemm_kernel<STARKV_F16>, ggrid, dim3(KVW_THR), 0, st, g);
-    SKV_HIP(hipGetLastError());
-    const void* fn = w_dtype == STARKV_BF16 ? kv_store_pick<STARKV_BF16>(splits, width)
-                                            : kv_store_pick<STARKV_F16>(splits, width);
-    SKV_CHECK(fn != nullptr, "write_kv: %d K splits", splits);
-    void* args[] = {(void*)&s};
-    SKV_HIP(hipLaunchKernel(fn, dim3(n, s.groups), dim3(KVS_THR), args, lds, st));
+    w.stream = (hipStream_t)stream;
+    w.w_dtype = w_dtype;
+    w.g = g;
+    w.ggrid = ggrid;
+    w.s = s;
+    w.store_fn = w_dtype == STARKV_BF16 ? kv_store_pick<STARKV_BF16>(splits, width)
+                                        : kv_store_pick<STARKV_F16>(splits, width);
+    SKV_CHECK(w.store_fn != nullptr, "write_kv: %d K splits", splits);
+    w.lds = lds;
     return STARKV_OK;
+}
+
+static int launch_store(WriteLaunch& w) {
+    void* args[] = {(void*)&w.s};
+    SKV_HIP(hipLaunchKernel(w.store_fn, dim3(w.s.n, w.s.groups), dim3(KVS_THR), args, w.lds, w.stream));
+    return STARKV_OK;
+}
+
+static int launch_write(WriteLaunch& w) {
+    if (w.w_dtype == STARKV_BF16)
+        hipLaunchKernelGGL(kv_gemm_kernel<STARKV_BF16>, w.ggrid, dim3(KVW_THR), 0, w.stream, w.g);
+    else
+        hipLaunchKernelGGL(kv_gemm_kernel<STARKV_F16>, w.ggrid, dim3(KVW_THR), 0, w.stream, w.g);
+    SKV_HIP(hipGetLastError());
+    return launch_store(w);
+}
+
+bool pending_write_on(hipStream_t stream, PendingGemm* out) {
+    if (!t_has_pending || t_pending.stream != stream) return false;
+    out->stream = t_pending.stream;
+    out->w_dtype = t_pending.w_dtype;
+    out->g = t_pending.g;
+    out->gx = (int)t_pending.ggrid.x;
+    out->gy = (int)t_pending.ggrid.y;
+    out->gz = (int)t_pending.ggrid.z;
+    return true;
+}
+
+int launch_pending_store() {
+    if (!t_has_pending) return STARKV_OK;
+    t_has_pending = false;
+    return launch_store(t_pending);
+}
+
+int flush_pending_write() {
+    if (!t_has_pending) return STARKV_OK;
+    t_has_pending = false;
+    return launch_write(t_pending);
+}
+
+}  // namespace starkv
+
+extern "C" {
+
+int starkv_write_kv(void* stream, const void* hidden, int64_t h_s0, const void* kv_down, int64_t w_s0, int w_dtype,
+                    int n, int hidden_size, int k_width, int v_rank, void* cache, int64_t c_s0, int64_t c_s1,
+                    int cache_dtype, int block_size, int64_t num_blocks, const void* slot_mapping, int slot_bits,
+                    int num_kv_heads, const int32_t* k_ranks, const int32_t* k_offsets, const int32_t* k_nouts,
+                    int row_bytes, void* codes_out, int64_t co_s0, void* workspace, size_t workspace_bytes) {
+    clear_error();
+    int rc = flush_pending_write();
+    if (rc) return rc;
+    WriteLaunch w;
+    rc = prepare_write(w, stream, hidden, h_s0, kv_down, w_s0, w_dtype, n, hidden_size, k_width, v_rank, cache, c_s0,
+                       c_s1, cache_dtype, block_size, num_blocks, slot_mapping, slot_bits, num_kv_heads, k_ranks,
+                       k_offsets, k_nouts, row_bytes, codes_out, co_s0, workspace, workspace_bytes);
+    if (rc || n == 0) return rc;
+    return launch_write(w);
+}
+
+int starkv_write_kv_deferred(void* stream, const void* hidden, int64_t h_s0, const void* kv_down, int64_t w_s0,
+                             int w_dtype, int n, int hidden_size, int k_width, int v_rank, void* cache, int64_t c_s0,
+                             int64_t c_s1, int cache_dtype, int block_size, int64_t num_blocks,
+                             const void* slot_mapping, int slot_bits, int num_kv_heads, const int32_t* k_ranks,
+                             const int32_t* k_offsets, const int32_t* k_nouts, int row_bytes, void* codes_out,
+                             int64_t co_s0, void* workspace, size_t workspace_bytes) {
+    clear_error();
+    int rc = flush_pending_write();
+    if (rc) return rc;
+    WriteLaunch w;
+    rc = prepare_write(w, stream, hidden, h_s0, kv_down, w_s0, w_dtype, n, hidden_size, k_width, v_rank, cache, c_s0,
+                       c_s1, cache_dtype, block_size, num_blocks, slot_mapping, slot_bits, num_kv_heads, k_ranks,
+                       k_offsets, k_nouts, row_bytes, codes_out, co_s0, workspace, workspace_bytes);
+    if (rc || n == 0) return rc;
+    t_pending = w;
+    t_has_pending = true;
+    return STARKV_OK;
+}
+
+int starkv_flush_write(void) {
+    clear_error();
+    return flush_pending_write();
 }
 
 }  // extern "C"

@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include "kv_gemm.hpp"
 #include "pack_rows.hpp"
 
 namespace starkv {
@@ -90,7 +91,7 @@ using namespace starkv;
 
 extern "C" {
 
-int starkv_abi_version(void) { return 5; }
+int starkv_abi_version(void) { return 6; }
 
 const char* starkv_last_error(void) { return g_err; }
 
@@ -99,6 +100,7 @@ int starkv_write_codes(void* stream, const void* k_codes, int64_t k_s0, const vo
                        int64_t num_blocks, const void* slot_mapping, int slot_bits, int n, int k_width,
                        int v_rank) {
     clear_error();
+    if (const int rc = flush_pending_write()) return rc;  // a deferred write goes first
     SKV_CHECK(n >= 0 && k_width >= 0 && v_rank >= 0, "write_codes: negative size");
     SKV_CHECK(block_size > 0, "write_codes: block_size must be positive");
     SKV_CHECK(slot_bits == 32 || slot_bits == 64, "write_codes: slot_mapping must be int32 or int64");
@@ -117,6 +119,7 @@ int starkv_pack_kv(void* stream, const void* k_codes, int64_t k_s0, const void* 
                    const void* slot_mapping, int slot_bits, int n, int num_kv_heads, const int32_t* k_ranks,
                    const int32_t* k_offsets, const int32_t* k_nouts, int k_width, int v_rank, int row_bytes) {
     clear_error();
+    if (const int rc = flush_pending_write()) return rc;  // a deferred write goes first
     SKV_CHECK(n >= 0 && num_kv_heads > 0 && k_width > 0 && v_rank > 0, "pack_kv: bad sizes");
     SKV_CHECK(k_width % 16 == 0, "pack_kv: k_width must be a multiple of 16 (head widths are)");
     SKV_CHECK(block_size > 0, "pack_kv: block_size must be positive");

@@ -13,6 +13,7 @@
 #include <torch/library.h>
 
 #include <optional>
+#include <vector>
 
 #include "../../include/starkv_hip.h"
 
@@ -48,7 +49,16 @@ at::Tensor workspace(const at::Tensor& like, size_t bytes) {
     return at::empty({(int64_t)bytes}, like.options().dtype(at::kByte));
 }
 
-// One bf16/fp16 decode call (paged_decode.py:150-226), at most 1024 requests.
+// A deferred write's operands and workspace, held from write_kv(deferred) until the
+// library has launched the write (the next decode op of this thread, or flush_write):
+// the caching allocator may hand out the workspace again only after that launch.
+static thread_local std::vector<at::Tensor> t_deferred_hold;
+
+static void release_deferred() { t_deferred_hold.clear(); }
+
+// One bf16/fp16 decode call (paged_decode.py:150-226), at most 1024 requests. A deferred
+// write of this thread on the same stream is launched inside it (its operands are then
+// released).
 void lowrank_decode(const at::Tensor& query, const at::Tensor& kv_cache, const at::Tensor& block_table,
                     const at::Tensor& seq_lens, int64_t max_seq_len, const at::Tensor& k_up, const at::Tensor& k_ranks,
                     const at::Tensor& k_head_offsets, int64_t k_width, int64_t v_col, const at::Tensor& v_up_by_q,
@@ -60,7 +70,7 @@ void lowrank_decode(const at::Tensor& query, const at::Tensor& kv_cache, const a
     TORCH_CHECK(grid > 0, "starkv.lowrank_decode: no grid for ", n, " requests");
     const at::Tensor ws = workspace(
         query, starkv_decode_workspace_bytes(kind, n, H, Hkv, (int)k_width, v_rank, (int)max_seq_len, grid));
-    check(starkv_lowrank_decode(stream_of(query), query.data_ptr(), query.stride(0), query.stride(1),
+    const int rc = starkv_lowrank_decode(stream_of(query), query.data_ptr(), query.stride(0), query.stride(1),
                                 dtype_code(query), kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1), kind,
                                 (int)kv_cache.size(1), i32(block_table, "block_table"), block_table.stride(0),
                                 block_table.stride(1), i32(seq_lens, "seq_lens"), n, H, Hkv, (int)max_seq_len,
@@ -69,11 +79,13 @@ void lowrank_decode(const at::Tensor& query, const at::Tensor& kv_cache, const a
                                 v_up_by_q.data_ptr(), v_up_by_q.stride(0), v_up_by_q.stride(1), dtype_code(v_up_by_q),
                                 v_rank, cos_sin.data_ptr(), cos_sin.stride(0), dtype_code(cos_sin), (float)scale,
                                 out.data_ptr(), out.stride(0), out.stride(1), dtype_code(out), ws.data_ptr(),
-                                (size_t)ws.numel(), grid),
-          "lowrank_decode");
+                                (size_t)ws.numel(), grid);
+    release_deferred();
+    check(rc, "lowrank_decode");
 }
 
-// One 3.2-bit decode call (paged_quant.py:357-411), at most 1024 requests.
+// One 3.2-bit decode call (paged_quant.py:357-411), at most 1024 requests; a deferred
+// write as in lowrank_decode.
 void quant_decode(const at::Tensor& query, const at::Tensor& kv_cache, const at::Tensor& block_table,
                   const at::Tensor& seq_lens, int64_t max_seq_len, int64_t k_width, int64_t v_rank, int64_t row_bytes,
                   const at::Tensor& k_up, const at::Tensor& tile_head, const at::Tensor& tile_nout,
@@ -90,7 +102,7 @@ void quant_decode(const at::Tensor& query, const at::Tensor& kv_cache, const at:
     TORCH_CHECK(need > 0, "starkv.quant_decode: heads [", head0, ", ", head0 + H, ") with K lanes [", k_lane0, ", ",
                 k_lane0 + k_width, ") do not fit a layer of ", row_num_heads, " heads and K width ", row_k_width);
     const at::Tensor ws = workspace(query, need);
-    check(starkv_quant_decode_group(
+    const int rc = starkv_quant_decode_group(
               stream_of(query), query.data_ptr(), query.stride(0), query.stride(1), dtype_code(query),
               kv_cache.data_ptr<uint8_t>(), kv_cache.stride(0), kv_cache.stride(1), (int)kv_cache.size(1),
               i32(block_table, "block_table"), block_table.stride(0), block_table.stride(1), i32(seq_lens, "seq_lens"),
@@ -99,8 +111,9 @@ void quant_decode(const at::Tensor& query, const at::Tensor& kv_cache, const at:
               v_up_by_q.data_ptr(), v_up_by_q.stride(0), v_up_by_q.stride(1), dtype_code(v_up_by_q),
               cos_sin.data_ptr(), cos_sin.stride(0), dtype_code(cos_sin), (float)scale, out.data_ptr(), out.stride(0),
               out.stride(1), dtype_code(out), ws.data_ptr(), (size_t)ws.numel(), grid, (int)row_k_width,
-              (int)row_num_heads, (int)head0, (int)k_lane0),
-          "quant_decode");
+              (int)row_num_heads, (int)head0, (int)k_lane0);
+    release_deferred();
+    check(rc, "quant_decode");
 }
 
 // 3.2-bit quantize + scatter (paged_quant.py:205-216).
@@ -136,13 +149,17 @@ void write_codes(const at::Tensor& key, const at::Tensor& value, const at::Tenso
 void write_kv(const at::Tensor& hidden, const at::Tensor& kv_down, int64_t k_width, const at::Tensor& kv_cache,
               const at::Tensor& slot_mapping, int64_t num_kv_heads, const std::optional<at::Tensor>& k_ranks,
               const std::optional<at::Tensor>& k_offsets, const std::optional<at::Tensor>& k_nouts, int64_t row_bytes,
-              const std::optional<at::Tensor>& codes) {
+              const std::optional<at::Tensor>& codes, bool deferred) {
     const c10::DeviceGuard guard(hidden.device());
     const int n = (int)hidden.size(0), hs = (int)hidden.size(1), width = (int)kv_down.size(0);
     const bool q = row_bytes > 0;
     TORCH_CHECK(!q || (k_ranks && k_offsets && k_nouts), "starkv.write_kv: 3.2-bit rows need the K head tables");
     const at::Tensor ws = workspace(hidden, starkv_write_kv_workspace_bytes(n, width, hs));
-    check(starkv_write_kv(stream_of(hidden), hidden.data_ptr(), hidden.stride(0), kv_down.data_ptr(),
+    // Either call launches a write still pending from before, whose operands are then free.
+    std::vector<at::Tensor> held;
+    held.swap(t_deferred_hold);
+    auto* fn = deferred ? &starkv_write_kv_deferred : &starkv_write_kv;
+    check(fn(stream_of(hidden), hidden.data_ptr(), hidden.stride(0), kv_down.data_ptr(),
                           kv_down.stride(0), dtype_code(hidden), n, hs, (int)k_width, width - (int)k_width,
                           kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1), q ? 0 : dtype_code(kv_cache),
                           (int)kv_cache.size(1), kv_cache.size(0), slot_mapping.data_ptr(), slot_bits(slot_mapping),
@@ -151,6 +168,18 @@ void write_kv(const at::Tensor& hidden, const at::Tensor& kv_down, int64_t k_wid
                           q ? (int)row_bytes : 0, codes ? codes->data_ptr() : nullptr, codes ? codes->stride(0) : 0,
                           ws.data_ptr(), (size_t)ws.numel()),
           "write_kv");
+    if (deferred && n > 0) {
+        t_deferred_hold = {hidden, kv_down, slot_mapping, ws};
+        for (const auto* t : {&k_ranks, &k_offsets, &k_nouts, &codes})
+            if (*t) t_deferred_hold.push_back(**t);
+    }
+}
+
+// Launches this thread's deferred write, if any.
+void flush_write() {
+    const int rc = starkv_flush_write();
+    release_deferred();
+    check(rc, "flush_write");
 }
 
 // q folded into U (paged_quant.py:241-255): ab [n, k_width, 128] fp16.
@@ -223,7 +252,8 @@ TORCH_LIBRARY(starkv, m) {
     m.def("write_codes(Tensor key, Tensor value, Tensor(a!) kv_cache, Tensor slot_mapping) -> ()");
     m.def("write_kv(Tensor hidden, Tensor kv_down, int k_width, Tensor(a!) kv_cache, Tensor slot_mapping, "
           "int num_kv_heads, Tensor? k_ranks, Tensor? k_offsets, Tensor? k_nouts, int row_bytes, "
-          "Tensor(b!)? codes) -> ()");
+          "Tensor(b!)? codes, bool deferred=False) -> ()");
+    m.def("flush_write() -> ()", &flush_write);
     m.def("fold_q(Tensor q, Tensor k_up, Tensor head_of_lane, float scale, Tensor(a!) ab) -> ()");
     m.def("stock_decode(Tensor query, Tensor k_cache, Tensor v_cache, Tensor block_table, Tensor seq_lens, "
           "int max_seq_len, float scale, Tensor(a!) out) -> ()");

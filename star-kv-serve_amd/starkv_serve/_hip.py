@@ -19,7 +19,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstarkv_hip.so")
 OPS_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstarkv_torch.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 F32, F16, BF16 = 0, 1, 2
 CACHE_Q3_2 = 16  # cache kind of the 3.2-bit QuantRow cache
@@ -42,6 +42,9 @@ SIGNATURES = {
     "starkv_write_kv_workspace_bytes": (_SZ, [_I, _I, _I]),
     "starkv_write_kv": (_I, [_P, _P, _I64, _P, _I64, _I, _I, _I, _I, _I, _P, _I64, _I64, _I, _I, _I64, _P, _I,
                              _I, _P, _P, _P, _I, _P, _I64, _P, _SZ]),
+    "starkv_write_kv_deferred": (_I, [_P, _P, _I64, _P, _I64, _I, _I, _I, _I, _I, _P, _I64, _I64, _I, _I, _I64, _P,
+                                      _I, _I, _P, _P, _P, _I, _P, _I64, _P, _SZ]),
+    "starkv_flush_write": (_I, []),
     "starkv_decode_grid": (_I, [_I, _I]),
     "starkv_decode_grid_for": (_I, [_I, _I, _I, _I, _I, _I, _I]),
     "starkv_stock_decode_workspace_bytes": (_SZ, [_I, _I, _I, _I]),

@@ -45,7 +45,7 @@ import torch
 import torch.nn.functional as F
 
 from starkv_serve.checkpoint import StarKVLayerWeights, layer_operands
-from starkv_serve.kernels.kv_write import write_codes, write_kv
+from starkv_serve.kernels.kv_write import flush_write, write_codes, write_kv
 from starkv_serve.kernels.paged_decode import paged_starkv_decode
 from starkv_serve.kernels.paged_quant import HEAD_DIM, pack_kv, paged_quant_decode
 from starkv_serve.kernels.prefill import prefill_attention
@@ -274,14 +274,17 @@ class StarKVAttentionImpl:
         prefill_attention(q, k, v, query_lens, self.scale, out=out)
 
     def write_from_hidden(self, hidden: torch.Tensor, kv_cache: torch.Tensor, slot_mapping: torch.Tensor,
-                          return_codes: bool = False) -> Optional[torch.Tensor]:
+                          return_codes: bool = False, deferred: bool = False) -> Optional[torch.Tensor]:
         """The step's write straight from the layer input: codes = hidden @ kv_down^T,
-        rounded to the model dtype (model.py:71), written or packed into their slots."""
+        rounded to the model dtype (model.py:71), written or packed into their slots.
+        ``deferred``: launched by the decode call that follows (``write_kv``)."""
         cache = self._cache(kv_cache)
         if self.row is None:
-            return write_kv(hidden, self.kv_down, cache, slot_mapping, self.k_width, return_codes=return_codes)
+            return write_kv(hidden, self.kv_down, cache, slot_mapping, self.k_width, return_codes=return_codes,
+                            deferred=deferred)
         return write_kv(hidden, self.kv_down, cache, slot_mapping, self.k_width, row=self.row, k_ranks=self.k_ranks,
-                        k_offsets=self.k_head_offsets, k_nouts=self.k_nouts, return_codes=return_codes)
+                        k_offsets=self.k_head_offsets, k_nouts=self.k_nouts, return_codes=return_codes,
+                        deferred=deferred)
 
     def forward_from_hidden(self, query: torch.Tensor, hidden: torch.Tensor, kv_cache: torch.Tensor,
                             attn_metadata: Optional[StarKVMetadata], output: torch.Tensor,
@@ -297,13 +300,20 @@ class StarKVAttentionImpl:
             codes = self.write_from_hidden(hidden[:n], kv_cache, md.slot_mapping[:n], return_codes=True)
             key, value = codes[:, :self.k_width], codes[:, self.k_width:]
             query_lens = self._prefill_lens(md)
-        else:
-            self.write_from_hidden(hidden[:n], kv_cache, md.slot_mapping[:n])
         Hq, Hd = self.num_heads, self.head_size
         nd = md.num_decode_tokens
+        # A decode-only step defers its write into the decode's first launch.
+        deferred = not md.num_prefills and nd > 0
+        if not md.num_prefills:
+            self.write_from_hidden(hidden[:n], kv_cache, md.slot_mapping[:n], deferred=deferred)
         if nd:
-            self._decode(query[:nd].view(nd, Hq, Hd), self._cache(kv_cache), md, output[:nd].view(nd, Hq, Hd),
-                         in_full_graph)
+            try:
+                self._decode(query[:nd].view(nd, Hq, Hd), self._cache(kv_cache), md, output[:nd].view(nd, Hq, Hd),
+                             in_full_graph)
+            except BaseException:
+                if deferred:
+                    flush_write()
+                raise
         if md.num_prefills:
             self._dense_prefill(query_lens, query[nd:n].view(n - nd, Hq, Hd), key[nd:n], value[nd:n],
                                 output[nd:n].view(n - nd, Hq, Hd))

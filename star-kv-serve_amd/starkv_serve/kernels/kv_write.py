@@ -39,7 +39,7 @@ def _slot_bits(slot_mapping: torch.Tensor) -> int:
 def write_kv(hidden: torch.Tensor, kv_down: torch.Tensor, kv_cache: torch.Tensor, slot_mapping: torch.Tensor,
              k_width: int, row: Optional[QuantRow] = None, k_ranks: Optional[torch.Tensor] = None,
              k_offsets: Optional[torch.Tensor] = None, k_nouts: Optional[torch.Tensor] = None,
-             return_codes: bool = False) -> Optional[torch.Tensor]:
+             return_codes: bool = False, deferred: bool = False) -> Optional[torch.Tensor]:
     """Writes the codes of ``hidden`` [n, hidden_size] (bf16/fp16) under ``kv_down``
     [k_width + v_rank, hidden_size] into their slots of ``kv_cache``.
 
@@ -50,7 +50,10 @@ def write_kv(hidden: torch.Tensor, kv_down: torch.Tensor, kv_cache: torch.Tensor
     the null block 0. Returns the rounded codes [n, k_width + v_rank] when
     ``return_codes`` (what ``F.linear(hidden, kv_down)`` returns), else None. Up to
     FUSED_MAX_TOKENS tokens run as one fused library call; more take F.linear, then the
-    store."""
+    store. ``deferred`` (fused calls only): the write's launches wait for this thread's
+    next decode call on the stream, which runs the code GEMM inside its own first launch
+    (one launch fewer per decode step); the next write or ``flush_write()`` launches a
+    write still pending."""
     n, hs = hidden.shape
     width = kv_down.shape[0]
     v_rank = width - k_width
@@ -88,8 +91,13 @@ def write_kv(hidden: torch.Tensor, kv_down: torch.Tensor, kv_cache: torch.Tensor
     else:
         heads, rb = 0, 0
     _hip.ops().write_kv(hidden, kv_down, int(k_width), kv_cache, slot_mapping.contiguous(), heads, k_ranks, k_offsets,
-                        k_nouts, rb, codes)
+                        k_nouts, rb, codes, bool(deferred))
     return codes
+
+
+def flush_write() -> None:
+    """Launches this thread's deferred write (``write_kv(..., deferred=True)``), if any."""
+    _hip.ops().flush_write()
 
 
 def write_codes(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
