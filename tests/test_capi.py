@@ -106,13 +106,13 @@ def test_write_kv_validation():
     L = _hip.lib()
     F32, F16, BF16 = 0, 1, 2
 
-    def call(**kw):
+    def call(fn=L.starkv_write_kv, **kw):
         a = dict(stream=None, hidden=None, h_s0=4096, kv_down=None, w_s0=4096, w_dtype=BF16, n=0, hidden_size=4096,
                  k_width=1280, v_rank=64, cache=None, c_s0=0, c_s1=1344, cache_dtype=BF16, block_size=16,
                  num_blocks=1, slots=None, slot_bits=32, heads=32, ranks=None, offsets=None, nouts=None,
                  row_bytes=0, codes=None, co_s0=0, ws=None, ws_bytes=0)
         a.update(kw)
-        return L.starkv_write_kv(*a.values())
+        return fn(*a.values())
 
     assert call() == 0  # n = 0: nothing to do
     assert call(w_dtype=F32) != 0 and b"bf16 or fp16" in L.starkv_last_error()
@@ -125,20 +125,10 @@ def test_write_kv_validation():
     assert call(n=1) != 0 and b"null pointer" in L.starkv_last_error()
     # The deferred form runs the same checks and records nothing when it fails or has no
     # tokens: flushing then launches nothing (no GPU here).
-    open_args = dict(stream=None, hidden=None, h_s0=4096, kv_down=None, w_s0=4096, w_dtype=BF16, n=0,
-                     hidden_size=4096, k_width=1280, v_rank=64, cache=None, c_s0=0, c_s1=1344, cache_dtype=BF16,
-                     block_size=16, num_blocks=1, slots=None, slot_bits=32, heads=32, ranks=None, offsets=None,
-                     nouts=None, row_bytes=0, codes=None, co_s0=0, ws=None, ws_bytes=0)
-
-    def call_deferred(**kw):
-        a = dict(open_args)
-        a.update(kw)
-        return L.starkv_write_kv_deferred(*a.values())
-
-    assert call_deferred() == 0
+    assert call(L.starkv_write_kv_deferred) == 0
     assert L.starkv_flush_write() == 0
-    assert call_deferred(k_width=1288) != 0 and b"multiple of 16" in L.starkv_last_error()
-    assert call_deferred(n=1) != 0 and b"null pointer" in L.starkv_last_error()
+    assert call(L.starkv_write_kv_deferred, k_width=1288) != 0 and b"multiple of 16" in L.starkv_last_error()
+    assert call(L.starkv_write_kv_deferred, n=1) != 0 and b"null pointer" in L.starkv_last_error()
     assert L.starkv_flush_write() == 0
     # workspace: split-K partials, a pure function of (n, width, hidden)
     assert L.starkv_write_kv_workspace_bytes(64, 1344, 4096) == 16 * 64 * 1344 * 4
