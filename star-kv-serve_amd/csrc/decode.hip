@@ -572,8 +572,8 @@ __global__ __launch_bounds__(PREP_THR) void write_prep_kernel(PrepArgs a, KvGemm
 // ---------------------------------------------------------------------------
 constexpr int MERGE_REQ = 4;
 constexpr int MERGE_THR = 64 * MERGE_REQ;
-constexpr int MERGE_PRE = 16;  // partials per request whose accumulator rows are read in the second round
 constexpr int MERGE_CB = 4;   // column blocks of 64: v_rank <= 256
+constexpr int MERGE_ML = 4;   // partials' (max, sum) per lane read in the second round: 256 per request
 
 // LDS of one merge workgroup: v_up_by_q[h] (v_rank x 128 WT), then the merged
 // low-rank outputs [MERGE_REQ][v_rank] (fp32).
@@ -590,7 +590,8 @@ __device__ __forceinline__ float lds_w<_Float16>(const _Float16* p, int i) { ret
 template <>
 __device__ __forceinline__ float lds_w<float>(const float* p, int i) { return p[i]; }
 
-template <typename WT>
+// CB: columns per lane (v_rank <= 64 CB); PRE partials' rows per wave in the second round.
+template <typename WT, int CB>
 __global__ __launch_bounds__(MERGE_THR) void merge_kernel(const uint8_t* __restrict__ ws, size_t ws_plan,
                                                           size_t ws_m, size_t ws_l, size_t ws_acc, int n, int Hq,
                                                           int v_rank, const WT* __restrict__ vup, int64_t vu_s0,
@@ -639,65 +640,90 @@ __global__ __launch_bounds__(MERGE_THR) void merge_kernel(const uint8_t* __restr
     const int k_lo = live ? pb / S : 0, nk = live ? (pe - 1) / S - k_lo + 1 : 0;
     const int64_t s0 = (int64_t)(k_lo + b) * Hq + h;  // slot index of partial k: s0 + k * Hq
 
-    // Load phase 2: partial k = lane's max and sum, and lane's columns c = lane + 64 j of the
-    // wave's first MERGE_PRE partials (k = sub + wpr i).
-    const float mk = lane < nk ? wm[s0 + (int64_t)lane * Hq] : -INFINITY;
-    const float lk = lane < nk ? wl[s0 + (int64_t)lane * Hq] : 0.f;
-    float pre[MERGE_PRE][MERGE_CB];
+    // Load phase 2: partials k = lane + 64 j's max and sum (j < MERGE_ML), and lane's columns
+    // c = lane + 64 j of the wave's first PRE partials (k = sub + wpr i).
+    constexpr int PRE = CB == 1 ? 32 : 16;
+    float mk[MERGE_ML], lk[MERGE_ML];
 #pragma unroll
-    for (int i = 0; i < MERGE_PRE; ++i)
+    for (int j = 0; j < MERGE_ML; ++j) {
+        const int k = lane + 64 * j;
+        mk[j] = k < nk ? wm[s0 + (int64_t)k * Hq] : -INFINITY;
+        lk[j] = k < nk ? wl[s0 + (int64_t)k * Hq] : 0.f;
+    }
+    float pre[PRE][CB];
 #pragma unroll
-        for (int j = 0; j < MERGE_CB; ++j) {
+    for (int i = 0; i < PRE; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j) {
             const int c = lane + 64 * j, k = sub + wpr * i;
             pre[i][j] = k < nk && c < v_rank ? wa[(s0 + (int64_t)k * Hq) * v_rank + c] : 0.f;
         }
-    float M = mk;
-    for (int k = lane + 64; k < nk; k += 64) M = fmaxf(M, wm[s0 + (int64_t)k * Hq]);
+    float M = mk[0];
+#pragma unroll
+    for (int j = 1; j < MERGE_ML; ++j) M = fmaxf(M, mk[j]);
+    for (int k = lane + 64 * MERGE_ML; k < nk; k += 64) M = fmaxf(M, wm[s0 + (int64_t)k * Hq]);
     M = wave_max(M);
-    const float wk = lane < nk ? exp2f(mk - M) : 0.f;  // weight of partial k = lane
-    float l = lk * wk;
-    for (int k = lane + 64; k < nk; k += 64) {
+    float wk[MERGE_ML];  // weight of partial lane + 64 j
+    float l = 0.f;
+#pragma unroll
+    for (int j = 0; j < MERGE_ML; ++j) {
+        wk[j] = lane + 64 * j < nk ? exp2f(mk[j] - M) : 0.f;
+        l = fmaf(lk[j], wk[j], l);
+    }
+    for (int k = lane + 64 * MERGE_ML; k < nk; k += 64) {
         const int64_t sl = s0 + (int64_t)k * Hq;
         l += wl[sl] * exp2f(wm[sl] - M);
     }
     l = wave_sum(l);
-    float acc[MERGE_CB] = {0.f, 0.f, 0.f, 0.f};
+    // Weight of partial k (wave-uniform), read across lanes (every lane active here).
+    static_assert(MERGE_ML == 4, "the weights in registers are wk[0 .. 3]");
+    const float wk0 = wk[0], wk1 = wk[1], wk2 = wk[2], wk3 = wk[3];
+    auto weight = [=](int k) -> float {
+        if (k < 64 * MERGE_ML) {
+            const int j = k >> 6;
+            const float x = j == 0 ? wk0 : j == 1 ? wk1 : j == 2 ? wk2 : wk3;
+            return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k & 63));
+        }
+        return exp2f(wm[s0 + (int64_t)k * Hq] - M);
+    };
+    float acc[CB];
 #pragma unroll
-    for (int i = 0; i < MERGE_PRE; ++i) {
-        const int k = sub + wpr * i;  // wave-uniform; below 64 (wpr <= 4)
-        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k));
+    for (int j = 0; j < CB; ++j) acc[j] = 0.f;
 #pragma unroll
-        for (int j = 0; j < MERGE_CB; ++j) acc[j] = fmaf(pre[i][j], w, acc[j]);
+    for (int i = 0; i < PRE; ++i) {
+        const int k = sub + wpr * i;  // wave-uniform
+        if (k >= nk) break;
+        const float w = weight(k);
+#pragma unroll
+        for (int j = 0; j < CB; ++j) acc[j] = fmaf(pre[i][j], w, acc[j]);
     }
-    // Requests spread over more than wpr MERGE_PRE workgroups: MERGE_PRE of the wave's
-    // partials' rows in flight at a time (columns past v_rank read column 0 and are never
-    // stored).
-    for (int i0 = MERGE_PRE; sub + wpr * i0 < nk; i0 += MERGE_PRE) {
-        float v[MERGE_PRE][MERGE_CB];
+    // Requests spread over more than wpr PRE workgroups: PRE of the wave's partials' rows
+    // in flight at a time (columns past v_rank read column 0 and are never stored).
+    for (int i0 = PRE; sub + wpr * i0 < nk; i0 += PRE) {
+        float v[PRE][CB];
 #pragma unroll
-        for (int u = 0; u < MERGE_PRE; ++u) {
+        for (int u = 0; u < PRE; ++u) {
             const int64_t sl = s0 + (int64_t)min(sub + wpr * (i0 + u), nk - 1) * Hq;
 #pragma unroll
-            for (int j = 0; j < MERGE_CB; ++j) {
+            for (int j = 0; j < CB; ++j) {
                 const int c = lane + 64 * j;
                 v[u][j] = wa[sl * v_rank + (c < v_rank ? c : 0)];
             }
         }
 #pragma unroll
-        for (int u = 0; u < MERGE_PRE; ++u) {
+        for (int u = 0; u < PRE; ++u) {
             const int k = sub + wpr * (i0 + u);
             if (k >= nk) break;
-            const float w = k < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k))
-                                   : exp2f(wm[s0 + (int64_t)k * Hq] - M);
+            const float w = weight(k);
 #pragma unroll
-            for (int j = 0; j < MERGE_CB; ++j) acc[j] = fmaf(v[u][j], w, acc[j]);
+            for (int j = 0; j < CB; ++j) acc[j] = fmaf(v[u][j], w, acc[j]);
         }
     }
     // Row (tid >> 6) of s_o: this wave's share of request r, scaled; a request's wpr rows
     // (rows r wpr + s) are added into row r before the lift.
     const float inv = 1.f / l;
 #pragma unroll
-    for (int j = 0; j < MERGE_CB; ++j)
+    for (int j = 0; j < CB; ++j)
         if (lane + 64 * j < v_rank) s_o[(tid >> 6) * v_rank + lane + 64 * j] = acc[j] * inv;
     if (lane == 0 && sub == 0) s_live[r] = live;
     __syncthreads();
@@ -838,20 +864,29 @@ struct CommonArgs {
     int grid;
 };
 
-template <typename WT>
-static int launch_merge(dim3 grid, size_t lds, hipStream_t stream, const DecodeParams& p, const WsLayout& wl,
-                        const CommonArgs& a) {
+template <typename WT, int CB>
+static int launch_merge_cb(dim3 grid, size_t lds, hipStream_t stream, const DecodeParams& p, const WsLayout& wl,
+                           const CommonArgs& a) {
     static size_t lds_allowed = 65536;  // per function: raised as larger v_rank need it (at most 132 KB)
     if (lds > lds_allowed) {
-        SKV_HIP(hipFuncSetAttribute((const void*)merge_kernel<WT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        SKV_HIP(hipFuncSetAttribute((const void*)merge_kernel<WT, CB>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                     (int)lds));
         lds_allowed = lds;
     }
-    hipLaunchKernelGGL(merge_kernel<WT>, grid, dim3(MERGE_THR), lds, stream, (const uint8_t*)p.ws, wl.plan, wl.m, wl.l,
-                       wl.acc, a.n, a.Hq, a.v_rank, (const WT*)a.vup, a.vu_s0, a.vu_s1, a.out, a.o_s0, a.o_s1,
+    hipLaunchKernelGGL((merge_kernel<WT, CB>), grid, dim3(MERGE_THR), lds, stream, (const uint8_t*)p.ws, wl.plan, wl.m,
+                       wl.l, wl.acc, a.n, a.Hq, a.v_rank, (const WT*)a.vup, a.vu_s0, a.vu_s1, a.out, a.o_s0, a.o_s1,
                        a.out_dt);
     SKV_HIP(hipGetLastError());
     return STARKV_OK;
+}
+
+// One column per lane up to V rank 64 (the partials' rows of 32 partials per wave in flight
+// together), else four.
+template <typename WT>
+static int launch_merge(dim3 grid, size_t lds, hipStream_t stream, const DecodeParams& p, const WsLayout& wl,
+                        const CommonArgs& a) {
+    return a.v_rank <= 64 ? launch_merge_cb<WT, 1>(grid, lds, stream, p, wl, a)
+                          : launch_merge_cb<WT, MERGE_CB>(grid, lds, stream, p, wl, a);
 }
 
 // Which decode form runs: 0 = the one-pass kernels where the shape fits them, else the
