@@ -566,9 +566,10 @@ __global__ __launch_bounds__(PREP_THR) void write_prep_kernel(PrepArgs a, KvGemm
 //    every row of v_up_by_q[h] serves MERGE_REQ outputs; a call of one or two requests
 //    gives each request 4 or 2 waves, which split its partials (partial k to wave k mod
 //    the waves) and add their rows before the lift. The loads come in two phases: the
-//    request's partial range (with v_up_by_q[h] staged into LDS meanwhile), then every
-//    partial's max and sum and the wave's first MERGE_PRE partials' accumulator rows
-//    together.
+//    request's partial range (with v_up_by_q[h] staged into LDS meanwhile), then the max
+//    and sum of the first 64 MERGE_ML partials and the wave's first PRE partials'
+//    accumulator rows together (PRE = 32 at V rank <= 64, else 16); further partials
+//    follow PRE rows at a time.
 // ---------------------------------------------------------------------------
 constexpr int MERGE_REQ = 4;
 constexpr int MERGE_THR = 64 * MERGE_REQ;
