@@ -574,7 +574,7 @@ __global__ __launch_bounds__(LIFT_THR) void lift_kernel(const uint8_t* __restric
                                                         int v_rank, int ld, const void* __restrict__ vup,
                                                         int64_t vu_s0, int64_t vu_s1, void* __restrict__ out,
                                                         int64_t o_s0, int64_t o_s1, int out_dt) {
-    static_assert(DQ == 16 || DQ == 4 || DQ == 2, "8 DQ output columns per workgroup: 128, 32 or 16");
+    static_assert(DQ == 16 || DQ == 4, "8 DQ output columns per workgroup: 128 or 32");
     constexpr int LIFT_WAVES = LIFT_THR / 64;
     constexpr int DW = 8 * DQ;  // output columns of this workgroup
     extern __shared__ __align__(16) uint8_t s_dyn[];
@@ -635,10 +635,6 @@ __global__ __launch_bounds__(LIFT_THR) void lift_kernel(const uint8_t* __restric
             if constexpr (DQ == 4) {
                 v += dpp_f<0x128>(v);  // row_ror:8
                 v += dpp_f<0x124>(v);  // row_ror:4
-            } else if constexpr (DQ == 2) {
-                v += dpp_f<0x128>(v);  // row_ror:8
-                v += dpp_f<0x124>(v);  // row_ror:4
-                v += dpp_f<0x122>(v);  // row_ror:2
             }
             acc[r][e] = sum_rows(v);
         }
@@ -825,16 +821,11 @@ int launch_merge_wide(const DecodeParams& p, int grid, int w_dt, const void* vup
                            stream, (const uint8_t*)p.ws, p.ws_plan, p.ws_m, p.ws_l, p.ws_acc, p.ws_o, p.n, p.Hq,
                            p.v_rank, p.acc_ld, p.pv_r);
     SKV_HIP(hipGetLastError());
-    // At most 8 requests: pairs of requests, 32 output columns per workgroup (one or two
-    // requests: 16, so the one request pair still fills 256 workgroups).
-    const bool small = p.n <= 8, tiny = p.n <= 2;
-    const int req = small ? 2 : 8, thr = small ? 1024 : 512, dq = tiny ? 2 : small ? 4 : 16;
-    const void* fn = tiny ? (w_dt == STARKV_BF16 ? (const void*)&lift_kernel<STARKV_BF16, 2, 1024, 2>
-                             : w_dt == STARKV_F16 ? (const void*)&lift_kernel<STARKV_F16, 2, 1024, 2>
-                                                  : (const void*)&lift_kernel<STARKV_F32, 2, 1024, 2>)
-                     : small ? (w_dt == STARKV_BF16 ? (const void*)&lift_kernel<STARKV_BF16, 2, 1024, 4>
-                                : w_dt == STARKV_F16 ? (const void*)&lift_kernel<STARKV_F16, 2, 1024, 4>
-                                                     : (const void*)&lift_kernel<STARKV_F32, 2, 1024, 4>)
+    const bool small = p.n <= 8;
+    const int req = small ? 2 : 8, thr = small ? 1024 : 512, dq = small ? 4 : 16;
+    const void* fn = small ? (w_dt == STARKV_BF16 ? (const void*)&lift_kernel<STARKV_BF16, 2, 1024, 4>
+                              : w_dt == STARKV_F16 ? (const void*)&lift_kernel<STARKV_F16, 2, 1024, 4>
+                                                   : (const void*)&lift_kernel<STARKV_F32, 2, 1024, 4>)
                            : (w_dt == STARKV_BF16 ? (const void*)&lift_kernel<STARKV_BF16, 8, 512, 16>
                               : w_dt == STARKV_F16 ? (const void*)&lift_kernel<STARKV_F16, 8, 512, 16>
                                                    : (const void*)&lift_kernel<STARKV_F32, 8, 512, 16>);
