@@ -453,40 +453,6 @@ __device__ __forceinline__ void raw8_f(const Raw8<DT>& v, float* o) {
     }
 }
 
-// Rank tile t's query head, first k_up row and valid ranks, the entries tile_table gives
-// it, from one wave (every lane active, t wave-uniform): bf16/fp16 from a lane scan of the
-// kv heads' tiles (kv head u's query heads take tiles t0(u) .. t0(u) + G nt(u) - 1, nt(u)
-// each), 3.2-bit straight from the tile arrays. A tile no head covers gets zeros.
-struct TileInfo {
-    int head, row, valid;
-};
-__device__ __forceinline__ TileInfo tile_info(const PrepArgs& a, int t, int lane) {
-    TileInfo ti{0, 0, 0};
-    if (a.t_head) {
-        ti.head = min(max(a.t_head[t] - a.head0, 0), a.Hq - 1);
-        ti.row = 16 * t;
-        ti.valid = 16;
-        return ti;
-    }
-    const int grp = a.Hq / a.Hkv;
-    const int R = lane < a.Hkv ? min(max(a.k_ranks[lane], 0), 16 * MAX_TT) : 0;
-    const int off = lane < a.Hkv ? a.k_offsets[lane] : 0;
-    const int nt = (R + 15) >> 4;
-    uint32_t incl = (uint32_t)(grp * nt);
-    scan32(incl);  // Hkv <= 32 lanes
-    const int t0 = (int)incl - grp * nt;
-    const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < a.Hkv && t >= t0 && t < t0 + grp * nt);
-    if (hit == 0) return ti;
-    const int kv = (int)__builtin_ctzll(hit);
-    const int t0k = __builtin_amdgcn_readlane(t0, kv), ntk = __builtin_amdgcn_readlane(nt, kv);
-    const int Rk = __builtin_amdgcn_readlane(R, kv), ok = __builtin_amdgcn_readlane(off, kv);
-    const int local = t - t0k, j = local % ntk;
-    ti.head = kv * grp + local / ntk;
-    ti.row = min(max(ok + 16 * j, 0), a.k_rows - 16);
-    ti.valid = min(16, Rk - 16 * j);
-    return ti;
-}
-
 // Fold workgroups of prep: AB[b][t][ks][lane] = 8 fp16 of tile row m = lane & 15,
 // columns 32 ks + 8 (lane >> 4) .. +8, scaled by scale*log2(e); rows past the head's
 // rank are zero (paged_decode.py:79-81 masks them). Row m holds rank m of the tile, or,
@@ -497,18 +463,17 @@ __device__ __forceinline__ TileInfo tile_info(const PrepArgs& a, int t, int lane
 // granules once and folds them with the query of each of its requests; every load is
 // issued before the first conversion, so their latencies overlap.
 template <int QT, int UT>
-__device__ void prep_fold(const PrepArgs& a, int tid, int bid) {
+__device__ void prep_fold(const PrepArgs& a, const TileTable& tt, int tid, int bid) {
     const int tp = bid % a.tile_pairs, b0 = (bid / a.tile_pairs) * PREP_REQ;
     const int t = 2 * tp + (tid >> 7), k2 = (tid >> 6) & 1, lane = tid & 63;
-    if (t >= a.TT) return;  // wave-uniform
-    const TileInfo ti = tile_info(a, t, lane);
+    if (t >= a.TT) return;
     const bool perm = a.t_head != nullptr;
     const int m = lane & 15, lg = lane >> 4;
     const int rr = perm ? 2 * (m >> 2) + ((m >> 1) & 1) + 8 * (m & 1) : m;
     const int c0 = 32 * k2 + 8 * lg;
-    const int h = ti.head;
-    const float s = rr < ti.valid ? (perm && (m & 2) ? a.sc * 0.0625f : a.sc) : 0.f;
-    const int64_t ur = (int64_t)(ti.row + rr) * a.ku_s0;
+    const int h = tt.head[t];
+    const float s = rr < tt.valid[t] ? (perm && (m & 2) ? a.sc * 0.0625f : a.sc) : 0.f;
+    const int64_t ur = (int64_t)(tt.row[t] + rr) * a.ku_s0;
     const Raw8<UT> ru0 = raw8<UT>(a.k_up, ur + c0), ru1 = raw8<UT>(a.k_up, ur + c0 + 64);
     Raw8<QT> rq0[PREP_REQ], rq1[PREP_REQ];
 #pragma unroll
@@ -541,13 +506,13 @@ __device__ void prep_fold(const PrepArgs& a, int tid, int bid) {
 }
 
 template <int QT>
-__device__ void prep_fold_q(const PrepArgs& a, int tid, int bid) {
+__device__ void prep_fold_q(const PrepArgs& a, const TileTable& tt, int tid, int bid) {
     if (a.ku_dt == STARKV_BF16)
-        prep_fold<QT, STARKV_BF16>(a, tid, bid);
+        prep_fold<QT, STARKV_BF16>(a, tt, tid, bid);
     else if (a.ku_dt == STARKV_F16)
-        prep_fold<QT, STARKV_F16>(a, tid, bid);
+        prep_fold<QT, STARKV_F16>(a, tt, tid, bid);
     else
-        prep_fold<QT, STARKV_F32>(a, tid, bid);
+        prep_fold<QT, STARKV_F32>(a, tt, tid, bid);
 }
 
 // Workgroup `bid` of prep's grid: 0 the prefix, 1 the plan, then the fold workgroups,
@@ -564,15 +529,15 @@ __device__ __forceinline__ void prep_block(const PrepArgs& a, int bid) {
         prep_records(a, tid, bid - 2 - a.fold_wgs, s_pp, s_len);
         return;
     }
+    tile_table(a, tt, tid);
     if (bid == 1) {
-        tile_table(a, tt, tid);
         prep_plan(a, tt, tid);
-    } else if (a.q_dt == STARKV_BF16) {  // the fold workgroups need only their own tiles
-        prep_fold_q<STARKV_BF16>(a, tid, bid - 2);
+    } else if (a.q_dt == STARKV_BF16) {
+        prep_fold_q<STARKV_BF16>(a, tt, tid, bid - 2);
     } else if (a.q_dt == STARKV_F16) {
-        prep_fold_q<STARKV_F16>(a, tid, bid - 2);
+        prep_fold_q<STARKV_F16>(a, tt, tid, bid - 2);
     } else {
-        prep_fold_q<STARKV_F32>(a, tid, bid - 2);
+        prep_fold_q<STARKV_F32>(a, tt, tid, bid - 2);
     }
 }
 
