@@ -61,7 +61,11 @@ int starkv_write_codes(void *stream, const void *k_codes, int64_t k_s0, const vo
  * Fused cache write of one layer step: codes = hidden @ kv_down^T (fp32 accumulate,
  * rounded to the model dtype with round-to-nearest-even, as F.linear returns them),
  * then either the bf16/fp16 scatter (row_bytes == 0) or the 3.2-bit quantize + scatter
- * (row_bytes == QuantRow.nbytes), in two launches. Replaces the code GEMM of
+ * (row_bytes == QuantRow.nbytes). Up to 256 tokens: split-K partial products, then a
+ * store launch; one token (hidden_size a multiple of 512, at most 4096) or two (hidden_size
+ * 4096): one launch whose workgroups own whole codes and store them (bf16/fp16 rows, the
+ * 3.2-bit K blocks), then for a 3.2-bit row one launch that packs the V latent. Replaces
+ * the code GEMM of
  * StarKVLlamaAttention.forward, starkv_serve/model.py:71 (kv = F.linear(hidden,
  * kv_down), kv_down = cat(k_down, v_down) from attention.py:161), followed by the cache
  * write of StarKVAttentionImpl.forward, starkv_serve/attention.py:179-188 (cat +
@@ -79,7 +83,8 @@ int starkv_write_codes(void *stream, const void *k_codes, int64_t k_s0, const vo
  *   codes_out [n, k_width + v_rank] of the model dtype, row stride co_s0, or NULL: the
  *             rounded codes (what F.linear returns)
  *   workspace >= starkv_write_kv_workspace_bytes(n, k_width + v_rank, hidden_size) bytes,
- *             16-byte aligned (fp32 split-K partials)
+ *             16-byte aligned (fp32 split-K partials, or the direct form's rounded codes
+ *             and V maxima)
  */
 size_t starkv_write_kv_workspace_bytes(int n, int width, int hidden_size);
 int starkv_write_kv(void *stream, const void *hidden, int64_t h_s0, const void *kv_down, int64_t w_s0,
@@ -94,7 +99,11 @@ int starkv_write_kv(void *stream, const void *hidden, int64_t h_s0, const void *
  * the same stream (starkv_lowrank_decode, starkv_quant_decode and their group and
  * no-alloc forms): that call runs the write's code GEMM inside its own first launch (the
  * page plan and query fold, which do not depend on the write), then the write's store,
- * then its decode kernels, so a decode step's write and decode take one launch fewer.
+ * then its decode kernels, so a decode step's write and decode take one launch fewer. A
+ * write of the direct form (one or two tokens, above) has no store launch: its 3.2-bit V
+ * latent is packed by the decode's logits pass when the decode is two-pass (P @ V, a later
+ * launch, is the first reader of V), else by its own launch; the write and decode of one
+ * token then take two launches fewer.
  * Same arguments, checks and results as starkv_write_kv; the reference has no
  * counterpart (its write and decode are separate framework calls, attention.py:179-217).
  * Until the write is launched, hidden, kv_down, the slot mapping, the head arrays and the

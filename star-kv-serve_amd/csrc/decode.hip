@@ -559,6 +559,24 @@ __global__ __launch_bounds__(PREP_THR) void write_prep_kernel(PrepArgs a, KvGemm
     const int gb = bid - prep_wgs;
     kv_gemm_block<DT>(g, gb % gx, (gb / gx) % gy, gb / (gx * gy));
 }
+// The same with the direct form of the write (one or two tokens): its jobs after prep's
+// workgroups.
+template <int DT, int TOK, int SL>
+__global__ __launch_bounds__(PREP_THR) void write_prep_direct_kernel(PrepArgs a, KvDirectParams d, int prep_wgs) {
+    const int bid = blockIdx.x;
+    if (bid < prep_wgs) {
+        prep_block(a, bid);
+        return;
+    }
+    kv_direct_block<DT, TOK, SL>(d, bid - prep_wgs);
+}
+template <int DT>
+static const void* write_prep_direct_fn(int n, int slices) {
+    if (slices == KVD_MAX_SLICES)
+        return n == 1 ? (const void*)&write_prep_direct_kernel<DT, 1, KVD_MAX_SLICES>
+                      : (const void*)&write_prep_direct_kernel<DT, 2, KVD_MAX_SLICES>;
+    return (const void*)&write_prep_direct_kernel<DT, 1, 0>;  // two tokens take the direct form only at SL
+}
 
 // ---------------------------------------------------------------------------
 // 3. merge: per (request, head) the partials' log-sum-exp, then the lift through
@@ -1084,6 +1102,7 @@ static int decode_common_body(DecodeParams& p, const CommonArgs& a, int fmt, int
     SKV_CHECK(TT >= 1 && TT <= MAX_TT, "decode: %d rank tiles (1..%d: k_width x heads per kv head <= %d)", TT,
               MAX_TT, MAX_TT * 16);
     const bool two = use_two_pass(fmt, p.k_width, a.v_rank, row_bytes, p.v_nout, TT);
+    p.vp.n = 0;
     const int lcap = two ? lcap_of(a.max_seq_len) : 0;
     const int pv_r = two ? pv_ratio(fmt, a.n, a.max_seq_len, a.grid) : 1;
     SKV_CHECK(a.max_seq_len <= (1 << 24), "decode: max_seq_len %d > 2^24", a.max_seq_len);
@@ -1188,18 +1207,28 @@ static int decode_common_body(DecodeParams& p, const CommonArgs& a, int fmt, int
     if (pending_write_on(stream, &pg)) {
         // A deferred write on this stream: its GEMM rides in prep's launch, its store
         // follows, and the decode kernels read the cache after both.
-        const int64_t gw = (int64_t)pg.gx * pg.gy * pg.gz;
+        const int64_t gw = pg.direct ? (int64_t)pg.d.jobs : (int64_t)pg.gx * pg.gy * pg.gz;
         SKV_CHECK(prep_grid + gw < ((int64_t)1 << 31), "decode: %d prep and %lld write workgroups", prep_grid,
                   (long long)gw);
-        if (pg.w_dtype == STARKV_BF16)
+        if (pg.direct) {
+            const void* fn = pg.w_dtype == STARKV_BF16 ? write_prep_direct_fn<STARKV_BF16>(pg.d.n, pg.d.slices)
+                                                       : write_prep_direct_fn<STARKV_F16>(pg.d.n, pg.d.slices);
+            int pw = prep_grid;
+            void* args[] = {(void*)&pa, (void*)&pg.d, (void*)&pw};
+            SKV_HIP(hipLaunchKernel(fn, dim3(prep_grid + (int)gw), dim3(PREP_THR), args, 0, stream));
+        } else if (pg.w_dtype == STARKV_BF16)
             hipLaunchKernelGGL(write_prep_kernel<STARKV_BF16>, dim3(prep_grid + (int)gw), dim3(PREP_THR), 0, stream,
                                pa, pg.g, prep_grid, pg.gx, pg.gy);
         else
             hipLaunchKernelGGL(write_prep_kernel<STARKV_F16>, dim3(prep_grid + (int)gw), dim3(PREP_THR), 0, stream,
                                pa, pg.g, prep_grid, pg.gx, pg.gy);
         SKV_HIP(hipGetLastError());
-        const int wrc = launch_pending_store();
-        if (wrc) return wrc;
+        // A direct 3.2-bit write's V latents are packed by the logits pass of a two-pass
+        // decode (P @ V, a later launch, reads them), else by their own launch.
+        if (!(two && fmt == FMT_Q4 && take_pending_vpack(&p.vp))) {
+            const int wrc = launch_pending_store();
+            if (wrc) return wrc;
+        }
     } else {
         const int wrc = flush_pending_write();  // a deferred write on another stream: its own launches
         if (wrc) return wrc;
@@ -1210,7 +1239,10 @@ static int decode_common_body(DecodeParams& p, const CommonArgs& a, int fmt, int
     int rc;
     if (two) {
         rc = fmt == FMT_Q4 ? launch_quant(p, 0, a.grid, stream) : launch_lowrank(p, fmt, 0, a.grid, stream);
-        if (rc) return rc;
+        if (rc) {
+            if (p.vp.n > 0) launch_vpack_on(p.vp, stream);  // the logits pass did not run: the write still lands
+            return rc;
+        }
         SKV_HIP(hipGetLastError());
         rc = launch_pv(p, fmt, a.grid, stream);
     } else {

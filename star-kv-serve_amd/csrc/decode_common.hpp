@@ -9,6 +9,7 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "pack_rows.hpp"
 
 namespace starkv {
 enum { FMT_BF16 = 0, FMT_F16 = 1, FMT_Q4 = 2 };
@@ -142,6 +143,7 @@ struct DecodeParams {
     size_t ws_o; int acc_ld;                       // two-pass calls: merged outputs; acc / o row floats
     int pv_r;                                      // two-pass calls: logits-pass ranges per P @ V range
     size_t ws_pages;                               // page records
+    VPackParams vp;                                // 3.2-bit logits pass: a direct write's V latents (vp.n > 0)
 };
 
 __device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }

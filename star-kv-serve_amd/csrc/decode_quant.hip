@@ -481,6 +481,16 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
         const uint32_t mb = (2 * g + 1 < c ? 0x0000ffffu : 0u) | (2 * g + 9 < c ? 0xffff0000u : 0u);
         s_omask[c][g] = make_uint2(ma, mb);
     }
+    // The logits pass of a step whose direct write left its V latents to pack: the last
+    // wave of each workgroup packs the workgroup's share of their bytes (P @ V, the next
+    // launch, reads them).
+    if constexpr (NB == 0) {
+        if (wave == NWAVE - 1 && p.vp.n > 0) {
+            const int64_t G = gridDim.x, b = blockIdx.x, nb = p.vp.v_bytes;
+            for (int t = 0; t < p.vp.n; ++t)
+                vpack_range(p.vp, t, (int)(b * nb / G), (int)((b + 1) * nb / G), b == 0, lane);
+        }
+    }
     if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
     QLoop st;
     if (!page_loop_init<3>(st, p, xcd_range(blockIdx.x, gridDim.x))) return;

@@ -1,5 +1,5 @@
-// Fused cache write of one layer step: the code projection hidden @ kv_down^T on MFMA,
-// then the bf16/fp16 scatter or the 3.2-bit quantize + scatter, in two launches.
+// Fused cache write of one layer step: the code projection hidden @ kv_down^T, then the
+// bf16/fp16 scatter or the 3.2-bit quantize + scatter.
 //
 // Reference: the model's code GEMM (starkv_serve/model.py:71: kv = F.linear(hidden,
 // kv_down), kv_down = [k_down; v_down], attention.py:161) and the cache write of
@@ -19,10 +19,15 @@
 //    from LDS exactly as pack_kv reads them from memory. For at most 16 tokens of a
 //    3.2-bit cache, `groups` workgroups per token (each forming the codes) share its H K
 //    blocks and V block, one block per wave.
+// One token (hidden a multiple of 512, at most 4096) or two (hidden 4096) take the direct form
+// instead (kv_gemm.hpp): kv_direct_kernel's workgroups own whole codes and store the
+// bf16/fp16 row, or pack the 3.2-bit K blocks; a 3.2-bit row's V latent then takes
+// kv_vpack_kernel (or, for a deferred write, the next decode's logits pass). Against
+// the split form at one 16K-token layer step (hidden 4096, 2170 codes) it drops the
+// store launch.
 #include <algorithm>
 
 #include "kv_gemm.hpp"
-#include "pack_rows.hpp"
 
 namespace starkv {
 
@@ -46,15 +51,16 @@ struct KvStoreParams {
     int groups;                       // 3.2-bit rows: workgroups per token (grid.y) sharing its H + 1 blocks
 };
 
-template <int DT>
-__device__ __forceinline__ uint16_t round_code(float x) {
-    if constexpr (DT == STARKV_BF16) return f32_to_bf16_rne(x);
-    else return __builtin_bit_cast(uint16_t, (_Float16)x);
+template <int DT, int TOK, int SL>
+__global__ __launch_bounds__(KVW_THR) void kv_direct_kernel(const KvDirectParams p) {
+    kv_direct_block<DT, TOK, SL>(p, blockIdx.x);
 }
-template <int DT>
-__device__ __forceinline__ float code_value(uint16_t r) {
-    if constexpr (DT == STARKV_BF16) return bf16_bits_to_f32(r);
-    else return (float)__builtin_bit_cast(_Float16, r);
+
+// The V latent of token blockIdx.x: wave w packs a quarter of its bytes (wave 0 also the
+// zero bytes and the scales).
+__global__ __launch_bounds__(256) void kv_vpack_kernel(const VPackParams q) {
+    const int w = threadIdx.x >> 6;
+    vpack_range(q, blockIdx.x, w * q.v_bytes / 4, (w + 1) * q.v_bytes / 4, w == 0, threadIdx.x & 63);
 }
 
 // S = the GEMM's K splits (a launch constant): exactly the S partials of each column load.
@@ -159,6 +165,9 @@ struct WriteLaunch {
     KvStoreParams s;
     const void* store_fn;
     size_t lds;
+    bool direct;        // the direct form (d, and v for a 3.2-bit row)
+    KvDirectParams d;
+    VPackParams v;
 };
 
 // The calling thread's deferred write (starkv_write_kv_deferred), launched by its next
@@ -224,6 +233,45 @@ static int prepare_write(WriteLaunch& w, void* stream, const void* hidden, int64
     s.groups = quant && n <= 16 ? std::max(1, std::min(8, (num_kv_heads + 1 + KVS_THR / 64 - 1) / (KVS_THR / 64))) : 1;
     const size_t lds = (size_t)width * sizeof(float);
     SKV_CHECK(lds <= 64 * 1024, "write_kv: %d codes per token exceed the 64 KB LDS block", width);
+    // Two tokens only at hidden 4096 (the compiled slice count: registers for both rows).
+    w.direct = hidden_size % 512 == 0 && hidden_size <= 512 * KVD_MAX_SLICES &&
+               (n == 1 || (n == 2 && hidden_size == 512 * KVD_MAX_SLICES));
+    if (w.direct) {
+        KvDirectParams& d = w.d;
+        memset(&d, 0, sizeof(d));
+        d.hidden = (const uint16_t*)hidden; d.h_s0 = h_s0;
+        d.w = (const uint16_t*)kv_down; d.w_s0 = w_s0;
+        d.n = n; d.slices = hidden_size / 512; d.width = width; d.k_width = k_width; d.v_rank = v_rank;
+        d.quant = quant;
+        d.codes = (uint16_t*)codes_out; d.co_s0 = co_s0;
+        d.cache = cache; d.c_s0 = c_s0; d.c_s1 = c_s1;
+        d.block_size = block_size; d.num_blocks = num_blocks;
+        d.slots = slot_mapping; d.slot_bits = slot_bits;
+        if (quant) {
+            // Workspace: the rounded codes [n][width] (uint16), then the V maxima.
+            d.k_jobs = num_kv_heads;
+            d.kt_jobs = codes_out ? (k_width + 15) / 16 : 0;
+            d.vtiles = (v_rank + 15) / 16;
+            d.jobs = d.k_jobs + d.kt_jobs + d.vtiles;
+            d.ranks = k_ranks; d.offsets = k_offsets; d.nouts = k_nouts; d.ks_off = rl.ks_off;
+            d.v_nout = rl.v_nout;
+            d.rc = (uint16_t*)workspace;
+            const size_t vm_off = ((size_t)n * width * 2 + 15) / 16 * 16;
+            d.vmax = (float*)((uint8_t*)workspace + vm_off);
+            SKV_CHECK(vm_off + (size_t)n * d.vtiles * 8 <= workspace_bytes, "write_kv: workspace %zu bytes too small",
+                      workspace_bytes);
+            VPackParams& v = w.v;
+            v.rc = d.rc; v.vmax = d.vmax;
+            v.n = n; v.width = width; v.k_width = k_width; v.vtiles = d.vtiles; v.dt = w_dtype;
+            v.v_rank = v_rank; v.v_nout = rl.v_nout; v.v_nbo = rl.v_nbo; v.v_bytes = rl.v_bytes;
+            v.vq_off = rl.vq_off; v.vs_off = rl.vs_off; v.row_bytes = rl.nbytes;
+            v.cache = (uint8_t*)cache; v.c_s0 = c_s0; v.c_s1 = c_s1;
+            v.block_size = block_size; v.num_blocks = num_blocks;
+            v.slots = slot_mapping; v.slot_bits = slot_bits;
+        } else {
+            d.jobs = (width + 15) / 16;
+        }
+    }
     w.stream = (hipStream_t)stream;
     w.w_dtype = w_dtype;
     w.g = g;
@@ -236,13 +284,41 @@ static int prepare_write(WriteLaunch& w, void* stream, const void* hidden, int64
     return STARKV_OK;
 }
 
+int launch_vpack_on(const VPackParams& v, hipStream_t stream) {
+    hipLaunchKernelGGL(kv_vpack_kernel, dim3(v.n), dim3(256), 0, stream, v);
+    SKV_HIP(hipGetLastError());
+    return STARKV_OK;
+}
+
+// The direct form's V latent (3.2-bit rows; nothing for bf16/fp16 rows).
+static int launch_vpack(const WriteLaunch& w) {
+    if (!w.d.quant) return STARKV_OK;
+    return launch_vpack_on(w.v, w.stream);
+}
+
+template <int DT>
+static const void* kv_direct_fn(int n, int slices) {
+    if (slices == KVD_MAX_SLICES)
+        return n == 1 ? (const void*)&kv_direct_kernel<DT, 1, KVD_MAX_SLICES>
+                      : (const void*)&kv_direct_kernel<DT, 2, KVD_MAX_SLICES>;
+    return (const void*)&kv_direct_kernel<DT, 1, 0>;
+}
+
 static int launch_store(WriteLaunch& w) {
+    if (w.direct) return launch_vpack(w);
     void* args[] = {(void*)&w.s};
     SKV_HIP(hipLaunchKernel(w.store_fn, dim3(w.s.n, w.s.groups), dim3(KVS_THR), args, w.lds, w.stream));
     return STARKV_OK;
 }
 
 static int launch_write(WriteLaunch& w) {
+    if (w.direct) {
+        const void* fn = w.w_dtype == STARKV_BF16 ? kv_direct_fn<STARKV_BF16>(w.d.n, w.d.slices)
+                                                    : kv_direct_fn<STARKV_F16>(w.d.n, w.d.slices);
+        void* args[] = {(void*)&w.d};
+        SKV_HIP(hipLaunchKernel(fn, dim3(w.d.jobs), dim3(KVW_THR), args, 0, w.stream));
+        return launch_vpack(w);
+    }
     if (w.w_dtype == STARKV_BF16)
         hipLaunchKernelGGL(kv_gemm_kernel<STARKV_BF16>, w.ggrid, dim3(KVW_THR), 0, w.stream, w.g);
     else
@@ -259,6 +335,15 @@ bool pending_write_on(hipStream_t stream, PendingGemm* out) {
     out->gx = (int)t_pending.ggrid.x;
     out->gy = (int)t_pending.ggrid.y;
     out->gz = (int)t_pending.ggrid.z;
+    out->direct = t_pending.direct;
+    out->d = t_pending.d;
+    return true;
+}
+
+bool take_pending_vpack(VPackParams* out) {
+    if (!t_has_pending || !t_pending.direct || !t_pending.d.quant) return false;
+    *out = t_pending.v;
+    t_has_pending = false;
     return true;
 }
 

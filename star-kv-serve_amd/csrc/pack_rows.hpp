@@ -59,6 +59,37 @@ __device__ __forceinline__ void pack_k_block(Src&& src, int R, int nout, int off
 // each block byte-aligned (nbo outlier bytes, nb bytes in all); an odd block ends in a
 // padding nibble 8 (paged_quant.py:184-199). src(c) is channel c. Bytes
 // [vq_off + nb, row_bytes) are written as zero (the reference leaves them unwritten).
+// The pieces (scales from the two maxima, one byte, the tail) are shared with the
+// direct write, which packs a row's bytes over several workgroups.
+struct VScales {
+    float s_out, s_in;
+};
+// a_out / a_in: max |x| over the outlier / inlier channels (0 when there are none).
+__device__ __forceinline__ VScales v_scales(float a_out, float a_in) {
+    return VScales{__fdiv_rn(fmaxf(a_out, 1e-5f), 7.0f), __fdiv_rn(fmaxf(a_in, 1e-5f), 3.0f)};
+}
+template <class Src>
+__device__ __forceinline__ uint8_t pack_v_byte(Src&& src, int j, int R, int nout, int nbo, VScales s) {
+    const bool in_out = j < nbo;
+    const int c_lo = in_out ? 2 * j : nout + 2 * (j - nbo);
+    const int c_end = in_out ? nout : R;
+    const float sc = in_out ? s.s_out : s.s_in;
+    const float lo = in_out ? -8.f : -4.f, hi = in_out ? 7.f : 3.f;
+    int nl = 8, nh = 8;
+    if (c_lo < c_end) nl = quant_code(src(c_lo), sc, lo, hi);
+    if (c_lo + 1 < c_end) nh = quant_code(src(c_lo + 1), sc, lo, hi);
+    return (uint8_t)(nl | (nh << 4));
+}
+// The zero bytes after the codes (lanes of one wave) and the two scales (lane 0).
+__device__ __forceinline__ void pack_v_tail(VScales s, int nout, int nb, int vq_off, int vs_off, int row_bytes,
+                                            uint8_t* row, int lane) {
+    for (int j = vq_off + nb + lane; j < row_bytes; j += 64) row[j] = 0;
+    if (lane == 0) {
+        const uint16_t so = f32_to_bf16_rne(nout > 0 ? s.s_out : 1.0f), si = f32_to_bf16_rne(s.s_in);
+        *(uint32_t*)(row + vs_off) = (uint32_t)so | ((uint32_t)si << 16);
+    }
+}
+
 template <class Src>
 __device__ __forceinline__ void pack_v_block(Src&& src, int R, int nout, int nbo, int nb, int vq_off, int vs_off,
                                              int row_bytes, uint8_t* row, int lane) {
@@ -67,26 +98,47 @@ __device__ __forceinline__ void pack_v_block(Src&& src, int R, int nout, int nbo
         const float x = fabsf(src(c));
         if (c < nout) a_out = fmaxf(a_out, x); else a_in = fmaxf(a_in, x);
     }
-    a_out = fmaxf(wave_max(a_out), 1e-5f);
-    a_in = fmaxf(wave_max(a_in), 1e-5f);
-    const float s_out = __fdiv_rn(a_out, 7.0f);
-    const float s_in = __fdiv_rn(a_in, 3.0f);
-    for (int j = lane; j < nb; j += 64) {
-        const bool in_out = j < nbo;
-        const int c_lo = in_out ? 2 * j : nout + 2 * (j - nbo);
-        const int c_end = in_out ? nout : R;
-        const float s = in_out ? s_out : s_in;
-        const float lo = in_out ? -8.f : -4.f, hi = in_out ? 7.f : 3.f;
-        int nl = 8, nh = 8;
-        if (c_lo < c_end) nl = quant_code(src(c_lo), s, lo, hi);
-        if (c_lo + 1 < c_end) nh = quant_code(src(c_lo + 1), s, lo, hi);
-        row[vq_off + j] = (uint8_t)(nl | (nh << 4));
+    const VScales s = v_scales(wave_max(a_out), wave_max(a_in));
+    for (int j = lane; j < nb; j += 64) row[vq_off + j] = pack_v_byte(src, j, R, nout, nbo, s);
+    pack_v_tail(s, nout, nb, vq_off, vs_off, row_bytes, row, lane);
+}
+
+__device__ __forceinline__ float code_value_rt(uint16_t r, int dt) {
+    return dt == STARKV_BF16 ? bf16_bits_to_f32(r) : (float)__builtin_bit_cast(_Float16, r);
+}
+
+// The V latent's bytes [j0, j1) of token t from rounded codes rc [n][width] (model dtype
+// dt; V codes from column k_width) and the maxima of their 16-code groups per class,
+// vmax [n][vtiles] (outlier, inlier): the direct write's workspace. One wave; `tail`:
+// also the zero bytes and the two scales. The maxima of the groups are the block's, so
+// the bytes are pack_v_block's.
+struct VPackParams {
+    const uint16_t* rc; const float* vmax;
+    int n, width, k_width, vtiles, dt;
+    int v_rank, v_nout, v_nbo, v_bytes, vq_off, vs_off, row_bytes;
+    uint8_t* cache; int64_t c_s0, c_s1;
+    int block_size; int64_t num_blocks;
+    const void* slots; int slot_bits;
+};
+
+__device__ __forceinline__ void vpack_range(const VPackParams& q, int t, int j0, int j1, bool tail, int lane) {
+    const int64_t slot = load_slot(q.slots, q.slot_bits, t);
+    if (slot >= q.num_blocks * q.block_size) return;  // past the cache: skipped
+    uint8_t* row = q.cache + (slot / q.block_size) * q.c_s0 + (slot % q.block_size) * q.c_s1;
+    const float2* vm = (const float2*)q.vmax + (int64_t)t * q.vtiles;
+    float a_out = 0.f, a_in = 0.f;
+    for (int i = lane; i < q.vtiles; i += 64) {
+        const float2 m = vm[i];
+        a_out = fmaxf(a_out, m.x);
+        a_in = fmaxf(a_in, m.y);
     }
-    for (int j = vq_off + nb + lane; j < row_bytes; j += 64) row[j] = 0;
-    if (lane == 0) {
-        const uint16_t so = f32_to_bf16_rne(nout > 0 ? s_out : 1.0f), si = f32_to_bf16_rne(s_in);
-        *(uint32_t*)(row + vs_off) = (uint32_t)so | ((uint32_t)si << 16);
-    }
+    const VScales s = v_scales(wave_max(a_out), wave_max(a_in));
+    const uint16_t* src = q.rc + (int64_t)t * q.width + q.k_width;
+    const int dt = q.dt;
+    for (int j = j0 + lane; j < j1; j += 64)
+        row[q.vq_off + j] = pack_v_byte([&](int c) { return code_value_rt(src[c], dt); }, j, q.v_rank, q.v_nout,
+                                        q.v_nbo, s);
+    if (tail) pack_v_tail(s, q.v_nout, q.v_bytes, q.vq_off, q.vs_off, q.row_bytes, row, lane);
 }
 
 // QuantRow (paged_quant.py:71-111) on the host: V outlier channels, V outlier bytes,

@@ -10,7 +10,11 @@ Pins:
   on [0, vq_off + v_bytes), and the pad bytes are 0;
 - slot -1 writes the null block 0; slots past the cache are skipped;
 - the same for a prompt's many tokens (above FUSED_MAX_TOKENS: the codes from F.linear,
-  then the store kernels).
+  then the store kernels);
+- one token (hidden a multiple of 512) or two (hidden 4096) take the direct form (each
+  workgroup owns whole codes): the same pins, K blocks wider than the form's LDS staging (144 codes)
+  included, and 3.2-bit rows written without codes_out (no code-only jobs) equal those
+  written with it.
 """
 import math
 
@@ -28,14 +32,14 @@ RANKS = [16, 32, 48, 64, 24, 16, 40, 56]
 V_RANK = 40
 
 
-def _layer(cuda, hidden, kv_quant, dtype):
+def _layer(cuda, hidden, kv_quant, dtype, ranks=RANKS, v_rank=V_RANK):
     import tempfile
     import os
     with tempfile.TemporaryDirectory() as d:
         path = os.path.join(d, "w.pt")
-        ck.write_fused_checkpoint(path, 1, len(RANKS), 128, hidden, {0: (RANKS, V_RANK)}, seed=hidden)
-        w = ck.load_fused_checkpoint(path, 1, len(RANKS), 128, dtype=dtype, kv_quant=kv_quant).layers[0]
-    return w, ck.layer_operands(w, len(RANKS), cuda, dtype)
+        ck.write_fused_checkpoint(path, 1, len(ranks), 128, hidden, {0: (ranks, v_rank)}, seed=hidden)
+        w = ck.load_fused_checkpoint(path, 1, len(ranks), 128, dtype=dtype, kv_quant=kv_quant).layers[0]
+    return w, ck.layer_operands(w, len(ranks), cuda, dtype)
 
 
 def _ulp(x, dtype):
@@ -65,7 +69,9 @@ def _slots(n, num_blocks, gen):
     return s
 
 
-@pytest.mark.parametrize("n,hidden,dtype", [(1, 4096, torch.bfloat16), (37, 4096, torch.bfloat16),
+@pytest.mark.parametrize("n,hidden,dtype", [(1, 4096, torch.bfloat16), (2, 4096, torch.bfloat16),
+                                            (2, 3072, torch.float16), (1, 512, torch.float16),
+                                            (1, 3072, torch.bfloat16), (37, 4096, torch.bfloat16),
                                             (64, 4096, torch.bfloat16), (130, 4096, torch.bfloat16),
                                             (9, 3072, torch.bfloat16), (21, 4096, torch.float16),
                                             (600, 4096, torch.bfloat16), (257, 4096, torch.float16)])
@@ -94,27 +100,36 @@ def test_write_kv_codes_and_cache(cuda, n, hidden, dtype):
     assert torch.equal(flat[rest].view(torch.int16), before.reshape(-1, w.cache_width)[rest].view(torch.int16))
 
 
-@pytest.mark.parametrize("n", [1, 37, 64, 600])
-def test_write_kv_quant_rows(cuda, n):
-    print(f"\n[write_kv quant] n={n}", flush=True)
-    w, ops = _layer(cuda, 4096, True, torch.bfloat16)
+@pytest.mark.parametrize("n,ranks,v_rank,dtype", [(1, RANKS, V_RANK, torch.bfloat16),
+                                                  (2, RANKS, V_RANK, torch.bfloat16),
+                                                  (2, [144, 32, 16], 300, torch.bfloat16),
+                                                  (1, [24] * 40, 1290, torch.float16),
+                                                  (37, RANKS, V_RANK, torch.bfloat16),
+                                                  (64, RANKS, V_RANK, torch.bfloat16),
+                                                  (600, RANKS, V_RANK, torch.bfloat16)])
+def test_write_kv_quant_rows(cuda, n, ranks, v_rank, dtype):
+    print(f"\n[write_kv quant] n={n} heads={len(ranks)} v_rank={v_rank} dtype={dtype}", flush=True)
+    w, ops = _layer(cuda, 4096, True, dtype, ranks, v_rank)
     row = ops.row
     g = torch.Generator().manual_seed(100 + n)
-    hid = torch.randn(n, 4096, generator=g).to(torch.bfloat16).to(cuda)
+    hid = torch.randn(n, 4096, generator=g).to(dtype).to(cuda)
     nb = max(4, (n + 15) // 16 + 2)
     cache = torch.full((nb, 16, row.nbytes), 0xA5, dtype=torch.uint8, device=cuda)
     slots = _slots(n, nb, g)
-    codes = write_kv(hid, ops.kv_down, cache, slots.to(cuda), w.k_width, row=row, k_ranks=ops.k_ranks,
-                     k_offsets=ops.k_head_offsets, k_nouts=ops.k_nouts, return_codes=True)
+    args = dict(row=row, k_ranks=ops.k_ranks, k_offsets=ops.k_head_offsets, k_nouts=ops.k_nouts)
+    codes = write_kv(hid, ops.kv_down, cache, slots.to(cuda), w.k_width, return_codes=True, **args)
+    cache2 = torch.full_like(cache, 0x5A)
+    write_kv(hid, ops.kv_down, cache2, slots.to(cuda), w.k_width, **args)
     torch.cuda.synchronize()
-    _check_codes(codes, hid, ops.kv_down, torch.bfloat16, f"quant n={n}")
-    lay = ref.row_layout(w.k_width, len(RANKS), w.v_rank)
+    _check_codes(codes, hid, ops.kv_down, dtype, f"quant n={n}")
+    lay = ref.row_layout(w.k_width, len(ranks), w.v_rank)
     assert lay["nbytes"] == row.nbytes
     c = codes.float().cpu().numpy()
     want = np.zeros((n, 1, row.nbytes), np.uint8)
-    widths, offsets, _ = ref.head_layout(RANKS)
-    cquant.pack_kv(c[:, :w.k_width], c[:, w.k_width:], want, np.arange(n), RANKS, offsets,
-                   [ref.n_outlier(r) for r in RANKS], w.v_rank, lay["ks_off"], lay["vs_off"], lay["vq_off"])
+    widths, offsets, _ = ref.head_layout(ranks)
+    cquant.pack_kv(c[:, :w.k_width], c[:, w.k_width:], want, np.arange(n), ranks, offsets,
+                   [ref.n_outlier(r) for r in ranks], w.v_rank, lay["ks_off"], lay["vs_off"], lay["vq_off"])
+    flat2 = cache2.reshape(-1, row.nbytes).cpu().numpy()
     flat = cache.reshape(-1, row.nbytes).cpu().numpy()
     end = lay["vq_off"] + lay["v_bytes"]
     for i, s in enumerate(slots.tolist()):
@@ -123,6 +138,7 @@ def test_write_kv_quant_rows(cuda, n):
             continue
         assert np.array_equal(flat[s, :end], want[i, 0, :end]), (i, s)
         assert not flat[s, end:].any(), (i, s)
+        assert np.array_equal(flat2[s], flat[s]), (i, s)  # written without codes_out
 
 
 def test_write_codes_matches_reference_scatter(cuda):
