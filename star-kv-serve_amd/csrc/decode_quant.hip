@@ -483,17 +483,28 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     }
     // The logits pass of a step whose direct write left its V latents to pack: the last
     // wave of each workgroup packs the workgroup's share of their bytes (P @ V, the next
-    // launch, reads them).
+    // launch, reads them); its loads are issued here and used after the setup below.
+    const bool vpk = NB == 0 && wave == NWAVE - 1 && p.vp.n > 0;
+    const int vj0 = (int)((int64_t)blockIdx.x * p.vp.v_bytes / gridDim.x);
+    const int vj1 = (int)((int64_t)(blockIdx.x + 1) * p.vp.v_bytes / gridDim.x);
+    VPackPre vpre;
     if constexpr (NB == 0) {
-        if (wave == NWAVE - 1 && p.vp.n > 0) {
-            const int64_t G = gridDim.x, b = blockIdx.x, nb = p.vp.v_bytes;
-            for (int t = 0; t < p.vp.n; ++t)
-                vpack_range(p.vp, t, (int)(b * nb / G), (int)((b + 1) * nb / G), b == 0, lane);
-        }
+        if (vpk && vpack_two_step(p.vp, vj0, vj1)) vpre = vpack_load(p.vp, vj0, vj1, lane);
     }
-    if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
+    auto vpack_share = [&]() {
+        if constexpr (NB == 0) {
+            if (vpk) {
+                if (vpack_two_step(p.vp, vj0, vj1)) vpack_store(p.vp, vpre, vj0, vj1, blockIdx.x == 0, lane);
+                else for (int t = 0; t < p.vp.n; ++t) vpack_range(p.vp, t, vj0, vj1, blockIdx.x == 0, lane);
+            }
+        }
+    };
     QLoop st;
-    if (!page_loop_init<3>(st, p, xcd_range(blockIdx.x, gridDim.x))) return;
+    // No wave plan (the merge reports NaN) or no pages: the workgroup packs its share and leaves.
+    if (plan[NWAVE * PLAN_STRIDE] == 0 || !page_loop_init<3>(st, p, xcd_range(blockIdx.x, gridDim.x))) {
+        vpack_share();
+        return;
+    }
 
     // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
     cint_p pw = plan + wave * PLAN_STRIDE;
@@ -612,6 +623,7 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
         doff[i] = off;
     }
     const DmaConst dc = dma_const(p, base, wave, base + (uint32_t)((p.nch + 2 * NB) * PAGE_STRIDE));
+    vpack_share();
     __syncthreads();
 
     st.pv = false;

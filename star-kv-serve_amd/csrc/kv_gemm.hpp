@@ -194,37 +194,9 @@ __device__ __forceinline__ void kv_direct_block(const KvDirectParams& p, int job
     const bool lane_st = lane < KVD_COLS * TOK && lt < p.n;
     float vmo = 0.f, vmi = 0.f;  // kind 3: this lane's |code| by class
     uint4 hv[TOK][NS];
-    for (int cr = c0; cr < c0 + nc; cr += 16) {
-        const int cb = cr + KVD_COLS * wave;
-        uint4 wv[KVD_COLS][NS];
-#pragma unroll
-        for (int i = 0; i < KVD_COLS; ++i)
-#pragma unroll
-            for (int s = 0; s < NS; ++s)
-                wv[i][s] = *(const uint4*)(p.w + (int64_t)min(cb + i, p.width - 1) * p.w_s0 + 512 * min(s, S - 1) +
-                                           8 * lane);
-        if (cr == c0) {
-#pragma unroll
-            for (int t = 0; t < TOK; ++t)
-#pragma unroll
-                for (int s = 0; s < NS; ++s)
-                    hv[t][s] = *(const uint4*)(p.hidden + (int64_t)min(t, p.n - 1) * p.h_s0 + 512 * min(s, S - 1) +
-                                               8 * lane);
-        }
-        float acc[KVD_COLS][TOK];
-#pragma unroll
-        for (int i = 0; i < KVD_COLS; ++i)
-#pragma unroll
-            for (int t = 0; t < TOK; ++t) acc[i][t] = 0.f;
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            if (SL > 0 || s < S) {
-#pragma unroll
-                for (int i = 0; i < KVD_COLS; ++i)
-#pragma unroll
-                    for (int t = 0; t < TOK; ++t) kvd_dot8<DT>(wv[i][s], hv[t][s], acc[i][t]);
-            }
-        }
+    // The products of round cb (this wave's KVD_COLS codes from cb) are summed over the
+    // wave and stored.
+    auto finish = [&](int cb, float (&acc)[KVD_COLS][TOK]) {
         float v = 0.f;
 #pragma unroll
         for (int i = 0; i < KVD_COLS; ++i)
@@ -234,7 +206,7 @@ __device__ __forceinline__ void kv_direct_block(const KvDirectParams& p, int job
                 if (lane == i * TOK + t) v = a;
             }
         const int c = cb + li;
-        if (!lane_st || c >= c0 + nc) continue;
+        if (!lane_st || c >= c0 + nc) return;
         const uint16_t r = round_code<DT>(v);
         if (p.codes && kind != 1) p.codes[(int64_t)lt * p.co_s0 + c] = r;
         if (kind == 0) {
@@ -248,6 +220,67 @@ __device__ __forceinline__ void kv_direct_block(const KvDirectParams& p, int job
             p.rc[(int64_t)lt * p.width + c] = r;
             const float x = fabsf(code_value<DT>(r));
             if (c - p.k_width < p.v_nout) vmo = x; else vmi = x;
+        }
+    };
+    auto load_w = [&](uint4 (&wv)[KVD_COLS][NS], int cb, int s) {
+#pragma unroll
+        for (int i = 0; i < KVD_COLS; ++i)
+            wv[i][s] = *(const uint4*)(p.w + (int64_t)min(cb + i, p.width - 1) * p.w_s0 + 512 * min(s, S - 1) +
+                                       8 * lane);
+    };
+    auto load_h = [&]() {
+#pragma unroll
+        for (int t = 0; t < TOK; ++t)
+#pragma unroll
+            for (int s = 0; s < NS; ++s)
+                hv[t][s] = *(const uint4*)(p.hidden + (int64_t)min(t, p.n - 1) * p.h_s0 + 512 * min(s, S - 1) + 8 * lane);
+    };
+    auto dot = [&](const uint4 (&wv)[KVD_COLS][NS], int s, float (&acc)[KVD_COLS][TOK]) {
+        if (SL > 0 || s < S) {
+#pragma unroll
+            for (int i = 0; i < KVD_COLS; ++i)
+#pragma unroll
+                for (int t = 0; t < TOK; ++t) kvd_dot8<DT>(wv[i][s], hv[t][s], acc[i][t]);
+        }
+    };
+    if (SL > 0 && nc == 32) {
+        // Two rounds (a K block of 17 .. 32 codes), straight-line: as slice s of the first
+        // round is used, its registers take slice s of the second, so the block's kv_down
+        // rows stream with one round trip.
+        uint4 wv[KVD_COLS][NS];
+        float a0[KVD_COLS][TOK], a1[KVD_COLS][TOK];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) load_w(wv, c0 + KVD_COLS * wave, s);
+        load_h();
+#pragma unroll
+        for (int i = 0; i < KVD_COLS; ++i)
+#pragma unroll
+            for (int t = 0; t < TOK; ++t) a0[i][t] = a1[i][t] = 0.f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            dot(wv, s, a0);
+            load_w(wv, c0 + 16 + KVD_COLS * wave, s);
+            __builtin_amdgcn_sched_barrier(0);  // the reload stays here (not sunk past later products)
+        }
+#pragma unroll
+        for (int s = 0; s < NS; ++s) dot(wv, s, a1);
+        finish(c0 + KVD_COLS * wave, a0);
+        finish(c0 + 16 + KVD_COLS * wave, a1);
+    } else {
+        for (int cr = c0; cr < c0 + nc; cr += 16) {
+            const int cb = cr + KVD_COLS * wave;
+            uint4 wv[KVD_COLS][NS];
+#pragma unroll
+            for (int s = 0; s < NS; ++s) load_w(wv, cb, s);
+            if (cr == c0) load_h();
+            float acc[KVD_COLS][TOK];
+#pragma unroll
+            for (int i = 0; i < KVD_COLS; ++i)
+#pragma unroll
+                for (int t = 0; t < TOK; ++t) acc[i][t] = 0.f;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) dot(wv, s, acc);
+            finish(cb, acc);
         }
     }
     if (kind == 1) {

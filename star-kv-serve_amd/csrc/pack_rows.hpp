@@ -141,6 +141,56 @@ __device__ __forceinline__ void vpack_range(const VPackParams& q, int t, int j0,
     if (tail) pack_v_tail(s, q.v_nout, q.v_bytes, q.vq_off, q.vs_off, q.row_bytes, row, lane);
 }
 
+// vpack_range in two steps for a range of at most 64 bytes and at most 128 maxima per
+// token (tokens < 2): vpack_load issues the loads (the lane's maxima, the codes of its
+// byte, the slot), vpack_store forms and stores the bytes, so work can sit between the
+// loads and their use.
+struct VPackPre {
+    float mo[2], mi[2];
+    uint16_t lo[2], hi[2];
+    int64_t slot[2];
+};
+__device__ __forceinline__ bool vpack_two_step(const VPackParams& q, int j0, int j1) {
+    return q.n <= 2 && q.vtiles <= 128 && j1 - j0 <= 64;
+}
+__device__ __forceinline__ int vpack_lo_channel(const VPackParams& q, int j) {
+    return j < q.v_nbo ? 2 * j : q.v_nout + 2 * (j - q.v_nbo);
+}
+__device__ __forceinline__ VPackPre vpack_load(const VPackParams& q, int j0, int j1, int lane) {
+    VPackPre r;
+    const int j = min(j0 + lane, max(j1 - 1, 0));
+    const int c = min(vpack_lo_channel(q, j), q.v_rank - 1), c1 = min(c + 1, q.v_rank - 1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int tt = min(t, q.n - 1);
+        r.slot[t] = load_slot(q.slots, q.slot_bits, tt);
+        const float2* vm = (const float2*)q.vmax + (int64_t)tt * q.vtiles;
+        const float2 a = vm[min(lane, q.vtiles - 1)], b = vm[min(lane + 64, q.vtiles - 1)];
+        r.mo[t] = fmaxf(a.x, b.x);
+        r.mi[t] = fmaxf(a.y, b.y);
+        const uint16_t* src = q.rc + (int64_t)tt * q.width + q.k_width;
+        r.lo[t] = src[c];
+        r.hi[t] = src[c1];
+    }
+    return r;
+}
+__device__ __forceinline__ void vpack_store(const VPackParams& q, const VPackPre& r, int j0, int j1, bool tail,
+                                            int lane) {
+    const int j = j0 + lane, c = vpack_lo_channel(q, min(j, max(j1 - 1, 0)));
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        if (t >= q.n) break;
+        const VScales s = v_scales(wave_max(r.mo[t]), wave_max(r.mi[t]));
+        if (r.slot[t] >= q.num_blocks * q.block_size) continue;  // past the cache: skipped
+        uint8_t* row = q.cache + (r.slot[t] / q.block_size) * q.c_s0 + (r.slot[t] % q.block_size) * q.c_s1;
+        const float vlo = code_value_rt(r.lo[t], q.dt), vhi = code_value_rt(r.hi[t], q.dt);
+        if (j < j1)
+            row[q.vq_off + j] = pack_v_byte([&](int ch) { return ch == c ? vlo : vhi; }, j, q.v_rank, q.v_nout,
+                                            q.v_nbo, s);
+        if (tail) pack_v_tail(s, q.v_nout, q.v_bytes, q.vq_off, q.vs_off, q.row_bytes, row, lane);
+    }
+}
+
 // QuantRow (paged_quant.py:71-111) on the host: V outlier channels, V outlier bytes,
 // V bytes, K-scale / V-scale / V-code offsets and the row size (16-byte aligned).
 struct RowLayout {
