@@ -357,9 +357,10 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
         (&s_p[0][0])[i] = 0;
         if (FMT == FMT_BF16) (&s_plo[0][0])[i] = 0;
     }
-    if (plan[NWAVE * PLAN_STRIDE] == 0) return;  // no wave plan: the merge reports NaN
+    const int planned = plan[NWAVE * PLAN_STRIDE], hS = ((cint_p)p.ws)[0], htot = ((cint_p)p.ws)[1 + p.n];
+    if (planned == 0) return;  // no wave plan: the merge reports NaN
     LrLoop st;
-    if (!page_loop_init<NBUF>(st, p, xcd_range(blockIdx.x, gridDim.x))) return;
+    if (!page_loop_init<NBUF>(st, p, xcd_range(blockIdx.x, gridDim.x), hS, htot)) return;
 
     // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
     cint_p pw = plan + wave * PLAN_STRIDE;

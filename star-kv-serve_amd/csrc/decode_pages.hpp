@@ -186,10 +186,10 @@ __device__ __forceinline__ bool page_ends_seg(const PageLoop& st) {
 
 // The workgroup's page range from the header (pages per workgroup S, all pages) and the
 // records of its first NBUF pages; false if the range is empty.
+// S, total: the header's pages per range and page count (read by the caller beside the
+// wave plan's flag, so the two loads share one latency).
 template <int NBUF>
-__device__ __forceinline__ bool page_loop_init(PageLoop& st, const DecodeParams& p, int g) {
-    cint_p hdr = (cint_p)p.ws;
-    const int S = hdr[0], total = hdr[1 + p.n];
+__device__ __forceinline__ bool page_loop_init(PageLoop& st, const DecodeParams& p, int g, int S, int total) {
     st.g = g;
     st.beg = min(g * S, total);
     st.end = min(st.beg + S, total);

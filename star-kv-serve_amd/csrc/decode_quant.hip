@@ -501,7 +501,8 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     };
     QLoop st;
     // No wave plan (the merge reports NaN) or no pages: the workgroup packs its share and leaves.
-    if (plan[NWAVE * PLAN_STRIDE] == 0 || !page_loop_init<3>(st, p, xcd_range(blockIdx.x, gridDim.x))) {
+    const int planned = plan[NWAVE * PLAN_STRIDE], hS = ((cint_p)p.ws)[0], htot = ((cint_p)p.ws)[1 + p.n];
+    if (planned == 0 || !page_loop_init<3>(st, p, xcd_range(blockIdx.x, gridDim.x), hS, htot)) {
         vpack_share();
         return;
     }

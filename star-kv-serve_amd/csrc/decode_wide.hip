@@ -104,12 +104,6 @@ struct PvParams {
     size_t ws_pages; // page records
 };
 
-typedef const __attribute__((address_space(4))) PvParams kpv_t;
-__device__ __forceinline__ const PvParams& pv_params() {
-    kpv_t* pp = (kpv_t*)__builtin_amdgcn_kernarg_segment_ptr();
-    asm volatile("" : "+s"(pp));
-    return *(const PvParams*)pp;
-}
 
 // Copy descriptors of one page (record r; valid false past the range: nothing is read):
 // its rows, its logits (request b, tokens 16 k .., every head), the reference maxima of the
@@ -173,16 +167,19 @@ __device__ __forceinline__ half2_t nib2(uint32_t w, uint32_t sel) {
 template <int FMT, int MB, int NLD, bool MULTI>
 __global__ __launch_bounds__(NTHR) void pv_kernel(const PvParams p0) {
     extern __shared__ __attribute__((aligned(16))) uint8_t s_pv[];
-    const PvParams& p = pv_params();
+    // The parameters by value: the page loop's fields stay in registers (this kernel has
+    // the registers to spare) instead of being reloaded where they are used.
+    const PvParams& p = p0;
     const int tid = threadIdx.x, lane = tid & 63, wave = rfl(tid >> 6);
     cint_p P = (cint_p)(p.ws + 4);  // P[b]: first page of request b
-    // Buffers start zeroed: rows past a request's end are never copied and must be finite.
-    // Done first: it overlaps the header loads.
-    for (int i = tid; i < p.lds_bytes / 16; i += NTHR) ((uint4*)s_pv)[i] = make_uint4(0, 0, 0, 0);
-    if (((cint_p)(p.ws + p.ws_plan))[NWAVE * PLAN_STRIDE] == 0) return;  // no plan: the merge reports NaN
-    const int g = xcd_range(blockIdx.x, gridDim.x);
+    // The plan's flag and the header together (one latency), then the buffers zeroed
+    // (rows past a request's end are never copied and must be finite).
+    const int planned = ((cint_p)(p.ws + p.ws_plan))[NWAVE * PLAN_STRIDE];
     const int S = ((cint_p)p.ws)[0];  // pages per logits-pass range
     const int total = P[p.n];
+    for (int i = tid; i < p.lds_bytes / 16; i += NTHR) ((uint4*)s_pv)[i] = make_uint4(0, 0, 0, 0);
+    if (planned == 0) return;  // no plan: the merge reports NaN
+    const int g = xcd_range(blockIdx.x, gridDim.x);
     const int beg = min(g * p.r * S, total), end = min(beg + p.r * S, total);
     if (beg >= end) return;
     // This workgroup's column window.
