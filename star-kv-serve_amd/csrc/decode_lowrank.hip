@@ -358,15 +358,40 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
         if (FMT == FMT_BF16) (&s_plo[0][0])[i] = 0;
     }
     const int planned = plan[NWAVE * PLAN_STRIDE], hS = ((cint_p)p.ws)[0], htot = ((cint_p)p.ws)[1 + p.n];
+    __syncthreads();  // the zero fill is done on every wave before a page copy lands
     if (planned == 0) return;  // no wave plan: the merge reports NaN
     LrLoop st;
     if (!page_loop_init<NBUF>(st, p, xcd_range(blockIdx.x, gridDim.x), hS, htot)) return;
+    // The first pages' copies go out as soon as their records are in: the rest of the
+    // setup (the wave plan, the lane addresses) runs under their latency.
+    const uint32_t base = lds_addr(s_pages);
+    uint32_t doff[NLD];  // copy offsets of this lane inside a page, per copy i (chunk 8 i + wave)
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+        const int ch = i * NWAVE + wave;
+        uint32_t off = 0x80000000u;  // past the descriptor range: no memory access
+        if (ch < CS_CHUNKS) {
+            off = cs_copy_offset(ch, lane, p.cs_s0b);
+        } else if (ch < C::K0) {
+            if constexpr (NB > 0) {
+                const int vb = (ch - C::V0) * 1024 + 16 * lane;  // byte inside the V rows
+                const int row = vb / C::VPITCH, col = vb % C::VPITCH;
+                if (col < 2 * p.v_rank) off = (uint32_t)(row * (int)p.c_s1 + 2 * p.v_col + col);
+            }
+        } else if (ch < p.nch) {
+            const int Tc = 2 * (ch - C::K0) + (lane >> 5), r = (lane >> 1) & 15, h = lane & 1;
+            if (Tc < p.k_width / 16) off = (uint32_t)(r * (int)p.c_s1 + 32 * Tc + 16 * h);
+        }
+        doff[i] = off;
+    }
+    const DmaConst dc = dma_const<NBUF>(p, base, wave, base + (uint32_t)((p.nch + 2 * NB) * page_stride<NBUF>()));
+    dma_page<NLD, 0, NBUF>(dc, st.rc, true, wave, doff);
+    if (NBUF == 3) dma_page<NLD, 1, NBUF>(dc, st.r1, st.beg + 1 < st.end, wave, doff);
 
     // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
     cint_p pw = plan + wave * PLAN_STRIDE;
     const int ntw = pw[0], nh = pw[1];
     const bool fast = pw[3] != 0;
-    const uint32_t base = lds_addr(s_pages);
     const uint32_t sp = lds_addr(&s_part[wave][0]);
     LaneAddr<MTV, NB> la;
     uint32_t swd[MTV];  // the wave's slot words (plan order), read with a few wide scalar loads
@@ -431,35 +456,12 @@ __global__ __launch_bounds__(NTHR) void lowrank_kernel(const DecodeParams p0) {
     sm.m = -INFINITY;
     sm.l = 0.f;
 
-    // Copy offsets of this lane inside a page, per copy i (chunk 8 i + wave).
-    uint32_t doff[NLD];
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-        const int ch = i * NWAVE + wave;
-        uint32_t off = 0x80000000u;  // past the descriptor range: no memory access
-        if (ch < CS_CHUNKS) {
-            off = cs_copy_offset(ch, lane, p.cs_s0b);
-        } else if (ch < C::K0) {
-            if constexpr (NB > 0) {
-                const int vb = (ch - C::V0) * 1024 + 16 * lane;  // byte inside the V rows
-                const int row = vb / C::VPITCH, col = vb % C::VPITCH;
-                if (col < 2 * p.v_rank) off = (uint32_t)(row * (int)p.c_s1 + 2 * p.v_col + col);
-            }
-        } else if (ch < p.nch) {
-            const int Tc = 2 * (ch - C::K0) + (lane >> 5), r = (lane >> 1) & 15, h = lane & 1;
-            if (Tc < p.k_width / 16) off = (uint32_t)(r * (int)p.c_s1 + 32 * Tc + 16 * h);
-        }
-        doff[i] = off;
-    }
-    const DmaConst dc = dma_const<NBUF>(p, base, wave, base + (uint32_t)((p.nch + 2 * NB) * page_stride<NBUF>()));
     __syncthreads();
 
     st.pv_moved = false;
     st.pv_end = false;
     st.pv_b = 0;
     st.pv_buf = 0;
-    dma_page<NLD, 0, NBUF>(dc, st.rc, true, wave, doff);
-    if (NBUF == 3) dma_page<NLD, 1, NBUF>(dc, st.r1, st.beg + 1 < st.end, wave, doff);
 
     half8_t ab[MTV][4];
     f32x4_t acc[NB > 0 ? NB : 1];

@@ -500,18 +500,37 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
         }
     };
     QLoop st;
-    // No wave plan (the merge reports NaN) or no pages: the workgroup packs its share and leaves.
     const int planned = plan[NWAVE * PLAN_STRIDE], hS = ((cint_p)p.ws)[0], htot = ((cint_p)p.ws)[1 + p.n];
+    __syncthreads();  // the zero fill is done on every wave before a page copy lands
+    // No wave plan (the merge reports NaN) or no pages: the workgroup packs its share and leaves.
     if (planned == 0 || !page_loop_init<3>(st, p, xcd_range(blockIdx.x, gridDim.x), hS, htot)) {
         vpack_share();
         return;
     }
+    // The first two pages' copies go out as soon as their records are in: the rest of the
+    // setup (the wave plan, the lane addresses) runs under their latency.
+    const uint32_t base = lds_addr(s_pages);
+    uint32_t doff[NLD];  // copy offsets of this lane inside a page, per copy i (chunk 8 i + wave)
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+        const int ch = i * NWAVE + wave;
+        uint32_t off = 0x80000000u;  // past the descriptor range: no memory access
+        if (ch < CS_CHUNKS) {
+            off = cs_copy_offset(ch, lane, p.cs_s0b);
+        } else if (ch < p.nch) {
+            const int G = 4 * (ch - CS_CHUNKS) + (lane >> 4), t = lane & 15;
+            if (G < p.row_g) off = (uint32_t)(t * (int)p.c_s1 + 16 * G);
+        }
+        doff[i] = off;
+    }
+    const DmaConst dc = dma_const(p, base, wave, base + (uint32_t)((p.nch + 2 * NB) * PAGE_STRIDE));
+    dma_page<NLD, 0>(dc, st.rc, true, wave, doff);
+    dma_page<NLD, 1>(dc, st.r1, st.beg + 1 < st.end, wave, doff);
 
     // This wave's plan: slots (rank tiles) and heads (at most 4: Hq <= 32).
     cint_p pw = plan + wave * PLAN_STRIDE;
     const int ntw = pw[0], nh = pw[1];
     const bool fast = pw[3] != 0;
-    const uint32_t base = lds_addr(s_pages);
     const uint32_t sp = lds_addr(&s_part[wave][0]);
     const int O4 = (p.v_nout + 3) & ~3;
     const uint32_t vt0 = base + (uint32_t)(p.nch * PAGE_STRIDE);  // V table
@@ -609,21 +628,6 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     sm.m = -INFINITY;
     sm.l = 0.f;
 
-    // Copy offsets of this lane inside a page, per copy i (chunk 8 i + wave).
-    uint32_t doff[NLD];
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-        const int ch = i * NWAVE + wave;
-        uint32_t off = 0x80000000u;  // past the descriptor range: no memory access
-        if (ch < CS_CHUNKS) {
-            off = cs_copy_offset(ch, lane, p.cs_s0b);
-        } else if (ch < p.nch) {
-            const int G = 4 * (ch - CS_CHUNKS) + (lane >> 4), t = lane & 15;
-            if (G < p.row_g) off = (uint32_t)(t * (int)p.c_s1 + 16 * G);
-        }
-        doff[i] = off;
-    }
-    const DmaConst dc = dma_const(p, base, wave, base + (uint32_t)((p.nch + 2 * NB) * PAGE_STRIDE));
     vpack_share();
     __syncthreads();
 
@@ -632,8 +636,6 @@ __global__ __launch_bounds__(NTHR) void quant_kernel(const DecodeParams p0) {
     st.pv_end = false;
     st.pv_b = 0;
     st.pv_buf = 0;
-    dma_page<NLD, 0>(dc, st.rc, true, wave, doff);
-    dma_page<NLD, 1>(dc, st.r1, st.beg + 1 < st.end, wave, doff);
 
     half8_t ab[MTV][4];
     f32x4_t acc[NB > 0 ? NB : 1];
