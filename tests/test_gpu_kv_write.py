@@ -59,12 +59,12 @@ def _check_codes(codes, hidden, kv_down, dtype, label):
     assert exact > 0.99, label
 
 
-def _slots(n, num_blocks, gen):
+def _slots(n, num_blocks, gen, past=None):
     """Distinct slots in [16, num_blocks * 16); the first token -1 (null block), the last
-    one past the cache."""
+    one past the cache (by default when n > 2)."""
     s = torch.randperm(num_blocks * 16 - 16, generator=gen)[:n] + 16
     s[0] = -1
-    if n > 2:
+    if (n > 2) if past is None else past:
         s[-1] = num_blocks * 16 + 3
     return s
 
@@ -139,6 +139,43 @@ def test_write_kv_quant_rows(cuda, n, ranks, v_rank, dtype):
         assert np.array_equal(flat[s, :end], want[i, 0, :end]), (i, s)
         assert not flat[s, end:].any(), (i, s)
         assert np.array_equal(flat2[s], flat[s]), (i, s)  # written without codes_out
+
+
+@pytest.mark.parametrize("quant", [False, True])
+def test_write_kv_direct_skips_slots_past_the_cache(cuda, quant):
+    """Two tokens (the direct form): token 0 to the null block, token 1 past the cache
+    (skipped); every slot but slot 0 of block 0 keeps its bytes."""
+    print(f"\n[write_kv direct past-cache] quant={quant}", flush=True)
+    w, ops = _layer(cuda, 4096, quant, torch.bfloat16)
+    g = torch.Generator().manual_seed(77)
+    hid = torch.randn(2, 4096, generator=g).to(torch.bfloat16).to(cuda)
+    nb = 4
+    slots = _slots(2, nb, g, past=True)
+    assert slots.tolist()[0] == -1 and slots.tolist()[1] >= nb * 16
+    if quant:
+        cache = torch.full((nb, 16, ops.row.nbytes), 0xA5, dtype=torch.uint8, device=cuda)
+        args = dict(row=ops.row, k_ranks=ops.k_ranks, k_offsets=ops.k_head_offsets, k_nouts=ops.k_nouts)
+    else:
+        cache = torch.full((nb, 16, w.cache_width), 7.0, dtype=torch.bfloat16, device=cuda)
+        args = {}
+    before = cache.clone()
+    codes = write_kv(hid, ops.kv_down, cache, slots.to(cuda), w.k_width, return_codes=True, **args)
+    torch.cuda.synchronize()
+    _check_codes(codes, hid, ops.kv_down, torch.bfloat16, f"direct past-cache quant={quant}")
+    flat, flat0 = cache.reshape(nb * 16, -1), before.reshape(nb * 16, -1)
+    assert torch.equal(flat[1:].view(torch.uint8), flat0[1:].view(torch.uint8)), "a slot other than the null slot changed"
+    if quant:
+        lay = ref.row_layout(w.k_width, len(RANKS), w.v_rank)
+        c = codes.float().cpu().numpy()
+        want = np.zeros((1, 1, ops.row.nbytes), np.uint8)
+        widths, offsets, _ = ref.head_layout(RANKS)
+        cquant.pack_kv(c[:1, :w.k_width], c[:1, w.k_width:], want, np.arange(1), RANKS, offsets,
+                       [ref.n_outlier(r) for r in RANKS], w.v_rank, lay["ks_off"], lay["vs_off"], lay["vq_off"])
+        end = lay["vq_off"] + lay["v_bytes"]
+        got = flat[0].cpu().numpy()
+        assert np.array_equal(got[:end], want[0, 0, :end]) and not got[end:].any()
+    else:
+        assert torch.equal(flat[0].view(torch.int16), codes[0].view(torch.int16))
 
 
 def test_write_codes_matches_reference_scatter(cuda):

@@ -124,6 +124,29 @@ def test_deferred_write_then_decode_is_bit_identical(cuda, tmp_path, name):
     assert_close(out_b, truth, name)
 
 
+@pytest.mark.parametrize("name", ["quant_two_pass_2req", "bf16_two_pass_2req"])
+def test_deferred_direct_write_skips_slots_past_the_cache(cuda, tmp_path, name):
+    """A deferred direct write (two tokens) whose second slot lies past the cache: the decode
+    that carries it (the 3.2-bit V latent packed by its logits pass) leaves the cache as the
+    immediate write does, and gives the same output."""
+    quant, lengths = CASES[name][3], CASES[name][4]
+    print(f"\n[deferred direct write past-cache] case={name}", flush=True)
+    w, impl, _ = _layer(cuda, tmp_path, name)
+    g = torch.Generator().manual_seed(34)
+    cache0, _, slots, hidden, query, md = _step(cuda, impl, w, quant, g, lengths)
+    slots = slots.clone()
+    slots[1] = cache0.shape[0] * W.BLOCK_SIZE + 5  # past the cache: skipped
+    ca = cache0.clone()
+    impl.write_from_hidden(hidden, ca, slots)
+    out_a = _decode(impl, query, ca, md)
+    cb = cache0.clone()
+    impl.write_from_hidden(hidden, cb, slots, deferred=True)
+    out_b = _decode(impl, query, cb, md)
+    torch.cuda.synchronize()
+    assert torch.equal(ca.view(torch.int16), cb.view(torch.int16)), "cache bytes differ"
+    assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16)), "outputs differ"
+
+
 @pytest.mark.parametrize("name", ["bf16_one_pass", "quant_one_pass", "bf16_two_pass_2req", "quant_two_pass_1req"])
 def test_deferred_write_flushed_and_replaced(cuda, tmp_path, name):
     quant, lengths = CASES[name][3], CASES[name][4]
