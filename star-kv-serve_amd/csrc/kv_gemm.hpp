@@ -119,9 +119,9 @@ __device__ __forceinline__ float code_value(uint16_t r) {
 
 // ---------------------------------------------------------------------------
 // The direct write: one token with hidden a multiple of 512 up to 512 KVD_MAX_SLICES, or
-// KVD_MAX_TOKENS with hidden 512 KVD_MAX_SLICES. Job j of a launch owns whole codes: 16 codes (the bf16/fp16 row's
-// codes, a 3.2-bit row's V codes, or K codes asked for as codes_out only), or the K
-// block of KV head j (3.2-bit), which it packs itself. Lane l of a wave holds channels
+// KVD_MAX_TOKENS tokens with hidden 512 KVD_MAX_SLICES. Job j of a launch owns whole
+// codes: 16 codes (the bf16/fp16 row's codes, a 3.2-bit row's V codes, or K codes asked
+// for as codes_out only), or the K block of KV head j (3.2-bit), which it packs itself. Lane l of a wave holds channels
 // 512 s + 8 l .. + 8 (s < slices) of each token row and of KVD_COLS kv_down rows, and a
 // code is the wave sum of the lanes' fp32 dot products (a fixed order). The V latent of
 // a 3.2-bit row needs its maxima over all V codes: V jobs store the rounded codes and
@@ -149,7 +149,7 @@ struct KvDirectParams {
     int vtiles;
 };
 
-// Lane products of KVD_COLS codes (kv_down rows wv) with TOK token rows (hv), s < slices.
+// acc += the fp32 products of 8 bf16/fp16 channels of a kv_down row (w) and a token row (h).
 template <int DT>
 __device__ __forceinline__ void kvd_dot8(uint4 w, uint4 h, float& acc) {
     const uint32_t wa[4] = {w.x, w.y, w.z, w.w}, ha[4] = {h.x, h.y, h.z, h.w};
