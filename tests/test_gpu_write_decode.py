@@ -43,35 +43,38 @@ CASES = {
     "quant_one_pass_2req": (R8, 48, 8, True, [16, 300]),
     "quant_two_pass_1req": (R8, 400, 8, True, [1030]),
     "quant_two_pass_2req": (R8, 1290, 8, True, [77, 520]),
+    "quant_two_pass_1req_f16": (R8, 1290, 8, True, [700]),
 }
+DTYPES = {"quant_two_pass_1req_f16": torch.float16}  # the model dtype, bf16 unless listed
 
 
 def _layer(cuda, tmp_path, name):
     ranks, v_rank, num_heads, quant, _ = CASES[name]
+    dt = DTYPES.get(name, torch.bfloat16)
     path = str(tmp_path / "fused_weights.pt")
     ck.write_fused_checkpoint(path, 1, len(ranks), 128, HIDDEN, {0: (ranks, v_rank)}, seed=31)
-    w = ck.load_fused_checkpoint(path, 1, len(ranks), 128, dtype=torch.bfloat16, kv_quant=quant).layers[0]
-    cs = W.cos_sin_table(MAX_MODEL_LEN, torch.bfloat16, cuda)
+    w = ck.load_fused_checkpoint(path, 1, len(ranks), 128, dtype=dt, kv_quant=quant).layers[0]
+    cs = W.cos_sin_table(MAX_MODEL_LEN, dt, cuda)
     impl = StarKVAttentionImpl(num_heads, 128, 128 ** -0.5, len(ranks), starkv_layer=w,
                                rotary_emb=types.SimpleNamespace(cos_sin_cache=cs), max_model_len=MAX_MODEL_LEN,
                                fused_write=True)
-    impl.to_device(cuda, torch.bfloat16)
+    impl.to_device(cuda, dt)
     return w, impl, cs
 
 
-def _step(cuda, impl, w, quant, g, lengths=LENGTHS):
+def _step(cuda, impl, w, quant, g, lengths=LENGTHS, dt=torch.bfloat16):
     """A cache with the prompts written, this step's slots, hidden rows and query."""
     bt, nblk = W._page_layout(lengths, g)
     n = len(lengths)
     width = impl.row.nbytes // 2 if quant else w.cache_width
     kv_cache = torch.zeros(nblk, 1, W.BLOCK_SIZE, width, dtype=torch.bfloat16, device=cuda)
     blocks, slots = W._token_slots([L - 1 for L in lengths], bt)
-    x = torch.randn(blocks.numel(), HIDDEN, generator=g).to(torch.bfloat16).to(cuda)
+    x = torch.randn(blocks.numel(), HIDDEN, generator=g).to(dt).to(cuda)
     impl.write_from_hidden(x, kv_cache, (blocks * W.BLOCK_SIZE + slots).to(cuda))
     pos = torch.tensor([L - 1 for L in lengths])
     step_slots = (bt[torch.arange(n), pos // W.BLOCK_SIZE].long() * W.BLOCK_SIZE + pos % W.BLOCK_SIZE).to(cuda)
-    hidden = torch.randn(n, HIDDEN, generator=g).to(torch.bfloat16).to(cuda)
-    query = torch.randn(n, impl.num_heads * 128, generator=g).to(torch.bfloat16).to(cuda)
+    hidden = torch.randn(n, HIDDEN, generator=g).to(dt).to(cuda)
+    query = torch.randn(n, impl.num_heads * 128, generator=g).to(dt).to(cuda)
     md = StarKVMetadata(num_actual_tokens=n, num_decodes=n, num_decode_tokens=n, num_prefills=0,
                         max_seq_len=max(lengths), seq_lens=torch.tensor(lengths, dtype=torch.int32, device=cuda),
                         block_table=bt.to(cuda), slot_mapping=step_slots)
@@ -80,7 +83,7 @@ def _step(cuda, impl, w, quant, g, lengths=LENGTHS):
 
 def _decode(impl, query, cache, md):
     n = query.shape[0]
-    out = torch.full((n, impl.num_heads, 128), float("nan"), dtype=torch.bfloat16, device=query.device)
+    out = torch.full((n, impl.num_heads, 128), float("nan"), dtype=query.dtype, device=query.device)
     impl._decode(query.view(n, impl.num_heads, 128), impl._cache(cache), md, out, False)
     return out
 
@@ -91,7 +94,7 @@ def test_deferred_write_then_decode_is_bit_identical(cuda, tmp_path, name):
     print(f"\n[deferred write] case={name}", flush=True)
     w, impl, cs = _layer(cuda, tmp_path, name)
     g = torch.Generator().manual_seed(32)
-    cache0, bt, slots, hidden, query, md = _step(cuda, impl, w, quant, g, lengths)
+    cache0, bt, slots, hidden, query, md = _step(cuda, impl, w, quant, g, lengths, DTYPES.get(name, torch.bfloat16))
 
     # The write on its own, then the decode.
     ca = cache0.clone()
