@@ -49,9 +49,10 @@ def test_decode_graph_replays(cuda, quant):
 
 
 @pytest.mark.parametrize("quant", [False, True])
-def test_write_graph_replays(cuda, tmp_path, quant):
-    print(f"\n[graph write] quant={quant}", flush=True)
-    ranks, hidden, n = [16, 32, 48, 64], 1024, 24
+@pytest.mark.parametrize("n,hidden", [(24, 1024), (1, 1024), (2, 4096)])  # the split form; the direct form
+def test_write_graph_replays(cuda, tmp_path, quant, n, hidden):
+    print(f"\n[graph write] quant={quant} n={n} hidden={hidden}", flush=True)
+    ranks = [16, 32, 48, 64]
     path = str(tmp_path / "w.pt")
     ck.write_fused_checkpoint(path, 1, len(ranks), 128, hidden, {0: (ranks, 64)}, seed=5)
     w = ck.load_fused_checkpoint(path, 1, len(ranks), 128, dtype=torch.bfloat16, kv_quant=quant).layers[0]

@@ -70,6 +70,7 @@ def _slots(n, num_blocks, gen, past=None):
 
 
 @pytest.mark.parametrize("n,hidden,dtype", [(1, 4096, torch.bfloat16), (2, 4096, torch.bfloat16),
+                                            (2, 4096, torch.float16),
                                             (2, 3072, torch.float16), (1, 512, torch.float16),
                                             (1, 3072, torch.bfloat16), (37, 4096, torch.bfloat16),
                                             (64, 4096, torch.bfloat16), (130, 4096, torch.bfloat16),
